@@ -1,0 +1,335 @@
+// C ABI of libgdn2_amd.so: argument validation and kernel dispatch.
+//
+// Every entry point validates its whole argument list before it launches
+// anything, mirroring the reference's fail-fast asserts
+// (crates/kernels/src/gdn_training.rs:286-342, :356-390; chunk.rs:110-124):
+// an unsupported shape, dtype or buffer size is an error, never a fallback.
+#include <climits>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "gdn2_seq.h"
+
+using namespace gdn2;
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+int ok() {
+    g_error.clear();
+    return GDN2_OK;
+}
+
+int check_shape(const gdn2_shape *s) {
+    if (!s) return fail(GDN2_ERR_ARGUMENT, "shape is null");
+    if (s->batch <= 0 || s->time <= 0 || s->heads <= 0)
+        return fail(GDN2_ERR_SHAPE, "GDN-2 requires nonempty axes (batch=%lld time=%lld heads=%lld)",
+                    (long long)s->batch, (long long)s->time, (long long)s->heads);
+    if (s->keys < 1 || s->keys > 128 || s->values < 1 || s->values > 128)
+        return fail(GDN2_ERR_SHAPE, "key/value widths must be 1..128 (keys=%lld values=%lld)",
+                    (long long)s->keys, (long long)s->values);
+    if (s->batch * s->heads > INT_MAX || s->time > INT_MAX / 2)
+        return fail(GDN2_ERR_SHAPE, "batch*heads or time exceeds the launch limits");
+    return GDN2_OK;
+}
+
+// dtype: -1 = F32 or BF16; otherwise the required dtype.
+int check_view(const gdn2_view *v, const char *name, int dtype, bool data_may_be_null) {
+    if (!v) return fail(GDN2_ERR_ARGUMENT, "%s: view is null", name);
+    if (!v->data && !data_may_be_null) return fail(GDN2_ERR_ARGUMENT, "%s: data is null", name);
+    if (v->dtype != GDN2_F32 && v->dtype != GDN2_BF16)
+        return fail(GDN2_ERR_DTYPE, "%s: unknown dtype %d", name, v->dtype);
+    if (dtype >= 0 && v->dtype != dtype)
+        return fail(GDN2_ERR_DTYPE, "%s: dtype must be %s", name, dtype == GDN2_F32 ? "F32" : "BF16");
+    for (int d = 0; d < 4; ++d)
+        if (v->stride[d] < 0) return fail(GDN2_ERR_ARGUMENT, "%s: negative stride", name);
+    return GDN2_OK;
+}
+
+int check_chunk(int chunk) {
+    if (chunk < 1 || chunk > 64) return fail(GDN2_ERR_ARGUMENT, "chunk must be 1..64 (got %d)", chunk);
+    return GDN2_OK;
+}
+
+int check_out_dtype(int32_t dt) {
+    if (dt != GDN2_F32 && dt != GDN2_BF16) return fail(GDN2_ERR_DTYPE, "output dtype must be F32 or BF16");
+    return GDN2_OK;
+}
+
+int launch_status(hipError_t e, const char *what) {
+    if (e != hipSuccess) return fail(GDN2_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+#define GDN2_TRY(x)                  \
+    do {                             \
+        int _rc = (x);               \
+        if (_rc != GDN2_OK) return _rc; \
+    } while (0)
+
+size_t seq_checkpoint_bytes(const gdn2_shape *s) {
+    const int64_t nck = (s->time + SEQ_CT - 1) / SEQ_CT;
+    return (size_t)(s->batch * s->heads) * nck * seq_state_floats((int)s->keys, (int)s->values) * 4;
+}
+
+size_t seq_workspace_bytes(const gdn2_shape *s) {
+    return (size_t)(s->batch * s->heads) * SEQ_CT * seq_state_floats((int)s->keys, (int)s->values) * 4;
+}
+
+int check_channel_inputs(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k,
+                         const gdn2_view *v, const gdn2_view *alpha, const gdn2_view *erase,
+                         const gdn2_view *write, const gdn2_view *valid, const gdn2_view *reset) {
+    GDN2_TRY(check_view(q, "q", -1, false));
+    GDN2_TRY(check_view(k, "k", q->dtype, false));
+    GDN2_TRY(check_view(v, "v", q->dtype, false));
+    GDN2_TRY(check_view(alpha, "alpha", GDN2_F32, false));
+    GDN2_TRY(check_view(erase, "erase", GDN2_F32, false));
+    GDN2_TRY(check_view(write, "write", GDN2_F32, false));
+    GDN2_TRY(check_view(valid, "valid", GDN2_F32, false));
+    GDN2_TRY(check_view(reset, "reset", GDN2_F32, false));
+    return GDN2_OK;
+}
+
+SeqArgs seq_args(const gdn2_shape *s, const gdn2_view *q, const gdn2_view *k, const gdn2_view *v,
+                 const gdn2_view *alpha, const gdn2_view *erase, const gdn2_view *write,
+                 const gdn2_view *valid, const gdn2_view *reset) {
+    SeqArgs a{};
+    a.B = (int)s->batch;
+    a.T = (int)s->time;
+    a.H = (int)s->heads;
+    a.K = (int)s->keys;
+    a.V = (int)s->values;
+    a.q = make_view(q);
+    a.k = make_view(k);
+    a.v = make_view(v);
+    a.alpha = make_view(alpha);
+    a.erase = make_view(erase);
+    a.write = make_view(write);
+    a.valid = make_view(valid);
+    a.reset = make_view(reset);
+    a.nck = (a.T + SEQ_CT - 1) / SEQ_CT;
+    return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gdn2_abi_version(void) { return 100; }
+
+const char *gdn2_last_error(void) { return g_error.c_str(); }
+
+size_t gdn2_training_checkpoint_bytes(const gdn2_shape *shape, int chunk) {
+    if (check_shape(shape) || check_chunk(chunk)) return 0;
+    return seq_checkpoint_bytes(shape);
+}
+
+size_t gdn2_training_workspace_bytes(const gdn2_shape *shape, int chunk) {
+    if (check_shape(shape) || check_chunk(chunk)) return 0;
+    return seq_workspace_bytes(shape);
+}
+
+int gdn2_training_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q,
+                       const gdn2_view *k, const gdn2_view *v, const gdn2_view *alpha,
+                       const gdn2_view *erase, const gdn2_view *write, const gdn2_view *valid,
+                       const gdn2_view *reset, const gdn2_view *initial, void *output,
+                       int32_t output_dtype, float *final_state, float *scores, void *checkpoint,
+                       size_t checkpoint_bytes, void *stream) {
+    GDN2_TRY(check_shape(shape));
+    GDN2_TRY(check_chunk(chunk));
+    GDN2_TRY(check_channel_inputs(shape, q, k, v, alpha, erase, write, valid, reset));
+    GDN2_TRY(check_view(initial, "initial", GDN2_F32, true));
+    GDN2_TRY(check_out_dtype(output_dtype));
+    if (!output || !final_state || !scores)
+        return fail(GDN2_ERR_ARGUMENT, "output, final_state and scores must be non-null");
+    if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
+    if (checkpoint_bytes < seq_checkpoint_bytes(shape))
+        return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
+                    seq_checkpoint_bytes(shape), checkpoint_bytes);
+    SeqArgs a = seq_args(shape, q, k, v, alpha, erase, write, valid, reset);
+    a.initial = make_view(initial);
+    a.out = output;
+    a.out_bf16 = output_dtype == GDN2_BF16;
+    a.final_state = final_state;
+    a.scores = scores;
+    a.ck = (float *)checkpoint;
+    return launch_status(launch_seq_fwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
+                         "gdn2_training_scan");
+}
+
+int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gdn2_view *q,
+                           const gdn2_view *k, const gdn2_view *v, const gdn2_view *alpha,
+                           const gdn2_view *erase, const gdn2_view *write,
+                           const gdn2_view *valid, const gdn2_view *reset,
+                           const void *checkpoint, size_t checkpoint_bytes,
+                           const gdn2_view *d_output, const float *d_final_state,
+                           const float *d_scores, void *dq, void *dk, void *dv, float *dalpha,
+                           float *derase, float *dwrite, float *d_initial, void *workspace,
+                           size_t workspace_bytes, void *stream) {
+    GDN2_TRY(check_shape(shape));
+    GDN2_TRY(check_chunk(chunk));
+    GDN2_TRY(check_channel_inputs(shape, q, k, v, alpha, erase, write, valid, reset));
+    if (d_output) GDN2_TRY(check_view(d_output, "d_output", q->dtype, true));
+    if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
+    if (checkpoint_bytes < seq_checkpoint_bytes(shape))
+        return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
+                    seq_checkpoint_bytes(shape), checkpoint_bytes);
+    if (!workspace) return fail(GDN2_ERR_ARGUMENT, "workspace is null");
+    if (workspace_bytes < seq_workspace_bytes(shape))
+        return fail(GDN2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
+                    seq_workspace_bytes(shape), workspace_bytes);
+    SeqArgs a = seq_args(shape, q, k, v, alpha, erase, write, valid, reset);
+    a.ck = (float *)checkpoint;
+    if (d_output) a.dout = make_view(d_output);
+    a.dfinal = d_final_state;
+    a.dscores = d_scores;
+    a.dq = dq;
+    a.dk = dk;
+    a.dv = dv;
+    a.dalpha = dalpha;
+    a.derase = derase;
+    a.dwrite = dwrite;
+    a.dinitial = d_initial;
+    a.replay = (float *)workspace;
+    return launch_status(launch_seq_bwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
+                         "gdn2_training_backward");
+}
+
+size_t gdn_scalar_checkpoint_bytes(const gdn2_shape *shape, int chunk) {
+    if (check_shape(shape) || check_chunk(chunk)) return 0;
+    return seq_checkpoint_bytes(shape);
+}
+
+size_t gdn_scalar_workspace_bytes(const gdn2_shape *shape, int chunk) {
+    if (check_shape(shape) || check_chunk(chunk)) return 0;
+    return seq_workspace_bytes(shape);
+}
+
+static int check_scalar_inputs(const gdn2_view *q, const gdn2_view *k, const gdn2_view *v,
+                               const gdn2_view *beta, const gdn2_view *g,
+                               const gdn2_view *valid, const gdn2_view *reset) {
+    GDN2_TRY(check_view(q, "q", -1, false));
+    GDN2_TRY(check_view(k, "k", q->dtype, false));
+    GDN2_TRY(check_view(v, "v", q->dtype, false));
+    GDN2_TRY(check_view(beta, "beta", GDN2_F32, false));
+    GDN2_TRY(check_view(g, "g", GDN2_F32, false));
+    GDN2_TRY(check_view(valid, "valid", GDN2_F32, false));
+    GDN2_TRY(check_view(reset, "reset", GDN2_F32, false));
+    return GDN2_OK;
+}
+
+int gdn_scalar_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q, const gdn2_view *k,
+                    const gdn2_view *v, const gdn2_view *beta, const gdn2_view *g,
+                    const gdn2_view *valid, const gdn2_view *reset, const gdn2_view *initial,
+                    void *output, int32_t output_dtype, float *final_state, float *scores,
+                    void *checkpoint, size_t checkpoint_bytes, void *stream) {
+    GDN2_TRY(check_shape(shape));
+    GDN2_TRY(check_chunk(chunk));
+    GDN2_TRY(check_scalar_inputs(q, k, v, beta, g, valid, reset));
+    GDN2_TRY(check_view(initial, "initial", GDN2_F32, true));
+    GDN2_TRY(check_out_dtype(output_dtype));
+    if (!output || !final_state || !scores)
+        return fail(GDN2_ERR_ARGUMENT, "output, final_state and scores must be non-null");
+    if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
+    if (checkpoint_bytes < seq_checkpoint_bytes(shape))
+        return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
+                    seq_checkpoint_bytes(shape), checkpoint_bytes);
+    SeqArgs a = seq_args(shape, q, k, v, beta, beta, beta, valid, reset);
+    a.scalar = 1;
+    a.beta = make_view(beta);
+    a.g = make_view(g);
+    a.initial = make_view(initial);
+    a.out = output;
+    a.out_bf16 = output_dtype == GDN2_BF16;
+    a.final_state = final_state;
+    a.scores = scores;
+    a.ck = (float *)checkpoint;
+    return launch_status(launch_seq_fwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
+                         "gdn_scalar_scan");
+}
+
+int gdn_scalar_backward(const gdn2_shape *shape, int chunk, const gdn2_view *q,
+                        const gdn2_view *k, const gdn2_view *v, const gdn2_view *beta,
+                        const gdn2_view *g, const gdn2_view *valid, const gdn2_view *reset,
+                        const void *checkpoint, size_t checkpoint_bytes,
+                        const gdn2_view *d_output, const float *d_final_state,
+                        const float *d_scores, void *dq, void *dk, void *dv, float *dbeta,
+                        float *dg, float *d_initial, void *workspace, size_t workspace_bytes,
+                        void *stream) {
+    GDN2_TRY(check_shape(shape));
+    GDN2_TRY(check_chunk(chunk));
+    GDN2_TRY(check_scalar_inputs(q, k, v, beta, g, valid, reset));
+    if (d_output) GDN2_TRY(check_view(d_output, "d_output", q->dtype, true));
+    if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
+    if (checkpoint_bytes < seq_checkpoint_bytes(shape))
+        return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
+                    seq_checkpoint_bytes(shape), checkpoint_bytes);
+    if (!workspace) return fail(GDN2_ERR_ARGUMENT, "workspace is null");
+    if (workspace_bytes < seq_workspace_bytes(shape))
+        return fail(GDN2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
+                    seq_workspace_bytes(shape), workspace_bytes);
+    SeqArgs a = seq_args(shape, q, k, v, beta, beta, beta, valid, reset);
+    a.scalar = 1;
+    a.beta = make_view(beta);
+    a.g = make_view(g);
+    a.ck = (float *)checkpoint;
+    if (d_output) a.dout = make_view(d_output);
+    a.dfinal = d_final_state;
+    a.dscores = d_scores;
+    a.dq = dq;
+    a.dk = dk;
+    a.dv = dv;
+    a.dbeta = dbeta;
+    a.dg = dg;
+    a.dinitial = d_initial;
+    a.replay = (float *)workspace;
+    return launch_status(launch_seq_bwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
+                         "gdn_scalar_backward");
+}
+
+int gdn2_decode_step(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k,
+                     const gdn2_view *v, const gdn2_view *alpha, const gdn2_view *erase,
+                     const gdn2_view *write, const gdn2_view *valid, const gdn2_view *reset,
+                     float *state, void *output, int32_t output_dtype, float *scores,
+                     void *stream) {
+    GDN2_TRY(check_shape(shape));
+    if (shape->time != 1) return fail(GDN2_ERR_SHAPE, "decode step needs time == 1");
+    GDN2_TRY(check_view(q, "q", -1, false));
+    GDN2_TRY(check_view(k, "k", q->dtype, false));
+    GDN2_TRY(check_view(v, "v", q->dtype, false));
+    GDN2_TRY(check_view(alpha, "alpha", GDN2_F32, false));
+    GDN2_TRY(check_view(erase, "erase", GDN2_F32, false));
+    GDN2_TRY(check_view(write, "write", GDN2_F32, false));
+    if (valid) GDN2_TRY(check_view(valid, "valid", GDN2_F32, true));
+    if (reset) GDN2_TRY(check_view(reset, "reset", GDN2_F32, true));
+    GDN2_TRY(check_out_dtype(output_dtype));
+    if (!state || !output || !scores)
+        return fail(GDN2_ERR_ARGUMENT, "state, output and scores must be non-null");
+    SeqArgs a = seq_args(shape, q, k, v, alpha, erase, write, valid, reset);
+    if (!valid) a.valid.data = nullptr;
+    if (!reset) a.reset.data = nullptr;
+    const int64_t K = shape->keys, V = shape->values;
+    gdn2_view st{state, GDN2_F32, 0, {shape->heads * K * V, K * V, V, 1}};
+    a.initial = make_view(&st);
+    a.final_state = state;  // each workgroup reads its slice before writing it
+    a.out = output;
+    a.out_bf16 = output_dtype == GDN2_BF16;
+    a.scores = scores;
+    a.ck = nullptr;
+    return launch_status(launch_seq_fwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
+                         "gdn2_decode_step");
+}
+
+}  // extern "C"

@@ -1,0 +1,81 @@
+"""ctypes binding of libgdn2_amd.so (declarations in include/gdn2.h).
+
+Loading fails loudly when the library has not been built: there is no CPU or
+eager-PyTorch fallback behind these functions.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG, "lib", "libgdn2_amd.so")
+
+GDN2_F32 = 0
+GDN2_BF16 = 1
+
+STATUS = {0: "OK", 1: "ARGUMENT", 2: "SHAPE", 3: "DTYPE", 4: "WORKSPACE", 5: "LAUNCH"}
+
+
+class Gdn2Shape(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_int64), ("time", ctypes.c_int64), ("heads", ctypes.c_int64),
+                ("keys", ctypes.c_int64), ("values", ctypes.c_int64)]
+
+
+class Gdn2View(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("dtype", ctypes.c_int32),
+                ("reserved", ctypes.c_int32), ("stride", ctypes.c_int64 * 4)]
+
+
+class Gdn2Error(RuntimeError):
+    def __init__(self, fn: str, status: int, message: str):
+        super().__init__(f"{fn}: {STATUS.get(status, status)}: {message}")
+        self.status = status
+
+
+# Exported symbols and their signatures: (name, restype, argtypes).
+_P = ctypes.c_void_p
+_V = ctypes.POINTER(Gdn2View)
+_S = ctypes.POINTER(Gdn2Shape)
+_F = ctypes.c_void_p  # float*
+_I = ctypes.c_int
+_Z = ctypes.c_size_t
+SIGNATURES = {
+    "gdn2_abi_version": (_I, []),
+    "gdn2_last_error": (ctypes.c_char_p, []),
+    "gdn2_training_checkpoint_bytes": (_Z, [_S, _I]),
+    "gdn2_training_workspace_bytes": (_Z, [_S, _I]),
+    "gdn2_training_scan": (_I, [_S, _I] + [_V] * 9 + [_P, ctypes.c_int32, _F, _F, _P, _Z, _P]),
+    "gdn2_training_backward": (_I, [_S, _I] + [_V] * 8 + [_P, _Z, _V, _F, _F] + [_P] * 3
+                               + [_F] * 4 + [_P, _Z, _P]),
+    "gdn_scalar_checkpoint_bytes": (_Z, [_S, _I]),
+    "gdn_scalar_workspace_bytes": (_Z, [_S, _I]),
+    "gdn_scalar_scan": (_I, [_S, _I] + [_V] * 8 + [_P, ctypes.c_int32, _F, _F, _P, _Z, _P]),
+    "gdn_scalar_backward": (_I, [_S, _I] + [_V] * 7 + [_P, _Z, _V, _F, _F] + [_P] * 3
+                            + [_F] * 3 + [_P, _Z, _P]),
+    "gdn2_decode_step": (_I, [_S] + [_V] * 8 + [_F, _P, ctypes.c_int32, _F, _P]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load the library (once).  Raises if it is missing or incomplete."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run __graft_entry__.build() (hipcc, gfx950). "
+                "There is no fallback implementation.")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(fn: str, status: int):
+    if status != 0:
+        raise Gdn2Error(fn, status, lib().gdn2_last_error().decode())

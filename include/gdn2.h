@@ -1,0 +1,163 @@
+/*
+ * gdn2.h -- C ABI of libgdn2_amd.so, the MI355X (gfx950) GDN-2 scan.
+ *
+ * The library is the drop-in replacement for delta-block-lm's GDN-2 scan
+ * operator.  Each entry point below names the reference interface it stands
+ * in for.  Plain pointers and sizes only: device pointers come from the
+ * caller's allocator (PyTorch, a Rust FFI crate, ...); the library itself
+ * never allocates device memory and never synchronises the stream.
+ *
+ * Layouts (reference crates/mixers/src/chunk.rs:126):
+ *   sequences  [batch, time, head, channel]     masks [batch, time] (f32 0/1)
+ *   states     [batch, head, key, value]        scores [batch, time, head]
+ * Inputs are strided views (element strides, any sign-free layout, stride 0
+ * allowed for broadcast gates).  Outputs and gradients are dense row-major.
+ *
+ * Semantics (reference crates/mixers/src/reference.rs:41-257, per valid token):
+ *   bar   = diag(alpha) S            (S zeroed first when reset[t] != 0)
+ *   delta = write .* v - (erase .* k)^T bar
+ *   S'    = bar + k delta^T,  out = S'^T q,  score = ||k|| * ||delta||
+ * Padding tokens (valid == 0) emit zero output and score and keep the state.
+ * At a zero edit the score takes the zero subgradient.
+ *
+ * Errors: every entry point validates before launching.  On failure it
+ * returns a nonzero status, launches nothing, and gdn2_last_error() (per
+ * calling thread) describes the failure.  There is no CPU fallback.
+ * Calls are asynchronous on `stream` (a hipStream_t; NULL = default stream).
+ */
+#ifndef GDN2_AMD_H
+#define GDN2_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__) || defined(__clang__)
+#define GDN2_API __attribute__((visibility("default")))
+#else
+#define GDN2_API
+#endif
+
+enum gdn2_dtype { GDN2_F32 = 0, GDN2_BF16 = 1 };
+
+enum gdn2_status {
+    GDN2_OK = 0,
+    GDN2_ERR_ARGUMENT = 1,  /* null pointer, bad enum, bad chunk */
+    GDN2_ERR_SHAPE = 2,     /* empty axis or unsupported key/value width */
+    GDN2_ERR_DTYPE = 3,     /* unsupported or mismatched dtypes */
+    GDN2_ERR_WORKSPACE = 4, /* checkpoint/workspace buffer too small */
+    GDN2_ERR_LAUNCH = 5     /* HIP launch error */
+};
+
+/* Logical problem size.  keys = d_k, values = d_v (each 1..128). */
+typedef struct gdn2_shape {
+    int64_t batch, time, heads, keys, values;
+} gdn2_shape;
+
+/* Strided read-only device view.  For sequence tensors the strides are those
+ * of [batch, time, head, channel]; for states [batch, head, key, value]; for
+ * masks [batch, time] (stride[2], stride[3] unused); for per-head scalars
+ * [batch, time, head] (stride[3] unused).  Strides are in elements. */
+typedef struct gdn2_view {
+    const void *data;
+    int32_t dtype; /* enum gdn2_dtype */
+    int32_t reserved;
+    int64_t stride[4];
+} gdn2_view;
+
+/* Version of this ABI (major * 100 + minor). */
+GDN2_API int gdn2_abi_version(void);
+
+/* Message of the last failure on the calling thread ("" after success). */
+GDN2_API const char *gdn2_last_error(void);
+
+/* ---- Channel-wise GDN-2 training scan ------------------------------------ */
+/* Replaces GdnTrainingOps::gdn_training_scan / gdn_training_backward
+ * (reference crates/kernels/src/gdn_training_ops.rs:27-68) and their CubeCL
+ * launches run_scan / run_backward (crates/kernels/src/gdn_training.rs:344-487).
+ * The reference packs [output ; final_state ; scores] into one f32 buffer
+ * (gdn_training_ops.rs:300-332); passing output = packed, final_state =
+ * packed + B*T*H*V, scores = packed + B*T*H*V + B*H*K*V with an f32 output
+ * reproduces that packing exactly.  The reference's private `checkpoint` and
+ * `auxiliary` tensors are replaced by one opaque checkpoint buffer written by
+ * the forward and read by the backward.
+ *
+ * q, k, v: F32 or BF16 (same dtype); alpha, erase, write, valid, reset,
+ * initial: F32.  initial.data may be NULL (zero state).  chunk: 1..64, the
+ * checkpoint interval in tokens (the reference allows 1..16,
+ * gdn_training.rs:370-373); results do not depend on it. */
+GDN2_API size_t gdn2_training_checkpoint_bytes(const gdn2_shape *shape, int chunk);
+
+GDN2_API int gdn2_training_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q,
+                       const gdn2_view *k, const gdn2_view *v, const gdn2_view *alpha,
+                       const gdn2_view *erase, const gdn2_view *write,
+                       const gdn2_view *valid, const gdn2_view *reset,
+                       const gdn2_view *initial, void *output, int32_t output_dtype,
+                       float *final_state, float *scores, void *checkpoint,
+                       size_t checkpoint_bytes, void *stream);
+
+/* Scratch the backward needs beyond the checkpoint. */
+GDN2_API size_t gdn2_training_workspace_bytes(const gdn2_shape *shape, int chunk);
+
+/* d_output ([B,T,H,V], F32 or BF16, strided), d_final_state ([B,H,K,V] F32,
+ * contiguous) and d_scores ([B,T,H] F32, contiguous) may each be NULL (zero
+ * adjoint).  Gradients are written densely: dq, dk, dv in the dtype of q/k/v;
+ * dalpha, derase, dwrite, d_initial in F32.  Any gradient pointer may be NULL
+ * (not wanted) except that the kernel still computes it internally. */
+GDN2_API int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gdn2_view *q,
+                           const gdn2_view *k, const gdn2_view *v, const gdn2_view *alpha,
+                           const gdn2_view *erase, const gdn2_view *write,
+                           const gdn2_view *valid, const gdn2_view *reset,
+                           const void *checkpoint, size_t checkpoint_bytes,
+                           const gdn2_view *d_output, const float *d_final_state,
+                           const float *d_scores, void *dq, void *dk, void *dv,
+                           float *dalpha, float *derase, float *dwrite, float *d_initial,
+                           void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- Scalar-gate gated delta rule (chunked, MFMA) ------------------------ */
+/* The scalar special case of the same recurrence: alpha[i] = exp(g),
+ * erase[i] = write[j] = beta for every channel.  beta and g are [B,T,H] F32
+ * (g is the log decay, finite).  No counterpart entry exists in the reference
+ * (it reaches this case only through the channel-wise op with broadcast
+ * gates); this is the chunk-WY fast path the north-star benchmark measures.
+ * chunk must be 64 (the computational chunk of the MFMA kernels). */
+GDN2_API size_t gdn_scalar_checkpoint_bytes(const gdn2_shape *shape, int chunk);
+
+GDN2_API int gdn_scalar_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q,
+                    const gdn2_view *k, const gdn2_view *v, const gdn2_view *beta,
+                    const gdn2_view *g, const gdn2_view *valid, const gdn2_view *reset,
+                    const gdn2_view *initial, void *output, int32_t output_dtype,
+                    float *final_state, float *scores, void *checkpoint,
+                    size_t checkpoint_bytes, void *stream);
+
+GDN2_API size_t gdn_scalar_workspace_bytes(const gdn2_shape *shape, int chunk);
+
+GDN2_API int gdn_scalar_backward(const gdn2_shape *shape, int chunk, const gdn2_view *q,
+                        const gdn2_view *k, const gdn2_view *v, const gdn2_view *beta,
+                        const gdn2_view *g, const gdn2_view *valid, const gdn2_view *reset,
+                        const void *checkpoint, size_t checkpoint_bytes,
+                        const gdn2_view *d_output, const float *d_final_state,
+                        const float *d_scores, void *dq, void *dk, void *dv, float *dbeta,
+                        float *dg, float *d_initial, void *workspace, size_t workspace_bytes,
+                        void *stream);
+
+/* ---- Decode step on a carried state -------------------------------------- */
+/* One token per sequence (time == 1) applied in place to state [B,H,K,V] F32.
+ * Equivalent to gdn2_training_scan with time = 1, initial = final_state =
+ * state; the reference reaches it as the T=1 scans of Mixer::prepare_sbd's
+ * noisy path (crates/mixers/src/sbd.rs:270-283).  valid/reset may have
+ * data == NULL (all valid, no reset). */
+GDN2_API int gdn2_decode_step(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k,
+                     const gdn2_view *v, const gdn2_view *alpha, const gdn2_view *erase,
+                     const gdn2_view *write, const gdn2_view *valid, const gdn2_view *reset,
+                     float *state, void *output, int32_t output_dtype, float *scores,
+                     void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN2_AMD_H */
