@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <string>
 
+#include "gdn2_chunk.h"
 #include "gdn2_seq.h"
 
 using namespace gdn2;
@@ -209,12 +210,55 @@ int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gdn2_view *
 
 size_t gdn_scalar_checkpoint_bytes(const gdn2_shape *shape, int chunk) {
     if (check_shape(shape) || check_chunk(chunk)) return 0;
-    return seq_checkpoint_bytes(shape);
+    // Large enough for whichever kernel family the call will select.
+    const size_t c = chunk_checkpoint_bytes(shape->batch, shape->time, shape->heads);
+    const size_t q = seq_checkpoint_bytes(shape);
+    return chunk_eligible_shape(shape, chunk) && c > q ? c : q;
 }
 
 size_t gdn_scalar_workspace_bytes(const gdn2_shape *shape, int chunk) {
     if (check_shape(shape) || check_chunk(chunk)) return 0;
-    return seq_workspace_bytes(shape);
+    const size_t c = chunk_workspace_bytes(shape->batch, shape->time, shape->heads);
+    const size_t q = seq_workspace_bytes(shape);
+    return chunk_eligible_shape(shape, chunk) && c > q ? c : q;
+}
+
+// The chunk-WY MFMA kernels take bf16 q/k/v with d_k = d_v = 64, chunk 64,
+// unit channel stride and 16-byte aligned token rows; everything else runs the
+// token-sequential kernels.  Forward and backward apply the same rule, so the
+// checkpoint format always matches.
+static bool rows_aligned(const gdn2_view *v) {
+    return v->stride[3] == 1 && ((uintptr_t)v->data & 15) == 0 && v->stride[0] % 8 == 0 &&
+           v->stride[1] % 8 == 0 && v->stride[2] % 8 == 0;
+}
+
+static bool use_chunk_path(const gdn2_shape *shape, int chunk, const gdn2_view *q,
+                           const gdn2_view *k, const gdn2_view *v) {
+    return chunk_eligible_shape(shape, chunk) && q->dtype == GDN2_BF16 && rows_aligned(q) &&
+           rows_aligned(k) && rows_aligned(v);
+}
+
+static ChunkArgs chunk_args(const gdn2_shape *s, const gdn2_view *q, const gdn2_view *k,
+                            const gdn2_view *v, const gdn2_view *beta, const gdn2_view *g,
+                            const gdn2_view *valid, const gdn2_view *reset) {
+    ChunkArgs a{};
+    a.B = (int)s->batch;
+    a.T = (int)s->time;
+    a.H = (int)s->heads;
+    a.nc = (a.T + CHUNK - 1) / CHUNK;
+    a.q = (const uint16_t *)q->data;
+    a.k = (const uint16_t *)k->data;
+    a.v = (const uint16_t *)v->data;
+    for (int d = 0; d < 3; ++d) {
+        a.qs[d] = q->stride[d];
+        a.ks[d] = k->stride[d];
+        a.vs[d] = v->stride[d];
+    }
+    a.beta = make_view(beta);
+    a.g = make_view(g);
+    a.valid = make_view(valid);
+    a.reset = make_view(reset);
+    return a;
 }
 
 static int check_scalar_inputs(const gdn2_view *q, const gdn2_view *k, const gdn2_view *v,
@@ -243,9 +287,19 @@ int gdn_scalar_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q, cons
     if (!output || !final_state || !scores)
         return fail(GDN2_ERR_ARGUMENT, "output, final_state and scores must be non-null");
     if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
-    if (checkpoint_bytes < seq_checkpoint_bytes(shape))
+    if (checkpoint_bytes < gdn_scalar_checkpoint_bytes(shape, chunk))
         return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
-                    seq_checkpoint_bytes(shape), checkpoint_bytes);
+                    gdn_scalar_checkpoint_bytes(shape, chunk), checkpoint_bytes);
+    if (use_chunk_path(shape, chunk, q, k, v)) {
+        ChunkArgs c = chunk_args(shape, q, k, v, beta, g, valid, reset);
+        c.initial = make_view(initial);
+        c.out = output;
+        c.out_bf16 = output_dtype == GDN2_BF16;
+        c.final_state = final_state;
+        c.scores = scores;
+        chunk_bind_checkpoint(c, checkpoint);
+        return launch_status(launch_chunk_fwd(c, (hipStream_t)stream), "gdn_scalar_scan");
+    }
     SeqArgs a = seq_args(shape, q, k, v, beta, beta, beta, valid, reset);
     a.scalar = 1;
     a.beta = make_view(beta);
@@ -273,13 +327,35 @@ int gdn_scalar_backward(const gdn2_shape *shape, int chunk, const gdn2_view *q,
     GDN2_TRY(check_scalar_inputs(q, k, v, beta, g, valid, reset));
     if (d_output) GDN2_TRY(check_view(d_output, "d_output", q->dtype, true));
     if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
-    if (checkpoint_bytes < seq_checkpoint_bytes(shape))
+    if (checkpoint_bytes < gdn_scalar_checkpoint_bytes(shape, chunk))
         return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
-                    seq_checkpoint_bytes(shape), checkpoint_bytes);
+                    gdn_scalar_checkpoint_bytes(shape, chunk), checkpoint_bytes);
     if (!workspace) return fail(GDN2_ERR_ARGUMENT, "workspace is null");
-    if (workspace_bytes < seq_workspace_bytes(shape))
+    if (workspace_bytes < gdn_scalar_workspace_bytes(shape, chunk))
         return fail(GDN2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
-                    seq_workspace_bytes(shape), workspace_bytes);
+                    gdn_scalar_workspace_bytes(shape, chunk), workspace_bytes);
+    if (use_chunk_path(shape, chunk, q, k, v)) {
+        if (d_output && d_output->data && !rows_aligned(d_output))
+            return fail(GDN2_ERR_ARGUMENT,
+                        "d_output needs unit channel stride and 16-byte aligned rows on the "
+                        "chunked path (chunk 64, bf16, d_k = d_v = 64)");
+        ChunkArgs c = chunk_args(shape, q, k, v, beta, g, valid, reset);
+        chunk_bind_checkpoint(c, const_cast<void *>(checkpoint));
+        c.ws_dstate = (float *)workspace;
+        if (d_output && d_output->data) {
+            c.dout = (const uint16_t *)d_output->data;
+            for (int d = 0; d < 3; ++d) c.ds[d] = d_output->stride[d];
+        }
+        c.dfinal = d_final_state;
+        c.dscores = d_scores;
+        c.dq = dq;
+        c.dk = dk;
+        c.dv = dv;
+        c.dbeta = dbeta;
+        c.dg = dg;
+        c.dinitial = d_initial;
+        return launch_status(launch_chunk_bwd(c, (hipStream_t)stream), "gdn_scalar_backward");
+    }
     SeqArgs a = seq_args(shape, q, k, v, beta, beta, beta, valid, reset);
     a.scalar = 1;
     a.beta = make_view(beta);

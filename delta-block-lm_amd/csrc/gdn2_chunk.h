@@ -1,0 +1,77 @@
+// Chunk-WY scalar-gate GDN kernels on MFMA (bf16 inputs, fp32 state).
+#pragma once
+
+#include "gdn2_common.h"
+
+namespace gdn2 {
+
+constexpr int CHUNK = 64;   // tokens per chunk (computational chunk)
+constexpr int CHUNK_D = 64; // d_k = d_v handled by these kernels
+
+// Per-chunk gate summary written by the prep kernel: chunk-local cumulative
+// log decay G, masked beta, validity and reset-segment index of every token.
+struct GateBlock {
+    float G[CHUNK];
+    float beta[CHUNK];
+    float val[CHUNK];
+    int seg[CHUNK];
+};
+
+// Per-chunk private storage handed from the forward to the backward.
+constexpr size_t CK_STATE_BYTES = CHUNK_D * CHUNK_D * sizeof(float);    // S at chunk start
+constexpr size_t CK_T_BYTES = CHUNK * CHUNK * sizeof(uint16_t);          // T = (I + A)^-1, bf16
+constexpr size_t CK_GATE_BYTES = sizeof(GateBlock);
+constexpr size_t CK_CHUNK_BYTES = CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES;
+
+struct ChunkArgs {
+    int B, T, H, nc;
+    // bf16 q/k/v with unit channel stride: element (b,t,h,c) at b*s0 + t*s1 + h*s2 + c
+    const uint16_t *q, *k, *v;
+    int64_t qs[3], ks[3], vs[3];
+    View beta, g, valid, reset, initial;
+    // forward outputs
+    void *out;
+    int out_bf16;
+    float *final_state, *scores;
+    // checkpoint: [B*H*nc] states, then T tiles, then gate blocks
+    float *ck_state;
+    uint16_t *ck_t;
+    GateBlock *ck_gate;
+    // backward
+    const uint16_t *dout;
+    int64_t ds[3];
+    const float *dfinal, *dscores;
+    void *dq, *dk, *dv;
+    float *dbeta, *dg, *dinitial;
+    float *ws_dstate;  // [B*H*nc] adjoint of the state at each chunk end
+};
+
+inline bool chunk_eligible_shape(const gdn2_shape *s, int chunk) {
+    return chunk == CHUNK && s->keys == CHUNK_D && s->values == CHUNK_D;
+}
+
+inline int64_t chunk_count(int64_t B, int64_t T, int64_t H) {
+    return B * H * ((T + CHUNK - 1) / CHUNK);
+}
+
+inline size_t chunk_checkpoint_bytes(int64_t B, int64_t T, int64_t H) {
+    return (size_t)chunk_count(B, T, H) * CK_CHUNK_BYTES;
+}
+
+inline size_t chunk_workspace_bytes(int64_t B, int64_t T, int64_t H) {
+    return (size_t)chunk_count(B, T, H) * CK_STATE_BYTES;
+}
+
+// Carve the checkpoint buffer into its three arrays.
+inline void chunk_bind_checkpoint(ChunkArgs &a, void *ck) {
+    const int64_t n = (int64_t)a.B * a.H * a.nc;
+    char *p = static_cast<char *>(ck);
+    a.ck_state = reinterpret_cast<float *>(p);
+    a.ck_t = reinterpret_cast<uint16_t *>(p + n * CK_STATE_BYTES);
+    a.ck_gate = reinterpret_cast<GateBlock *>(p + n * (CK_STATE_BYTES + CK_T_BYTES));
+}
+
+hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream);
+hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream);
+
+}  // namespace gdn2

@@ -32,12 +32,9 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t x) {
     return __uint_as_float(((uint32_t)x) << 16);
 }
 
-// Round to nearest even; NaN stays a quiet NaN.
+// Round to nearest even (gfx950 v_cvt_pk_bf16_f32; NaN stays NaN).
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (bf16_t)(u >> 16);
+    return __builtin_bit_cast(bf16_t, static_cast<__bf16>(f));
 }
 
 template <typename T> struct Elem;
