@@ -341,7 +341,7 @@ int gdn_scalar_backward(const gdn2_shape *shape, int chunk, const gdn2_view *q,
                         "chunked path (chunk 64, bf16, d_k = d_v = 64)");
         ChunkArgs c = chunk_args(shape, q, k, v, beta, g, valid, reset);
         chunk_bind_checkpoint(c, const_cast<void *>(checkpoint));
-        c.ws_dstate = (float *)workspace;
+        chunk_bind_workspace(c, workspace);
         if (d_output && d_output->data) {
             c.dout = (const uint16_t *)d_output->data;
             for (int d = 0; d < 3; ++d) c.ds[d] = d_output->stride[d];

@@ -17,11 +17,21 @@ struct GateBlock {
     int seg[CHUNK];
 };
 
-// Per-chunk private storage handed from the forward to the backward.
-constexpr size_t CK_STATE_BYTES = CHUNK_D * CHUNK_D * sizeof(float);    // S at chunk start
-constexpr size_t CK_T_BYTES = CHUNK * CHUNK * sizeof(uint16_t);          // T = (I + A)^-1, bf16
+// Per-chunk private storage handed from the forward to the backward: S at the
+// chunk start (f32, stored transposed: S^T row-major), T = (I + A)^-1 (bf16),
+// the gate block; plus the chunk's affine state map S_next = M S + N (M bf16
+// row-major, N f32 transposed), a forward temporary.  Transposed f32 matrices
+// let each MFMA lane move its four accumulator rows with one 16-byte access.
+constexpr size_t CK_STATE_BYTES = CHUNK_D * CHUNK_D * sizeof(float);
+constexpr size_t CK_T_BYTES = CHUNK * CHUNK * sizeof(uint16_t);
 constexpr size_t CK_GATE_BYTES = sizeof(GateBlock);
-constexpr size_t CK_CHUNK_BYTES = CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES;
+constexpr size_t CK_MAP_M_BYTES = CHUNK_D * CHUNK_D * sizeof(uint16_t);
+constexpr size_t CK_MAP_N_BYTES = CHUNK_D * CHUNK_D * sizeof(float);
+constexpr size_t CK_CHUNK_BYTES =
+    CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES + CK_MAP_M_BYTES + CK_MAP_N_BYTES;
+// Backward workspace per chunk: dS at the chunk end (f32, transposed) and the
+// adjoint map (same layouts as the forward map).
+constexpr size_t WS_CHUNK_BYTES = CK_STATE_BYTES + CK_MAP_M_BYTES + CK_MAP_N_BYTES;
 
 struct ChunkArgs {
     int B, T, H, nc;
@@ -37,6 +47,8 @@ struct ChunkArgs {
     float *ck_state;
     uint16_t *ck_t;
     GateBlock *ck_gate;
+    uint16_t *map_m;  // affine map of the pass being run (forward: checkpoint; backward: workspace)
+    float *map_n;
     // backward
     const uint16_t *dout;
     int64_t ds[3];
@@ -44,6 +56,8 @@ struct ChunkArgs {
     void *dq, *dk, *dv;
     float *dbeta, *dg, *dinitial;
     float *ws_dstate;  // [B*H*nc] adjoint of the state at each chunk end
+    uint16_t *ws_m;    // backward affine map dS_start = M dS_end + N
+    float *ws_n;
 };
 
 inline bool chunk_eligible_shape(const gdn2_shape *s, int chunk) {
@@ -59,7 +73,7 @@ inline size_t chunk_checkpoint_bytes(int64_t B, int64_t T, int64_t H) {
 }
 
 inline size_t chunk_workspace_bytes(int64_t B, int64_t T, int64_t H) {
-    return (size_t)chunk_count(B, T, H) * CK_STATE_BYTES;
+    return (size_t)chunk_count(B, T, H) * WS_CHUNK_BYTES;
 }
 
 // Carve the checkpoint buffer into its three arrays.
@@ -69,6 +83,18 @@ inline void chunk_bind_checkpoint(ChunkArgs &a, void *ck) {
     a.ck_state = reinterpret_cast<float *>(p);
     a.ck_t = reinterpret_cast<uint16_t *>(p + n * CK_STATE_BYTES);
     a.ck_gate = reinterpret_cast<GateBlock *>(p + n * (CK_STATE_BYTES + CK_T_BYTES));
+    a.map_m = reinterpret_cast<uint16_t *>(p + n * (CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES));
+    a.map_n = reinterpret_cast<float *>(
+        p + n * (CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES + CK_MAP_M_BYTES));
+}
+
+// Carve the backward workspace.
+inline void chunk_bind_workspace(ChunkArgs &a, void *ws) {
+    const int64_t n = (int64_t)a.B * a.H * a.nc;
+    char *p = static_cast<char *>(ws);
+    a.ws_dstate = reinterpret_cast<float *>(p);
+    a.ws_m = reinterpret_cast<uint16_t *>(p + n * CK_STATE_BYTES);
+    a.ws_n = reinterpret_cast<float *>(p + n * (CK_STATE_BYTES + CK_MAP_M_BYTES));
 }
 
 hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream);

@@ -221,24 +221,16 @@ __device__ void ut_inverse(const float *Af, float *Tf, float (*Xs)[16 * LDX], in
 }
 
 struct PrepSmem {
-    uint16_t Ks[TILE];
-    float Af[C * LDF];
-    float Tf[C * LDF];
-    float Xs[4][16 * LDX];
+    uint16_t slot[4][TILE];  // K rows (then T), (beta gam K)^T, (lam K)^T, (beta V)^T
+    union {
+        struct {
+            float Af[C * LDF];
+            float Tf[C * LDF];
+            float Xs[4][16 * LDX];
+        } inv;
+        uint16_t wu[4][TILE];  // W^T hi/lo, U^T hi/lo once the inverse is done
+    } u;
     GateLds gl;
-};
-
-struct StateSmem {
-    uint16_t Ks[TILE];  // [t][i]
-    uint16_t Kl[TILE];  // [i][t] = lam_t k_t[i]
-    uint16_t Vt[TILE];  // [j][t]; then the low half of R^T (in place)
-    uint16_t Tb[TILE];  // [t][s]
-    uint16_t St[TILE];  // [j][i] = S0[i][j]
-    uint16_t Rt[TILE];  // [j][t] high half of R^T
-    uint16_t Dt[TILE];  // [j][t] high half of delta^T
-    uint16_t Dl[TILE];  // low half
-    float gam[C], beta[C];
-    float gamC;
 };
 
 struct OutSmem {
@@ -248,27 +240,35 @@ struct OutSmem {
     float dd[2][C];
 };
 
-// Chunk-start state, transposed to bf16 St[j][i], from a row-major f32 64x64.
-__device__ __forceinline__ void load_state_t(uint16_t *St, const float *S0, int tid) {
-    const int i = tid >> 3, j0 = 8 * (tid & 7);
-    const float4 *src = reinterpret_cast<const float4 *>(S0 + i * D + j0);
+// Chunk-start state as the bf16 tile St[j][i] = S[i][j], from the transposed
+// f32 checkpoint layout (S^T row-major, which is also St's layout).
+__device__ __forceinline__ void load_state_t(uint16_t *St, const float *S0t, int tid) {
+    const int j = tid >> 3, i0 = 8 * (tid & 7);
+    const float4 *src = reinterpret_cast<const float4 *>(S0t + j * D + i0);
     const float4 v0 = src[0], v1 = src[1];
-    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) St[(j0 + e) * LDB + i] = bf16_bits(v[e]);
+    *reinterpret_cast<uint4 *>(&St[j * LDB + i0]) =
+        make_uint4(bf16_pack2(v0.x, v0.y), bf16_pack2(v0.z, v0.w), bf16_pack2(v1.x, v1.y),
+                   bf16_pack2(v1.z, v1.w));
 }
 
 }  // namespace
 
-// ---- prep: gates and the UT inverse of every chunk ----------------------------
+// ---- prep: gates, the UT inverse and the affine state map of every chunk -------
+// W = T diag(beta gam) K, U = T diag(beta) V, and the chunk's state map
+//   S_C = A S0 + B,  A = gam_63 I - (lam K)^T W,  B = (lam K)^T U.
 __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
     __shared__ PrepSmem sm;
+    uint16_t *Ks = sm.slot[0], *KBGt = sm.slot[1], *KLt = sm.slot[2], *VBt = sm.slot[3];
+    uint16_t *Tb = sm.slot[0];  // over K once A is formed
+    uint16_t *Wt = sm.u.wu[0], *Wtl = sm.u.wu[1], *Ut = sm.u.wu[2], *Utl = sm.u.wu[3];
     const int tid = threadIdx.x, w = tid >> 6;
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tg = c * C + t;
+    const int tm = w >> 1, tn0 = 2 * (w & 1);
     const bool inb = tg < a.T;
     // Every load issued up front; masks are applied once the values arrive.
     const uint4 kraw = load8(a.k, a.ks, b, tg, h, cb, inb);
+    const uint4 vraw = load8(a.v, a.vs, b, tg, h, cb, inb);
     const float vld = inb ? ld4<float>(a.valid, b, tg, 0, 0) : 0.f;
     float rst = 0.f, gt = 0.f, bt = 0.f;
     if (w == 0 && inb) {
@@ -277,7 +277,8 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         bt = ld4<float>(a.beta, b, tg, h, 0);
     }
     const bool on = vld != 0.f;
-    put_row8(sm.Ks, t, cb, mask8(kraw, on));
+    const uint4 k8 = mask8(kraw, on), v8 = mask8(vraw, on);
+    put_row8(Ks, t, cb, k8);
     if (w == 0) {
         const float G = wave_scan_add(on ? gt : 0.f);
         const int seg = wave_scan_add((on && rst != 0.f) ? 1 : 0);
@@ -290,162 +291,206 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         gb->seg[t] = seg;
     }
     __syncthreads();
+    {  // scaled transposes of K and V for the W/U/A/B products
+        const float be = sm.gl.beta[t], ga = sm.gl.gam[t], la = sm.gl.lam[t];
+        Pack8 kp, vp;
+        kp.u = k8;
+        vp.u = v8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float kf = bf16_val(kp.h[e]), vf = bf16_val(vp.h[e]);
+            KBGt[(8 * cb + e) * LDB + t] = bf16_bits(be * ga * kf);
+            KLt[(8 * cb + e) * LDB + t] = bf16_bits(la * kf);
+            VBt[(8 * cb + e) * LDB + t] = bf16_bits(be * vf);
+        }
+    }
     // A = strict_lower(beta_t Gam_ts k_t.k_s) in f32 (tiles with tn <= tm only).
-    {
-        const int tm = w >> 1, tn0 = 2 * (w & 1);
-        if (tn0 <= tm) {
-            f32x4 kk[2] = {zero4(), zero4()};
-            gemm2(kk, &sm.Ks[(16 * tm) * LDB], sm.Ks, tn0);
-            const RowGates rg = row_gates(sm.gl, tm);
+    if (tn0 <= tm) {
+        f32x4 kk[2] = {zero4(), zero4()};
+        gemm2(kk, &Ks[(16 * tm) * LDB], Ks, tn0);
+        const RowGates rg = row_gates(sm.gl, tm);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int ss = 16 * (tn0 + j) + acc_col();
-                const float Gs = sm.gl.G[ss];
-                const int sgs = sm.gl.seg[ss];
+        for (int j = 0; j < 2; ++j) {
+            const int ss = 16 * (tn0 + j) + acc_col();
+            const float Gs = sm.gl.G[ss];
+            const int sgs = sm.gl.seg[ss];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int tt = 16 * tm + acc_row(i);
-                    const float v = (ss < tt && rg.seg[i] == sgs)
-                                        ? rg.beta[i] * __expf(rg.G[i] - Gs) * kk[j][i]
-                                        : 0.f;
-                    sm.Af[tt * LDF + ss] = v;
-                }
+            for (int i = 0; i < 4; ++i) {
+                const int tt = 16 * tm + acc_row(i);
+                sm.u.inv.Af[tt * LDF + ss] = (ss < tt && rg.seg[i] == sgs)
+                                                 ? rg.beta[i] * __expf(rg.G[i] - Gs) * kk[j][i]
+                                                 : 0.f;
             }
         }
     }
     __syncthreads();
-    ut_inverse(sm.Af, sm.Tf, sm.Xs, w);
-    // T (bf16, row-major, zero above the diagonal) to the checkpoint.
+    ut_inverse(sm.u.inv.Af, sm.u.inv.Tf, sm.u.inv.Xs, w);
+    // T (bf16, row-major, zero above the diagonal): LDS operand and checkpoint.
     {
         const int r = tid >> 3, c0 = 8 * (tid & 7);
         uint32_t pk[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int s0 = c0 + 2 * e;
-            pk[e] = bf16_pack2(s0 <= r ? sm.Tf[r * LDF + s0] : 0.f,
-                               s0 + 1 <= r ? sm.Tf[r * LDF + s0 + 1] : 0.f);
+            pk[e] = bf16_pack2(s0 <= r ? sm.u.inv.Tf[r * LDF + s0] : 0.f,
+                               s0 + 1 <= r ? sm.u.inv.Tf[r * LDF + s0 + 1] : 0.f);
         }
-        *reinterpret_cast<uint4 *>(a.ck_t + (int64_t)ci * C * C + r * C + c0) =
-            make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        const uint4 v = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        *reinterpret_cast<uint4 *>(a.ck_t + (int64_t)ci * C * C + r * C + c0) = v;
+        *reinterpret_cast<uint4 *>(&Tb[r * LDB + c0]) = v;
+    }
+    __syncthreads();
+    // W = T (beta gam K), U = T (beta V): stored transposed as hi/lo pairs.
+    {
+        f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
+        gemm2(x, &Tb[(16 * tm) * LDB], KBGt, tn0);
+        gemm2(y, &Tb[(16 * tm) * LDB], VBt, tn0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            store_tile_t_split(&Wt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Wtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
+            store_tile_t_split(&Ut[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Utl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, y[j]);
+        }
+    }
+    __syncthreads();
+    // A = gam_63 I - (lam K)^T W (bf16, row-major), B = (lam K)^T U (f32).
+    {
+        f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
+        gemm2(x, &KLt[(16 * tm) * LDB], Wt, tn0);
+        gemm2(x, &KLt[(16 * tm) * LDB], Wtl, tn0);
+        gemm2(y, &KLt[(16 * tm) * LDB], Ut, tn0);
+        gemm2(y, &KLt[(16 * tm) * LDB], Utl, tn0);
+        const float gC = sm.gl.gamC;
+        uint16_t *Am = a.map_m + (int64_t)ci * D * D;
+        float *Bt = a.map_n + (int64_t)ci * D * D;  // B transposed: Bt[col][row]
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int cc = 16 * (tn0 + j) + acc_col();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 16 * tm + acc_row(i);
+                Am[r * D + cc] = bf16_bits((r == cc ? gC : 0.f) - x[j][i]);
+            }
+            *reinterpret_cast<float4 *>(&Bt[cc * D + 16 * tm + acc_row(0)]) =
+                make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
+        }
     }
 }
 
-// ---- state: the sequential inter-chunk recurrence -------------------------------
-__global__ void __launch_bounds__(NT) chunk_state_kernel(ChunkArgs a) {
-    __shared__ StateSmem sm;
-    const int tid = threadIdx.x, w = tid >> 6;
-    const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
-    const int t = tid & 63, cb = tid >> 6;
-    const int tm = w >> 1, tn0 = 2 * (w & 1);
+// ---- affine scan: the only sequential part -----------------------------------
+// X_{next} = M_c X + N_c over the chunks of one (batch, head): forward
+// (S_C = A S0 + B, c ascending, X0 = initial state) or backward
+// (dS0 = M dS_C + N, c descending, X0 = adjoint of the final state).  X before
+// each step goes to ckpt[c], transposed (X^T row-major).  Columns of X evolve independently, so each of the
+// four waves owns 16 columns; M fragments come straight from global memory
+// (prefetched one chunk ahead), X is re-packed through a wave-private LDS tile
+// into the bf16 hi/lo operand of the next product.
+struct AffineArgs {
+    int nc, B, H;
+    const uint16_t *m;
+    const float *n;
+    float *ckpt;
+    View x0;          // [B,H,64,64] strided (data may be null: zero)
+    float *xout;      // [B,H,64,64] dense (may be null)
+    int reverse;
+};
 
-    f32x4 Sacc[2];
+template <int SL, typename F, typename Gt>
+__device__ __forceinline__ void affine_step(int s, const AffineArgs &p, int bh, int j,
+                                            f32x4 (&X)[4], bf16x8_t (&mf)[3][4][2],
+                                            f32x4 (&nf)[3][4], uint16_t *xh, uint16_t *xl,
+                                            F &fetch, Gt &chunk_of) {
+    const int c = chunk_of(s);
+    float *ck = p.ckpt + ((int64_t)bh * p.nc + c) * D * D;  // X^T
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int tm = 0; tm < 4; ++tm) {
+        *reinterpret_cast<float4 *>(&ck[j * D + 16 * tm + acc_row(0)]) =
+            make_float4(X[tm][0], X[tm][1], X[tm][2], X[tm][3]);
+        store_tile_t_split(xh + 16 * tm, xl + 16 * tm, LDB, X[tm]);  // [col][row]
+    }
+    __syncthreads();
+    f32x4 Y[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            Sacc[j][i] = a.initial.data ? ld4<float>(a.initial, b, h, 16 * tm + acc_row(i),
-                                                     16 * (tn0 + j) + acc_col())
-                                        : 0.f;
-
-    // Register prefetch of one chunk: K/V rows, a T row segment, gate scalars.
-    // None of these loads depends on another, so one chunk costs one latency.
-    uint4 kr, vr, tr;
-    float pG, pBeta, pVal, pG63;
-    int pSeg, pSeg63;
-    auto fetch = [&](int c) {
-        const int64_t ci = (int64_t)bh * a.nc + c;
-        const GateBlock *gb = a.ck_gate + ci;
-        const int tg = c * C + t;
-        kr = load8(a.k, a.ks, b, tg, h, cb, tg < a.T);
-        vr = load8(a.v, a.vs, b, tg, h, cb, tg < a.T);
-        tr = *reinterpret_cast<const uint4 *>(a.ck_t + ci * C * C + (tid >> 3) * C + 8 * (tid & 7));
-        pG = gb->G[t];
-        pBeta = gb->beta[t];
-        pVal = gb->val[t];
-        pSeg = gb->seg[t];
-        pG63 = gb->G[63];
-        pSeg63 = gb->seg[63];
-    };
-    fetch(0);
-    for (int c = 0; c < a.nc; ++c) {
-        const int64_t ci = (int64_t)bh * a.nc + c;
-        // Stage the prefetched chunk.
-        {
-            const bool on = pVal != 0.f;
-            const uint4 k8 = mask8(kr, on);
-            put_row8(sm.Ks, t, cb, k8);
-            put_col8(sm.Vt, t, cb, mask8(vr, on));
-            const float lam = pSeg == pSeg63 ? __expf(pG63 - pG) : 0.f;
-            Pack8 kp;
-            kp.u = k8;
+    for (int tm = 0; tm < 4; ++tm) Y[tm] = nf[SL][tm];
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                sm.Kl[(8 * cb + e) * LDB + t] = bf16_bits(lam * bf16_val(kp.h[e]));
-            *reinterpret_cast<uint4 *>(&sm.Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = tr;
-            if (w == 0) {
-                sm.gam[t] = pSeg == 0 ? __expf(pG) : 0.f;
-                sm.beta[t] = pBeta;
-                if (t == 0) sm.gamC = pSeg63 == 0 ? __expf(pG63) : 0.f;
-            }
+    for (int kk = 0; kk < 2; ++kk) {
+        const bf16x8_t bh_ = frag(xh, LDB, 32 * kk), bl_ = frag(xl, LDB, 32 * kk);
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) {
+            Y[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][tm][kk], bh_, Y[tm], 0, 0, 0);
+            Y[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][tm][kk], bl_, Y[tm], 0, 0, 0);
         }
-        // Chunk-start state: checkpoint (f32) and the bf16 transposed operand.
-        float *ck = a.ck_state + ci * D * D;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                ck[(16 * tm + acc_row(i)) * D + 16 * (tn0 + j) + acc_col()] = Sacc[j][i];
-            store_tile_t(&sm.St[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, Sacc[j]);
-        }
-        if (c + 1 < a.nc) fetch(c + 1);
-        __syncthreads();
-        // R = beta (V - gam K S0), stored transposed (hi; lo over V^T in place).
-        {
-            f32x4 x[2] = {zero4(), zero4()};
-            gemm2(x, &sm.Ks[(16 * tm) * LDB], sm.St, tn0);
-            const int r0 = 16 * tm + 4 * (lane_id() >> 4);
-            const float4 be = *reinterpret_cast<const float4 *>(&sm.beta[r0]);
-            const float4 ga = *reinterpret_cast<const float4 *>(&sm.gam[r0]);
-            const float bev[4] = {be.x, be.y, be.z, be.w}, gav[4] = {ga.x, ga.y, ga.z, ga.w};
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                uint16_t *vt = &sm.Vt[(16 * (tn0 + j)) * LDB + 16 * tm];
-                float vv[4];
-                ld4_bf16(vt + acc_col() * LDB + 4 * (lane_id() >> 4), vv);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) x[j][i] = bev[i] * (vv[i] - gav[i] * x[j][i]);
-                // Each lane overwrites exactly the V^T entries it just read.
-                store_tile_t_split(&sm.Rt[(16 * (tn0 + j)) * LDB + 16 * tm], vt, LDB, x[j]);
-            }
-        }
-        __syncthreads();
-        // delta = T R.
-        {
-            f32x4 x[2] = {zero4(), zero4()};
-            gemm2(x, &sm.Tb[(16 * tm) * LDB], sm.Rt, tn0);
-            gemm2(x, &sm.Tb[(16 * tm) * LDB], sm.Vt, tn0);
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                store_tile_t_split(&sm.Dt[(16 * (tn0 + j)) * LDB + 16 * tm],
-                                   &sm.Dl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
-        }
-        __syncthreads();
-        // S_C = gam_C S0 + (lam K)^T delta, in the accumulators.
-        const float gC = sm.gamC;
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) Sacc[j][i] *= gC;
-        gemm2(Sacc, &sm.Kl[(16 * tm) * LDB], sm.Dt, tn0);
-        gemm2(Sacc, &sm.Kl[(16 * tm) * LDB], sm.Dl, tn0);
-        __syncthreads();
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int tm = 0; tm < 4; ++tm) X[tm] = Y[tm];
+    if (s + 3 < p.nc) fetch(chunk_of(s + 3), mf[SL], nf[SL]);
+    __syncthreads();
+}
+
+// One wave per workgroup: wave w of head bh owns state columns 16w..16w+15,
+// which evolve independently (Y = M X acts on columns), so the four column
+// groups of a head run as four workgroups spread over the CUs.
+// NC > 0: the chunk count is a compile-time constant and the chunk loop is
+// straight-line code, so the loads of the three-deep (M, N) ring are waited
+// for one by one; NC == 0 runs any count in a rolled loop.
+template <int NC>
+__global__ void __launch_bounds__(64) affine_scan_kernel(AffineArgs p) {
+    __shared__ uint16_t xs[1][2][16 * LDB];
+    const int w = blockIdx.x & 3, l = lane_id();
+    const int bh = blockIdx.x >> 2, b = bh / p.H, h = bh % p.H;
+    const int j = 16 * w + (l & 15);  // this lane's state column
+    // Three chunks of (M, N) in flight: one global latency spans three steps.
+    bf16x8_t mf[3][4][2];
+    f32x4 nf[3][4];
+    auto chunk_of = [&](int s) { return p.reverse ? p.nc - 1 - s : s; };
+    auto fetch = [&](int c, bf16x8_t (&m)[4][2], f32x4 (&n)[4]) {
+        const int64_t ci = (int64_t)bh * p.nc + c;
+        const uint16_t *M = p.m + ci * D * D;
+        const float *N = p.n + ci * D * D;
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) {
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+                m[tm][kk] = __builtin_bit_cast(
+                    bf16x8_t, *reinterpret_cast<const uint4 *>(M + (16 * tm + (l & 15)) * D +
+                                                               32 * kk + 8 * (l >> 4)));
+            const float4 nv = *reinterpret_cast<const float4 *>(&N[j * D + 16 * tm + acc_row(0)]);
+            n[tm] = f32x4{nv.x, nv.y, nv.z, nv.w};
+        }
+    };
+    if (0 < p.nc) fetch(chunk_of(0), mf[0], nf[0]);
+    // X loads sit between the first and later fetches so that waiting for
+    // them stays within the 63 outstanding loads the wait counter tracks.
+    f32x4 X[4];
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            a.final_state[((int64_t)bh * D + 16 * tm + acc_row(i)) * D + 16 * (tn0 + j) +
-                          acc_col()] = Sacc[j][i];
+            X[tm][i] = p.x0.data ? ld4<float>(p.x0, b, h, 16 * tm + acc_row(i), j) : 0.f;
+    if (1 < p.nc) fetch(chunk_of(1), mf[1], nf[1]);
+    if (2 < p.nc) fetch(chunk_of(2), mf[2], nf[2]);
+    uint16_t *xh = xs[0][0], *xl = xs[0][1];
+    if constexpr (NC > 0) {
+#pragma unroll
+        for (int s = 0; s < NC; ++s) {
+            if (s % 3 == 0) affine_step<0>(s, p, bh, j, X, mf, nf, xh, xl, fetch, chunk_of);
+            if (s % 3 == 1) affine_step<1>(s, p, bh, j, X, mf, nf, xh, xl, fetch, chunk_of);
+            if (s % 3 == 2) affine_step<2>(s, p, bh, j, X, mf, nf, xh, xl, fetch, chunk_of);
+        }
+    } else {
+        for (int s = 0; s < p.nc; s += 3) {
+            affine_step<0>(s, p, bh, j, X, mf, nf, xh, xl, fetch, chunk_of);
+            if (s + 1 < p.nc) affine_step<1>(s + 1, p, bh, j, X, mf, nf, xh, xl, fetch, chunk_of);
+            if (s + 2 < p.nc) affine_step<2>(s + 2, p, bh, j, X, mf, nf, xh, xl, fetch, chunk_of);
+        }
+    }
+    if (p.xout)
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                p.xout[((int64_t)bh * D + 16 * tm + acc_row(i)) * D + j] = X[tm][i];
 }
 
 // ---- out: outputs and scores of every chunk --------------------------------------
@@ -576,14 +621,43 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
     }
 }
 
+// Straight-line instantiations cover sequences up to 16 chunks (1024 tokens).
+static void launch_affine_scan(const AffineArgs &p, hipStream_t stream) {
+    const dim3 grid(p.B * p.H * 4), block(64);
+    switch (p.nc) {
+#define GDN2_AFFINE_CASE(n) \
+    case n: hipLaunchKernelGGL(affine_scan_kernel<n>, grid, block, 0, stream, p); return;
+        GDN2_AFFINE_CASE(1) GDN2_AFFINE_CASE(2) GDN2_AFFINE_CASE(3) GDN2_AFFINE_CASE(4)
+        GDN2_AFFINE_CASE(5) GDN2_AFFINE_CASE(6) GDN2_AFFINE_CASE(7) GDN2_AFFINE_CASE(8)
+        GDN2_AFFINE_CASE(9) GDN2_AFFINE_CASE(10) GDN2_AFFINE_CASE(11) GDN2_AFFINE_CASE(12)
+        GDN2_AFFINE_CASE(13) GDN2_AFFINE_CASE(14) GDN2_AFFINE_CASE(15) GDN2_AFFINE_CASE(16)
+#undef GDN2_AFFINE_CASE
+    default: hipLaunchKernelGGL(affine_scan_kernel<0>, grid, block, 0, stream, p);
+    }
+}
+
+static AffineArgs affine_args(const ChunkArgs &a) {
+    AffineArgs p{};
+    p.nc = a.nc;
+    p.B = a.B;
+    p.H = a.H;
+    return p;
+}
+
 hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream) {
     const int nchunks = a.B * a.H * a.nc;
     hipLaunchKernelGGL(chunk_prep_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
-    hipLaunchKernelGGL(chunk_state_kernel, dim3(a.B * a.H), dim3(NT), 0, stream, a);
+    AffineArgs p = affine_args(a);
+    p.m = a.map_m;
+    p.n = a.map_n;
+    p.ckpt = a.ck_state;
+    p.x0 = a.initial;
+    p.xout = a.final_state;
+    p.reverse = 0;
+    launch_affine_scan(p, stream);
     hipLaunchKernelGGL(chunk_out_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
     return hipGetLastError();
 }
-
 
 // ---- backward -------------------------------------------------------------------
 // Given the chunk-start state S0 (forward checkpoint) and the adjoint dS of the
@@ -607,8 +681,8 @@ hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream) {
 
 namespace {
 
-struct BStateSmem {
-    uint16_t slot[13][TILE];
+struct BPrepSmem {
+    uint16_t slot[14][TILE];
     GateLds gl;
     float kk[NW][C];
     float dd[2][C];
@@ -645,18 +719,19 @@ __device__ __forceinline__ float col_reduce(const f32x4 &x) {
     return s;
 }
 
-// Stage a row-major f32 64x64 matrix (row i = tid>>3, 8 columns) into the
-// bf16 transposed tile dstT[j][i] and (optionally) the row-major tile dst[i][j].
+// Stage a 64x64 f32 matrix S, held transposed (S^T row-major, the checkpoint
+// layout; this thread's part is row j = tid>>3 of S^T, 8 entries), into the bf16
+// tile dstT[j][i] = S[i][j] and (optionally) the row-major tile dst[i][j].
 __device__ __forceinline__ void stage_mat(uint16_t *dstT, uint16_t *dst, const float4 (&v)[2],
                                           int tid) {
-    const int i = tid >> 3, j0 = 8 * (tid & 7);
+    const int j = tid >> 3, i0 = 8 * (tid & 7);
     const float x[8] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) dstT[(j0 + e) * LDB + i] = bf16_bits(x[e]);
+    *reinterpret_cast<uint4 *>(&dstT[j * LDB + i0]) =
+        make_uint4(bf16_pack2(x[0], x[1]), bf16_pack2(x[2], x[3]), bf16_pack2(x[4], x[5]),
+                   bf16_pack2(x[6], x[7]));
     if (dst)
-        *reinterpret_cast<uint4 *>(&dst[i * LDB + j0]) =
-            make_uint4(bf16_pack2(x[0], x[1]), bf16_pack2(x[2], x[3]), bf16_pack2(x[4], x[5]),
-                       bf16_pack2(x[6], x[7]));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[(i0 + e) * LDB + j] = bf16_bits(x[e]);
 }
 
 __device__ __forceinline__ void load_mat(float4 (&v)[2], const float *src, int tid) {
@@ -671,180 +746,157 @@ __device__ __forceinline__ void store_grad(void *dst, int64_t idx, float x) {
 
 }  // namespace
 
-__global__ void __launch_bounds__(NT) chunk_bstate_kernel(ChunkArgs a) {
-    __shared__ BStateSmem sm;
-    uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *Vt = sm.slot[2], *Tb = sm.slot[3];
-    uint16_t *Ttb = sm.slot[4], *St = sm.slot[5], *dSt = sm.slot[6], *dOt = sm.slot[7];
-    uint16_t *QGt = sm.slot[8], *KBGt = sm.slot[9], *Rt = sm.slot[10], *Pt = sm.slot[11];
-    uint16_t *Ptl = sm.slot[12];
-    uint16_t *Dd = sm.slot[10], *Ddl = sm.slot[2];  // ddelta^T (hi, lo) after phase B
-    uint16_t *dRt = sm.slot[3];                      // dR^T after phase C
+// The backward state recurrence is affine too: with
+//   X = P^T dO + diag(c) delta,  Y = (gam Q)^T dO,  W = T diag(beta gam) K,
+//   ddelta = X + diag(lam) K dS_C  and  dS0 = gam_63 dS_C + Y - W^T ddelta,
+// so dS0 = M dS_C + N with M = gam_63 I - W^T diag(lam) K and N = Y - W^T X.
+// bprep builds (M, N) for every chunk in parallel.
+__global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
+    __shared__ BPrepSmem sm;
+    uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *Vt = sm.slot[2], *dOt = sm.slot[3];
+    uint16_t *Tb = sm.slot[4], *St = sm.slot[5], *QGt = sm.slot[6], *KBGt = sm.slot[7];
+    uint16_t *KLt = sm.slot[8], *Rt = sm.slot[9], *Pt = sm.slot[10], *Ptl = sm.slot[11];
+    uint16_t *Wt = sm.slot[12], *Wtl = sm.slot[13];
+    uint16_t *Xt = sm.slot[9], *Xtl = sm.slot[2];  // after phase 2
     const int tid = threadIdx.x, w = tid >> 6;
-    const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
+    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
-
-    f32x4 dS[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            dS[j][i] = a.dfinal ? a.dfinal[((int64_t)bh * D + 16 * tm + acc_row(i)) * D +
-                                           16 * (tn0 + j) + acc_col()]
-                                : 0.f;
-
-    for (int c = a.nc - 1; c >= 0; --c) {
-        const int64_t ci = (int64_t)bh * a.nc + c;
-        const int tg = c * C + t;
-        const bool inb = tg < a.T;
-        const GateBlock *gb = a.ck_gate + ci;
+    const int tg = c * C + t;
+    const bool inb = tg < a.T;
+    const GateBlock *gb = a.ck_gate + ci;
+    {
         const uint4 qr = load8(a.q, a.qs, b, tg, h, cb, inb);
         const uint4 kr = load8(a.k, a.ks, b, tg, h, cb, inb);
         const uint4 vr = load8(a.v, a.vs, b, tg, h, cb, inb);
         const uint4 dor = a.dout ? load8(a.dout, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
-        const uint4 trw = *reinterpret_cast<const uint4 *>(a.ck_t + ci * C * C + (tid >> 3) * C +
-                                                          8 * (tid & 7));
+        const uint4 trw = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C +
+                                                          (tid >> 3) * C + 8 * (tid & 7));
         float4 s0[2];
-        load_mat(s0, a.ck_state + ci * D * D, tid);
-        const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
-        const int sg = gb->seg[t];
+        load_mat(s0, a.ck_state + (int64_t)ci * D * D, tid);
+        const float G = gb->G[t], be = gb->beta[t], va = gb->val[t], G63 = gb->G[63];
+        const int sg = gb->seg[t], sg63 = gb->seg[63];
         const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
-        // dS at the chunk end: workspace copy (f32) and the bf16 transposed operand.
-        float *wd = a.ws_dstate + ci * D * D;
+        const bool on = va != 0.f;
+        const float gam = sg == 0 ? __expf(G) : 0.f, lam = sg == sg63 ? __expf(G63 - G) : 0.f;
+        Pack8 qp, kp;
+        qp.u = mask8(qr, on);
+        kp.u = mask8(kr, on);
+        put_row8(Qs, t, cb, qp.u);
+        put_row8(Ks, t, cb, kp.u);
+        put_col8(Vt, t, cb, mask8(vr, on));
+        put_col8(dOt, t, cb, mask8(dor, on));
+        float ksq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float qf = bf16_val(qp.h[e]), kf = bf16_val(kp.h[e]);
+            QGt[(8 * cb + e) * LDB + t] = bf16_bits(gam * qf);
+            KBGt[(8 * cb + e) * LDB + t] = bf16_bits(be * gam * kf);
+            KLt[(8 * cb + e) * LDB + t] = bf16_bits(lam * kf);
+            ksq += kf * kf;
+        }
+        sm.kk[cb][t] = ksq;
+        *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
+        stage_mat(St, nullptr, s0, tid);
+        if (w == 0) {
+            gates_derive(sm.gl, G, be, va, sg);
+            sm.dsc[t] = dsc;
+        }
+    }
+    __syncthreads();
+    const RowGates rg = row_gates(sm.gl, tm);
+    const int r0 = 16 * tm + 4 * (lane_id() >> 4);
+    // Phase 1: R (Rt, lo over V^T), P^T (hi/lo), Y in registers, W^T (hi/lo).
+    f32x4 yacc[2] = {zero4(), zero4()};
+    {
+        f32x4 x[2] = {zero4(), zero4()}, pq[2] = {zero4(), zero4()}, wa[2] = {zero4(), zero4()};
+        gemm2(x, &Ks[(16 * tm) * LDB], St, tn0);
+        if (tn0 <= tm) gemm2(pq, &Qs[(16 * tm) * LDB], Ks, tn0);
+        gemm2(yacc, &QGt[(16 * tm) * LDB], dOt, tn0);
+        gemm2(wa, &Tb[(16 * tm) * LDB], KBGt, tn0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                wd[(16 * tm + acc_row(i)) * D + 16 * (tn0 + j) + acc_col()] = dS[j][i];
-            store_tile_t(&dSt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, dS[j]);
-        }
-        stage_mat(St, nullptr, s0, tid);
-        {
-            const bool on = va != 0.f;
-            const float gam = sg == 0 ? __expf(G) : 0.f;
-            Pack8 qp, kp;
-            qp.u = mask8(qr, on);
-            kp.u = mask8(kr, on);
-            put_row8(Qs, t, cb, qp.u);
-            put_row8(Ks, t, cb, kp.u);
-            put_col8(Vt, t, cb, mask8(vr, on));
-            put_col8(dOt, t, cb, mask8(dor, on));
-            float ksq = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float qf = bf16_val(qp.h[e]), kf = bf16_val(kp.h[e]);
-                QGt[(8 * cb + e) * LDB + t] = bf16_bits(gam * qf);
-                KBGt[(8 * cb + e) * LDB + t] = bf16_bits(-be * gam * kf);
-                ksq += kf * kf;
-            }
-            sm.kk[cb][t] = ksq;
-            Pack8 tp;
-            tp.u = trw;
-            *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) Ttb[(8 * (tid & 7) + e) * LDB + (tid >> 3)] = tp.h[e];
-            if (w == 0) {
-                gates_derive(sm.gl, G, be, va, sg);
-                sm.dsc[t] = dsc;
-            }
-        }
-        __syncthreads();
-        // Phase A: R (Rt hi, lo over V^T), P^T (hi/lo), lam K dS^T in registers.
-        const RowGates rg = row_gates(sm.gl, tm);
-        f32x4 kds[2] = {zero4(), zero4()};
-        {
-            f32x4 x[2] = {zero4(), zero4()};
-            gemm2(x, &Ks[(16 * tm) * LDB], St, tn0);
-            gemm2(kds, &Ks[(16 * tm) * LDB], dSt, tn0);
-            f32x4 pq[2] = {zero4(), zero4()};
-            if (tn0 <= tm) gemm2(pq, &Qs[(16 * tm) * LDB], Ks, tn0);
-            const float4 lm = lds_f4(&sm.gl.lam[16 * tm + 4 * (lane_id() >> 4)]);
-            const float lmv[4] = {lm.x, lm.y, lm.z, lm.w};
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int ss = 16 * (tn0 + j) + acc_col();
-                const float Gs = sm.gl.G[ss];
-                const int sgs = sm.gl.seg[ss];
-                uint16_t *vt = &Vt[(16 * (tn0 + j)) * LDB + 16 * tm];
-                float vv[4];
-                ld4_bf16(vt + acc_col() * LDB + 4 * (lane_id() >> 4), vv);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int tt = 16 * tm + acc_row(i);
-                    x[j][i] = rg.beta[i] * (vv[i] - rg.gam[i] * x[j][i]);
-                    pq[j][i] *= (ss <= tt && rg.seg[i] == sgs) ? __expf(rg.G[i] - Gs) : 0.f;
-                    kds[j][i] *= lmv[i];
-                }
-                store_tile_t_split(&Rt[(16 * (tn0 + j)) * LDB + 16 * tm], vt, LDB, x[j]);
-                store_tile_t_split(&Pt[(16 * (tn0 + j)) * LDB + 16 * tm],
-                                   &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq[j]);
-            }
-        }
-        __syncthreads();
-        // Phase B: delta = T R (registers) and |delta_s|^2.
-        f32x4 dl[2] = {zero4(), zero4()};
-        {
-            gemm2(dl, &Tb[(16 * tm) * LDB], Rt, tn0);
-            gemm2(dl, &Tb[(16 * tm) * LDB], Vt, tn0);
-            float p[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) p[i] = dl[0][i] * dl[0][i] + dl[1][i] * dl[1][i];
-            row_reduce_store(p, sm.dd[w & 1], tm);
-        }
-        __syncthreads();
-        // Phase C: ddelta = P^T dO + lam K dS^T + c delta, stored transposed (hi/lo).
-        {
-            float cs[4];
+            const int ss = 16 * (tn0 + j) + acc_col();
+            const float Gs = sm.gl.G[ss];
+            const int sgs = sm.gl.seg[ss];
+            uint16_t *vt = &Vt[(16 * (tn0 + j)) * LDB + 16 * tm];
+            float vv[4];
+            ld4_bf16(vt + acc_col() * LDB + 4 * (lane_id() >> 4), vv);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int ss = 16 * tm + acc_row(i);
-                float kk = 0.f;
-#pragma unroll
-                for (int q = 0; q < NW; ++q) kk += sm.kk[q][ss];
-                const float nk = sqrtf(kk), nd = sqrtf(sm.dd[0][ss] + sm.dd[1][ss]);
-                cs[i] = (nk > 0.f && nd > 0.f) ? sm.dsc[ss] * nk / nd : 0.f;
+                const int tt = 16 * tm + acc_row(i);
+                x[j][i] = rg.beta[i] * (vv[i] - rg.gam[i] * x[j][i]);
+                pq[j][i] *= (ss <= tt && rg.seg[i] == sgs) ? __expf(rg.G[i] - Gs) : 0.f;
             }
-            f32x4 x[2] = {kds[0], kds[1]};
-            gemm2(x, &Pt[(16 * tm) * LDB], dOt, tn0);
-            gemm2(x, &Ptl[(16 * tm) * LDB], dOt, tn0);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) x[j][i] += cs[i] * dl[j][i];
-                store_tile_t_split(&Dd[(16 * (tn0 + j)) * LDB + 16 * tm],
-                                   &Ddl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
-            }
+            store_tile_t_split(&Rt[(16 * (tn0 + j)) * LDB + 16 * tm], vt, LDB, x[j]);
+            store_tile_t_split(&Pt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq[j]);
+            store_tile_t_split(&Wt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Wtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, wa[j]);
         }
-        __syncthreads();
-        // Phase D: dR = T^T ddelta, stored transposed.
-        {
-            f32x4 x[2] = {zero4(), zero4()};
-            gemm2(x, &Ttb[(16 * tm) * LDB], Dd, tn0);
-            gemm2(x, &Ttb[(16 * tm) * LDB], Ddl, tn0);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) store_tile_t(&dRt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
-        }
-        __syncthreads();
-        // Phase E: dS <- gam_63 dS + (gam Q)^T dO - (beta gam K)^T dR.
-        {
-            const float gC = sm.gl.gamC;
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) dS[j][i] *= gC;
-            gemm2(dS, &QGt[(16 * tm) * LDB], dOt, tn0);
-            gemm2(dS, &KBGt[(16 * tm) * LDB], dRt, tn0);
-        }
-        __syncthreads();
     }
-    if (a.dinitial)
+    __syncthreads();
+    // Phase 2: delta = T R (registers, |delta_s|^2); M = gam_63 I - W^T diag(lam) K.
+    f32x4 dl[2] = {zero4(), zero4()};
+    {
+        gemm2(dl, &Tb[(16 * tm) * LDB], Rt, tn0);
+        gemm2(dl, &Tb[(16 * tm) * LDB], Vt, tn0);
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[i] = dl[0][i] * dl[0][i] + dl[1][i] * dl[1][i];
+        row_reduce_store(p, sm.dd[w & 1], tm);
+        f32x4 x[2] = {zero4(), zero4()};
+        gemm2(x, &Wt[(16 * tm) * LDB], KLt, tn0);
+        gemm2(x, &Wtl[(16 * tm) * LDB], KLt, tn0);
+        const float gC = sm.gl.gamC;
+        uint16_t *Mm = a.ws_m + (int64_t)ci * D * D;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                a.dinitial[((int64_t)bh * D + 16 * tm + acc_row(i)) * D + 16 * (tn0 + j) +
-                           acc_col()] = dS[j][i];
+            for (int i = 0; i < 4; ++i) {
+                const int r = 16 * tm + acc_row(i), cc = 16 * (tn0 + j) + acc_col();
+                Mm[r * D + cc] = bf16_bits((r == cc ? gC : 0.f) - x[j][i]);
+            }
+    }
+    __syncthreads();
+    // Phase 3: X = P^T dO + diag(c) delta, stored transposed (hi/lo).
+    {
+        float cs[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ss = r0 + i;
+            float kq = 0.f;
+#pragma unroll
+            for (int q = 0; q < NW; ++q) kq += sm.kk[q][ss];
+            const float nk = sqrtf(kq), nd = sqrtf(sm.dd[0][ss] + sm.dd[1][ss]);
+            cs[i] = (nk > 0.f && nd > 0.f) ? sm.dsc[ss] * nk / nd : 0.f;
+        }
+        f32x4 x[2] = {zero4(), zero4()};
+        gemm2(x, &Pt[(16 * tm) * LDB], dOt, tn0);
+        gemm2(x, &Ptl[(16 * tm) * LDB], dOt, tn0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[j][i] += cs[i] * dl[j][i];
+            store_tile_t_split(&Xt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Xtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
+        }
+    }
+    __syncthreads();
+    // Phase 4: N = Y - W^T X.
+    {
+        f32x4 x[2] = {zero4(), zero4()};
+        gemm2(x, &Wt[(16 * tm) * LDB], Xt, tn0);
+        gemm2(x, &Wt[(16 * tm) * LDB], Xtl, tn0);
+        gemm2(x, &Wtl[(16 * tm) * LDB], Xt, tn0);
+        float *Nt = a.ws_n + (int64_t)ci * D * D;  // N transposed: Nt[col][row]
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            *reinterpret_cast<float4 *>(&Nt[(16 * (tn0 + j) + acc_col()) * D + 16 * tm +
+                                            acc_row(0)]) =
+                make_float4(yacc[j][0] - x[j][0], yacc[j][1] - x[j][1], yacc[j][2] - x[j][2],
+                            yacc[j][3] - x[j][3]);
+    }
 }
-
 __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     __shared__ BGradSmem sm;
     uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *dOs = sm.slot[2], *Qt = sm.slot[3];
@@ -1160,8 +1212,21 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
 }
 
 hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream) {
-    hipLaunchKernelGGL(chunk_bstate_kernel, dim3(a.B * a.H), dim3(NT), 0, stream, a);
-    hipLaunchKernelGGL(chunk_bgrad_kernel, dim3(a.B * a.H * a.nc), dim3(NT), 0, stream, a);
+    const int nchunks = a.B * a.H * a.nc;
+    hipLaunchKernelGGL(chunk_bprep_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
+    AffineArgs p = affine_args(a);
+    p.m = a.ws_m;
+    p.n = a.ws_n;
+    p.ckpt = a.ws_dstate;
+    p.x0.data = a.dfinal;
+    p.x0.s0 = (int64_t)a.H * D * D;
+    p.x0.s1 = D * D;
+    p.x0.s2 = D;
+    p.x0.s3 = 1;
+    p.xout = a.dinitial;
+    p.reverse = 1;
+    launch_affine_scan(p, stream);
+    hipLaunchKernelGGL(chunk_bgrad_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
     return hipGetLastError();
 }
 
