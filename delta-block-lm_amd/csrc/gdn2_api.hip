@@ -33,6 +33,22 @@ int ok() {
     return GDN2_OK;
 }
 
+// Stage timing (gdn2_stage_timing): six stages, an event pair each; the
+// forward records pairs 0-2, the backward pairs 3-5.
+constexpr int kStages = 6;
+const char *const kStageNames[kStages] = {"chunk_prep", "state_scan", "chunk_out",
+                                          "chunk_bprep", "adjoint_scan", "chunk_bgrad"};
+hipEvent_t g_stage_ev[2 * kStages];
+bool g_stage_ready = false;  // events created
+bool g_stage_on = false;
+bool g_stage_ran[kStages];
+
+const hipEvent_t *stage_events(int first_stage) {
+    if (!g_stage_on) return nullptr;
+    for (int i = 0; i < 3; ++i) g_stage_ran[first_stage + i] = true;
+    return g_stage_ev + 2 * first_stage;
+}
+
 int check_shape(const gdn2_shape *s) {
     if (!s) return fail(GDN2_ERR_ARGUMENT, "shape is null");
     if (s->batch <= 0 || s->time <= 0 || s->heads <= 0)
@@ -298,7 +314,8 @@ int gdn_scalar_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q, cons
         c.final_state = final_state;
         c.scores = scores;
         chunk_bind_checkpoint(c, checkpoint);
-        return launch_status(launch_chunk_fwd(c, (hipStream_t)stream), "gdn_scalar_scan");
+        return launch_status(launch_chunk_fwd(c, (hipStream_t)stream, stage_events(0)),
+                             "gdn_scalar_scan");
     }
     SeqArgs a = seq_args(shape, q, k, v, beta, beta, beta, valid, reset);
     a.scalar = 1;
@@ -354,7 +371,8 @@ int gdn_scalar_backward(const gdn2_shape *shape, int chunk, const gdn2_view *q,
         c.dbeta = dbeta;
         c.dg = dg;
         c.dinitial = d_initial;
-        return launch_status(launch_chunk_bwd(c, (hipStream_t)stream), "gdn_scalar_backward");
+        return launch_status(launch_chunk_bwd(c, (hipStream_t)stream, stage_events(3)),
+                             "gdn_scalar_backward");
     }
     SeqArgs a = seq_args(shape, q, k, v, beta, beta, beta, valid, reset);
     a.scalar = 1;
@@ -373,6 +391,37 @@ int gdn_scalar_backward(const gdn2_shape *shape, int chunk, const gdn2_view *q,
     a.replay = (float *)workspace;
     return launch_status(launch_seq_bwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
                          "gdn_scalar_backward");
+}
+
+int gdn2_stage_timing(int enable) {
+    if (enable && !g_stage_ready) {
+        for (int i = 0; i < 2 * kStages; ++i) {
+            const hipError_t e = hipEventCreate(&g_stage_ev[i]);
+            if (e != hipSuccess) {
+                for (int j = 0; j < i; ++j) (void)hipEventDestroy(g_stage_ev[j]);
+                return fail(GDN2_ERR_LAUNCH, "gdn2_stage_timing: hipEventCreate: %s",
+                            hipGetErrorString(e));
+            }
+        }
+        g_stage_ready = true;
+    }
+    for (int i = 0; i < kStages; ++i) g_stage_ran[i] = false;
+    g_stage_on = enable != 0;
+    return ok();
+}
+
+int gdn2_stage_count(void) { return kStages; }
+
+const char *gdn2_stage_name(int stage) {
+    return stage >= 0 && stage < kStages ? kStageNames[stage] : nullptr;
+}
+
+float gdn2_stage_ms(int stage) {
+    if (stage < 0 || stage >= kStages || !g_stage_ready || !g_stage_ran[stage]) return -1.f;
+    float ms = -1.f;
+    if (hipEventElapsedTime(&ms, g_stage_ev[2 * stage], g_stage_ev[2 * stage + 1]) != hipSuccess)
+        return -1.f;
+    return ms;
 }
 
 int gdn2_decode_step(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k,

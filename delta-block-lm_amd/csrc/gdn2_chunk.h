@@ -97,7 +97,9 @@ inline void chunk_bind_workspace(ChunkArgs &a, void *ws) {
     a.ws_n = reinterpret_cast<float *>(p + n * (CK_STATE_BYTES + CK_MAP_M_BYTES));
 }
 
-hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream);
-hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream);
+// Optional event pairs recorded around each kernel: ev[2i], ev[2i+1] for
+// stage i of the pass (three stages per pass); null = no timing.
+hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
+hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
 
 }  // namespace gdn2

@@ -430,15 +430,20 @@ __device__ __forceinline__ void affine_step(int s, const AffineArgs &p, int bh, 
 
 // One wave per workgroup: wave w of head bh owns state columns 16w..16w+15,
 // which evolve independently (Y = M X acts on columns), so the four column
-// groups of a head run as four workgroups spread over the CUs.
+// groups of a head run as four workgroups spread over the CUs.  Workgroups
+// are dealt to the 8 XCDs round-robin by index; the four column groups of a
+// head take indices with equal residue mod 8, so they share one XCD's L2 and
+// the head's M tiles leave HBM once.
 // NC > 0: the chunk count is a compile-time constant and the chunk loop is
 // straight-line code, so the loads of the three-deep (M, N) ring are waited
 // for one by one; NC == 0 runs any count in a rolled loop.
 template <int NC>
 __global__ void __launch_bounds__(64) affine_scan_kernel(AffineArgs p) {
     __shared__ uint16_t xs[1][2][16 * LDB];
-    const int w = blockIdx.x & 3, l = lane_id();
-    const int bh = blockIdx.x >> 2, b = bh / p.H, h = bh % p.H;
+    const int x = blockIdx.x, l = lane_id();
+    const int w = (x >> 3) & 3, bh = (x & 7) + 8 * (x >> 5);
+    if (bh >= p.B * p.H) return;
+    const int b = bh / p.H, h = bh % p.H;
     const int j = 16 * w + (l & 15);  // this lane's state column
     // Three chunks of (M, N) in flight: one global latency spans three steps.
     bf16x8_t mf[3][4][2];
@@ -623,7 +628,7 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
 
 // Straight-line instantiations cover sequences up to 16 chunks (1024 tokens).
 static void launch_affine_scan(const AffineArgs &p, hipStream_t stream) {
-    const dim3 grid(p.B * p.H * 4), block(64);
+    const dim3 grid(32 * ((p.B * p.H + 7) / 8)), block(64);  // see affine_scan_kernel
     switch (p.nc) {
 #define GDN2_AFFINE_CASE(n) \
     case n: hipLaunchKernelGGL(affine_scan_kernel<n>, grid, block, 0, stream, p); return;
@@ -644,9 +649,15 @@ static AffineArgs affine_args(const ChunkArgs &a) {
     return p;
 }
 
-hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream) {
+static inline void mark(const hipEvent_t *ev, int i, hipStream_t stream) {
+    if (ev) (void)hipEventRecord(ev[i], stream);
+}
+
+hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
     const int nchunks = a.B * a.H * a.nc;
+    mark(ev, 0, stream);
     hipLaunchKernelGGL(chunk_prep_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
+    mark(ev, 1, stream);
     AffineArgs p = affine_args(a);
     p.m = a.map_m;
     p.n = a.map_n;
@@ -654,8 +665,12 @@ hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream) {
     p.x0 = a.initial;
     p.xout = a.final_state;
     p.reverse = 0;
+    mark(ev, 2, stream);
     launch_affine_scan(p, stream);
+    mark(ev, 3, stream);
+    mark(ev, 4, stream);
     hipLaunchKernelGGL(chunk_out_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
+    mark(ev, 5, stream);
     return hipGetLastError();
 }
 
@@ -1211,9 +1226,11 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     }
 }
 
-hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream) {
+hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
     const int nchunks = a.B * a.H * a.nc;
+    mark(ev, 0, stream);
     hipLaunchKernelGGL(chunk_bprep_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
+    mark(ev, 1, stream);
     AffineArgs p = affine_args(a);
     p.m = a.ws_m;
     p.n = a.ws_n;
@@ -1225,8 +1242,12 @@ hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream) {
     p.x0.s3 = 1;
     p.xout = a.dinitial;
     p.reverse = 1;
+    mark(ev, 2, stream);
     launch_affine_scan(p, stream);
+    mark(ev, 3, stream);
+    mark(ev, 4, stream);
     hipLaunchKernelGGL(chunk_bgrad_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
+    mark(ev, 5, stream);
     return hipGetLastError();
 }
 

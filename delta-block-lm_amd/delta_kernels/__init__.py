@@ -22,7 +22,7 @@ from ._lib import GDN2_BF16, GDN2_F32, Gdn2Shape, Gdn2View, check, lib
 
 __all__ = ["GdnTrainingOutput", "gdn_training_scan", "gdn_training_backward",
            "gdn_scalar_scan", "gdn_scalar_forward", "gdn_scalar_backward", "gdn_decode_step",
-           "lib"]
+           "stage_timing", "stage_times", "lib"]
 
 
 class GdnTrainingOutput(NamedTuple):
@@ -321,3 +321,24 @@ def gdn_decode_step(state, q, k, v, alpha, erase, write, valid=None, reset=None)
                                 _ptr(out), _code(out), _ptr(scores), _stream(q))
     check("gdn2_decode_step", rc)
     return out, scores
+
+
+# ---- measurement ----------------------------------------------------------------
+
+
+def stage_timing(enable: bool = True) -> None:
+    """Record HIP events around each chunk-path kernel of the following calls
+    (gdn2_stage_timing); not for use under graph capture."""
+    check("gdn2_stage_timing", lib().gdn2_stage_timing(1 if enable else 0))
+
+
+def stage_times() -> dict:
+    """Per-kernel durations (ms) of the most recent timed calls, by stage name;
+    call after synchronising the stream.  Stages that have not run are absent."""
+    L = lib()
+    out = {}
+    for i in range(L.gdn2_stage_count()):
+        ms = L.gdn2_stage_ms(i)
+        if ms >= 0:
+            out[L.gdn2_stage_name(i).decode()] = ms
+    return out

@@ -54,6 +54,10 @@ SIGNATURES = {
     "gdn_scalar_backward": (_I, [_S, _I] + [_V] * 7 + [_P, _Z, _V, _F, _F] + [_P] * 3
                             + [_F] * 3 + [_P, _Z, _P]),
     "gdn2_decode_step": (_I, [_S] + [_V] * 8 + [_F, _P, ctypes.c_int32, _F, _P]),
+    "gdn2_stage_timing": (_I, [_I]),
+    "gdn2_stage_count": (_I, []),
+    "gdn2_stage_name": (ctypes.c_char_p, [_I]),
+    "gdn2_stage_ms": (ctypes.c_float, [_I]),
 }
 
 _lib = None

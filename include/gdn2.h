@@ -156,6 +156,22 @@ GDN2_API int gdn2_decode_step(const gdn2_shape *shape, const gdn2_view *q, const
                      float *state, void *output, int32_t output_dtype, float *scores,
                      void *stream);
 
+/* Measurement hook.  No counterpart in the reference: it serves benchmarks
+ * that need the duration of each kernel of the chunk-WY path, measured on the
+ * stream the kernels run on.  After gdn2_stage_timing(1), every chunk-path
+ * call of gdn_scalar_scan / gdn_scalar_backward records a pair of HIP events
+ * around each of its kernels on the call's stream; gdn2_stage_ms(i) returns
+ * the duration of stage i in the most recent call that ran it (the caller
+ * synchronises the stream first), or a negative value if stage i has not run
+ * since timing was enabled.  Stages: 0 prep, 1 state scan, 2 output
+ * (forward); 3 backward prep, 4 adjoint scan, 5 gradients (backward).
+ * Process-wide state for the current device: not for use during graph
+ * capture or from several threads at once.  Returns GDN2_OK or an error. */
+GDN2_API int gdn2_stage_timing(int enable);
+GDN2_API int gdn2_stage_count(void);
+GDN2_API const char *gdn2_stage_name(int stage);
+GDN2_API float gdn2_stage_ms(int stage);
+
 #ifdef __cplusplus
 }
 #endif
