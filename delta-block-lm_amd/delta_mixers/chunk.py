@@ -46,13 +46,18 @@ class ScanBackend(str, enum.Enum):
     def is_fused(self) -> bool:
         return not self.is_tensor_solver()
 
+    def partitions(self) -> int:
+        return {ScanBackend.FUSED_PARALLEL128: 2, ScanBackend.FUSED_PARALLEL256: 4}.get(self, 1)
+
     def training_algorithm(self) -> str:
+        """Run-report label.  `fused_gdn2` keeps the reference's label (run reports
+        compare by it); the explicit MI355X selector names its own kernels."""
         return {
             ScanBackend.TENSOR_SOLVER: "differentiable_chunk_tensor_solver",
             ScanBackend.FUSED_GPU: "fused_kron_gpu",
             ScanBackend.FUSED_PARALLEL128: "fused_kron_parallel128_gpu",
             ScanBackend.FUSED_PARALLEL256: "fused_kron_parallel256_gpu",
-            ScanBackend.FUSED_GDN2: "fused_gdn2_mi355x_hip",
+            ScanBackend.FUSED_GDN2: "fused_gdn2_gpu",
             ScanBackend.HIP_GDN2: "fused_gdn2_mi355x_hip",
         }[self]
 
