@@ -17,21 +17,28 @@ struct GateBlock {
     int seg[CHUNK];
 };
 
-// Per-chunk private storage handed from the forward to the backward: S at the
-// chunk start (f32, stored transposed: S^T row-major), T = (I + A)^-1 (bf16),
-// the gate block; plus the chunk's affine state map S_next = M S + N (M bf16
-// row-major, N f32 transposed), a forward temporary.  Transposed f32 matrices
+// Per-chunk private storage handed from the forward to the backward:
+//   state  S at the chunk start, f32, transposed (S^T row-major)
+//   T      (I + A)^-1, bf16 row-major
+//   gate   GateBlock
+//   delta  the chunk's edits delta[t][v], f32 row-major
+//   Wt     W^T = (T diag(beta gam) K)^T as a bf16 hi/lo pair, row-major
+//   Mt     the adjoint map M = A_c^T, bf16 row-major
+// plus the forward state map S_next = A_c S + B_c (A_c bf16 row-major, B_c f32
+// transposed), read only by the forward state scan.  Transposed f32 matrices
 // let each MFMA lane move its four accumulator rows with one 16-byte access.
 constexpr size_t CK_STATE_BYTES = CHUNK_D * CHUNK_D * sizeof(float);
 constexpr size_t CK_T_BYTES = CHUNK * CHUNK * sizeof(uint16_t);
 constexpr size_t CK_GATE_BYTES = sizeof(GateBlock);
+constexpr size_t CK_DELTA_BYTES = CHUNK * CHUNK_D * sizeof(float);
+constexpr size_t CK_WT_BYTES = 2 * CHUNK_D * CHUNK * sizeof(uint16_t);
 constexpr size_t CK_MAP_M_BYTES = CHUNK_D * CHUNK_D * sizeof(uint16_t);
 constexpr size_t CK_MAP_N_BYTES = CHUNK_D * CHUNK_D * sizeof(float);
-constexpr size_t CK_CHUNK_BYTES =
-    CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES + CK_MAP_M_BYTES + CK_MAP_N_BYTES;
-// Backward workspace per chunk: dS at the chunk end (f32, transposed) and the
-// adjoint map (same layouts as the forward map).
-constexpr size_t WS_CHUNK_BYTES = CK_STATE_BYTES + CK_MAP_M_BYTES + CK_MAP_N_BYTES;
+constexpr size_t CK_CHUNK_BYTES = CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES + CK_DELTA_BYTES +
+                                  CK_WT_BYTES + 2 * CK_MAP_M_BYTES + CK_MAP_N_BYTES;
+// Backward workspace per chunk: dS at the chunk end (f32, transposed) and N of
+// the adjoint map (f32, transposed).
+constexpr size_t WS_CHUNK_BYTES = CK_STATE_BYTES + CK_MAP_N_BYTES;
 
 struct ChunkArgs {
     int B, T, H, nc;
@@ -43,12 +50,15 @@ struct ChunkArgs {
     void *out;
     int out_bf16;
     float *final_state, *scores;
-    // checkpoint: [B*H*nc] states, then T tiles, then gate blocks
+    // checkpoint arrays, each [B*H*nc] per-chunk blocks
     float *ck_state;
     uint16_t *ck_t;
     GateBlock *ck_gate;
-    uint16_t *map_m;  // affine map of the pass being run (forward: checkpoint; backward: workspace)
-    float *map_n;
+    float *ck_delta;
+    uint16_t *ck_wt;   // W^T hi, then W^T lo
+    uint16_t *ck_mt;   // adjoint map M = A_c^T
+    uint16_t *map_m;   // forward state map A_c
+    float *map_n;      // forward state map B_c^T
     // backward
     const uint16_t *dout;
     int64_t ds[3];
@@ -56,8 +66,7 @@ struct ChunkArgs {
     void *dq, *dk, *dv;
     float *dbeta, *dg, *dinitial;
     float *ws_dstate;  // [B*H*nc] adjoint of the state at each chunk end
-    uint16_t *ws_m;    // backward affine map dS_start = M dS_end + N
-    float *ws_n;
+    float *ws_n;       // N of the adjoint map dS_start = M dS_end + N
 };
 
 inline bool chunk_eligible_shape(const gdn2_shape *s, int chunk) {
@@ -76,16 +85,25 @@ inline size_t chunk_workspace_bytes(int64_t B, int64_t T, int64_t H) {
     return (size_t)chunk_count(B, T, H) * WS_CHUNK_BYTES;
 }
 
-// Carve the checkpoint buffer into its three arrays.
+// Carve the checkpoint buffer into its arrays.
 inline void chunk_bind_checkpoint(ChunkArgs &a, void *ck) {
     const int64_t n = (int64_t)a.B * a.H * a.nc;
     char *p = static_cast<char *>(ck);
     a.ck_state = reinterpret_cast<float *>(p);
-    a.ck_t = reinterpret_cast<uint16_t *>(p + n * CK_STATE_BYTES);
-    a.ck_gate = reinterpret_cast<GateBlock *>(p + n * (CK_STATE_BYTES + CK_T_BYTES));
-    a.map_m = reinterpret_cast<uint16_t *>(p + n * (CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES));
-    a.map_n = reinterpret_cast<float *>(
-        p + n * (CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES + CK_MAP_M_BYTES));
+    p += n * CK_STATE_BYTES;
+    a.ck_t = reinterpret_cast<uint16_t *>(p);
+    p += n * CK_T_BYTES;
+    a.ck_gate = reinterpret_cast<GateBlock *>(p);
+    p += n * CK_GATE_BYTES;
+    a.ck_delta = reinterpret_cast<float *>(p);
+    p += n * CK_DELTA_BYTES;
+    a.ck_wt = reinterpret_cast<uint16_t *>(p);
+    p += n * CK_WT_BYTES;
+    a.ck_mt = reinterpret_cast<uint16_t *>(p);
+    p += n * CK_MAP_M_BYTES;
+    a.map_m = reinterpret_cast<uint16_t *>(p);
+    p += n * CK_MAP_M_BYTES;
+    a.map_n = reinterpret_cast<float *>(p);
 }
 
 // Carve the backward workspace.
@@ -93,12 +111,9 @@ inline void chunk_bind_workspace(ChunkArgs &a, void *ws) {
     const int64_t n = (int64_t)a.B * a.H * a.nc;
     char *p = static_cast<char *>(ws);
     a.ws_dstate = reinterpret_cast<float *>(p);
-    a.ws_m = reinterpret_cast<uint16_t *>(p + n * CK_STATE_BYTES);
-    a.ws_n = reinterpret_cast<float *>(p + n * (CK_STATE_BYTES + CK_MAP_M_BYTES));
+    a.ws_n = reinterpret_cast<float *>(p + n * CK_STATE_BYTES);
 }
 
-// Optional event pairs recorded around each kernel: ev[2i], ev[2i+1] for
-// stage i of the pass (three stages per pass); null = no timing.
 hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
 hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
 

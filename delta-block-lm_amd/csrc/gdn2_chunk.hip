@@ -362,19 +362,31 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         gemm2(y, &KLt[(16 * tm) * LDB], Ut, tn0);
         gemm2(y, &KLt[(16 * tm) * LDB], Utl, tn0);
         const float gC = sm.gl.gamC;
-        uint16_t *Am = a.map_m + (int64_t)ci * D * D;
-        float *Bt = a.map_n + (int64_t)ci * D * D;  // B transposed: Bt[col][row]
+        uint16_t *Ac = sm.slot[0], *Mt = sm.slot[1];  // T and (beta gam K)^T are dead
+        float *Bt = a.map_n + (int64_t)ci * D * D;    // B transposed: Bt[col][row]
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int cc = 16 * (tn0 + j) + acc_col();
+            f32x4 am;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = 16 * tm + acc_row(i);
-                Am[r * D + cc] = bf16_bits((r == cc ? gC : 0.f) - x[j][i]);
-            }
+            for (int i = 0; i < 4; ++i) am[i] = (16 * tm + acc_row(i) == cc ? gC : 0.f) - x[j][i];
+            store_tile_rm(&Ac[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, am);
+            store_tile_t(&Mt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, am);
             *reinterpret_cast<float4 *>(&Bt[cc * D + 16 * tm + acc_row(0)]) =
                 make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
         }
+    }
+    __syncthreads();
+    // Rows out: A_c (forward state map), M = A_c^T (adjoint map), W^T hi and lo.
+    {
+        const int r = tid >> 3, c0 = 8 * (tid & 7);
+        const int64_t o = (int64_t)ci * D * D + r * D + c0;
+        const uint16_t *Ac = sm.slot[0], *Mt = sm.slot[1];
+        *reinterpret_cast<uint4 *>(a.map_m + o) = *reinterpret_cast<const uint4 *>(&Ac[r * LDB + c0]);
+        *reinterpret_cast<uint4 *>(a.ck_mt + o) = *reinterpret_cast<const uint4 *>(&Mt[r * LDB + c0]);
+        uint16_t *wt = a.ck_wt + 2 * (int64_t)ci * D * C + r * C + c0;
+        *reinterpret_cast<uint4 *>(wt) = *reinterpret_cast<const uint4 *>(&Wt[r * LDB + c0]);
+        *reinterpret_cast<uint4 *>(wt + D * C) = *reinterpret_cast<const uint4 *>(&Wtl[r * LDB + c0]);
     }
 }
 
@@ -576,10 +588,15 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
         float p[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) p[i] = x[0][i] * x[0][i] + x[1][i] * x[1][i];
+        float *dck = a.ck_delta + (int64_t)ci * C * D;  // checkpoint for the backward
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j) {
             store_tile_t_split(&Dt[(16 * (tn0 + j)) * LDB + 16 * tm],
                                &Dl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                dck[(16 * tm + acc_row(i)) * D + 16 * (tn0 + j) + acc_col()] = x[j][i];
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -696,21 +713,21 @@ hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream, const hipEve
 
 namespace {
 
-struct BPrepSmem {
-    uint16_t slot[14][TILE];
+struct BPrepSmem {  // fits twice in one CU's LDS
+    uint16_t slot[8][TILE];
     GateLds gl;
     float kk[NW][C];
-    float dd[2][C];
+    float dd[NW][C];
     float dsc[C];
 };
 
 struct BGradSmem {
-    uint16_t slot[14][TILE];
+    uint16_t slot[15][TILE];
     GateLds gl;
     float kk[NW][C];
-    float dd[2][C];
+    float dd[NW][C];
     float dsc[C];
-    float g1[2][C], g2[2][C], b1[2][C], b2[2][C], zr[2][C], zc[4][C], dlam[2][C];
+    float g1[2][C], ku[2][C], b1[2][C], b2[2][C], zr[2][C], zc[4][C], dlam[2][C];
     float frob[NW];
 };
 
@@ -736,14 +753,15 @@ __device__ __forceinline__ float col_reduce(const f32x4 &x) {
 
 // Stage a 64x64 f32 matrix S, held transposed (S^T row-major, the checkpoint
 // layout; this thread's part is row j = tid>>3 of S^T, 8 entries), into the bf16
-// tile dstT[j][i] = S[i][j] and (optionally) the row-major tile dst[i][j].
+// tile dstT[j][i] = S[i][j] and the row-major tile dst[i][j] (either may be null).
 __device__ __forceinline__ void stage_mat(uint16_t *dstT, uint16_t *dst, const float4 (&v)[2],
                                           int tid) {
     const int j = tid >> 3, i0 = 8 * (tid & 7);
     const float x[8] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w};
-    *reinterpret_cast<uint4 *>(&dstT[j * LDB + i0]) =
-        make_uint4(bf16_pack2(x[0], x[1]), bf16_pack2(x[2], x[3]), bf16_pack2(x[4], x[5]),
-                   bf16_pack2(x[6], x[7]));
+    if (dstT)
+        *reinterpret_cast<uint4 *>(&dstT[j * LDB + i0]) =
+            make_uint4(bf16_pack2(x[0], x[1]), bf16_pack2(x[2], x[3]), bf16_pack2(x[4], x[5]),
+                       bf16_pack2(x[6], x[7]));
     if (dst)
 #pragma unroll
         for (int e = 0; e < 8; ++e) dst[(i0 + e) * LDB + j] = bf16_bits(x[e]);
@@ -764,54 +782,59 @@ __device__ __forceinline__ void store_grad(void *dst, int64_t idx, float x) {
 // The backward state recurrence is affine too: with
 //   X = P^T dO + diag(c) delta,  Y = (gam Q)^T dO,  W = T diag(beta gam) K,
 //   ddelta = X + diag(lam) K dS_C  and  dS0 = gam_63 dS_C + Y - W^T ddelta,
-// so dS0 = M dS_C + N with M = gam_63 I - W^T diag(lam) K and N = Y - W^T X.
-// bprep builds (M, N) for every chunk in parallel.
+// so dS0 = M dS_C + N with M = gam_63 I - W^T diag(lam) K = A_c^T and
+// N = Y - W^T X.  M and W^T come from the forward prep, delta from the forward
+// output kernel; bprep builds N for every chunk in parallel.
 __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     __shared__ BPrepSmem sm;
-    uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *Vt = sm.slot[2], *dOt = sm.slot[3];
-    uint16_t *Tb = sm.slot[4], *St = sm.slot[5], *QGt = sm.slot[6], *KBGt = sm.slot[7];
-    uint16_t *KLt = sm.slot[8], *Rt = sm.slot[9], *Pt = sm.slot[10], *Ptl = sm.slot[11];
-    uint16_t *Wt = sm.slot[12], *Wtl = sm.slot[13];
-    uint16_t *Xt = sm.slot[9], *Xtl = sm.slot[2];  // after phase 2
+    uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *QGt = sm.slot[2], *dOt = sm.slot[3];
+    uint16_t *Wt = sm.slot[4], *Wtl = sm.slot[5], *Pt = sm.slot[6], *Ptl = sm.slot[7];
+    uint16_t *Xt = sm.slot[0], *Xtl = sm.slot[1];  // over Q/K after phase 1
     const int tid = threadIdx.x, w = tid >> 6;
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
     const int tg = c * C + t;
     const bool inb = tg < a.T;
     const GateBlock *gb = a.ck_gate + ci;
+    const float *dck = a.ck_delta + (int64_t)ci * C * D;
+    const int r0 = 16 * tm + 4 * (lane_id() >> 4);
+    float dl[2][4];  // delta at this wave's X tile, used in phase 2
     {
         const uint4 qr = load8(a.q, a.qs, b, tg, h, cb, inb);
         const uint4 kr = load8(a.k, a.ks, b, tg, h, cb, inb);
-        const uint4 vr = load8(a.v, a.vs, b, tg, h, cb, inb);
         const uint4 dor = a.dout ? load8(a.dout, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
-        const uint4 trw = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C +
-                                                          (tid >> 3) * C + 8 * (tid & 7));
-        float4 s0[2];
-        load_mat(s0, a.ck_state + (int64_t)ci * D * D, tid);
-        const float G = gb->G[t], be = gb->beta[t], va = gb->val[t], G63 = gb->G[63];
-        const int sg = gb->seg[t], sg63 = gb->seg[63];
+        const uint16_t *wsrc = a.ck_wt + 2 * (int64_t)ci * D * C + (tid >> 3) * C + 8 * (tid & 7);
+        const uint4 wh = *reinterpret_cast<const uint4 *>(wsrc);
+        const uint4 wl = *reinterpret_cast<const uint4 *>(wsrc + D * C);
+        const float4 d0 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb);
+        const float4 d1 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb + 4);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dl[j][i] = dck[(r0 + i) * D + 16 * (tn0 + j) + acc_col()];
+        const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
+        const int sg = gb->seg[t];
         const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
         const bool on = va != 0.f;
-        const float gam = sg == 0 ? __expf(G) : 0.f, lam = sg == sg63 ? __expf(G63 - G) : 0.f;
+        const float gam = sg == 0 ? __expf(G) : 0.f;
         Pack8 qp, kp;
         qp.u = mask8(qr, on);
         kp.u = mask8(kr, on);
         put_row8(Qs, t, cb, qp.u);
         put_row8(Ks, t, cb, kp.u);
-        put_col8(Vt, t, cb, mask8(vr, on));
         put_col8(dOt, t, cb, mask8(dor, on));
+        *reinterpret_cast<uint4 *>(&Wt[(tid >> 3) * LDB + 8 * (tid & 7)]) = wh;
+        *reinterpret_cast<uint4 *>(&Wtl[(tid >> 3) * LDB + 8 * (tid & 7)]) = wl;
         float ksq = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const float qf = bf16_val(qp.h[e]), kf = bf16_val(kp.h[e]);
             QGt[(8 * cb + e) * LDB + t] = bf16_bits(gam * qf);
-            KBGt[(8 * cb + e) * LDB + t] = bf16_bits(be * gam * kf);
-            KLt[(8 * cb + e) * LDB + t] = bf16_bits(lam * kf);
             ksq += kf * kf;
         }
         sm.kk[cb][t] = ksq;
-        *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
-        stage_mat(St, nullptr, s0, tid);
+        sm.dd[cb][t] = d0.x * d0.x + d0.y * d0.y + d0.z * d0.z + d0.w * d0.w + d1.x * d1.x +
+                       d1.y * d1.y + d1.z * d1.z + d1.w * d1.w;
         if (w == 0) {
             gates_derive(sm.gl, G, be, va, sg);
             sm.dsc[t] = dsc;
@@ -819,70 +842,40 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     }
     __syncthreads();
     const RowGates rg = row_gates(sm.gl, tm);
-    const int r0 = 16 * tm + 4 * (lane_id() >> 4);
-    // Phase 1: R (Rt, lo over V^T), P^T (hi/lo), Y in registers, W^T (hi/lo).
+    // Phase 1: P (causal tiles, masked) -> P^T hi/lo; Y = (gam Q)^T dO in registers.
     f32x4 yacc[2] = {zero4(), zero4()};
     {
-        f32x4 x[2] = {zero4(), zero4()}, pq[2] = {zero4(), zero4()}, wa[2] = {zero4(), zero4()};
-        gemm2(x, &Ks[(16 * tm) * LDB], St, tn0);
-        if (tn0 <= tm) gemm2(pq, &Qs[(16 * tm) * LDB], Ks, tn0);
+        f32x4 pq[2] = {zero4(), zero4()};
         gemm2(yacc, &QGt[(16 * tm) * LDB], dOt, tn0);
-        gemm2(wa, &Tb[(16 * tm) * LDB], KBGt, tn0);
+        if (tn0 <= tm) gemm2(pq, &Qs[(16 * tm) * LDB], Ks, tn0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int ss = 16 * (tn0 + j) + acc_col();
             const float Gs = sm.gl.G[ss];
             const int sgs = sm.gl.seg[ss];
-            uint16_t *vt = &Vt[(16 * (tn0 + j)) * LDB + 16 * tm];
-            float vv[4];
-            ld4_bf16(vt + acc_col() * LDB + 4 * (lane_id() >> 4), vv);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tt = 16 * tm + acc_row(i);
-                x[j][i] = rg.beta[i] * (vv[i] - rg.gam[i] * x[j][i]);
                 pq[j][i] *= (ss <= tt && rg.seg[i] == sgs) ? __expf(rg.G[i] - Gs) : 0.f;
             }
-            store_tile_t_split(&Rt[(16 * (tn0 + j)) * LDB + 16 * tm], vt, LDB, x[j]);
             store_tile_t_split(&Pt[(16 * (tn0 + j)) * LDB + 16 * tm],
                                &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq[j]);
-            store_tile_t_split(&Wt[(16 * (tn0 + j)) * LDB + 16 * tm],
-                               &Wtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, wa[j]);
         }
     }
     __syncthreads();
-    // Phase 2: delta = T R (registers, |delta_s|^2); M = gam_63 I - W^T diag(lam) K.
-    f32x4 dl[2] = {zero4(), zero4()};
-    {
-        gemm2(dl, &Tb[(16 * tm) * LDB], Rt, tn0);
-        gemm2(dl, &Tb[(16 * tm) * LDB], Vt, tn0);
-        float p[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) p[i] = dl[0][i] * dl[0][i] + dl[1][i] * dl[1][i];
-        row_reduce_store(p, sm.dd[w & 1], tm);
-        f32x4 x[2] = {zero4(), zero4()};
-        gemm2(x, &Wt[(16 * tm) * LDB], KLt, tn0);
-        gemm2(x, &Wtl[(16 * tm) * LDB], KLt, tn0);
-        const float gC = sm.gl.gamC;
-        uint16_t *Mm = a.ws_m + (int64_t)ci * D * D;
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = 16 * tm + acc_row(i), cc = 16 * (tn0 + j) + acc_col();
-                Mm[r * D + cc] = bf16_bits((r == cc ? gC : 0.f) - x[j][i]);
-            }
-    }
-    __syncthreads();
-    // Phase 3: X = P^T dO + diag(c) delta, stored transposed (hi/lo).
+    // Phase 2: X = P^T dO + diag(c) delta, stored transposed (hi/lo).
     {
         float cs[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int ss = r0 + i;
-            float kq = 0.f;
+            float kq = 0.f, dq = 0.f;
 #pragma unroll
-            for (int q = 0; q < NW; ++q) kq += sm.kk[q][ss];
-            const float nk = sqrtf(kq), nd = sqrtf(sm.dd[0][ss] + sm.dd[1][ss]);
+            for (int q = 0; q < NW; ++q) {
+                kq += sm.kk[q][ss];
+                dq += sm.dd[q][ss];
+            }
+            const float nk = sqrtf(kq), nd = sqrtf(dq);
             cs[i] = (nk > 0.f && nd > 0.f) ? sm.dsc[ss] * nk / nd : 0.f;
         }
         f32x4 x[2] = {zero4(), zero4()};
@@ -897,7 +890,7 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
         }
     }
     __syncthreads();
-    // Phase 4: N = Y - W^T X.
+    // Phase 3: N = Y - W^T X.
     {
         f32x4 x[2] = {zero4(), zero4()};
         gemm2(x, &Wt[(16 * tm) * LDB], Xt, tn0);
@@ -912,26 +905,36 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
                             yacc[j][3] - x[j][3]);
     }
 }
+
+// bgrad: every gradient of one chunk, given S0, the edits delta (forward
+// checkpoint) and dS at the chunk end (adjoint scan).  Phases between barriers:
+//   A  dO S0^T, K dS, KK^T, QK^T (registers); P^T -> LDS
+//   D  delta dS^T (-> dlam); ddelta = P^T dO + lam K dS + c delta -> LDS
+//   E  dR = T^T ddelta -> dV, dbeta (sum dR v), dR rows
+//   F  dR S0^T (-> dK, dbeta, dgam); dA, dP masked -> MA, MP (+ transposes)
+//   G  dQ = MP K + gam dO S0^T;  dK = (MA + MA^T) K + MP^T Q + ...
+//   H  gate gradients: dbeta, and dg by a reverse scan of dG (wave 0)
 __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     __shared__ BGradSmem sm;
     uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *dOs = sm.slot[2], *Qt = sm.slot[3];
-    uint16_t *Kt = sm.slot[4], *dOt = sm.slot[5], *Vt = sm.slot[6], *Tb = sm.slot[7];
-    uint16_t *Ttb = sm.slot[8], *S0t = sm.slot[9], *S0b = sm.slot[10], *dSt = sm.slot[11];
-    uint16_t *dSb = sm.slot[12];
+    uint16_t *Kt = sm.slot[4], *dOt = sm.slot[5], *Vt = sm.slot[6], *Ttb = sm.slot[7];
+    uint16_t *S0b = sm.slot[8], *dSt = sm.slot[9], *dSb = sm.slot[10];
+    uint16_t *Dh = sm.slot[11], *Dlo = sm.slot[12];  // delta rows (hi/lo)
+    uint16_t *Pt = sm.slot[13], *Ptl = sm.slot[14];  // A..D
     // Later tenants of dead slots.
-    uint16_t *Pt = sm.slot[0], *Ptl = sm.slot[11];                    // phase B..D
-    uint16_t *Rt = sm.slot[1], *Rl = sm.slot[6];                      // phase B..C
-    uint16_t *Dh = sm.slot[9], *Dlo = sm.slot[13];                    // delta rows, C..F
-    uint16_t *Dd = sm.slot[7], *Ddl = sm.slot[1];                     // ddelta^T, D..E
-    uint16_t *dRr = sm.slot[6];                                       // dR rows, E..F
-    uint16_t *MA = sm.slot[0], *MAt = sm.slot[11];                    // F..G
-    uint16_t *MP = sm.slot[5], *MPl = sm.slot[8], *MPt = sm.slot[7], *MPtl = sm.slot[1];
+    uint16_t *Dd = sm.slot[0], *Ddl = sm.slot[1];  // ddelta^T, D..E
+    uint16_t *dRr = sm.slot[9];                    // dR rows, E..F
+    uint16_t *MA = sm.slot[0], *MAt = sm.slot[1];  // F..G
+    uint16_t *MP = sm.slot[5], *MPl = sm.slot[6], *MPt = sm.slot[7], *MPtl = sm.slot[10];
     const int tid = threadIdx.x, w = tid >> 6;
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
     const int tg = c * C + t;
     const bool inb = tg < a.T;
     const GateBlock *gb = a.ck_gate + ci;
+    const float *dck = a.ck_delta + (int64_t)ci * C * D;
+    const int r0 = 16 * tm + 4 * (lane_id() >> 4);
+    float dl[2][4];  // delta at this wave's tile (rows r0.., columns 16 (tn0 + j) + lane)
     {
         const uint4 qr = load8(a.q, a.qs, b, tg, h, cb, inb);
         const uint4 kr = load8(a.k, a.ks, b, tg, h, cb, inb);
@@ -942,6 +945,12 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         float4 s0[2], ds[2];
         load_mat(s0, a.ck_state + (int64_t)ci * D * D, tid);
         load_mat(ds, a.ws_dstate + (int64_t)ci * D * D, tid);
+        const float4 d0 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb);
+        const float4 d1 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb + 4);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dl[j][i] = dck[(r0 + i) * D + 16 * (tn0 + j) + acc_col()];
         const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
         const int sg = gb->seg[t];
         const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
@@ -964,11 +973,26 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
             ksq += kf * kf;
         }
         sm.kk[cb][t] = ksq;
-        *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
 #pragma unroll
         for (int e = 0; e < 8; ++e) Ttb[(8 * (tid & 7) + e) * LDB + (tid >> 3)] = tp.h[e];
-        stage_mat(S0t, S0b, s0, tid);
+        stage_mat(nullptr, S0b, s0, tid);
         stage_mat(dSt, dSb, ds, tid);
+        {  // delta row t, channels 8cb..: hi/lo rows and |delta_t|^2 partial
+            const float x[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+            uint16_t hi[8], lo[8];
+            float dsq = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                split_bf16(x[e], hi[e], lo[e]);
+                dsq += x[e] * x[e];
+            }
+            Pack8 ph, pl;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ph.h[e] = hi[e], pl.h[e] = lo[e];
+            put_row8(Dh, t, cb, ph.u);
+            put_row8(Dlo, t, cb, pl.u);
+            sm.dd[cb][t] = dsq;
+        }
         float fr = s0[0].x * ds[0].x + s0[0].y * ds[0].y + s0[0].z * ds[0].z + s0[0].w * ds[0].w +
                    s0[1].x * ds[1].x + s0[1].y * ds[1].y + s0[1].z * ds[1].z + s0[1].w * ds[1].w;
 #pragma unroll
@@ -981,18 +1005,16 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     }
     __syncthreads();
     const RowGates rg = row_gates(sm.gl, tm);
-    const int r0 = 16 * tm + 4 * (lane_id() >> 4);
     float lmv[4];
     {
         const float4 lm = lds_f4(&sm.gl.lam[r0]);
         lmv[0] = lm.x, lmv[1] = lm.y, lmv[2] = lm.z, lmv[3] = lm.w;
     }
-    // Phase A (registers only): dO S0^T, lam K dS^T, KK^T, QK^T, V - gam K S0.
+    // Phase A: dO S0^T, lam K dS, KK^T, QK^T in registers; P^T (hi/lo) -> LDS.
     f32x4 dos[2] = {zero4(), zero4()}, kds[2] = {zero4(), zero4()};
-    f32x4 kk[2] = {zero4(), zero4()}, qk[2] = {zero4(), zero4()}, vmk[2] = {zero4(), zero4()};
+    f32x4 kk[2] = {zero4(), zero4()}, qk[2] = {zero4(), zero4()};
     gemm2(dos, &dOs[(16 * tm) * LDB], S0b, tn0);
     gemm2(kds, &Ks[(16 * tm) * LDB], dSt, tn0);
-    gemm2(vmk, &Ks[(16 * tm) * LDB], S0t, tn0);
     if (tn0 <= tm) {
         gemm2(kk, &Ks[(16 * tm) * LDB], Ks, tn0);
         gemm2(qk, &Qs[(16 * tm) * LDB], Ks, tn0);
@@ -1001,62 +1023,37 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         float p[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            float vv[4], qv[4];
-            ld4_bf16(&Vt[(16 * (tn0 + j) + acc_col()) * LDB + r0], vv);
+            const int ss = 16 * (tn0 + j) + acc_col();
+            const float Gs = sm.gl.G[ss];
+            const int sgs = sm.gl.seg[ss];
+            float qv[4];
             ld4_bf16(&Qt[(16 * (tn0 + j) + acc_col()) * LDB + r0], qv);
+            f32x4 pq = qk[j];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                vmk[j][i] = vv[i] - rg.gam[i] * vmk[j][i];
+                const int tt = 16 * tm + acc_row(i);
                 kds[j][i] *= lmv[i];
                 p[i] += qv[i] * dos[j][i];  // q_t . (dO S0^T)_t
+                pq[i] *= (ss <= tt && rg.seg[i] == sgs) ? __expf(rg.G[i] - Gs) : 0.f;
             }
+            store_tile_t_split(&Pt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq);
         }
         row_reduce_store(p, sm.g1[w & 1], tm);
     }
     __syncthreads();
-    // Phase B: P^T (hi/lo) over Q/dS^T, R (hi over K, lo over V^T).
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int ss = 16 * (tn0 + j) + acc_col();
-        const float Gs = sm.gl.G[ss];
-        const int sgs = sm.gl.seg[ss];
-        f32x4 pq = qk[j], x;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int tt = 16 * tm + acc_row(i);
-            pq[i] *= (ss <= tt && rg.seg[i] == sgs) ? __expf(rg.G[i] - Gs) : 0.f;
-            x[i] = rg.beta[i] * vmk[j][i];
-        }
-        store_tile_t_split(&Pt[(16 * (tn0 + j)) * LDB + 16 * tm],
-                           &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq);
-        store_tile_t_split(&Rt[(16 * (tn0 + j)) * LDB + 16 * tm],
-                           &Rl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x);
-    }
-    __syncthreads();
-    // Phase C: delta = T R -> registers and rows (hi/lo); |delta_s|^2.
-    f32x4 dl[2] = {zero4(), zero4()};
-    {
-        gemm2(dl, &Tb[(16 * tm) * LDB], Rt, tn0);
-        gemm2(dl, &Tb[(16 * tm) * LDB], Rl, tn0);
-        float p[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) p[i] = dl[0][i] * dl[0][i] + dl[1][i] * dl[1][i];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            store_tile_rm_split(&Dh[(16 * tm) * LDB + 16 * (tn0 + j)],
-                                &Dlo[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, dl[j]);
-        row_reduce_store(p, sm.dd[w & 1], tm);
-    }
-    __syncthreads();
-    // Phase D: delta dS^T (-> dlam), ddelta = P^T dO + lam K dS^T + c delta (-> ddelta^T).
+    // Phase D: delta dS^T (-> dlam), ddelta = P^T dO + lam K dS + c delta (-> ddelta^T).
     float cs[4], ck[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int ss = r0 + i;
-        float kq = 0.f;
+        float kq = 0.f, dq = 0.f;
 #pragma unroll
-        for (int q = 0; q < NW; ++q) kq += sm.kk[q][ss];
-        const float nk = sqrtf(kq), nd = sqrtf(sm.dd[0][ss] + sm.dd[1][ss]);
+        for (int q = 0; q < NW; ++q) {
+            kq += sm.kk[q][ss];
+            dq += sm.dd[q][ss];
+        }
+        const float nk = sqrtf(kq), nd = sqrtf(dq);
         const bool ok = nk > 0.f && nd > 0.f;
         cs[i] = ok ? sm.dsc[ss] * nk / nd : 0.f;
         ck[i] = ok ? sm.dsc[ss] * nd / nk : 0.f;
@@ -1086,7 +1083,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         }
     }
     __syncthreads();
-    // Phase E: dR = T^T ddelta -> dV, dbeta (R part), dR rows.
+    // Phase E: dR = T^T ddelta -> dV, dbeta (sum_v dR v part), dR rows.
     {
         f32x4 x[2] = {zero4(), zero4()};
         gemm2(x, &Ttb[(16 * tm) * LDB], Dd, tn0);
@@ -1094,9 +1091,11 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         float p[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
+            float vv[4];
+            ld4_bf16(&Vt[(16 * (tn0 + j) + acc_col()) * LDB + r0], vv);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                p[i] += x[j][i] * vmk[j][i];
+                p[i] += x[j][i] * vv[i];
                 const int tq = c * C + r0 + i;
                 if (a.dv && tq < a.T)
                     store_grad(a.dv, (((int64_t)b * a.T + tq) * a.H + h) * D + 16 * (tn0 + j) + acc_col(),
@@ -1107,8 +1106,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         row_reduce_store(p, sm.b2[w & 1], tm);
     }
     __syncthreads();
-    // Phase F: dR S0^T (-> dK, dgam), dA and dP (masked) -> MA, MP (+ transposes),
-    // and the gate-gradient partial sums.
+    // Phase F: dR S0^T (-> dK; sum_k k dR S0^T -> dbeta and dgam), dA and dP
+    // (masked) -> MA, MP (+ transposes), and the gate-gradient partial sums.
     f32x4 drs[2] = {zero4(), zero4()};
     gemm2(drs, &dRr[(16 * tm) * LDB], S0b, tn0);
     {
@@ -1118,9 +1117,9 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
             float kv[4];
             ld4_bf16(&Kt[(16 * (tn0 + j) + acc_col()) * LDB + r0], kv);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) p2[i] -= rg.beta[i] * kv[i] * drs[j][i];
+            for (int i = 0; i < 4; ++i) p2[i] += kv[i] * drs[j][i];
         }
-        row_reduce_store(p2, sm.g2[w & 1], tm);
+        row_reduce_store(p2, sm.ku[w & 1], tm);
     }
     {
         f32x4 da[2] = {zero4(), zero4()}, dp[2] = {zero4(), zero4()};
@@ -1193,13 +1192,16 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         }
     }
     __syncthreads();
-    // Phase H: gate gradients (wave 0, lane == token).
+    // Phase H: gate gradients (wave 0, lane == token).  With u_t = k_t . (dR S0^T)_t:
+    //   dbeta_t = sum dA Gam KK^T + sum_v dR v - gam_t u_t,
+    //   dG_t   = row - column sums of Z + gam_t (q_t . (dO S0^T)_t - beta_t u_t) - lam_t dlam_t.
     if (w == 0) {
-        const float gam = sm.gl.gam[t], lam = sm.gl.lam[t];
+        const float gam = sm.gl.gam[t], lam = sm.gl.lam[t], bet = sm.gl.beta[t];
         const float dlam = sm.dlam[0][t] + sm.dlam[1][t];
+        const float u = sm.ku[0][t] + sm.ku[1][t];
         float dG = sm.zr[0][t] + sm.zr[1][t] -
                    (sm.zc[0][t] + sm.zc[1][t] + sm.zc[2][t] + sm.zc[3][t]) +
-                   gam * (sm.g1[0][t] + sm.g1[1][t] + sm.g2[0][t] + sm.g2[1][t]) - lam * dlam;
+                   gam * (sm.g1[0][t] + sm.g1[1][t] - bet * u) - lam * dlam;
         float tail = lam * dlam;
 #pragma unroll
         for (int m = 1; m < 64; m <<= 1) tail += __shfl_xor(tail, m);
@@ -1221,7 +1223,9 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         if (tg < a.T) {
             const int64_t o = ((int64_t)b * a.T + tg) * a.H + h;
             if (a.dg) a.dg[o] = (on && !rs) ? x : 0.f;
-            if (a.dbeta) a.dbeta[o] = on ? sm.b1[0][t] + sm.b1[1][t] + sm.b2[0][t] + sm.b2[1][t] : 0.f;
+            if (a.dbeta)
+                a.dbeta[o] = on ? sm.b1[0][t] + sm.b1[1][t] + sm.b2[0][t] + sm.b2[1][t] - gam * u
+                                : 0.f;
         }
     }
 }
@@ -1232,7 +1236,7 @@ hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream, const hipEve
     hipLaunchKernelGGL(chunk_bprep_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
     mark(ev, 1, stream);
     AffineArgs p = affine_args(a);
-    p.m = a.ws_m;
+    p.m = a.ck_mt;
     p.n = a.ws_n;
     p.ckpt = a.ws_dstate;
     p.x0.data = a.dfinal;
