@@ -154,6 +154,33 @@ __device__ __forceinline__ void ld4_bf16(const uint16_t *p, float (&o)[4]) {
     o[3] = bf16_val((uint16_t)(v.y >> 16));
 }
 
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: in each 16-lane group, lane i supplies the address of
+// four 16-bit elements M[i][0..3]; lane j receives M[4e + j/4][j%4], e < 4.
+__device__ __forceinline__ v4s lds_tr16(const uint16_t *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s *)p);
+}
+
+// Accumulator-layout values (rows row0 + 4(l/16) + e, column col0 + l%16) of a
+// row-major bf16 LDS tile, with one transpose read.
+__device__ __forceinline__ void ld4_rm_tr(const uint16_t *Z, int row0, int col0, float (&o)[4]) {
+    const int l = lane_id(), i = l & 15;
+    const v4s v = lds_tr16(Z + (row0 + 4 * (l >> 4) + (i >> 2)) * LDB + col0 + 4 * (i & 3));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = bf16_val((uint16_t)v[e]);
+}
+
+// Sum over the 16 lanes of a DPP row (lanes 16r..16r+15), left in every lane:
+// quad swaps (lane ^ 1, lane ^ 2) then half-row and row mirrors.
+__device__ __forceinline__ float row16_sum(float x) {
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x140, 0xF, 0xF, false));
+    return x;
+}
+
 // T = (I + A)^-1 for the strictly lower 64x64 A in Af; result in Tf (lower
 // blocks).  Called by all waves; ends with a barrier.  Blocks are 16x16:
 //   1. diagonal blocks T_bb = (I + A_bb)^-1 by forward substitution (waves 0-3,
@@ -599,8 +626,7 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int m = 1; m < 16; m <<= 1) p[i] += __shfl_xor(p[i], m);
+            p[i] = row16_sum(p[i]);
             if (acc_col() == 0) sm.dd[w & 1][16 * tm + acc_row(i)] = p[i];
         }
     }
@@ -737,8 +763,7 @@ __device__ __forceinline__ float4 lds_f4(const float *p) { return *reinterpret_c
 __device__ __forceinline__ void row_reduce_store(float (&p)[4], float *dst, int tm) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int m = 1; m < 16; m <<= 1) p[i] += __shfl_xor(p[i], m);
+        p[i] = row16_sum(p[i]);
         if (acc_col() == 0) dst[16 * tm + acc_row(i)] = p[i];
     }
 }
@@ -934,7 +959,6 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     const GateBlock *gb = a.ck_gate + ci;
     const float *dck = a.ck_delta + (int64_t)ci * C * D;
     const int r0 = 16 * tm + 4 * (lane_id() >> 4);
-    float dl[2][4];  // delta at this wave's tile (rows r0.., columns 16 (tn0 + j) + lane)
     {
         const uint4 qr = load8(a.q, a.qs, b, tg, h, cb, inb);
         const uint4 kr = load8(a.k, a.ks, b, tg, h, cb, inb);
@@ -947,10 +971,6 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         load_mat(ds, a.ws_dstate + (int64_t)ci * D * D, tid);
         const float4 d0 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb);
         const float4 d1 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb + 4);
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dl[j][i] = dck[(r0 + i) * D + 16 * (tn0 + j) + acc_col()];
         const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
         const int sg = gb->seg[t];
         const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
@@ -1058,17 +1078,21 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         cs[i] = ok ? sm.dsc[ss] * nk / nd : 0.f;
         ck[i] = ok ? sm.dsc[ss] * nd / nk : 0.f;
     }
-    f32x4 dkl[2] = {zero4(), zero4()};
+    // dK accumulates lam (delta dS^T) here, -beta gam dR S0^T in F, the rest in G.
+    f32x4 dka[2] = {zero4(), zero4()};
     {
-        gemm2(dkl, &Dh[(16 * tm) * LDB], dSb, tn0);
-        gemm2(dkl, &Dlo[(16 * tm) * LDB], dSb, tn0);
+        gemm2(dka, &Dh[(16 * tm) * LDB], dSb, tn0);
+        gemm2(dka, &Dlo[(16 * tm) * LDB], dSb, tn0);
         float p[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             float kv[4];
             ld4_bf16(&Kt[(16 * (tn0 + j) + acc_col()) * LDB + r0], kv);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) p[i] += kv[i] * dkl[j][i];
+            for (int i = 0; i < 4; ++i) {
+                p[i] += kv[i] * dka[j][i];
+                dka[j][i] *= lmv[i];
+            }
         }
         row_reduce_store(p, sm.dlam[w & 1], tm);
         f32x4 x[2] = {kds[0], kds[1]};
@@ -1076,8 +1100,11 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         gemm2(x, &Ptl[(16 * tm) * LDB], dOt, tn0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
+            float dh[4], dlo[4];  // delta at this tile: hi + lo rows
+            ld4_rm_tr(Dh, 16 * tm, 16 * (tn0 + j), dh);
+            ld4_rm_tr(Dlo, 16 * tm, 16 * (tn0 + j), dlo);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x[j][i] += cs[i] * dl[j][i];
+            for (int i = 0; i < 4; ++i) x[j][i] += cs[i] * (dh[i] + dlo[i]);
             store_tile_t_split(&Dd[(16 * (tn0 + j)) * LDB + 16 * tm],
                                &Ddl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
         }
@@ -1117,7 +1144,10 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
             float kv[4];
             ld4_bf16(&Kt[(16 * (tn0 + j) + acc_col()) * LDB + r0], kv);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) p2[i] += kv[i] * drs[j][i];
+            for (int i = 0; i < 4; ++i) {
+                p2[i] += kv[i] * drs[j][i];
+                dka[j][i] -= rg.beta[i] * rg.gam[i] * drs[j][i];
+            }
         }
         row_reduce_store(p2, sm.ku[w & 1], tm);
     }
@@ -1181,8 +1211,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
                 const int tq = c * C + r0 + i;
                 const bool on = sm.gl.val[r0 + i] != 0.f;
                 const float dq = x[j][i] + rg.gam[i] * dos[j][i];
-                const float dk = y[j][i] - rg.beta[i] * rg.gam[i] * drs[j][i] +
-                                 lmv[i] * dkl[j][i] + ck[i] * kv[i];
+                const float dk = y[j][i] + dka[j][i] + ck[i] * kv[i];
                 if (tq < a.T) {
                     const int64_t o = (((int64_t)b * a.T + tq) * a.H + h) * D + 16 * (tn0 + j) + acc_col();
                     if (a.dq) store_grad(a.dq, o, on ? dq : 0.f);
