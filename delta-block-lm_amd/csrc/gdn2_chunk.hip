@@ -191,8 +191,8 @@ __device__ void ut_inverse(const float *Af, float *Tf, float (*Xs)[16 * LDX], in
     const int l = lane_id();
     if (w < 4) {
         // Lane (col, part) holds rows part, part+4, part+8, part+12 of column col;
-        // the four parts of a column split each row's dot product.
-        const int col = l & 15, part = l >> 4;
+        // the four parts of a column (one DPP quad) split each row's dot product.
+        const int col = l >> 2, part = l & 3;
         const float *Ab = Af + (16 * w) * LDF + 16 * w;
         float Tq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -203,8 +203,10 @@ __device__ void ut_inverse(const float *Af, float *Tf, float (*Xs)[16 * LDX], in
                 const int s = part + 4 * m;
                 if (s < r) acc += Ab[r * LDF + s] * Tq[m];
             }
-            acc += __shfl_xor(acc, 16);
-            acc += __shfl_xor(acc, 32);
+            acc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                       0, __builtin_bit_cast(int, acc), 0xB1, 0xF, 0xF, false));  // lane ^ 1
+            acc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                       0, __builtin_bit_cast(int, acc), 0x4E, 0xF, 0xF, false));  // lane ^ 2
             if ((r & 3) == part) Tq[r >> 2] = (r == col ? 1.f : 0.f) - acc;
         }
         float *Tb = Tf + (16 * w) * LDF + 16 * w;
