@@ -18,7 +18,7 @@ struct GateBlock {
 };
 
 // Per-chunk private storage handed from the forward to the backward:
-//   state  S at the chunk start, f32, transposed (S^T row-major)
+//   state  S at the chunk start, bf16, transposed (S^T row-major)
 //   T      (I + A)^-1, bf16 row-major
 //   gate   GateBlock
 //   delta  the chunk's edits delta[t][v], f32 row-major
@@ -27,7 +27,7 @@ struct GateBlock {
 // plus the forward state map S_next = A_c S + B_c (A_c bf16 row-major, B_c f32
 // transposed), read only by the forward state scan.  Transposed f32 matrices
 // let each MFMA lane move its four accumulator rows with one 16-byte access.
-constexpr size_t CK_STATE_BYTES = CHUNK_D * CHUNK_D * sizeof(float);
+constexpr size_t CK_STATE_BYTES = CHUNK_D * CHUNK_D * sizeof(uint16_t);
 constexpr size_t CK_T_BYTES = CHUNK * CHUNK * sizeof(uint16_t);
 constexpr size_t CK_GATE_BYTES = sizeof(GateBlock);
 constexpr size_t CK_DELTA_BYTES = CHUNK * CHUNK_D * sizeof(float);
@@ -36,7 +36,7 @@ constexpr size_t CK_MAP_M_BYTES = CHUNK_D * CHUNK_D * sizeof(uint16_t);
 constexpr size_t CK_MAP_N_BYTES = CHUNK_D * CHUNK_D * sizeof(float);
 constexpr size_t CK_CHUNK_BYTES = CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES + CK_DELTA_BYTES +
                                   CK_WT_BYTES + 2 * CK_MAP_M_BYTES + CK_MAP_N_BYTES;
-// Backward workspace per chunk: dS at the chunk end (f32, transposed) and N of
+// Backward workspace per chunk: dS at the chunk end (bf16, transposed) and N of
 // the adjoint map (f32, transposed).
 constexpr size_t WS_CHUNK_BYTES = CK_STATE_BYTES + CK_MAP_N_BYTES;
 
@@ -51,7 +51,7 @@ struct ChunkArgs {
     int out_bf16;
     float *final_state, *scores;
     // checkpoint arrays, each [B*H*nc] per-chunk blocks
-    float *ck_state;
+    uint16_t *ck_state;
     uint16_t *ck_t;
     GateBlock *ck_gate;
     float *ck_delta;
@@ -65,7 +65,7 @@ struct ChunkArgs {
     const float *dfinal, *dscores;
     void *dq, *dk, *dv;
     float *dbeta, *dg, *dinitial;
-    float *ws_dstate;  // [B*H*nc] adjoint of the state at each chunk end
+    uint16_t *ws_dstate;  // [B*H*nc] adjoint of the state at each chunk end
     float *ws_n;       // N of the adjoint map dS_start = M dS_end + N
 };
 
@@ -89,7 +89,7 @@ inline size_t chunk_workspace_bytes(int64_t B, int64_t T, int64_t H) {
 inline void chunk_bind_checkpoint(ChunkArgs &a, void *ck) {
     const int64_t n = (int64_t)a.B * a.H * a.nc;
     char *p = static_cast<char *>(ck);
-    a.ck_state = reinterpret_cast<float *>(p);
+    a.ck_state = reinterpret_cast<uint16_t *>(p);
     p += n * CK_STATE_BYTES;
     a.ck_t = reinterpret_cast<uint16_t *>(p);
     p += n * CK_T_BYTES;
@@ -110,7 +110,7 @@ inline void chunk_bind_checkpoint(ChunkArgs &a, void *ck) {
 inline void chunk_bind_workspace(ChunkArgs &a, void *ws) {
     const int64_t n = (int64_t)a.B * a.H * a.nc;
     char *p = static_cast<char *>(ws);
-    a.ws_dstate = reinterpret_cast<float *>(p);
+    a.ws_dstate = reinterpret_cast<uint16_t *>(p);
     a.ws_n = reinterpret_cast<float *>(p + n * CK_STATE_BYTES);
 }
 

@@ -270,14 +270,11 @@ struct OutSmem {
 };
 
 // Chunk-start state as the bf16 tile St[j][i] = S[i][j], from the transposed
-// f32 checkpoint layout (S^T row-major, which is also St's layout).
-__device__ __forceinline__ void load_state_t(uint16_t *St, const float *S0t, int tid) {
+// bf16 checkpoint layout (S^T row-major, which is also St's layout).
+__device__ __forceinline__ void load_state_t(uint16_t *St, const uint16_t *S0t, int tid) {
     const int j = tid >> 3, i0 = 8 * (tid & 7);
-    const float4 *src = reinterpret_cast<const float4 *>(S0t + j * D + i0);
-    const float4 v0 = src[0], v1 = src[1];
     *reinterpret_cast<uint4 *>(&St[j * LDB + i0]) =
-        make_uint4(bf16_pack2(v0.x, v0.y), bf16_pack2(v0.z, v0.w), bf16_pack2(v1.x, v1.y),
-                   bf16_pack2(v1.z, v1.w));
+        *reinterpret_cast<const uint4 *>(S0t + j * D + i0);
 }
 
 }  // namespace
@@ -423,7 +420,8 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
 // X_{next} = M_c X + N_c over the chunks of one (batch, head): forward
 // (S_C = A S0 + B, c ascending, X0 = initial state) or backward
 // (dS0 = M dS_C + N, c descending, X0 = adjoint of the final state).  X before
-// each step goes to ckpt[c], transposed (X^T row-major).  Columns of X evolve independently, so each of the
+// each step goes to ckpt[c], transposed (X^T row-major) and rounded to bf16
+// (every consumer uses it as a bf16 MFMA operand).  Columns of X evolve independently, so each of the
 // four waves owns 16 columns; M fragments come straight from global memory
 // (prefetched one chunk ahead), X is re-packed through a wave-private LDS tile
 // into the bf16 hi/lo operand of the next product.
@@ -431,7 +429,7 @@ struct AffineArgs {
     int nc, B, H;
     const uint16_t *m;
     const float *n;
-    float *ckpt;
+    uint16_t *ckpt;  // X^T per chunk, bf16
     View x0;          // [B,H,64,64] strided (data may be null: zero)
     float *xout;      // [B,H,64,64] dense (may be null)
     int reverse;
@@ -443,11 +441,11 @@ __device__ __forceinline__ void affine_step(int s, const AffineArgs &p, int bh, 
                                             f32x4 (&nf)[3][4], uint16_t *xh, uint16_t *xl,
                                             F &fetch, Gt &chunk_of) {
     const int c = chunk_of(s);
-    float *ck = p.ckpt + ((int64_t)bh * p.nc + c) * D * D;  // X^T
+    uint16_t *ck = p.ckpt + ((int64_t)bh * p.nc + c) * D * D;  // X^T, bf16
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm) {
-        *reinterpret_cast<float4 *>(&ck[j * D + 16 * tm + acc_row(0)]) =
-            make_float4(X[tm][0], X[tm][1], X[tm][2], X[tm][3]);
+        *reinterpret_cast<uint2 *>(&ck[j * D + 16 * tm + acc_row(0)]) =
+            make_uint2(bf16_pack2(X[tm][0], X[tm][1]), bf16_pack2(X[tm][2], X[tm][3]));
         store_tile_t_split(xh + 16 * tm, xl + 16 * tm, LDB, X[tm]);  // [col][row]
     }
     __syncthreads();
@@ -778,26 +776,33 @@ __device__ __forceinline__ float col_reduce(const f32x4 &x) {
     return s;
 }
 
-// Stage a 64x64 f32 matrix S, held transposed (S^T row-major, the checkpoint
-// layout; this thread's part is row j = tid>>3 of S^T, 8 entries), into the bf16
+// Stage a 64x64 bf16 matrix S, held transposed (S^T row-major, the checkpoint
+// layout; this thread's part is row j = tid>>3 of S^T, 8 entries), into the
 // tile dstT[j][i] = S[i][j] and the row-major tile dst[i][j] (either may be null).
-__device__ __forceinline__ void stage_mat(uint16_t *dstT, uint16_t *dst, const float4 (&v)[2],
-                                          int tid) {
+__device__ __forceinline__ void stage_mat(uint16_t *dstT, uint16_t *dst, const uint4 v, int tid) {
     const int j = tid >> 3, i0 = 8 * (tid & 7);
-    const float x[8] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w};
-    if (dstT)
-        *reinterpret_cast<uint4 *>(&dstT[j * LDB + i0]) =
-            make_uint4(bf16_pack2(x[0], x[1]), bf16_pack2(x[2], x[3]), bf16_pack2(x[4], x[5]),
-                       bf16_pack2(x[6], x[7]));
-    if (dst)
+    if (dstT) *reinterpret_cast<uint4 *>(&dstT[j * LDB + i0]) = v;
+    if (dst) {
+        Pack8 p;
+        p.u = v;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dst[(i0 + e) * LDB + j] = bf16_bits(x[e]);
+        for (int e = 0; e < 8; ++e) dst[(i0 + e) * LDB + j] = p.h[e];
+    }
 }
 
-__device__ __forceinline__ void load_mat(float4 (&v)[2], const float *src, int tid) {
-    const float4 *p = reinterpret_cast<const float4 *>(src + (tid >> 3) * D + 8 * (tid & 7));
-    v[0] = p[0];
-    v[1] = p[1];
+__device__ __forceinline__ uint4 load_mat(const uint16_t *src, int tid) {
+    return *reinterpret_cast<const uint4 *>(src + (tid >> 3) * D + 8 * (tid & 7));
+}
+
+// sum_e a[e] b[e] over eight bf16 pairs.
+__device__ __forceinline__ float dot8_bf16(const uint4 a, const uint4 b) {
+    Pack8 pa, pb;
+    pa.u = a;
+    pb.u = b;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += bf16_val(pa.h[e]) * bf16_val(pb.h[e]);
+    return s;
 }
 
 __device__ __forceinline__ void store_grad(void *dst, int64_t idx, float x) {
@@ -968,9 +973,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         const uint4 dor = a.dout ? load8(a.dout, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
         const uint4 trw = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C +
                                                           (tid >> 3) * C + 8 * (tid & 7));
-        float4 s0[2], ds[2];
-        load_mat(s0, a.ck_state + (int64_t)ci * D * D, tid);
-        load_mat(ds, a.ws_dstate + (int64_t)ci * D * D, tid);
+        const uint4 s0 = load_mat(a.ck_state + (int64_t)ci * D * D, tid);
+        const uint4 ds = load_mat(a.ws_dstate + (int64_t)ci * D * D, tid);
         const float4 d0 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb);
         const float4 d1 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb + 4);
         const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
@@ -1015,8 +1019,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
             put_row8(Dlo, t, cb, pl.u);
             sm.dd[cb][t] = dsq;
         }
-        float fr = s0[0].x * ds[0].x + s0[0].y * ds[0].y + s0[0].z * ds[0].z + s0[0].w * ds[0].w +
-                   s0[1].x * ds[1].x + s0[1].y * ds[1].y + s0[1].z * ds[1].z + s0[1].w * ds[1].w;
+        float fr = dot8_bf16(s0, ds);
 #pragma unroll
         for (int m = 1; m < 64; m <<= 1) fr += __shfl_xor(fr, m);
         if (lane_id() == 0) sm.frob[w] = fr;
