@@ -79,31 +79,55 @@ __device__ __forceinline__ void put_col8(uint16_t *tile, int t, int cb, uint4 v)
     for (int e = 0; e < 8; ++e) tile[(8 * cb + e) * LDB + t] = p.h[e];
 }
 
-// Inclusive wave scans (64 lanes).
-__device__ __forceinline__ float wave_scan_add(float x) {
-    const int l = lane_id();
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const float y = __shfl_up(x, d);
-        if (l >= d) x += y;
-    }
+// DPP lane moves (gfx9 controls): lanes whose source is outside the pattern,
+// or whose row is masked off, read 0.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, false));
+}
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xF, false);
+}
+
+// Sum over the 16 lanes of a DPP row (lanes 16r..16r+15), left in every lane:
+// quad swaps (lane ^ 1, lane ^ 2) then half-row and row mirrors.
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp<0xB1>(x);
+    x += dpp<0x4E>(x);
+    x += dpp<0x141>(x);
+    x += dpp<0x140>(x);
     return x;
 }
-__device__ __forceinline__ int wave_scan_add(int x) {
-    const int l = lane_id();
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int y = __shfl_up(x, d);
-        if (l >= d) x += y;
-    }
+
+// Sum over the 64 lanes of a wave, left in every lane.
+__device__ __forceinline__ float wave_sum(float x) {
+    const int r = __builtin_bit_cast(int, row16_sum(x));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(r, 0)) +
+           __builtin_bit_cast(float, __builtin_amdgcn_readlane(r, 16)) +
+           __builtin_bit_cast(float, __builtin_amdgcn_readlane(r, 32)) +
+           __builtin_bit_cast(float, __builtin_amdgcn_readlane(r, 48));
+}
+
+// Inclusive scan over the 64 lanes of a wave: shifts right by 1, 2, 4, 8 within
+// each row, then lane 15 of rows 0/2 into rows 1/3 and lane 31 into rows 2-3.
+template <typename Tv>
+__device__ __forceinline__ Tv wave_scan_add(Tv x) {
+    x += dpp<0x111>(x);
+    x += dpp<0x112>(x);
+    x += dpp<0x114>(x);
+    x += dpp<0x118>(x);
+    x += dpp<0x142, 0xA>(x);
+    x += dpp<0x143, 0xC>(x);
     return x;
 }
 
 // Wave 0 (lane == token): decays derived from a gate block.
 __device__ __forceinline__ void gates_derive(GateLds &gl, float G, float beta, float val, int seg) {
     const int t = lane_id();
-    const float G63 = __shfl(G, 63);
-    const int seg63 = __shfl(seg, 63);
+    const float G63 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, G), 63));
+    const int seg63 = __builtin_amdgcn_readlane(seg, 63);
     gl.G[t] = G;
     gl.beta[t] = beta;
     gl.val[t] = val;
@@ -169,16 +193,6 @@ __device__ __forceinline__ void ld4_rm_tr(const uint16_t *Z, int row0, int col0,
     const v4s v = lds_tr16(Z + (row0 + 4 * (l >> 4) + (i >> 2)) * LDB + col0 + 4 * (i & 3));
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] = bf16_val((uint16_t)v[e]);
-}
-
-// Sum over the 16 lanes of a DPP row (lanes 16r..16r+15), left in every lane:
-// quad swaps (lane ^ 1, lane ^ 2) then half-row and row mirrors.
-__device__ __forceinline__ float row16_sum(float x) {
-    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
-    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
-    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
-    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x140, 0xF, 0xF, false));
-    return x;
 }
 
 // T = (I + A)^-1 for the strictly lower 64x64 A in Af; result in Tf (lower
@@ -1019,9 +1033,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
             put_row8(Dlo, t, cb, pl.u);
             sm.dd[cb][t] = dsq;
         }
-        float fr = dot8_bf16(s0, ds);
-#pragma unroll
-        for (int m = 1; m < 64; m <<= 1) fr += __shfl_xor(fr, m);
+        const float fr = wave_sum(dot8_bf16(s0, ds));
         if (lane_id() == 0) sm.frob[w] = fr;
         if (w == 0) {
             gates_derive(sm.gl, G, be, va, sg);
@@ -1229,36 +1241,31 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     // Phase H: gate gradients (wave 0, lane == token).  With u_t = k_t . (dR S0^T)_t:
     //   dbeta_t = sum dA Gam KK^T + sum_v dR v - gam_t u_t,
     //   dG_t   = row - column sums of Z + gam_t (q_t . (dO S0^T)_t - beta_t u_t) - lam_t dlam_t.
+    // Lane t holds token s = 63 - t, so a forward scan over lanes sums suffixes:
+    // dg_s = sum_{r >= s} dG_r.
     if (w == 0) {
-        const float gam = sm.gl.gam[t], lam = sm.gl.lam[t], bet = sm.gl.beta[t];
-        const float dlam = sm.dlam[0][t] + sm.dlam[1][t];
-        const float u = sm.ku[0][t] + sm.ku[1][t];
-        float dG = sm.zr[0][t] + sm.zr[1][t] -
-                   (sm.zc[0][t] + sm.zc[1][t] + sm.zc[2][t] + sm.zc[3][t]) +
-                   gam * (sm.g1[0][t] + sm.g1[1][t] - bet * u) - lam * dlam;
-        float tail = lam * dlam;
-#pragma unroll
-        for (int m = 1; m < 64; m <<= 1) tail += __shfl_xor(tail, m);
-        if (t == 63) {
+        const int s = 63 - t, ts = c * C + s;
+        const float gam = sm.gl.gam[s], lam = sm.gl.lam[s], bet = sm.gl.beta[s];
+        const float dlam = sm.dlam[0][s] + sm.dlam[1][s];
+        const float u = sm.ku[0][s] + sm.ku[1][s];
+        float dG = sm.zr[0][s] + sm.zr[1][s] -
+                   (sm.zc[0][s] + sm.zc[1][s] + sm.zc[2][s] + sm.zc[3][s]) +
+                   gam * (sm.g1[0][s] + sm.g1[1][s] - bet * u) - lam * dlam;
+        const float tail = wave_sum(lam * dlam);
+        if (s == 63) {
             float fr = 0.f;
 #pragma unroll
             for (int q = 0; q < NW; ++q) fr += sm.frob[q];
             dG += tail + sm.gl.gamC * fr;
         }
-        // reverse inclusive scan: dg_u = sum_{t >= u} dG_t
-        float x = dG;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const float y = __shfl_down(x, d);
-            if (t + d < 64) x += y;
-        }
-        const bool on = sm.gl.val[t] != 0.f;
-        const bool rs = on && (t == 0 ? sm.gl.seg[0] == 1 : sm.gl.seg[t] != sm.gl.seg[t - 1]);
-        if (tg < a.T) {
-            const int64_t o = ((int64_t)b * a.T + tg) * a.H + h;
+        const float x = wave_scan_add(dG);
+        const bool on = sm.gl.val[s] != 0.f;
+        const bool rs = on && (s == 0 ? sm.gl.seg[0] == 1 : sm.gl.seg[s] != sm.gl.seg[s - 1]);
+        if (ts < a.T) {
+            const int64_t o = ((int64_t)b * a.T + ts) * a.H + h;
             if (a.dg) a.dg[o] = (on && !rs) ? x : 0.f;
             if (a.dbeta)
-                a.dbeta[o] = on ? sm.b1[0][t] + sm.b1[1][t] + sm.b2[0][t] + sm.b2[1][t] - gam * u
+                a.dbeta[o] = on ? sm.b1[0][s] + sm.b1[1][s] + sm.b2[0][s] + sm.b2[1][s] - gam * u
                                 : 0.f;
         }
     }
