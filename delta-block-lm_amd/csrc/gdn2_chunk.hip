@@ -980,32 +980,33 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     const GateBlock *gb = a.ck_gate + ci;
     const float *dck = a.ck_delta + (int64_t)ci * C * D;
     const int r0 = 16 * tm + 4 * (lane_id() >> 4);
+    // Every load is issued here, phase A's operands first.  Phase A's tiles go
+    // to LDS before the first barrier; the rest (V, T, delta and the transposed
+    // copies phase A does not read) are written after phase A, so phase A runs
+    // while the tail of the loads is still arriving.
+    const uint4 qr = load8(a.q, a.qs, b, tg, h, cb, inb);
+    const uint4 kr = load8(a.k, a.ks, b, tg, h, cb, inb);
+    const uint4 dor = a.dout ? load8(a.dout, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
+    const uint4 s0 = load_mat(a.ck_state + (int64_t)ci * D * D, tid);
+    const uint4 ds = load_mat(a.ws_dstate + (int64_t)ci * D * D, tid);
+    const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
+    const int sg = gb->seg[t];
+    const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
+    const uint4 vr = load8(a.v, a.vs, b, tg, h, cb, inb);
+    const uint4 trw = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C +
+                                                      (tid >> 3) * C + 8 * (tid & 7));
+    const float4 d0 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb);
+    const float4 d1 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb + 4);
+    const bool on = va != 0.f;
+    const uint4 k8 = mask8(kr, on), d8 = mask8(dor, on);
     {
-        const uint4 qr = load8(a.q, a.qs, b, tg, h, cb, inb);
-        const uint4 kr = load8(a.k, a.ks, b, tg, h, cb, inb);
-        const uint4 vr = load8(a.v, a.vs, b, tg, h, cb, inb);
-        const uint4 dor = a.dout ? load8(a.dout, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
-        const uint4 trw = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C +
-                                                          (tid >> 3) * C + 8 * (tid & 7));
-        const uint4 s0 = load_mat(a.ck_state + (int64_t)ci * D * D, tid);
-        const uint4 ds = load_mat(a.ws_dstate + (int64_t)ci * D * D, tid);
-        const float4 d0 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb);
-        const float4 d1 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb + 4);
-        const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
-        const int sg = gb->seg[t];
-        const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
-        const bool on = va != 0.f;
-        const uint4 q8 = mask8(qr, on), k8 = mask8(kr, on), d8 = mask8(dor, on);
+        const uint4 q8 = mask8(qr, on);
         put_row8(Qs, t, cb, q8);
         put_row8(Ks, t, cb, k8);
         put_row8(dOs, t, cb, d8);
         put_col8(Qt, t, cb, q8);
-        put_col8(Kt, t, cb, k8);
-        put_col8(dOt, t, cb, d8);
-        put_col8(Vt, t, cb, mask8(vr, on));
-        Pack8 kp, tp;
+        Pack8 kp;
         kp.u = k8;
-        tp.u = trw;
         float ksq = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -1013,26 +1014,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
             ksq += kf * kf;
         }
         sm.kk[cb][t] = ksq;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) Ttb[(8 * (tid & 7) + e) * LDB + (tid >> 3)] = tp.h[e];
         stage_mat(nullptr, S0b, s0, tid);
-        stage_mat(dSt, dSb, ds, tid);
-        {  // delta row t, channels 8cb..: hi/lo rows and |delta_t|^2 partial
-            const float x[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-            uint16_t hi[8], lo[8];
-            float dsq = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                split_bf16(x[e], hi[e], lo[e]);
-                dsq += x[e] * x[e];
-            }
-            Pack8 ph, pl;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ph.h[e] = hi[e], pl.h[e] = lo[e];
-            put_row8(Dh, t, cb, ph.u);
-            put_row8(Dlo, t, cb, pl.u);
-            sm.dd[cb][t] = dsq;
-        }
+        stage_mat(dSt, nullptr, ds, tid);
         const float fr = wave_sum(dot8_bf16(s0, ds));
         if (lane_id() == 0) sm.frob[w] = fr;
         if (w == 0) {
@@ -1077,6 +1060,27 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
                                &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq);
         }
         row_reduce_store(p, sm.g1[w & 1], tm);
+    }
+    {  // second half of the staging: operands of phases D-G that A does not read
+        put_col8(Kt, t, cb, k8);
+        put_col8(dOt, t, cb, d8);
+        put_col8(Vt, t, cb, mask8(vr, on));
+        Pack8 tp;
+        tp.u = trw;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) Ttb[(8 * (tid & 7) + e) * LDB + (tid >> 3)] = tp.h[e];
+        stage_mat(nullptr, dSb, ds, tid);
+        const float x[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+        Pack8 ph, pl;
+        float dsq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            split_bf16(x[e], ph.h[e], pl.h[e]);
+            dsq += x[e] * x[e];
+        }
+        put_row8(Dh, t, cb, ph.u);
+        put_row8(Dlo, t, cb, pl.u);
+        sm.dd[cb][t] = dsq;
     }
     __syncthreads();
     // Phase D: delta dS^T (-> dlam), ddelta = P^T dO + lam K dS + c delta (-> ddelta^T).
