@@ -283,14 +283,6 @@ struct OutSmem {
     float dd[2][C];
 };
 
-// Chunk-start state as the bf16 tile St[j][i] = S[i][j], from the transposed
-// bf16 checkpoint layout (S^T row-major, which is also St's layout).
-__device__ __forceinline__ void load_state_t(uint16_t *St, const uint16_t *S0t, int tid) {
-    const int j = tid >> 3, i0 = 8 * (tid & 7);
-    *reinterpret_cast<uint4 *>(&St[j * LDB + i0]) =
-        *reinterpret_cast<const uint4 *>(S0t + j * D + i0);
-}
-
 }  // namespace
 
 // ---- prep: gates, the UT inverse and the affine state map of every chunk -------
@@ -331,17 +323,15 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         gb->seg[t] = seg;
     }
     __syncthreads();
-    {  // scaled transposes of K and V for the W/U/A/B products
+    {  // scaled transposes of K for the W/A products
         const float be = sm.gl.beta[t], ga = sm.gl.gam[t], la = sm.gl.lam[t];
-        Pack8 kp, vp;
+        Pack8 kp;
         kp.u = k8;
-        vp.u = v8;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float kf = bf16_val(kp.h[e]), vf = bf16_val(vp.h[e]);
+            const float kf = bf16_val(kp.h[e]);
             KBGt[(8 * cb + e) * LDB + t] = bf16_bits(be * ga * kf);
             KLt[(8 * cb + e) * LDB + t] = bf16_bits(la * kf);
-            VBt[(8 * cb + e) * LDB + t] = bf16_bits(be * vf);
         }
     }
     // A = strict_lower(beta_t Gam_ts k_t.k_s) in f32 (tiles with tn <= tm only).
@@ -378,6 +368,13 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         const uint4 v = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         *reinterpret_cast<uint4 *>(a.ck_t + (int64_t)ci * C * C + r * C + c0) = v;
         *reinterpret_cast<uint4 *>(&Tb[r * LDB + c0]) = v;
+    }
+    {  // (beta V)^T for U, written once the inverse no longer needs the time
+        const float be = sm.gl.beta[t];
+        Pack8 vp;
+        vp.u = v8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) VBt[(8 * cb + e) * LDB + t] = bf16_bits(be * bf16_val(vp.h[e]));
     }
     __syncthreads();
     // W = T (beta gam K), U = T (beta V): stored transposed as hi/lo pairs.
@@ -564,21 +561,24 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
     const int tm = w >> 1, tn0 = 2 * (w & 1);
     const GateBlock *gb = a.ck_gate + ci;
     const bool inb = tg < a.T;
+    // T is read only from phase 2: its load is issued last and written to LDS
+    // after phase 1.
+    const uint4 qr = load8(a.q, a.qs, b, tg, h, cb, inb);
+    const uint4 kr = load8(a.k, a.ks, b, tg, h, cb, inb);
+    const uint4 vr = load8(a.v, a.vs, b, tg, h, cb, inb);
+    const uint4 s0r = *reinterpret_cast<const uint4 *>(a.ck_state + (int64_t)ci * D * D +
+                                                       (tid >> 3) * D + 8 * (tid & 7));
+    const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
+    const int sg = gb->seg[t];
+    const uint4 trw =
+        *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C + (tid >> 3) * C + 8 * (tid & 7));
     {
-        const uint4 qr = load8(a.q, a.qs, b, tg, h, cb, inb);
-        const uint4 kr = load8(a.k, a.ks, b, tg, h, cb, inb);
-        const uint4 vr = load8(a.v, a.vs, b, tg, h, cb, inb);
-        const uint4 trw =
-            *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C + (tid >> 3) * C + 8 * (tid & 7));
-        load_state_t(St, a.ck_state + (int64_t)ci * D * D, tid);
-        const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
-        const int sg = gb->seg[t];
         const bool on = va != 0.f;
         const uint4 k8 = mask8(kr, on);
         put_row8(Qs, t, cb, mask8(qr, on));
         put_row8(Ks, t, cb, k8);
         put_col8(Vt, t, cb, mask8(vr, on));
-        *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
+        *reinterpret_cast<uint4 *>(&St[(tid >> 3) * LDB + 8 * (tid & 7)]) = s0r;  // S0^T rows
         Pack8 kp;
         kp.u = k8;
         float ksq = 0.f;
@@ -620,6 +620,7 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
                                 &Pl[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, pq[j]);
         }
     }
+    *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
     __syncthreads();
     // Phase 2: delta = T R (-> Dt/Dl over the Q/K slots) and |delta_t|^2.
     {
@@ -844,23 +845,25 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     const GateBlock *gb = a.ck_gate + ci;
     const float *dck = a.ck_delta + (int64_t)ci * C * D;
     const int r0 = 16 * tm + 4 * (lane_id() >> 4);
+    // Loads in order of use: phase 1's operands, then delta (phase 2), then W^T
+    // (phase 3); each later group is written to LDS after the phase before it.
+    const uint4 qr = load8(a.q, a.qs, b, tg, h, cb, inb);
+    const uint4 kr = load8(a.k, a.ks, b, tg, h, cb, inb);
+    const uint4 dor = a.dout ? load8(a.dout, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
+    const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
+    const int sg = gb->seg[t];
+    const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
+    const float4 d0 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb);
+    const float4 d1 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb + 4);
     float dl[2][4];  // delta at this wave's X tile, used in phase 2
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dl[j][i] = dck[(r0 + i) * D + 16 * (tn0 + j) + acc_col()];
+    const uint16_t *wsrc = a.ck_wt + 2 * (int64_t)ci * D * C + (tid >> 3) * C + 8 * (tid & 7);
+    const uint4 wh = *reinterpret_cast<const uint4 *>(wsrc);
+    const uint4 wl = *reinterpret_cast<const uint4 *>(wsrc + D * C);
     {
-        const uint4 qr = load8(a.q, a.qs, b, tg, h, cb, inb);
-        const uint4 kr = load8(a.k, a.ks, b, tg, h, cb, inb);
-        const uint4 dor = a.dout ? load8(a.dout, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
-        const uint16_t *wsrc = a.ck_wt + 2 * (int64_t)ci * D * C + (tid >> 3) * C + 8 * (tid & 7);
-        const uint4 wh = *reinterpret_cast<const uint4 *>(wsrc);
-        const uint4 wl = *reinterpret_cast<const uint4 *>(wsrc + D * C);
-        const float4 d0 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb);
-        const float4 d1 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb + 4);
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dl[j][i] = dck[(r0 + i) * D + 16 * (tn0 + j) + acc_col()];
-        const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
-        const int sg = gb->seg[t];
-        const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
         const bool on = va != 0.f;
         const float gam = sg == 0 ? __expf(G) : 0.f;
         Pack8 qp, kp;
@@ -869,8 +872,6 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
         put_row8(Qs, t, cb, qp.u);
         put_row8(Ks, t, cb, kp.u);
         put_col8(dOt, t, cb, mask8(dor, on));
-        *reinterpret_cast<uint4 *>(&Wt[(tid >> 3) * LDB + 8 * (tid & 7)]) = wh;
-        *reinterpret_cast<uint4 *>(&Wtl[(tid >> 3) * LDB + 8 * (tid & 7)]) = wl;
         float ksq = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -879,8 +880,6 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
             ksq += kf * kf;
         }
         sm.kk[cb][t] = ksq;
-        sm.dd[cb][t] = d0.x * d0.x + d0.y * d0.y + d0.z * d0.z + d0.w * d0.w + d1.x * d1.x +
-                       d1.y * d1.y + d1.z * d1.z + d1.w * d1.w;
         if (w == 0) {
             gates_derive(sm.gl, G, be, va, sg);
             sm.dsc[t] = dsc;
@@ -908,6 +907,10 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
                                &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq[j]);
         }
     }
+    sm.dd[cb][t] = d0.x * d0.x + d0.y * d0.y + d0.z * d0.z + d0.w * d0.w + d1.x * d1.x +
+                   d1.y * d1.y + d1.z * d1.z + d1.w * d1.w;
+    *reinterpret_cast<uint4 *>(&Wt[(tid >> 3) * LDB + 8 * (tid & 7)]) = wh;
+    *reinterpret_cast<uint4 *>(&Wtl[(tid >> 3) * LDB + 8 * (tid & 7)]) = wl;
     __syncthreads();
     // Phase 2: X = P^T dO + diag(c) delta, stored transposed (hi/lo).
     {
