@@ -11,12 +11,13 @@
 
 #include "gdn2_chunk.h"
 #include "gdn2_seq.h"
+#include "gdn2_status.h"
 
-using namespace gdn2;
+namespace gdn2 {
 
 namespace {
-
 thread_local std::string g_error;
+}
 
 int fail(int code, const char *fmt, ...) {
     char buf[512];
@@ -32,6 +33,31 @@ int ok() {
     g_error.clear();
     return GDN2_OK;
 }
+
+const char *last_error() { return g_error.c_str(); }
+
+int check_view(const gdn2_view *v, const char *name, int dtype, bool data_may_be_null) {
+    if (!v) return fail(GDN2_ERR_ARGUMENT, "%s: view is null", name);
+    if (!v->data && !data_may_be_null) return fail(GDN2_ERR_ARGUMENT, "%s: data is null", name);
+    if (v->dtype != GDN2_F32 && v->dtype != GDN2_BF16)
+        return fail(GDN2_ERR_DTYPE, "%s: unknown dtype %d", name, v->dtype);
+    if (dtype >= 0 && v->dtype != dtype)
+        return fail(GDN2_ERR_DTYPE, "%s: dtype must be %s", name, dtype == GDN2_F32 ? "F32" : "BF16");
+    for (int d = 0; d < 4; ++d)
+        if (v->stride[d] < 0) return fail(GDN2_ERR_ARGUMENT, "%s: negative stride", name);
+    return GDN2_OK;
+}
+
+int launch_status(hipError_t e, const char *what) {
+    if (e != hipSuccess) return fail(GDN2_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+}  // namespace gdn2
+
+using namespace gdn2;
+
+namespace {
 
 // Stage timing (gdn2_stage_timing): six stages, an event pair each; the
 // forward records pairs 0-2, the backward pairs 3-5.
@@ -62,19 +88,6 @@ int check_shape(const gdn2_shape *s) {
     return GDN2_OK;
 }
 
-// dtype: -1 = F32 or BF16; otherwise the required dtype.
-int check_view(const gdn2_view *v, const char *name, int dtype, bool data_may_be_null) {
-    if (!v) return fail(GDN2_ERR_ARGUMENT, "%s: view is null", name);
-    if (!v->data && !data_may_be_null) return fail(GDN2_ERR_ARGUMENT, "%s: data is null", name);
-    if (v->dtype != GDN2_F32 && v->dtype != GDN2_BF16)
-        return fail(GDN2_ERR_DTYPE, "%s: unknown dtype %d", name, v->dtype);
-    if (dtype >= 0 && v->dtype != dtype)
-        return fail(GDN2_ERR_DTYPE, "%s: dtype must be %s", name, dtype == GDN2_F32 ? "F32" : "BF16");
-    for (int d = 0; d < 4; ++d)
-        if (v->stride[d] < 0) return fail(GDN2_ERR_ARGUMENT, "%s: negative stride", name);
-    return GDN2_OK;
-}
-
 int check_chunk(int chunk) {
     if (chunk < 1 || chunk > 64) return fail(GDN2_ERR_ARGUMENT, "chunk must be 1..64 (got %d)", chunk);
     return GDN2_OK;
@@ -84,17 +97,6 @@ int check_out_dtype(int32_t dt) {
     if (dt != GDN2_F32 && dt != GDN2_BF16) return fail(GDN2_ERR_DTYPE, "output dtype must be F32 or BF16");
     return GDN2_OK;
 }
-
-int launch_status(hipError_t e, const char *what) {
-    if (e != hipSuccess) return fail(GDN2_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
-    return ok();
-}
-
-#define GDN2_TRY(x)                  \
-    do {                             \
-        int _rc = (x);               \
-        if (_rc != GDN2_OK) return _rc; \
-    } while (0)
 
 size_t seq_checkpoint_bytes(const gdn2_shape *s) {
     const int64_t nck = (s->time + SEQ_CT - 1) / SEQ_CT;
@@ -146,7 +148,7 @@ extern "C" {
 
 int gdn2_abi_version(void) { return 100; }
 
-const char *gdn2_last_error(void) { return g_error.c_str(); }
+const char *gdn2_last_error(void) { return gdn2::last_error(); }
 
 size_t gdn2_training_checkpoint_bytes(const gdn2_shape *shape, int chunk) {
     if (check_shape(shape) || check_chunk(chunk)) return 0;

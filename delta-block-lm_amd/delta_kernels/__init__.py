@@ -342,3 +342,8 @@ def stage_times() -> dict:
         if ms >= 0:
             out[L.gdn2_stage_name(i).decode()] = ms
     return out
+
+
+from .mixer_ops import causal_conv, decay, l2_norm, rms_norm  # noqa: E402
+
+__all__ += ["causal_conv", "l2_norm", "rms_norm", "decay"]

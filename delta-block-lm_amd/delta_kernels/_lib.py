@@ -33,6 +33,16 @@ class Gdn2Error(RuntimeError):
         self.status = status
 
 
+class Gdn2ConvShape(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_int64), ("time", ctypes.c_int64),
+                ("channels", ctypes.c_int64), ("taps", ctypes.c_int64)]
+
+
+class Gdn2RowsShape(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_int64), ("time", ctypes.c_int64), ("heads", ctypes.c_int64),
+                ("width", ctypes.c_int64)]
+
+
 # Exported symbols and their signatures: (name, restype, argtypes).
 _P = ctypes.c_void_p
 _V = ctypes.POINTER(Gdn2View)
@@ -54,6 +64,19 @@ SIGNATURES = {
     "gdn_scalar_backward": (_I, [_S, _I] + [_V] * 7 + [_P, _Z, _V, _F, _F] + [_P] * 3
                             + [_F] * 3 + [_P, _Z, _P]),
     "gdn2_decode_step": (_I, [_S] + [_V] * 8 + [_F, _P, ctypes.c_int32, _F, _P]),
+    "gdn2_conv_forward": (_I, [ctypes.POINTER(Gdn2ConvShape)] + [_V] * 4 + [_I, _F, _P]),
+    "gdn2_conv_workspace_bytes": (_Z, [ctypes.POINTER(Gdn2ConvShape)]),
+    "gdn2_conv_backward": (_I, [ctypes.POINTER(Gdn2ConvShape)] + [_V] * 4 + [_I, _V, _F, _F, _P,
+                                                                              _Z, _P]),
+    "gdn2_norm_forward": (_I, [ctypes.POINTER(Gdn2RowsShape), _I, ctypes.c_float] + [_V] * 3
+                          + [_F, _F, _P]),
+    "gdn2_norm_workspace_bytes": (_Z, [ctypes.POINTER(Gdn2RowsShape)]),
+    "gdn2_norm_backward": (_I, [ctypes.POINTER(Gdn2RowsShape), _I] + [_V] * 3 + [_F, _V]
+                           + [_F] * 3 + [_P, _Z, _P]),
+    "gdn2_decay_forward": (_I, [ctypes.POINTER(Gdn2RowsShape)] + [_V] * 3 + [_F, _P]),
+    "gdn2_decay_workspace_bytes": (_Z, [ctypes.POINTER(Gdn2RowsShape)]),
+    "gdn2_decay_backward": (_I, [ctypes.POINTER(Gdn2RowsShape)] + [_V] * 4 + [_F] * 3
+                            + [_P, _Z, _P]),
     "gdn2_stage_timing": (_I, [_I]),
     "gdn2_stage_count": (_I, []),
     "gdn2_stage_name": (ctypes.c_char_p, [_I]),

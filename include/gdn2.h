@@ -156,6 +156,78 @@ GDN2_API int gdn2_decode_step(const gdn2_shape *shape, const gdn2_view *q, const
                      float *state, void *output, int32_t output_dtype, float *scores,
                      void *stream);
 
+/* ---- Mixer prologue / epilogue operators --------------------------------- */
+/* The elementwise and row-local operators around the scan in the reference's
+ * GDN mixer (crates/mixers/src/lib.rs:456-525, :667-688), as the reference's
+ * custom ops expose them (crates/kernels/src/conv.rs, norm.rs, decay.rs).  All
+ * tensors are F32; inputs are strided views, outputs and gradients are dense.
+ * Parameter gradients are reduced deterministically through a caller-provided
+ * workspace (its size from the *_workspace_bytes query). */
+
+/* Rows of a [batch, time, heads, width] tensor (width = channels of one row). */
+typedef struct gdn2_rows_shape {
+    int64_t batch, time, heads, width;
+} gdn2_rows_shape;
+
+/* Depthwise causal convolution with `taps` lags over [batch, time, channels]
+ * (reference crates/kernels/src/conv.rs:22-45 forward, :47-104 VJP; the
+ * mixer's causal_conv, crates/mixers/src/lib.rs:696-725):
+ *   y[b,t,c] = sum_{l < taps, l <= t} x[b,t-l,c] w[l,c] m(b, t-l, t),
+ *   m(b,s,d) = valid[b,s] valid[b,d] [docs[b,s] == docs[b,d]]
+ * (a lag never crosses a document boundary or an invalid token).  x views
+ * [batch, time, channels] (stride[3] unused), w views [taps, channels],
+ * valid/docs [batch, time].  activation 1 applies SiLU to y in the same pass
+ * (the mixer applies it right after the convolution, lib.rs:463-466);
+ * activation 0 is the reference operator itself.  taps 1..8. */
+typedef struct gdn2_conv_shape {
+    int64_t batch, time, channels, taps;
+} gdn2_conv_shape;
+
+GDN2_API int gdn2_conv_forward(const gdn2_conv_shape *shape, const gdn2_view *x,
+                               const gdn2_view *w, const gdn2_view *valid, const gdn2_view *docs,
+                               int activation, float *y, void *stream);
+GDN2_API size_t gdn2_conv_workspace_bytes(const gdn2_conv_shape *shape);
+/* dy: [batch, time, channels] view.  dx dense [batch, time, channels], dw dense
+ * [taps, channels]; either may be NULL (not wanted). */
+GDN2_API int gdn2_conv_backward(const gdn2_conv_shape *shape, const gdn2_view *x,
+                                const gdn2_view *w, const gdn2_view *valid, const gdn2_view *docs,
+                                int activation, const gdn2_view *dy, float *dx, float *dw,
+                                void *workspace, size_t workspace_bytes, void *stream);
+
+/* Row normalization (reference crates/kernels/src/norm.rs:22-72 forward,
+ * :74-164 VJPs), rows of width <= 1024:
+ *   mode 0 (L2):        y = x / sqrt(sum x^2 + eps)
+ *   mode 1 (RMS):       y = w x / sqrt(mean x^2 + eps)
+ *   mode 2 (gated RMS): z = x sigmoid(gate), y = w z / sqrt(mean z^2 + eps)
+ * weight [width] (modes 1, 2; view stride[0]) and gate (mode 2, same shape as
+ * x) may otherwise be NULL.  inverse [rows] receives 1/sqrt(...) for the
+ * backward. */
+GDN2_API int gdn2_norm_forward(const gdn2_rows_shape *shape, int mode, float epsilon,
+                               const gdn2_view *x, const gdn2_view *weight, const gdn2_view *gate,
+                               float *y, float *inverse, void *stream);
+GDN2_API size_t gdn2_norm_workspace_bytes(const gdn2_rows_shape *shape);
+/* dx (and dgate for mode 2) dense like x; dweight [width] (modes 1, 2).  Any
+ * gradient pointer may be NULL. */
+GDN2_API int gdn2_norm_backward(const gdn2_rows_shape *shape, int mode, const gdn2_view *x,
+                                const gdn2_view *weight, const gdn2_view *gate,
+                                const float *inverse, const gdn2_view *dy, float *dx, float *dgate,
+                                float *dweight, void *workspace, size_t workspace_bytes,
+                                void *stream);
+
+/* Decay gate (reference crates/kernels/src/decay.rs): with z = x + bias[h,k],
+ * softplus(z) = z for z > 20 else log1p(exp(z)),
+ *   alpha = exp(-exp(scale[h]) softplus(z)).
+ * x [batch, time, heads, width], bias [heads * width], scale [heads] (views use
+ * stride[0]).  Backward: dx, dbias [heads * width], dscale [heads]. */
+GDN2_API int gdn2_decay_forward(const gdn2_rows_shape *shape, const gdn2_view *x,
+                                const gdn2_view *bias, const gdn2_view *scale, float *y,
+                                void *stream);
+GDN2_API size_t gdn2_decay_workspace_bytes(const gdn2_rows_shape *shape);
+GDN2_API int gdn2_decay_backward(const gdn2_rows_shape *shape, const gdn2_view *x,
+                                 const gdn2_view *bias, const gdn2_view *scale,
+                                 const gdn2_view *dy, float *dx, float *dbias, float *dscale,
+                                 void *workspace, size_t workspace_bytes, void *stream);
+
 /* Measurement hook.  No counterpart in the reference: it serves benchmarks
  * that need the duration of each kernel of the chunk-WY path, measured on the
  * stream the kernels run on.  After gdn2_stage_timing(1), every chunk-path
