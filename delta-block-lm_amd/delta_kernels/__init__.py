@@ -345,5 +345,8 @@ def stage_times() -> dict:
 
 
 from .mixer_ops import causal_conv, decay, l2_norm, rms_norm  # noqa: E402
+from .train_ops import (FusedAdamW, adamw_update, cross_entropy_rows,  # noqa: E402
+                        linear_cross_entropy)
 
-__all__ += ["causal_conv", "l2_norm", "rms_norm", "decay"]
+__all__ += ["causal_conv", "l2_norm", "rms_norm", "decay", "cross_entropy_rows",
+            "linear_cross_entropy", "adamw_update", "FusedAdamW"]

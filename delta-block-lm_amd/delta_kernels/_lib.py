@@ -43,6 +43,11 @@ class Gdn2RowsShape(ctypes.Structure):
                 ("width", ctypes.c_int64)]
 
 
+class Gdn2AdamwTensor(ctypes.Structure):
+    _fields_ = [("param", ctypes.c_void_p), ("grad", ctypes.c_void_p), ("first", ctypes.c_void_p),
+                ("second", ctypes.c_void_p), ("numel", ctypes.c_int64)]
+
+
 # Exported symbols and their signatures: (name, restype, argtypes).
 _P = ctypes.c_void_p
 _V = ctypes.POINTER(Gdn2View)
@@ -77,6 +82,16 @@ SIGNATURES = {
     "gdn2_decay_workspace_bytes": (_Z, [ctypes.POINTER(Gdn2RowsShape)]),
     "gdn2_decay_backward": (_I, [ctypes.POINTER(Gdn2RowsShape)] + [_V] * 4 + [_F] * 3
                             + [_P, _Z, _P]),
+    "gdn2_cross_entropy_forward": (_I, [ctypes.c_int64, ctypes.c_int64, _V, _P, ctypes.c_int64,
+                                        _F, _F, _P]),
+    "gdn2_cross_entropy_backward": (_I, [ctypes.c_int64, ctypes.c_int64, _V, _P, ctypes.c_int64,
+                                         _F, _F, ctypes.c_int64, _P, _P]),
+    "gdn2_cross_entropy_fused": (_I, [ctypes.c_int64, ctypes.c_int64, _V, _P, ctypes.c_int64,
+                                      ctypes.c_float, _F, _P, _P]),
+    "gdn2_adamw_workspace_bytes": (_Z, [ctypes.c_int32, ctypes.POINTER(Gdn2AdamwTensor)]),
+    "gdn2_adamw_update": (_I, [ctypes.c_int32, ctypes.POINTER(Gdn2AdamwTensor), _I,
+                               ctypes.c_int64, ctypes.c_double, ctypes.c_float, ctypes.c_float,
+                               _I, _P, _Z, _P]),
     "gdn2_stage_timing": (_I, [_I]),
     "gdn2_stage_count": (_I, []),
     "gdn2_stage_name": (ctypes.c_char_p, [_I]),

@@ -1,0 +1,172 @@
+"""The lm512 GDN language model and its training step.
+
+Each of the `layers` blocks is pre-norm residual
+    x += mixer(rms_norm(x));  x += swiglu(rms_norm(x))
+followed by a final RMSNorm and the tied embedding as output head, with AdamW
+(block structure: crates/experiment/src/model.rs:300-364; train step:
+crates/experiment/src/train.rs:335-357; optimizer: update.rs:43-96).  Widths
+follow configuration 4, which is not the reference's own lm512 (d_model 512,
+8 layers, H8 K64 V64, SwiGLU 1408, vocab 32768, tied head).  The mixer is the scalar-gate gated delta rule:
+    q = l2(silu(conv(x Wq)))   k = l2(silu(conv(x Wk)))   v = silu(conv(x Wv))
+    beta = sigmoid(x Wb)       g = -exp(decay_scale) * softplus(x Wg + decay_bias)
+    o = scan(q, k, v, beta, g)                       chunk-WY HIP kernels
+    y = (rms_norm(o) * silu(x Wgate)) Wout           SiLU output gate
+The convolution and every norm are the library's HIP operators (float32, as the
+reference's); projections and the MLP are GEMMs in `compute_dtype` (bfloat16 by
+default, float32 master weights).  In bfloat16, q/k/v enter the scan as bf16 and
+take the chunk-WY MFMA path (d_k = d_v = 64, chunk 64); in float32 the scan runs
+the token-sequential kernels.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+import delta_kernels as dk
+
+
+@dataclass
+class GdnLMConfig:
+    vocab: int = 32768
+    d_model: int = 512
+    layers: int = 8
+    heads: int = 8
+    key_dim: int = 64
+    value_dim: int = 64
+    conv_taps: int = 4
+    mlp_width: int = 1408
+    chunk: int = 64
+    norm_epsilon: float = 1e-6  # the reference model's RMSNorm epsilon (model.rs:108-111)
+    decay_bias: float = -4.0  # the reference mixer's initial bias (alpha close to 1)
+    compute_dtype: torch.dtype = torch.bfloat16
+
+
+def _linear(i, o, device):
+    w = torch.empty(o, i, device=device)
+    torch.nn.init.normal_(w, std=i ** -0.5)
+    return torch.nn.Parameter(w)
+
+
+def _mm(x, w):
+    return F.linear(x, w.to(x.dtype))
+
+
+class ScalarGdnMixer(torch.nn.Module):
+    def __init__(self, cfg: GdnLMConfig, device=None):
+        super().__init__()
+        self.cfg = cfg
+        D, H, K, V = cfg.d_model, cfg.heads, cfg.key_dim, cfg.value_dim
+        self.q = _linear(D, H * K, device)
+        self.k = _linear(D, H * K, device)
+        self.v = _linear(D, H * V, device)
+        self.beta = _linear(D, H, device)
+        self.decay = _linear(D, H, device)
+        self.gate = _linear(D, H * V, device)
+        self.out = _linear(H * V, D, device)
+        conv = lambda c: torch.nn.Parameter(  # noqa: E731
+            torch.empty(cfg.conv_taps, c, device=device).uniform_(-0.1, 0.1))
+        self.q_conv, self.k_conv, self.v_conv = conv(H * K), conv(H * K), conv(H * V)
+        self.decay_scale = torch.nn.Parameter(torch.zeros(H, device=device))
+        self.decay_bias = torch.nn.Parameter(torch.full((H,), cfg.decay_bias, device=device))
+        self.norm_weight = torch.nn.Parameter(torch.ones(V, device=device))
+
+    def forward(self, x, valid, docs):
+        """x [B, T, d_model] in compute_dtype; valid/docs [B, T] float32."""
+        cfg = self.cfg
+        B, T, _ = x.shape
+        H, K, V = cfg.heads, cfg.key_dim, cfg.value_dim
+        cd = cfg.compute_dtype
+
+        def branch(w, conv, width):
+            y = dk.causal_conv(_mm(x, w).float(), conv, valid, docs, activation="silu")
+            return y.view(B, T, H, width)
+
+        q = dk.l2_norm(branch(self.q, self.q_conv, K)).to(cd)
+        k = dk.l2_norm(branch(self.k, self.k_conv, K)).to(cd)
+        v = branch(self.v, self.v_conv, V).to(cd)
+        beta = torch.sigmoid(_mm(x, self.beta).float())
+        g = -torch.exp(self.decay_scale) * F.softplus(_mm(x, self.decay).float() +
+                                                      self.decay_bias)
+        o, _, _ = dk.gdn_scalar_scan(q, k, v, beta, g, valid, None, None, cfg.chunk)
+        o = dk.rms_norm(o.float(), self.norm_weight, None, cfg.norm_epsilon)
+        y = o.reshape(B, T, H * V) * F.silu(_mm(x, self.gate).float())
+        return _mm(y.to(cd), self.out)
+
+
+class SwiGLU(torch.nn.Module):
+    def __init__(self, cfg: GdnLMConfig, device=None):
+        super().__init__()
+        D, M = cfg.d_model, cfg.mlp_width
+        self.w1 = _linear(D, M, device)
+        self.w3 = _linear(D, M, device)
+        self.w2 = _linear(M, D, device)
+
+    def forward(self, x):
+        return _mm(F.silu(_mm(x, self.w1)) * _mm(x, self.w3), self.w2)
+
+
+class Block(torch.nn.Module):
+    def __init__(self, cfg: GdnLMConfig, device=None):
+        super().__init__()
+        self.cfg = cfg
+        self.norm1 = torch.nn.Parameter(torch.ones(cfg.d_model, device=device))
+        self.norm2 = torch.nn.Parameter(torch.ones(cfg.d_model, device=device))
+        self.mixer = ScalarGdnMixer(cfg, device)
+        self.mlp = SwiGLU(cfg, device)
+
+    def forward(self, x, valid, docs):
+        """x [B, T, d_model] float32 residual stream."""
+        eps, cd = self.cfg.norm_epsilon, self.cfg.compute_dtype
+        x = x + self.mixer(dk.rms_norm(x, self.norm1, None, eps).to(cd), valid, docs).float()
+        return x + self.mlp(dk.rms_norm(x, self.norm2, None, eps).to(cd)).float()
+
+
+class GdnLM(torch.nn.Module):
+    def __init__(self, cfg: GdnLMConfig, device=None):
+        super().__init__()
+        self.cfg = cfg
+        self.embed = torch.nn.Parameter(torch.randn(cfg.vocab, cfg.d_model, device=device) * 0.02)
+        self.blocks = torch.nn.ModuleList(Block(cfg, device) for _ in range(cfg.layers))
+        self.norm = torch.nn.Parameter(torch.ones(cfg.d_model, device=device))
+
+    def features(self, tokens):
+        """tokens [B, T] int64 -> final-norm features [B, T, d_model] float32."""
+        B, T = tokens.shape
+        valid = torch.ones(B, T, device=tokens.device)
+        docs = torch.zeros(B, T, device=tokens.device)
+        x = self.embed[tokens]
+        for blk in self.blocks:
+            x = blk(x, valid, docs)
+        return dk.rms_norm(x, self.norm, None, self.cfg.norm_epsilon)
+
+    def forward(self, tokens):
+        """tokens [B, T] int64 -> logits [B, T, vocab] in compute_dtype."""
+        return _mm(self.features(tokens).to(self.cfg.compute_dtype), self.embed)
+
+    def loss(self, tokens):
+        """Mean next-token cross entropy over positions 0..T-2: the tied head and
+        the loss in one operator (logits computed once, replaced in place by
+        their gradient)."""
+        cd = self.cfg.compute_dtype
+        h = self.features(tokens[:, :-1]).to(cd)
+        return dk.linear_cross_entropy(h.reshape(-1, self.cfg.d_model), self.embed.to(cd),
+                                       tokens[:, 1:].reshape(-1))
+
+
+def make_optimizer(model: GdnLM, lr: float = 1e-3, weight_decay: float = 0.01,
+                   clip: float = 1.0):
+    """The reference's optimizer (FusedAdamW: per-parameter gradient clipping,
+    then AdamW; crates/experiment/src/train.rs:20-38) over float32 master
+    weights, with its default hyperparameters (config.rs:442-444)."""
+    return dk.FusedAdamW(model.parameters(), lr=lr, weight_decay=weight_decay, clip=clip)
+
+
+def train_step(model: GdnLM, opt: torch.optim.Optimizer, tokens: torch.Tensor) -> torch.Tensor:
+    """One forward, backward and AdamW update; returns the detached loss."""
+    opt.zero_grad(set_to_none=True)
+    loss = model.loss(tokens)
+    loss.backward()
+    opt.step()
+    return loss.detach()

@@ -228,6 +228,66 @@ GDN2_API int gdn2_decay_backward(const gdn2_rows_shape *shape, const gdn2_view *
                                  const gdn2_view *dy, float *dx, float *dbias, float *dscale,
                                  void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- Training-step operators ---------------------------------------------- */
+
+/* Row cross entropy (reference crates/kernels/src/cross_entropy.rs:7-60 forward,
+ * :62-83 backward; op cross_entropy_rows, cross_entropy_ops.rs:108-117):
+ *   m = max_c x[r,c],  s = ln sum_c exp(x[r,c] - m)
+ *   loss[r] = (m - x[r, target[r]]) + s,   stats[2r] = m, stats[2r+1] = s
+ *   dx[r,c] = (exp(x[r,c] - m - s) - [c == target[r]]) * upstream[r]
+ * x: [rows, width] F32 or BF16 (stride[0] between rows, stride[1] between
+ * columns).  target: int64 class ids, target[r * target_stride] (the reference
+ * passes integral f32 labels); an id outside [0, width) gives loss NaN and no
+ * one-hot term.  upstream: f32, upstream[r * upstream_stride].  dx: contiguous
+ * [rows, width] in x's dtype. */
+GDN2_API int gdn2_cross_entropy_forward(int64_t rows, int64_t width, const gdn2_view *x,
+                                        const int64_t *target, int64_t target_stride,
+                                        float *loss, float *stats, void *stream);
+GDN2_API int gdn2_cross_entropy_backward(int64_t rows, int64_t width, const gdn2_view *x,
+                                         const int64_t *target, int64_t target_stride,
+                                         const float *stats, const float *upstream,
+                                         int64_t upstream_stride, void *dx, void *stream);
+/* Forward and gradient in one pass over the rows, for a loss whose upstream
+ * gradient per row is the constant `scale` (a mean over rows: 1 / rows):
+ * loss[r] as above and dx[r,c] = (exp(x[r,c] - m - s) - [c == target[r]]) * scale.
+ * dx may be x's own storage (x contiguous): the logits are then replaced by
+ * their gradient.  No counterpart in the reference, which runs the two kernels
+ * above; it serves training steps that need the logits only for this loss. */
+GDN2_API int gdn2_cross_entropy_fused(int64_t rows, int64_t width, const gdn2_view *x,
+                                      const int64_t *target, int64_t target_stride, float scale,
+                                      float *loss, void *dx, void *stream);
+
+/* AdamW with per-parameter gradient clipping (reference
+ * crates/kernels/src/update.rs:46-82 adam_kernel and :116-199 adam; op
+ * adamw_update, update_ops.rs:90-117; caller FusedAdamW,
+ * crates/experiment/src/update.rs:43-96).  For each tensor, with its own
+ * gradient norm n = sqrt(sum g^2):
+ *   g' = g * min(clip / (n + FLT_MIN), 1)
+ *   m  = g' (1 - 0.9)        [+ 0.9 m_prev   when initialized]
+ *   v  = g'^2 (1 - 0.999)    [+ 0.999 v_prev when initialized]
+ *   param = param * (1 - lr weight_decay) - lr (m / c1) / (sqrt(v / c2) + 1e-5)
+ * with c1 = 1 - 0.9^time and c2 = 1 - 0.999^time in f32, every operation
+ * rounded in this order (no fused multiply-adds).  param, first and second are
+ * updated in place; all f32 and contiguous. */
+typedef struct gdn2_adamw_tensor {
+    float *param;
+    const float *grad;
+    float *first;  /* first moment (read only when initialized) */
+    float *second; /* second moment */
+    int64_t numel;
+} gdn2_adamw_tensor;
+
+/* One launch pair for a whole parameter set: the descriptor table and the
+ * per-chunk squared-norm partials live in the workspace.  With reuse_table
+ * nonzero the workspace must still hold the table that a previous call wrote
+ * for the same tensors; the call then skips rewriting it.  The norms are
+ * reduced in a fixed order: results do not depend on the launch. */
+GDN2_API size_t gdn2_adamw_workspace_bytes(int32_t count, const gdn2_adamw_tensor *tensors);
+GDN2_API int gdn2_adamw_update(int32_t count, const gdn2_adamw_tensor *tensors, int initialized,
+                               int64_t time, double lr, float weight_decay, float clip,
+                               int reuse_table, void *workspace, size_t workspace_bytes,
+                               void *stream);
+
 /* Measurement hook.  No counterpart in the reference: it serves benchmarks
  * that need the duration of each kernel of the chunk-WY path, measured on the
  * stream the kernels run on.  After gdn2_stage_timing(1), every chunk-path
