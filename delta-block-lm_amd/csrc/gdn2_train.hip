@@ -147,14 +147,20 @@ __device__ Lse row_lse(const CeArgs &a, int64_t r) {
     return acc;
 }
 
+// x[r, target[r]] (thread 0 only), or NaN for a label outside [0, width).  Read
+// before the row's reduction barrier: the fused kernel overwrites x after it.
 template <typename T>
-__device__ void write_row_loss(const CeArgs &a, int64_t r, Lse t, float *loss, float *stats) {
+__device__ float target_logit(const CeArgs &a, int64_t r) {
+    if (threadIdx.x != 0) return 0.f;
+    const int64_t label = a.target[r * a.ts];
+    return label >= 0 && label < a.width ? Elem<T>::load(a.x, r * a.rs + label * a.cs)
+                                         : __builtin_nanf("");
+}
+
+__device__ void write_row_loss(int64_t r, Lse t, float xl, float *loss, float *stats) {
     if (threadIdx.x != 0) return;
     const float logsum = logf(t.s);
-    const int64_t label = a.target[r * a.ts];
-    float l = __builtin_nanf("");
-    if (label >= 0 && label < a.width) l = (t.m - Elem<T>::load(a.x, r * a.rs + label * a.cs)) + logsum;
-    loss[r] = l;
+    loss[r] = (t.m - xl) + logsum;
     if (stats) {
         stats[2 * r] = t.m;
         stats[2 * r + 1] = logsum;
@@ -192,8 +198,9 @@ template <typename T>
 __global__ void __launch_bounds__(kCeThreads) ce_forward_kernel(CeArgs a) {
     __shared__ Lse red[kCeThreads / 64];
     const int64_t r = blockIdx.x;
+    const float xl = target_logit<T>(a, r);
     const Lse t = lse_block(row_lse<T>(a, r), red);
-    write_row_loss<T>(a, r, t, a.loss, a.stats);
+    write_row_loss(r, t, xl, a.loss, a.stats);
 }
 
 template <typename T>
@@ -206,10 +213,12 @@ template <typename T>
 __global__ void __launch_bounds__(kCeThreads) ce_fused_kernel(CeArgs a) {
     __shared__ Lse red[kCeThreads / 64];
     const int64_t r = blockIdx.x;
+    const float xl = target_logit<T>(a, r);
     const Lse t = lse_block(row_lse<T>(a, r), red);
-    write_row_loss<T>(a, r, t, a.loss, nullptr);
-    // Every thread has read its elements of row r (lse_block's barrier) before
-    // any of them is overwritten; each element is rewritten by its own reader.
+    write_row_loss(r, t, xl, a.loss, nullptr);
+    // Every thread has read its elements of row r, and thread 0 the target
+    // logit, before lse_block's barrier; past it each element is rewritten
+    // only by the thread that read it.
     write_row_grad<T>(a, r, t.m, logf(t.s), a.scale);
 }
 

@@ -54,20 +54,20 @@ def _mm(x, w):
 
 
 class ScalarGdnMixer(torch.nn.Module):
+    """Input projections packed in one weight, rows [q | k | v | gate | beta |
+    decay] (one GEMM per direction; the reference packs its seven projections
+    the same way at execution time, crates/mixers/src/projections.rs:31-44),
+    and one depthwise convolution over the q | k | v channels."""
+
     def __init__(self, cfg: GdnLMConfig, device=None):
         super().__init__()
         self.cfg = cfg
         D, H, K, V = cfg.d_model, cfg.heads, cfg.key_dim, cfg.value_dim
-        self.q = _linear(D, H * K, device)
-        self.k = _linear(D, H * K, device)
-        self.v = _linear(D, H * V, device)
-        self.beta = _linear(D, H, device)
-        self.decay = _linear(D, H, device)
-        self.gate = _linear(D, H * V, device)
+        self.widths = (H * K, H * K, H * V, H * V, H, H)  # q, k, v, gate, beta, decay
+        self.in_proj = _linear(D, sum(self.widths), device)
         self.out = _linear(H * V, D, device)
-        conv = lambda c: torch.nn.Parameter(  # noqa: E731
-            torch.empty(cfg.conv_taps, c, device=device).uniform_(-0.1, 0.1))
-        self.q_conv, self.k_conv, self.v_conv = conv(H * K), conv(H * K), conv(H * V)
+        self.qkv_conv = torch.nn.Parameter(
+            torch.empty(cfg.conv_taps, 2 * H * K + H * V, device=device).uniform_(-0.1, 0.1))
         self.decay_scale = torch.nn.Parameter(torch.zeros(H, device=device))
         self.decay_bias = torch.nn.Parameter(torch.full((H,), cfg.decay_bias, device=device))
         self.norm_weight = torch.nn.Parameter(torch.ones(V, device=device))
@@ -78,33 +78,36 @@ class ScalarGdnMixer(torch.nn.Module):
         B, T, _ = x.shape
         H, K, V = cfg.heads, cfg.key_dim, cfg.value_dim
         cd = cfg.compute_dtype
-
-        def branch(w, conv, width):
-            y = dk.causal_conv(_mm(x, w).float(), conv, valid, docs, activation="silu")
-            return y.view(B, T, H, width)
-
-        q = dk.l2_norm(branch(self.q, self.q_conv, K)).to(cd)
-        k = dk.l2_norm(branch(self.k, self.k_conv, K)).to(cd)
-        v = branch(self.v, self.v_conv, V).to(cd)
-        beta = torch.sigmoid(_mm(x, self.beta).float())
-        g = -torch.exp(self.decay_scale) * F.softplus(_mm(x, self.decay).float() +
-                                                      self.decay_bias)
+        z = _mm(x, self.in_proj)
+        qkv_w = 2 * H * K + H * V
+        qkv = dk.causal_conv(z[..., :qkv_w].float(), self.qkv_conv, valid, docs,
+                             activation="silu")
+        qk = dk.l2_norm(qkv[..., :2 * H * K].view(B, T, 2 * H, K)).to(cd)
+        q, k = qk[:, :, :H], qk[:, :, H:]
+        v = qkv[..., 2 * H * K:].to(cd).view(B, T, H, V)
+        rest = z[..., qkv_w:].float()
+        gate, beta, dec = rest[..., :H * V], rest[..., H * V:H * V + H], rest[..., H * V + H:]
+        beta = torch.sigmoid(beta)
+        g = -torch.exp(self.decay_scale) * F.softplus(dec + self.decay_bias)
         o, _, _ = dk.gdn_scalar_scan(q, k, v, beta, g, valid, None, None, cfg.chunk)
         o = dk.rms_norm(o.float(), self.norm_weight, None, cfg.norm_epsilon)
-        y = o.reshape(B, T, H * V) * F.silu(_mm(x, self.gate).float())
+        y = o.reshape(B, T, H * V) * F.silu(gate)
         return _mm(y.to(cd), self.out)
 
 
 class SwiGLU(torch.nn.Module):
+    """w13 packs the gate and up projections ([w1 | w3] rows): one GEMM."""
+
     def __init__(self, cfg: GdnLMConfig, device=None):
         super().__init__()
         D, M = cfg.d_model, cfg.mlp_width
-        self.w1 = _linear(D, M, device)
-        self.w3 = _linear(D, M, device)
+        self.M = M
+        self.w13 = _linear(D, 2 * M, device)
         self.w2 = _linear(M, D, device)
 
     def forward(self, x):
-        return _mm(F.silu(_mm(x, self.w1)) * _mm(x, self.w3), self.w2)
+        h = _mm(x, self.w13)
+        return _mm(F.silu(h[..., :self.M]) * h[..., self.M:], self.w2)
 
 
 class Block(torch.nn.Module):

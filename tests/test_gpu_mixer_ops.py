@@ -116,3 +116,65 @@ def test_operators_reject_cpu_and_wrong_dtype(dk):
         dk.l2_norm(x)
     with pytest.raises(TypeError):
         dk.l2_norm(x.cuda().double())
+
+
+def _docs_valid(rng, B, T):
+    valid = np.ones((B, T), np.float32)
+    valid[0, T // 3] = 0
+    valid[-1, T - 2:] = 0
+    reset = np.zeros((B, T), np.float32)
+    reset[:, 0] = 1
+    reset[0, T // 2] = 1
+    reset[-1, 33] = 1  # inside the second 32-step segment
+    return valid, np.cumsum(valid * reset, axis=1).astype(np.float32)
+
+
+@pytest.mark.parametrize("taps", [3, 4, 8])
+@pytest.mark.parametrize("act", [None, "silu"])
+def test_causal_conv_long_sequences(dk, taps, act):
+    """Several 32-step time segments per sequence, documents crossing them."""
+    rng = np.random.default_rng(taps)
+    B, T, C = 2, 130, 96  # channel count not a multiple of 64
+    x = rng.normal(size=(B, T, C)).astype(np.float32)
+    w = (rng.normal(size=(taps, C)) * 0.5).astype(np.float32)
+    u = rng.normal(size=(B, T, C)).astype(np.float32)
+    valid, docs = _docs_valid(rng, B, T)
+    xg, wg = up(x, True), up(w, True)
+    y = dk.causal_conv(xg, wg, up(valid), up(docs), activation=act)
+    silu = act == "silu"
+    ref_gate("conv output", y, mo.causal_conv(x, w, valid, docs, silu))
+    (y * up(u)).sum().backward()
+    dx, dw = mo.causal_conv_vjp(x, w, valid, docs, u, silu)
+    ref_gate("conv dx", xg.grad, dx)
+    ref_gate("conv dw", wg.grad, dw)
+
+
+@pytest.mark.parametrize("width", [64, 128, 192, 256, 512, 768, 1024])
+@pytest.mark.parametrize("mode,eps", mf.NORM_MODES)
+@pytest.mark.parametrize("rows", [(3, 37, 5), (2, 1100, 2)])
+def test_norms_contiguous_rows(dk, width, mode, eps, rows):
+    """Contiguous rows (the 16-byte-access kernels): partial workgroups, and more
+    rows than the backward grid holds (each group loops)."""
+    if mode == 0 and eps != 1e-6:
+        pytest.skip("l2_norm has the reference's fixed epsilon")
+    rng = np.random.default_rng(width + mode)
+    B, T, H = rows
+    x = rng.normal(size=(B, T, H, width)).astype(np.float32)
+    gate = (rng.normal(size=x.shape) * 2).astype(np.float32)
+    weight = rng.normal(size=width).astype(np.float32)
+    u = rng.normal(size=x.shape).astype(np.float32)
+    xg, gg, wg = up(x, True), up(gate, True), up(weight, True)
+    if mode == 0:
+        y = dk.l2_norm(xg)
+    elif mode == 1:
+        y = dk.rms_norm(xg, wg, None, eps)
+    else:
+        y = dk.rms_norm(xg, wg, gg, eps)
+    ref_gate("norm output", y, mo.row_norm(x, weight, gate, mode, eps)[0])
+    (y * up(u)).sum().backward()
+    dx, dg, dw = mo.row_norm_vjp(x, weight, gate, mode, eps, u)
+    ref_gate("norm dx", xg.grad, dx)
+    if mode >= 1:
+        ref_gate("norm dweight", wg.grad, dw)
+    if mode == 2:
+        ref_gate("norm dgate", gg.grad, dg)

@@ -167,3 +167,32 @@ def test_fused_adamw_multi_tensor_matches_per_tensor_calls():
             states[i] = (m, v)
         for p, r in zip(ps, refs):
             assert torch.equal(p.detach(), r), "multi-tensor and per-tensor updates differ"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fused_cross_entropy_in_place_reads_target_before_overwrite(dtype):
+    """The in-place fused kernel must read x[r, target] before any thread of
+    the row writes its gradient: every label here sits in columns that the
+    row's last wave reads and rewrites."""
+    _need_gpu()
+    import ctypes
+    import delta_kernels as dk
+    from delta_kernels import _ptr, _stream, _view
+    rows, width = 512, 32768
+    rng = np.random.default_rng(9)
+    x = (rng.normal(size=(rows, width)) * 2).astype(np.float32)
+    vec = 4 if dtype == torch.float32 else 8
+    cols = np.arange(width)
+    last_wave = cols[(cols // vec) % 256 >= 192]
+    t = rng.choice(last_wave, size=rows)
+    xd = torch.from_numpy(x).cuda().to(dtype)
+    xr = xd.double().cpu().numpy()
+    td = torch.from_numpy(t).cuda()
+    loss = torch.empty(rows, device="cuda")
+    rc = dk.lib().gdn2_cross_entropy_fused(rows, width, ctypes.byref(_view(xd)), _ptr(td), 1,
+                                           ctypes.c_float(1.0), _ptr(loss), _ptr(xd), _stream(xd))
+    assert rc == 0
+    ref_loss, _ = to.cross_entropy_rows(xr, t)
+    gate("loss", loss, ref_loss, 1e-5)
+    tol = 1e-5 if dtype == torch.float32 else 2.0 ** -8
+    gate("dx", xd, to.cross_entropy_rows_vjp(xr, t, np.ones(rows)), tol)
