@@ -39,10 +39,13 @@ const char *last_error() { return g_error.c_str(); }
 int check_view(const gdn2_view *v, const char *name, int dtype, bool data_may_be_null) {
     if (!v) return fail(GDN2_ERR_ARGUMENT, "%s: view is null", name);
     if (!v->data && !data_may_be_null) return fail(GDN2_ERR_ARGUMENT, "%s: data is null", name);
-    if (v->dtype != GDN2_F32 && v->dtype != GDN2_BF16)
+    if (v->dtype != GDN2_F32 && v->dtype != GDN2_BF16 && v->dtype != GDN2_I32)
         return fail(GDN2_ERR_DTYPE, "%s: unknown dtype %d", name, v->dtype);
+    if (dtype < 0 && v->dtype == GDN2_I32)
+        return fail(GDN2_ERR_DTYPE, "%s: dtype must be F32 or BF16", name);
     if (dtype >= 0 && v->dtype != dtype)
-        return fail(GDN2_ERR_DTYPE, "%s: dtype must be %s", name, dtype == GDN2_F32 ? "F32" : "BF16");
+        return fail(GDN2_ERR_DTYPE, "%s: dtype must be %s", name,
+                    dtype == GDN2_F32 ? "F32" : (dtype == GDN2_BF16 ? "BF16" : "I32"));
     for (int d = 0; d < 4; ++d)
         if (v->stride[d] < 0) return fail(GDN2_ERR_ARGUMENT, "%s: negative stride", name);
     return GDN2_OK;
@@ -118,6 +121,20 @@ int check_channel_inputs(const gdn2_shape *shape, const gdn2_view *q, const gdn2
     GDN2_TRY(check_view(write, "write", GDN2_F32, false));
     GDN2_TRY(check_view(valid, "valid", GDN2_F32, false));
     GDN2_TRY(check_view(reset, "reset", GDN2_F32, false));
+    return GDN2_OK;
+}
+
+int check_doc_inputs(const gdn2_view *q, const gdn2_view *k, const gdn2_view *v,
+                     const gdn2_view *alpha, const gdn2_view *erase, const gdn2_view *write,
+                     const gdn2_view *doc_start, const gdn2_view *doc_end) {
+    GDN2_TRY(check_view(q, "q", -1, false));
+    GDN2_TRY(check_view(k, "k", q->dtype, false));
+    GDN2_TRY(check_view(v, "v", q->dtype, false));
+    GDN2_TRY(check_view(alpha, "alpha", GDN2_F32, false));
+    GDN2_TRY(check_view(erase, "erase", GDN2_F32, false));
+    GDN2_TRY(check_view(write, "write", GDN2_F32, false));
+    GDN2_TRY(check_view(doc_start, "doc_start", GDN2_I32, false));
+    GDN2_TRY(check_view(doc_end, "doc_end", GDN2_I32, false));
     return GDN2_OK;
 }
 
@@ -224,6 +241,73 @@ int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gdn2_view *
     a.replay = (float *)workspace;
     return launch_status(launch_seq_bwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
                          "gdn2_training_backward");
+}
+
+size_t gdn2_scan_checkpoint_bytes(const gdn2_shape *shape) {
+    if (check_shape(shape)) return 0;
+    return seq_checkpoint_bytes(shape);
+}
+
+size_t gdn2_scan_workspace_bytes(const gdn2_shape *shape) {
+    if (check_shape(shape)) return 0;
+    return seq_workspace_bytes(shape);
+}
+
+int gdn2_scan(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k, const gdn2_view *v,
+              const gdn2_view *alpha, const gdn2_view *erase, const gdn2_view *write,
+              const gdn2_view *doc_start, const gdn2_view *doc_end, void *output,
+              int32_t output_dtype, void *checkpoint, size_t checkpoint_bytes, void *stream) {
+    GDN2_TRY(check_shape(shape));
+    GDN2_TRY(check_doc_inputs(q, k, v, alpha, erase, write, doc_start, doc_end));
+    GDN2_TRY(check_out_dtype(output_dtype));
+    if (!output) return fail(GDN2_ERR_ARGUMENT, "output is null");
+    if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
+    if (checkpoint_bytes < seq_checkpoint_bytes(shape))
+        return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
+                    seq_checkpoint_bytes(shape), checkpoint_bytes);
+    SeqArgs a = seq_args(shape, q, k, v, alpha, erase, write, nullptr, nullptr);
+    a.doc = 1;
+    a.doc_start = make_view(doc_start);
+    a.doc_end = make_view(doc_end);
+    a.out = output;
+    a.out_bf16 = output_dtype == GDN2_BF16;
+    a.ck = (float *)checkpoint;
+    return launch_status(launch_seq_fwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
+                         "gdn2_scan");
+}
+
+int gdn2_backward(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k,
+                  const gdn2_view *v, const gdn2_view *alpha, const gdn2_view *erase,
+                  const gdn2_view *write, const gdn2_view *doc_start, const gdn2_view *doc_end,
+                  const void *checkpoint, size_t checkpoint_bytes, const gdn2_view *d_output,
+                  void *dq, void *dk, void *dv, float *dalpha, float *derase, float *dwrite,
+                  void *workspace, size_t workspace_bytes, void *stream) {
+    GDN2_TRY(check_shape(shape));
+    GDN2_TRY(check_doc_inputs(q, k, v, alpha, erase, write, doc_start, doc_end));
+    if (d_output) GDN2_TRY(check_view(d_output, "d_output", q->dtype, true));
+    if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
+    if (checkpoint_bytes < seq_checkpoint_bytes(shape))
+        return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
+                    seq_checkpoint_bytes(shape), checkpoint_bytes);
+    if (!workspace) return fail(GDN2_ERR_ARGUMENT, "workspace is null");
+    if (workspace_bytes < seq_workspace_bytes(shape))
+        return fail(GDN2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
+                    seq_workspace_bytes(shape), workspace_bytes);
+    SeqArgs a = seq_args(shape, q, k, v, alpha, erase, write, nullptr, nullptr);
+    a.doc = 1;
+    a.doc_start = make_view(doc_start);
+    a.doc_end = make_view(doc_end);
+    a.ck = (float *)checkpoint;
+    if (d_output) a.dout = make_view(d_output);
+    a.dq = dq;
+    a.dk = dk;
+    a.dv = dv;
+    a.dalpha = dalpha;
+    a.derase = derase;
+    a.dwrite = dwrite;
+    a.replay = (float *)workspace;
+    return launch_status(launch_seq_bwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
+                         "gdn2_backward");
 }
 
 size_t gdn_scalar_checkpoint_bytes(const gdn2_shape *shape, int chunk) {

@@ -11,6 +11,12 @@ constexpr int SEQ_KR = 16;  // state rows held by one thread
 struct SeqArgs {
     int B, T, H, K, V;
     View q, k, v, alpha, erase, write, valid, reset, initial;
+    // Document limits (int32 [batch, time] views, inclusive; end < start marks
+    // padding).  When set they replace valid/reset, and the backward follows
+    // the reference's doc-limit VJP: the adjoint is cleared at tokens with
+    // end == t and passes through resets.
+    int doc;
+    View doc_start, doc_end;
     // Scalar-gate mode: alpha[i] = exp(g), erase[i] = write[j] = beta, with
     // beta and g read as [batch, time, head] views; gradients dbeta and dg.
     int scalar;

@@ -49,7 +49,7 @@ __device__ __forceinline__ void stage_tokens(const SeqArgs &a, int b, int h, int
                                              float (*sq)[KP], float (*sk)[KP],
                                              float (*sa)[KP], float (*se)[KP],
                                              float (*sv)[VP], float (*sw)[VP],
-                                             float *sval, float *srst, int tid) {
+                                             float *sval, float *srst, float *saclr, int tid) {
     constexpr int CT = SEQ_CT;
     for (int idx = tid; idx < CT * KP; idx += NT) {
         const int tt = idx / KP, c = idx % KP, t = t0 + tt;
@@ -73,13 +73,24 @@ __device__ __forceinline__ void stage_tokens(const SeqArgs &a, int b, int h, int
     }
     if (tid < CT) {
         const int t = t0 + tid;
-        float val = 0.f, rst = 0.f;
+        float val = 0.f, rst = 0.f, clr = 0.f;
         if (t < a.T) {
-            val = a.valid.data ? ld4<float>(a.valid, b, t, 0, 0) : 1.f;
-            rst = a.reset.data ? ld4<float>(a.reset, b, t, 0, 0) : 0.f;
+            if (a.doc) {
+                const int32_t st = reinterpret_cast<const int32_t *>(
+                    a.doc_start.data)[b * a.doc_start.s0 + t * a.doc_start.s1];
+                const int32_t en = reinterpret_cast<const int32_t *>(
+                    a.doc_end.data)[b * a.doc_end.s0 + t * a.doc_end.s1];
+                val = en >= st ? 1.f : 0.f;
+                rst = st == t ? 1.f : 0.f;
+                clr = en == t ? 1.f : 0.f;
+            } else {
+                val = a.valid.data ? ld4<float>(a.valid, b, t, 0, 0) : 1.f;
+                rst = a.reset.data ? ld4<float>(a.reset, b, t, 0, 0) : 0.f;
+            }
         }
         sval[tid] = val;
         srst[tid] = rst;
+        if (saclr) saclr[tid] = clr;
     }
 }
 
@@ -112,7 +123,7 @@ __global__ void __launch_bounds__((KP / SEQ_KR) * VP) seq_fwd_kernel(SeqArgs a) 
             for (int r = 0; r < KR; ++r) ck[r * NT + tid] = S[r];
         }
         stage_tokens<KP, VP, NT, TIN>(a, b, h, t0, s.q, s.k, s.a, s.e, s.v, s.w, s.val, s.rst,
-                                      tid);
+                                      nullptr, tid);
         __syncthreads();
         const int nt = min(CT, a.T - t0);
         for (int tt = 0; tt < nt; ++tt) {
@@ -153,7 +164,7 @@ __global__ void __launch_bounds__((KP / SEQ_KR) * VP) seq_fwd_kernel(SeqArgs a) 
                 store_out(a.out, a.out_bf16, (((int64_t)b * a.T + t0 + tt) * a.H + h) * a.V + c,
                           s.o[tt][c]);
         }
-        if (tid < nt) {
+        if (a.scores && tid < nt) {
             float sc = 0.f;
             if (s.val[tid] != 0.f) {
                 float kk = 0.f, dd = 0.f;
@@ -169,10 +180,11 @@ __global__ void __launch_bounds__((KP / SEQ_KR) * VP) seq_fwd_kernel(SeqArgs a) 
 #pragma unroll
     for (int r = 0; r < KR; ++r) sh.st[(i0 + r) * (VP + 1) + j] = S[r];
     __syncthreads();
-    for (int idx = tid; idx < a.K * a.V; idx += NT) {
-        const int i = idx / a.V, c = idx % a.V;
-        a.final_state[(int64_t)bh * a.K * a.V + idx] = sh.st[i * (VP + 1) + c];
-    }
+    if (a.final_state)
+        for (int idx = tid; idx < a.K * a.V; idx += NT) {
+            const int i = idx / a.V, c = idx % a.V;
+            a.final_state[(int64_t)bh * a.K * a.V + idx] = sh.st[i * (VP + 1) + c];
+        }
 }
 
 template <int KP, int VP>
@@ -180,7 +192,7 @@ struct SeqBwdSmem {
     static constexpr int CT = SEQ_CT, NW = (KP / SEQ_KR) * VP / 64;
     float q[CT][KP], k[CT][KP], a[CT][KP], e[CT][KP];
     float v[CT][VP], w[CT][VP], dy[CT][VP], d[CT][VP];
-    float val[CT], rst[CT], sa[CT], kk[CT], dd[CT];
+    float val[CT], rst[CT], aclr[CT], sa[CT], kk[CT], dd[CT];
     float red[2][NW][4][KP];
 };
 
@@ -222,7 +234,7 @@ __global__ void __launch_bounds__((KP / SEQ_KR) * VP) seq_bwd_kernel(SeqArgs a) 
     for (int blk = a.nck - 1; blk >= 0; --blk) {
         const int t0 = blk * CT, nt = min(CT, a.T - t0);
         stage_tokens<KP, VP, NT, TIN>(a, b, h, t0, s.q, s.k, s.a, s.e, s.v, s.w, s.val, s.rst,
-                                      tid);
+                                      s.aclr, tid);
         for (int idx = tid; idx < CT * VP; idx += NT) {
             const int tt = idx / VP, c = idx % VP, t = t0 + tt;
             s.dy[tt][c] = (a.dout.data && t < a.T && c < a.V) ? ld4<TIN>(a.dout, b, t, h, c) : 0.f;
@@ -297,6 +309,10 @@ __global__ void __launch_bounds__((KP / SEQ_KR) * VP) seq_bwd_kernel(SeqArgs a) 
             const float nk = s.kk[tt], nd = s.dd[tt], sadj = s.sa[tt];
             float dd = 0.f;
             if (nk > 0.f && nd > 0.f) dd = sadj * nk * delta / nd;  // score VJP, zero subgradient
+            if (s.aclr[tt] != 0.f) {  // doc limits: a document ends here
+#pragma unroll
+                for (int r = 0; r < KR; ++r) adj[r] = 0.f;
+            }
             float part = 0.f;
 #pragma unroll
             for (int r = 0; r < KR; ++r) {
@@ -314,7 +330,7 @@ __global__ void __launch_bounds__((KP / SEQ_KR) * VP) seq_bwd_kernel(SeqArgs a) 
                 ge[r] = -kr * bar * dd;
                 const float dbar = adj[r] - er * kr * dd;
                 ga[r] = dbar * prev[r];
-                adj[r] = rst ? 0.f : ar * dbar;
+                adj[r] = (rst && !a.doc) ? 0.f : ar * dbar;
             }
             // Sum over the value columns held by this wave (lanes sharing ig).
 #pragma unroll

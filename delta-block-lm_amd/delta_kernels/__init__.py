@@ -18,9 +18,10 @@ from typing import NamedTuple, Optional
 
 import torch
 
-from ._lib import GDN2_BF16, GDN2_F32, Gdn2Shape, Gdn2View, check, lib
+from ._lib import GDN2_BF16, GDN2_F32, GDN2_I32, Gdn2Shape, Gdn2View, check, lib
 
-__all__ = ["GdnTrainingOutput", "gdn_training_scan", "gdn_training_backward",
+__all__ = ["GdnTrainingOutput", "gdn_training_scan", "gdn_training_backward", "gdn2_scan",
+           "gdn2_scan_forward", "gdn2_backward",
            "gdn_scalar_scan", "gdn_scalar_forward", "gdn_scalar_backward", "gdn_decode_step",
            "stage_timing", "stage_times", "lib"]
 
@@ -37,6 +38,8 @@ def _code(t: torch.Tensor) -> int:
         return GDN2_F32
     if t.dtype == torch.bfloat16:
         return GDN2_BF16
+    if t.dtype == torch.int32:
+        return GDN2_I32
     raise TypeError(f"GDN-2 tensors must be float32 or bfloat16, got {t.dtype}")
 
 
@@ -194,6 +197,95 @@ def gdn_training_scan(q, k, v, alpha, erase, write, valid, reset, initial=None,
         initial = initial.float()
     out, final, scores = _TrainingScan.apply(q, k, v, *gates, valid, reset, initial, chunk_size)
     return GdnTrainingOutput(out, final, scores)
+
+
+# ---- document-limit scan ----------------------------------------------------------
+
+
+def _doc_limits(doc_start, doc_end, B, T, device):
+    for name, t in (("doc_start", doc_start), ("doc_end", doc_end)):
+        if t.dtype != torch.int32 or tuple(t.shape) != (B, T) or t.device != device:
+            raise ValueError(f"{name} must be an int32 [batch, time] tensor on the inputs' device")
+
+
+def gdn2_scan_forward(q, k, v, alpha, erase, write, doc_start, doc_end):
+    """Raw forward of the document-limit scan (crates/kernels/src/ops.rs:19-31):
+    returns (output, checkpoint)."""
+    L = lib()
+    shape = _shape(q, v)
+    B, T, H, K = q.shape
+    V = v.shape[3]
+    out = torch.empty((B, T, H, V), dtype=q.dtype, device=q.device)
+    nck = L.gdn2_scan_checkpoint_bytes(ctypes.byref(shape))
+    if nck == 0:
+        check("gdn2_scan_checkpoint_bytes", 1)
+    ck = torch.empty((nck,), dtype=torch.uint8, device=q.device)
+    views = [_view(x) for x in (q, k, v, alpha, erase, write, doc_start, doc_end)]
+    with torch.cuda.device(q.device):
+        rc = L.gdn2_scan(ctypes.byref(shape), *[ctypes.byref(x) for x in views], _ptr(out),
+                         _code(out), _ptr(ck), nck, _stream(q))
+    check("gdn2_scan", rc)
+    return out, ck
+
+
+def gdn2_backward(q, k, v, alpha, erase, write, d_output, checkpoint, doc_start, doc_end):
+    """Raw VJP of the document-limit scan (crates/kernels/src/ops.rs:33-55):
+    returns (dq, dk, dv, dalpha, derase, dwrite)."""
+    L = lib()
+    shape = _shape(q, v)
+    B, T, H, K = q.shape
+    V = v.shape[3]
+    dev = q.device
+    dq = torch.empty((B, T, H, K), dtype=q.dtype, device=dev)
+    dk = torch.empty((B, T, H, K), dtype=q.dtype, device=dev)
+    dv = torch.empty((B, T, H, V), dtype=q.dtype, device=dev)
+    da = torch.empty((B, T, H, K), dtype=torch.float32, device=dev)
+    de = torch.empty((B, T, H, K), dtype=torch.float32, device=dev)
+    dw = torch.empty((B, T, H, V), dtype=torch.float32, device=dev)
+    nws = L.gdn2_scan_workspace_bytes(ctypes.byref(shape))
+    ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=dev)
+    if d_output is not None and d_output.dtype != q.dtype:
+        d_output = d_output.to(q.dtype)
+    views = [_view(x) for x in (q, k, v, alpha, erase, write, doc_start, doc_end)]
+    dov = _view(d_output)
+    with torch.cuda.device(dev):
+        rc = L.gdn2_backward(ctypes.byref(shape), *[ctypes.byref(x) for x in views],
+                             _ptr(checkpoint), checkpoint.numel(),
+                             ctypes.byref(dov) if d_output is not None else None, _ptr(dq),
+                             _ptr(dk), _ptr(dv), _ptr(da), _ptr(de), _ptr(dw), _ptr(ws), nws,
+                             _stream(q))
+    check("gdn2_backward", rc)
+    return dq, dk, dv, da, de, dw
+
+
+class _DocScan(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, alpha, erase, write, doc_start, doc_end):
+        out, ck = gdn2_scan_forward(q, k, v, alpha, erase, write, doc_start, doc_end)
+        ctx.save_for_backward(q, k, v, alpha, erase, write, doc_start, doc_end)
+        ctx.checkpoint = ck
+        return out
+
+    @staticmethod
+    def backward(ctx, d_out):
+        q, k, v, alpha, erase, write, doc_start, doc_end = ctx.saved_tensors
+        grads = gdn2_backward(q, k, v, alpha, erase, write, d_out, ctx.checkpoint, doc_start,
+                              doc_end)
+        return grads + (None, None)
+
+
+def gdn2_scan(q, k, v, alpha, erase, write, doc_start, doc_end):
+    """Document-limit GDN-2 scan (crates/kernels/src/ops.rs:254-276): output
+    [B,T,H,V] in q's dtype, differentiable in q, k, v, alpha, erase, write.
+    doc_start/doc_end: int32 [B,T] inclusive limits; end < start marks padding
+    and start == t resets the state.  The gates are taken in float32, as the
+    reference casts them (ops.rs:264-267)."""
+    B, T = q.shape[:2]
+    _check_shapes(q, k, v, [("alpha", alpha, q.shape[3]), ("erase", erase, q.shape[3]),
+                            ("write", write, v.shape[3])], doc_start, doc_end, None)
+    _doc_limits(doc_start, doc_end, B, T, q.device)
+    gates = [g if g.dtype == torch.float32 else g.float() for g in (alpha, erase, write)]
+    return _DocScan.apply(q, k, v, *gates, doc_start, doc_end)
 
 
 # ---- scalar-gate gated delta rule -------------------------------------------------

@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(_PKG, "lib", "libgdn2_amd.so")
 
 GDN2_F32 = 0
 GDN2_BF16 = 1
+GDN2_I32 = 2
 
 STATUS = {0: "OK", 1: "ARGUMENT", 2: "SHAPE", 3: "DTYPE", 4: "WORKSPACE", 5: "LAUNCH"}
 
@@ -63,6 +64,10 @@ SIGNATURES = {
     "gdn2_training_scan": (_I, [_S, _I] + [_V] * 9 + [_P, ctypes.c_int32, _F, _F, _P, _Z, _P]),
     "gdn2_training_backward": (_I, [_S, _I] + [_V] * 8 + [_P, _Z, _V, _F, _F] + [_P] * 3
                                + [_F] * 4 + [_P, _Z, _P]),
+    "gdn2_scan_checkpoint_bytes": (_Z, [_S]),
+    "gdn2_scan_workspace_bytes": (_Z, [_S]),
+    "gdn2_scan": (_I, [_S] + [_V] * 8 + [_P, ctypes.c_int32, _P, _Z, _P]),
+    "gdn2_backward": (_I, [_S] + [_V] * 8 + [_P, _Z, _V] + [_P] * 3 + [_F] * 3 + [_P, _Z, _P]),
     "gdn_scalar_checkpoint_bytes": (_Z, [_S, _I]),
     "gdn_scalar_workspace_bytes": (_Z, [_S, _I]),
     "gdn_scalar_scan": (_I, [_S, _I] + [_V] * 8 + [_P, ctypes.c_int32, _F, _F, _P, _Z, _P]),

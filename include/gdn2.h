@@ -41,7 +41,7 @@ extern "C" {
 #define GDN2_API
 #endif
 
-enum gdn2_dtype { GDN2_F32 = 0, GDN2_BF16 = 1 };
+enum gdn2_dtype { GDN2_F32 = 0, GDN2_BF16 = 1, GDN2_I32 = 2 /* document limits only */ };
 
 enum gdn2_status {
     GDN2_OK = 0,
@@ -116,6 +116,41 @@ GDN2_API int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gd
                            const float *d_scores, void *dq, void *dk, void *dv,
                            float *dalpha, float *derase, float *dwrite, float *d_initial,
                            void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- Document-limit GDN-2 scan -------------------------------------------- */
+/* Replaces Gdn2Ops::gdn2_scan / gdn2_backward (reference
+ * crates/kernels/src/ops.rs:17-276, CubeCL launches crates/kernels/src/gdn2.rs);
+ * semantics of the f64 oracle crates/mixers/src/gdn2_reference.rs:84-226.
+ * Packed documents are described per token by inclusive int32 limits
+ * doc_start[b,t], doc_end[b,t] (I32 views, strides [batch, time]):
+ *   end < start      padding: zero output, state kept
+ *   start == t       the state is zeroed before the token's update
+ * The backward is the reference's doc-limit VJP: the state adjoint is cleared
+ * at tokens with end == t (before that token's output gradient is added) and
+ * passes unchanged through padding.  For documents whose tokens all carry the
+ * same (start, end) this is the exact gradient.  Zero initial state; no final
+ * state or score outputs.  q, k, v: F32 or BF16 (same dtype); alpha, erase,
+ * write: F32.  The checkpoint (opaque) replaces the reference's
+ * [B, H, T/16, 48, 64] checkpoint tensor. */
+GDN2_API size_t gdn2_scan_checkpoint_bytes(const gdn2_shape *shape);
+
+GDN2_API int gdn2_scan(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k,
+                       const gdn2_view *v, const gdn2_view *alpha, const gdn2_view *erase,
+                       const gdn2_view *write, const gdn2_view *doc_start,
+                       const gdn2_view *doc_end, void *output, int32_t output_dtype,
+                       void *checkpoint, size_t checkpoint_bytes, void *stream);
+
+GDN2_API size_t gdn2_scan_workspace_bytes(const gdn2_shape *shape);
+
+/* d_output: [B,T,H,V] in q's dtype (strided).  Gradients dense: dq, dk, dv in
+ * q's dtype, dalpha, derase, dwrite F32; any may be NULL (not wanted). */
+GDN2_API int gdn2_backward(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k,
+                           const gdn2_view *v, const gdn2_view *alpha, const gdn2_view *erase,
+                           const gdn2_view *write, const gdn2_view *doc_start,
+                           const gdn2_view *doc_end, const void *checkpoint,
+                           size_t checkpoint_bytes, const gdn2_view *d_output, void *dq, void *dk,
+                           void *dv, float *dalpha, float *derase, float *dwrite, void *workspace,
+                           size_t workspace_bytes, void *stream);
 
 /* ---- Scalar-gate gated delta rule (chunked, MFMA) ------------------------ */
 /* The scalar special case of the same recurrence: alpha[i] = exp(g),
