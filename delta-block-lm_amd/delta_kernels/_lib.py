@@ -49,6 +49,12 @@ class Gdn2AdamwTensor(ctypes.Structure):
                 ("second", ctypes.c_void_p), ("numel", ctypes.c_int64)]
 
 
+class Gdn2HolaShape(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_int64), ("time", ctypes.c_int64), ("heads", ctypes.c_int64),
+                ("keys", ctypes.c_int64), ("values", ctypes.c_int64),
+                ("capacity", ctypes.c_int32), ("chunk", ctypes.c_int32)]
+
+
 # Exported symbols and their signatures: (name, restype, argtypes).
 _P = ctypes.c_void_p
 _V = ctypes.POINTER(Gdn2View)
@@ -97,6 +103,12 @@ SIGNATURES = {
     "gdn2_adamw_update": (_I, [ctypes.c_int32, ctypes.POINTER(Gdn2AdamwTensor), _I,
                                ctypes.c_int64, ctypes.c_double, ctypes.c_float, ctypes.c_float,
                                _I, _P, _Z, _P]),
+    "gdn2_hola_schedule": (_I, [ctypes.POINTER(Gdn2HolaShape), _I] + [_V] * 3 + [_F, _P]),
+    "gdn2_hola_checkpoint_bytes": (_Z, [ctypes.POINTER(Gdn2HolaShape)]),
+    "gdn2_hola_read": (_I, [ctypes.POINTER(Gdn2HolaShape), _I] + [_V] * 7 + [_F, _F, _P, _Z, _P]),
+    "gdn2_hola_workspace_bytes": (_Z, [ctypes.POINTER(Gdn2HolaShape)]),
+    "gdn2_hola_backward": (_I, [ctypes.POINTER(Gdn2HolaShape)] + [_V] * 6 + [_P, _Z, _F, _V]
+                           + [_F] * 4 + [_P, _Z, _P]),
     "gdn2_stage_timing": (_I, [_I]),
     "gdn2_stage_count": (_I, []),
     "gdn2_stage_name": (ctypes.c_char_p, [_I]),

@@ -323,6 +323,57 @@ GDN2_API int gdn2_adamw_update(int32_t count, const gdn2_adamw_tensor *tensors, 
                                int reuse_table, void *workspace, size_t workspace_bytes,
                                void *stream);
 
+/* ---- HOLA exact-memory cache read (the consumer of the scan's scores) ------- */
+/* Replaces HolaOps::hola_schedule / hola_read / hola_backward (reference
+ * crates/kernels/src/hola_ops.rs:17-425, kernels crates/kernels/src/hola.rs;
+ * semantics of the scalar oracle crates/mixers/src/hola_checks.rs:294-391).
+ * Per (batch, head), chunks of `chunk` tokens in order:
+ *   * every valid query t attends with softmax, scale 1/sqrt(keys), to the
+ *     cache kept before its chunk plus tokens first..t of its chunk, restricted
+ *     to valid tokens of its own document, next to a learned sink logit
+ *     sink[h] whose value is zero; invalid queries output zero;
+ *   * after the chunk the cache keeps, of cache + chunk, the valid tokens whose
+ *     document equals that of the chunk's last physical slot (padding
+ *     included), the `capacity` highest by score (recency: by position),
+ *     ties to the earlier position.
+ * Scores choose membership only: they take no gradient.  q, k: [B,T,H,keys],
+ * v: [B,T,H,values], scores [B,T,H] (stride[3] unused), valid and documents
+ * [B,T], sink [H] (stride[0]); all F32 views.  keys, values 1..128, capacity
+ * 1..64, chunk 1..16 (the reference's chunk limit). */
+typedef struct gdn2_hola_shape {
+    int64_t batch, time, heads, keys, values;
+    int32_t capacity, chunk;
+} gdn2_hola_shape;
+
+/* Positions only (hola_ops.rs:358-385): schedule [B, H, ceil(T/chunk) + 1,
+ * capacity] F32, the cache before the first chunk and after each chunk, -1 for
+ * an empty slot. */
+GDN2_API int gdn2_hola_schedule(const gdn2_hola_shape *shape, int recency,
+                                const gdn2_view *scores, const gdn2_view *valid,
+                                const gdn2_view *documents, float *schedule, void *stream);
+
+/* Read (hola_ops.rs:387-425): output [B,T,H,values] F32 dense, and optionally
+ * the final cache positions [B,H,capacity].  The checkpoint (opaque, sized by
+ * gdn2_hola_checkpoint_bytes) keeps the schedule, per-key visibility ends and
+ * the softmax statistics for the backward. */
+GDN2_API size_t gdn2_hola_checkpoint_bytes(const gdn2_hola_shape *shape);
+GDN2_API int gdn2_hola_read(const gdn2_hola_shape *shape, int recency, const gdn2_view *q,
+                            const gdn2_view *k, const gdn2_view *v, const gdn2_view *scores,
+                            const gdn2_view *valid, const gdn2_view *documents,
+                            const gdn2_view *sink, float *output, float *final_positions,
+                            void *checkpoint, size_t checkpoint_bytes, void *stream);
+
+/* VJP of sum(output * d_output) in q, k, v (dense [B,T,H,*] F32) and sink
+ * [H]; `output` is the read's own output.  d_output may be NULL (zero). */
+GDN2_API size_t gdn2_hola_workspace_bytes(const gdn2_hola_shape *shape);
+GDN2_API int gdn2_hola_backward(const gdn2_hola_shape *shape, const gdn2_view *q,
+                                const gdn2_view *k, const gdn2_view *v, const gdn2_view *valid,
+                                const gdn2_view *documents, const gdn2_view *sink,
+                                const void *checkpoint, size_t checkpoint_bytes,
+                                const float *output, const gdn2_view *d_output, float *dq,
+                                float *dk, float *dv, float *dsink, void *workspace,
+                                size_t workspace_bytes, void *stream);
+
 /* Measurement hook.  No counterpart in the reference: it serves benchmarks
  * that need the duration of each kernel of the chunk-WY path, measured on the
  * stream the kernels run on.  After gdn2_stage_timing(1), every chunk-path
