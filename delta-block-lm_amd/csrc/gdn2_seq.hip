@@ -22,11 +22,51 @@
 
 namespace gdn2 {
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+    return x + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                             0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the NG adjacent lanes of a key group (NG = 2, 4 or 8), in all of
+// them: DPP quad swaps, then the half-row mirror pairs the two quads.
 template <int NG>
 __device__ __forceinline__ float group_sum(float x) {
-#pragma unroll
-    for (int m = 1; m < NG; m <<= 1) x += __shfl_xor(x, m);
+    x = dpp_add<0xB1>(x);                  // lane ^ 1
+    if (NG >= 4) x = dpp_add<0x4E>(x);     // lane ^ 2
+    if (NG >= 8) x = dpp_add<0x141>(x);    // quad <-> quad within 8 lanes
     return x;
+}
+
+// x[l] + x[l ^ 16] and x[l] + x[l ^ 32] in every lane: a permlane swap of x
+// with itself returns both halves of each pair.  Each result element is
+// copied into a plain int before the bit cast: bit-casting an element of the
+// returned vector directly reads element 0.
+__device__ __forceinline__ float pair_sum(int a, int b) {
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float swap16_sum(float x) {
+    const int i = __builtin_bit_cast(int, x);
+    const auto r = __builtin_amdgcn_permlane16_swap(i, i, false, false);
+    const int r0 = r[0], r1 = r[1];
+    return pair_sum(r0, r1);
+}
+__device__ __forceinline__ float swap32_sum(float x) {
+    const int i = __builtin_bit_cast(int, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(i, i, false, false);
+    const int r0 = r[0], r1 = r[1];
+    return pair_sum(r0, r1);
+}
+
+// Sum over the lanes of a wave that share a key group (lane % NG), in all of
+// them: row rotations by multiples of NG sum the same-group lanes of each
+// 16-lane row, then the four rows are combined with permlane swaps.
+template <int NG>
+__device__ __forceinline__ float column_sum(float x) {
+    if (NG <= 2) x = dpp_add<0x122>(x);   // row_ror 2
+    if (NG <= 4) x = dpp_add<0x124>(x);   // row_ror 4
+    x = dpp_add<0x128>(x);                // row_ror 8
+    return swap32_sum(swap16_sum(x));
 }
 
 template <int KP, int VP>
@@ -334,14 +374,11 @@ __global__ void __launch_bounds__((KP / SEQ_KR) * VP) seq_bwd_kernel(SeqArgs a) 
             }
             // Sum over the value columns held by this wave (lanes sharing ig).
 #pragma unroll
-            for (int m = NG; m < 64; m <<= 1) {
-#pragma unroll
-                for (int r = 0; r < KR; ++r) {
-                    gq[r] += __shfl_xor(gq[r], m);
-                    gk[r] += __shfl_xor(gk[r], m);
-                    ge[r] += __shfl_xor(ge[r], m);
-                    ga[r] += __shfl_xor(ga[r], m);
-                }
+            for (int r = 0; r < KR; ++r) {
+                gq[r] = column_sum<NG>(gq[r]);
+                gk[r] = column_sum<NG>(gk[r]);
+                ge[r] = column_sum<NG>(ge[r]);
+                ga[r] = column_sum<NG>(ga[r]);
             }
             if (lane < NG) {
 #pragma unroll
