@@ -102,12 +102,12 @@ int check_out_dtype(int32_t dt) {
 }
 
 size_t seq_checkpoint_bytes(const gdn2_shape *s) {
-    const int64_t nck = (s->time + SEQ_CT - 1) / SEQ_CT;
-    return (size_t)(s->batch * s->heads) * nck * seq_state_floats((int)s->keys, (int)s->values) * 4;
+    return (size_t)seq_checkpoint_floats(s->batch, s->time, s->heads, (int)s->keys,
+                                         (int)s->values) * 4;
 }
 
 size_t seq_workspace_bytes(const gdn2_shape *s) {
-    return (size_t)(s->batch * s->heads) * SEQ_CT * seq_state_floats((int)s->keys, (int)s->values) * 4;
+    return (size_t)seq_workspace_floats(s->batch, s->heads, (int)s->keys, (int)s->values) * 4;
 }
 
 int check_channel_inputs(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k,
@@ -200,7 +200,7 @@ int gdn2_training_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q,
     a.out_bf16 = output_dtype == GDN2_BF16;
     a.final_state = final_state;
     a.scores = scores;
-    a.ck = (float *)checkpoint;
+    seq_bind_checkpoint(a, checkpoint);
     return launch_status(launch_seq_fwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
                          "gdn2_training_scan");
 }
@@ -227,7 +227,7 @@ int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gdn2_view *
         return fail(GDN2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
                     seq_workspace_bytes(shape), workspace_bytes);
     SeqArgs a = seq_args(shape, q, k, v, alpha, erase, write, valid, reset);
-    a.ck = (float *)checkpoint;
+    seq_bind_checkpoint(a, checkpoint);
     if (d_output) a.dout = make_view(d_output);
     a.dfinal = d_final_state;
     a.dscores = d_scores;
@@ -271,7 +271,7 @@ int gdn2_scan(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k, c
     a.doc_end = make_view(doc_end);
     a.out = output;
     a.out_bf16 = output_dtype == GDN2_BF16;
-    a.ck = (float *)checkpoint;
+    seq_bind_checkpoint(a, checkpoint);
     return launch_status(launch_seq_fwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
                          "gdn2_scan");
 }
@@ -297,7 +297,7 @@ int gdn2_backward(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *
     a.doc = 1;
     a.doc_start = make_view(doc_start);
     a.doc_end = make_view(doc_end);
-    a.ck = (float *)checkpoint;
+    seq_bind_checkpoint(a, checkpoint);
     if (d_output) a.dout = make_view(d_output);
     a.dq = dq;
     a.dk = dk;
@@ -412,7 +412,7 @@ int gdn_scalar_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q, cons
     a.out_bf16 = output_dtype == GDN2_BF16;
     a.final_state = final_state;
     a.scores = scores;
-    a.ck = (float *)checkpoint;
+    seq_bind_checkpoint(a, checkpoint);
     return launch_status(launch_seq_fwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
                          "gdn_scalar_scan");
 }
@@ -464,7 +464,7 @@ int gdn_scalar_backward(const gdn2_shape *shape, int chunk, const gdn2_view *q,
     a.scalar = 1;
     a.beta = make_view(beta);
     a.g = make_view(g);
-    a.ck = (float *)checkpoint;
+    seq_bind_checkpoint(a, checkpoint);
     if (d_output) a.dout = make_view(d_output);
     a.dfinal = d_final_state;
     a.dscores = d_scores;
@@ -538,7 +538,7 @@ int gdn2_decode_step(const gdn2_shape *shape, const gdn2_view *q, const gdn2_vie
     a.out = output;
     a.out_bf16 = output_dtype == GDN2_BF16;
     a.scores = scores;
-    a.ck = nullptr;
+    seq_bind_checkpoint(a, nullptr);
     return launch_status(launch_seq_fwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
                          "gdn2_decode_step");
 }

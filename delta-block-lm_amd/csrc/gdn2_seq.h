@@ -6,7 +6,6 @@
 namespace gdn2 {
 
 constexpr int SEQ_CT = 16;  // tokens per staging block == checkpoint interval
-constexpr int SEQ_KR = 16;  // state rows held by one thread
 
 struct SeqArgs {
     int B, T, H, K, V;
@@ -26,20 +25,43 @@ struct SeqArgs {
     void *out;
     int out_bf16;
     float *final_state, *scores;
-    float *ck;  // checkpoints [B*H][nck][KR][NT]; null = not written (decode)
+    // Checkpoint (null = not written, decode), carved by seq_bind_checkpoint:
+    //   ck       [B*H][nck][K_pad][V_pad]  state at the start of every block
+    //   ck_delta [B*H][nck*SEQ_CT][V_pad]  the edit delta of every token
+    //   ck_norm  [B*H][nck*SEQ_CT][2]      |k| and |delta| of every token
+    float *ck, *ck_delta, *ck_norm;
     int nck;
     // backward
     View dout;
     const float *dfinal, *dscores;
     void *dq, *dk, *dv;
     float *dalpha, *derase, *dwrite, *dinitial;
-    float *replay;  // [B*H][SEQ_CT][KR][NT]
+    float *replay;  // [B*H][SEQ_CT][K_pad * V_pad], thread-major
 };
 
 // Padded widths used by the kernels: 32, 64 or 128.
 inline int seq_pad(int n) { return n <= 32 ? 32 : (n <= 64 ? 64 : 128); }
-inline int64_t seq_threads(int K, int V) { return (int64_t)(seq_pad(K) / SEQ_KR) * seq_pad(V); }
 inline int64_t seq_state_floats(int K, int V) { return (int64_t)seq_pad(K) * seq_pad(V); }
+
+inline int64_t seq_checkpoint_floats(int64_t B, int64_t T, int64_t H, int K, int V) {
+    const int64_t nck = (T + SEQ_CT - 1) / SEQ_CT, tp = nck * SEQ_CT;
+    return B * H * (nck * seq_state_floats(K, V) + tp * seq_pad(V) + tp * 2);
+}
+
+inline int64_t seq_workspace_floats(int64_t B, int64_t H, int K, int V) {
+    return B * H * SEQ_CT * seq_state_floats(K, V);
+}
+
+inline void seq_bind_checkpoint(SeqArgs &a, const void *ck) {
+    a.ck = static_cast<float *>(const_cast<void *>(ck));
+    if (!ck) {
+        a.ck_delta = a.ck_norm = nullptr;
+        return;
+    }
+    const int64_t bh = (int64_t)a.B * a.H, tp = (int64_t)a.nck * SEQ_CT;
+    a.ck_delta = a.ck + bh * a.nck * seq_state_floats(a.K, a.V);
+    a.ck_norm = a.ck_delta + bh * tp * seq_pad(a.V);
+}
 
 hipError_t launch_seq_fwd(const SeqArgs &a, bool in_bf16, hipStream_t stream);
 hipError_t launch_seq_bwd(const SeqArgs &a, bool in_bf16, hipStream_t stream);

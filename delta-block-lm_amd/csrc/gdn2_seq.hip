@@ -1,23 +1,37 @@
 // Token-sequential GDN-2 scan for gfx950: the general channel-wise surface.
 //
-// Semantics follow crates/mixers/src/reference.rs:41-257 (forward and VJP)
-// and the stateful fused kernels crates/kernels/src/gdn_training.rs:12-284.
+// Semantics follow crates/mixers/src/reference.rs:41-257 (forward and VJP),
+// the stateful fused kernels crates/kernels/src/gdn_training.rs:12-284 and,
+// with document limits, crates/mixers/src/gdn2_reference.rs:84-226.
 //
-// Work decomposition (one workgroup per (batch, head)):
-//   thread tid owns value column j = tid / NG and the KR = 16 key rows
-//   i0 = (tid % NG) * 16 .. i0 + 15 of the fp32 state, NG = KP / 16.  The NG
-//   threads of one column are adjacent lanes of one wavefront, so the two
-//   per-token reductions over keys (the edit delta and the output) are lane
-//   butterflies with no LDS round trip and no barrier.  Token inputs are
-//   staged through LDS 16 tokens at a time with coalesced strided loads;
-//   outputs are staged back and stored coalesced.
+// One workgroup per (batch, head).  Value columns evolve independently in the
+// recurrence, so each wave owns a block of value columns and walks the tokens
+// without workgroup barriers; only the per-key gradients of the backward are
+// summed across waves.
 //
-// Checkpoints: the forward stores the state every SEQ_CT tokens in a private
-// thread-major layout (one coalesced row per register).  The backward walks
-// blocks in reverse, replays a block from its checkpoint (storing the 16
-// pre-token states in a scratch buffer) and then runs the token VJP in
-// reverse.  Per-key gradients are reduced over value columns with a wave
-// butterfly, then across waves through a double-buffered LDS slab.
+// Forward: thread tid owns value column j = tid / NG and the KR = 16 key rows
+//   i0 = (tid % NG) * 16 .. i0 + 15 of the fp32 state (NG = K_pad / 16
+//   adjacent lanes per column), so the two per-token key reductions (the edit
+//   delta and the output) are DPP butterflies over NG lanes.
+// Backward: lane l of wave w owns key rows RL*(l/4) .. +RL-1 (RL = K_pad/16)
+//   and value columns 16w + 4(l%4) .. +3.  The edit adjoint (a sum over keys)
+//   is four local terms per column plus a sum over the 16 lanes of one column
+//   quad position; the per-key gradients (sums over value columns) are four
+//   local terms plus a quad butterfly.  Each wave leaves its per-key partials
+//   of FT tokens in LDS, and the workgroup sums them over waves and stores
+//   dq/dk/dalpha/derase once per FT tokens.
+//
+// Token inputs are staged through LDS SEQ_CT tokens at a time.  The next
+// block's global loads are issued before the current block's token loop and
+// written to LDS after it, so their latency hides behind the loop.
+//
+// Checkpoints: the forward stores the state at the start of every block
+// (row-major fp32), the edit delta of every token and the norms |k|, |delta|.
+// The backward walks blocks in reverse and replays a block from its
+// checkpoint with the forward's own deltas (the same rounded operations, so
+// the replayed states are the forward's), keeping the pre-token states in a
+// thread-major scratch area that the reverse token loop reads one token
+// ahead.
 #include "gdn2_seq.h"
 
 namespace gdn2 {
@@ -36,6 +50,11 @@ __device__ __forceinline__ float group_sum(float x) {
     if (NG >= 4) x = dpp_add<0x4E>(x);     // lane ^ 2
     if (NG >= 8) x = dpp_add<0x141>(x);    // quad <-> quad within 8 lanes
     return x;
+}
+
+// Sum over the 16 lanes of a DPP row, in all of them.
+__device__ __forceinline__ float row16_sum(float x) {
+    return dpp_add<0x140>(group_sum<8>(x));  // row mirror pairs the two halves
 }
 
 // x[l] + x[l ^ 16] and x[l] + x[l ^ 32] in every lane: a permlane swap of x
@@ -58,23 +77,235 @@ __device__ __forceinline__ float swap32_sum(float x) {
     return pair_sum(r0, r1);
 }
 
-// Sum over the lanes of a wave that share a key group (lane % NG), in all of
-// them: row rotations by multiples of NG sum the same-group lanes of each
-// 16-lane row, then the four rows are combined with permlane swaps.
-template <int NG>
-__device__ __forceinline__ float column_sum(float x) {
-    if (NG <= 2) x = dpp_add<0x122>(x);   // row_ror 2
-    if (NG <= 4) x = dpp_add<0x124>(x);   // row_ror 4
-    x = dpp_add<0x128>(x);                // row_ror 8
+// Sum over the lanes of a wave congruent to this lane modulo S (S = 4 or 8),
+// in all of them: row rotations by 4 (S = 4) and 8 within each 16-lane row,
+// then the four rows combined with permlane swaps.
+template <int S>
+__device__ __forceinline__ float stride_sum(float x) {
+    static_assert(S == 4 || S == 8, "stride");
+    if (S == 4) x = dpp_add<0x124>(x);  // row_ror 4
+    x = dpp_add<0x128>(x);              // row_ror 8
     return swap32_sum(swap16_sum(x));
 }
 
+template <int N>
+__device__ __forceinline__ void lds_get(const float *p, float (&x)[N]) {
+    static_assert(N % 2 == 0, "even runs");
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (int m = 0; m < N; m += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(p + m);
+            x[m] = v.x, x[m + 1] = v.y, x[m + 2] = v.z, x[m + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < N; m += 2) {
+            const float2 v = *reinterpret_cast<const float2 *>(p + m);
+            x[m] = v.x, x[m + 1] = v.y;
+        }
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void lds_put(float *p, const float (&x)[N]) {
+    static_assert(N % 2 == 0, "even runs");
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (int m = 0; m < N; m += 4)
+            *reinterpret_cast<float4 *>(p + m) = make_float4(x[m], x[m + 1], x[m + 2], x[m + 3]);
+    } else {
+#pragma unroll
+        for (int m = 0; m < N; m += 2)
+            *reinterpret_cast<float2 *>(p + m) = make_float2(x[m], x[m + 1]);
+    }
+}
+
+template <typename TIN>
+__device__ __forceinline__ void store_in(void *p, int64_t i, float x) {
+    Elem<TIN>::store(p, i, x);
+}
+
+// One thread's share of a block of SEQ_CT tokens, held in registers between
+// the global loads and the LDS stores.  Element n of an array is flat index
+// tid + n * NT of the block's [SEQ_CT][width] tile.  The registers hold the
+// raw loaded bits (bf16 inputs zero-extended): every conversion, exponential
+// and flag test happens at the LDS store, so nothing waits for the loads
+// until then.
+template <int KP, int VP, int NT, bool BWD>
+struct TokenRegs {
+    static constexpr int NK = SEQ_CT * KP / NT, NV = SEQ_CT * VP / NT;
+    static_assert(NK * NT == SEQ_CT * KP && NV * NT == SEQ_CT * VP, "block split");
+    uint32_t q[NK], k[NK], a[NK], e[NK];
+    uint32_t v[NV], w[NV];
+    uint32_t dy[BWD ? NV : 1], d[BWD ? NV : 1];
+    // Per-token words (threads tid < SEQ_CT): doc limits (start, end) or the
+    // valid/reset masks; dscores and the forward's |k|, |delta|.
+    uint32_t f0, f1, sa, nk, nd;
+    bool in;
+};
+
+template <typename T>
+__device__ __forceinline__ float raw_f(uint32_t r) {
+    if constexpr (sizeof(T) == 2) return __uint_as_float(r << 16);
+    else return __uint_as_float(r);
+}
+
+constexpr uint32_t NEG_INF_BITS = 0xff800000u;
+constexpr uint32_t ONE_BITS = 0x3f800000u;
+
+// One input of a (batch, head): element (t, c) at p[t * st + c * sc] (sc = 0
+// broadcasts a per-token value over the channels).  Built once per
+// workgroup, so the block loads carry two strides per input instead of the
+// whole view.
+struct Stream {
+    const char *p;
+    int64_t st, sc;
+};
+
+__device__ __forceinline__ Stream make_stream(const View &v, int b, int h, int esize,
+                                              bool broadcast = false) {
+    if (!v.data) return Stream{nullptr, 0, 0};
+    return Stream{static_cast<const char *>(v.data) + ((int64_t)b * v.s0 + (int64_t)h * v.s2) * esize,
+                  v.s1, broadcast ? 0 : v.s3};
+}
+
+// Token inputs of one (batch, head): q, k, the key gates a (alpha, or g in
+// scalar mode) and e (erase, or beta), v, the write gate w (write, or beta),
+// the output adjoint dy, and the per-token words f0/f1 (valid/reset masks,
+// or the document limits start/end).
+struct TokenSrc {
+    Stream q, k, a, e, v, w, dy, f0, f1;
+};
+
+template <typename TIN>
+__device__ __forceinline__ TokenSrc make_src(const SeqArgs &a, int b, int h) {
+    TokenSrc s;
+    s.q = make_stream(a.q, b, h, sizeof(TIN));
+    s.k = make_stream(a.k, b, h, sizeof(TIN));
+    s.a = a.scalar ? make_stream(a.g, b, h, 4, true) : make_stream(a.alpha, b, h, 4);
+    s.e = a.scalar ? make_stream(a.beta, b, h, 4, true) : make_stream(a.erase, b, h, 4);
+    s.v = make_stream(a.v, b, h, sizeof(TIN));
+    s.w = a.scalar ? make_stream(a.beta, b, h, 4, true) : make_stream(a.write, b, h, 4);
+    s.dy = make_stream(a.dout, b, h, sizeof(TIN));
+    const View &f0 = a.doc ? a.doc_start : a.valid, &f1 = a.doc ? a.doc_end : a.reset;
+    s.f0 = f0.data ? Stream{static_cast<const char *>(f0.data) + (int64_t)b * f0.s0 * 4, f0.s1, 0}
+                   : Stream{nullptr, 0, 0};
+    s.f1 = f1.data ? Stream{static_cast<const char *>(f1.data) + (int64_t)b * f1.s0 * 4, f1.s1, 0}
+                   : Stream{nullptr, 0, 0};
+    return s;
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t ld_s(const Stream &s, int64_t t, int64_t c) {
+    const int64_t i = t * s.st + c * s.sc;
+    if constexpr (sizeof(T) == 2) return reinterpret_cast<const uint16_t *>(s.p)[i];
+    else return reinterpret_cast<const uint32_t *>(s.p)[i];
+}
+
+// The per-workgroup scalars the block loads need besides the streams.
+struct BlockCtx {
+    int T, K, V, scalar, doc, H, b, h, bh;
+    int64_t tp;
+    const float *ck_delta, *ck_norm, *dscores;
+};
+
+__device__ __forceinline__ BlockCtx make_ctx(const SeqArgs &a, int b, int h, int bh) {
+    return BlockCtx{a.T, a.K, a.V, a.scalar, a.doc, a.H, b, h, bh, (int64_t)a.nck * SEQ_CT,
+                    a.ck_delta, a.ck_norm, a.dscores};
+}
+
+template <int KP, int VP, int NT, bool BWD, typename TIN>
+__device__ __forceinline__ void load_tokens(const TokenSrc &src, const BlockCtx &x, int t0, int tid,
+                                            TokenRegs<KP, VP, NT, BWD> &r) {
+    using R = TokenRegs<KP, VP, NT, BWD>;
+    // A thread's elements of a [SEQ_CT][width] tile share one channel and step
+    // through the tokens NT / width apart.
+    constexpr int KS = NT / KP, VS = NT / VP;
+    static_assert(KS * KP == NT && VS * VP == NT, "token-major split");
+    const int ck = tid % KP, tk = t0 + tid / KP, cv = tid % VP, tv = t0 + tid / VP;
+#pragma unroll
+    for (int n = 0; n < R::NK; ++n) {
+        const int t = tk + n * KS;
+        r.q[n] = r.k[n] = r.e[n] = 0u;
+        r.a[n] = x.scalar ? NEG_INF_BITS : 0u;  // exp(-inf) = 0 beyond the sequence
+        if (t < x.T && ck < x.K) {
+            r.q[n] = ld_s<TIN>(src.q, t, ck);
+            r.k[n] = ld_s<TIN>(src.k, t, ck);
+            r.a[n] = ld_s<float>(src.a, t, ck);
+            r.e[n] = ld_s<float>(src.e, t, ck);
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < R::NV; ++n) {
+        const int t = tv + n * VS;
+        r.v[n] = r.w[n] = 0u;
+        if constexpr (BWD) r.dy[n] = r.d[n] = 0u;
+        if (t < x.T && cv < x.V) {
+            r.v[n] = ld_s<TIN>(src.v, t, cv);
+            r.w[n] = ld_s<float>(src.w, t, cv);
+            if constexpr (BWD) {
+                if (src.dy.p) r.dy[n] = ld_s<TIN>(src.dy, t, cv);
+                r.d[n] = __float_as_uint(x.ck_delta[((int64_t)x.bh * x.tp + t) * VP + cv]);
+            }
+        }
+    }
+    const int t = t0 + tid;
+    r.in = tid < SEQ_CT && t < x.T;
+    r.f0 = x.doc ? 0u : ONE_BITS;
+    r.f1 = r.sa = r.nk = r.nd = 0u;
+    if (r.in) {
+        if (src.f0.p) r.f0 = ld_s<float>(src.f0, t, 0);
+        if (src.f1.p) r.f1 = ld_s<float>(src.f1, t, 0);
+        if constexpr (BWD) {
+            if (x.dscores) r.sa = __float_as_uint(x.dscores[((int64_t)x.b * x.T + t) * x.H + x.h]);
+            r.nk = __float_as_uint(x.ck_norm[((int64_t)x.bh * x.tp + t) * 2]);
+            r.nd = __float_as_uint(x.ck_norm[((int64_t)x.bh * x.tp + t) * 2 + 1]);
+        }
+    }
+}
+
+// Token flags (valid, reset, adjoint clear) from a thread's per-token words.
+template <int KP, int VP, int NT, bool BWD>
+__device__ __forceinline__ void token_flags(const SeqArgs &a, const TokenRegs<KP, VP, NT, BWD> &r,
+                                            int t, float &val, float &rst, float &clr) {
+    val = rst = clr = 0.f;
+    if (!r.in) return;
+    if (a.doc) {
+        const int32_t st = (int32_t)r.f0, en = (int32_t)r.f1;
+        val = en >= st ? 1.f : 0.f;
+        rst = st == t ? 1.f : 0.f;
+        clr = en == t ? 1.f : 0.f;
+    } else {
+        val = __uint_as_float(r.f0);
+        rst = __uint_as_float(r.f1);
+    }
+}
+
+// ---- forward ---------------------------------------------------------------------
+
+// Forward lane tile: RL key rows x CL value columns per lane, RGN row groups
+// and CLN column lanes per wave (16 value columns per wave).  Eight row groups
+// keep the per-token LDS reads of the key-side rows (a, e.k, k, q) at
+// 4 RL floats per lane while the key sums stay three lane steps deep.
+template <int KP>
+struct FwdLayout {
+    static constexpr int RGN = KP <= 64 ? 8 : 16;
+    static constexpr int RL = KP / RGN;
+    static constexpr int CLN = 64 / RGN;
+    static constexpr int CL = 16 / CLN;
+};
+
 template <int KP, int VP>
-struct SeqFwdSmem {
-    static constexpr int CT = SEQ_CT;
-    float q[CT][KP], k[CT][KP], a[CT][KP], e[CT][KP];
-    float v[CT][VP], w[CT][VP], o[CT][VP], d[CT][VP];
-    float val[CT], rst[CT];
+struct FwdTokens {
+    float q[SEQ_CT][KP], k[SEQ_CT][KP], a[SEQ_CT][KP], ek[SEQ_CT][KP];
+    float wv[SEQ_CT][VP];
+    float val[SEQ_CT], rst[SEQ_CT];
+};
+
+template <int KP, int VP>
+struct alignas(16) SeqFwdSmem {
+    FwdTokens<KP, VP> buf[2];
+    float o[SEQ_CT][VP], d[SEQ_CT][VP];
 };
 
 template <int KP, int VP>
@@ -83,65 +314,74 @@ union SeqFwdShared {
     float st[KP * (VP + 1)];  // state transpose slab (row stride VP+1)
 };
 
-// Stage SEQ_CT tokens starting at t0 into LDS as fp32 (zero beyond T/K/V).
+// Stage a block for the forward in two passes (a barrier between them): the
+// token flags, then the operands with padding and resets folded in, so the
+// token loop has no branches.  A padded token (or one beyond the sequence)
+// gets a = 1 and zero e.k, k, q and w.v: the state passes unchanged and its
+// edit and output are zero.  A reset token gets a = 0, which zeroes the
+// carried state before the edit.
 template <int KP, int VP, int NT, typename TIN>
-__device__ __forceinline__ void stage_tokens(const SeqArgs &a, int b, int h, int t0,
-                                             float (*sq)[KP], float (*sk)[KP],
-                                             float (*sa)[KP], float (*se)[KP],
-                                             float (*sv)[VP], float (*sw)[VP],
-                                             float *sval, float *srst, float *saclr, int tid) {
-    constexpr int CT = SEQ_CT;
-    for (int idx = tid; idx < CT * KP; idx += NT) {
-        const int tt = idx / KP, c = idx % KP, t = t0 + tt;
-        const bool in = t < a.T && c < a.K;
-        sq[tt][c] = in ? ld4<TIN>(a.q, b, t, h, c) : 0.f;
-        sk[tt][c] = in ? ld4<TIN>(a.k, b, t, h, c) : 0.f;
-        if (a.scalar) {
-            sa[tt][c] = in ? expf(ld4<float>(a.g, b, t, h, 0)) : 0.f;
-            se[tt][c] = in ? ld4<float>(a.beta, b, t, h, 0) : 0.f;
-        } else {
-            sa[tt][c] = in ? ld4<float>(a.alpha, b, t, h, c) : 0.f;
-            se[tt][c] = in ? ld4<float>(a.erase, b, t, h, c) : 0.f;
-        }
-    }
-    for (int idx = tid; idx < CT * VP; idx += NT) {
-        const int tt = idx / VP, c = idx % VP, t = t0 + tt;
-        const bool in = t < a.T && c < a.V;
-        sv[tt][c] = in ? ld4<TIN>(a.v, b, t, h, c) : 0.f;
-        sw[tt][c] = in ? (a.scalar ? ld4<float>(a.beta, b, t, h, 0) : ld4<float>(a.write, b, t, h, c))
-                       : 0.f;
-    }
-    if (tid < CT) {
-        const int t = t0 + tid;
-        float val = 0.f, rst = 0.f, clr = 0.f;
-        if (t < a.T) {
-            if (a.doc) {
-                const int32_t st = reinterpret_cast<const int32_t *>(
-                    a.doc_start.data)[b * a.doc_start.s0 + t * a.doc_start.s1];
-                const int32_t en = reinterpret_cast<const int32_t *>(
-                    a.doc_end.data)[b * a.doc_end.s0 + t * a.doc_end.s1];
-                val = en >= st ? 1.f : 0.f;
-                rst = st == t ? 1.f : 0.f;
-                clr = en == t ? 1.f : 0.f;
-            } else {
-                val = a.valid.data ? ld4<float>(a.valid, b, t, 0, 0) : 1.f;
-                rst = a.reset.data ? ld4<float>(a.reset, b, t, 0, 0) : 0.f;
-            }
-        }
-        sval[tid] = val;
-        srst[tid] = rst;
-        if (saclr) saclr[tid] = clr;
+__device__ __forceinline__ void store_fwd_flags(const SeqArgs &a,
+                                                const TokenRegs<KP, VP, NT, false> &r,
+                                                FwdTokens<KP, VP> &s, int t0, int tid) {
+    if (tid < SEQ_CT) {
+        float val, rst, clr;
+        token_flags(a, r, t0 + tid, val, rst, clr);
+        s.val[tid] = val;
+        s.rst[tid] = rst;
     }
 }
 
+template <int KP, int VP, int NT, typename TIN>
+__device__ __forceinline__ void store_fwd_data(const SeqArgs &a,
+                                               const TokenRegs<KP, VP, NT, false> &r,
+                                               FwdTokens<KP, VP> &s, int tid) {
+    using R = TokenRegs<KP, VP, NT, false>;
+#pragma unroll
+    for (int n = 0; n < R::NK; ++n) {
+        const int idx = tid + n * NT, tt = idx / KP, c = idx % KP;
+        const bool on = s.val[tt] != 0.f, rs = s.rst[tt] != 0.f;
+        const float kf = raw_f<TIN>(r.k[n]), af = __uint_as_float(r.a[n]);
+        s.q[tt][c] = on ? raw_f<TIN>(r.q[n]) : 0.f;
+        s.k[tt][c] = on ? kf : 0.f;
+        s.a[tt][c] = on ? (rs ? 0.f : (a.scalar ? expf(af) : af)) : 1.f;
+        s.ek[tt][c] = on ? __uint_as_float(r.e[n]) * kf : 0.f;
+    }
+#pragma unroll
+    for (int n = 0; n < R::NV; ++n) {
+        const int idx = tid + n * NT, tt = idx / VP, c = idx % VP;
+        s.wv[tt][c] = s.val[tt] != 0.f ? __uint_as_float(r.w[n]) * raw_f<TIN>(r.v[n]) : 0.f;
+    }
+}
+
+// One token's operands for a forward lane.
+template <int RL, int CL>
+struct FwdTok {
+    float a[RL], ek[RL], k[RL], q[RL], wv[CL];
+};
+
+template <int KP, int VP, int RL, int CL>
+__device__ __forceinline__ void fetch_fwd(const FwdTokens<KP, VP> &B, int tt, int r0, int c0,
+                                          FwdTok<RL, CL> &x) {
+    lds_get<RL>(&B.a[tt][r0], x.a);
+    lds_get<RL>(&B.ek[tt][r0], x.ek);
+    lds_get<RL>(&B.k[tt][r0], x.k);
+    lds_get<RL>(&B.q[tt][r0], x.q);
+    lds_get<CL>(&B.wv[tt][c0], x.wv);
+}
+
+#pragma clang fp contract(off)
 template <int KP, int VP, typename TIN>
-__global__ void __launch_bounds__((KP / SEQ_KR) * VP) seq_fwd_kernel(SeqArgs a) {
-    constexpr int NG = KP / SEQ_KR, NT = NG * VP, CT = SEQ_CT, KR = SEQ_KR;
+__global__ void __launch_bounds__(4 * VP) seq_fwd_kernel(SeqArgs a) {
+    using L = FwdLayout<KP>;
+    constexpr int RL = L::RL, CL = L::CL, CLN = L::CLN, NT = 4 * VP, CT = SEQ_CT;
     __shared__ SeqFwdShared<KP, VP> sh;
     SeqFwdSmem<KP, VP> &s = sh.s;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int rg = lane / CLN, cl = lane % CLN;
+    const int r0 = RL * rg, c0 = 16 * w + CL * cl;  // first key row / value column of this lane
     const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
-    const int ig = tid % NG, j = tid / NG, i0 = ig * KR;
+    const int64_t tp = (int64_t)a.nck * CT;
 
     // Initial state, coalesced through the transpose slab.
     for (int idx = tid; idx < KP * VP; idx += NT) {
@@ -151,74 +391,118 @@ __global__ void __launch_bounds__((KP / SEQ_KR) * VP) seq_fwd_kernel(SeqArgs a) 
                                       : 0.f;
     }
     __syncthreads();
-    float S[KR];
+    float S[RL][CL];
 #pragma unroll
-    for (int r = 0; r < KR; ++r) S[r] = sh.st[(i0 + r) * (VP + 1) + j];
+    for (int ri = 0; ri < RL; ++ri)
+#pragma unroll
+        for (int cj = 0; cj < CL; ++cj) S[ri][cj] = sh.st[(r0 + ri) * (VP + 1) + c0 + cj];
     __syncthreads();
 
-    for (int t0 = 0, blk = 0; t0 < a.T; t0 += CT, ++blk) {
+    const TokenSrc src = make_src<TIN>(a, b, h);
+    const BlockCtx ctx = make_ctx(a, b, h, bh);
+    TokenRegs<KP, VP, NT, false> nx;
+    load_tokens<KP, VP, NT, false, TIN>(src, ctx, 0, tid, nx);
+    store_fwd_flags<KP, VP, NT, TIN>(a, nx, s.buf[0], 0, tid);
+    __syncthreads();
+    store_fwd_data<KP, VP, NT, TIN>(a, nx, s.buf[0], tid);
+    __syncthreads();
+
+    for (int blk = 0; blk < a.nck; ++blk) {
+        const int t0 = blk * CT, nt = min(CT, a.T - t0);
+        const FwdTokens<KP, VP> &B = s.buf[blk & 1];
         if (a.ck) {
-            float *ck = a.ck + ((int64_t)bh * a.nck + blk) * KR * NT;
+            float *ck = a.ck + ((int64_t)bh * a.nck + blk) * KP * VP;
 #pragma unroll
-            for (int r = 0; r < KR; ++r) ck[r * NT + tid] = S[r];
+            for (int ri = 0; ri < RL; ++ri) lds_put<CL>(ck + (r0 + ri) * VP + c0, S[ri]);
         }
-        stage_tokens<KP, VP, NT, TIN>(a, b, h, t0, s.q, s.k, s.a, s.e, s.v, s.w, s.val, s.rst,
-                                      nullptr, tid);
-        __syncthreads();
-        const int nt = min(CT, a.T - t0);
-        for (int tt = 0; tt < nt; ++tt) {
-            if (s.val[tt] == 0.f) {  // padding: zero output/edit, frozen state
-                if (ig == 0) {
-                    s.o[tt][j] = 0.f;
-                    s.d[tt][j] = 0.f;
+        if (blk + 1 < a.nck) load_tokens<KP, VP, NT, false, TIN>(src, ctx, t0 + CT, tid, nx);
+        // One token: S <- a S, delta = w v - S^T (e k), S += k delta^T,
+        // o = S^T q.  Key sums keep two partial chains per column.
+        auto step = [&](int tt, const FwdTok<RL, CL> &x) {
+            float p0[CL], p1[CL], delta[CL], o[CL];
+#pragma unroll
+            for (int cj = 0; cj < CL; ++cj) p0[cj] = p1[cj] = 0.f;
+#pragma unroll
+            for (int ri = 0; ri < RL; ++ri)
+#pragma unroll
+                for (int cj = 0; cj < CL; ++cj) {
+                    S[ri][cj] = S[ri][cj] * x.a[ri];
+                    if (ri & 1) p1[cj] = __builtin_fmaf(x.ek[ri], S[ri][cj], p1[cj]);
+                    else p0[cj] = __builtin_fmaf(x.ek[ri], S[ri][cj], p0[cj]);
                 }
-                continue;
-            }
-            if (s.rst[tt] != 0.f) {
 #pragma unroll
-                for (int r = 0; r < KR; ++r) S[r] = 0.f;
+            for (int cj = 0; cj < CL; ++cj) {
+                delta[cj] = x.wv[cj] - stride_sum<CLN>(p0[cj] + p1[cj]);
+                p0[cj] = p1[cj] = 0.f;
             }
-            float part = 0.f;
 #pragma unroll
-            for (int r = 0; r < KR; ++r) {
-                S[r] *= s.a[tt][i0 + r];
-                part += s.e[tt][i0 + r] * s.k[tt][i0 + r] * S[r];
-            }
-            const float delta = s.w[tt][j] * s.v[tt][j] - group_sum<NG>(part);
-            float o = 0.f;
+            for (int ri = 0; ri < RL; ++ri)
 #pragma unroll
-            for (int r = 0; r < KR; ++r) {
-                S[r] += s.k[tt][i0 + r] * delta;
-                o += s.q[tt][i0 + r] * S[r];
-            }
-            o = group_sum<NG>(o);
-            if (ig == 0) {
-                s.o[tt][j] = o;
-                s.d[tt][j] = delta;
-            }
+                for (int cj = 0; cj < CL; ++cj) {
+                    S[ri][cj] = __builtin_fmaf(x.k[ri], delta[cj], S[ri][cj]);
+                    if (ri & 1) p1[cj] = __builtin_fmaf(x.q[ri], S[ri][cj], p1[cj]);
+                    else p0[cj] = __builtin_fmaf(x.q[ri], S[ri][cj], p0[cj]);
+                }
+#pragma unroll
+            for (int cj = 0; cj < CL; ++cj) o[cj] = stride_sum<CLN>(p0[cj] + p1[cj]);
+            // Every row group holds the same sums; all lanes store them.
+            lds_put<CL>(&s.o[tt][c0], o);
+            lds_put<CL>(&s.d[tt][c0], delta);
+        };
+        // All SEQ_CT tokens straight-line (tokens past the sequence are staged
+        // as padding), two operand sets in turn so the next token's LDS reads
+        // overlap this one.
+        FwdTok<RL, CL> x[2];
+        fetch_fwd<KP, VP, RL, CL>(B, 0, r0, c0, x[0]);
+#pragma unroll
+        for (int tt = 0; tt < CT; ++tt) {
+            if (tt + 1 < CT) fetch_fwd<KP, VP, RL, CL>(B, tt + 1, r0, c0, x[(tt + 1) & 1]);
+            step(tt, x[tt & 1]);
         }
         __syncthreads();
-        for (int idx = tid; idx < nt * VP; idx += NT) {
-            const int tt = idx / VP, c = idx % VP;
-            if (c < a.V)
-                store_out(a.out, a.out_bf16, (((int64_t)b * a.T + t0 + tt) * a.H + h) * a.V + c,
-                          s.o[tt][c]);
+        // Stage the next block first: its loads are the oldest memory
+        // operations still in flight, so waiting for them does not wait for
+        // this block's output stores.
+        if (blk + 1 < a.nck) {
+            store_fwd_flags<KP, VP, NT, TIN>(a, nx, s.buf[(blk + 1) & 1], t0 + CT, tid);
+            __syncthreads();
+            store_fwd_data<KP, VP, NT, TIN>(a, nx, s.buf[(blk + 1) & 1], tid);
         }
-        if (a.scores && tid < nt) {
-            float sc = 0.f;
-            if (s.val[tid] != 0.f) {
-                float kk = 0.f, dd = 0.f;
-                for (int c = 0; c < a.K; ++c) kk += s.k[tid][c] * s.k[tid][c];
-                for (int c = 0; c < a.V; ++c) dd += s.d[tid][c] * s.d[tid][c];
-                sc = sqrtf(kk * dd);
+        for (int idx = tid; idx < CT * VP; idx += NT) {
+            const int tt = idx / VP, c = idx % VP;
+            if (tt < nt) {
+                if (c < a.V)
+                    store_out(a.out, a.out_bf16, (((int64_t)b * a.T + t0 + tt) * a.H + h) * a.V + c,
+                              s.o[tt][c]);
+                if (a.ck) a.ck_delta[((int64_t)bh * tp + t0 + tt) * VP + c] = s.d[tt][c];
             }
-            a.scores[((int64_t)b * a.T + t0 + tid) * a.H + h] = sc;
+        }
+        // Scores |k| |delta| (zero on padding) and the checkpoint norms: one
+        // 16-lane row per token.
+        for (int tt = tid >> 4; tt < CT; tt += NT / 16) {
+            const int l = tid & 15;
+            float kk = 0.f, dd = 0.f;
+            for (int c = l; c < KP; c += 16) kk = __builtin_fmaf(B.k[tt][c], B.k[tt][c], kk);
+            for (int c = l; c < VP; c += 16) dd = __builtin_fmaf(s.d[tt][c], s.d[tt][c], dd);
+            kk = row16_sum(kk);
+            dd = row16_sum(dd);
+            if (l == 0 && tt < nt) {
+                const int t = t0 + tt;
+                if (a.scores)
+                    a.scores[((int64_t)b * a.T + t) * a.H + h] = B.val[tt] != 0.f ? sqrtf(kk * dd) : 0.f;
+                if (a.ck) {
+                    a.ck_norm[((int64_t)bh * tp + t) * 2] = sqrtf(kk);
+                    a.ck_norm[((int64_t)bh * tp + t) * 2 + 1] = sqrtf(dd);
+                }
+            }
         }
         __syncthreads();
     }
     // Final state through the transpose slab.
 #pragma unroll
-    for (int r = 0; r < KR; ++r) sh.st[(i0 + r) * (VP + 1) + j] = S[r];
+    for (int ri = 0; ri < RL; ++ri)
+#pragma unroll
+        for (int cj = 0; cj < CL; ++cj) sh.st[(r0 + ri) * (VP + 1) + c0 + cj] = S[ri][cj];
     __syncthreads();
     if (a.final_state)
         for (int idx = tid; idx < a.K * a.V; idx += NT) {
@@ -226,227 +510,363 @@ __global__ void __launch_bounds__((KP / SEQ_KR) * VP) seq_fwd_kernel(SeqArgs a) 
             a.final_state[(int64_t)bh * a.K * a.V + idx] = sh.st[i * (VP + 1) + c];
         }
 }
+#pragma clang fp contract(on)
+
+// ---- backward --------------------------------------------------------------------
 
 template <int KP, int VP>
-struct SeqBwdSmem {
-    static constexpr int CT = SEQ_CT, NW = (KP / SEQ_KR) * VP / 64;
-    float q[CT][KP], k[CT][KP], a[CT][KP], e[CT][KP];
-    float v[CT][VP], w[CT][VP], dy[CT][VP], d[CT][VP];
-    float val[CT], rst[CT], aclr[CT], sa[CT], kk[CT], dd[CT];
-    float red[2][NW][4][KP];
+struct SeqBwdCfg {
+    static constexpr int CL = VP == 128 ? 4 : 2;  // value columns per lane
+    static constexpr int NW = VP / (4 * CL);      // waves (16 row groups x 4 column lanes)
+    static constexpr int NT = 64 * NW;
+    static constexpr int RL = KP / 16;            // key rows per lane
+    static constexpr int FT0 = 4096 / (NW * KP);
+    static constexpr int FT = FT0 >= SEQ_CT ? SEQ_CT : FT0;  // tokens per cross-wave sum
+    static constexpr int RP = KP + 4;   // partial-sum row pitch (spreads LDS banks)
+    // Up to 64 key rows the registers hold the next block's checkpoint and the
+    // next token's LDS operands as well.
+    static constexpr bool AHEAD = RL <= 4;
+    static_assert(SEQ_CT % FT == 0, "flush groups tile a block");
 };
 
 template <int KP, int VP>
-union SeqBwdShared {
-    SeqBwdSmem<KP, VP> s;
-    float st[KP * (VP + 1)];
+struct alignas(16) SeqBwdSmem {
+    using Cfg = SeqBwdCfg<KP, VP>;
+    float q[SEQ_CT][KP], k[SEQ_CT][KP], a[SEQ_CT][KP], e[SEQ_CT][KP];
+    float v[SEQ_CT][VP], w[SEQ_CT][VP], dy[SEQ_CT][VP], d[SEQ_CT][VP];
+    float dd[SEQ_CT][VP];  // edit adjoint of every token (zero on padding)
+    float val[SEQ_CT], rst[SEQ_CT], clr[SEQ_CT], cs[SEQ_CT], ks[SEQ_CT];
+    // red[slot][wave][quantity][key]: per-wave sums over the wave's value
+    // columns of the q-gradient, adj.delta, bar.ddelta and dalpha terms.
+    float red[Cfg::FT][Cfg::NW][4][Cfg::RP];
 };
 
-template <typename TIN>
-__device__ __forceinline__ void store_in(void *p, int64_t i, float x) {
-    Elem<TIN>::store(p, i, x);
+// Stage a block for the backward in two passes (a barrier between them): the
+// per-token flags and score-VJP coefficients, then the operands.  Padded
+// tokens get a = 1 and zero q, k, e, dy (their delta is zero): the adjoint
+// passes unchanged and every gradient but dalpha comes out zero (the flush
+// zeroes dalpha).  With masks, a reset token gets a = 0, which cuts the
+// adjoint; with document limits its own a stays (the adjoint crosses resets).
+template <int KP, int VP, int NT, typename TIN>
+__device__ __forceinline__ void store_bwd_flags(const SeqArgs &a,
+                                                const TokenRegs<KP, VP, NT, true> &r,
+                                                SeqBwdSmem<KP, VP> &s, int t0, int tid) {
+    if (tid < SEQ_CT) {
+        float val, rst, clr;
+        token_flags(a, r, t0 + tid, val, rst, clr);
+        s.val[tid] = val;
+        s.rst[tid] = rst;
+        s.clr[tid] = clr;
+        // Score VJP (zero subgradient at |k| |delta| = 0): ddelta += cs delta,
+        // dk += ks k.
+        const float sa = __uint_as_float(r.sa), nk = __uint_as_float(r.nk), nd = __uint_as_float(r.nd);
+        const bool ok = val != 0.f && nk > 0.f && nd > 0.f;
+        s.cs[tid] = ok ? sa * nk / nd : 0.f;
+        s.ks[tid] = ok ? sa * nd / nk : 0.f;
+    }
 }
 
+template <int KP, int VP, int NT, typename TIN>
+__device__ __forceinline__ void store_bwd_data(const SeqArgs &a,
+                                               const TokenRegs<KP, VP, NT, true> &r,
+                                               SeqBwdSmem<KP, VP> &s, int tid) {
+    using R = TokenRegs<KP, VP, NT, true>;
+#pragma unroll
+    for (int n = 0; n < R::NK; ++n) {
+        const int idx = tid + n * NT, tt = idx / KP, c = idx % KP;
+        const bool on = s.val[tt] != 0.f, cut = s.rst[tt] != 0.f && !a.doc;
+        const float af = __uint_as_float(r.a[n]);
+        s.q[tt][c] = on ? raw_f<TIN>(r.q[n]) : 0.f;
+        s.k[tt][c] = on ? raw_f<TIN>(r.k[n]) : 0.f;
+        s.a[tt][c] = on ? (cut ? 0.f : (a.scalar ? expf(af) : af)) : 1.f;
+        s.e[tt][c] = on ? __uint_as_float(r.e[n]) : 0.f;
+    }
+#pragma unroll
+    for (int n = 0; n < R::NV; ++n) {
+        const int idx = tid + n * NT, tt = idx / VP, c = idx % VP;
+        const bool on = s.val[tt] != 0.f;
+        s.v[tt][c] = raw_f<TIN>(r.v[n]);
+        s.w[tt][c] = __uint_as_float(r.w[n]);
+        s.dy[tt][c] = on ? raw_f<TIN>(r.dy[n]) : 0.f;
+        s.d[tt][c] = __uint_as_float(r.d[n]);
+    }
+}
+
+template <int KP, int VP, int RL, int CL>
+__device__ __forceinline__ void load_ck(const SeqArgs &a, int bh, int blk, int r0, int c0,
+                                        float (&S)[RL][CL]) {
+    const float *ck = a.ck + ((int64_t)bh * a.nck + blk) * KP * VP;
+#pragma unroll
+    for (int ri = 0; ri < RL; ++ri) lds_get<CL>(ck + (r0 + ri) * VP + c0, S[ri]);
+}
+
+// One token's operands for a backward lane.
+template <int RL, int CL>
+struct BwdTok {
+    float q[RL], k[RL], a[RL], e[RL], dy[CL], d[CL];
+    float cs;
+};
+
+template <int KP, int VP, int RL, int CL>
+__device__ __forceinline__ void fetch_bwd(const SeqBwdSmem<KP, VP> &s, int tt, int r0, int c0,
+                                          BwdTok<RL, CL> &x) {
+    lds_get<RL>(&s.q[tt][r0], x.q);
+    lds_get<RL>(&s.k[tt][r0], x.k);
+    lds_get<RL>(&s.a[tt][r0], x.a);
+    lds_get<RL>(&s.e[tt][r0], x.e);
+    lds_get<CL>(&s.dy[tt][c0], x.dy);
+    lds_get<CL>(&s.d[tt][c0], x.d);
+    x.cs = s.cs[tt];
+}
+
+// Sum the per-wave partials of tokens g0 .. g0+FT-1 (those below nt) and
+// store dq, dk, dalpha, derase, dv, dwrite; scalar-gate mode keeps derase and
+// dalpha in the consumed e/a rows of LDS for the per-token chain rule.
 template <int KP, int VP, typename TIN>
-__global__ void __launch_bounds__((KP / SEQ_KR) * VP) seq_bwd_kernel(SeqArgs a) {
-    constexpr int NG = KP / SEQ_KR, NT = NG * VP, CT = SEQ_CT, KR = SEQ_KR, NW = NT / 64;
-    __shared__ SeqBwdShared<KP, VP> sh;
-    SeqBwdSmem<KP, VP> &s = sh.s;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ void flush_group(const SeqArgs &a, SeqBwdSmem<KP, VP> &s, int b, int h,
+                                            int t0, int g0, int nt, int tid) {
+    using Cfg = SeqBwdCfg<KP, VP>;
+    for (int idx = tid; idx < Cfg::FT * KP; idx += Cfg::NT) {
+        const int sl = idx / KP, i = idx % KP, tt = g0 + sl;
+        if (tt >= nt) continue;
+        float gq = 0.f, gad = 0.f, gbd = 0.f, ga = 0.f;
+#pragma unroll
+        for (int wv = 0; wv < Cfg::NW; ++wv) {
+            gq += s.red[sl][wv][0][i];
+            gad += s.red[sl][wv][1][i];
+            gbd += s.red[sl][wv][2][i];
+            ga += s.red[sl][wv][3][i];
+        }
+        if (s.val[tt] == 0.f) ga = 0.f;  // padding: the adjoint passed through
+        const float kr = s.k[tt][i], er = s.e[tt][i];
+        const float dk = __builtin_fmaf(s.ks[tt], kr, __builtin_fmaf(-er, gbd, gad));
+        const float de = -kr * gbd;
+        if (i < a.K) {
+            const int64_t o = (((int64_t)b * a.T + t0 + tt) * a.H + h) * a.K + i;
+            if (a.dq) store_in<TIN>(a.dq, o, gq);
+            if (a.dk) store_in<TIN>(a.dk, o, dk);
+            if (a.dalpha) a.dalpha[o] = ga;
+            if (a.derase) a.derase[o] = de;
+        }
+        if (a.scalar) {
+            s.a[tt][i] = i < a.K ? ga : 0.f;
+            s.e[tt][i] = i < a.K ? de : 0.f;
+        }
+    }
+    for (int idx = tid; idx < Cfg::FT * VP; idx += Cfg::NT) {
+        const int sl = idx / VP, j = idx % VP, tt = g0 + sl;
+        if (tt >= nt || j >= a.V) continue;
+        const float dd = s.dd[tt][j];
+        const int64_t o = (((int64_t)b * a.T + t0 + tt) * a.H + h) * a.V + j;
+        if (a.dv) store_in<TIN>(a.dv, o, s.w[tt][j] * dd);
+        if (a.dwrite) a.dwrite[o] = s.v[tt][j] * dd;
+    }
+}
+
+#pragma clang fp contract(off)
+template <int KP, int VP, typename TIN>
+__global__ void __launch_bounds__((SeqBwdCfg<KP, VP>::NT)) seq_bwd_kernel(SeqArgs a) {
+    using Cfg = SeqBwdCfg<KP, VP>;
+    constexpr int NT = Cfg::NT, RL = Cfg::RL, CL = Cfg::CL, FT = Cfg::FT, CT = SEQ_CT;
+    constexpr bool AHEAD = Cfg::AHEAD;
+    __shared__ SeqBwdSmem<KP, VP> s;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int rg = lane >> 2, cl = lane & 3;
+    const int r0 = RL * rg, c0 = 4 * CL * w + CL * cl;  // first key row / value column of this lane
     const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
-    const int ig = tid % NG, j = tid / NG, i0 = ig * KR;
     const int64_t KV = (int64_t)a.K * a.V;
 
-    // Adjoint of the final state, coalesced through the transpose slab.
-    for (int idx = tid; idx < KP * VP; idx += NT) {
-        const int i = idx / VP, c = idx % VP;
-        sh.st[i * (VP + 1) + c] =
-            (a.dfinal && i < a.K && c < a.V) ? a.dfinal[bh * KV + (int64_t)i * a.V + c] : 0.f;
-    }
-    __syncthreads();
-    float adj[KR];
+    float adj[RL][CL];
 #pragma unroll
-    for (int r = 0; r < KR; ++r) adj[r] = sh.st[(i0 + r) * (VP + 1) + j];
+    for (int ri = 0; ri < RL; ++ri)
+#pragma unroll
+        for (int cj = 0; cj < CL; ++cj) {
+            const int i = r0 + ri, j = c0 + cj;
+            adj[ri][cj] = (a.dfinal && i < a.K && j < a.V) ? a.dfinal[bh * KV + (int64_t)i * a.V + j]
+                                                           : 0.f;
+        }
+
+    // Pre-token states of the current block: CL floats at
+    // rp + ((tt * RL + ri) * NT + tid) * CL.
+    float *rp = a.replay + (int64_t)bh * CT * KP * VP;
+
+    const TokenSrc src = make_src<TIN>(a, b, h);
+    const BlockCtx ctx = make_ctx(a, b, h, bh);
+    TokenRegs<KP, VP, NT, true> nx;
+    float ckn[RL][CL];
+    load_tokens<KP, VP, NT, true, TIN>(src, ctx, (a.nck - 1) * CT, tid, nx);
+    if (AHEAD) load_ck<KP, VP, RL, CL>(a, bh, a.nck - 1, r0, c0, ckn);
+    store_bwd_flags<KP, VP, NT, TIN>(a, nx, s, (a.nck - 1) * CT, tid);
+    __syncthreads();
+    store_bwd_data<KP, VP, NT, TIN>(a, nx, s, tid);
     __syncthreads();
 
-    float *rp = a.replay + (int64_t)bh * CT * KR * NT;
-    int buf = 0;
     for (int blk = a.nck - 1; blk >= 0; --blk) {
         const int t0 = blk * CT, nt = min(CT, a.T - t0);
-        stage_tokens<KP, VP, NT, TIN>(a, b, h, t0, s.q, s.k, s.a, s.e, s.v, s.w, s.val, s.rst,
-                                      s.aclr, tid);
-        for (int idx = tid; idx < CT * VP; idx += NT) {
-            const int tt = idx / VP, c = idx % VP, t = t0 + tt;
-            s.dy[tt][c] = (a.dout.data && t < a.T && c < a.V) ? ld4<TIN>(a.dout, b, t, h, c) : 0.f;
-        }
-        if (tid < CT) {
-            const int t = t0 + tid;
-            s.sa[tid] = (a.dscores && t < a.T) ? a.dscores[((int64_t)b * a.T + t) * a.H + h] : 0.f;
-        }
-        // Replay the block from its checkpoint; rp[tt] = state before token tt.
-        float S[KR];
-        const float *ck = a.ck + ((int64_t)bh * a.nck + blk) * KR * NT;
+        // Resets and adjoint clears as wave-uniform bit masks.
+        const uint64_t rm = __ballot(lane < CT && s.rst[lane & (CT - 1)] != 0.f &&
+                                     s.val[lane & (CT - 1)] != 0.f);
+        const uint64_t cm = __ballot(lane < CT && s.clr[lane & (CT - 1)] != 0.f &&
+                                     s.val[lane & (CT - 1)] != 0.f);
+        if (!AHEAD) load_ck<KP, VP, RL, CL>(a, bh, blk, r0, c0, ckn);
+        float S[RL][CL];
 #pragma unroll
-        for (int r = 0; r < KR; ++r) S[r] = ck[r * NT + tid];
-        __syncthreads();
+        for (int ri = 0; ri < RL; ++ri)
+#pragma unroll
+            for (int cj = 0; cj < CL; ++cj) S[ri][cj] = ckn[ri][cj];
+        // The earlier block's inputs: issued here, written to LDS after the
+        // token loop.
+        if (blk > 0) {
+            load_tokens<KP, VP, NT, true, TIN>(src, ctx, t0 - CT, tid, nx);
+            if (AHEAD) load_ck<KP, VP, RL, CL>(a, bh, blk - 1, r0, c0, ckn);
+        }
+        // Replay the block with the forward's deltas: padding leaves S as is
+        // (a = 1, k = 0, delta = 0); a reset zeroes it first.
         for (int tt = 0; tt < nt; ++tt) {
+            const bool rs = (rm >> tt) & 1;
 #pragma unroll
-            for (int r = 0; r < KR; ++r) rp[((int64_t)tt * KR + r) * NT + tid] = S[r];
-            if (s.val[tt] == 0.f) {
-                if (ig == 0) s.d[tt][j] = 0.f;
-                continue;
-            }
-            if (s.rst[tt] != 0.f) {
+            for (int ri = 0; ri < RL; ++ri)
 #pragma unroll
-                for (int r = 0; r < KR; ++r) S[r] = 0.f;
-            }
-            float part = 0.f;
+                for (int cj = 0; cj < CL; ++cj) S[ri][cj] = rs ? 0.f : S[ri][cj];
 #pragma unroll
-            for (int r = 0; r < KR; ++r) {
-                S[r] *= s.a[tt][i0 + r];
-                part += s.e[tt][i0 + r] * s.k[tt][i0 + r] * S[r];
-            }
-            const float delta = s.w[tt][j] * s.v[tt][j] - group_sum<NG>(part);
+            for (int ri = 0; ri < RL; ++ri) lds_put<CL>(rp + ((tt * RL + ri) * NT + tid) * CL, S[ri]);
+            float dl[CL], al[RL], kr[RL];
+            lds_get<CL>(&s.d[tt][c0], dl);
+            lds_get<RL>(&s.a[tt][r0], al);
+            lds_get<RL>(&s.k[tt][r0], kr);
 #pragma unroll
-            for (int r = 0; r < KR; ++r) S[r] += s.k[tt][i0 + r] * delta;
-            if (ig == 0) s.d[tt][j] = delta;
+            for (int ri = 0; ri < RL; ++ri)
+#pragma unroll
+                for (int cj = 0; cj < CL; ++cj)
+                    S[ri][cj] = __builtin_fmaf(kr[ri], dl[cj], S[ri][cj] * al[ri]);
         }
-        __syncthreads();
-        if (tid < nt) {
-            float kk = 0.f, dd = 0.f;
-            for (int c = 0; c < a.K; ++c) kk += s.k[tid][c] * s.k[tid][c];
-            for (int c = 0; c < a.V; ++c) dd += s.d[tid][c] * s.d[tid][c];
-            s.kk[tid] = sqrtf(kk);
-            s.dd[tid] = sqrtf(dd);
+        auto load_prev = [&](int tt, float (&p)[RL][CL]) {
+#pragma unroll
+            for (int ri = 0; ri < RL; ++ri) lds_get<CL>(rp + ((tt * RL + ri) * NT + tid) * CL, p[ri]);
+        };
+        // One token of the reverse sweep.
+        auto step = [&](int tt, const float (&prev)[RL][CL], const BwdTok<RL, CL> &xin) {
+            BwdTok<RL, CL> xl;
+            if (!AHEAD) fetch_bwd<KP, VP, RL, CL>(s, tt, r0, c0, xl);
+            const BwdTok<RL, CL> &x = AHEAD ? xin : xl;
+            const int slot = tt % FT;
+            // Document limits: the adjoint is cleared where a document ends.
+            if ((cm >> tt) & 1) {
+#pragma unroll
+                for (int ri = 0; ri < RL; ++ri)
+#pragma unroll
+                    for (int cj = 0; cj < CL; ++cj) adj[ri][cj] = 0.f;
+            }
+#pragma unroll
+            for (int ri = 0; ri < RL; ++ri)
+#pragma unroll
+                for (int cj = 0; cj < CL; ++cj)
+                    adj[ri][cj] = __builtin_fmaf(x.q[ri], x.dy[cj], adj[ri][cj]);
+            // Edit adjoint ddelta_j = sum_i k_i adj_ij + cs delta_j.
+            float dd[CL];
+#pragma unroll
+            for (int cj = 0; cj < CL; ++cj) {
+                float p = 0.f;
+#pragma unroll
+                for (int ri = 0; ri < RL; ++ri) p = __builtin_fmaf(x.k[ri], adj[ri][cj], p);
+                dd[cj] = __builtin_fmaf(x.cs, x.d[cj], stride_sum<4>(p));
+            }
+            // Per-key terms summed over this lane's columns, then over the
+            // column quad; lane cl keeps quantity cl.
+            float *red = &s.red[slot][w][cl][r0];
+#pragma unroll
+            for (int ri = 0; ri < RL; ++ri) {
+                const float ek = x.e[ri] * x.k[ri];
+                float gq = 0.f, gad = 0.f, gbd = 0.f, ga = 0.f;
+#pragma unroll
+                for (int cj = 0; cj < CL; ++cj) {
+                    const float p = prev[ri][cj];
+                    const float bar = x.a[ri] * p;
+                    gq = __builtin_fmaf(__builtin_fmaf(x.k[ri], x.d[cj], bar), x.dy[cj], gq);
+                    gad = __builtin_fmaf(adj[ri][cj], x.d[cj], gad);
+                    gbd = __builtin_fmaf(bar, dd[cj], gbd);
+                    const float dbar = __builtin_fmaf(-ek, dd[cj], adj[ri][cj]);
+                    ga = __builtin_fmaf(dbar, p, ga);
+                    adj[ri][cj] = x.a[ri] * dbar;
+                }
+                gq = group_sum<4>(gq);
+                gad = group_sum<4>(gad);
+                gbd = group_sum<4>(gbd);
+                ga = group_sum<4>(ga);
+                red[ri] = cl == 0 ? gq : (cl == 1 ? gad : (cl == 2 ? gbd : ga));
+            }
+            // Every row group holds the same column sums; all lanes store them.
+            lds_put<CL>(&s.dd[tt][c0], dd);
+            if (slot == 0) {  // tokens tt .. tt+FT-1 are complete
+                __syncthreads();
+                flush_group<KP, VP, TIN>(a, s, b, h, t0, tt, nt, tid);
+                __syncthreads();
+            }
+        };
+        // Two sets of (pre-token state, operands) in turn: the next token's
+        // scratch and LDS reads overlap this one.
+        float pa[RL][CL], pb[RL][CL];
+        BwdTok<RL, CL> xa, xb;
+        load_prev(nt - 1, pa);
+        if (AHEAD) fetch_bwd<KP, VP, RL, CL>(s, nt - 1, r0, c0, xa);
+        for (int tt = nt - 1; tt >= 0; tt -= 2) {
+            if (tt > 0) {
+                load_prev(tt - 1, pb);
+                if (AHEAD) fetch_bwd<KP, VP, RL, CL>(s, tt - 1, r0, c0, xb);
+            }
+            step(tt, pa, xa);
+            if (tt == 0) break;
+            if (tt > 1) {
+                load_prev(tt - 2, pa);
+                if (AHEAD) fetch_bwd<KP, VP, RL, CL>(s, tt - 2, r0, c0, xa);
+            }
+            step(tt - 1, pb, xb);
         }
-        __syncthreads();
-
-        for (int tt = nt - 1; tt >= 0; --tt) {
-            const int t = t0 + tt;
-            const int64_t tok = ((int64_t)b * a.T + t) * a.H + h;
-            if (s.val[tt] == 0.f) {  // padding: exact zero gradients, adjoint passes through
-                for (int idx = tid; idx < a.K; idx += NT) {
-                    if (a.dq) store_in<TIN>(a.dq, tok * a.K + idx, 0.f);
-                    if (a.dk) store_in<TIN>(a.dk, tok * a.K + idx, 0.f);
-                    if (a.dalpha) a.dalpha[tok * a.K + idx] = 0.f;
-                    if (a.derase) a.derase[tok * a.K + idx] = 0.f;
+        if (a.scalar) {  // chain rule onto beta and the log gate g
+            for (int tt = tid >> 4; tt < CT; tt += NT / 16) {
+                const int l = tid & 15;
+                float de = 0.f, da = 0.f, dw = 0.f;
+                for (int c = l; c < KP; c += 16) {
+                    de += s.e[tt][c];
+                    da += s.a[tt][c];
                 }
-                for (int idx = tid; idx < a.V; idx += NT) {
-                    if (a.dv) store_in<TIN>(a.dv, tok * a.V + idx, 0.f);
-                    if (a.dwrite) a.dwrite[tok * a.V + idx] = 0.f;
+                for (int c = l; c < VP; c += 16) dw = __builtin_fmaf(s.v[tt][c], s.dd[tt][c], dw);
+                de = row16_sum(de);
+                da = row16_sum(da);
+                dw = row16_sum(dw);
+                if (l == 0 && tt < nt) {
+                    const int t = t0 + tt;
+                    const int64_t tok = ((int64_t)b * a.T + t) * a.H + h;
+                    const bool on = s.val[tt] != 0.f;
+                    if (a.dbeta) a.dbeta[tok] = on ? de + dw : 0.f;
+                    if (a.dg) a.dg[tok] = on ? expf(ld4<float>(a.g, b, t, h, 0)) * da : 0.f;
                 }
-                if (a.scalar && tid == 0) {
-                    if (a.dbeta) a.dbeta[tok] = 0.f;
-                    if (a.dg) a.dg[tok] = 0.f;
-                }
-                continue;
-            }
-            const bool rst = s.rst[tt] != 0.f;
-            float prev[KR];
-#pragma unroll
-            for (int r = 0; r < KR; ++r) prev[r] = rst ? 0.f : rp[((int64_t)tt * KR + r) * NT + tid];
-            const float dy = s.dy[tt][j], delta = s.d[tt][j];
-            const float nk = s.kk[tt], nd = s.dd[tt], sadj = s.sa[tt];
-            float dd = 0.f;
-            if (nk > 0.f && nd > 0.f) dd = sadj * nk * delta / nd;  // score VJP, zero subgradient
-            if (s.aclr[tt] != 0.f) {  // doc limits: a document ends here
-#pragma unroll
-                for (int r = 0; r < KR; ++r) adj[r] = 0.f;
-            }
-            float part = 0.f;
-#pragma unroll
-            for (int r = 0; r < KR; ++r) {
-                adj[r] += s.q[tt][i0 + r] * dy;
-                part += s.k[tt][i0 + r] * adj[r];
-            }
-            dd += group_sum<NG>(part);
-            float gq[KR], gk[KR], ge[KR], ga[KR];
-#pragma unroll
-            for (int r = 0; r < KR; ++r) {
-                const float kr = s.k[tt][i0 + r], er = s.e[tt][i0 + r], ar = s.a[tt][i0 + r];
-                const float bar = ar * prev[r];
-                gq[r] = (bar + kr * delta) * dy;
-                gk[r] = adj[r] * delta - er * bar * dd;
-                ge[r] = -kr * bar * dd;
-                const float dbar = adj[r] - er * kr * dd;
-                ga[r] = dbar * prev[r];
-                adj[r] = (rst && !a.doc) ? 0.f : ar * dbar;
-            }
-            // Sum over the value columns held by this wave (lanes sharing ig).
-#pragma unroll
-            for (int r = 0; r < KR; ++r) {
-                gq[r] = column_sum<NG>(gq[r]);
-                gk[r] = column_sum<NG>(gk[r]);
-                ge[r] = column_sum<NG>(ge[r]);
-                ga[r] = column_sum<NG>(ga[r]);
-            }
-            if (lane < NG) {
-#pragma unroll
-                for (int r = 0; r < KR; ++r) {
-                    s.red[buf][wave][0][i0 + r] = gq[r];
-                    s.red[buf][wave][1][i0 + r] = gk[r];
-                    s.red[buf][wave][2][i0 + r] = ga[r];
-                    s.red[buf][wave][3][i0 + r] = ge[r];
-                }
-            }
-            if (ig == 0 && j < a.V) {
-                if (a.dv) store_in<TIN>(a.dv, tok * a.V + j, s.w[tt][j] * dd);
-                if (a.dwrite) a.dwrite[tok * a.V + j] = s.v[tt][j] * dd;
-                // Scalar mode keeps dwrite_j in the (already consumed) dy slot.
-                if (a.scalar) s.dy[tt][j] = s.v[tt][j] * dd;
             }
             __syncthreads();
-            const float kscale = (nk > 0.f && nd > 0.f) ? sadj * nd / nk : 0.f;
-            for (int idx = tid; idx < 4 * a.K; idx += NT) {
-                const int qn = idx / a.K, i = idx % a.K;
-                float acc = 0.f;
-#pragma unroll
-                for (int w = 0; w < NW; ++w) acc += s.red[buf][w][qn][i];
-                if (qn == 0) {
-                    if (a.dq) store_in<TIN>(a.dq, tok * a.K + i, acc);
-                } else if (qn == 1) {
-                    if (a.dk) store_in<TIN>(a.dk, tok * a.K + i, acc + kscale * s.k[tt][i]);
-                } else if (qn == 2) {
-                    if (a.dalpha) a.dalpha[tok * a.K + i] = acc;
-                    if (a.scalar) s.a[tt][i] = acc;  // alpha row of token tt is consumed
-                } else {
-                    if (a.derase) a.derase[tok * a.K + i] = acc;
-                    if (a.scalar) s.e[tt][i] = acc;
-                }
-            }
-            buf ^= 1;
         }
-        __syncthreads();
-        if (a.scalar) {  // chain rule onto beta and the log gate g
-            if (tid < nt && s.val[tid] != 0.f) {
-                const int t = t0 + tid;
-                const int64_t tok = ((int64_t)b * a.T + t) * a.H + h;
-                float de = 0.f, dw = 0.f, da = 0.f;
-                for (int c = 0; c < a.K; ++c) {
-                    de += s.e[tid][c];
-                    da += s.a[tid][c];
-                }
-                for (int c = 0; c < a.V; ++c) dw += s.dy[tid][c];
-                if (a.dbeta) a.dbeta[tok] = de + dw;
-                if (a.dg) a.dg[tok] = expf(ld4<float>(a.g, b, t, h, 0)) * da;
-            }
+        if (blk > 0) {
+            store_bwd_flags<KP, VP, NT, TIN>(a, nx, s, t0 - CT, tid);
+            __syncthreads();
+            store_bwd_data<KP, VP, NT, TIN>(a, nx, s, tid);
             __syncthreads();
         }
     }
     // Initial-state adjoint.
+    if (a.dinitial) {
 #pragma unroll
-    for (int r = 0; r < KR; ++r) sh.st[(i0 + r) * (VP + 1) + j] = adj[r];
-    __syncthreads();
-    if (a.dinitial)
-        for (int idx = tid; idx < a.K * a.V; idx += NT) {
-            const int i = idx / a.V, c = idx % a.V;
-            a.dinitial[bh * KV + idx] = sh.st[i * (VP + 1) + c];
-        }
+        for (int ri = 0; ri < RL; ++ri)
+#pragma unroll
+            for (int cj = 0; cj < CL; ++cj) {
+                const int i = r0 + ri, j = c0 + cj;
+                if (i < a.K && j < a.V) a.dinitial[bh * KV + (int64_t)i * a.V + j] = adj[ri][cj];
+            }
+    }
 }
+#pragma clang fp contract(on)
 
 template <int KP, int VP>
 static hipError_t fwd_typed(const SeqArgs &a, bool bf16, hipStream_t st) {
-    constexpr int NT = (KP / SEQ_KR) * VP;
+    constexpr int NT = 4 * VP;
     if (bf16)
         hipLaunchKernelGGL((seq_fwd_kernel<KP, VP, bf16_t>), dim3(a.B * a.H), dim3(NT), 0, st, a);
     else
@@ -456,7 +876,7 @@ static hipError_t fwd_typed(const SeqArgs &a, bool bf16, hipStream_t st) {
 
 template <int KP, int VP>
 static hipError_t bwd_typed(const SeqArgs &a, bool bf16, hipStream_t st) {
-    constexpr int NT = (KP / SEQ_KR) * VP;
+    constexpr int NT = SeqBwdCfg<KP, VP>::NT;
     if (bf16)
         hipLaunchKernelGGL((seq_bwd_kernel<KP, VP, bf16_t>), dim3(a.B * a.H), dim3(NT), 0, st, a);
     else
@@ -481,6 +901,7 @@ hipError_t launch_seq_fwd(const SeqArgs &a, bool bf16, hipStream_t st) {
 }
 
 hipError_t launch_seq_bwd(const SeqArgs &a, bool bf16, hipStream_t st) {
+    if (!a.ck || !a.replay) return hipErrorInvalidValue;
     GDN2_SEQ_DISPATCH(bwd_typed)
 }
 
