@@ -93,84 +93,172 @@ __device__ __forceinline__ int64_t token(const HolaArgs &a, int b, int t, int h)
 
 // ---- schedule ---------------------------------------------------------------------
 
+// One wave per (batch, head), chunks in order.  The cache entries carry their
+// ranking key and document in LDS, and the next chunk's token words (valid,
+// document, score) are loaded while the current chunk is ranked, so a chunk
+// costs LDS work only.
 __global__ void __launch_bounds__(64) hola_schedule_kernel(HolaArgs a) {
-    __shared__ float cache[kMaxCapacity], next[kMaxCapacity];
-    __shared__ float pos[kMaxSlots], pri[kMaxSlots];
+    __shared__ float cpos[kMaxCapacity], cpri[kMaxCapacity], cdoc[kMaxCapacity];
+    __shared__ float pos[kMaxSlots], pri[kMaxSlots], sdoc[kMaxSlots];
+    __shared__ __align__(16) uint64_t key[kMaxSlots];
+    __shared__ float npos[kMaxCapacity], npri[kMaxCapacity], ndoc[kMaxCapacity];
     const int lane = threadIdx.x, bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
     const int slots = a.cap + a.chunk;
     float *sched = a.schedule + (int64_t)bh * (a.nc + 1) * a.cap;
     if (lane < a.cap) {
-        cache[lane] = -1.f;
+        cpos[lane] = -1.f;
+        cpri[lane] = cdoc[lane] = 0.f;
         sched[lane] = -1.f;
     }
+    // Candidate slots past capacity + chunk stay empty for good.
+    for (int sl = lane; sl < kMaxSlots; sl += 64) {
+        pos[sl] = -1.f;
+        pri[sl] = 0.f;
+        key[sl] = 0;
+    }
+    // Token words of a chunk: lane j < chunk holds token first + j.
+    float tv = 0.f, td = 0.f, ts = 0.f;
+    auto fetch = [&](int c) {
+        const int t = c * a.chunk + lane;
+        tv = td = ts = 0.f;
+        if (lane < a.chunk && t < a.T) {
+            tv = ldf(a.valid, b, t);
+            td = ldf(a.docs, b, t);
+            if (!a.recency) ts = ldf(a.scores, b, t, h);
+        }
+    };
+    fetch(0);
     __syncthreads();
     for (int c = 0; c < a.nc; ++c) {
-        const int first = c * a.chunk, end = min(first + a.chunk, a.T);
+        const int first = c * a.chunk, end = min(first + a.chunk, a.T), n = end - first;
+        const float mv = tv, md = td, ms = ts;
+        if (c + 1 < a.nc) fetch(c + 1);
         // The document of the chunk's last PHYSICAL slot, padding included.
-        const float last_doc = ldf(a.docs, b, end - 1);
-        if (lane < a.cap) next[lane] = -1.f;
-        for (int s = lane; s < slots; s += 64) {
-            float p = -1.f;
-            if (s < a.cap) {
-                p = cache[s];
-            } else {
-                const int t = first + s - a.cap;
-                if (t < end) {
-                    if (a.expiry) a.expiry[token(a, b, t, h)] = (float)end;
-                    if (ldf(a.valid, b, t) >= 0.5f) p = (float)t;
-                }
-            }
-            float score = 0.f;
-            if (p >= 0.f) {
-                const int t = (int)p;
-                if (ldf(a.docs, b, t) == last_doc) score = a.recency ? p : ldf(a.scores, b, t, h);
-                else p = -1.f;
-            }
-            pos[s] = p;
-            pri[s] = score;
+        const float last_doc = readlane_f(md, n - 1);
+        if (lane < n && a.expiry) a.expiry[token(a, b, first + lane, h)] = (float)end;
+        // Candidates: the cache, then the chunk's valid tokens; only the last
+        // slot's document is eligible.
+        if (lane < a.cap) {
+            const float p = cpos[lane];
+            const bool ok = p >= 0.f && cdoc[lane] == last_doc;
+            pos[lane] = ok ? p : -1.f;
+            pri[lane] = cpri[lane];
+            sdoc[lane] = cdoc[lane];
+        }
+        if (lane < a.chunk) {
+            const int t = first + lane;
+            const bool ok = lane < n && mv >= 0.5f && md == last_doc;
+            pos[a.cap + lane] = ok ? (float)t : -1.f;
+            pri[a.cap + lane] = a.recency ? (float)t : ms;
+            sdoc[a.cap + lane] = md;
+        }
+        if (lane < a.cap) npos[lane] = -1.f;
+        __syncthreads();
+        // Ranking keys: the order-preserving bits of the score (or position)
+        // above the complemented position, so "beats" (higher key, ties to
+        // the earlier position) is one unsigned compare; empty and ineligible
+        // slots get key 0 and never beat.
+        for (int sl = lane; sl < a.cap + a.chunk; sl += 64) {
+            const float p = pos[sl];
+            const uint32_t u = __float_as_uint(pri[sl]);
+            const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+            key[sl] = p >= 0.f ? ((uint64_t)ord << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)p) : 0;
         }
         __syncthreads();
-        for (int s = lane; s < slots; s += 64) {
-            const float p = pos[s];
-            if (p < 0.f) continue;
-            const float sc = pri[s];
-            int rank = 0;
-            for (int o = 0; o < slots; ++o) {
-                const float po = pos[o];
-                if (po >= 0.f && (pri[o] > sc || (pri[o] == sc && po < p))) ++rank;
+        // Rank = number of eligible candidates that beat this one (higher key,
+        // then earlier position): an exact top-capacity with no sort.  Each
+        // lane ranks candidates lane and lane + 64 in one pass over the
+        // candidate list, read four at a time (empty slots never beat).
+        {
+            const int s1 = lane + 64;
+            const float p0 = pos[lane], c0 = pri[lane];
+            const float p1 = s1 < kMaxSlots ? pos[s1] : -1.f, c1 = s1 < kMaxSlots ? pri[s1] : 0.f;
+            const uint64_t k0 = key[lane], k1 = s1 < kMaxSlots ? key[s1] : 0;
+            int r0 = 0, r1 = 0;
+#pragma unroll 10
+            for (int o = 0; o < kMaxSlots; o += 2) {
+                const ulonglong2 ko = *reinterpret_cast<const ulonglong2 *>(&key[o]);
+                r0 += (ko.x > k0) + (ko.y > k0);
+                r1 += (ko.x > k1) + (ko.y > k1);
             }
-            if (rank < a.cap) next[rank] = p;
+            if (p0 >= 0.f && r0 < a.cap) {
+                npos[r0] = p0;
+                npri[r0] = c0;
+                ndoc[r0] = sdoc[lane];
+            }
+            if (p1 >= 0.f && r1 < a.cap) {
+                npos[r1] = p1;
+                npri[r1] = c1;
+                ndoc[r1] = sdoc[s1];
+            }
         }
         __syncthreads();
         if (lane < a.cap) {
-            const float p = next[lane];
-            cache[lane] = p;
+            const float p = npos[lane];
+            cpos[lane] = p;
+            cpri[lane] = npri[lane];
+            cdoc[lane] = ndoc[lane];
             sched[(int64_t)(c + 1) * a.cap + lane] = p;
             if (p >= 0.f && a.expiry)
                 a.expiry[token(a, b, (int)p, h)] = (float)min(end + a.chunk, a.T);
         }
         __syncthreads();
     }
-    if (a.final_positions && lane < a.cap) a.final_positions[(int64_t)bh * a.cap + lane] = cache[lane];
+    if (a.final_positions && lane < a.cap) a.final_positions[(int64_t)bh * a.cap + lane] = cpos[lane];
 }
 
 // ---- chunk slots ------------------------------------------------------------------
 
+// dst[j * LD + i] = x(b, pos_j, h, i) for rows j < MAXS (zero where j >= S,
+// pos_j < 0 or i >= w), by NT threads.  Loads go out 16 per thread at a time
+// before any is used, so a gather costs a few memory latencies rather than
+// one per row.
+template <int D, int LD, int MAXS, int NT = 64>
+__device__ __forceinline__ void gather_rows(const View &x, int b, int h, int w, const float *pos,
+                                            int S, float *dst) {
+    constexpr int PER = MAXS * D / NT, BATCH = 16;
+    static_assert(PER * NT == MAXS * D, "whole workgroups");
+    const int lane = threadIdx.x;
+    for (int n0 = 0; n0 < PER; n0 += BATCH) {
+        float r[BATCH];
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+            const int idx = lane + NT * (n0 + u), j = idx / D, i = idx % D;
+            r[u] = 0.f;
+            if (n0 + u < PER && j < S && i < w) {
+                const float p = pos[j];
+                if (p >= 0.f) r[u] = ldf(x, b, (int)p, h, i);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+            const int idx = lane + NT * (n0 + u), j = idx / D, i = idx % D;
+            if (n0 + u < PER) dst[j * LD + i] = r[u];
+        }
+    }
+}
+
 template <int DK, int DV>
 struct SlotTiles {
-    float K[kMaxSlots][DK + 1];  // +1: lanes reading different rows hit different banks
-    float V[kMaxSlots][DV];
+    // +1: lanes reading different rows of one column hit different banks
+    float K[kMaxSlots][DK + 1];
+    float V[kMaxSlots][DV + 1];
+    float Q[kMaxChunk][DK];
     float pos[kMaxSlots], doc[kMaxSlots];
+    float tpos[kMaxChunk], tval[kMaxChunk], tdoc[kMaxChunk];
 };
 
-// Slots of chunk c: the cache before the chunk, then the chunk's tokens.
-// Empty or invalid slots get position -1 and zero rows.
+// Slots of chunk c (the cache before the chunk, then the chunk's tokens; empty
+// or invalid slots get position -1 and zero rows), and the chunk's queries.
+constexpr int kReadWaves = 4;  // waves per chunk in the read and the query VJP
+constexpr int kReadThreads = 64 * kReadWaves;
+
 template <int DK, int DV>
 __device__ void stage_slots(const HolaArgs &a, int b, int h, int c, SlotTiles<DK, DV> &s) {
     const int lane = threadIdx.x, first = c * a.chunk, end = min(first + a.chunk, a.T);
     const int slots = a.cap + a.chunk;
     const float *sched = a.schedule + ((int64_t)(b * a.H + h) * (a.nc + 1) + c) * a.cap;
-    for (int j = lane; j < slots; j += 64) {
+    for (int j = lane; j < slots; j += kReadThreads) {
         float p = -1.f;
         if (j < a.cap) {
             p = sched[j];
@@ -181,19 +269,21 @@ __device__ void stage_slots(const HolaArgs &a, int b, int h, int c, SlotTiles<DK
         s.pos[j] = p;
         s.doc[j] = p >= 0.f ? ldf(a.docs, b, (int)p) : 0.f;
     }
-    __syncthreads();
-    for (int j = 0; j < slots; ++j) {
-        const float p = s.pos[j];
-        const int t = p >= 0.f ? (int)p : 0;
-        for (int i = lane; i < DK; i += 64)
-            s.K[j][i] = (p >= 0.f && i < a.dk) ? ldf(a.k, b, t, h, i) : 0.f;
-        for (int i = lane; i < DV; i += 64)
-            s.V[j][i] = (p >= 0.f && i < a.dv) ? ldf(a.v, b, t, h, i) : 0.f;
+    if (lane < kMaxChunk) {
+        const int t = first + lane;
+        const bool in = lane < a.chunk && t < end;
+        s.tpos[lane] = in ? (float)t : -1.f;
+        s.tval[lane] = in ? ldf(a.valid, b, t) : 0.f;
+        s.tdoc[lane] = in ? ldf(a.docs, b, t) : 0.f;
     }
+    __syncthreads();
+    gather_rows<DK, DK + 1, kMaxSlots, kReadThreads>(a.k, b, h, a.dk, s.pos, slots, &s.K[0][0]);
+    gather_rows<DV, DV + 1, kMaxSlots, kReadThreads>(a.v, b, h, a.dv, s.pos, slots, &s.V[0][0]);
+    gather_rows<DK, DK, kMaxChunk, kReadThreads>(a.q, b, h, a.dk, s.tpos, kMaxChunk, &s.Q[0][0]);
     __syncthreads();
 }
 
-// Logit of query (in LDS) against slot j, or -FLT_MAX when j is not visible.
+// Logit of query row qs against slot j, or -FLT_MAX when j is not visible.
 template <int DK, int DV>
 __device__ __forceinline__ bool slot_logit(const HolaArgs &a, const SlotTiles<DK, DV> &s,
                                            const float *qs, int j, bool active, int t, float doc,
@@ -209,20 +299,21 @@ __device__ __forceinline__ bool slot_logit(const HolaArgs &a, const SlotTiles<DK
 }
 
 template <int DK, int DV>
-__global__ void __launch_bounds__(64) hola_forward_kernel(HolaArgs a) {
+__global__ void __launch_bounds__(kReadThreads) hola_forward_kernel(HolaArgs a) {
     __shared__ SlotTiles<DK, DV> s;
-    __shared__ float P[kMaxSlots];
-    __shared__ float qs[DK];
-    const int lane = threadIdx.x;
+    __shared__ float Pw[kReadWaves][kMaxSlots];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = blockIdx.x % a.nc, bh = blockIdx.x / a.nc, b = bh / a.H, h = bh % a.H;
     const int first = c * a.chunk, end = min(first + a.chunk, a.T), slots = a.cap + a.chunk;
     stage_slots<DK, DV>(a, b, h, c, s);
     const float sink = ldf(a.sink, h);
-    for (int t = first; t < end; ++t) {
-        const bool active = ldf(a.valid, b, t) >= 0.5f;
-        const float doc = ldf(a.docs, b, t);
-        for (int i = lane; i < DK; i += 64) qs[i] = i < a.dk ? ldf(a.q, b, t, h, i) : 0.f;
-        __syncthreads();
+    float *P = Pw[wave];
+    // Each wave takes every fourth query of the chunk.
+    for (int t = first + wave; t < end; t += kReadWaves) {
+        const int tt = t - first;
+        const bool active = s.tval[tt] >= 0.5f;
+        const float doc = s.tdoc[tt];
+        const float *qs = s.Q[tt];
         float lg[2];
         bool vis[2];
         float m = sink;
@@ -239,7 +330,7 @@ __global__ void __launch_bounds__(64) hola_forward_kernel(HolaArgs a) {
         // Normalised before the value product: finite values cannot overflow.
         if (lane < slots) P[lane] = w0 * inv;
         if (lane + 64 < slots) P[lane + 64] = w1 * inv;
-        __syncthreads();
+        __builtin_amdgcn_wave_barrier();
         const int64_t tok = token(a, b, t, h);
         for (int j = lane; j < a.dv; j += 64) {
             float o = 0.f;
@@ -251,40 +342,61 @@ __global__ void __launch_bounds__(64) hola_forward_kernel(HolaArgs a) {
             a.stats[2 * tok] = m;
             a.stats[2 * tok + 1] = inv;
         }
-        __syncthreads();
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
 // ---- backward ---------------------------------------------------------------------
 
 template <int DK, int DV>
-__global__ void __launch_bounds__(64) hola_query_backward_kernel(HolaArgs a) {
+__global__ void __launch_bounds__(kReadThreads) hola_query_backward_kernel(HolaArgs a) {
     __shared__ SlotTiles<DK, DV> s;
-    __shared__ float D[kMaxSlots];
-    __shared__ float qs[DK], gs[DV];
-    const int lane = threadIdx.x;
+    __shared__ float Dw[kReadWaves][kMaxSlots];
+    __shared__ float G[kMaxChunk][DV], O[kMaxChunk][DV];
+    __shared__ float stat[kMaxChunk][2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = blockIdx.x % a.nc, bh = blockIdx.x / a.nc, b = bh / a.H, h = bh % a.H;
     const int first = c * a.chunk, end = min(first + a.chunk, a.T), slots = a.cap + a.chunk;
     stage_slots<DK, DV>(a, b, h, c, s);
-    const float sink = ldf(a.sink, h);
-    for (int t = first; t < end; ++t) {
-        const bool active = ldf(a.valid, b, t) >= 0.5f;
-        const float doc = ldf(a.docs, b, t);
-        const int64_t tok = token(a, b, t, h);
-        for (int i = lane; i < DK; i += 64) qs[i] = i < a.dk ? ldf(a.q, b, t, h, i) : 0.f;
-        float dl = 0.f;
-        for (int j = lane; j < DV; j += 64) {
-            const float g = (j < a.dv && a.dout.data) ? ldf(a.dout, b, t, h, j) : 0.f;
-            gs[j] = g;
-            if (active && j < a.dv) dl += g * a.fwd_out[tok * a.dv + j];
+    // The chunk's output adjoints, forward outputs and softmax statistics.
+    {
+        constexpr int PER = kMaxChunk * DV / kReadThreads;
+#pragma unroll
+        for (int n = 0; n < PER; ++n) {
+            const int idx = tid + kReadThreads * n, tt = idx / DV, j = idx % DV, t = first + tt;
+            float g = 0.f, o = 0.f;
+            if (tt < end - first && j < a.dv) {
+                const int64_t tok = token(a, b, t, h);
+                if (a.dout.data) g = ldf(a.dout, b, t, h, j);
+                o = a.fwd_out[tok * a.dv + j];
+            }
+            G[tt][j] = g;
+            O[tt][j] = o;
         }
+        if (tid < 2 * kMaxChunk) {
+            const int tt = tid >> 1, t = first + tt;
+            stat[tt][tid & 1] = tt < end - first ? a.stats[2 * token(a, b, t, h) + (tid & 1)] : 0.f;
+        }
+    }
+    __syncthreads();
+    const float sink = ldf(a.sink, h);
+    float *D = Dw[wave];
+    // Each wave takes every fourth query of the chunk.
+    for (int t = first + wave; t < end; t += kReadWaves) {
+        const int tt = t - first;
+        const bool active = s.tval[tt] >= 0.5f;
+        const float doc = s.tdoc[tt];
+        const int64_t tok = token(a, b, t, h);
+        const float *qs = s.Q[tt], *gs = G[tt];
+        float dl = 0.f;
+        for (int j = lane; j < DV; j += 64)
+            if (active) dl += gs[j] * O[tt][j];
         const float delta = wave_sum(dl);
-        const float m = a.stats[2 * tok], inv = a.stats[2 * tok + 1];
+        const float m = stat[tt][0], inv = stat[tt][1];
         if (lane == 0) {
             a.aux[2 * tok] = delta;
             a.aux[2 * tok + 1] = active ? -delta * expf(sink - m) * inv : 0.f;
         }
-        __syncthreads();
         for (int j = lane; j < slots; j += 64) {
             float lg, p = 0.f, d = 0.f;
             if (slot_logit<DK, DV>(a, s, qs, j, active, t, doc, lg)) {
@@ -295,18 +407,16 @@ __global__ void __launch_bounds__(64) hola_query_backward_kernel(HolaArgs a) {
                 d = p * (dot - delta) * a.scale;
             }
             D[j] = d;
-            float *pr = a.pairs + (tok * slots + j) * 2;
-            pr[0] = p;
-            pr[1] = d;
+            reinterpret_cast<float2 *>(a.pairs)[tok * slots + j] = make_float2(p, d);
         }
-        __syncthreads();
+        __builtin_amdgcn_wave_barrier();
         for (int i = lane; i < a.dk; i += 64) {
             float g = 0.f;
             if (active)
                 for (int j = 0; j < slots; ++j) g += D[j] * s.K[j][i];
             a.gq[tok * a.dk + i] = g;
         }
-        __syncthreads();
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -314,6 +424,9 @@ template <int DK, int DV>
 __global__ void __launch_bounds__(64) hola_key_backward_kernel(HolaArgs a) {
     constexpr int RK = (DK + 63) / 64, RV = (DV + 63) / 64;
     __shared__ int map[kMaxChunk];
+    __shared__ float Q[kMaxChunk][DK], G[kMaxChunk][DV];
+    __shared__ float2 PD[kMaxChunk][kMaxChunk];  // (probability, logit gradient) [query][key]
+    __shared__ float qpos[kMaxChunk];
     const int lane = threadIdx.x;
     const int c = blockIdx.x % a.nc, bh = blockIdx.x / a.nc, b = bh / a.H, h = bh % a.H;
     const int first = c * a.chunk, end = min(first + a.chunk, a.T), n = end - first;
@@ -328,10 +441,16 @@ __global__ void __launch_bounds__(64) hola_key_backward_kernel(HolaArgs a) {
         for (int r = 0; r < RV; ++r) dva[j][r] = 0.f;
     }
     // Queries that can see a key of this chunk end at its expiry.
-    int last = end;
-    for (int j = 0; j < n; ++j) last = max(last, (int)a.expiry[token(a, b, first + j, h)]);
+    float lastf = (float)end;
+    if (lane < n) lastf = fmaxf(lastf, a.expiry[token(a, b, first + lane, h)]);
+    const int last = (int)wave_max(lastf);
     for (int cq = c; cq * a.chunk < last; ++cq) {
-        if (lane < kMaxChunk) map[lane] = -1;
+        const int q0 = cq * a.chunk, q1 = min(q0 + a.chunk, a.T), nq = q1 - q0;
+        // Where this chunk's keys sit among the slots of query chunk cq.
+        if (lane < kMaxChunk) {
+            map[lane] = -1;
+            qpos[lane] = lane < nq ? (float)(q0 + lane) : -1.f;
+        }
         __syncthreads();
         if (cq == c) {
             if (lane < n) map[lane] = a.cap + lane;
@@ -340,32 +459,42 @@ __global__ void __launch_bounds__(64) hola_key_backward_kernel(HolaArgs a) {
             if (p >= (float)first && p < (float)end) map[(int)p - first] = lane;
         }
         __syncthreads();
-        int sl[kMaxChunk];
+        // The chunk's queries, output adjoints and the pairs of the mapped slots.
+        gather_rows<DK, DK, kMaxChunk>(a.q, b, h, a.dk, qpos, kMaxChunk, &Q[0][0]);
+        if (a.dout.data) gather_rows<DV, DV, kMaxChunk>(a.dout, b, h, a.dv, qpos, kMaxChunk, &G[0][0]);
+        else
+            for (int idx = lane; idx < kMaxChunk * DV; idx += 64) G[idx / DV][idx % DV] = 0.f;
+        {
+            constexpr int PER = kMaxChunk * kMaxChunk / 64;
+            float2 r[PER];
 #pragma unroll
-        for (int j = 0; j < kMaxChunk; ++j) sl[j] = j < n ? map[j] : -1;
-        const int t1 = min(cq * a.chunk + a.chunk, a.T);
-        for (int t = cq * a.chunk; t < t1; ++t) {
-            const int64_t tok = token(a, b, t, h);
+            for (int u = 0; u < PER; ++u) {
+                const int idx = lane + 64 * u, tq = idx / kMaxChunk, j = idx % kMaxChunk;
+                const int sl = map[j];
+                r[u] = make_float2(0.f, 0.f);
+                if (tq < nq && sl >= 0)
+                    r[u] = reinterpret_cast<const float2 *>(a.pairs)[token(a, b, q0 + tq, h) * slots + sl];
+            }
+#pragma unroll
+            for (int u = 0; u < PER; ++u) {
+                const int idx = lane + 64 * u;
+                PD[idx / kMaxChunk][idx % kMaxChunk] = r[u];
+            }
+        }
+        __syncthreads();
+        for (int tq = 0; tq < nq; ++tq) {
             float qv[RK], gv[RV];
 #pragma unroll
-            for (int r = 0; r < RK; ++r) {
-                const int i = lane + 64 * r;
-                qv[r] = i < a.dk ? ldf(a.q, b, t, h, i) : 0.f;
-            }
+            for (int r = 0; r < RK; ++r) qv[r] = lane + 64 * r < DK ? Q[tq][lane + 64 * r] : 0.f;
 #pragma unroll
-            for (int r = 0; r < RV; ++r) {
-                const int i = lane + 64 * r;
-                gv[r] = (i < a.dv && a.dout.data) ? ldf(a.dout, b, t, h, i) : 0.f;
-            }
-            const float *pr = a.pairs + tok * slots * 2;
+            for (int r = 0; r < RV; ++r) gv[r] = lane + 64 * r < DV ? G[tq][lane + 64 * r] : 0.f;
 #pragma unroll
             for (int j = 0; j < kMaxChunk; ++j) {
-                if (sl[j] < 0) continue;
-                const float p = pr[2 * sl[j]], d = pr[2 * sl[j] + 1];
+                const float2 pd = PD[tq][j];
 #pragma unroll
-                for (int r = 0; r < RK; ++r) dka[j][r] += d * qv[r];
+                for (int r = 0; r < RK; ++r) dka[j][r] += pd.y * qv[r];
 #pragma unroll
-                for (int r = 0; r < RV; ++r) dva[j][r] += p * gv[r];
+                for (int r = 0; r < RV; ++r) dva[j][r] += pd.x * gv[r];
             }
         }
         __syncthreads();
@@ -413,7 +542,7 @@ void launch_widths(const HolaArgs &a, dim3 grid, hipStream_t st) {
     const int kp = pad_width(a.dk), vp = pad_width(a.dv);
 #define GDN2_HOLA_CASE(P, Q)                                                    \
     if (kp == P && vp == Q) {                                                   \
-        hipLaunchKernelGGL((K<P, Q>::fn), grid, dim3(64), 0, st, a);            \
+        hipLaunchKernelGGL((K<P, Q>::fn), grid, dim3(K<P, Q>::threads), 0, st, a); \
         return;                                                                 \
     }
     GDN2_HOLA_CASE(32, 32) GDN2_HOLA_CASE(32, 64) GDN2_HOLA_CASE(32, 128)
@@ -421,9 +550,18 @@ void launch_widths(const HolaArgs &a, dim3 grid, hipStream_t st) {
     GDN2_HOLA_CASE(128, 32) GDN2_HOLA_CASE(128, 64) GDN2_HOLA_CASE(128, 128)
 #undef GDN2_HOLA_CASE
 }
-template <int P, int Q> struct Fwd { static constexpr auto fn = hola_forward_kernel<P, Q>; };
-template <int P, int Q> struct QBwd { static constexpr auto fn = hola_query_backward_kernel<P, Q>; };
-template <int P, int Q> struct KBwd { static constexpr auto fn = hola_key_backward_kernel<P, Q>; };
+template <int P, int Q> struct Fwd {
+    static constexpr auto fn = hola_forward_kernel<P, Q>;
+    static constexpr int threads = kReadThreads;
+};
+template <int P, int Q> struct QBwd {
+    static constexpr auto fn = hola_query_backward_kernel<P, Q>;
+    static constexpr int threads = kReadThreads;
+};
+template <int P, int Q> struct KBwd {
+    static constexpr auto fn = hola_key_backward_kernel<P, Q>;
+    static constexpr int threads = 64;
+};
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
