@@ -209,11 +209,20 @@ __global__ void __launch_bounds__(64) hola_schedule_kernel(HolaArgs a) {
 
 // ---- chunk slots ------------------------------------------------------------------
 
+constexpr int kReadWaves = 4;  // waves per chunk in the read and the query VJP
+constexpr int kReadThreads = 64 * kReadWaves;
+constexpr int kWaveQueries = kMaxChunk / kReadWaves;
+
+// Query tt of a chunk is handled by wave tt % 4 as its (tt / 4)-th query;
+// transposed query tiles keep each wave's four queries of one channel in one
+// 16-byte group.
+__device__ __forceinline__ int query_slot(int tt) { return ((tt & 3) << 2) | (tt >> 2); }
+
 // dst[j * LD + i] = x(b, pos_j, h, i) for rows j < MAXS (zero where j >= S,
 // pos_j < 0 or i >= w), by NT threads.  Loads go out 16 per thread at a time
 // before any is used, so a gather costs a few memory latencies rather than
 // one per row.
-template <int D, int LD, int MAXS, int NT = 64>
+template <int D, int LD, int MAXS, int NT = 64, bool TQ = false>
 __device__ __forceinline__ void gather_rows(const View &x, int b, int h, int w, const float *pos,
                                             int S, float *dst) {
     constexpr int PER = MAXS * D / NT, BATCH = 16;
@@ -233,7 +242,10 @@ __device__ __forceinline__ void gather_rows(const View &x, int b, int h, int w, 
 #pragma unroll
         for (int u = 0; u < BATCH; ++u) {
             const int idx = lane + NT * (n0 + u), j = idx / D, i = idx % D;
-            if (n0 + u < PER) dst[j * LD + i] = r[u];
+            if (n0 + u < PER) {
+                if (TQ) dst[i * MAXS + query_slot(j)] = r[u];
+                else dst[j * LD + i] = r[u];
+            }
         }
     }
 }
@@ -243,16 +255,13 @@ struct SlotTiles {
     // +1: lanes reading different rows of one column hit different banks
     float K[kMaxSlots][DK + 1];
     float V[kMaxSlots][DV + 1];
-    float Q[kMaxChunk][DK];
+    float QT[DK][kMaxChunk] __attribute__((aligned(16)));  // [channel][query_slot(tt)]
     float pos[kMaxSlots], doc[kMaxSlots];
     float tpos[kMaxChunk], tval[kMaxChunk], tdoc[kMaxChunk];
 };
 
 // Slots of chunk c (the cache before the chunk, then the chunk's tokens; empty
 // or invalid slots get position -1 and zero rows), and the chunk's queries.
-constexpr int kReadWaves = 4;  // waves per chunk in the read and the query VJP
-constexpr int kReadThreads = 64 * kReadWaves;
-
 template <int DK, int DV>
 __device__ void stage_slots(const HolaArgs &a, int b, int h, int c, SlotTiles<DK, DV> &s) {
     const int lane = threadIdx.x, first = c * a.chunk, end = min(first + a.chunk, a.T);
@@ -279,70 +288,116 @@ __device__ void stage_slots(const HolaArgs &a, int b, int h, int c, SlotTiles<DK
     __syncthreads();
     gather_rows<DK, DK + 1, kMaxSlots, kReadThreads>(a.k, b, h, a.dk, s.pos, slots, &s.K[0][0]);
     gather_rows<DV, DV + 1, kMaxSlots, kReadThreads>(a.v, b, h, a.dv, s.pos, slots, &s.V[0][0]);
-    gather_rows<DK, DK, kMaxChunk, kReadThreads>(a.q, b, h, a.dk, s.tpos, kMaxChunk, &s.Q[0][0]);
+    gather_rows<DK, DK, kMaxChunk, kReadThreads, true>(a.q, b, h, a.dk, s.tpos, kMaxChunk,
+                                                      &s.QT[0][0]);
     __syncthreads();
 }
 
-// Logit of query row qs against slot j, or -FLT_MAX when j is not visible.
+// The four queries of a wave (tt = wave + 4u): token, activity, document.
+struct WaveQueries {
+    int t[kWaveQueries];
+    bool on[kWaveQueries], act[kWaveQueries];
+    float doc[kWaveQueries];
+};
+
 template <int DK, int DV>
-__device__ __forceinline__ bool slot_logit(const HolaArgs &a, const SlotTiles<DK, DV> &s,
-                                           const float *qs, int j, bool active, int t, float doc,
-                                           float &logit) {
-    logit = -FLT_MAX;
-    const float p = s.pos[j];
-    if (!(active && p >= 0.f && p <= (float)t && s.doc[j] == doc)) return false;
-    float d = 0.f;
+__device__ __forceinline__ WaveQueries wave_queries(const SlotTiles<DK, DV> &s, int wave, int first,
+                                                    int n) {
+    WaveQueries w;
+#pragma unroll
+    for (int u = 0; u < kWaveQueries; ++u) {
+        const int tt = wave + kReadWaves * u;
+        w.t[u] = first + tt;
+        w.on[u] = tt < n;
+        w.act[u] = tt < n && s.tval[tt] >= 0.5f;
+        w.doc[u] = tt < n ? s.tdoc[tt] : 0.f;
+    }
+    return w;
+}
+
+// Scaled logits of the wave's queries against slot j (-FLT_MAX where the slot
+// is not visible: empty, later than the query, another document, or an
+// inactive query).  One K read and one 16-byte query read per channel.
+template <int DK, int DV>
+__device__ __forceinline__ void wave_logits(const HolaArgs &a, const SlotTiles<DK, DV> &s,
+                                            const WaveQueries &w, int wave, int j,
+                                            float (&lg)[kWaveQueries]) {
+    float acc[kWaveQueries] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
-    for (int i = 0; i < DK; ++i) d += qs[i] * s.K[j][i];
-    logit = d * a.scale;
-    return true;
+    for (int i = 0; i < DK; ++i) {
+        const float kv = s.K[j][i];
+        const float4 q4 = *reinterpret_cast<const float4 *>(&s.QT[i][4 * wave]);
+        acc[0] += q4.x * kv;
+        acc[1] += q4.y * kv;
+        acc[2] += q4.z * kv;
+        acc[3] += q4.w * kv;
+    }
+    const float p = s.pos[j], d = s.doc[j];
+#pragma unroll
+    for (int u = 0; u < kWaveQueries; ++u) {
+        const bool vis = w.act[u] && p >= 0.f && p <= (float)w.t[u] && d == w.doc[u];
+        lg[u] = vis ? acc[u] * a.scale : -FLT_MAX;
+    }
 }
 
 template <int DK, int DV>
 __global__ void __launch_bounds__(kReadThreads) hola_forward_kernel(HolaArgs a) {
     __shared__ SlotTiles<DK, DV> s;
-    __shared__ float Pw[kReadWaves][kMaxSlots];
+    __shared__ float4 PT[kReadWaves][kMaxSlots];  // normalised probabilities, [slot][query]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = blockIdx.x % a.nc, bh = blockIdx.x / a.nc, b = bh / a.H, h = bh % a.H;
     const int first = c * a.chunk, end = min(first + a.chunk, a.T), slots = a.cap + a.chunk;
     stage_slots<DK, DV>(a, b, h, c, s);
     const float sink = ldf(a.sink, h);
-    float *P = Pw[wave];
-    // Each wave takes every fourth query of the chunk.
-    for (int t = first + wave; t < end; t += kReadWaves) {
-        const int tt = t - first;
-        const bool active = s.tval[tt] >= 0.5f;
-        const float doc = s.tdoc[tt];
-        const float *qs = s.Q[tt];
-        float lg[2];
-        bool vis[2];
-        float m = sink;
+    const WaveQueries w = wave_queries(s, wave, first, end - first);
+    float lg[2][kWaveQueries];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int j = lane + 64 * r;
-            vis[r] = j < slots && slot_logit<DK, DV>(a, s, qs, j, active, t, doc, lg[r]);
-            if (vis[r]) m = fmaxf(m, lg[r]);
-        }
-        m = wave_max(m);
-        const float w0 = vis[0] ? expf(lg[0] - m) : 0.f;
-        const float w1 = vis[1] ? expf(lg[1] - m) : 0.f;
-        const float inv = 1.f / (wave_sum(w0 + w1) + expf(sink - m));
+    for (int r = 0; r < 2; ++r) {
+        const int j = lane + 64 * r;
+        if (j < slots) wave_logits(a, s, w, wave, j, lg[r]);
+        else
+            for (int u = 0; u < kWaveQueries; ++u) lg[r][u] = -FLT_MAX;
+    }
+    float m[kWaveQueries], inv[kWaveQueries], p0[kWaveQueries], p1[kWaveQueries];
+#pragma unroll
+    for (int u = 0; u < kWaveQueries; ++u) m[u] = wave_max(fmaxf(sink, fmaxf(lg[0][u], lg[1][u])));
+#pragma unroll
+    for (int u = 0; u < kWaveQueries; ++u) {
+        p0[u] = lg[0][u] > -FLT_MAX ? expf(lg[0][u] - m[u]) : 0.f;
+        p1[u] = lg[1][u] > -FLT_MAX ? expf(lg[1][u] - m[u]) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kWaveQueries; ++u) {
+        inv[u] = 1.f / (wave_sum(p0[u] + p1[u]) + expf(sink - m[u]));
         // Normalised before the value product: finite values cannot overflow.
-        if (lane < slots) P[lane] = w0 * inv;
-        if (lane + 64 < slots) P[lane + 64] = w1 * inv;
-        __builtin_amdgcn_wave_barrier();
-        const int64_t tok = token(a, b, t, h);
-        for (int j = lane; j < a.dv; j += 64) {
-            float o = 0.f;
-            if (active)
-                for (int k = 0; k < slots; ++k) o += P[k] * s.V[k][j];
-            a.out[tok * a.dv + j] = o;
+        p0[u] *= inv[u];
+        p1[u] *= inv[u];
+    }
+    if (lane < slots) PT[wave][lane] = make_float4(p0[0], p0[1], p0[2], p0[3]);
+    if (lane + 64 < slots) PT[wave][lane + 64] = make_float4(p1[0], p1[1], p1[2], p1[3]);
+    __builtin_amdgcn_wave_barrier();
+    for (int j = lane; j < a.dv; j += 64) {
+        float o[kWaveQueries] = {0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < slots; ++k) {
+            const float vv = s.V[k][j];
+            const float4 p4 = PT[wave][k];
+            o[0] += p4.x * vv;
+            o[1] += p4.y * vv;
+            o[2] += p4.z * vv;
+            o[3] += p4.w * vv;
         }
-        if (lane == 0) {
-            a.stats[2 * tok] = m;
-            a.stats[2 * tok + 1] = inv;
+#pragma unroll
+        for (int u = 0; u < kWaveQueries; ++u)
+            if (w.on[u]) a.out[token(a, b, w.t[u], h) * a.dv + j] = w.act[u] ? o[u] : 0.f;
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int u = 0; u < kWaveQueries; ++u) {
+            if (!w.on[u]) continue;
+            const int64_t tok = token(a, b, w.t[u], h);
+            a.stats[2 * tok] = m[u];
+            a.stats[2 * tok + 1] = inv[u];
         }
-        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -351,27 +406,33 @@ __global__ void __launch_bounds__(kReadThreads) hola_forward_kernel(HolaArgs a) 
 template <int DK, int DV>
 __global__ void __launch_bounds__(kReadThreads) hola_query_backward_kernel(HolaArgs a) {
     __shared__ SlotTiles<DK, DV> s;
-    __shared__ float Dw[kReadWaves][kMaxSlots];
-    __shared__ float G[kMaxChunk][DV], O[kMaxChunk][DV];
+    __shared__ float4 DT[kReadWaves][kMaxSlots];  // logit gradients, [slot][query]
+    __shared__ float GT[DV][kMaxChunk] __attribute__((aligned(16)));  // dO, [channel][query_slot]
+    __shared__ float O[kMaxChunk][DV + 1];
     __shared__ float stat[kMaxChunk][2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = blockIdx.x % a.nc, bh = blockIdx.x / a.nc, b = bh / a.H, h = bh % a.H;
     const int first = c * a.chunk, end = min(first + a.chunk, a.T), slots = a.cap + a.chunk;
     stage_slots<DK, DV>(a, b, h, c, s);
-    // The chunk's output adjoints, forward outputs and softmax statistics.
+    // The chunk's output adjoints (transposed), forward outputs and softmax
+    // statistics.
     {
         constexpr int PER = kMaxChunk * DV / kReadThreads;
+        float g[PER], o[PER];
 #pragma unroll
         for (int n = 0; n < PER; ++n) {
             const int idx = tid + kReadThreads * n, tt = idx / DV, j = idx % DV, t = first + tt;
-            float g = 0.f, o = 0.f;
+            g[n] = o[n] = 0.f;
             if (tt < end - first && j < a.dv) {
-                const int64_t tok = token(a, b, t, h);
-                if (a.dout.data) g = ldf(a.dout, b, t, h, j);
-                o = a.fwd_out[tok * a.dv + j];
+                if (a.dout.data) g[n] = ldf(a.dout, b, t, h, j);
+                o[n] = a.fwd_out[token(a, b, t, h) * a.dv + j];
             }
-            G[tt][j] = g;
-            O[tt][j] = o;
+        }
+#pragma unroll
+        for (int n = 0; n < PER; ++n) {
+            const int idx = tid + kReadThreads * n, tt = idx / DV, j = idx % DV;
+            GT[j][query_slot(tt)] = g[n];
+            O[tt][j] = o[n];
         }
         if (tid < 2 * kMaxChunk) {
             const int tt = tid >> 1, t = first + tt;
@@ -380,43 +441,64 @@ __global__ void __launch_bounds__(kReadThreads) hola_query_backward_kernel(HolaA
     }
     __syncthreads();
     const float sink = ldf(a.sink, h);
-    float *D = Dw[wave];
-    // Each wave takes every fourth query of the chunk.
-    for (int t = first + wave; t < end; t += kReadWaves) {
-        const int tt = t - first;
-        const bool active = s.tval[tt] >= 0.5f;
-        const float doc = s.tdoc[tt];
-        const int64_t tok = token(a, b, t, h);
-        const float *qs = s.Q[tt], *gs = G[tt];
+    const WaveQueries w = wave_queries(s, wave, first, end - first);
+    float delta[kWaveQueries], m[kWaveQueries], inv[kWaveQueries];
+#pragma unroll
+    for (int u = 0; u < kWaveQueries; ++u) {
+        const int tt = wave + kReadWaves * u;
         float dl = 0.f;
-        for (int j = lane; j < DV; j += 64)
-            if (active) dl += gs[j] * O[tt][j];
-        const float delta = wave_sum(dl);
-        const float m = stat[tt][0], inv = stat[tt][1];
-        if (lane == 0) {
-            a.aux[2 * tok] = delta;
-            a.aux[2 * tok + 1] = active ? -delta * expf(sink - m) * inv : 0.f;
+        if (w.act[u])
+            for (int j = lane; j < DV; j += 64) dl += GT[j][query_slot(tt)] * O[tt][j];
+        delta[u] = wave_sum(dl);
+        m[u] = w.on[u] ? stat[tt][0] : 0.f;
+        inv[u] = w.on[u] ? stat[tt][1] : 0.f;
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int u = 0; u < kWaveQueries; ++u) {
+            if (!w.on[u]) continue;
+            const int64_t tok = token(a, b, w.t[u], h);
+            a.aux[2 * tok] = delta[u];
+            a.aux[2 * tok + 1] = w.act[u] ? -delta[u] * expf(sink - m[u]) * inv[u] : 0.f;
         }
-        for (int j = lane; j < slots; j += 64) {
-            float lg, p = 0.f, d = 0.f;
-            if (slot_logit<DK, DV>(a, s, qs, j, active, t, doc, lg)) {
-                p = expf(lg - m) * inv;
-                float dot = 0.f;
+    }
+    for (int j = lane; j < slots; j += 64) {
+        float lg[kWaveQueries], dot[kWaveQueries] = {0.f, 0.f, 0.f, 0.f};
+        wave_logits(a, s, w, wave, j, lg);
 #pragma unroll 8
-                for (int i = 0; i < DV; ++i) dot += gs[i] * s.V[j][i];
-                d = p * (dot - delta) * a.scale;
-            }
-            D[j] = d;
-            reinterpret_cast<float2 *>(a.pairs)[tok * slots + j] = make_float2(p, d);
+        for (int i = 0; i < DV; ++i) {
+            const float vv = s.V[j][i];
+            const float4 g4 = *reinterpret_cast<const float4 *>(&GT[i][4 * wave]);
+            dot[0] += g4.x * vv;
+            dot[1] += g4.y * vv;
+            dot[2] += g4.z * vv;
+            dot[3] += g4.w * vv;
         }
-        __builtin_amdgcn_wave_barrier();
-        for (int i = lane; i < a.dk; i += 64) {
-            float g = 0.f;
-            if (active)
-                for (int j = 0; j < slots; ++j) g += D[j] * s.K[j][i];
-            a.gq[tok * a.dk + i] = g;
+        float d[kWaveQueries];
+#pragma unroll
+        for (int u = 0; u < kWaveQueries; ++u) {
+            const float p = lg[u] > -FLT_MAX ? expf(lg[u] - m[u]) * inv[u] : 0.f;
+            d[u] = lg[u] > -FLT_MAX ? p * (dot[u] - delta[u]) * a.scale : 0.f;
+            if (w.on[u])
+                reinterpret_cast<float2 *>(a.pairs)[token(a, b, w.t[u], h) * slots + j] =
+                    make_float2(p, d[u]);
         }
-        __builtin_amdgcn_wave_barrier();
+        DT[wave][j] = make_float4(d[0], d[1], d[2], d[3]);
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (int i = lane; i < a.dk; i += 64) {
+        float g[kWaveQueries] = {0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < slots; ++j) {
+            const float kv = s.K[j][i];
+            const float4 d4 = DT[wave][j];
+            g[0] += d4.x * kv;
+            g[1] += d4.y * kv;
+            g[2] += d4.z * kv;
+            g[3] += d4.w * kv;
+        }
+#pragma unroll
+        for (int u = 0; u < kWaveQueries; ++u)
+            if (w.on[u]) a.gq[token(a, b, w.t[u], h) * a.dk + i] = w.act[u] ? g[u] : 0.f;
     }
 }
 
