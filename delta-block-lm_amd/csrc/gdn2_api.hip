@@ -539,7 +539,7 @@ int gdn2_decode_step(const gdn2_shape *shape, const gdn2_view *q, const gdn2_vie
     a.out_bf16 = output_dtype == GDN2_BF16;
     a.scores = scores;
     seq_bind_checkpoint(a, nullptr);
-    return launch_status(launch_seq_fwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
+    return launch_status(launch_seq_decode(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
                          "gdn2_decode_step");
 }
 

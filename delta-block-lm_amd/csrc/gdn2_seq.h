@@ -64,6 +64,8 @@ inline void seq_bind_checkpoint(SeqArgs &a, const void *ck) {
 }
 
 hipError_t launch_seq_fwd(const SeqArgs &a, bool in_bf16, hipStream_t stream);
+// One token (T == 1, masks only) on a carried state; no checkpoint.
+hipError_t launch_seq_decode(const SeqArgs &a, bool in_bf16, hipStream_t stream);
 hipError_t launch_seq_bwd(const SeqArgs &a, bool in_bf16, hipStream_t stream);
 
 }  // namespace gdn2

@@ -77,15 +77,34 @@ __device__ __forceinline__ float swap32_sum(float x) {
     return pair_sum(r0, r1);
 }
 
+// x[l ^ 4]: the half-row mirror (l -> 7 - l) followed by a reversed quad.
+__device__ __forceinline__ float xor4(float x) {
+    const int m = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, m, 0x1B, 0xF, 0xF, false));
+}
+
 // Sum over the lanes of a wave congruent to this lane modulo S (S = 4 or 8),
-// in all of them: row rotations by 4 (S = 4) and 8 within each 16-lane row,
-// then the four rows combined with permlane swaps.
+// in all of them, as a balanced pairwise tree over the lane index (lane ^ 4
+// for S = 4, then lane ^ 8 by a half-row rotation, then permlane swaps for
+// lane ^ 16 and lane ^ 32).  Every step pairs two lanes symmetrically, so all
+// the lanes of a group get bit-identical sums.
 template <int S>
 __device__ __forceinline__ float stride_sum(float x) {
     static_assert(S == 4 || S == 8, "stride");
-    if (S == 4) x = dpp_add<0x124>(x);  // row_ror 4
-    x = dpp_add<0x128>(x);              // row_ror 8
+    if (S == 4) x = x + xor4(x);
+    x = dpp_add<0x128>(x);  // row_ror 8 == lane ^ 8
     return swap32_sum(swap16_sum(x));
+}
+
+// Balanced pairwise sum of p[0..N) in index order: the order in which the
+// lane trees above combine row groups (pairs g ^ 1, then g ^ 2, ...).
+template <int N>
+__device__ __forceinline__ float tree_sum(float (&p)[N]) {
+#pragma unroll
+    for (int w = 1; w < N; w *= 2)
+#pragma unroll
+        for (int i = 0; i < N; i += 2 * w) p[i] = p[i] + p[i + w];
+    return p[0];
 }
 
 template <int N>
@@ -449,15 +468,22 @@ __global__ void __launch_bounds__(4 * VP) seq_fwd_kernel(SeqArgs a) {
             lds_put<CL>(&s.o[tt][c0], o);
             lds_put<CL>(&s.d[tt][c0], delta);
         };
-        // All SEQ_CT tokens straight-line (tokens past the sequence are staged
-        // as padding), two operand sets in turn so the next token's LDS reads
-        // overlap this one.
-        FwdTok<RL, CL> x[2];
-        fetch_fwd<KP, VP, RL, CL>(B, 0, r0, c0, x[0]);
+        if (nt == CT) {
+            // A full block: straight-line code, two operand sets in turn so the
+            // next token's LDS reads overlap this one.
+            FwdTok<RL, CL> x[2];
+            fetch_fwd<KP, VP, RL, CL>(B, 0, r0, c0, x[0]);
 #pragma unroll
-        for (int tt = 0; tt < CT; ++tt) {
-            if (tt + 1 < CT) fetch_fwd<KP, VP, RL, CL>(B, tt + 1, r0, c0, x[(tt + 1) & 1]);
-            step(tt, x[tt & 1]);
+            for (int tt = 0; tt < CT; ++tt) {
+                if (tt + 1 < CT) fetch_fwd<KP, VP, RL, CL>(B, tt + 1, r0, c0, x[(tt + 1) & 1]);
+                step(tt, x[tt & 1]);
+            }
+        } else {  // the sequence's last, partial block (and decode steps)
+            for (int tt = 0; tt < nt; ++tt) {
+                FwdTok<RL, CL> x;
+                fetch_fwd<KP, VP, RL, CL>(B, tt, r0, c0, x);
+                step(tt, x);
+            }
         }
         __syncthreads();
         // Stage the next block first: its loads are the oldest memory
@@ -864,6 +890,113 @@ __global__ void __launch_bounds__((SeqBwdCfg<KP, VP>::NT)) seq_bwd_kernel(SeqArg
 }
 #pragma clang fp contract(on)
 
+// ---- decode ----------------------------------------------------------------------
+
+// One token on a carried state (T == 1): thread j owns value column j with
+// all its key rows in registers, so the state is read and written once,
+// coalesced across the columns.  Every sum follows the forward kernel's order
+// (per row group two interleaved chains, then the balanced tree over row
+// groups; the score norms as the forward's 16-lane trees), so a decode step
+// is bit-identical to a one-token scan.
+template <int KP, int VP, typename TIN>
+__global__ void __launch_bounds__(VP < 64 ? 64 : VP) seq_decode_kernel(SeqArgs a) {
+    using L = FwdLayout<KP>;
+    constexpr int NTD = VP < 64 ? 64 : VP, RGN = L::RGN, RL = L::RL;
+    __shared__ float sq[KP], sk[KP], sa[KP], sek[KP], sd[VP];
+    const int j = threadIdx.x, bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
+    const TokenSrc src = make_src<TIN>(a, b, h);
+    const bool jin = j < a.V;
+    float S[KP];
+#pragma unroll
+    for (int i = 0; i < KP; ++i)
+        S[i] = (jin && i < a.K && a.initial.data) ? ld4<float>(a.initial, b, h, i, j) : 0.f;
+    const float val = src.f0.p ? __uint_as_float(ld_s<float>(src.f0, 0, 0)) : 1.f;
+    const float rst = src.f1.p ? __uint_as_float(ld_s<float>(src.f1, 0, 0)) : 0.f;
+    const bool on = val != 0.f;
+    // Operands staged as the forward stages them: padding folds to a = 1 and
+    // zero q, k, e.k, w.v; a reset to a = 0.
+    for (int i = j; i < KP; i += NTD) {
+        float qf = 0.f, kf = 0.f, af = 0.f, ef = 0.f;
+        if (i < a.K) {
+            qf = raw_f<TIN>(ld_s<TIN>(src.q, 0, i));
+            kf = raw_f<TIN>(ld_s<TIN>(src.k, 0, i));
+            const float g = __uint_as_float(ld_s<float>(src.a, 0, i));
+            af = a.scalar ? expf(g) : g;
+            ef = __uint_as_float(ld_s<float>(src.e, 0, i));
+        } else if (a.scalar) {
+            af = 0.f;
+        }
+        sq[i] = on ? qf : 0.f;
+        sk[i] = on ? kf : 0.f;
+        sa[i] = on ? (rst != 0.f ? 0.f : af) : 1.f;
+        sek[i] = on ? ef * kf : 0.f;
+    }
+    float wv = 0.f;
+    if (jin && on) wv = __uint_as_float(ld_s<float>(src.w, 0, j)) * raw_f<TIN>(ld_s<TIN>(src.v, 0, j));
+    __syncthreads();
+    float pg[RGN], og[RGN];
+#pragma unroll
+    for (int g = 0; g < RGN; ++g) {
+        float p0 = 0.f, p1 = 0.f;
+#pragma unroll
+        for (int ri = 0; ri < RL; ++ri) {
+            const int i = g * RL + ri;
+            S[i] = S[i] * sa[i];
+            if (ri & 1) p1 = __builtin_fmaf(sek[i], S[i], p1);
+            else p0 = __builtin_fmaf(sek[i], S[i], p0);
+        }
+        pg[g] = p0 + p1;
+    }
+    const float delta = wv - tree_sum(pg);
+#pragma unroll
+    for (int g = 0; g < RGN; ++g) {
+        float p0 = 0.f, p1 = 0.f;
+#pragma unroll
+        for (int ri = 0; ri < RL; ++ri) {
+            const int i = g * RL + ri;
+            S[i] = __builtin_fmaf(sk[i], delta, S[i]);
+            if (ri & 1) p1 = __builtin_fmaf(sq[i], S[i], p1);
+            else p0 = __builtin_fmaf(sq[i], S[i], p0);
+        }
+        og[g] = p0 + p1;
+    }
+    const float o = tree_sum(og);
+    const int64_t tok = (int64_t)b * a.T * a.H + h;
+    if (jin) {
+        store_out(a.out, a.out_bf16, tok * a.V + j, o);
+        if (a.final_state) {
+            float *fs = a.final_state + (int64_t)bh * a.K * a.V + j;
+#pragma unroll
+            for (int i = 0; i < KP; ++i)
+                if (i < a.K) fs[(int64_t)i * a.V] = S[i];
+        }
+    }
+    if (j < VP) sd[j] = delta;
+    __syncthreads();
+    // Score |k| |delta| with the forward's 16-lane sums.
+    if (j == 0 && a.scores) {
+        float kk[16], dd[16];
+#pragma unroll
+        for (int l = 0; l < 16; ++l) {
+            kk[l] = dd[l] = 0.f;
+            for (int c = l; c < KP; c += 16) kk[l] = __builtin_fmaf(sk[c], sk[c], kk[l]);
+            for (int c = l; c < VP; c += 16) dd[l] = __builtin_fmaf(sd[c], sd[c], dd[l]);
+        }
+        const float k2 = tree_sum(kk), d2 = tree_sum(dd);
+        a.scores[tok] = on ? sqrtf(k2 * d2) : 0.f;
+    }
+}
+
+template <int KP, int VP>
+static hipError_t decode_typed(const SeqArgs &a, bool bf16, hipStream_t st) {
+    constexpr int NTD = VP < 64 ? 64 : VP;
+    if (bf16)
+        hipLaunchKernelGGL((seq_decode_kernel<KP, VP, bf16_t>), dim3(a.B * a.H), dim3(NTD), 0, st, a);
+    else
+        hipLaunchKernelGGL((seq_decode_kernel<KP, VP, float>), dim3(a.B * a.H), dim3(NTD), 0, st, a);
+    return hipGetLastError();
+}
+
 template <int KP, int VP>
 static hipError_t fwd_typed(const SeqArgs &a, bool bf16, hipStream_t st) {
     constexpr int NT = 4 * VP;
@@ -898,6 +1031,11 @@ static hipError_t bwd_typed(const SeqArgs &a, bool bf16, hipStream_t st) {
 
 hipError_t launch_seq_fwd(const SeqArgs &a, bool bf16, hipStream_t st) {
     GDN2_SEQ_DISPATCH(fwd_typed)
+}
+
+hipError_t launch_seq_decode(const SeqArgs &a, bool bf16, hipStream_t st) {
+    if (a.T != 1 || a.doc) return hipErrorInvalidValue;
+    GDN2_SEQ_DISPATCH(decode_typed)
 }
 
 hipError_t launch_seq_bwd(const SeqArgs &a, bool bf16, hipStream_t st) {
