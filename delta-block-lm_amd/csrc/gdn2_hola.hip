@@ -103,7 +103,6 @@ __global__ void __launch_bounds__(64) hola_schedule_kernel(HolaArgs a) {
     __shared__ __align__(16) uint64_t key[kMaxSlots];
     __shared__ float npos[kMaxCapacity], npri[kMaxCapacity], ndoc[kMaxCapacity];
     const int lane = threadIdx.x, bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
-    const int slots = a.cap + a.chunk;
     float *sched = a.schedule + (int64_t)bh * (a.nc + 1) * a.cap;
     if (lane < a.cap) {
         cpos[lane] = -1.f;

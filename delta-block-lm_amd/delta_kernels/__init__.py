@@ -440,7 +440,8 @@ from .mixer_ops import causal_conv, decay, l2_norm, rms_norm  # noqa: E402
 from .train_ops import (FusedAdamW, adamw_update, cross_entropy_rows,  # noqa: E402
                         linear_cross_entropy)
 from .hola_ops import HolaReadOutput, hola_read, hola_schedule  # noqa: E402
+from . import lm_ops  # noqa: E402
 
 __all__ += ["causal_conv", "l2_norm", "rms_norm", "decay", "cross_entropy_rows",
             "linear_cross_entropy", "adamw_update", "FusedAdamW", "HolaReadOutput", "hola_read",
-            "hola_schedule"]
+            "hola_schedule", "lm_ops"]

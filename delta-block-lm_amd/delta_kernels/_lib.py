@@ -55,6 +55,12 @@ class Gdn2HolaShape(ctypes.Structure):
                 ("capacity", ctypes.c_int32), ("chunk", ctypes.c_int32)]
 
 
+class Gdn2LmMixerShape(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_int64), ("time", ctypes.c_int64), ("heads", ctypes.c_int64),
+                ("keys", ctypes.c_int64), ("values", ctypes.c_int64), ("taps", ctypes.c_int64),
+                ("z_stride", ctypes.c_int64)]
+
+
 # Exported symbols and their signatures: (name, restype, argtypes).
 _P = ctypes.c_void_p
 _V = ctypes.POINTER(Gdn2View)
@@ -62,6 +68,8 @@ _S = ctypes.POINTER(Gdn2Shape)
 _F = ctypes.c_void_p  # float*
 _I = ctypes.c_int
 _Z = ctypes.c_size_t
+_L = ctypes.c_int64
+_M = ctypes.POINTER(Gdn2LmMixerShape)
 SIGNATURES = {
     "gdn2_abi_version": (_I, []),
     "gdn2_last_error": (ctypes.c_char_p, []),
@@ -109,6 +117,17 @@ SIGNATURES = {
     "gdn2_hola_workspace_bytes": (_Z, [ctypes.POINTER(Gdn2HolaShape)]),
     "gdn2_hola_backward": (_I, [ctypes.POINTER(Gdn2HolaShape)] + [_V] * 6 + [_P, _Z, _F, _V]
                            + [_F] * 4 + [_P, _Z, _P]),
+    "gdn2_lm_norm_forward": (_I, [_L, _L, ctypes.c_float] + [_P] * 7),
+    "gdn2_lm_norm_workspace_bytes": (_Z, [_L, _L]),
+    "gdn2_lm_norm_backward": (_I, [_L, _L] + [_P] * 9 + [_Z, _P]),
+    "gdn2_lm_mixer_in_forward": (_I, [_M] + [_P] * 10),
+    "gdn2_lm_mixer_in_workspace_bytes": (_Z, [_M]),
+    "gdn2_lm_mixer_in_backward": (_I, [_M] + [_P] * 16 + [_Z, _P]),
+    "gdn2_lm_mixer_out_forward": (_I, [_M, _P, _P, _P, ctypes.c_float, _P, _P, _P]),
+    "gdn2_lm_mixer_out_workspace_bytes": (_Z, [_M]),
+    "gdn2_lm_mixer_out_backward": (_I, [_M] + [_P] * 9 + [_Z, _P]),
+    "gdn2_lm_swiglu_forward": (_I, [_L, _L, _P, _P, _P]),
+    "gdn2_lm_swiglu_backward": (_I, [_L, _L, _P, _P, _P, _P]),
     "gdn2_stage_timing": (_I, [_I]),
     "gdn2_stage_count": (_I, []),
     "gdn2_stage_name": (ctypes.c_char_p, [_I]),

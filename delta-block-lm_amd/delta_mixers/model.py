@@ -16,6 +16,15 @@ reference's); projections and the MLP are GEMMs in `compute_dtype` (bfloat16 by
 default, float32 master weights).  In bfloat16, q/k/v enter the scan as bf16 and
 take the chunk-WY MFMA path (d_k = d_v = 64, chunk 64); in float32 the scan runs
 the token-sequential kernels.
+
+With `fused` (the default for bfloat16) each block is one autograd node whose
+backward is written out: the GEMMs stay torch (hipBLASLt) calls and everything
+between them runs in the library's fused step operators (delta_kernels.lm_ops):
+residual add + RMSNorm to bf16, convolution + SiLU + L2 + gates from the packed
+projection, the output gate, SwiGLU, and their VJPs writing bf16 gradients in
+place.  The rounding points are those of the unfused bf16 composition; the
+residual stream is carried as (u, r) pairs, u float32 and r the bf16 branch
+output, added inside the next norm.
 """
 from __future__ import annotations
 
@@ -41,6 +50,7 @@ class GdnLMConfig:
     norm_epsilon: float = 1e-6  # the reference model's RMSNorm epsilon (model.rs:108-111)
     decay_bias: float = -4.0  # the reference mixer's initial bias (alpha close to 1)
     compute_dtype: torch.dtype = torch.bfloat16
+    fused: bool = True  # bfloat16 only: the fused step operators (module docstring)
 
 
 def _linear(i, o, device):
@@ -126,6 +136,92 @@ class Block(torch.nn.Module):
         return x + self.mlp(dk.rms_norm(x, self.norm2, None, eps).to(cd)).float()
 
 
+class _FusedBlock(torch.autograd.Function):
+    """One block on the fused operators: (u, r) -> (u', r') with the block input
+    x = u + r (r bf16 or None), u' = x + mixer(norm1(x)), r' = mlp(norm2(u'))."""
+
+    @staticmethod
+    def forward(ctx, u_prev, r_prev, norm1, in_proj, conv_w, decay_scale, decay_bias, onorm,
+                out_w, norm2, w13, w2, valid, docs, reset, cfg):
+        B, T, D = u_prev.shape
+        H, R, cd, eps = cfg.heads, B * T, cfg.compute_dtype, cfg.norm_epsilon
+        lm = dk.lm_ops
+        w_in, w_out, w_13, w_2 = (w.to(cd) for w in (in_proj, out_w, w13, w2))
+        x, n1, inv1 = lm.norm_forward(u_prev.reshape(R, D),
+                                      None if r_prev is None else r_prev.reshape(R, D), norm1, eps)
+        z = torch.mm(n1, w_in.t())
+        qkv, beta, g = lm.mixer_in_forward(z, conv_w, valid, docs, decay_scale, decay_bias, B, T, H)
+        q, k, v = qkv[:, :, :H], qkv[:, :, H:2 * H], qkv[:, :, 2 * H:]
+        o, _, _, ck = dk.gdn_scalar_forward(q, k, v, beta, g, valid, reset, None, cfg.chunk)
+        yg, inv_o = lm.mixer_out_forward(o, z, onorm, eps, B, T, H)
+        m = torch.mm(yg, w_out.t())
+        u, n2, inv2 = lm.norm_forward(x, m, norm2, eps)
+        h = torch.mm(n2, w_13.t())
+        a = lm.swiglu_forward(h)
+        r = torch.mm(a, w_2.t())
+        ctx.save_for_backward(x, n1, inv1, z, qkv, beta, g, o, yg, inv_o, u, n2, inv2, h, a,
+                              norm1, conv_w, decay_scale, decay_bias, onorm, norm2, valid, docs,
+                              reset, w_in, w_out, w_13, w_2)
+        ctx.ck, ctx.cfg, ctx.has_r = ck, cfg, r_prev is not None
+        return u.view(B, T, D), r.view(B, T, D)
+
+    @staticmethod
+    def backward(ctx, du, dr):
+        (x, n1, inv1, z, qkv, beta, g, o, yg, inv_o, u, n2, inv2, h, a, norm1, conv_w,
+         decay_scale, decay_bias, onorm, norm2, valid, docs, reset, w_in, w_out, w_13,
+         w_2) = ctx.saved_tensors
+        cfg, ck = ctx.cfg, ctx.ck
+        ctx.ck = None
+        B, T, D = du.shape
+        H, R = cfg.heads, B * T
+        lm = dk.lm_ops
+        du = du.reshape(R, D).float().contiguous()
+        dr = dr.reshape(R, D).to(cfg.compute_dtype).contiguous()
+        # MLP branch
+        da = torch.mm(dr, w_2)
+        dw2 = torch.mm(dr.t(), a)
+        dh = lm.swiglu_backward(h, da)
+        dw13 = torch.mm(dh.t(), n2)
+        dn2 = torch.mm(dh, w_13)
+        du_in, dm, dnorm2 = lm.norm_backward(u, norm2, inv2, dn2, du, True)
+        # mixer branch
+        dyg = torch.mm(dm, w_out)
+        dwout = torch.mm(dm.t(), yg)
+        dz = torch.empty_like(z)
+        d_o, donorm = lm.mixer_out_backward(o, z, onorm, inv_o, dyg, dz, B, T, H)
+        q, k, v = qkv[:, :, :H], qkv[:, :, H:2 * H], qkv[:, :, 2 * H:]
+        dq, dkk, dv, dbeta, dg, _ = dk.gdn_scalar_backward(q, k, v, beta, g, valid, reset, ck,
+                                                           cfg.chunk, d_o)
+        dconv, dds, ddb = lm.mixer_in_backward(z, conv_w, valid, docs, decay_scale, decay_bias,
+                                               dq, dkk, dv, dbeta, dg, dz, B, T, H)
+        dwin = torch.mm(dz.t(), n1)
+        dn1 = torch.mm(dz, w_in)
+        dx, dxb, dnorm1 = lm.norm_backward(x, norm1, inv1, dn1, du_in, ctx.has_r)
+        return (dx.view(B, T, D), None if dxb is None else dxb.view(B, T, D), dnorm1,
+                dwin.float(), dconv, dds, ddb, donorm, dwout.float(), dnorm2, dw13.float(),
+                dw2.float(), None, None, None, None)
+
+
+class _FusedFinalNorm(torch.autograd.Function):
+    """The final RMSNorm of the (u, r) stream, to bf16 [B T, D]."""
+
+    @staticmethod
+    def forward(ctx, u, r, weight, eps):
+        B, T, D = u.shape
+        x, y, inv = dk.lm_ops.norm_forward(u.reshape(B * T, D),
+                                           None if r is None else r.reshape(B * T, D), weight, eps)
+        ctx.save_for_backward(x, weight, inv)
+        ctx.shape, ctx.has_r = (B, T, D), r is not None
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, weight, inv = ctx.saved_tensors
+        dx, dxb, dw = dk.lm_ops.norm_backward(x, weight, inv, dy.to(torch.bfloat16).contiguous(),
+                                              None, ctx.has_r)
+        return dx.view(ctx.shape), None if dxb is None else dxb.view(ctx.shape), dw, None
+
+
 class GdnLM(torch.nn.Module):
     def __init__(self, cfg: GdnLMConfig, device=None):
         super().__init__()
@@ -144,8 +240,39 @@ class GdnLM(torch.nn.Module):
             x = blk(x, valid, docs)
         return dk.rms_norm(x, self.norm, None, self.cfg.norm_epsilon)
 
+    def _fused(self) -> bool:
+        """The fused operators cover bf16 models with K = V = 64, an even power-of-two
+        head count up to 32, d_model 128 or a multiple of 256 up to 1024, and an
+        MLP width that is a multiple of 8; other shapes take the unfused path."""
+        c = self.cfg
+        H = c.heads
+        return (c.fused and c.compute_dtype == torch.bfloat16 and c.key_dim == 64 and
+                c.value_dim == 64 and 2 <= H <= 32 and H & (H - 1) == 0 and
+                (c.d_model == 128 or (c.d_model % 256 == 0 and c.d_model <= 1024)) and
+                c.mlp_width % 8 == 0 and 1 <= c.conv_taps <= 8)
+
+    def features_bf16(self, tokens):
+        """tokens [B, T] -> final-norm features [B T, d_model] bf16 on the
+        fused step operators."""
+        cfg = self.cfg
+        B, T = tokens.shape
+        dev = tokens.device
+        valid = torch.ones(B, T, device=dev)
+        docs = torch.zeros(B, T, device=dev)
+        reset = torch.zeros(B, T, device=dev)
+        u, r = self.embed[tokens], None
+        for blk in self.blocks:
+            mx, mlp = blk.mixer, blk.mlp
+            u, r = _FusedBlock.apply(u, r, blk.norm1, mx.in_proj, mx.qkv_conv, mx.decay_scale,
+                                     mx.decay_bias, mx.norm_weight, mx.out, blk.norm2, mlp.w13,
+                                     mlp.w2, valid, docs, reset, cfg)
+        return _FusedFinalNorm.apply(u, r, self.norm, cfg.norm_epsilon)
+
     def forward(self, tokens):
         """tokens [B, T] int64 -> logits [B, T, vocab] in compute_dtype."""
+        if self._fused():
+            B, T = tokens.shape
+            return _mm(self.features_bf16(tokens), self.embed).view(B, T, -1)
         return _mm(self.features(tokens).to(self.cfg.compute_dtype), self.embed)
 
     def loss(self, tokens):
@@ -153,7 +280,10 @@ class GdnLM(torch.nn.Module):
         the loss in one operator (logits computed once, replaced in place by
         their gradient)."""
         cd = self.cfg.compute_dtype
-        h = self.features(tokens[:, :-1]).to(cd)
+        if self._fused():
+            h = self.features_bf16(tokens[:, :-1])
+        else:
+            h = self.features(tokens[:, :-1]).to(cd)
         return dk.linear_cross_entropy(h.reshape(-1, self.cfg.d_model), self.embed.to(cd),
                                        tokens[:, 1:].reshape(-1))
 

@@ -323,6 +323,81 @@ GDN2_API int gdn2_adamw_update(int32_t count, const gdn2_adamw_tensor *tensors, 
                                int reuse_table, void *workspace, size_t workspace_bytes,
                                void *stream);
 
+/* ---- Fused operators of the lm512 training step ------------------------------ */
+/* No counterpart in the reference, whose model composes the f32 operators
+ * above one by one (crates/mixers/src/lib.rs:456-525; block
+ * crates/experiment/src/model.rs:300-364).  They serve a bf16 training step of
+ * that model: each folds the casts, slices, residual adds and pointwise ops
+ * around a GEMM into one pass, computing in f32 and rounding to bf16 exactly
+ * where the unfused bf16 composition rounds.  All tensors are dense and
+ * row-major; "bf16" arguments point to bfloat16 storage.  Parameter gradients
+ * are reduced deterministically through the workspace. */
+
+/* RMSNorm with the residual add in front, rows of `width` (128, or a multiple
+ * of 256 up to 1024):  u = x + residual (bf16; NULL: u = x),
+ *   y = bf16(weight * u / sqrt(mean u^2 + epsilon)),  inverse[r] = 1/sqrt(...).
+ * u (f32, may be NULL) receives the sum.  x, u, weight 16-byte aligned. */
+GDN2_API int gdn2_lm_norm_forward(int64_t rows, int64_t width, float epsilon, const float *x,
+                                  const void *residual, const float *weight, float *u, void *y,
+                                  float *inverse, void *stream);
+GDN2_API size_t gdn2_lm_norm_workspace_bytes(int64_t rows, int64_t width);
+/* VJP with the residual gradient added: dx = dres + J^T dy (dy bf16; dres f32
+ * or NULL).  dx (f32) and dx_bf16 (bf16 copy, may be NULL); dweight [width]. */
+GDN2_API int gdn2_lm_norm_backward(int64_t rows, int64_t width, const float *x,
+                                   const float *weight, const float *inverse, const void *dy,
+                                   const float *dres, float *dx, void *dx_bf16, float *dweight,
+                                   void *workspace, size_t workspace_bytes, void *stream);
+
+/* The GDN mixer around the scalar-gate scan.  z is the packed input
+ * projection, bf16 [batch, time, z_stride], per token
+ *   [q (H K) | k (H K) | v (H V) | gate (H V) | beta (H) | decay (H)]
+ * with keys = values = 64, heads a power of two up to 32, taps 1..8. */
+typedef struct gdn2_lm_mixer_shape {
+    int64_t batch, time, heads, keys, values, taps, z_stride;
+} gdn2_lm_mixer_shape;
+
+/* qkv bf16 [batch, time, 3 H 64] = per-head L2 (q, k; epsilon 1e-6) of
+ * silu(causal_conv(z[..., :3 H 64], conv_w)) (conv_w f32 [taps, 3 H 64]; the
+ * masks as for gdn2_conv_forward); beta, g f32 [batch, time, H]:
+ *   beta = sigmoid(z_beta),  g = -exp(decay_scale[h]) softplus(z_decay + decay_bias[h]). */
+GDN2_API int gdn2_lm_mixer_in_forward(const gdn2_lm_mixer_shape *shape, const void *z,
+                                      const float *conv_w, const float *valid, const float *docs,
+                                      const float *decay_scale, const float *decay_bias,
+                                      void *qkv, float *beta, float *g, void *stream);
+GDN2_API size_t gdn2_lm_mixer_in_workspace_bytes(const gdn2_lm_mixer_shape *shape);
+/* From the scan's gradients (dq, dk, dv bf16 [batch, time, H, 64]; dbeta, dg
+ * f32 [batch, time, H]): the q, k, v, beta and decay columns of dz (bf16, z's
+ * layout; the gate columns are left to gdn2_lm_mixer_out_backward), dconv_w
+ * [taps, 3 H 64], ddecay_scale [H], ddecay_bias [H]. */
+GDN2_API int gdn2_lm_mixer_in_backward(const gdn2_lm_mixer_shape *shape, const void *z,
+                                       const float *conv_w, const float *valid, const float *docs,
+                                       const float *decay_scale, const float *decay_bias,
+                                       const void *dq, const void *dk, const void *dv,
+                                       const float *dbeta, const float *dg, void *dz,
+                                       float *dconv_w, float *ddecay_scale, float *ddecay_bias,
+                                       void *workspace, size_t workspace_bytes, void *stream);
+
+/* Output gate: y bf16 [batch, time, H 64] = rms_norm(o, norm_w) * silu(gate)
+ * per head (o bf16 [batch, time, H, 64], the scan output; gate from z);
+ * inverse [batch time H]. */
+GDN2_API int gdn2_lm_mixer_out_forward(const gdn2_lm_mixer_shape *shape, const void *o,
+                                       const void *z, const float *norm_w, float epsilon, void *y,
+                                       float *inverse, void *stream);
+GDN2_API size_t gdn2_lm_mixer_out_workspace_bytes(const gdn2_lm_mixer_shape *shape);
+/* d_o bf16 (the scan's output gradient), the gate columns of dz, dnorm_w [64]. */
+GDN2_API int gdn2_lm_mixer_out_backward(const gdn2_lm_mixer_shape *shape, const void *o,
+                                        const void *z, const float *norm_w, const float *inverse,
+                                        const void *dy, void *d_o, void *dz, float *dnorm_w,
+                                        void *workspace, size_t workspace_bytes, void *stream);
+
+/* SwiGLU: h bf16 [rows, 2 width] = [gate | up] ->
+ *   a bf16 [rows, width] = bf16(bf16(silu(gate)) * up);
+ * the VJP writes both halves of dh.  width a multiple of 8, 16-byte aligned. */
+GDN2_API int gdn2_lm_swiglu_forward(int64_t rows, int64_t width, const void *h, void *a,
+                                    void *stream);
+GDN2_API int gdn2_lm_swiglu_backward(int64_t rows, int64_t width, const void *h, const void *da,
+                                     void *dh, void *stream);
+
 /* ---- HOLA exact-memory cache read (the consumer of the scan's scores) ------- */
 /* Replaces HolaOps::hola_schedule / hola_read / hola_backward (reference
  * crates/kernels/src/hola_ops.rs:17-425, kernels crates/kernels/src/hola.rs;
