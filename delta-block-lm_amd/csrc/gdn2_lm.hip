@@ -28,7 +28,9 @@
 namespace gdn2 {
 namespace {
 
-constexpr int kSegRows = 32;        // time steps per convolution segment
+constexpr int kSegRows = 32;        // time steps per convolution segment (one workgroup)
+constexpr int kWaveRows = 8;        // time steps per wave of a segment
+constexpr int kInWaves = kSegRows / kWaveRows;
 constexpr int kBwdBlocks = 1024;    // workgroups of the persistent row VJPs (fixed: deterministic)
 constexpr int kSumWaves = 16;
 
@@ -57,9 +59,17 @@ __device__ __forceinline__ float sum64(float x) {
     return readlane_f(x, 0) + readlane_f(x, 16) + readlane_f(x, 32) + readlane_f(x, 48);
 }
 
-__device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + expf(-x)); }
-// SiLU as the bf16 model's pointwise op evaluates it.
-__device__ __forceinline__ float silu_div(float x) { return x / (1.f + expf(-x)); }
+// The pointwise ops use the hardware exp2 / reciprocal / reciprocal square
+// root (v_exp_f32, v_rcp_f32, v_rsq_f32, about 1 ulp each): these kernels
+// would otherwise be bound by the VALU work of IEEE division and libm exp,
+// and the results are rounded to bf16 anyway (relative error ~1e-6 at most,
+// against bf16's 2^-9).
+__device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float frsq(float x) { return __builtin_amdgcn_rsqf(x); }
+__device__ __forceinline__ float sigm(float x) { return frcp(1.f + fexp(-x)); }
+// SiLU, x / (1 + exp(-x)).
+__device__ __forceinline__ float silu_div(float x) { return x * frcp(1.f + fexp(-x)); }
 // up * d silu(x) / dx.
 __device__ __forceinline__ float silu_vjp(float x, float up) {
     const float s = sigm(x);
@@ -94,8 +104,10 @@ __global__ void __launch_bounds__(64 * kSumWaves) lm_colsum_kernel(const float *
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t i = (int64_t)blockIdx.x * 64 + lane;
     float s = 0.f;
-    if (i < n)
+    if (i < n) {
+#pragma unroll 16
         for (int64_t k = w; k < segs; k += kSumWaves) s += part[k * n + i];
+    }
     red[w][lane] = s;
     __syncthreads();
     if (w == 0 && i < n) {
@@ -161,7 +173,7 @@ __global__ void __launch_bounds__(256) lm_norm_fwd_kernel(NormArgs a) {
         ss += dot4(z[k], z[k]);
     }
     ss = group_sum<G>(ss);
-    const float inv = 1.f / sqrtf(ss / (float)a.W + a.eps);
+    const float inv = frsq(ss * (1.f / (float)a.W) + a.eps);
     if (!live) return;
     if (lane == 0) a.inv[row] = inv;
 #pragma unroll
@@ -252,34 +264,56 @@ struct InArgs {
 
 __host__ __device__ inline int64_t in_segments(int64_t T) { return (T + kSegRows - 1) / kSegRows; }
 
-// Sliding window over time: slot l holds row t - l (value, document, valid);
-// rows outside [0, T) read as zero, invalid.
+// The rows a segment reads, fetched up front: slot i is row tb + i of this
+// thread's channel (rows outside [0, T) read as zero).  The lag masks are
+// wave-uniform, so they live in LDS: mk[r][l] = mask of the lag from slot
+// r - l to slot r, valid[s] valid[r] [docs[s] == docs[r]] (0 past the window
+// or outside [0, T)); lane r computes row r's W masks.
 template <int W>
-struct Window {
-    float x[W], d[W], v[W];
-    __device__ __forceinline__ void clear() {
+constexpr int mask_pitch() { return (W + 3) & ~3; }
+
+template <int NR, int W>
+struct Rows {
+    float x[NR];
+    float (*mk)[mask_pitch<W>()];
+
+    __device__ __forceinline__ void fetch(const InArgs &a, int64_t b, int64_t tb, int c,
+                                          float (*lds)[mask_pitch<W>()]) {
+        mk = lds;
 #pragma unroll
-        for (int l = 0; l < W; ++l) x[l] = d[l] = v[l] = 0.f;
-    }
-    __device__ __forceinline__ void push(const InArgs &a, int64_t b, int64_t t, int c) {
-#pragma unroll
-        for (int l = W - 1; l > 0; --l) {
-            x[l] = x[l - 1];
-            d[l] = d[l - 1];
-            v[l] = v[l - 1];
+        for (int i = 0; i < NR; ++i) {
+            const int64_t t = tb + i;
+            const int64_t tc = t < 0 ? 0 : (t >= a.T ? a.T - 1 : t);  // in bounds; masked below
+            x[i] = bf16_to_f32(a.z[(b * a.T + tc) * a.zs + c]);
         }
-        const bool in = t >= 0 && t < a.T;
-        x[0] = in ? bf16_to_f32(a.z[(b * a.T + t) * a.zs + c]) : 0.f;
-        d[0] = in ? a.docs[b * a.T + t] : 0.f;
-        v[0] = in ? a.valid[b * a.T + t] : 0.f;
+        const int lane = threadIdx.x & 63;
+        if (lane < NR) {
+            auto row = [&](int64_t t, float &d, float &v) {
+                const bool in = t >= 0 && t < a.T;
+                d = in ? a.docs[b * a.T + t] : 0.f;
+                v = in ? a.valid[b * a.T + t] : 0.f;
+            };
+            float dr, vr;
+            row(tb + lane, dr, vr);
+#pragma unroll
+            for (int l = 0; l < W; ++l) {
+                float ds = 0.f, vs = 0.f;
+                if (lane - l >= 0) row(tb + lane - l, ds, vs);
+                mk[lane][l] = ds == dr ? vs * vr : 0.f;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const bool in = tb + i >= 0 && tb + i < a.T;
+            x[i] = in ? x[i] : 0.f;
+        }
     }
-    __device__ __forceinline__ float mask(int s, int r) const {
-        return d[s] == d[r] ? v[s] * v[r] : 0.f;
-    }
-    __device__ __forceinline__ float pre(const float *w) const {
+    // Pre-activation output of slot r (r >= W - 1).
+    __device__ __forceinline__ float pre(const float *w, int r) const {
         float s = 0.f;
 #pragma unroll
-        for (int l = 0; l < W; ++l) s += x[l] * w[l] * mask(l, 0);
+        for (int l = 0; l < W; ++l) s += x[r - l] * w[l] * mk[r][l];
         return s;
     }
 };
@@ -303,16 +337,18 @@ __device__ void gates_forward(const InArgs &a, int64_t b, int64_t t0, int64_t t1
     }
 }
 
-// Grid (B nseg, C / 64 + 1), one wave: block column y < C / 64 holds 64
-// channels (one head of q, k or v); the last column does the gates.
+// Grid (B nseg, C / 64 + 1): block column y < C / 64 holds 64 channels (one
+// head of q, k or v), its 4 waves 8 time steps each; the last column does the
+// gates (wave 0).
 template <int W>
-__global__ void __launch_bounds__(64) lm_in_fwd_kernel(InArgs a) {
+__global__ void __launch_bounds__(64 * kInWaves) lm_in_fwd_kernel(InArgs a) {
+    constexpr int NR = kWaveRows + W - 1;
     const int64_t nseg = in_segments(a.T);
     const int64_t b = blockIdx.x / nseg, t0 = (blockIdx.x % nseg) * kSegRows;
     const int64_t t1 = min(t0 + kSegRows, a.T);
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     if ((int)blockIdx.y == a.C / 64) {
-        gates_forward(a, b, t0, t1, lane);
+        if (wv == 0) gates_forward(a, b, t0, t1, lane);
         return;
     }
     const int c = blockIdx.y * 64 + lane;
@@ -320,14 +356,17 @@ __global__ void __launch_bounds__(64) lm_in_fwd_kernel(InArgs a) {
     float w[W];
 #pragma unroll
     for (int l = 0; l < W; ++l) w[l] = a.w[l * a.C + c];
-    Window<W> win;
-    win.clear();
-    for (int64_t t = t0 - (W - 1); t < t0; ++t) win.push(a, b, t, c);
-    for (int64_t t = t0; t < t1; ++t) {
-        win.push(a, b, t, c);
-        const float p = win.pre(w);
+    __shared__ __align__(16) float mk[kInWaves][NR][mask_pitch<W>()];
+    const int64_t tw = t0 + kWaveRows * wv;  // this wave's first row
+    Rows<NR, W> rw;
+    rw.fetch(a, b, tw - (W - 1), c, mk[wv]);
+#pragma unroll
+    for (int i = 0; i < kWaveRows; ++i) {
+        const int64_t t = tw + i;
+        if (t >= t1) continue;  // wave-uniform
+        const float p = rw.pre(w, i + W - 1);
         float s = p * sigm(p);
-        if (l2) s = s * (1.f / sqrtf(sum64(s * s) + 1e-6f));
+        if (l2) s = s * frsq(sum64(s * s) + 1e-6f);
         a.qkv[(b * a.T + t) * a.C + c] = f32_to_bf16(s);
     }
 }
@@ -366,19 +405,23 @@ __device__ void gates_backward(const InArgs &a, int64_t b, int64_t t0, int64_t t
     }
 }
 
-// VJP of lm_in_fwd_kernel, the sweep of a convolution VJP: with gr the
-// gradient at the pre-activation of row t (recomputed: window, SiLU, L2),
+// VJP of lm_in_fwd_kernel (the VJP of a convolution): with gr the gradient at
+// the pre-activation of row t (recomputed: window, SiLU, L2),
 //   dz[t]  = sum_l gr[t + l] w[l] mask(t -> t + l)
 //   dw[l] += gr[t] z[t - l] mask(t - l -> t)     (t in this segment)
-// t runs from t0 to t1 + W - 2 (rows of the next segment recomputed).
+// Each wave computes gr for its 8 rows into LDS (the last wave also for the
+// next segment's first W - 1 rows), then emits dz and dw for its rows; the
+// waves' dw are added in order into one partial per workgroup.
 template <int W>
-__global__ void __launch_bounds__(64) lm_in_bwd_kernel(InArgs a) {
+__global__ void __launch_bounds__(64 * kInWaves) lm_in_bwd_kernel(InArgs a) {
+    constexpr int NG = kWaveRows + W - 1;  // gradient rows of the last wave
+    constexpr int NR = NG + W - 1;         // rows read: tw - (W - 1) .. tw + NG - 1
     const int64_t nseg = in_segments(a.T);
     const int64_t b = blockIdx.x / nseg, t0 = (blockIdx.x % nseg) * kSegRows;
     const int64_t t1 = min(t0 + kSegRows, a.T);
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     if ((int)blockIdx.y == a.C / 64) {
-        gates_backward(a, b, t0, t1, lane);
+        if (wv == 0) gates_backward(a, b, t0, t1, lane);
         return;
     }
     const int c = blockIdx.y * 64 + lane;
@@ -400,50 +443,70 @@ __global__ void __launch_bounds__(64) lm_in_bwd_kernel(InArgs a) {
         width = (int64_t)a.H * a.V;
         col = c - 2 * HK;
     }
-    float w[W], dw[W], gr[W];
+    float w[W];
 #pragma unroll
-    for (int l = 0; l < W; ++l) {
-        w[l] = a.w[l * a.C + c];
-        dw[l] = 0.f;
-        gr[l] = 0.f;
+    for (int l = 0; l < W; ++l) w[l] = a.w[l * a.C + c];
+    __shared__ __align__(16) float mk[kInWaves][NR][mask_pitch<W>()];
+    __shared__ float gsh[kSegRows + W - 1][64];  // gr of row t0 + j
+    __shared__ float dwr[kInWaves][W][64];
+    const int64_t tw = t0 + kWaveRows * wv;  // this wave's first row; slot i + W - 1 is row tw + i
+    Rows<NR, W> rw;
+    rw.fetch(a, b, tw - (W - 1), c, mk[wv]);
+    const int ng = wv == kInWaves - 1 ? NG : kWaveRows;  // wave-uniform
+    float up[NG];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        const int64_t t = tw + i;
+        up[i] = i < ng ? bf16_to_f32(src[(b * a.T + (t < a.T ? t : a.T - 1)) * width + col]) : 0.f;
     }
-    Window<W> win;
-    win.clear();
-    for (int64_t t = t0 - (W - 1); t < t0; ++t) win.push(a, b, t, c);
-    for (int64_t t = t0; t < t1 + W - 1; ++t) {
-        win.push(a, b, t, c);
 #pragma unroll
-        for (int l = W - 1; l > 0; --l) gr[l] = gr[l - 1];
-        gr[0] = 0.f;
-        if (t < a.T) {  // wave-uniform
-            const float p = win.pre(w);
+    for (int i = 0; i < NG; ++i) {
+        if (i >= ng) continue;  // wave-uniform
+        float gv = 0.f;
+        if (tw + i < a.T) {  // wave-uniform
+            const float p = rw.pre(w, i + W - 1);
             const float sg = sigm(p), s = p * sg;
-            float up = bf16_to_f32(src[(b * a.T + t) * width + col]);
+            float u = up[i];
             if (l2) {
-                const float inv = 1.f / sqrtf(sum64(s * s) + 1e-6f);
-                const float corr = sum64(up * s) * inv * inv;
-                up = (up - s * corr) * inv;
+                const float inv = frsq(sum64(s * s) + 1e-6f);
+                const float corr = sum64(u * s) * inv * inv;
+                u = (u - s * corr) * inv;
             }
-            gr[0] = up * sg * (1.f + p * (1.f - sg));
+            gv = u * sg * (1.f + p * (1.f - sg));
         }
-        if (t < t1) {
+        gsh[kWaveRows * wv + i][lane] = gv;
+    }
+    __syncthreads();
+    float dw[W];
 #pragma unroll
-            for (int l = 0; l < W; ++l) dw[l] += gr[0] * win.x[l] * win.mask(l, 0);
+    for (int l = 0; l < W; ++l) dw[l] = 0.f;
+#pragma unroll
+    for (int i = 0; i < kWaveRows; ++i) {
+        if (tw + i >= t1) continue;  // wave-uniform
+        const int r = i + W - 1, j = kWaveRows * wv + i;
+        const float g0 = gsh[j][lane];
+#pragma unroll
+        for (int l = 0; l < W; ++l) dw[l] += g0 * rw.x[r - l] * rw.mk[r][l];
+        float sum = 0.f;
+#pragma unroll
+        for (int l = 0; l < W; ++l) {
+            const float m = rw.mk[r + l][l];  // lag from row tw + i to row tw + i + l
+            if (m != 0.f) sum += gsh[j + l][lane] * w[l] * m;
         }
-        const int64_t td = t - (W - 1);  // row whose gradient is now complete (slot W - 1)
-        if (td >= t0) {
-            float s = 0.f;
+        a.dz[(b * a.T + tw + i) * a.zs + c] = f32_to_bf16(sum);
+    }
 #pragma unroll
-            for (int l = 0; l < W; ++l) {
-                const float m = win.mask(W - 1, W - 1 - l);
-                if (m != 0.f) s += gr[W - 1 - l] * w[l] * m;
-            }
-            a.dz[(b * a.T + td) * a.zs + c] = f32_to_bf16(s);
+    for (int l = 0; l < W; ++l) dwr[wv][l][lane] = dw[l];
+    __syncthreads();
+    if (wv == 0) {
+        float *part = a.wpart + (int64_t)blockIdx.x * W * a.C;
+#pragma unroll
+        for (int l = 0; l < W; ++l) {
+            float t = dwr[0][l][lane];
+            for (int q = 1; q < kInWaves; ++q) t += dwr[q][l][lane];
+            part[l * a.C + c] = t;
         }
     }
-    float *part = a.wpart + (int64_t)blockIdx.x * W * a.C;
-#pragma unroll
-    for (int l = 0; l < W; ++l) part[l * a.C + c] = dw[l];
 }
 
 // ddecay_bias[h] = sum of the decay-column gradients; ddecay_scale[h] =
@@ -457,8 +520,10 @@ __global__ void __launch_bounds__(64 * kSumWaves) lm_gate_sum_kernel(const float
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int n = 2 * H;
     float s = 0.f;
-    if (lane < n)
+    if (lane < n) {
+#pragma unroll 8
         for (int64_t k = w; k < segs; k += kSumWaves) s += part[k * n + lane];
+    }
     red[w][lane] = s;
     __syncthreads();
     if (w == 0 && lane < n) {
@@ -494,7 +559,7 @@ __global__ void __launch_bounds__(256) lm_out_fwd_kernel(OutArgs a) {
     const int h = (int)(r % a.H);
     const float4 o = ld_bf4(a.o + r * 64 + 4 * lane);
     const float ss = sum16(dot4(o, o));
-    const float inv = 1.f / sqrtf(ss / 64.f + a.eps);
+    const float inv = frsq(ss * (1.f / 64.f) + a.eps);
     if (!live) return;
     const float4 w = ld_f4(a.w + 4 * lane);
     const float4 g = ld_bf4(a.z + bt * a.zs + a.gcol + h * 64 + 4 * lane);
@@ -649,14 +714,14 @@ InArgs in_args(const gdn2_lm_mixer_shape *s, const void *z, const float *conv_w,
 template <template <int> class K>
 void launch_taps(int W, dim3 grid, hipStream_t st, const InArgs &a) {
     switch (W) {
-        case 1: hipLaunchKernelGGL(K<1>::fn, grid, dim3(64), 0, st, a); break;
-        case 2: hipLaunchKernelGGL(K<2>::fn, grid, dim3(64), 0, st, a); break;
-        case 3: hipLaunchKernelGGL(K<3>::fn, grid, dim3(64), 0, st, a); break;
-        case 4: hipLaunchKernelGGL(K<4>::fn, grid, dim3(64), 0, st, a); break;
-        case 5: hipLaunchKernelGGL(K<5>::fn, grid, dim3(64), 0, st, a); break;
-        case 6: hipLaunchKernelGGL(K<6>::fn, grid, dim3(64), 0, st, a); break;
-        case 7: hipLaunchKernelGGL(K<7>::fn, grid, dim3(64), 0, st, a); break;
-        default: hipLaunchKernelGGL(K<8>::fn, grid, dim3(64), 0, st, a); break;
+        case 1: hipLaunchKernelGGL(K<1>::fn, grid, dim3(64 * kInWaves), 0, st, a); break;
+        case 2: hipLaunchKernelGGL(K<2>::fn, grid, dim3(64 * kInWaves), 0, st, a); break;
+        case 3: hipLaunchKernelGGL(K<3>::fn, grid, dim3(64 * kInWaves), 0, st, a); break;
+        case 4: hipLaunchKernelGGL(K<4>::fn, grid, dim3(64 * kInWaves), 0, st, a); break;
+        case 5: hipLaunchKernelGGL(K<5>::fn, grid, dim3(64 * kInWaves), 0, st, a); break;
+        case 6: hipLaunchKernelGGL(K<6>::fn, grid, dim3(64 * kInWaves), 0, st, a); break;
+        case 7: hipLaunchKernelGGL(K<7>::fn, grid, dim3(64 * kInWaves), 0, st, a); break;
+        default: hipLaunchKernelGGL(K<8>::fn, grid, dim3(64 * kInWaves), 0, st, a); break;
     }
 }
 template <int W> struct InFwd { static constexpr auto fn = lm_in_fwd_kernel<W>; };

@@ -238,6 +238,40 @@ def test_lm_bfloat16_chunk_path_matches_bf16_rounded_composition():
         assert far <= 1.5 * spread, f"d{n}: {far:.3e} from float64, spread {spread:.3e}"
 
 
+def test_lm_fused_matches_unfused_within_bf16_spread():
+    """The fused bf16 model (delta_kernels.lm_ops, one autograd node per block)
+    against the unfused bf16 composition of the reference-mirrored operators,
+    same weights and tokens.  Both hold the same bf16 values but sum in
+    different orders (and the fused weight gradients stay float32), so they
+    differ by bf16 rounding flips: per gradient, their distance must be at most
+    the bf16 spread against exact float64; the losses within 2e-4 relative."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from dataclasses import replace
+
+    from delta_mixers.model import GdnLM
+    cfg = _small(torch.bfloat16)
+    fused = _perturbed_model(cfg)
+    assert fused._fused()
+    plain = GdnLM(replace(cfg, fused=False), device="cuda")
+    plain.load_state_dict(fused.state_dict())
+    assert not plain._fused()
+    tokens = torch.randint(0, cfg.vocab, (2, 131), generator=torch.Generator().manual_seed(1))
+    lf = fused.loss(tokens.cuda())
+    lf.backward()
+    lp = plain.loss(tokens.cuda())
+    lp.backward()
+    assert abs(lf.item() - lp.item()) <= 2e-4 * abs(lp.item())
+    _, g16 = _reference_grads(fused, tokens, cfg, True)
+    _, g64 = _reference_grads(fused, tokens, cfg, False)
+    for (n, a), (_, b) in zip(fused.named_parameters(), plain.named_parameters()):
+        ga, gb = a.grad.double().cpu().numpy(), b.grad.double().cpu().numpy()
+        assert np.all(np.isfinite(ga)), f"d{n}: nonfinite values"
+        spread = _normwise(g16[n], g64[n])
+        dist = np.linalg.norm(ga - gb) / np.linalg.norm(g64[n])
+        assert dist <= spread, f"d{n}: fused vs unfused {dist:.3e}, spread {spread:.3e}"
+
+
 def test_lm_training_steps_reduce_loss():
     """AdamW steps on one fixed batch drive its loss down (the update wiring)."""
     if not torch.cuda.is_available():

@@ -10,10 +10,10 @@ other side of a rounding boundary, never further), and f32 outputs and
 parameter gradients (fixed-order sums) within 1e-5 normwise.  Also: the two
 mixer VJPs write complementary column sets of dz (every column exactly once),
 ragged sizes (rows not a multiple of the workgroup's, T not a multiple of the
-32-step segment), masks with padding and document boundaries, and the
-fused model against the unfused one.
+32-step segment), masks with padding and document boundaries.  The fused
+model against the unfused one is in test_gpu_lm.py (it needs that file's
+float64 reference for its gate).
 """
-import numpy as np
 import pytest
 
 torch = pytest.importorskip("torch")
@@ -48,8 +48,9 @@ def _bf16_close(name, got, ref, slack=1e-6, loose=None):
 
 
 def _ambiguous(x):
-    """Entries of x (float64) within 1e-6 relative of a bf16 rounding boundary."""
-    return (x * (1 + 1e-6)).to(BF) != (x * (1 - 1e-6)).to(BF)
+    """Entries of x (float64) within 1e-5 relative of a bf16 rounding boundary
+    (the kernels' f32 pointwise ops are accurate to about 1e-6 relative)."""
+    return (x * (1 + 1e-5)).to(BF) != (x * (1 - 1e-5)).to(BF)
 
 
 def _zstride(H):
@@ -252,33 +253,3 @@ def test_swiglu_matches_bf16_composition(rows, M):
     ds = (d * u).to(BF).double()  # the product's gradient is held in bf16
     _bf16_close("dgate", dh[:, :M], ds * sg * (1 + g * (1 - sg)), slack=1e-5)
     _bf16_close("dup", dh[:, M:], d * s, slack=1e-5, loose=amb)
-
-
-# ---- the fused model ------------------------------------------------------------------
-
-
-def test_fused_lm_matches_unfused_composition():
-    """Same weights and tokens: the fused bf16 model against the unfused bf16
-    composition of the reference-mirrored operators.  Rounding points agree,
-    summation orders do not, so results differ by bf16 rounding flips that the
-    network carries along: loss within 1e-3 relative, gradients within 2e-2
-    normwise (bf16 rounding alone moves them 2-10 %)."""
-    _lm()
-    from dataclasses import replace
-
-    from delta_mixers.model import GdnLM, GdnLMConfig
-    cfg = GdnLMConfig(vocab=512, d_model=128, layers=2, heads=2, key_dim=64, value_dim=64,
-                      mlp_width=256, chunk=64)
-    torch.manual_seed(0)
-    fused = GdnLM(cfg, device="cuda")
-    plain = GdnLM(replace(cfg, fused=False), device="cuda")
-    plain.load_state_dict(fused.state_dict())
-    tokens = torch.randint(0, cfg.vocab, (2, 131), generator=_gen(3)).cuda()
-    lf = fused.loss(tokens)
-    lf.backward()
-    lp = plain.loss(tokens)
-    lp.backward()
-    assert abs(lf.item() - lp.item()) <= 1e-3 * abs(lp.item())
-    for (n, a), (_, b) in zip(fused.named_parameters(), plain.named_parameters()):
-        assert a.grad is not None and torch.isfinite(a.grad).all(), n
-        _normwise(f"d{n}", a.grad, b.grad, 2e-2)
