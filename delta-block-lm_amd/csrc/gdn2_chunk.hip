@@ -853,13 +853,19 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
     const int sg = gb->seg[t];
     const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
-    const float4 d0 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb);
-    const float4 d1 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb + 4);
-    float dl[2][4];  // delta at this wave's X tile, used in phase 2
+    // The score adjoint's term c delta (and the norms c needs) only exists when a
+    // score adjoint is given; a.dscores is uniform, so the branches cost nothing.
+    const bool score_adj = a.dscores != nullptr;
+    float4 d0 = make_float4(0.f, 0.f, 0.f, 0.f), d1 = d0;
+    float dl[2][4] = {};  // delta at this wave's X tile, used in phase 2
+    if (score_adj) {
+        d0 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb);
+        d1 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb + 4);
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dl[j][i] = dck[(r0 + i) * D + 16 * (tn0 + j) + acc_col()];
+            for (int i = 0; i < 4; ++i) dl[j][i] = dck[(r0 + i) * D + 16 * (tn0 + j) + acc_col()];
+    }
     const uint16_t *wsrc = a.ck_wt + 2 * (int64_t)ci * D * C + (tid >> 3) * C + 8 * (tid & 7);
     const uint4 wh = *reinterpret_cast<const uint4 *>(wsrc);
     const uint4 wl = *reinterpret_cast<const uint4 *>(wsrc + D * C);
@@ -879,7 +885,7 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
             QGt[(8 * cb + e) * LDB + t] = bf16_bits(gam * qf);
             ksq += kf * kf;
         }
-        sm.kk[cb][t] = ksq;
+        if (score_adj) sm.kk[cb][t] = ksq;
         if (w == 0) {
             gates_derive(sm.gl, G, be, va, sg);
             sm.dsc[t] = dsc;
@@ -907,33 +913,35 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
                                &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq[j]);
         }
     }
-    sm.dd[cb][t] = d0.x * d0.x + d0.y * d0.y + d0.z * d0.z + d0.w * d0.w + d1.x * d1.x +
-                   d1.y * d1.y + d1.z * d1.z + d1.w * d1.w;
+    if (score_adj)
+        sm.dd[cb][t] = d0.x * d0.x + d0.y * d0.y + d0.z * d0.z + d0.w * d0.w + d1.x * d1.x +
+                       d1.y * d1.y + d1.z * d1.z + d1.w * d1.w;
     *reinterpret_cast<uint4 *>(&Wt[(tid >> 3) * LDB + 8 * (tid & 7)]) = wh;
     *reinterpret_cast<uint4 *>(&Wtl[(tid >> 3) * LDB + 8 * (tid & 7)]) = wl;
     __syncthreads();
     // Phase 2: X = P^T dO + diag(c) delta, stored transposed (hi/lo).
     {
-        float cs[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int ss = r0 + i;
-            float kq = 0.f, dq = 0.f;
-#pragma unroll
-            for (int q = 0; q < NW; ++q) {
-                kq += sm.kk[q][ss];
-                dq += sm.dd[q][ss];
-            }
-            const float nk = sqrtf(kq), nd = sqrtf(dq);
-            cs[i] = (nk > 0.f && nd > 0.f) ? sm.dsc[ss] * nk / nd : 0.f;
-        }
         f32x4 x[2] = {zero4(), zero4()};
         gemm2(x, &Pt[(16 * tm) * LDB], dOt, tn0);
         gemm2(x, &Ptl[(16 * tm) * LDB], dOt, tn0);
+        if (score_adj) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int ss = r0 + i;
+                float kq = 0.f, dq = 0.f;
+#pragma unroll
+                for (int q = 0; q < NW; ++q) {
+                    kq += sm.kk[q][ss];
+                    dq += sm.dd[q][ss];
+                }
+                const float nk = sqrtf(kq), nd = sqrtf(dq);
+                const float cs = (nk > 0.f && nd > 0.f) ? sm.dsc[ss] * nk / nd : 0.f;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) x[j][i] += cs * dl[j][i];
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) x[j][i] += cs[i] * dl[j][i];
             store_tile_t_split(&Xt[(16 * (tn0 + j)) * LDB + 16 * tm],
                                &Xtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
         }
@@ -995,6 +1003,9 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
     const int sg = gb->seg[t];
     const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
+    // The score adjoint's terms (c delta in ddelta, c' k in dk, and the norms
+    // behind them) only exist when a score adjoint is given (uniform branches).
+    const bool score_adj = a.dscores != nullptr;
     const uint4 vr = load8(a.v, a.vs, b, tg, h, cb, inb);
     const uint4 trw = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C +
                                                       (tid >> 3) * C + 8 * (tid & 7));
@@ -1008,15 +1019,17 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         put_row8(Ks, t, cb, k8);
         put_row8(dOs, t, cb, d8);
         put_col8(Qt, t, cb, q8);
-        Pack8 kp;
-        kp.u = k8;
-        float ksq = 0.f;
+        if (score_adj) {
+            Pack8 kp;
+            kp.u = k8;
+            float ksq = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float kf = bf16_val(kp.h[e]);
-            ksq += kf * kf;
+            for (int e = 0; e < 8; ++e) {
+                const float kf = bf16_val(kp.h[e]);
+                ksq += kf * kf;
+            }
+            sm.kk[cb][t] = ksq;
         }
-        sm.kk[cb][t] = ksq;
         stage_mat(nullptr, S0b, s0, tid);
         stage_mat(dSt, nullptr, ds, tid);
         const float fr = wave_sum(dot8_bf16(s0, ds));
@@ -1083,24 +1096,26 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         }
         put_row8(Dh, t, cb, ph.u);
         put_row8(Dlo, t, cb, pl.u);
-        sm.dd[cb][t] = dsq;
+        if (score_adj) sm.dd[cb][t] = dsq;
     }
     __syncthreads();
     // Phase D: delta dS^T (-> dlam), ddelta = P^T dO + lam K dS + c delta (-> ddelta^T).
-    float cs[4], ck[4];
+    float cs[4] = {0.f, 0.f, 0.f, 0.f}, ck[4] = {0.f, 0.f, 0.f, 0.f};
+    if (score_adj) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int ss = r0 + i;
-        float kq = 0.f, dq = 0.f;
+        for (int i = 0; i < 4; ++i) {
+            const int ss = r0 + i;
+            float kq = 0.f, dq = 0.f;
 #pragma unroll
-        for (int q = 0; q < NW; ++q) {
-            kq += sm.kk[q][ss];
-            dq += sm.dd[q][ss];
+            for (int q = 0; q < NW; ++q) {
+                kq += sm.kk[q][ss];
+                dq += sm.dd[q][ss];
+            }
+            const float nk = sqrtf(kq), nd = sqrtf(dq);
+            const bool ok = nk > 0.f && nd > 0.f;
+            cs[i] = ok ? sm.dsc[ss] * nk / nd : 0.f;
+            ck[i] = ok ? sm.dsc[ss] * nd / nk : 0.f;
         }
-        const float nk = sqrtf(kq), nd = sqrtf(dq);
-        const bool ok = nk > 0.f && nd > 0.f;
-        cs[i] = ok ? sm.dsc[ss] * nk / nd : 0.f;
-        ck[i] = ok ? sm.dsc[ss] * nd / nk : 0.f;
     }
     // dK accumulates lam (delta dS^T) here, -beta gam dR S0^T in F, the rest in G.
     f32x4 dka[2] = {zero4(), zero4()};
@@ -1124,11 +1139,13 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         gemm2(x, &Ptl[(16 * tm) * LDB], dOt, tn0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            float dh[4], dlo[4];  // delta at this tile: hi + lo rows
-            ld4_rm_tr(Dh, 16 * tm, 16 * (tn0 + j), dh);
-            ld4_rm_tr(Dlo, 16 * tm, 16 * (tn0 + j), dlo);
+            if (score_adj) {
+                float dh[4], dlo[4];  // delta at this tile: hi + lo rows
+                ld4_rm_tr(Dh, 16 * tm, 16 * (tn0 + j), dh);
+                ld4_rm_tr(Dlo, 16 * tm, 16 * (tn0 + j), dlo);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x[j][i] += cs[i] * (dh[i] + dlo[i]);
+                for (int i = 0; i < 4; ++i) x[j][i] += cs[i] * (dh[i] + dlo[i]);
+            }
             store_tile_t_split(&Dd[(16 * (tn0 + j)) * LDB + 16 * tm],
                                &Ddl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
         }
@@ -1228,8 +1245,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         gemm2(y, &MPtl[(16 * tm) * LDB], Qt, tn0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            float kv[4];
-            ld4_bf16(&Kt[(16 * (tn0 + j) + acc_col()) * LDB + r0], kv);
+            float kv[4] = {0.f, 0.f, 0.f, 0.f};
+            if (score_adj) ld4_bf16(&Kt[(16 * (tn0 + j) + acc_col()) * LDB + r0], kv);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tq = c * C + r0 + i;
