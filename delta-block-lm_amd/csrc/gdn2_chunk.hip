@@ -123,6 +123,24 @@ __device__ __forceinline__ Tv wave_scan_add(Tv x) {
     return x;
 }
 
+// Row sums of an accumulator tile: p[i] is this lane's term of row 4(l/16) + i;
+// the sum over the 16 lanes of each DPP row goes to dst[16 tm + row].  An
+// exchange butterfly: across lane bit 3 each lane keeps two rows (rows 0, 1 if
+// the bit is clear, else 2, 3) and sends the other two; across the half-row
+// mirror (which flips lane bit 2) it keeps one of those; two quad steps finish.
+// Lanes with l % 4 == 0 then hold row 2 b3 + b2 and store it.
+__device__ __forceinline__ void row_reduce_store(const float (&p)[4], float *dst, int tm) {
+    const int n = lane_id() & 15;
+    const bool b3 = (n & 8) != 0, b2 = (n & 4) != 0;
+    const float s0 = b3 ? p[0] : p[2], s1 = b3 ? p[1] : p[3];
+    const float a0 = (b3 ? p[2] : p[0]) + dpp<0x128>(s0);  // row_ror:8, lane n ^ 8
+    const float a1 = (b3 ? p[3] : p[1]) + dpp<0x128>(s1);
+    float x = (b2 ? a1 : a0) + dpp<0x141>(b2 ? a0 : a1);  // row_half_mirror
+    x += dpp<0x4E>(x);
+    x += dpp<0xB1>(x);
+    if ((n & 3) == 0) dst[16 * tm + 4 * (lane_id() >> 4) + 2 * b3 + b2] = x;
+}
+
 // Wave 0 (lane == token): decays derived from a gate block.
 __device__ __forceinline__ void gates_derive(GateLds &gl, float G, float beta, float val, int seg) {
     const int t = lane_id();
@@ -639,11 +657,7 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
             for (int i = 0; i < 4; ++i)
                 dck[(16 * tm + acc_row(i)) * D + 16 * (tn0 + j) + acc_col()] = x[j][i];
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            p[i] = row16_sum(p[i]);
-            if (acc_col() == 0) sm.dd[w & 1][16 * tm + acc_row(i)] = p[i];
-        }
+        row_reduce_store(p, sm.dd[w & 1], tm);
     }
     __syncthreads();
     // Phase 3: O = gam Q S0 + P delta, staged through LDS for coalesced stores.
@@ -773,15 +787,6 @@ struct BGradSmem {
 };
 
 __device__ __forceinline__ float4 lds_f4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
-
-// Row partial sums p[i] over this lane's 16 tile columns -> dst[row] (lanes of column 0).
-__device__ __forceinline__ void row_reduce_store(float (&p)[4], float *dst, int tm) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        p[i] = row16_sum(p[i]);
-        if (acc_col() == 0) dst[16 * tm + acc_row(i)] = p[i];
-    }
-}
 
 // Column sum over the 16 rows of a tile (value per lane column) -> all lanes.
 __device__ __forceinline__ float col_reduce(const f32x4 &x) {
@@ -1047,6 +1052,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         lmv[0] = lm.x, lmv[1] = lm.y, lmv[2] = lm.z, lmv[3] = lm.w;
     }
     // Phase A: dO S0^T, lam K dS, KK^T, QK^T in registers; P^T (hi/lo) -> LDS.
+    float gmA[2][4];  // Gam at this wave's tiles, formed here and reused in phase F
     f32x4 dos[2] = {zero4(), zero4()}, kds[2] = {zero4(), zero4()};
     f32x4 kk[2] = {zero4(), zero4()}, qk[2] = {zero4(), zero4()};
     gemm2(dos, &dOs[(16 * tm) * LDB], S0b, tn0);
@@ -1070,7 +1076,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
                 const int tt = 16 * tm + acc_row(i);
                 kds[j][i] *= lmv[i];
                 p[i] += qv[i] * dos[j][i];  // q_t . (dO S0^T)_t
-                pq[i] *= (ss <= tt && rg.seg[i] == sgs) ? __expf(rg.G[i] - Gs) : 0.f;
+                gmA[j][i] = (ss <= tt && rg.seg[i] == sgs) ? __expf(rg.G[i] - Gs) : 0.f;
+                pq[i] *= gmA[j][i];
             }
             store_tile_t_split(&Pt[(16 * (tn0 + j)) * LDB + 16 * tm],
                                &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq);
@@ -1204,14 +1211,11 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int ss = 16 * (tn0 + j) + acc_col();
-            const float Gs = sm.gl.G[ss];
-            const int sgs = sm.gl.seg[ss];
             f32x4 ma, mp, z;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tt = 16 * tm + acc_row(i);
-                const bool same = rg.seg[i] == sgs;
-                const float gm = (ss <= tt && same) ? __expf(rg.G[i] - Gs) : 0.f;
+                const float gm = gmA[j][i];
                 const float dA = ss < tt ? -da[j][i] : 0.f;
                 const float dP = dp[j][i];
                 ma[i] = dA * rg.beta[i] * gm;
