@@ -213,6 +213,34 @@ __device__ __forceinline__ void ld4_rm_tr(const uint16_t *Z, int row0, int col0,
     for (int e = 0; e < 4; ++e) o[e] = bf16_val((uint16_t)v[e]);
 }
 
+// MFMA operand fragment of a tile held in the other orientation: lane
+// (n = l%16, g = l/16) receives Z[r0 + 8g + e][c0 + n], e < 8, i.e. the
+// fragment of the matrix Y[n][r] = Z[r][n] at reduction offset r0 and row block
+// c0.  Two transpose reads of four rows each; like lds_tr16, every lane of the
+// wave runs it.
+__device__ __forceinline__ bf16x8_t frag_tr(const uint16_t *Z, int r0, int c0) {
+    const int l = lane_id(), i = l & 15;
+    const uint16_t *p = Z + (r0 + 8 * (l >> 4) + (i >> 2)) * LDB + c0 + 4 * (i & 3);
+    const v4s x = lds_tr16(p), y = lds_tr16(p + 4 * LDB);
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    const v8s v = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// acc[j] += X[16 rows][0:64] * Y_j[16 rows][0:64]^T with Y_j[n][r] =
+// Z[r][16 (tn0 + j) + n]: the B operand is read across a row-major tile Z.
+__device__ __forceinline__ void gemm2_tr(f32x4 (&acc)[2], const uint16_t *X, const uint16_t *Z,
+                                         int tn0) {
+#pragma unroll
+    for (int r = 0; r < 64; r += 32) {
+        const bf16x8_t x = frag(X, LDB, r);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, frag_tr(Z, r, 16 * (tn0 + j)), acc[j],
+                                                             0, 0, 0);
+    }
+}
+
 // T = (I + A)^-1 for the strictly lower 64x64 A in Af; result in Tf (lower
 // blocks).  Called by all waves; ends with a barrier.  Blocks are 16x16:
 //   1. diagonal blocks T_bb = (I + A_bb)^-1 by forward substitution (waves 0-3,
@@ -796,20 +824,6 @@ __device__ __forceinline__ float col_reduce(const f32x4 &x) {
     return s;
 }
 
-// Stage a 64x64 bf16 matrix S, held transposed (S^T row-major, the checkpoint
-// layout; this thread's part is row j = tid>>3 of S^T, 8 entries), into the
-// tile dstT[j][i] = S[i][j] and the row-major tile dst[i][j] (either may be null).
-__device__ __forceinline__ void stage_mat(uint16_t *dstT, uint16_t *dst, const uint4 v, int tid) {
-    const int j = tid >> 3, i0 = 8 * (tid & 7);
-    if (dstT) *reinterpret_cast<uint4 *>(&dstT[j * LDB + i0]) = v;
-    if (dst) {
-        Pack8 p;
-        p.u = v;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dst[(i0 + e) * LDB + j] = p.h[e];
-    }
-}
-
 __device__ __forceinline__ uint4 load_mat(const uint16_t *src, int tid) {
     return *reinterpret_cast<const uint4 *>(src + (tid >> 3) * D + 8 * (tid & 7));
 }
@@ -978,15 +992,18 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
 //   H  gate gradients: dbeta, and dg by a reverse scan of dG (wave 0)
 __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     __shared__ BGradSmem sm;
-    uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *dOs = sm.slot[2], *Qt = sm.slot[3];
-    uint16_t *Kt = sm.slot[4], *dOt = sm.slot[5], *Vt = sm.slot[6], *Ttb = sm.slot[7];
-    uint16_t *S0b = sm.slot[8], *dSt = sm.slot[9], *dSb = sm.slot[10];
+    // Every input tile is staged once, in the orientation it is stored in (rows
+    // of Q, K, dO, V, T; S0^T and dS^T as checkpointed), and read the other way
+    // with transpose reads.
+    uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *dOs = sm.slot[2];
+    uint16_t *Vr = sm.slot[6], *Tr = sm.slot[7];     // V rows, T rows (T[t][s])
+    uint16_t *S0t = sm.slot[8], *dSt = sm.slot[9];   // S0^T, dS^T rows
     uint16_t *Dh = sm.slot[11], *Dlo = sm.slot[12];  // delta rows (hi/lo)
     uint16_t *Pt = sm.slot[13], *Ptl = sm.slot[14];  // A..D
-    // Later tenants of dead slots.
-    uint16_t *Dd = sm.slot[0], *Ddl = sm.slot[1];  // ddelta^T, D..E
+    // Later tenants of free or dead slots.
+    uint16_t *Dd = sm.slot[3], *Ddl = sm.slot[4];  // ddelta^T, D..E
     uint16_t *dRr = sm.slot[9];                    // dR rows, E..F
-    uint16_t *MA = sm.slot[0], *MAt = sm.slot[1];  // F..G
+    uint16_t *MA = sm.slot[3], *MAt = sm.slot[4];  // F..G
     uint16_t *MP = sm.slot[5], *MPl = sm.slot[6], *MPt = sm.slot[7], *MPtl = sm.slot[10];
     const int tid = threadIdx.x, w = tid >> 6;
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
@@ -1023,7 +1040,6 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         put_row8(Qs, t, cb, q8);
         put_row8(Ks, t, cb, k8);
         put_row8(dOs, t, cb, d8);
-        put_col8(Qt, t, cb, q8);
         if (score_adj) {
             Pack8 kp;
             kp.u = k8;
@@ -1035,8 +1051,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
             }
             sm.kk[cb][t] = ksq;
         }
-        stage_mat(nullptr, S0b, s0, tid);
-        stage_mat(dSt, nullptr, ds, tid);
+        *reinterpret_cast<uint4 *>(&S0t[(tid >> 3) * LDB + 8 * (tid & 7)]) = s0;
+        *reinterpret_cast<uint4 *>(&dSt[(tid >> 3) * LDB + 8 * (tid & 7)]) = ds;
         const float fr = wave_sum(dot8_bf16(s0, ds));
         if (lane_id() == 0) sm.frob[w] = fr;
         if (w == 0) {
@@ -1055,7 +1071,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     float gmA[2][4];  // Gam at this wave's tiles, formed here and reused in phase F
     f32x4 dos[2] = {zero4(), zero4()}, kds[2] = {zero4(), zero4()};
     f32x4 kk[2] = {zero4(), zero4()}, qk[2] = {zero4(), zero4()};
-    gemm2(dos, &dOs[(16 * tm) * LDB], S0b, tn0);
+    gemm2_tr(dos, &dOs[(16 * tm) * LDB], S0t, tn0);  // B[k][v] = S0^T[v][k]
     gemm2(kds, &Ks[(16 * tm) * LDB], dSt, tn0);
     if (tn0 <= tm) {
         gemm2(kk, &Ks[(16 * tm) * LDB], Ks, tn0);
@@ -1069,7 +1085,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
             const float Gs = sm.gl.G[ss];
             const int sgs = sm.gl.seg[ss];
             float qv[4];
-            ld4_bf16(&Qt[(16 * (tn0 + j) + acc_col()) * LDB + r0], qv);
+            ld4_rm_tr(Qs, 16 * tm, 16 * (tn0 + j), qv);
             f32x4 pq = qk[j];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -1085,14 +1101,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         row_reduce_store(p, sm.g1[w & 1], tm);
     }
     {  // second half of the staging: operands of phases D-G that A does not read
-        put_col8(Kt, t, cb, k8);
-        put_col8(dOt, t, cb, d8);
-        put_col8(Vt, t, cb, mask8(vr, on));
-        Pack8 tp;
-        tp.u = trw;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) Ttb[(8 * (tid & 7) + e) * LDB + (tid >> 3)] = tp.h[e];
-        stage_mat(nullptr, dSb, ds, tid);
+        put_row8(Vr, t, cb, mask8(vr, on));
+        *reinterpret_cast<uint4 *>(&Tr[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
         const float x[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
         Pack8 ph, pl;
         float dsq = 0.f;
@@ -1127,13 +1137,13 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     // dK accumulates lam (delta dS^T) here, -beta gam dR S0^T in F, the rest in G.
     f32x4 dka[2] = {zero4(), zero4()};
     {
-        gemm2(dka, &Dh[(16 * tm) * LDB], dSb, tn0);
-        gemm2(dka, &Dlo[(16 * tm) * LDB], dSb, tn0);
+        gemm2_tr(dka, &Dh[(16 * tm) * LDB], dSt, tn0);  // B[k][v] = dS^T[v][k]
+        gemm2_tr(dka, &Dlo[(16 * tm) * LDB], dSt, tn0);
         float p[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             float kv[4];
-            ld4_bf16(&Kt[(16 * (tn0 + j) + acc_col()) * LDB + r0], kv);
+            ld4_rm_tr(Ks, 16 * tm, 16 * (tn0 + j), kv);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 p[i] += kv[i] * dka[j][i];
@@ -1142,8 +1152,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         }
         row_reduce_store(p, sm.dlam[w & 1], tm);
         f32x4 x[2] = {kds[0], kds[1]};
-        gemm2(x, &Pt[(16 * tm) * LDB], dOt, tn0);
-        gemm2(x, &Ptl[(16 * tm) * LDB], dOt, tn0);
+        gemm2_tr(x, &Pt[(16 * tm) * LDB], dOs, tn0);  // B[v][t] = dO[t][v]
+        gemm2_tr(x, &Ptl[(16 * tm) * LDB], dOs, tn0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             if (score_adj) {
@@ -1161,13 +1171,21 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     // Phase E: dR = T^T ddelta -> dV, dbeta (sum_v dR v part), dR rows.
     {
         f32x4 x[2] = {zero4(), zero4()};
-        gemm2(x, &Ttb[(16 * tm) * LDB], Dd, tn0);
-        gemm2(x, &Ttb[(16 * tm) * LDB], Ddl, tn0);
+#pragma unroll
+        for (int r = 0; r < 64; r += 32) {
+            const bf16x8_t tt = frag_tr(Tr, r, 16 * tm);  // A[s][t] = T[t][s]
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint16_t *Yh = &Dd[(16 * (tn0 + j)) * LDB], *Yl = &Ddl[(16 * (tn0 + j)) * LDB];
+                x[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tt, frag(Yh, LDB, r), x[j], 0, 0, 0);
+                x[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tt, frag(Yl, LDB, r), x[j], 0, 0, 0);
+            }
+        }
         float p[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             float vv[4];
-            ld4_bf16(&Vt[(16 * (tn0 + j) + acc_col()) * LDB + r0], vv);
+            ld4_rm_tr(Vr, 16 * tm, 16 * (tn0 + j), vv);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 p[i] += x[j][i] * vv[i];
@@ -1184,13 +1202,13 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     // Phase F: dR S0^T (-> dK; sum_k k dR S0^T -> dbeta and dgam), dA and dP
     // (masked) -> MA, MP (+ transposes), and the gate-gradient partial sums.
     f32x4 drs[2] = {zero4(), zero4()};
-    gemm2(drs, &dRr[(16 * tm) * LDB], S0b, tn0);
+    gemm2_tr(drs, &dRr[(16 * tm) * LDB], S0t, tn0);  // B[k][v] = S0^T[v][k]
     {
         float p2[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             float kv[4];
-            ld4_bf16(&Kt[(16 * (tn0 + j) + acc_col()) * LDB + r0], kv);
+            ld4_rm_tr(Ks, 16 * tm, 16 * (tn0 + j), kv);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 p2[i] += kv[i] * drs[j][i];
@@ -1239,18 +1257,28 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     __syncthreads();
     // Phase G: dQ and dK.
     {
-        f32x4 x[2] = {zero4(), zero4()};
-        gemm2(x, &MP[(16 * tm) * LDB], Kt, tn0);
-        gemm2(x, &MPl[(16 * tm) * LDB], Kt, tn0);
-        f32x4 y[2] = {zero4(), zero4()};
-        gemm2(y, &MA[(16 * tm) * LDB], Kt, tn0);
-        gemm2(y, &MAt[(16 * tm) * LDB], Kt, tn0);
-        gemm2(y, &MPt[(16 * tm) * LDB], Qt, tn0);
-        gemm2(y, &MPtl[(16 * tm) * LDB], Qt, tn0);
+        f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
+#pragma unroll
+        for (int r = 0; r < 64; r += 32) {
+            const bf16x8_t mp = frag(&MP[(16 * tm) * LDB], LDB, r), mpl = frag(&MPl[(16 * tm) * LDB], LDB, r);
+            const bf16x8_t ma = frag(&MA[(16 * tm) * LDB], LDB, r), mat = frag(&MAt[(16 * tm) * LDB], LDB, r);
+            const bf16x8_t pt = frag(&MPt[(16 * tm) * LDB], LDB, r), ptl = frag(&MPtl[(16 * tm) * LDB], LDB, r);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const bf16x8_t kb = frag_tr(Ks, r, 16 * (tn0 + j));  // B[k][s] = K[s][k]
+                const bf16x8_t qb = frag_tr(Qs, r, 16 * (tn0 + j));  // B[k][t] = Q[t][k]
+                x[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mp, kb, x[j], 0, 0, 0);
+                x[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mpl, kb, x[j], 0, 0, 0);
+                y[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ma, kb, y[j], 0, 0, 0);
+                y[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mat, kb, y[j], 0, 0, 0);
+                y[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pt, qb, y[j], 0, 0, 0);
+                y[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ptl, qb, y[j], 0, 0, 0);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             float kv[4] = {0.f, 0.f, 0.f, 0.f};
-            if (score_adj) ld4_bf16(&Kt[(16 * (tn0 + j) + acc_col()) * LDB + r0], kv);
+            if (score_adj) ld4_rm_tr(Ks, 16 * tm, 16 * (tn0 + j), kv);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tq = c * C + r0 + i;
