@@ -241,6 +241,20 @@ __device__ __forceinline__ void gemm2_tr(f32x4 (&acc)[2], const uint16_t *X, con
     }
 }
 
+// acc[j] += X * Y_j^T with the A operand read across a row-major tile Z
+// (X[m][r] = Z[r][m0 + m]) and Y_j the row tile (tn0 + j) of Y.
+__device__ __forceinline__ void gemm2_atr(f32x4 (&acc)[2], const uint16_t *Z, int m0,
+                                          const uint16_t *Y, int tn0) {
+#pragma unroll
+    for (int r = 0; r < 64; r += 32) {
+        const bf16x8_t x = frag_tr(Z, r, m0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                x, frag(Y + (16 * (tn0 + j)) * LDB, LDB, r), acc[j], 0, 0, 0);
+    }
+}
+
 // T = (I + A)^-1 for the strictly lower 64x64 A in Af; result in Tf (lower
 // blocks).  Called by all waves; ends with a barrier.  Blocks are 16x16:
 //   1. diagonal blocks T_bb = (I + A_bb)^-1 by forward substitution (waves 0-3,
@@ -336,7 +350,9 @@ struct OutSmem {
 //   S_C = A S0 + B,  A = gam_63 I - (lam K)^T W,  B = (lam K)^T U.
 __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
     __shared__ PrepSmem sm;
-    uint16_t *Ks = sm.slot[0], *KBGt = sm.slot[1], *KLt = sm.slot[2], *VBt = sm.slot[3];
+    // beta gam K, lam K and beta V are staged as scaled rows; the products that
+    // need them transposed read across them.
+    uint16_t *Ks = sm.slot[0], *KBGs = sm.slot[1], *KLs = sm.slot[2], *VBs = sm.slot[3];
     uint16_t *Tb = sm.slot[0];  // over K once A is formed
     uint16_t *Wt = sm.u.wu[0], *Wtl = sm.u.wu[1], *Ut = sm.u.wu[2], *Utl = sm.u.wu[3];
     const int tid = threadIdx.x, w = tid >> 6;
@@ -369,16 +385,19 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         gb->seg[t] = seg;
     }
     __syncthreads();
-    {  // scaled transposes of K for the W/A products
-        const float be = sm.gl.beta[t], ga = sm.gl.gam[t], la = sm.gl.lam[t];
+    {  // scaled rows of K for the W/A products
+        const float bg = sm.gl.beta[t] * sm.gl.gam[t], la = sm.gl.lam[t];
         Pack8 kp;
         kp.u = k8;
+        uint32_t kb[4], kl[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float kf = bf16_val(kp.h[e]);
-            KBGt[(8 * cb + e) * LDB + t] = bf16_bits(be * ga * kf);
-            KLt[(8 * cb + e) * LDB + t] = bf16_bits(la * kf);
+        for (int e = 0; e < 8; e += 2) {
+            const float k0 = bf16_val(kp.h[e]), k1 = bf16_val(kp.h[e + 1]);
+            kb[e / 2] = bf16_pack2(bg * k0, bg * k1);
+            kl[e / 2] = bf16_pack2(la * k0, la * k1);
         }
+        put_row8(KBGs, t, cb, make_uint4(kb[0], kb[1], kb[2], kb[3]));
+        put_row8(KLs, t, cb, make_uint4(kl[0], kl[1], kl[2], kl[3]));
     }
     // A = strict_lower(beta_t Gam_ts k_t.k_s) in f32 (tiles with tn <= tm only).
     if (tn0 <= tm) {
@@ -415,19 +434,22 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         *reinterpret_cast<uint4 *>(a.ck_t + (int64_t)ci * C * C + r * C + c0) = v;
         *reinterpret_cast<uint4 *>(&Tb[r * LDB + c0]) = v;
     }
-    {  // (beta V)^T for U, written once the inverse no longer needs the time
+    {  // beta V rows for U, written once the inverse no longer needs the time
         const float be = sm.gl.beta[t];
         Pack8 vp;
         vp.u = v8;
+        uint32_t vb[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) VBt[(8 * cb + e) * LDB + t] = bf16_bits(be * bf16_val(vp.h[e]));
+        for (int e = 0; e < 8; e += 2)
+            vb[e / 2] = bf16_pack2(be * bf16_val(vp.h[e]), be * bf16_val(vp.h[e + 1]));
+        put_row8(VBs, t, cb, make_uint4(vb[0], vb[1], vb[2], vb[3]));
     }
     __syncthreads();
     // W = T (beta gam K), U = T (beta V): stored transposed as hi/lo pairs.
     {
         f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
-        gemm2(x, &Tb[(16 * tm) * LDB], KBGt, tn0);
-        gemm2(y, &Tb[(16 * tm) * LDB], VBt, tn0);
+        gemm2_tr(x, &Tb[(16 * tm) * LDB], KBGs, tn0);  // B[k][t] = (beta gam K)[t][k]
+        gemm2_tr(y, &Tb[(16 * tm) * LDB], VBs, tn0);   // B[v][t] = (beta V)[t][v]
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             store_tile_t_split(&Wt[(16 * (tn0 + j)) * LDB + 16 * tm],
@@ -440,12 +462,12 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
     // A = gam_63 I - (lam K)^T W (bf16, row-major), B = (lam K)^T U (f32).
     {
         f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
-        gemm2(x, &KLt[(16 * tm) * LDB], Wt, tn0);
-        gemm2(x, &KLt[(16 * tm) * LDB], Wtl, tn0);
-        gemm2(y, &KLt[(16 * tm) * LDB], Ut, tn0);
-        gemm2(y, &KLt[(16 * tm) * LDB], Utl, tn0);
+        gemm2_atr(x, KLs, 16 * tm, Wt, tn0);  // A[k][t] = (lam K)[t][k]
+        gemm2_atr(x, KLs, 16 * tm, Wtl, tn0);
+        gemm2_atr(y, KLs, 16 * tm, Ut, tn0);
+        gemm2_atr(y, KLs, 16 * tm, Utl, tn0);
         const float gC = sm.gl.gamC;
-        uint16_t *Ac = sm.slot[0], *Mt = sm.slot[1];  // T and (beta gam K)^T are dead
+        uint16_t *Ac = sm.slot[0], *Mt = sm.slot[1];  // T and beta gam K are dead
         float *Bt = a.map_n + (int64_t)ci * D * D;    // B transposed: Bt[col][row]
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -853,7 +875,9 @@ __device__ __forceinline__ void store_grad(void *dst, int64_t idx, float x) {
 // output kernel; bprep builds N for every chunk in parallel.
 __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     __shared__ BPrepSmem sm;
-    uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *QGt = sm.slot[2], *dOt = sm.slot[3];
+    // Tiles are staged as rows (gam Q scaled per token) and read across with
+    // transpose reads where a product needs them transposed.
+    uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *QGs = sm.slot[2], *dOs = sm.slot[3];
     uint16_t *Wt = sm.slot[4], *Wtl = sm.slot[5], *Pt = sm.slot[6], *Ptl = sm.slot[7];
     uint16_t *Xt = sm.slot[0], *Xtl = sm.slot[1];  // over Q/K after phase 1
     const int tid = threadIdx.x, w = tid >> 6;
@@ -896,14 +920,17 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
         kp.u = mask8(kr, on);
         put_row8(Qs, t, cb, qp.u);
         put_row8(Ks, t, cb, kp.u);
-        put_col8(dOt, t, cb, mask8(dor, on));
+        put_row8(dOs, t, cb, mask8(dor, on));
         float ksq = 0.f;
+        uint32_t qg[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float qf = bf16_val(qp.h[e]), kf = bf16_val(kp.h[e]);
-            QGt[(8 * cb + e) * LDB + t] = bf16_bits(gam * qf);
-            ksq += kf * kf;
+        for (int e = 0; e < 8; e += 2) {
+            const float q0 = bf16_val(qp.h[e]), q1 = bf16_val(qp.h[e + 1]);
+            const float k0 = bf16_val(kp.h[e]), k1 = bf16_val(kp.h[e + 1]);
+            qg[e / 2] = bf16_pack2(gam * q0, gam * q1);
+            ksq += k0 * k0 + k1 * k1;
         }
+        put_row8(QGs, t, cb, make_uint4(qg[0], qg[1], qg[2], qg[3]));
         if (score_adj) sm.kk[cb][t] = ksq;
         if (w == 0) {
             gates_derive(sm.gl, G, be, va, sg);
@@ -916,7 +943,14 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     f32x4 yacc[2] = {zero4(), zero4()};
     {
         f32x4 pq[2] = {zero4(), zero4()};
-        gemm2(yacc, &QGt[(16 * tm) * LDB], dOt, tn0);
+#pragma unroll
+        for (int r = 0; r < 64; r += 32) {  // Y[k][v] = sum_t (gam Q)[t][k] dO[t][v]
+            const bf16x8_t x = frag_tr(QGs, r, 16 * tm);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                yacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, frag_tr(dOs, r, 16 * (tn0 + j)),
+                                                                  yacc[j], 0, 0, 0);
+        }
         if (tn0 <= tm) gemm2(pq, &Qs[(16 * tm) * LDB], Ks, tn0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -941,8 +975,8 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     // Phase 2: X = P^T dO + diag(c) delta, stored transposed (hi/lo).
     {
         f32x4 x[2] = {zero4(), zero4()};
-        gemm2(x, &Pt[(16 * tm) * LDB], dOt, tn0);
-        gemm2(x, &Ptl[(16 * tm) * LDB], dOt, tn0);
+        gemm2_tr(x, &Pt[(16 * tm) * LDB], dOs, tn0);  // B[v][t] = dO[t][v]
+        gemm2_tr(x, &Ptl[(16 * tm) * LDB], dOs, tn0);
         if (score_adj) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {

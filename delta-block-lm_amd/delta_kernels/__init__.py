@@ -163,6 +163,9 @@ class _TrainingScan(torch.autograd.Function):
     def forward(ctx, q, k, v, alpha, erase, write, valid, reset, initial, chunk):
         out, final, scores, ck = _training_forward(q, k, v, alpha, erase, write, valid, reset,
                                                    initial, chunk)
+        # Unused outputs reach backward as None (not zero tensors), so the
+        # kernels skip the work of adjoints that are absent.
+        ctx.set_materialize_grads(False)
         ctx.save_for_backward(q, k, v, alpha, erase, write, valid, reset)
         ctx.checkpoint = ck
         ctx.chunk = chunk
@@ -352,6 +355,9 @@ class _ScalarScan(torch.autograd.Function):
     def forward(ctx, q, k, v, beta, g, valid, reset, initial, chunk):
         out, final, scores, ck = gdn_scalar_forward(q, k, v, beta, g, valid, reset, initial,
                                                     chunk)
+        # Unused outputs reach backward as None (not zero tensors), so the
+        # kernels skip the work of adjoints that are absent.
+        ctx.set_materialize_grads(False)
         ctx.save_for_backward(q, k, v, beta, g, valid, reset)
         ctx.checkpoint = ck
         ctx.chunk = chunk

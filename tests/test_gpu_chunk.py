@@ -149,3 +149,26 @@ def test_chunk_backward_full_size_matches_sequential_kernel(dk):
     g16 = run_bwd(dk, p, 16, use_final=False, use_scores=False)
     for name, a, b in zip(("dq", "dk", "dv", "dbeta", "dg"), g64[:5], g16[:5]):
         gate(f"{name} vs sequential", a, host(b), TOL_BF16)
+
+
+@pytest.mark.parametrize("B,T,H", [(2, 200, 2)])
+def test_autograd_passes_absent_adjoints_as_none(dk, B, T, H):
+    """Only the output feeds the loss: autograd hands the backward None for the
+    final-state and score adjoints (no zero tensors), and the gradients equal,
+    bit for bit, the raw backward given explicit zero adjoints."""
+    p = problem(21, B, T, H, masks=True)
+    x = {n: dev(p[n], torch.bfloat16).requires_grad_(True) for n in ("q", "k", "v")}
+    beta, g = dev(p["beta"]).requires_grad_(True), dev(p["g"]).requires_grad_(True)
+    valid, reset, init = dev(p["valid"]), dev(p["reset"]), dev(p["initial"])
+    dO = dev(p["dO"], torch.bfloat16)
+    out, fin, sc = dk.gdn_scalar_scan(x["q"], x["k"], x["v"], beta, g, valid, reset, init)
+    out.backward(dO)
+    _, _, _, ck = dk.gdn_scalar_forward(x["q"].detach(), x["k"].detach(), x["v"].detach(),
+                                        beta.detach(), g.detach(), valid, reset, init, 64)
+    ref = dk.gdn_scalar_backward(x["q"].detach(), x["k"].detach(), x["v"].detach(),
+                                 beta.detach(), g.detach(), valid, reset, ck, 64, dO,
+                                 torch.zeros_like(fin), torch.zeros_like(sc))
+    for name, got, want in (("dq", x["q"].grad, ref[0]), ("dk", x["k"].grad, ref[1]),
+                            ("dv", x["v"].grad, ref[2]), ("dbeta", beta.grad, ref[3]),
+                            ("dg", g.grad, ref[4])):
+        assert torch.equal(got, want), f"{name}: None adjoints differ from zero adjoints"
