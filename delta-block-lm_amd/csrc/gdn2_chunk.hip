@@ -861,10 +861,6 @@ __device__ __forceinline__ float dot8_bf16(const uint4 a, const uint4 b) {
     return s;
 }
 
-__device__ __forceinline__ void store_grad(void *dst, int64_t idx, float x) {
-    reinterpret_cast<uint16_t *>(dst)[idx] = bf16_bits(x);
-}
-
 }  // namespace
 
 // The backward state recurrence is affine too: with
@@ -1039,6 +1035,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     uint16_t *dRr = sm.slot[9];                    // dR rows, E..F
     uint16_t *MA = sm.slot[3], *MAt = sm.slot[4];  // F..G
     uint16_t *MP = sm.slot[5], *MPl = sm.slot[6], *MPt = sm.slot[7], *MPtl = sm.slot[10];
+    uint16_t *dQt = sm.slot[2], *dKt = sm.slot[8], *dVt = sm.slot[11];  // gradients, G..end
     const int tid = threadIdx.x, w = tid >> 6;
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
@@ -1202,7 +1199,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         }
     }
     __syncthreads();
-    // Phase E: dR = T^T ddelta -> dV, dbeta (sum_v dR v part), dR rows.
+    // Phase E: dR = T^T ddelta -> dV (kept for the stores), dbeta (sum_v dR v part), dR rows.
+    f32x4 dvv[2];
     {
         f32x4 x[2] = {zero4(), zero4()};
 #pragma unroll
@@ -1223,10 +1221,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 p[i] += x[j][i] * vv[i];
-                const int tq = c * C + r0 + i;
-                if (a.dv && tq < a.T)
-                    store_grad(a.dv, (((int64_t)b * a.T + tq) * a.H + h) * D + 16 * (tn0 + j) + acc_col(),
-                               sm.gl.val[r0 + i] != 0.f ? rg.beta[i] * x[j][i] : 0.f);
+                dvv[j][i] = sm.gl.val[r0 + i] != 0.f ? rg.beta[i] * x[j][i] : 0.f;
             }
             store_tile_rm(&dRr[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, x[j]);
         }
@@ -1313,21 +1308,36 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         for (int j = 0; j < 2; ++j) {
             float kv[4] = {0.f, 0.f, 0.f, 0.f};
             if (score_adj) ld4_rm_tr(Ks, 16 * tm, 16 * (tn0 + j), kv);
+            f32x4 gq, gk;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int tq = c * C + r0 + i;
                 const bool on = sm.gl.val[r0 + i] != 0.f;
-                const float dq = x[j][i] + rg.gam[i] * dos[j][i];
-                const float dk = y[j][i] + dka[j][i] + ck[i] * kv[i];
-                if (tq < a.T) {
-                    const int64_t o = (((int64_t)b * a.T + tq) * a.H + h) * D + 16 * (tn0 + j) + acc_col();
-                    if (a.dq) store_grad(a.dq, o, on ? dq : 0.f);
-                    if (a.dk) store_grad(a.dk, o, on ? dk : 0.f);
-                }
+                gq[i] = on ? x[j][i] + rg.gam[i] * dos[j][i] : 0.f;
+                gk[i] = on ? y[j][i] + dka[j][i] + ck[i] * kv[i] : 0.f;
             }
+            // Transposed gradient tiles ([channel][token]) in slots phase G does not read.
+            store_tile_t(&dQt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, gq);
+            store_tile_t(&dKt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, gk);
+            store_tile_t(&dVt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, dvv[j]);
         }
     }
     __syncthreads();
+    // dq, dk, dv: lane (token 16 (w%4) + l%16, channels 32 (w/4) + 8 (l/16) ..) reads
+    // its eight channels across the transposed tiles and stores one 16-byte row
+    // piece per gradient.  Every lane runs the transpose reads.
+    {
+        const int l = lane_id();
+        const int tq = c * C + 16 * (w & 3) + (l & 15);
+        const bf16x8_t gq = frag_tr(dQt, 32 * (w >> 2), 16 * (w & 3));
+        const bf16x8_t gk = frag_tr(dKt, 32 * (w >> 2), 16 * (w & 3));
+        const bf16x8_t gv = frag_tr(dVt, 32 * (w >> 2), 16 * (w & 3));
+        if (tq < a.T) {
+            const int64_t o = (((int64_t)b * a.T + tq) * a.H + h) * D + 32 * (w >> 2) + 8 * (l >> 4);
+            if (a.dq) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dq) + o) = gq;
+            if (a.dk) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dk) + o) = gk;
+            if (a.dv) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dv) + o) = gv;
+        }
+    }
     // Phase H: gate gradients (wave 0, lane == token).  With u_t = k_t . (dR S0^T)_t:
     //   dbeta_t = sum dA Gam KK^T + sum_v dR v - gam_t u_t,
     //   dG_t   = row - column sums of Z + gam_t (q_t . (dO S0^T)_t - beta_t u_t) - lam_t dlam_t.
