@@ -690,26 +690,30 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
     }
     *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
     __syncthreads();
-    // Phase 2: delta = T R (-> Dt/Dl over the Q/K slots) and |delta_t|^2.
+    // Phase 2: delta = T R (-> Dt/Dl over the Q/K slots) and |delta_t|^2; delta
+    // itself stays in registers for the checkpoint.
+    f32x4 dlt[2] = {zero4(), zero4()};
     {
-        f32x4 x[2] = {zero4(), zero4()};
-        gemm2(x, &Tb[(16 * tm) * LDB], Rt, tn0);
-        gemm2(x, &Tb[(16 * tm) * LDB], Vt, tn0);
+        gemm2(dlt, &Tb[(16 * tm) * LDB], Rt, tn0);
+        gemm2(dlt, &Tb[(16 * tm) * LDB], Vt, tn0);
         float p[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p[i] = x[0][i] * x[0][i] + x[1][i] * x[1][i];
-        float *dck = a.ck_delta + (int64_t)ci * C * D;  // checkpoint for the backward
+        for (int i = 0; i < 4; ++i) p[i] = dlt[0][i] * dlt[0][i] + dlt[1][i] * dlt[1][i];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < 2; ++j)
             store_tile_t_split(&Dt[(16 * (tn0 + j)) * LDB + 16 * tm],
-                               &Dl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                dck[(16 * tm + acc_row(i)) * D + 16 * (tn0 + j) + acc_col()] = x[j][i];
-        }
+                               &Dl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, dlt[j]);
         row_reduce_store(p, sm.dd[w & 1], tm);
     }
     __syncthreads();
+    // delta (f32, row-major) over the R^T-lo and T slots, dead from here on; it
+    // leaves for the checkpoint as 16-byte row pieces after the last barrier.
+    float *Df = reinterpret_cast<float *>(sm.slot[2]);
+    static_assert(C * LDF * sizeof(float) <= 2 * sizeof(sm.slot[0]), "delta tile spans two slots");
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Df[(16 * tm + acc_row(i)) * LDF + 16 * (tn0 + j) + acc_col()] = dlt[j][i];
     // Phase 3: O = gam Q S0 + P delta, staged through LDS for coalesced stores.
     {
         f32x4 x[2] = {qs[0], qs[1]};
@@ -738,10 +742,13 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
         const float dd = sm.dd[0][t] + sm.dd[1][t];
         a.scores[((int64_t)b * a.T + tg) * a.H + h] = sm.gl.val[t] != 0.f ? sqrtf(kk * dd) : 0.f;
     }
-    if (a.out_bf16) {
-        __syncthreads();
+    __syncthreads();
+    {
         const int r = tid >> 3, c0 = 8 * (tid & 7), tq = t0 + r;
-        if (tq < a.T)
+        float *dck = a.ck_delta + (int64_t)ci * C * D + r * D + c0;  // checkpoint for the backward
+        *reinterpret_cast<float4 *>(dck) = *reinterpret_cast<const float4 *>(&Df[r * LDF + c0]);
+        *reinterpret_cast<float4 *>(dck + 4) = *reinterpret_cast<const float4 *>(&Df[r * LDF + c0 + 4]);
+        if (a.out_bf16 && tq < a.T)
             *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.out) +
                                        (((int64_t)b * a.T + tq) * a.H + h) * D + c0) =
                 *reinterpret_cast<const uint4 *>(&Os[r * LDB + c0]);
