@@ -38,7 +38,6 @@ constexpr int D = CHUNK_D;
 constexpr int NW = 8, NT = 64 * NW;
 constexpr int LDB = 72;  // bf16 row stride of a 64x64 LDS tile
 constexpr int LDF = 68;  // fp32 row stride
-constexpr int LDX = 17;
 constexpr int TILE = 64 * LDB;
 
 struct GateLds {
@@ -261,7 +260,9 @@ __device__ __forceinline__ void gemm2_atr(f32x4 (&acc)[2], const uint16_t *Z, in
 //      four lanes per column share each row's dot product);
 //   2. T_10 = -T_11 A_10 T_00 and T_32 = -T_33 A_32 T_22;
 //   3. T_21 (32x32, blocks r = 2,3 x c = 0,1) = -T_22(32) A_21(32) T_11(32).
-__device__ void ut_inverse(const float *Af, float *Tf, float (*Xs)[16 * LDX], int w) {
+// Products chain through registers (the second factor of each step is an
+// accumulator tile), so the three steps take three barriers.
+__device__ void ut_inverse(const float *Af, float *Tf, int w) {
     const int l = lane_id();
     if (w < 4) {
         // Lane (col, part) holds rows part, part+4, part+8, part+12 of column col;
@@ -290,35 +291,34 @@ __device__ void ut_inverse(const float *Af, float *Tf, float (*Xs)[16 * LDX], in
     __syncthreads();
     auto blkA = [&](int r, int c) { return Af + (16 * r) * LDF + 16 * c; };
     auto blkT = [&](int r, int c) { return Tf + (16 * r) * LDF + 16 * c; };
-    if (w < 2) {  // X = A_{2w+1,2w} T_{2w,2w}
-        f32x4 x = zero4();
-        mm16_f32(x, blkA(2 * w + 1, 2 * w), LDF, blkT(2 * w, 2 * w), LDF);
+    // acc += Z[16x16] Y with Y an accumulator tile: instruction i reduces over
+    // Y's rows 4(l/16) + i (the rows lane l holds), Z read at the same columns.
+    auto mm_acc = [&](f32x4 &acc, const float *Z, const f32x4 &Y) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) Xs[w][acc_row(i) * LDX + acc_col()] = x[i];
-    }
-    __syncthreads();
-    if (w < 2) {  // T_{2w+1,2w} = -T_{2w+1,2w+1} X
-        f32x4 y = zero4();
-        mm16_f32(y, blkT(2 * w + 1, 2 * w + 1), LDF, Xs[w], LDX);
+        for (int i = 0; i < 4; ++i)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Z[(l & 15) * LDF + 4 * (l >> 4) + i], Y[i], acc,
+                                                       0, 0, 0);
+    };
+    if (w < 2) {  // T_{2w+1,2w} = -T_{2w+1,2w+1} (A_{2w+1,2w} T_{2w,2w})
+        f32x4 x = zero4(), y = zero4();
+        mm16_f32(x, blkA(2 * w + 1, 2 * w), LDF, blkT(2 * w, 2 * w), LDF);
+        mm_acc(y, blkT(2 * w + 1, 2 * w + 1), x);
         float *dst = blkT(2 * w + 1, 2 * w);
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[acc_row(i) * LDF + acc_col()] = -y[i];
     }
     __syncthreads();
-    const int r = 2 + (w >> 1), c = w & 1;
-    if (w < 4) {  // Y_rc = sum_{m=c..1} A_rm T_mc
-        f32x4 x = zero4();
-        for (int m = c; m < 2; ++m) mm16_f32(x, blkA(r, m), LDF, blkT(m, c), LDF);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) Xs[w][acc_row(i) * LDX + acc_col()] = x[i];
-    }
-    __syncthreads();
-    if (w < 4) {  // T_rc = -sum_{m=2..r} T_rm Y_mc
-        f32x4 y = zero4();
-        for (int m = 2; m <= r; ++m) mm16_f32(y, blkT(r, m), LDF, Xs[2 * (m - 2) + c], LDX);
+    if (w < 4) {  // T_rc = -sum_{m=2..r} T_rm Y_mc, Y_mc = sum_{m'=c..1} A_mm' T_m'c (own Y's)
+        const int r = 2 + (w >> 1), c = w & 1;
+        f32x4 y2 = zero4(), y3 = zero4(), t = zero4();
+        for (int m = c; m < 2; ++m) mm16_f32(y2, blkA(2, m), LDF, blkT(m, c), LDF);
+        if (r == 3)
+            for (int m = c; m < 2; ++m) mm16_f32(y3, blkA(3, m), LDF, blkT(m, c), LDF);
+        mm_acc(t, blkT(r, 2), y2);
+        if (r == 3) mm_acc(t, blkT(3, 3), y3);
         float *dst = blkT(r, c);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dst[acc_row(i) * LDF + acc_col()] = -y[i];
+        for (int i = 0; i < 4; ++i) dst[acc_row(i) * LDF + acc_col()] = -t[i];
     }
     __syncthreads();
 }
@@ -329,7 +329,6 @@ struct PrepSmem {
         struct {
             float Af[C * LDF];
             float Tf[C * LDF];
-            float Xs[4][16 * LDX];
         } inv;
         uint16_t wu[4][TILE];  // W^T hi/lo, U^T hi/lo once the inverse is done
     } u;
@@ -419,7 +418,7 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         }
     }
     __syncthreads();
-    ut_inverse(sm.u.inv.Af, sm.u.inv.Tf, sm.u.inv.Xs, w);
+    ut_inverse(sm.u.inv.Af, sm.u.inv.Tf, w);
     // T (bf16, row-major, zero above the diagonal): LDS operand and checkpoint.
     {
         const int r = tid >> 3, c0 = 8 * (tid & 7);
