@@ -22,7 +22,6 @@ struct GateBlock {
 //   T      (I + A)^-1, bf16 row-major
 //   gate   GateBlock
 //   delta  the chunk's edits delta[t][v], f32 row-major
-//   Wt     W^T = (T diag(beta gam) K)^T as a bf16 hi/lo pair, row-major
 //   Mt     the adjoint map M = A_c^T, bf16 row-major
 // plus the forward state map S_next = A_c S + B_c (A_c bf16 row-major, B_c f32
 // transposed), read only by the forward state scan.  Transposed f32 matrices
@@ -31,11 +30,10 @@ constexpr size_t CK_STATE_BYTES = CHUNK_D * CHUNK_D * sizeof(uint16_t);
 constexpr size_t CK_T_BYTES = CHUNK * CHUNK * sizeof(uint16_t);
 constexpr size_t CK_GATE_BYTES = sizeof(GateBlock);
 constexpr size_t CK_DELTA_BYTES = CHUNK * CHUNK_D * sizeof(float);
-constexpr size_t CK_WT_BYTES = 2 * CHUNK_D * CHUNK * sizeof(uint16_t);
 constexpr size_t CK_MAP_M_BYTES = CHUNK_D * CHUNK_D * sizeof(uint16_t);
 constexpr size_t CK_MAP_N_BYTES = CHUNK_D * CHUNK_D * sizeof(float);
 constexpr size_t CK_CHUNK_BYTES = CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES + CK_DELTA_BYTES +
-                                  CK_WT_BYTES + 2 * CK_MAP_M_BYTES + CK_MAP_N_BYTES;
+                                  2 * CK_MAP_M_BYTES + CK_MAP_N_BYTES;
 // Backward workspace per chunk: dS at the chunk end (bf16, transposed) and N of
 // the adjoint map (f32, transposed).
 constexpr size_t WS_CHUNK_BYTES = CK_STATE_BYTES + CK_MAP_N_BYTES;
@@ -55,7 +53,6 @@ struct ChunkArgs {
     uint16_t *ck_t;
     GateBlock *ck_gate;
     float *ck_delta;
-    uint16_t *ck_wt;   // W^T hi, then W^T lo
     uint16_t *ck_mt;   // adjoint map M = A_c^T
     uint16_t *map_m;   // forward state map A_c
     float *map_n;      // forward state map B_c^T
@@ -97,8 +94,6 @@ inline void chunk_bind_checkpoint(ChunkArgs &a, void *ck) {
     p += n * CK_GATE_BYTES;
     a.ck_delta = reinterpret_cast<float *>(p);
     p += n * CK_DELTA_BYTES;
-    a.ck_wt = reinterpret_cast<uint16_t *>(p);
-    p += n * CK_WT_BYTES;
     a.ck_mt = reinterpret_cast<uint16_t *>(p);
     p += n * CK_MAP_M_BYTES;
     a.map_m = reinterpret_cast<uint16_t *>(p);

@@ -481,16 +481,14 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         }
     }
     __syncthreads();
-    // Rows out: A_c (forward state map), M = A_c^T (adjoint map), W^T hi and lo.
+    // Rows out: A_c (forward state map) and M = A_c^T (adjoint map).  W is not
+    // checkpointed: bprep forms it again from T and K.
     {
         const int r = tid >> 3, c0 = 8 * (tid & 7);
         const int64_t o = (int64_t)ci * D * D + r * D + c0;
         const uint16_t *Ac = sm.slot[0], *Mt = sm.slot[1];
         *reinterpret_cast<uint4 *>(a.map_m + o) = *reinterpret_cast<const uint4 *>(&Ac[r * LDB + c0]);
         *reinterpret_cast<uint4 *>(a.ck_mt + o) = *reinterpret_cast<const uint4 *>(&Mt[r * LDB + c0]);
-        uint16_t *wt = a.ck_wt + 2 * (int64_t)ci * D * C + r * C + c0;
-        *reinterpret_cast<uint4 *>(wt) = *reinterpret_cast<const uint4 *>(&Wt[r * LDB + c0]);
-        *reinterpret_cast<uint4 *>(wt + D * C) = *reinterpret_cast<const uint4 *>(&Wtl[r * LDB + c0]);
     }
 }
 
@@ -873,15 +871,17 @@ __device__ __forceinline__ float dot8_bf16(const uint4 a, const uint4 b) {
 //   X = P^T dO + diag(c) delta,  Y = (gam Q)^T dO,  W = T diag(beta gam) K,
 //   ddelta = X + diag(lam) K dS_C  and  dS0 = gam_63 dS_C + Y - W^T ddelta,
 // so dS0 = M dS_C + N with M = gam_63 I - W^T diag(lam) K = A_c^T and
-// N = Y - W^T X.  M and W^T come from the forward prep, delta from the forward
-// output kernel; bprep builds N for every chunk in parallel.
+// N = Y - W^T X.  M and T come from the forward prep, delta from the forward
+// output kernel; bprep forms W = T (beta gam K) again (the same operands and
+// products as prep, so the same bits) and builds N for every chunk in parallel.
 __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     __shared__ BPrepSmem sm;
     // Tiles are staged as rows (gam Q scaled per token) and read across with
     // transpose reads where a product needs them transposed.
     uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *QGs = sm.slot[2], *dOs = sm.slot[3];
-    uint16_t *Wt = sm.slot[4], *Wtl = sm.slot[5], *Pt = sm.slot[6], *Ptl = sm.slot[7];
+    uint16_t *Tb = sm.slot[4], *KBGs = sm.slot[5], *Pt = sm.slot[6], *Ptl = sm.slot[7];
     uint16_t *Xt = sm.slot[0], *Xtl = sm.slot[1];  // over Q/K after phase 1
+    uint16_t *Wt = sm.slot[4], *Wtl = sm.slot[5];  // over T and beta gam K after phase 1
     const int tid = threadIdx.x, w = tid >> 6;
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
@@ -890,11 +890,13 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     const GateBlock *gb = a.ck_gate + ci;
     const float *dck = a.ck_delta + (int64_t)ci * C * D;
     const int r0 = 16 * tm + 4 * (lane_id() >> 4);
-    // Loads in order of use: phase 1's operands, then delta (phase 2), then W^T
-    // (phase 3); each later group is written to LDS after the phase before it.
+    // Loads in order of use: phase 1's operands (T among them), then delta
+    // (phase 2); W is formed in phase 1 and written to LDS in phase 2.
     const uint4 qr = load8(a.q, a.qs, b, tg, h, cb, inb);
     const uint4 kr = load8(a.k, a.ks, b, tg, h, cb, inb);
     const uint4 dor = a.dout ? load8(a.dout, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
+    const uint4 trow = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C +
+                                                         (tid >> 3) * C + 8 * (tid & 7));
     const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
     const int sg = gb->seg[t];
     const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
@@ -911,12 +913,9 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) dl[j][i] = dck[(r0 + i) * D + 16 * (tn0 + j) + acc_col()];
     }
-    const uint16_t *wsrc = a.ck_wt + 2 * (int64_t)ci * D * C + (tid >> 3) * C + 8 * (tid & 7);
-    const uint4 wh = *reinterpret_cast<const uint4 *>(wsrc);
-    const uint4 wl = *reinterpret_cast<const uint4 *>(wsrc + D * C);
     {
         const bool on = va != 0.f;
-        const float gam = sg == 0 ? __expf(G) : 0.f;
+        const float gam = sg == 0 ? __expf(G) : 0.f, bg = be * gam;
         Pack8 qp, kp;
         qp.u = mask8(qr, on);
         kp.u = mask8(kr, on);
@@ -924,15 +923,18 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
         put_row8(Ks, t, cb, kp.u);
         put_row8(dOs, t, cb, mask8(dor, on));
         float ksq = 0.f;
-        uint32_t qg[4];
+        uint32_t qg[4], kb[4];
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
             const float q0 = bf16_val(qp.h[e]), q1 = bf16_val(qp.h[e + 1]);
             const float k0 = bf16_val(kp.h[e]), k1 = bf16_val(kp.h[e + 1]);
             qg[e / 2] = bf16_pack2(gam * q0, gam * q1);
+            kb[e / 2] = bf16_pack2(bg * k0, bg * k1);
             ksq += k0 * k0 + k1 * k1;
         }
         put_row8(QGs, t, cb, make_uint4(qg[0], qg[1], qg[2], qg[3]));
+        put_row8(KBGs, t, cb, make_uint4(kb[0], kb[1], kb[2], kb[3]));
+        *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trow;
         if (score_adj) sm.kk[cb][t] = ksq;
         if (w == 0) {
             gates_derive(sm.gl, G, be, va, sg);
@@ -941,8 +943,10 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     }
     __syncthreads();
     const RowGates rg = row_gates(sm.gl, tm);
-    // Phase 1: P (causal tiles, masked) -> P^T hi/lo; Y = (gam Q)^T dO in registers.
-    f32x4 yacc[2] = {zero4(), zero4()};
+    // Phase 1: P (causal tiles, masked) -> P^T hi/lo; Y = (gam Q)^T dO and
+    // W = T (beta gam K) in registers.
+    f32x4 yacc[2] = {zero4(), zero4()}, wacc[2] = {zero4(), zero4()};
+    gemm2_tr(wacc, &Tb[(16 * tm) * LDB], KBGs, tn0);  // B[k][t] = (beta gam K)[t][k]
     {
         f32x4 pq[2] = {zero4(), zero4()};
 #pragma unroll
@@ -971,10 +975,12 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     if (score_adj)
         sm.dd[cb][t] = d0.x * d0.x + d0.y * d0.y + d0.z * d0.z + d0.w * d0.w + d1.x * d1.x +
                        d1.y * d1.y + d1.z * d1.z + d1.w * d1.w;
-    *reinterpret_cast<uint4 *>(&Wt[(tid >> 3) * LDB + 8 * (tid & 7)]) = wh;
-    *reinterpret_cast<uint4 *>(&Wtl[(tid >> 3) * LDB + 8 * (tid & 7)]) = wl;
     __syncthreads();
-    // Phase 2: X = P^T dO + diag(c) delta, stored transposed (hi/lo).
+    // Phase 2: X = P^T dO + diag(c) delta, stored transposed (hi/lo); W^T hi/lo.
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        store_tile_t_split(&Wt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                           &Wtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, wacc[j]);
     {
         f32x4 x[2] = {zero4(), zero4()};
         gemm2_tr(x, &Pt[(16 * tm) * LDB], dOs, tn0);  // B[v][t] = dO[t][v]
