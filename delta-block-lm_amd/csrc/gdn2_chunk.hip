@@ -1029,7 +1029,7 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
 //   A  dO S0^T, K dS, KK^T, QK^T (registers); P^T -> LDS
 //   D  delta dS^T (-> dlam); ddelta = P^T dO + lam K dS + c delta -> LDS
 //   E  dR = T^T ddelta -> dV, dbeta (sum dR v), dR rows
-//   F  dR S0^T (-> dK, dbeta, dgam); dA, dP masked -> MA, MP (+ transposes)
+//   F  dR S0^T (-> dK, dbeta, dgam); dA, dP masked -> MA^T, MP^T
 //   G  dQ = MP K + gam dO S0^T;  dK = (MA + MA^T) K + MP^T Q + ...
 //   H  gate gradients: dbeta, and dg by a reverse scan of dG (wave 0)
 __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
@@ -1045,8 +1045,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     // Later tenants of free or dead slots.
     uint16_t *Dd = sm.slot[3], *Ddl = sm.slot[4];  // ddelta^T, D..E
     uint16_t *dRr = sm.slot[9];                    // dR rows, E..F
-    uint16_t *MA = sm.slot[3], *MAt = sm.slot[4];  // F..G
-    uint16_t *MP = sm.slot[5], *MPl = sm.slot[6], *MPt = sm.slot[7], *MPtl = sm.slot[10];
+    // F..G: MA and MP are stored transposed only; phase G reads them both ways.
+    uint16_t *MAt = sm.slot[4], *MPt = sm.slot[7], *MPtl = sm.slot[10];
     uint16_t *dQt = sm.slot[2], *dKt = sm.slot[8], *dVt = sm.slot[11];  // gradients, G..end
     const int tid = threadIdx.x, w = tid >> 6;
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
@@ -1241,7 +1241,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     }
     __syncthreads();
     // Phase F: dR S0^T (-> dK; sum_k k dR S0^T -> dbeta and dgam), dA and dP
-    // (masked) -> MA, MP (+ transposes), and the gate-gradient partial sums.
+    // (masked) -> MA^T, MP^T, and the gate-gradient partial sums.
     f32x4 drs[2] = {zero4(), zero4()};
     gemm2_tr(drs, &dRr[(16 * tm) * LDB], S0t, tn0);  // B[k][v] = S0^T[v][k]
     {
@@ -1283,10 +1283,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
                 z[i] = (dA * rg.beta[i] * kk[j][i] + dP * qk[j][i]) * gm;
                 pz[i] += z[i];
             }
-            store_tile_rm(&MA[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, ma);
             store_tile_t(&MAt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, ma);
-            store_tile_rm_split(&MP[(16 * tm) * LDB + 16 * (tn0 + j)],
-                                &MPl[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, mp);
             store_tile_t_split(&MPt[(16 * (tn0 + j)) * LDB + 16 * tm],
                                &MPtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, mp);
             const float zc = col_reduce(z);
@@ -1301,8 +1298,9 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
 #pragma unroll
         for (int r = 0; r < 64; r += 32) {
-            const bf16x8_t mp = frag(&MP[(16 * tm) * LDB], LDB, r), mpl = frag(&MPl[(16 * tm) * LDB], LDB, r);
-            const bf16x8_t ma = frag(&MA[(16 * tm) * LDB], LDB, r), mat = frag(&MAt[(16 * tm) * LDB], LDB, r);
+            // MP and MA rows, read across their transposes.
+            const bf16x8_t mp = frag_tr(MPt, r, 16 * tm), mpl = frag_tr(MPtl, r, 16 * tm);
+            const bf16x8_t ma = frag_tr(MAt, r, 16 * tm), mat = frag(&MAt[(16 * tm) * LDB], LDB, r);
             const bf16x8_t pt = frag(&MPt[(16 * tm) * LDB], LDB, r), ptl = frag(&MPtl[(16 * tm) * LDB], LDB, r);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
