@@ -617,7 +617,7 @@ __global__ void __launch_bounds__(64) affine_scan_kernel(AffineArgs p) {
 __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
     __shared__ OutSmem sm;
     uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *Vt = sm.slot[2], *Tb = sm.slot[3];
-    uint16_t *St = sm.slot[4], *Rt = sm.slot[5], *P = sm.slot[6], *Pl = sm.slot[7];
+    uint16_t *St = sm.slot[4], *Rt = sm.slot[5], *Pt = sm.slot[6], *Ptl = sm.slot[7];  // P^T hi/lo
     uint16_t *Dt = sm.slot[0], *Dl = sm.slot[1];  // over Q/K after phase 1
     uint16_t *Os = sm.slot[4];                    // over S0^T after phase 1
     const int tid = threadIdx.x, w = tid >> 6;
@@ -681,8 +681,8 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
                 pq[j][i] *= (ss <= tt && rg.seg[i] == sgs) ? __expf(rg.G[i] - Gs) : 0.f;
             }
             store_tile_t_split(&Rt[(16 * (tn0 + j)) * LDB + 16 * tm], vt, LDB, x[j]);
-            store_tile_rm_split(&P[(16 * tm) * LDB + 16 * (tn0 + j)],
-                                &Pl[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, pq[j]);
+            store_tile_t_split(&Pt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq[j]);
         }
     }
     *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
@@ -714,9 +714,9 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
     // Phase 3: O = gam Q S0 + P delta, staged through LDS for coalesced stores.
     {
         f32x4 x[2] = {qs[0], qs[1]};
-        gemm2(x, &P[(16 * tm) * LDB], Dt, tn0);
-        gemm2(x, &P[(16 * tm) * LDB], Dl, tn0);
-        gemm2(x, &Pl[(16 * tm) * LDB], Dt, tn0);
+        gemm2_atr(x, Pt, 16 * tm, Dt, tn0);  // A[t][s] = P^T[s][t]
+        gemm2_atr(x, Pt, 16 * tm, Dl, tn0);
+        gemm2_atr(x, Ptl, 16 * tm, Dt, tn0);
         if (a.out_bf16) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) store_tile_rm(&Os[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, x[j]);
