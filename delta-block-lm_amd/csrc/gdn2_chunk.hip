@@ -466,7 +466,7 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         gemm2_atr(y, KLs, 16 * tm, Ut, tn0);
         gemm2_atr(y, KLs, 16 * tm, Utl, tn0);
         const float gC = sm.gl.gamC;
-        uint16_t *Ac = sm.slot[0], *Mt = sm.slot[1];  // T and beta gam K are dead
+        uint16_t *Mt = sm.slot[1];  // A_c^T over beta gam K, which is dead
         float *Bt = a.map_n + (int64_t)ci * D * D;    // B transposed: Bt[col][row]
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -474,21 +474,24 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
             f32x4 am;
 #pragma unroll
             for (int i = 0; i < 4; ++i) am[i] = (16 * tm + acc_row(i) == cc ? gC : 0.f) - x[j][i];
-            store_tile_rm(&Ac[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, am);
             store_tile_t(&Mt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, am);
             *reinterpret_cast<float4 *>(&Bt[cc * D + 16 * tm + acc_row(0)]) =
                 make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
         }
     }
     __syncthreads();
-    // Rows out: A_c (forward state map) and M = A_c^T (adjoint map).  W is not
-    // checkpointed: bprep forms it again from T and K.
+    // Rows out: M = A_c^T (adjoint map) row by row, and A_c (forward state map)
+    // read across it: lane (row 16 (w%4) + l%16, columns 32 (w/4) + 8 (l/16) ..)
+    // stores one 16-byte row piece.  Every lane runs the transpose reads.  W is
+    // not checkpointed: bprep forms it again from T and K.
     {
-        const int r = tid >> 3, c0 = 8 * (tid & 7);
-        const int64_t o = (int64_t)ci * D * D + r * D + c0;
-        const uint16_t *Ac = sm.slot[0], *Mt = sm.slot[1];
-        *reinterpret_cast<uint4 *>(a.map_m + o) = *reinterpret_cast<const uint4 *>(&Ac[r * LDB + c0]);
-        *reinterpret_cast<uint4 *>(a.ck_mt + o) = *reinterpret_cast<const uint4 *>(&Mt[r * LDB + c0]);
+        const int r = tid >> 3, c0 = 8 * (tid & 7), l = lane_id();
+        const uint16_t *Mt = sm.slot[1];
+        const bf16x8_t ar = frag_tr(Mt, 32 * (w >> 2), 16 * (w & 3));
+        *reinterpret_cast<uint4 *>(a.ck_mt + (int64_t)ci * D * D + r * D + c0) =
+            *reinterpret_cast<const uint4 *>(&Mt[r * LDB + c0]);
+        *reinterpret_cast<bf16x8_t *>(a.map_m + (int64_t)ci * D * D + (16 * (w & 3) + (l & 15)) * D +
+                                      32 * (w >> 2) + 8 * (l >> 4)) = ar;
     }
 }
 
