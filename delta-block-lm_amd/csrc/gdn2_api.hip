@@ -63,7 +63,10 @@ using namespace gdn2;
 namespace {
 
 // Stage timing (gdn2_stage_timing): six stages, an event pair each; the
-// forward records pairs 0-2, the backward pairs 3-5.
+// forward records pairs 0-2, the backward pairs 3-5.  A measurement hook for
+// benchmarks only: the events and flags below are process-wide (not thread
+// safe), and no event is recorded on a stream that is being captured, so a
+// graph never holds them.
 constexpr int kStages = 6;
 const char *const kStageNames[kStages] = {"chunk_prep", "state_scan", "chunk_out",
                                           "chunk_bprep", "adjoint_scan", "chunk_bgrad"};
@@ -72,8 +75,11 @@ bool g_stage_ready = false;  // events created
 bool g_stage_on = false;
 bool g_stage_ran[kStages];
 
-const hipEvent_t *stage_events(int first_stage) {
+const hipEvent_t *stage_events(int first_stage, hipStream_t stream) {
     if (!g_stage_on) return nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+        return nullptr;
     for (int i = 0; i < 3; ++i) g_stage_ran[first_stage + i] = true;
     return g_stage_ev + 2 * first_stage;
 }
@@ -160,6 +166,15 @@ SeqArgs seq_args(const gdn2_shape *s, const gdn2_view *q, const gdn2_view *k, co
 }
 
 }  // namespace
+
+static int scalar_backward_impl(const gdn2_shape *shape, int chunk, const gdn2_view *q,
+                                const gdn2_view *k, const gdn2_view *v, const gdn2_view *beta,
+                                const gdn2_view *g, const gdn2_view *valid,
+                                const gdn2_view *reset, const void *checkpoint,
+                                size_t checkpoint_bytes, const gdn2_view *d_output,
+                                const float *d_final_state, const float *d_scores, void *dq,
+                                void *dk, void *dv, float *dbeta, float *dg, float *d_initial,
+                                void *workspace, size_t workspace_bytes, void *stream);
 
 extern "C" {
 
@@ -400,7 +415,7 @@ int gdn_scalar_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q, cons
         c.final_state = final_state;
         c.scores = scores;
         chunk_bind_checkpoint(c, checkpoint);
-        return launch_status(launch_chunk_fwd(c, (hipStream_t)stream, stage_events(0)),
+        return launch_status(launch_chunk_fwd(c, (hipStream_t)stream, stage_events(0, (hipStream_t)stream)),
                              "gdn_scalar_scan");
     }
     SeqArgs a = seq_args(shape, q, k, v, beta, beta, beta, valid, reset);
@@ -425,6 +440,21 @@ int gdn_scalar_backward(const gdn2_shape *shape, int chunk, const gdn2_view *q,
                         const float *d_scores, void *dq, void *dk, void *dv, float *dbeta,
                         float *dg, float *d_initial, void *workspace, size_t workspace_bytes,
                         void *stream) {
+    return scalar_backward_impl(shape, chunk, q, k, v, beta, g, valid, reset, checkpoint,
+                                checkpoint_bytes, d_output, d_final_state, d_scores, dq, dk, dv,
+                                dbeta, dg, d_initial, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"
+
+static int scalar_backward_impl(const gdn2_shape *shape, int chunk, const gdn2_view *q,
+                                const gdn2_view *k, const gdn2_view *v, const gdn2_view *beta,
+                                const gdn2_view *g, const gdn2_view *valid,
+                                const gdn2_view *reset, const void *checkpoint,
+                                size_t checkpoint_bytes, const gdn2_view *d_output,
+                                const float *d_final_state, const float *d_scores, void *dq,
+                                void *dk, void *dv, float *dbeta, float *dg, float *d_initial,
+                                void *workspace, size_t workspace_bytes, void *stream) {
     GDN2_TRY(check_shape(shape));
     GDN2_TRY(check_chunk(chunk));
     GDN2_TRY(check_scalar_inputs(q, k, v, beta, g, valid, reset));
@@ -457,7 +487,7 @@ int gdn_scalar_backward(const gdn2_shape *shape, int chunk, const gdn2_view *q,
         c.dbeta = dbeta;
         c.dg = dg;
         c.dinitial = d_initial;
-        return launch_status(launch_chunk_bwd(c, (hipStream_t)stream, stage_events(3)),
+        return launch_status(launch_chunk_bwd(c, (hipStream_t)stream, stage_events(3, (hipStream_t)stream)),
                              "gdn_scalar_backward");
     }
     SeqArgs a = seq_args(shape, q, k, v, beta, beta, beta, valid, reset);
@@ -478,6 +508,8 @@ int gdn_scalar_backward(const gdn2_shape *shape, int chunk, const gdn2_view *q,
     return launch_status(launch_seq_bwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
                          "gdn_scalar_backward");
 }
+
+extern "C" {
 
 int gdn2_stage_timing(int enable) {
     if (enable && !g_stage_ready) {

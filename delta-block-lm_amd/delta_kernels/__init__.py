@@ -72,6 +72,14 @@ def _stream(t: torch.Tensor):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
+def _rows_aligned(t: torch.Tensor) -> bool:
+    """True when every token row of t is a 16-byte aligned run of unit-stride
+    channels: the form in which the chunk kernels read sequence rows."""
+    el = t.element_size()
+    return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+            and all((s * el) % 16 == 0 for s in t.stride()[:-1]))
+
+
 def _mask(m: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
     if m.dtype != torch.float32:
         m = m.to(torch.float32)
@@ -334,8 +342,13 @@ def gdn_scalar_backward(q, k, v, beta, g, valid, reset, checkpoint, chunk: int =
     dinit = torch.empty((B, H, K, V), dtype=torch.float32, device=dev)
     nws = L.gdn_scalar_workspace_bytes(ctypes.byref(shape), chunk)
     ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=dev)
-    if d_output is not None and d_output.dtype != q.dtype:
-        d_output = d_output.to(q.dtype)
+    if d_output is not None:
+        if d_output.dtype != q.dtype:
+            d_output = d_output.to(q.dtype)
+        if not _rows_aligned(d_output):
+            # Autograd often hands over an expanded (stride-0) upstream, e.g.
+            # from out.sum(); the chunk kernels read 16-byte row pieces.
+            d_output = d_output.contiguous()
     dfin = None if d_final_state is None else d_final_state.float().contiguous()
     dsc = None if d_scores is None else d_scores.float().contiguous()
     views = [_view(x) for x in (q, k, v, beta, g, valid, reset)]

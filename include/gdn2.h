@@ -158,7 +158,12 @@ GDN2_API int gdn2_backward(const gdn2_shape *shape, const gdn2_view *q, const gd
  * (g is the log decay, finite).  No counterpart entry exists in the reference
  * (it reaches this case only through the channel-wise op with broadcast
  * gates); this is the chunk-WY fast path the north-star benchmark measures.
- * chunk must be 64 (the computational chunk of the MFMA kernels). */
+ * The chunk-WY MFMA kernels run when chunk == 64, d_k == d_v == 64 and
+ * q, k, v are BF16 with unit channel stride, 16-byte aligned data and every
+ * other stride a multiple of 8 elements; any other call takes the
+ * token-sequential kernels.  On the chunk-WY path d_output must satisfy the
+ * same row rule (a stride-0 broadcast upstream is rejected with
+ * GDN2_ERR_ARGUMENT: pass a dense copy). */
 GDN2_API size_t gdn_scalar_checkpoint_bytes(const gdn2_shape *shape, int chunk);
 
 GDN2_API int gdn_scalar_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q,
@@ -458,8 +463,10 @@ GDN2_API int gdn2_hola_backward(const gdn2_hola_shape *shape, const gdn2_view *q
  * synchronises the stream first), or a negative value if stage i has not run
  * since timing was enabled.  Stages: 0 prep, 1 state scan, 2 output
  * (forward); 3 backward prep, 4 adjoint scan, 5 gradients (backward).
- * Process-wide state for the current device: not for use during graph
- * capture or from several threads at once.  Returns GDN2_OK or an error. */
+ * Process-wide state for the current device, not thread safe: enable it only
+ * in single-threaded measurement runs.  A call whose stream is being captured
+ * into a graph records no events (the stage then keeps its last duration).
+ * Returns GDN2_OK or an error. */
 GDN2_API int gdn2_stage_timing(int enable);
 GDN2_API int gdn2_stage_count(void);
 GDN2_API const char *gdn2_stage_name(int stage);

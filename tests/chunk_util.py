@@ -1,0 +1,67 @@
+"""Inputs and runners shared by the chunk-WY GPU tests: seeded scalar-gate
+problems (bf16-rounded q/k/v/dO, f32 gates, optional masks and initial state),
+the forward/backward through the C ABI, and the f64 oracle's gradients."""
+import numpy as np
+import torch
+
+from gpu_util import dev
+from oracle import oracle
+
+
+def problem(seed, B, T, H, masks=True, initial=True, K=64, V=64, reset_every=0):
+    """reset_every > 0 adds a valid reset every reset_every tokens of the
+    first sequence and a padded run before each (long sequences)."""
+    rng = np.random.default_rng(seed)
+    q = rng.normal(size=(B, T, H, K))
+    k = rng.normal(size=(B, T, H, K))
+    q /= np.sqrt((q * q).sum(-1, keepdims=True) + 1e-6)
+    k /= np.sqrt((k * k).sum(-1, keepdims=True) + 1e-6)
+    bf = lambda x: torch.tensor(x, dtype=torch.float32).to(torch.bfloat16).float().numpy()  # noqa
+    p = dict(q=bf(q), k=bf(k), v=bf(rng.normal(size=(B, T, H, V))),
+             beta=(1 / (1 + np.exp(-rng.normal(size=(B, T, H))))).astype(np.float32),
+             g=(-np.log1p(np.exp(rng.normal(size=(B, T, H))))).astype(np.float32),
+             valid=np.ones((B, T), np.float32), reset=np.zeros((B, T), np.float32),
+             initial=(0.1 * rng.normal(size=(B, H, K, V))).astype(np.float32) if initial else None,
+             dO=bf(rng.normal(size=(B, T, H, V))),
+             dF=(0.1 * rng.normal(size=(B, H, K, V))).astype(np.float32),
+             dS=(0.1 * rng.normal(size=(B, T, H))).astype(np.float32))
+    if masks:
+        p["valid"][0, 5] = 0
+        p["valid"][0, min(70, T - 2):min(75, T - 1)] = 0
+        p["valid"][-1, T - 9:] = 0
+        p["reset"][0, 40] = 1
+        p["reset"][0, min(72, T - 2)] = 1  # reset on padding: ignored
+        if T > 130:
+            p["reset"][-1, 129] = 1
+        for t in range(reset_every, T - 1, reset_every or T):
+            p["reset"][0, t] = 1
+            p["valid"][0, t - 3:t - 1] = 0
+    return p
+
+
+def run_fwd(dk, p, chunk=64):
+    x = {n: dev(p[n], torch.bfloat16) for n in ("q", "k", "v")}
+    out, fin, sc, ck = dk.gdn_scalar_forward(x["q"], x["k"], x["v"], dev(p["beta"]), dev(p["g"]),
+                                             dev(p["valid"]), dev(p["reset"]),
+                                             dev(p["initial"]), chunk)
+    return out, fin, sc
+
+
+def scalar_oracle_grads(p):
+    a, e, w = oracle.scalar_gates(p["beta"], p["g"], p["q"].shape[3], p["v"].shape[3])
+    g = oracle.backward(p["q"], p["k"], p["v"], a, e, w, p["valid"], p["reset"], p["initial"],
+                        p["dO"], p["dF"], p["dS"])
+    db, dg = oracle.scalar_gate_grads(p["g"], g)
+    return g, db, dg
+
+
+def run_bwd(dk, p, chunk=64, use_final=True, use_scores=True):
+    x = {n: dev(p[n], torch.bfloat16) for n in ("q", "k", "v")}
+    beta, g, valid, reset = (dev(p[n]) for n in ("beta", "g", "valid", "reset"))
+    init = dev(p["initial"])
+    out, fin, sc, ck = dk.gdn_scalar_forward(x["q"], x["k"], x["v"], beta, g, valid, reset, init,
+                                             chunk)
+    return dk.gdn_scalar_backward(x["q"], x["k"], x["v"], beta, g, valid, reset, ck, chunk,
+                                  dev(p["dO"], torch.bfloat16),
+                                  dev(p["dF"]) if use_final else None,
+                                  dev(p["dS"]) if use_scores else None)
