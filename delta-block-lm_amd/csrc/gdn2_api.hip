@@ -7,6 +7,7 @@
 #include <climits>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "gdn2_chunk.h"
@@ -165,6 +166,36 @@ SeqArgs seq_args(const gdn2_shape *s, const gdn2_view *q, const gdn2_view *k, co
     return a;
 }
 
+}  // namespace
+
+// Device scratch of gdn_scalar_backward_noalloc: a fixed array in every
+// device's copy of the code object, held until the process ends.  Host code
+// never uses the array's name as an address: each device's address comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+static __device__ __align__(256) unsigned char scratch[GDN2_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];  // per device, null until first use
+
+int noalloc_scratch(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(GDN2_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(GDN2_ERR_ARGUMENT, "device ordinal %d outside 0..%d", dev, kMaxDevices - 1);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(GDN2_ERR_LAUNCH, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return GDN2_OK;
+}
 }  // namespace
 
 static int scalar_backward_impl(const gdn2_shape *shape, int chunk, const gdn2_view *q,
@@ -443,6 +474,30 @@ int gdn_scalar_backward(const gdn2_shape *shape, int chunk, const gdn2_view *q,
     return scalar_backward_impl(shape, chunk, q, k, v, beta, g, valid, reset, checkpoint,
                                 checkpoint_bytes, d_output, d_final_state, d_scores, dq, dk, dv,
                                 dbeta, dg, d_initial, workspace, workspace_bytes, stream);
+}
+
+int gdn_scalar_backward_noalloc(const gdn2_shape *shape, int chunk, const gdn2_view *q,
+                                const gdn2_view *k, const gdn2_view *v, const gdn2_view *beta,
+                                const gdn2_view *g, const gdn2_view *valid,
+                                const gdn2_view *reset, const void *checkpoint,
+                                size_t checkpoint_bytes, const gdn2_view *d_output,
+                                const float *d_final_state, const float *d_scores, void *dq,
+                                void *dk, void *dv, float *dbeta, float *dg, float *d_initial,
+                                void *stream) {
+    GDN2_TRY(check_shape(shape));
+    GDN2_TRY(check_chunk(chunk));
+    const size_t need = gdn_scalar_workspace_bytes(shape, chunk);
+    if (need > GDN2_NOALLOC_SCRATCH_BYTES)
+        return fail(GDN2_ERR_WORKSPACE,
+                    "gdn_scalar_backward_noalloc: this shape needs %zu bytes of scratch, above "
+                    "the library's fixed %zu-byte device scratch; call gdn_scalar_backward "
+                    "with a workspace instead",
+                    need, (size_t)GDN2_NOALLOC_SCRATCH_BYTES);
+    void *ws = nullptr;
+    GDN2_TRY(noalloc_scratch(&ws));
+    return scalar_backward_impl(shape, chunk, q, k, v, beta, g, valid, reset, checkpoint,
+                                checkpoint_bytes, d_output, d_final_state, d_scores, dq, dk, dv,
+                                dbeta, dg, d_initial, ws, GDN2_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 }  // extern "C"

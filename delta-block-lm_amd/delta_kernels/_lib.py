@@ -87,6 +87,8 @@ SIGNATURES = {
     "gdn_scalar_scan": (_I, [_S, _I] + [_V] * 8 + [_P, ctypes.c_int32, _F, _F, _P, _Z, _P]),
     "gdn_scalar_backward": (_I, [_S, _I] + [_V] * 7 + [_P, _Z, _V, _F, _F] + [_P] * 3
                             + [_F] * 3 + [_P, _Z, _P]),
+    "gdn_scalar_backward_noalloc": (_I, [_S, _I] + [_V] * 7 + [_P, _Z, _V, _F, _F] + [_P] * 3
+                                    + [_F] * 3 + [_P]),
     "gdn2_decode_step": (_I, [_S] + [_V] * 8 + [_F, _P, ctypes.c_int32, _F, _P]),
     "gdn2_conv_forward": (_I, [ctypes.POINTER(Gdn2ConvShape)] + [_V] * 4 + [_I, _F, _P]),
     "gdn2_conv_workspace_bytes": (_Z, [ctypes.POINTER(Gdn2ConvShape)]),

@@ -184,6 +184,26 @@ GDN2_API int gdn_scalar_backward(const gdn2_shape *shape, int chunk, const gdn2_
                         float *dg, float *d_initial, void *workspace, size_t workspace_bytes,
                         void *stream);
 
+/* The same backward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  It
+ * calls no allocating routine: its scratch is a fixed device array of
+ * GDN2_NOALLOC_SCRATCH_BYTES inside the library (one per device, held until
+ * the process ends), and a shape whose gdn_scalar_workspace_bytes exceeds
+ * that size is rejected with GDN2_ERR_WORKSPACE.  Every call on a device
+ * shares that device's array, so calls that overlap in time on one device
+ * (other streams, other threads) race; calls in order on one stream do not.
+ * Arguments and results are those of gdn_scalar_backward. */
+#define GDN2_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+GDN2_API int gdn_scalar_backward_noalloc(const gdn2_shape *shape, int chunk, const gdn2_view *q,
+                        const gdn2_view *k, const gdn2_view *v, const gdn2_view *beta,
+                        const gdn2_view *g, const gdn2_view *valid, const gdn2_view *reset,
+                        const void *checkpoint, size_t checkpoint_bytes,
+                        const gdn2_view *d_output, const float *d_final_state,
+                        const float *d_scores, void *dq, void *dk, void *dv, float *dbeta,
+                        float *dg, float *d_initial, void *stream);
+
 /* ---- Decode step on a carried state -------------------------------------- */
 /* One token per sequence (time == 1) applied in place to state [B,H,K,V] F32.
  * Equivalent to gdn2_training_scan with time = 1, initial = final_state =
