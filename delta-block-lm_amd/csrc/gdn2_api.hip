@@ -359,22 +359,31 @@ int gdn2_backward(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *
 size_t gdn_scalar_checkpoint_bytes(const gdn2_shape *shape, int chunk) {
     if (check_shape(shape) || check_chunk(chunk)) return 0;
     // Large enough for whichever kernel family the call will select.
-    const size_t c = chunk_checkpoint_bytes(shape->batch, shape->time, shape->heads);
+    size_t c = 0;
+    if (chunk_eligible_shape(shape, chunk))
+        c = chunk_checkpoint_bytes(shape->batch, shape->time, shape->heads);
+    else if (wide_eligible_shape(shape, chunk))
+        c = wide_checkpoint_bytes(shape->batch, shape->time, shape->heads);
     const size_t q = seq_checkpoint_bytes(shape);
-    return chunk_eligible_shape(shape, chunk) && c > q ? c : q;
+    return c > q ? c : q;
 }
 
 size_t gdn_scalar_workspace_bytes(const gdn2_shape *shape, int chunk) {
     if (check_shape(shape) || check_chunk(chunk)) return 0;
-    const size_t c = chunk_workspace_bytes(shape->batch, shape->time, shape->heads);
+    size_t c = 0;
+    if (chunk_eligible_shape(shape, chunk))
+        c = chunk_workspace_bytes(shape->batch, shape->time, shape->heads);
+    else if (wide_eligible_shape(shape, chunk))
+        c = wide_workspace_bytes(shape->batch, shape->time, shape->heads);
     const size_t q = seq_workspace_bytes(shape);
-    return chunk_eligible_shape(shape, chunk) && c > q ? c : q;
+    return c > q ? c : q;
 }
 
-// The chunk-WY MFMA kernels take bf16 q/k/v with d_k = d_v = 64, chunk 64,
-// unit channel stride and 16-byte aligned token rows; everything else runs the
-// token-sequential kernels.  Forward and backward apply the same rule, so the
-// checkpoint format always matches.
+// The chunk-WY MFMA kernels take bf16 q/k/v with d_k = d_v = 64 (gdn2_chunk.hip)
+// or 128 (gdn2_chunk_wide.hip), chunk 64, unit channel stride and 16-byte
+// aligned token rows; everything else runs the token-sequential kernels.
+// Forward and backward apply the same rule, so the checkpoint format always
+// matches.
 static bool rows_aligned(const gdn2_view *v) {
     return v->stride[3] == 1 && ((uintptr_t)v->data & 15) == 0 && v->stride[0] % 8 == 0 &&
            v->stride[1] % 8 == 0 && v->stride[2] % 8 == 0;
@@ -382,8 +391,8 @@ static bool rows_aligned(const gdn2_view *v) {
 
 static bool use_chunk_path(const gdn2_shape *shape, int chunk, const gdn2_view *q,
                            const gdn2_view *k, const gdn2_view *v) {
-    return chunk_eligible_shape(shape, chunk) && q->dtype == GDN2_BF16 && rows_aligned(q) &&
-           rows_aligned(k) && rows_aligned(v);
+    return (chunk_eligible_shape(shape, chunk) || wide_eligible_shape(shape, chunk)) &&
+           q->dtype == GDN2_BF16 && rows_aligned(q) && rows_aligned(k) && rows_aligned(v);
 }
 
 static ChunkArgs chunk_args(const gdn2_shape *s, const gdn2_view *q, const gdn2_view *k,
@@ -445,9 +454,13 @@ int gdn_scalar_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q, cons
         c.out_bf16 = output_dtype == GDN2_BF16;
         c.final_state = final_state;
         c.scores = scores;
+        const hipEvent_t *ev = stage_events(0, (hipStream_t)stream);
+        if (wide_eligible_shape(shape, chunk)) {
+            wide_bind_checkpoint(c, checkpoint);
+            return launch_status(launch_wide_fwd(c, (hipStream_t)stream, ev), "gdn_scalar_scan");
+        }
         chunk_bind_checkpoint(c, checkpoint);
-        return launch_status(launch_chunk_fwd(c, (hipStream_t)stream, stage_events(0, (hipStream_t)stream)),
-                             "gdn_scalar_scan");
+        return launch_status(launch_chunk_fwd(c, (hipStream_t)stream, ev), "gdn_scalar_scan");
     }
     SeqArgs a = seq_args(shape, q, k, v, beta, beta, beta, valid, reset);
     a.scalar = 1;
@@ -526,10 +539,16 @@ static int scalar_backward_impl(const gdn2_shape *shape, int chunk, const gdn2_v
         if (d_output && d_output->data && !rows_aligned(d_output))
             return fail(GDN2_ERR_ARGUMENT,
                         "d_output needs unit channel stride and 16-byte aligned rows on the "
-                        "chunked path (chunk 64, bf16, d_k = d_v = 64)");
+                        "chunked path (chunk 64, bf16, d_k = d_v = 64 or 128)");
         ChunkArgs c = chunk_args(shape, q, k, v, beta, g, valid, reset);
-        chunk_bind_checkpoint(c, const_cast<void *>(checkpoint));
-        chunk_bind_workspace(c, workspace);
+        const bool wide = wide_eligible_shape(shape, chunk);
+        if (wide) {
+            wide_bind_checkpoint(c, const_cast<void *>(checkpoint));
+            wide_bind_workspace(c, workspace);
+        } else {
+            chunk_bind_checkpoint(c, const_cast<void *>(checkpoint));
+            chunk_bind_workspace(c, workspace);
+        }
         if (d_output && d_output->data) {
             c.dout = (const uint16_t *)d_output->data;
             for (int d = 0; d < 3; ++d) c.ds[d] = d_output->stride[d];
@@ -542,7 +561,9 @@ static int scalar_backward_impl(const gdn2_shape *shape, int chunk, const gdn2_v
         c.dbeta = dbeta;
         c.dg = dg;
         c.dinitial = d_initial;
-        return launch_status(launch_chunk_bwd(c, (hipStream_t)stream, stage_events(3, (hipStream_t)stream)),
+        const hipEvent_t *ev = stage_events(3, (hipStream_t)stream);
+        return launch_status(wide ? launch_wide_bwd(c, (hipStream_t)stream, ev)
+                                  : launch_chunk_bwd(c, (hipStream_t)stream, ev),
                              "gdn_scalar_backward");
     }
     SeqArgs a = seq_args(shape, q, k, v, beta, beta, beta, valid, reset);

@@ -64,6 +64,12 @@ struct ChunkArgs {
     float *dbeta, *dg, *dinitial;
     uint16_t *ws_dstate;  // [B*H*nc] adjoint of the state at each chunk end
     float *ws_n;       // N of the adjoint map dS_start = M dS_end + N
+    // Wide path (d_k = d_v = 128, value blocks of 64): per-chunk |k_t|^2 and the
+    // value blocks' partial |delta_t|^2 (forward checkpoint), and the gradient
+    // partials the first value block hands to the second (backward workspace).
+    float *ck_kk, *ck_ddp;
+    float *ws_gq, *ws_gk, *ws_gb, *ws_gg;
+    int pass;  // value block of a bgrad launch
 };
 
 inline bool chunk_eligible_shape(const gdn2_shape *s, int chunk) {
@@ -108,6 +114,76 @@ inline void chunk_bind_workspace(ChunkArgs &a, void *ws) {
     a.ws_dstate = reinterpret_cast<uint16_t *>(p);
     a.ws_n = reinterpret_cast<float *>(p + n * CK_STATE_BYTES);
 }
+
+// ---- wide path: d_k = d_v = WIDE_D, value blocks of 64 -------------------------
+constexpr int WIDE_D = 128;
+constexpr int WIDE_NVB = WIDE_D / 64;
+
+inline bool wide_eligible_shape(const gdn2_shape *s, int chunk) {
+    return chunk == CHUNK && s->keys == WIDE_D && s->values == WIDE_D;
+}
+
+// Checkpoint per chunk: S0^T (bf16 D x D), T (bf16 C x C), GateBlock, delta (f32
+// C x D), M = A_c^T and A_c (bf16 D x D), B_c^T (f32 D x D), |k|^2 and the value
+// blocks' |delta|^2 (f32 C each).
+constexpr size_t WCK_STATE = (size_t)WIDE_D * WIDE_D * 2;
+constexpr size_t WCK_T = CK_T_BYTES;
+constexpr size_t WCK_GATE = CK_GATE_BYTES;
+constexpr size_t WCK_DELTA = (size_t)CHUNK * WIDE_D * 4;
+constexpr size_t WCK_MAPM = (size_t)WIDE_D * WIDE_D * 2;
+constexpr size_t WCK_MAPN = (size_t)WIDE_D * WIDE_D * 4;
+constexpr size_t WCK_NORM = (size_t)CHUNK * (1 + WIDE_NVB) * 4;
+constexpr size_t WCK_CHUNK =
+    WCK_STATE + WCK_T + WCK_GATE + WCK_DELTA + 2 * WCK_MAPM + WCK_MAPN + WCK_NORM;
+// Backward workspace per chunk: dS^T (bf16), N^T (f32), and the first value
+// block's dq/dk (f32 C x D each) and dbeta/dG (f32 C each) partials.
+constexpr size_t WWS_CHUNK = WCK_STATE + WCK_MAPN + 2 * (size_t)CHUNK * WIDE_D * 4 +
+                             2 * (size_t)CHUNK * 4;
+
+inline size_t wide_checkpoint_bytes(int64_t B, int64_t T, int64_t H) {
+    return (size_t)chunk_count(B, T, H) * WCK_CHUNK;
+}
+
+inline size_t wide_workspace_bytes(int64_t B, int64_t T, int64_t H) {
+    return (size_t)chunk_count(B, T, H) * WWS_CHUNK;
+}
+
+inline void wide_bind_checkpoint(ChunkArgs &a, void *ck) {
+    const int64_t n = (int64_t)a.B * a.H * a.nc;
+    char *p = static_cast<char *>(ck);
+    a.ck_state = reinterpret_cast<uint16_t *>(p);
+    p += n * WCK_STATE;
+    a.ck_t = reinterpret_cast<uint16_t *>(p);
+    p += n * WCK_T;
+    a.ck_gate = reinterpret_cast<GateBlock *>(p);
+    p += n * WCK_GATE;
+    a.ck_delta = reinterpret_cast<float *>(p);
+    p += n * WCK_DELTA;
+    a.ck_mt = reinterpret_cast<uint16_t *>(p);
+    p += n * WCK_MAPM;
+    a.map_m = reinterpret_cast<uint16_t *>(p);
+    p += n * WCK_MAPM;
+    a.map_n = reinterpret_cast<float *>(p);
+    p += n * WCK_MAPN;
+    a.ck_kk = reinterpret_cast<float *>(p);
+    a.ck_ddp = a.ck_kk + n * CHUNK;
+}
+
+inline void wide_bind_workspace(ChunkArgs &a, void *ws) {
+    const int64_t n = (int64_t)a.B * a.H * a.nc;
+    char *p = static_cast<char *>(ws);
+    a.ws_dstate = reinterpret_cast<uint16_t *>(p);
+    p += n * WCK_STATE;
+    a.ws_n = reinterpret_cast<float *>(p);
+    p += n * WCK_MAPN;
+    a.ws_gq = reinterpret_cast<float *>(p);
+    a.ws_gk = a.ws_gq + n * CHUNK * WIDE_D;
+    a.ws_gb = a.ws_gk + n * CHUNK * WIDE_D;
+    a.ws_gg = a.ws_gb + n * CHUNK;
+}
+
+hipError_t launch_wide_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
+hipError_t launch_wide_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
 
 hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
 hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);

@@ -1,0 +1,1192 @@
+// Chunk-WY scalar-gate gated delta rule for d_k = d_v = 128 on gfx950 MFMA.
+//
+// The chunk form is that of gdn2_chunk.hip (per chunk of C = 64 tokens with
+// start state S0: A = strict_lower(beta_t Gam_ts k_t.k_s), T = (I + A)^-1,
+// R = diag(beta)(V - diag(gam) K S0), delta = T R, O = diag(gam) Q S0 +
+// (Gam .* Q K^T) delta, S_C = A_c S0 + B_c with A_c = gam_63 I - (lam K)^T W,
+// B_c = (lam K)^T U, W = T diag(beta gam) K, U = T diag(beta) V).  Key-side
+// products reduce over all D = 128 key channels; value columns evolve
+// independently, so every value-side product is cut into value blocks of 64
+// columns, one workgroup each (grid = chunks x 2):
+//   prep   block vb: gates, A, T (block 0 writes them), W and U of block vb,
+//          and block vb's 64 columns of A_c and of B_c
+//   scan   four waves per (batch, head, 16 state columns); each wave owns a
+//          quarter of the 128 rows and the column block is shared through LDS
+//   out    block vb: delta, O and |delta|^2 of the block's 64 value columns;
+//          a small kernel then forms the scores from both blocks' partials
+//   bprep  block vb: N of the adjoint map for the block's 64 value columns
+//   bgrad  two launches: block 0 leaves its dq, dk, dbeta, dG partials in the
+//          workspace, block 1 adds its own and writes the gradients
+// Precision follows gdn2_chunk.hip: R, delta, P, dd, dP, W, U and the scan's X
+// enter their products as bf16 hi + lo pairs; S0, T, Q, K, V, dS as bf16.
+#include "gdn2_chunk_tile.h"
+
+namespace gdn2 {
+
+namespace {
+
+constexpr int KD = WIDE_D;      // key width (= value width)
+constexpr int NVB = WIDE_NVB;   // value blocks of 64
+constexpr int NKB = KD / 64;    // key blocks of 64
+constexpr int LDK = KD + 8;     // bf16 row stride of a 64 x KD tile
+constexpr int KTILE = 64 * LDK;
+static_assert(NVB == 2 && NKB == 2, "the wide kernels cut D into two blocks of 64");
+
+// Workgroup x -> (chunk, value block): both blocks of a chunk share x mod 8
+// and so one XCD (workgroups go to the XCDs round-robin by index).
+__device__ __forceinline__ bool chunk_block(int x, int nch, int &ci, int &vb) {
+    const int g = x / (8 * NVB), r = x % (8 * NVB);
+    vb = r >> 3;
+    ci = 8 * g + (r & 7);
+    return ci < nch;
+}
+
+inline dim3 chunk_block_grid(int nch) { return dim3(8 * NVB * ((nch + 7) / 8)); }
+
+// Token t's channel pieces [8 cb, 8 cb + 8) and [64 + 8 cb, 72 + 8 cb).
+struct Row2 {
+    uint4 p[NKB];
+};
+__device__ __forceinline__ Row2 load_row2(const uint16_t *base, const int64_t *s, int b, int tg,
+                                          int h, int cb, bool inb) {
+    Row2 r;
+#pragma unroll
+    for (int i = 0; i < NKB; ++i) r.p[i] = load8(base, s, b, tg, h, cb + 8 * i, inb);
+    return r;
+}
+__device__ __forceinline__ void put_row2(uint16_t *tile, int t, int cb, const Row2 &r) {
+#pragma unroll
+    for (int i = 0; i < NKB; ++i) put_row8(tile, t, cb + 8 * i, r.p[i], LDK);
+}
+// Piece i of a row, i uniform but not a compile-time constant (no dynamic
+// register indexing).
+__device__ __forceinline__ uint4 piece(const Row2 &r, int i) { return i == 0 ? r.p[0] : r.p[1]; }
+__device__ __forceinline__ Row2 mask_row2(Row2 r, bool on) {
+#pragma unroll
+    for (int i = 0; i < NKB; ++i) r.p[i] = mask8(r.p[i], on);
+    return r;
+}
+__device__ __forceinline__ uint4 scale8(uint4 v, float f) {
+    Pack8 p;
+    p.u = v;
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) o[e / 2] = bf16_pack2(f * bf16_val(p.h[e]), f * bf16_val(p.h[e + 1]));
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+__device__ __forceinline__ float sq8(uint4 v) {
+    Pack8 p;
+    p.u = v;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float x = bf16_val(p.h[e]);
+        s += x * x;
+    }
+    return s;
+}
+
+// A [64 x KD] bf16 matrix stored densely per chunk (row stride KD) into a
+// [64 x LDK] LDS tile: two 16-byte pieces per thread.
+__device__ __forceinline__ void stage_mat(uint16_t *tile, const uint16_t *src, int tid) {
+#pragma unroll
+    for (int i = 0; i < NKB; ++i) {
+        const int p = tid + NT * i, r = p / (KD / 8), c0 = 8 * (p % (KD / 8));
+        *reinterpret_cast<uint4 *>(&tile[r * LDK + c0]) =
+            *reinterpret_cast<const uint4 *>(src + r * KD + c0);
+    }
+}
+struct Mat2 {
+    uint4 p[NKB];
+};
+__device__ __forceinline__ Mat2 load_mat2(const uint16_t *src, int tid) {
+    Mat2 m;
+#pragma unroll
+    for (int i = 0; i < NKB; ++i) {
+        const int p = tid + NT * i, r = p / (KD / 8), c0 = 8 * (p % (KD / 8));
+        m.p[i] = *reinterpret_cast<const uint4 *>(src + r * KD + c0);
+    }
+    return m;
+}
+__device__ __forceinline__ void put_mat2(uint16_t *tile, const Mat2 &m, int tid) {
+#pragma unroll
+    for (int i = 0; i < NKB; ++i) {
+        const int p = tid + NT * i, r = p / (KD / 8), c0 = 8 * (p % (KD / 8));
+        *reinterpret_cast<uint4 *>(&tile[r * LDK + c0]) = m.p[i];
+    }
+}
+
+struct WPrepSmem {
+    uint16_t ks[KTILE];    // K rows; T (bf16, row stride LDB) once A is formed; then the
+                           // block's A_c^T rows [64][KD] for the row stores
+    uint16_t kl[KTILE];    // lam K rows
+    uint16_t kbg[TILE];    // beta gam K rows, key columns of block vb
+    uint16_t vbt[TILE];    // beta V rows, value columns of block vb
+    union {
+        struct {
+            float Af[C * LDF];
+            float Tf[C * LDF];
+        } inv;
+        uint16_t wu[4][TILE];  // W^T hi/lo, U^T hi/lo of block vb
+    } u;
+    GateLds gl;
+};
+
+}  // namespace
+
+// ---- prep: gates, the UT inverse and block vb of the chunk's state map ---------
+__global__ void __launch_bounds__(NT) wide_prep_kernel(ChunkArgs a) {
+    __shared__ WPrepSmem sm;
+    int ci, vb;
+    if (!chunk_block(blockIdx.x, a.B * a.H * a.nc, ci, vb)) return;
+    uint16_t *Ks = sm.ks, *KLs = sm.kl, *KBGs = sm.kbg, *VBs = sm.vbt;
+    uint16_t *Tb = sm.ks;  // over K once A is formed
+    uint16_t *Wt = sm.u.wu[0], *Wtl = sm.u.wu[1], *Ut = sm.u.wu[2], *Utl = sm.u.wu[3];
+    const int tid = threadIdx.x, w = tid >> 6;
+    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = tid & 63, cb = tid >> 6, tg = c * C + t;
+    const int tm = w >> 1, tn0 = 2 * (w & 1);
+    const bool inb = tg < a.T;
+    const Row2 kraw = load_row2(a.k, a.ks, b, tg, h, cb, inb);
+    const uint4 vraw = load8(a.v + 64 * vb, a.vs, b, tg, h, cb, inb);
+    const float vld = inb ? ld4<float>(a.valid, b, tg, 0, 0) : 0.f;
+    float rst = 0.f, gt = 0.f, bt = 0.f;
+    if (w == 0 && inb) {
+        rst = ld4<float>(a.reset, b, tg, 0, 0);
+        gt = ld4<float>(a.g, b, tg, h, 0);
+        bt = ld4<float>(a.beta, b, tg, h, 0);
+    }
+    const bool on = vld != 0.f;
+    const Row2 k8 = mask_row2(kraw, on);
+    const uint4 v8 = mask8(vraw, on);
+    put_row2(Ks, t, cb, k8);
+    if (w == 0) {
+        const float G = wave_scan_add(on ? gt : 0.f);
+        const int seg = wave_scan_add((on && rst != 0.f) ? 1 : 0);
+        const float bm = on ? bt : 0.f;
+        gates_derive(sm.gl, G, bm, on ? 1.f : 0.f, seg);
+        if (vb == 0) {
+            GateBlock *gb = a.ck_gate + ci;
+            gb->G[t] = G;
+            gb->beta[t] = bm;
+            gb->val[t] = on ? 1.f : 0.f;
+            gb->seg[t] = seg;
+        }
+    }
+    __syncthreads();
+    {  // scaled rows: lam K (all key channels), beta gam K (key block vb)
+        const float bg = sm.gl.beta[t] * sm.gl.gam[t], la = sm.gl.lam[t];
+#pragma unroll
+        for (int i = 0; i < NKB; ++i) put_row8(KLs, t, cb + 8 * i, scale8(k8.p[i], la), LDK);
+        put_row8(KBGs, t, cb, scale8(piece(k8, vb), bg));
+    }
+    // A = strict_lower(beta_t Gam_ts k_t.k_s) in f32 (tiles with tn <= tm only).
+    if (tn0 <= tm) {
+        f32x4 kk[2] = {zero4(), zero4()};
+        gemm2<KD, LDK, LDK>(kk, &Ks[(16 * tm) * LDK], Ks, tn0);
+        const RowGates rg = row_gates(sm.gl, tm);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int ss = 16 * (tn0 + j) + acc_col();
+            const float Gs = sm.gl.G[ss];
+            const int sgs = sm.gl.seg[ss];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tt = 16 * tm + acc_row(i);
+                sm.u.inv.Af[tt * LDF + ss] = (ss < tt && rg.seg[i] == sgs)
+                                                 ? rg.beta[i] * __expf(rg.G[i] - Gs) * kk[j][i]
+                                                 : 0.f;
+            }
+        }
+    }
+    __syncthreads();
+    ut_inverse(sm.u.inv.Af, sm.u.inv.Tf, w);
+    {  // T (bf16, row-major, zero above the diagonal): LDS operand and checkpoint
+        const int r = tid >> 3, c0 = 8 * (tid & 7);
+        uint32_t pk[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int s0 = c0 + 2 * e;
+            pk[e] = bf16_pack2(s0 <= r ? sm.u.inv.Tf[r * LDF + s0] : 0.f,
+                               s0 + 1 <= r ? sm.u.inv.Tf[r * LDF + s0 + 1] : 0.f);
+        }
+        const uint4 v = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        if (vb == 0) *reinterpret_cast<uint4 *>(a.ck_t + (int64_t)ci * C * C + r * C + c0) = v;
+        *reinterpret_cast<uint4 *>(&Tb[r * LDB + c0]) = v;
+    }
+    put_row8(VBs, t, cb, scale8(v8, sm.gl.beta[t]));
+    __syncthreads();
+    // W_vb = T (beta gam K)[:, block vb], U_vb = T (beta V_vb): transposed hi/lo.
+    {
+        f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
+        gemm2_tr(x, &Tb[(16 * tm) * LDB], KBGs, tn0);
+        gemm2_tr(y, &Tb[(16 * tm) * LDB], VBs, tn0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            store_tile_t_split(&Wt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Wtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
+            store_tile_t_split(&Ut[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Utl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, y[j]);
+        }
+    }
+    __syncthreads();
+    // Columns of block vb: A_c[:, vb] = gam_63 I[:, vb] - (lam K)^T W_vb (bf16; its
+    // transpose staged in LDS), B_c[:, vb] = (lam K)^T U_vb (f32, stored transposed).
+    {
+        const float gC = sm.gl.gamC;
+        uint16_t *Mt = sm.ks;  // [64 block columns][KD rows]; T is dead
+        float *Bt = a.map_n + (int64_t)ci * KD * KD;
+#pragma unroll
+        for (int rb = 0; rb < NKB; ++rb) {
+            const int mt = tm + 4 * rb;  // row tile of A_c / B_c (key channel)
+            f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
+            gemm2_atr<64, LDK, LDB>(x, KLs, 16 * mt, Wt, tn0);  // A[k][t] = (lam K)[t][k]
+            gemm2_atr<64, LDK, LDB>(x, KLs, 16 * mt, Wtl, tn0);
+            gemm2_atr<64, LDK, LDB>(y, KLs, 16 * mt, Ut, tn0);
+            gemm2_atr<64, LDK, LDB>(y, KLs, 16 * mt, Utl, tn0);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int cl = 16 * (tn0 + j) + acc_col();  // column within the block
+                f32x4 am;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    am[i] = (16 * mt + acc_row(i) == 64 * vb + cl ? gC : 0.f) - x[j][i];
+                store_tile_t(&Mt[(16 * (tn0 + j)) * LDK + 16 * mt], LDK, am);
+                *reinterpret_cast<float4 *>(&Bt[(64 * vb + cl) * KD + 16 * mt + acc_row(0)]) =
+                    make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
+            }
+        }
+    }
+    __syncthreads();
+    // Rows out: M = A_c^T rows 64 vb .. 64 vb + 63 (whole rows), and A_c's block
+    // columns read across them (16-byte pieces of A_c rows).
+    {
+        const uint16_t *Mt = sm.ks;
+        const int l = lane_id();
+#pragma unroll
+        for (int i = 0; i < NKB; ++i) {
+            const int p = tid + NT * i, r = p / (KD / 8), c0 = 8 * (p % (KD / 8));
+            *reinterpret_cast<uint4 *>(a.ck_mt + (int64_t)ci * KD * KD + (64 * vb + r) * KD + c0) =
+                *reinterpret_cast<const uint4 *>(&Mt[r * LDK + c0]);
+        }
+#pragma unroll
+        for (int i = 0; i < NKB; ++i) {
+            const int c0 = 16 * ((w & 3) + 4 * i), r0 = 32 * (w >> 2);
+            const bf16x8_t ar = frag_tr<LDK>(Mt, r0, c0);  // A_c[c0 + n][64 vb + r0 + 8 g + e]
+            *reinterpret_cast<bf16x8_t *>(a.map_m + (int64_t)ci * KD * KD + (c0 + (l & 15)) * KD +
+                                          64 * vb + r0 + 8 * (l >> 4)) = ar;
+        }
+    }
+}
+
+// ---- affine scan over chunks (d = 128) -------------------------------------------
+// X_next = M_c X + N_c per chunk of one (batch, head), forward (states, M = A_c,
+// N = B_c) or reverse (state adjoints, M = A_c^T, N from bprep).  Columns of X
+// evolve independently: a workgroup owns 16 of them, and its four waves own a
+// quarter of the 128 rows each.  Per step every wave writes its rows of X
+// (bf16 hi/lo, transposed) to a double-buffered LDS block, one barrier, then
+// multiplies its rows of M (registers, three chunks ahead) against the whole
+// 128 x 16 block.  X before each step goes to ckpt[c] as X^T in bf16.
+namespace {
+constexpr int SW = 4;               // waves per scan workgroup
+constexpr int SRT = KD / 16 / SW;   // row tiles per wave
+constexpr int SKS = KD / 32;        // reduction steps of a 16x16x32 product
+constexpr int LDX = KD + 8;
+constexpr int NCG = KD / 16;        // 16-column groups per state
+}  // namespace
+
+struct WScanArgs {
+    int nc, B, H;
+    const uint16_t *m;   // [chunk][KD][KD] bf16 row-major
+    const float *n;      // [chunk][KD cols][KD rows] f32 (N^T)
+    uint16_t *ckpt;      // [chunk][KD cols][KD rows] bf16 (X^T)
+    View x0;             // [B,H,KD,KD] strided (data may be null: zero)
+    float *xout;         // [B,H,KD,KD] dense (may be null)
+    int reverse;
+};
+
+template <int SL, typename F, typename Gt>
+__device__ __forceinline__ void wscan_step(int s, const WScanArgs &p, int bh, int j, int w,
+                                           f32x4 (&X)[SRT], bf16x8_t (&mf)[3][SRT][SKS],
+                                           f32x4 (&nf)[3][SRT], uint16_t (*xs)[2][16 * LDX],
+                                           F &fetch, Gt &chunk_of) {
+    const int c = chunk_of(s);
+    uint16_t *ck = p.ckpt + ((int64_t)bh * p.nc + c) * KD * KD;
+    uint16_t *xh = xs[s & 1][0], *xl = xs[s & 1][1];
+#pragma unroll
+    for (int rt = 0; rt < SRT; ++rt) {
+        const int mt = SRT * w + rt;
+        *reinterpret_cast<uint2 *>(&ck[j * KD + 16 * mt + acc_row(0)]) =
+            make_uint2(bf16_pack2(X[rt][0], X[rt][1]), bf16_pack2(X[rt][2], X[rt][3]));
+        store_tile_t_split(xh + 16 * mt, xl + 16 * mt, LDX, X[rt]);  // [col][row]
+    }
+    __syncthreads();
+    // Y = M X from zero, then X = Y + N: N stays an ordinary operand that is
+    // waited for only at the end of the step.
+    f32x4 Y[SRT];
+#pragma unroll
+    for (int rt = 0; rt < SRT; ++rt) Y[rt] = zero4();
+#pragma unroll
+    for (int kk = 0; kk < SKS; ++kk) {
+        const bf16x8_t bh_ = frag(xh, LDX, 32 * kk), bl_ = frag(xl, LDX, 32 * kk);
+#pragma unroll
+        for (int rt = 0; rt < SRT; ++rt) {
+            Y[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][rt][kk], bh_, Y[rt], 0, 0, 0);
+            Y[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][rt][kk], bl_, Y[rt], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int rt = 0; rt < SRT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) X[rt][i] = Y[rt][i] + nf[SL][rt][i];
+    // Unconditional (the last chunk again past the end): every step issues the
+    // same loads, so the wait for a ring slot counts only the later steps' loads
+    // and stores instead of draining the whole queue.
+    fetch(chunk_of(min(s + 3, p.nc - 1)), mf[SL], nf[SL]);
+}
+
+// Workgroup x -> (head bh, column group cg); the NCG groups of a head take
+// indices with equal residue mod 8, so they share one XCD's L2.
+__global__ void __launch_bounds__(64 * SW) wide_scan_kernel(WScanArgs p) {
+    __shared__ uint16_t xs[2][2][16 * LDX];
+    const int x = blockIdx.x, w = threadIdx.x >> 6, l = lane_id();
+    const int cg = (x >> 3) % NCG, bh = (x & 7) + 8 * (x / (8 * NCG));
+    if (bh >= p.B * p.H) return;
+    const int b = bh / p.H, h = bh % p.H;
+    const int j = 16 * cg + (l & 15);  // this lane's state column
+    bf16x8_t mf[3][SRT][SKS];
+    f32x4 nf[3][SRT];
+    auto chunk_of = [&](int s) { return p.reverse ? p.nc - 1 - s : s; };
+    auto fetch = [&](int c, bf16x8_t (&m)[SRT][SKS], f32x4 (&n)[SRT]) {
+        const int64_t cix = (int64_t)bh * p.nc + c;
+        const uint16_t *M = p.m + cix * KD * KD;
+        const float *N = p.n + cix * KD * KD;
+#pragma unroll
+        for (int rt = 0; rt < SRT; ++rt) {
+            const int mt = SRT * w + rt;
+#pragma unroll
+            for (int kk = 0; kk < SKS; ++kk)
+                m[rt][kk] = __builtin_bit_cast(
+                    bf16x8_t, *reinterpret_cast<const uint4 *>(M + (16 * mt + (l & 15)) * KD +
+                                                               32 * kk + 8 * (l >> 4)));
+            const float4 nv = *reinterpret_cast<const float4 *>(&N[j * KD + 16 * mt + acc_row(0)]);
+            n[rt] = f32x4{nv.x, nv.y, nv.z, nv.w};
+        }
+    };
+    fetch(chunk_of(0), mf[0], nf[0]);
+    f32x4 X[SRT];
+#pragma unroll
+    for (int rt = 0; rt < SRT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            X[rt][i] = p.x0.data ? ld4<float>(p.x0, b, h, 16 * (SRT * w + rt) + acc_row(i), j) : 0.f;
+    fetch(chunk_of(min(1, p.nc - 1)), mf[1], nf[1]);
+    fetch(chunk_of(min(2, p.nc - 1)), mf[2], nf[2]);
+    int s = 0;
+    for (; s + 2 < p.nc; s += 3) {  // whole ring turns
+        wscan_step<0>(s, p, bh, j, w, X, mf, nf, xs, fetch, chunk_of);
+        wscan_step<1>(s + 1, p, bh, j, w, X, mf, nf, xs, fetch, chunk_of);
+        wscan_step<2>(s + 2, p, bh, j, w, X, mf, nf, xs, fetch, chunk_of);
+    }
+    if (s < p.nc) wscan_step<0>(s, p, bh, j, w, X, mf, nf, xs, fetch, chunk_of);
+    if (s + 1 < p.nc) wscan_step<1>(s + 1, p, bh, j, w, X, mf, nf, xs, fetch, chunk_of);
+    if (p.xout)
+#pragma unroll
+        for (int rt = 0; rt < SRT; ++rt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                p.xout[((int64_t)bh * KD + 16 * (SRT * w + rt) + acc_row(i)) * KD + j] = X[rt][i];
+}
+
+static void launch_wide_scan(const WScanArgs &p, hipStream_t stream) {
+    const dim3 grid(8 * NCG * ((p.B * p.H + 7) / 8)), block(64 * SW);
+    hipLaunchKernelGGL(wide_scan_kernel, grid, block, 0, stream, p);
+}
+
+// ---- out: value block vb of the outputs, the edits and their norms -------------
+namespace {
+struct WOutSmem {
+    uint16_t q[KTILE];   // Q rows; delta^T hi (row stride LDB) from phase 2
+    uint16_t k[KTILE];   // K rows; delta^T lo from phase 2
+    uint16_t st[KTILE];  // S0^T rows of block vb ([v][k]); O rows (LDB) in phase 3
+    uint16_t vt[TILE];   // V_vb^T, then R^T lo; with tb: delta f32 rows from phase 3
+    uint16_t tb[TILE];   // T rows
+    uint16_t rt[TILE];   // R^T hi
+    uint16_t pt[TILE], ptl[TILE];  // P^T hi/lo
+    GateLds gl;
+    float kk[NW][C];
+    float dd[2][C];
+};
+}  // namespace
+
+__global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a) {
+    __shared__ WOutSmem sm;
+    int ci, vb;
+    if (!chunk_block(blockIdx.x, a.B * a.H * a.nc, ci, vb)) return;
+    uint16_t *Qs = sm.q, *Ks = sm.k, *Vt = sm.vt, *Tb = sm.tb, *St = sm.st, *Rt = sm.rt;
+    uint16_t *Pt = sm.pt, *Ptl = sm.ptl;
+    uint16_t *Dt = sm.q, *Dl = sm.k;  // over Q/K after phase 1
+    uint16_t *Os = sm.st;             // over S0^T after phase 2
+    const int tid = threadIdx.x, w = tid >> 6;
+    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = tid & 63, cb = tid >> 6, t0 = c * C, tg = t0 + t;
+    const int tm = w >> 1, tn0 = 2 * (w & 1);
+    const GateBlock *gb = a.ck_gate + ci;
+    const bool inb = tg < a.T;
+    const Row2 qr = load_row2(a.q, a.qs, b, tg, h, cb, inb);
+    const Row2 kr = load_row2(a.k, a.ks, b, tg, h, cb, inb);
+    const uint4 vr = load8(a.v + 64 * vb, a.vs, b, tg, h, cb, inb);
+    const Mat2 s0r = load_mat2(a.ck_state + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
+    const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
+    const int sg = gb->seg[t];
+    const uint4 trw =
+        *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C + (tid >> 3) * C + 8 * (tid & 7));
+    {
+        const bool on = va != 0.f;
+        const Row2 k8 = mask_row2(kr, on);
+        put_row2(Qs, t, cb, mask_row2(qr, on));
+        put_row2(Ks, t, cb, k8);
+        put_col8(Vt, t, cb, mask8(vr, on));
+        put_mat2(St, s0r, tid);
+        float ksq = 0.f;
+#pragma unroll
+        for (int i = 0; i < NKB; ++i) ksq += sq8(k8.p[i]);
+        sm.kk[cb][t] = ksq;
+        if (w == 0) gates_derive(sm.gl, G, be, va, sg);
+    }
+    __syncthreads();
+    // Phase 1: R (-> Rt, lo over Vt), P (hi/lo), and gam Q S0 kept in registers.
+    f32x4 qs[2] = {zero4(), zero4()};
+    {
+        f32x4 x[2] = {zero4(), zero4()};
+        gemm2<KD, LDK, LDK>(x, &Ks[(16 * tm) * LDK], St, tn0);
+        gemm2<KD, LDK, LDK>(qs, &Qs[(16 * tm) * LDK], St, tn0);
+        f32x4 pq[2] = {zero4(), zero4()};
+        if (tn0 <= tm) gemm2<KD, LDK, LDK>(pq, &Qs[(16 * tm) * LDK], Ks, tn0);
+        const RowGates rg = row_gates(sm.gl, tm);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int ss = 16 * (tn0 + j) + acc_col();
+            const float Gs = sm.gl.G[ss];
+            const int sgs = sm.gl.seg[ss];
+            uint16_t *vt = &Vt[(16 * (tn0 + j)) * LDB + 16 * tm];
+            float vv[4];
+            ld4_bf16(vt + acc_col() * LDB + 4 * (lane_id() >> 4), vv);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tt = 16 * tm + acc_row(i);
+                x[j][i] = rg.beta[i] * (vv[i] - rg.gam[i] * x[j][i]);
+                qs[j][i] *= rg.gam[i];
+                pq[j][i] *= (ss <= tt && rg.seg[i] == sgs) ? __expf(rg.G[i] - Gs) : 0.f;
+            }
+            store_tile_t_split(&Rt[(16 * (tn0 + j)) * LDB + 16 * tm], vt, LDB, x[j]);
+            store_tile_t_split(&Pt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq[j]);
+        }
+    }
+    *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
+    __syncthreads();
+    // Phase 2: delta = T R (-> Dt/Dl over the Q/K tiles) and |delta_t|^2 of the block.
+    f32x4 dlt[2] = {zero4(), zero4()};
+    {
+        gemm2(dlt, &Tb[(16 * tm) * LDB], Rt, tn0);
+        gemm2(dlt, &Tb[(16 * tm) * LDB], Vt, tn0);
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[i] = dlt[0][i] * dlt[0][i] + dlt[1][i] * dlt[1][i];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            store_tile_t_split(&Dt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Dl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, dlt[j]);
+        row_reduce_store(p, sm.dd[w & 1], tm);
+    }
+    __syncthreads();
+    float *Df = reinterpret_cast<float *>(sm.vt);  // over V^T/R^T-lo and T, dead from here on
+    static_assert(C * LDF * sizeof(float) <= 2 * TILE * sizeof(uint16_t), "delta over vt+tb");
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            Df[(16 * tm + acc_row(i)) * LDF + 16 * (tn0 + j) + acc_col()] = dlt[j][i];
+    // Phase 3: O = gam Q S0 + P delta, staged through LDS for coalesced stores.
+    {
+        f32x4 x[2] = {qs[0], qs[1]};
+        gemm2_atr(x, Pt, 16 * tm, Dt, tn0);
+        gemm2_atr(x, Pt, 16 * tm, Dl, tn0);
+        gemm2_atr(x, Ptl, 16 * tm, Dt, tn0);
+        if (a.out_bf16) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) store_tile_rm(&Os[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, x[j]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int tq = t0 + 16 * tm + acc_row(i);
+                    if (tq < a.T)
+                        reinterpret_cast<float *>(a.out)[(((int64_t)b * a.T + tq) * a.H + h) * KD +
+                                                         64 * vb + 16 * (tn0 + j) + acc_col()] = x[j][i];
+                }
+        }
+    }
+    if (tid < 64) {  // |k_t|^2 (block 0) and this block's |delta_t|^2 for the scores
+        float kk = 0.f;
+#pragma unroll
+        for (int q = 0; q < NW; ++q) kk += sm.kk[q][t];
+        if (vb == 0) a.ck_kk[(int64_t)ci * C + t] = kk;
+        a.ck_ddp[((int64_t)ci * NVB + vb) * C + t] = sm.dd[0][t] + sm.dd[1][t];
+    }
+    __syncthreads();
+    {
+        const int r = tid >> 3, c0 = 8 * (tid & 7), tq = t0 + r;
+        float *dck = a.ck_delta + (int64_t)ci * C * KD + r * KD + 64 * vb + c0;
+        *reinterpret_cast<float4 *>(dck) = *reinterpret_cast<const float4 *>(&Df[r * LDF + c0]);
+        *reinterpret_cast<float4 *>(dck + 4) = *reinterpret_cast<const float4 *>(&Df[r * LDF + c0 + 4]);
+        if (a.out_bf16 && tq < a.T)
+            *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.out) +
+                                       (((int64_t)b * a.T + tq) * a.H + h) * KD + 64 * vb + c0) =
+                *reinterpret_cast<const uint4 *>(&Os[r * LDB + c0]);
+    }
+}
+
+// Scores from the blocks' partial norms: score_t = |k_t| |delta_t| on valid
+// tokens, 0 on padding.
+__global__ void __launch_bounds__(256) wide_score_kernel(ChunkArgs a) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t nch = (int64_t)a.B * a.H * a.nc;
+    if (i >= nch * C) return;
+    const int64_t ci = i / C;
+    const int t = (int)(i % C), bh = (int)(ci / a.nc), c = (int)(ci % a.nc);
+    const int b = bh / a.H, h = bh % a.H, tg = c * C + t;
+    if (tg >= a.T) return;
+    float dd = 0.f;
+#pragma unroll
+    for (int vb = 0; vb < NVB; ++vb) dd += a.ck_ddp[(ci * NVB + vb) * C + t];
+    const float kk = a.ck_kk[ci * C + t];
+    a.scores[((int64_t)b * a.T + tg) * a.H + h] = a.ck_gate[ci].val[t] != 0.f ? sqrtf(kk * dd) : 0.f;
+}
+
+// ---- backward prep: N of the adjoint map, value block vb -------------------------
+// dS0 = M dS_C + N with M = A_c^T and N = Y - W^T X, Y = (gam Q)^T dO,
+// X = P^T dO + diag(c) delta, W = T diag(beta gam) K (formed again from T and K
+// with prep's operands and products); the block's 64 columns of N per workgroup.
+namespace {
+struct WBPrepSmem {
+    uint16_t q[KTILE], k[KTILE];  // Q, K rows; X^T hi/lo (row stride LDB) from phase 2
+    union {
+        struct {
+            uint16_t qg[KTILE];   // gam Q rows
+            uint16_t tb[TILE];    // T rows
+            uint16_t kbg[KTILE];  // beta gam K rows
+        } p1;
+        uint16_t wt[2][KD * LDB];  // W^T hi/lo ([k][t]) from phase 2
+    } u;
+    uint16_t dos[TILE];            // dO rows of block vb
+    uint16_t pt[TILE], ptl[TILE];  // P^T hi/lo
+    GateLds gl;
+    float dsc[C];
+};
+}  // namespace
+
+__global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a) {
+    __shared__ WBPrepSmem sm;
+    int ci, vb;
+    if (!chunk_block(blockIdx.x, a.B * a.H * a.nc, ci, vb)) return;
+    uint16_t *Qs = sm.q, *Ks = sm.k, *QGs = sm.u.p1.qg, *Tb = sm.u.p1.tb, *KBGs = sm.u.p1.kbg;
+    uint16_t *dOs = sm.dos, *Pt = sm.pt, *Ptl = sm.ptl;
+    uint16_t *Xt = sm.q, *Xtl = sm.k;                  // over Q/K after phase 1
+    uint16_t *Wt = sm.u.wt[0], *Wtl = sm.u.wt[1];      // over the phase-1 operands
+    const int tid = threadIdx.x, w = tid >> 6;
+    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
+    const int tg = c * C + t;
+    const bool inb = tg < a.T;
+    const GateBlock *gb = a.ck_gate + ci;
+    const float *dck = a.ck_delta + (int64_t)ci * C * KD + 64 * vb;
+    const int r0 = 16 * tm + 4 * (lane_id() >> 4);
+    const Row2 qr = load_row2(a.q, a.qs, b, tg, h, cb, inb);
+    const Row2 kr = load_row2(a.k, a.ks, b, tg, h, cb, inb);
+    const uint4 dor =
+        a.dout ? load8(a.dout + 64 * vb, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
+    const uint4 trow = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C +
+                                                         (tid >> 3) * C + 8 * (tid & 7));
+    const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
+    const int sg = gb->seg[t];
+    const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
+    const bool score_adj = a.dscores != nullptr;
+    float dl[2][4] = {};  // delta at this wave's X tile
+    if (score_adj) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dl[j][i] = dck[(r0 + i) * KD + 16 * (tn0 + j) + acc_col()];
+    }
+    {
+        const bool on = va != 0.f;
+        const float gam = sg == 0 ? __expf(G) : 0.f, bg = be * gam;
+        const Row2 q8 = mask_row2(qr, on), k8 = mask_row2(kr, on);
+        put_row2(Qs, t, cb, q8);
+        put_row2(Ks, t, cb, k8);
+        put_row8(dOs, t, cb, mask8(dor, on));
+#pragma unroll
+        for (int i = 0; i < NKB; ++i) {
+            put_row8(QGs, t, cb + 8 * i, scale8(q8.p[i], gam), LDK);
+            put_row8(KBGs, t, cb + 8 * i, scale8(k8.p[i], bg), LDK);
+        }
+        *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trow;
+        if (w == 0) {
+            gates_derive(sm.gl, G, be, va, sg);
+            sm.dsc[t] = dsc;
+        }
+    }
+    __syncthreads();
+    const RowGates rg = row_gates(sm.gl, tm);
+    // Phase 1: W = T (beta gam K) and Y = (gam Q)^T dO_vb in registers; P^T hi/lo.
+    f32x4 wacc[NKB][2], yacc[NKB][2];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+        wacc[kb][0] = wacc[kb][1] = yacc[kb][0] = yacc[kb][1] = zero4();
+        gemm2_tr<64, LDB, LDK>(wacc[kb], &Tb[(16 * tm) * LDB], KBGs, tn0 + 4 * kb);
+        const int mt = tm + 4 * kb;  // row tile of Y (key channel)
+#pragma unroll
+        for (int r = 0; r < 64; r += 32) {  // Y[k][v] = sum_t (gam Q)[t][k] dO[t][v]
+            const bf16x8_t x = frag_tr<LDK>(QGs, r, 16 * mt);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                yacc[kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    x, frag_tr(dOs, r, 16 * (tn0 + j)), yacc[kb][j], 0, 0, 0);
+        }
+    }
+    {
+        f32x4 pq[2] = {zero4(), zero4()};
+        if (tn0 <= tm) gemm2<KD, LDK, LDK>(pq, &Qs[(16 * tm) * LDK], Ks, tn0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int ss = 16 * (tn0 + j) + acc_col();
+            const float Gs = sm.gl.G[ss];
+            const int sgs = sm.gl.seg[ss];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tt = 16 * tm + acc_row(i);
+                pq[j][i] *= (ss <= tt && rg.seg[i] == sgs) ? __expf(rg.G[i] - Gs) : 0.f;
+            }
+            store_tile_t_split(&Pt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq[j]);
+        }
+    }
+    __syncthreads();
+    // Phase 2: W^T hi/lo; X = P^T dO_vb + diag(c) delta_vb, stored transposed (hi/lo).
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            store_tile_t_split(&Wt[(16 * (tn0 + 4 * kb + j)) * LDB + 16 * tm],
+                               &Wtl[(16 * (tn0 + 4 * kb + j)) * LDB + 16 * tm], LDB, wacc[kb][j]);
+    {
+        f32x4 x[2] = {zero4(), zero4()};
+        gemm2_tr(x, &Pt[(16 * tm) * LDB], dOs, tn0);  // B[v][t] = dO[t][v]
+        gemm2_tr(x, &Ptl[(16 * tm) * LDB], dOs, tn0);
+        if (score_adj) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int ss = r0 + i;
+                float dq = 0.f;
+#pragma unroll
+                for (int v2 = 0; v2 < NVB; ++v2) dq += a.ck_ddp[((int64_t)ci * NVB + v2) * C + ss];
+                const float nk = sqrtf(a.ck_kk[(int64_t)ci * C + ss]), nd = sqrtf(dq);
+                const float cs = (nk > 0.f && nd > 0.f) ? sm.dsc[ss] * nk / nd : 0.f;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) x[j][i] += cs * dl[j][i];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            store_tile_t_split(&Xt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Xtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
+    }
+    __syncthreads();
+    // Phase 3: N = Y - W^T X for the block's 64 columns, all KD rows.
+    float *Nt = a.ws_n + (int64_t)ci * KD * KD;  // N transposed: Nt[col][row]
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+        const int mt = tm + 4 * kb;
+        f32x4 x[2] = {zero4(), zero4()};
+        gemm2(x, &Wt[(16 * mt) * LDB], Xt, tn0);
+        gemm2(x, &Wt[(16 * mt) * LDB], Xtl, tn0);
+        gemm2(x, &Wtl[(16 * mt) * LDB], Xt, tn0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            *reinterpret_cast<float4 *>(&Nt[(64 * vb + 16 * (tn0 + j) + acc_col()) * KD + 16 * mt +
+                                            acc_row(0)]) =
+                make_float4(yacc[kb][j][0] - x[j][0], yacc[kb][j][1] - x[j][1],
+                            yacc[kb][j][2] - x[j][2], yacc[kb][j][3] - x[j][3]);
+    }
+}
+
+// ---- bgrad: every gradient of one chunk, value block a.pass --------------------
+// The phases of gdn2_chunk.hip's gradient kernel with dO, S0, dS, delta, V and
+// dV cut to value block vb.  Everything a value block contributes to dq, dk,
+// dbeta and dG is a sum over its value columns, so block 0 leaves its
+// contributions in the workspace (f32, accumulator layout) and block 1 adds
+// its own before the masks, the dG reverse scan and the stores.
+namespace {
+struct WBGradSmem {
+    uint16_t q[KTILE];    // Q rows
+    uint16_t k[KTILE];    // K rows
+    uint16_t s0t[KTILE];  // S0^T rows of block vb (..F); with dos: dK^T [KD][LDB] (G..)
+    uint16_t dos[TILE];   // dO rows of block vb (..F)
+    uint16_t dst[KTILE];  // dS^T rows of block vb (A..D); dR rows (E..F)
+    uint16_t vr[TILE];    // V rows of block vb (..E); dV^T (G..)
+    uint16_t tr[TILE];    // T rows (..E); MA^T (F..G)
+    uint16_t dh[TILE], dlo[TILE];  // delta rows hi/lo (..F); dQ^T [KD][LDB] over both (G..)
+    uint16_t pt[TILE], ptl[TILE];  // P^T hi/lo (A..D); ddelta^T (D..E); MP^T (F..G)
+    GateLds gl;
+    float dsc[C];
+    float g1[2][C], ku[2][C], b1[2][C], b2[2][C], zr[2][C], zc[4][C], dlam[2][C];
+    float frob[NW];
+};
+}  // namespace
+
+__global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
+    __shared__ WBGradSmem sm;
+    const int vb = a.pass;
+    const bool first = vb == 0, last = vb == NVB - 1;
+    uint16_t *Qs = sm.q, *Ks = sm.k, *dOs = sm.dos, *S0t = sm.s0t, *dSt = sm.dst;
+    uint16_t *Vr = sm.vr, *Tr = sm.tr, *Dh = sm.dh, *Dlo = sm.dlo, *Pt = sm.pt, *Ptl = sm.ptl;
+    uint16_t *Dd = sm.pt, *Ddl = sm.ptl;  // ddelta^T, D..E
+    uint16_t *dRr = sm.dst;               // dR rows, E..F
+    uint16_t *MAt = sm.tr, *MPt = sm.pt, *MPtl = sm.ptl;
+    uint16_t *dQt = sm.dh, *dKt = sm.s0t, *dVt = sm.vr;
+    static_assert(sizeof(sm.dh) + sizeof(sm.dlo) >= KD * LDB * 2, "dQ^T over dh, dlo");
+    static_assert(sizeof(sm.s0t) + sizeof(sm.dos) >= KD * LDB * 2, "dK^T over s0t, dos");
+    const int tid = threadIdx.x, w = tid >> 6;
+    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
+    const int tg = c * C + t;
+    const bool inb = tg < a.T;
+    const GateBlock *gb = a.ck_gate + ci;
+    const float *dck = a.ck_delta + (int64_t)ci * C * KD + 64 * vb;
+    const int r0 = 16 * tm + 4 * (lane_id() >> 4);
+    const Row2 qr = load_row2(a.q, a.qs, b, tg, h, cb, inb);
+    const Row2 kr = load_row2(a.k, a.ks, b, tg, h, cb, inb);
+    const uint4 dor =
+        a.dout ? load8(a.dout + 64 * vb, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
+    const Mat2 s0 = load_mat2(a.ck_state + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
+    const Mat2 ds = load_mat2(a.ws_dstate + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
+    const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
+    const int sg = gb->seg[t];
+    const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
+    const bool score_adj = a.dscores != nullptr;
+    const uint4 vr = load8(a.v + 64 * vb, a.vs, b, tg, h, cb, inb);
+    const uint4 trw = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C +
+                                                      (tid >> 3) * C + 8 * (tid & 7));
+    const float4 d0 = *reinterpret_cast<const float4 *>(dck + t * KD + 8 * cb);
+    const float4 d1 = *reinterpret_cast<const float4 *>(dck + t * KD + 8 * cb + 4);
+    const bool on = va != 0.f;
+    {
+        put_row2(Qs, t, cb, mask_row2(qr, on));
+        put_row2(Ks, t, cb, mask_row2(kr, on));
+        put_row8(dOs, t, cb, mask8(dor, on));
+        put_mat2(S0t, s0, tid);
+        put_mat2(dSt, ds, tid);
+        float fr = 0.f;
+#pragma unroll
+        for (int i = 0; i < NKB; ++i) fr += dot8_bf16(s0.p[i], ds.p[i]);
+        fr = wave_sum(fr);
+        if (lane_id() == 0) sm.frob[w] = fr;
+        if (w == 0) {
+            gates_derive(sm.gl, G, be, va, sg);
+            sm.dsc[t] = dsc;
+        }
+    }
+    __syncthreads();
+    const RowGates rg = row_gates(sm.gl, tm);
+    float lmv[4];
+    {
+        const float4 lm = lds_f4(&sm.gl.lam[r0]);
+        lmv[0] = lm.x, lmv[1] = lm.y, lmv[2] = lm.z, lmv[3] = lm.w;
+    }
+    // Phase A: dO S0^T (key tiles of both key blocks), lam K dS, KK^T, QK^T;
+    // P^T (hi/lo) -> LDS.
+    float gmA[2][4];
+    f32x4 dos[NKB][2], kds[2] = {zero4(), zero4()};
+    f32x4 kk[2] = {zero4(), zero4()}, qk[2] = {zero4(), zero4()};
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+        dos[kb][0] = dos[kb][1] = zero4();
+        gemm2_tr<64, LDB, LDK>(dos[kb], &dOs[(16 * tm) * LDB], S0t, tn0 + 4 * kb);
+    }
+    gemm2<KD, LDK, LDK>(kds, &Ks[(16 * tm) * LDK], dSt, tn0);
+    if (tn0 <= tm) {
+        gemm2<KD, LDK, LDK>(kk, &Ks[(16 * tm) * LDK], Ks, tn0);
+        gemm2<KD, LDK, LDK>(qk, &Qs[(16 * tm) * LDK], Ks, tn0);
+    }
+    {
+        float p[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float qv[4];
+                ld4_rm_tr<LDK>(Qs, 16 * tm, 16 * (tn0 + 4 * kb + j), qv);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) p[i] += qv[i] * dos[kb][j][i];  // q_t . (dO S0^T)_t
+            }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int ss = 16 * (tn0 + j) + acc_col();
+            const float Gs = sm.gl.G[ss];
+            const int sgs = sm.gl.seg[ss];
+            f32x4 pq = qk[j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tt = 16 * tm + acc_row(i);
+                kds[j][i] *= lmv[i];
+                gmA[j][i] = (ss <= tt && rg.seg[i] == sgs) ? __expf(rg.G[i] - Gs) : 0.f;
+                pq[i] *= gmA[j][i];
+            }
+            store_tile_t_split(&Pt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq);
+        }
+        row_reduce_store(p, sm.g1[w & 1], tm);
+    }
+    {  // second half of the staging: V, T and delta (hi/lo) of the block
+        put_row8(Vr, t, cb, mask8(vr, on));
+        *reinterpret_cast<uint4 *>(&Tr[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
+        const float x[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+        Pack8 ph, pl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) split_bf16(x[e], ph.h[e], pl.h[e]);
+        put_row8(Dh, t, cb, ph.u);
+        put_row8(Dlo, t, cb, pl.u);
+    }
+    __syncthreads();
+    // Phase D: delta dS^T (-> dlam), ddelta = P^T dO + lam K dS + c delta.
+    float cs[4] = {0.f, 0.f, 0.f, 0.f}, ck[4] = {0.f, 0.f, 0.f, 0.f};
+    if (score_adj) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ss = r0 + i;
+            float dq = 0.f;
+#pragma unroll
+            for (int v2 = 0; v2 < NVB; ++v2) dq += a.ck_ddp[((int64_t)ci * NVB + v2) * C + ss];
+            const float nk = sqrtf(a.ck_kk[(int64_t)ci * C + ss]), nd = sqrtf(dq);
+            const bool ok = nk > 0.f && nd > 0.f;
+            cs[i] = ok ? sm.dsc[ss] * nk / nd : 0.f;
+            ck[i] = ok ? sm.dsc[ss] * nd / nk : 0.f;
+        }
+    }
+    f32x4 dka[NKB][2];
+    f32x4 xd[2] = {kds[0], kds[1]};
+    {
+        float p[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+            dka[kb][0] = dka[kb][1] = zero4();
+            gemm2_tr<64, LDB, LDK>(dka[kb], &Dh[(16 * tm) * LDB], dSt, tn0 + 4 * kb);
+            gemm2_tr<64, LDB, LDK>(dka[kb], &Dlo[(16 * tm) * LDB], dSt, tn0 + 4 * kb);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float kv[4];
+                ld4_rm_tr<LDK>(Ks, 16 * tm, 16 * (tn0 + 4 * kb + j), kv);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    p[i] += kv[i] * dka[kb][j][i];
+                    dka[kb][j][i] *= lmv[i];
+                }
+            }
+        }
+        row_reduce_store(p, sm.dlam[w & 1], tm);
+        gemm2_tr(xd, &Pt[(16 * tm) * LDB], dOs, tn0);  // B[v][t] = dO[t][v]
+        gemm2_tr(xd, &Ptl[(16 * tm) * LDB], dOs, tn0);
+        if (score_adj) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float dh[4], dlo[4];
+                ld4_rm_tr(Dh, 16 * tm, 16 * (tn0 + j), dh);
+                ld4_rm_tr(Dlo, 16 * tm, 16 * (tn0 + j), dlo);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xd[j][i] += cs[i] * (dh[i] + dlo[i]);
+            }
+        }
+    }
+    __syncthreads();  // P^T read by every wave before ddelta^T takes its tiles
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        store_tile_t_split(&Dd[(16 * (tn0 + j)) * LDB + 16 * tm],
+                           &Ddl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, xd[j]);
+    __syncthreads();
+    // Phase E: dR = T^T ddelta -> dV, the sum_v dR v part of dbeta, dR rows.
+    f32x4 dvv[2];
+    {
+        f32x4 x[2] = {zero4(), zero4()};
+#pragma unroll
+        for (int r = 0; r < 64; r += 32) {
+            const bf16x8_t tt = frag_tr(Tr, r, 16 * tm);  // A[s][t] = T[t][s]
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint16_t *Yh = &Dd[(16 * (tn0 + j)) * LDB], *Yl = &Ddl[(16 * (tn0 + j)) * LDB];
+                x[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tt, frag(Yh, LDB, r), x[j], 0, 0, 0);
+                x[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tt, frag(Yl, LDB, r), x[j], 0, 0, 0);
+            }
+        }
+        float p[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float vv[4];
+            ld4_rm_tr(Vr, 16 * tm, 16 * (tn0 + j), vv);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                p[i] += x[j][i] * vv[i];
+                dvv[j][i] = sm.gl.val[r0 + i] != 0.f ? rg.beta[i] * x[j][i] : 0.f;
+            }
+            store_tile_rm(&dRr[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, x[j]);
+        }
+        row_reduce_store(p, sm.b2[w & 1], tm);
+    }
+    __syncthreads();
+    // Phase F: dR S0^T (-> dK, dbeta, dgam), dA and dP (masked) -> MA^T, MP^T.
+    {
+        float p2[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+            f32x4 drs[2] = {zero4(), zero4()};
+            gemm2_tr<64, LDB, LDK>(drs, &dRr[(16 * tm) * LDB], S0t, tn0 + 4 * kb);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float kv[4];
+                ld4_rm_tr<LDK>(Ks, 16 * tm, 16 * (tn0 + 4 * kb + j), kv);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    p2[i] += kv[i] * drs[j][i];
+                    dka[kb][j][i] -= rg.beta[i] * rg.gam[i] * drs[j][i];
+                }
+            }
+        }
+        row_reduce_store(p2, sm.ku[w & 1], tm);
+    }
+    {
+        f32x4 da[2] = {zero4(), zero4()}, dp[2] = {zero4(), zero4()};
+        if (tn0 <= tm) {
+            gemm2(da, &dRr[(16 * tm) * LDB], Dh, tn0);
+            gemm2(da, &dRr[(16 * tm) * LDB], Dlo, tn0);
+            gemm2(dp, &dOs[(16 * tm) * LDB], Dh, tn0);
+            gemm2(dp, &dOs[(16 * tm) * LDB], Dlo, tn0);
+        }
+        float pb[4] = {0.f, 0.f, 0.f, 0.f}, pz[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int ss = 16 * (tn0 + j) + acc_col();
+            f32x4 ma, mp, z;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tt = 16 * tm + acc_row(i);
+                const float gm = gmA[j][i];
+                const float dA = ss < tt ? -da[j][i] : 0.f;
+                const float dP = dp[j][i];
+                ma[i] = dA * rg.beta[i] * gm;
+                mp[i] = dP * gm;
+                pb[i] += dA * gm * kk[j][i];
+                z[i] = (dA * rg.beta[i] * kk[j][i] + dP * qk[j][i]) * gm;
+                pz[i] += z[i];
+            }
+            store_tile_t(&MAt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, ma);
+            store_tile_t_split(&MPt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &MPtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, mp);
+            const float zc = col_reduce(z);
+            if ((lane_id() >> 4) == 0) sm.zc[tm][ss] = zc;
+        }
+        row_reduce_store(pb, sm.b1[w & 1], tm);
+        row_reduce_store(pz, sm.zr[w & 1], tm);
+    }
+    __syncthreads();
+    // Phase G: this block's dQ = MP K + gam dO S0^T and dK = (MA + MA^T) K + MP^T Q
+    // + lam delta dS^T - beta gam dR S0^T; block 0 leaves them in the workspace,
+    // block 1 adds them, masks and stages the rows.
+    {
+        f32x4 x[NKB][2], y[NKB][2];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) x[kb][0] = x[kb][1] = y[kb][0] = y[kb][1] = zero4();
+#pragma unroll
+        for (int r = 0; r < 64; r += 32) {
+            const bf16x8_t mp = frag_tr(MPt, r, 16 * tm), mpl = frag_tr(MPtl, r, 16 * tm);
+            const bf16x8_t ma = frag_tr(MAt, r, 16 * tm), mat = frag(&MAt[(16 * tm) * LDB], LDB, r);
+            const bf16x8_t pt = frag(&MPt[(16 * tm) * LDB], LDB, r), ptl = frag(&MPtl[(16 * tm) * LDB], LDB, r);
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int tn = 16 * (tn0 + 4 * kb + j);
+                    const bf16x8_t kbf = frag_tr<LDK>(Ks, r, tn);  // B[k][s] = K[s][k]
+                    const bf16x8_t qbf = frag_tr<LDK>(Qs, r, tn);  // B[k][t] = Q[t][k]
+                    x[kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mp, kbf, x[kb][j], 0, 0, 0);
+                    x[kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mpl, kbf, x[kb][j], 0, 0, 0);
+                    y[kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ma, kbf, y[kb][j], 0, 0, 0);
+                    y[kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mat, kbf, y[kb][j], 0, 0, 0);
+                    y[kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pt, qbf, y[kb][j], 0, 0, 0);
+                    y[kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ptl, qbf, y[kb][j], 0, 0, 0);
+                }
+        }
+        // Partials in accumulator layout: one float4 per lane and tile.
+        const int64_t pbase = (((int64_t)ci * NW + w) * NKB * 2) * 64 + lane_id();
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float kv[4] = {0.f, 0.f, 0.f, 0.f};
+                if (score_adj && last) ld4_rm_tr<LDK>(Ks, 16 * tm, 16 * (tn0 + 4 * kb + j), kv);
+                f32x4 gq, gk;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    gq[i] = x[kb][j][i] + rg.gam[i] * dos[kb][j][i];
+                    gk[i] = y[kb][j][i] + dka[kb][j][i] + ck[i] * kv[i];
+                }
+                const int64_t pi = pbase + (kb * 2 + j) * 64;
+                float4 *wq = reinterpret_cast<float4 *>(a.ws_gq) + pi;
+                float4 *wk = reinterpret_cast<float4 *>(a.ws_gk) + pi;
+                if (!last) {
+                    *wq = make_float4(gq[0], gq[1], gq[2], gq[3]);
+                    *wk = make_float4(gk[0], gk[1], gk[2], gk[3]);
+                } else {
+                    if (!first) {
+                        const float4 pq = *wq, pk = *wk;
+                        gq[0] += pq.x, gq[1] += pq.y, gq[2] += pq.z, gq[3] += pq.w;
+                        gk[0] += pk.x, gk[1] += pk.y, gk[2] += pk.z, gk[3] += pk.w;
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const bool von = sm.gl.val[r0 + i] != 0.f;
+                        gq[i] = von ? gq[i] : 0.f;
+                        gk[i] = von ? gk[i] : 0.f;
+                    }
+                    // Transposed gradient tiles ([channel][token]) in dead slots.
+                    store_tile_t(&dQt[(16 * (tn0 + 4 * kb + j)) * LDB + 16 * tm], LDB, gq);
+                    store_tile_t(&dKt[(16 * (tn0 + 4 * kb + j)) * LDB + 16 * tm], LDB, gk);
+                }
+            }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) store_tile_t(&dVt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, dvv[j]);
+    }
+    __syncthreads();
+    // Rows out: lane (token 16 (w%4) + l%16, channels 32 (w/4) + 8 (l/16) ..) of
+    // every 64-channel block stores one 16-byte piece per gradient.
+    {
+        const int l = lane_id();
+        const int tq = c * C + 16 * (w & 3) + (l & 15);
+        const int64_t row = ((int64_t)b * a.T + tq) * a.H + h;
+        const bf16x8_t gv = frag_tr(dVt, 32 * (w >> 2), 16 * (w & 3));
+        if (tq < a.T && a.dv)
+            *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dv) + row * KD + 64 * vb +
+                                          32 * (w >> 2) + 8 * (l >> 4)) = gv;
+        if (last) {
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+                const bf16x8_t gq = frag_tr(dQt, 64 * kb + 32 * (w >> 2), 16 * (w & 3));
+                const bf16x8_t gk = frag_tr(dKt, 64 * kb + 32 * (w >> 2), 16 * (w & 3));
+                const int64_t o = row * KD + 64 * kb + 32 * (w >> 2) + 8 * (l >> 4);
+                if (tq < a.T && a.dq) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dq) + o) = gq;
+                if (tq < a.T && a.dk) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dk) + o) = gk;
+            }
+        }
+    }
+    // Phase H: gate gradients (wave 0, lane == token; lane t holds token 63 - t).
+    if (w == 0) {
+        const int s = 63 - t, ts = c * C + s;
+        const float gam = sm.gl.gam[s], lam = sm.gl.lam[s], bet = sm.gl.beta[s];
+        const float dlam = sm.dlam[0][s] + sm.dlam[1][s];
+        const float u = sm.ku[0][s] + sm.ku[1][s];
+        float dG = sm.zr[0][s] + sm.zr[1][s] -
+                   (sm.zc[0][s] + sm.zc[1][s] + sm.zc[2][s] + sm.zc[3][s]) +
+                   gam * (sm.g1[0][s] + sm.g1[1][s] - bet * u) - lam * dlam;
+        const float tail = wave_sum(lam * dlam);
+        if (s == 63) {
+            float fr = 0.f;
+#pragma unroll
+            for (int q = 0; q < NW; ++q) fr += sm.frob[q];
+            dG += tail + sm.gl.gamC * fr;
+        }
+        float db = sm.b1[0][s] + sm.b1[1][s] + sm.b2[0][s] + sm.b2[1][s] - gam * u;
+        const int64_t gi = (int64_t)ci * C + s;
+        if (!last) {
+            a.ws_gg[gi] = dG;
+            a.ws_gb[gi] = db;
+        } else {
+            if (!first) {
+                dG += a.ws_gg[gi];
+                db += a.ws_gb[gi];
+            }
+            const float x = wave_scan_add(dG);
+            const bool von = sm.gl.val[s] != 0.f;
+            const bool rs = von && (s == 0 ? sm.gl.seg[0] == 1 : sm.gl.seg[s] != sm.gl.seg[s - 1]);
+            if (ts < a.T) {
+                const int64_t o = ((int64_t)b * a.T + ts) * a.H + h;
+                if (a.dg) a.dg[o] = (von && !rs) ? x : 0.f;
+                if (a.dbeta) a.dbeta[o] = von ? db : 0.f;
+            }
+        }
+    }
+}
+
+static inline void wmark(const hipEvent_t *ev, int i, hipStream_t stream) {
+    if (ev) (void)hipEventRecord(ev[i], stream);
+}
+
+hipError_t launch_wide_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
+    const int nch = a.B * a.H * a.nc;
+    wmark(ev, 0, stream);
+    hipLaunchKernelGGL(wide_prep_kernel, chunk_block_grid(nch), dim3(NT), 0, stream, a);
+    wmark(ev, 1, stream);
+    WScanArgs p{};
+    p.nc = a.nc;
+    p.B = a.B;
+    p.H = a.H;
+    p.m = a.map_m;
+    p.n = a.map_n;
+    p.ckpt = a.ck_state;
+    p.x0 = a.initial;
+    p.xout = a.final_state;
+    p.reverse = 0;
+    wmark(ev, 2, stream);
+    launch_wide_scan(p, stream);
+    wmark(ev, 3, stream);
+    wmark(ev, 4, stream);
+    hipLaunchKernelGGL(wide_out_kernel, chunk_block_grid(nch), dim3(NT), 0, stream, a);
+    hipLaunchKernelGGL(wide_score_kernel, dim3((unsigned)(((int64_t)nch * C + 255) / 256)), dim3(256),
+                       0, stream, a);
+    wmark(ev, 5, stream);
+    return hipGetLastError();
+}
+
+hipError_t launch_wide_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
+    const int nch = a.B * a.H * a.nc;
+    wmark(ev, 0, stream);
+    hipLaunchKernelGGL(wide_bprep_kernel, chunk_block_grid(nch), dim3(NT), 0, stream, a);
+    wmark(ev, 1, stream);
+    WScanArgs p{};
+    p.nc = a.nc;
+    p.B = a.B;
+    p.H = a.H;
+    p.m = a.ck_mt;
+    p.n = a.ws_n;
+    p.ckpt = a.ws_dstate;
+    p.x0.data = a.dfinal;
+    p.x0.s0 = (int64_t)a.H * KD * KD;
+    p.x0.s1 = (int64_t)KD * KD;
+    p.x0.s2 = KD;
+    p.x0.s3 = 1;
+    p.xout = a.dinitial;
+    p.reverse = 1;
+    wmark(ev, 2, stream);
+    launch_wide_scan(p, stream);
+    wmark(ev, 3, stream);
+    wmark(ev, 4, stream);
+    for (int pass = 0; pass < NVB; ++pass) {
+        ChunkArgs q = a;
+        q.pass = pass;
+        hipLaunchKernelGGL(wide_bgrad_kernel, dim3(nch), dim3(NT), 0, stream, q);
+    }
+    wmark(ev, 5, stream);
+    return hipGetLastError();
+}
+
+}  // namespace gdn2

@@ -158,7 +158,7 @@ GDN2_API int gdn2_backward(const gdn2_shape *shape, const gdn2_view *q, const gd
  * (g is the log decay, finite).  No counterpart entry exists in the reference
  * (it reaches this case only through the channel-wise op with broadcast
  * gates); this is the chunk-WY fast path the north-star benchmark measures.
- * The chunk-WY MFMA kernels run when chunk == 64, d_k == d_v == 64 and
+ * The chunk-WY MFMA kernels run when chunk == 64, d_k == d_v (64 or 128) and
  * q, k, v are BF16 with unit channel stride, 16-byte aligned data and every
  * other stride a multiple of 8 elements; any other call takes the
  * token-sequential kernels.  On the chunk-WY path d_output must satisfy the

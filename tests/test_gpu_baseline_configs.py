@@ -92,11 +92,20 @@ def test_lm512_full_size_split_continuation(dk):
 
 @pytest.mark.parametrize("b,h", [(0, 0), (3, 15)])
 def test_long8k_full_size_oracle_slices(dk, b, h):
-    """Config 2 at full size (B4 T8192 H16 d_k = d_v = 128, bf16): forward and
-    backward checked on whole sequences against the f64 oracle."""
+    """Config 2 at full size (B4 T8192 H16 d_k = d_v = 128, bf16) on the
+    d = 128 chunk-WY MFMA path (128 chunks per sequence): forward and backward
+    checked on whole sequences against the f64 oracle."""
     cfg, p = _cfg(2)
-    xs, out, fin, sc = _run_scalar(dk, p, torch.bfloat16, 64)
-    (out.float() * dev(p["d_output"])).sum().backward()
+    dk.stage_timing(True)
+    try:
+        xs, out, fin, sc = _run_scalar(dk, p, torch.bfloat16, 64)
+        (out.float() * dev(p["d_output"])).sum().backward()
+        torch.cuda.synchronize()
+        ran = set(dk.stage_times())
+    finally:
+        dk.stage_timing(False)
+    assert {"chunk_prep", "state_scan", "chunk_out", "chunk_bprep", "adjoint_scan",
+            "chunk_bgrad"} <= ran, f"config 2 must take the chunk-WY path: {sorted(ran)}"
     s = _slice(p, b, h)
     (o, f, c), grads = _oracle_scalar(s, cfg.keys, cfg.values, dO=s["d_output"])
     gate("output", out[b:b + 1, :, h:h + 1], o, TOL_BF16)

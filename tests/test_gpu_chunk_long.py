@@ -82,13 +82,14 @@ def test_long_chunk_path_matches_oracle(dk, T, H, reset_every):
     gate("d_initial", dinit, og["initial"], TOL_BF16)
 
 
-def test_long_split_continuation(dk):
+@pytest.mark.parametrize("D", [64, 128])
+def test_long_split_continuation(dk, D):
     """T = 8192 (128 chunks) scanned whole equals [0, 4096) then [4096, 8192)
     from the carried state; the backward of the two halves, chained through
     the state adjoint (the second half's d_initial is the first half's final
-    adjoint), equals the whole sequence's backward."""
+    adjoint), equals the whole sequence's backward.  d_k = d_v = 64 and 128."""
     T, half = 8192, 4096
-    p = problem(11, 2, T, 2, masks=False)
+    p = problem(11, 2, T, 2, masks=False, K=D, V=D)
     whole_fwd, whole_grads, ran = _fwd_bwd(dk, p)
     assert CHUNK_STAGES <= ran
     first = {n: (x[:, :half] if x is not None and x.ndim in (2, 3, 4) and x.shape[1] == T else x)
