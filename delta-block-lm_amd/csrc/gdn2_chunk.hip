@@ -63,7 +63,7 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
     uint16_t *Ks = sm.slot[0], *KBGs = sm.slot[1], *KLs = sm.slot[2], *VBs = sm.slot[3];
     uint16_t *Tb = sm.slot[0];  // over K once A is formed
     uint16_t *Wt = sm.u.wu[0], *Wtl = sm.u.wu[1], *Ut = sm.u.wu[2], *Utl = sm.u.wu[3];
-    const int tid = threadIdx.x, w = tid >> 6;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tg = c * C + t;
     const int tm = w >> 1, tn0 = 2 * (w & 1);
@@ -260,10 +260,11 @@ __device__ __forceinline__ void affine_step(int s, const AffineArgs &p, int bh, 
 
 // One wave per workgroup: wave w of head bh owns state columns 16w..16w+15,
 // which evolve independently (Y = M X acts on columns), so the four column
-// groups of a head run as four workgroups spread over the CUs.  Workgroups
-// are dealt to the 8 XCDs round-robin by index; the four column groups of a
-// head take indices with equal residue mod 8, so they share one XCD's L2 and
-// the head's M tiles leave HBM once.
+// groups of a head run as four workgroups spread over the CUs (the scan is
+// bound by the loads each CU can stream per step: a four-wave workgroup per
+// head, sharing M through L1, measured twice as slow).  Workgroups are dealt
+// to the 8 XCDs round-robin by index; the four column groups of a head take
+// indices with equal residue mod 8, so they share one XCD's L2.
 // NC > 0: the chunk count is a compile-time constant and the chunk loop is
 // straight-line code, so the loads of the three-deep (M, N) ring are waited
 // for one by one; NC == 0 runs any count in a rolled loop.
@@ -338,7 +339,7 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
     uint16_t *St = sm.slot[4], *Rt = sm.slot[5], *Pt = sm.slot[6], *Ptl = sm.slot[7];  // P^T hi/lo
     uint16_t *Dt = sm.slot[0], *Dl = sm.slot[1];  // over Q/K after phase 1
     uint16_t *Os = sm.slot[4];                    // over S0^T after phase 1
-    const int tid = threadIdx.x, w = tid >> 6;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, t0 = c * C, tg = t0 + t;
     const int tm = w >> 1, tn0 = 2 * (w & 1);
@@ -579,7 +580,7 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     uint16_t *Tb = sm.slot[4], *KBGs = sm.slot[5], *Pt = sm.slot[6], *Ptl = sm.slot[7];
     uint16_t *Xt = sm.slot[0], *Xtl = sm.slot[1];  // over Q/K after phase 1
     uint16_t *Wt = sm.slot[4], *Wtl = sm.slot[5];  // over T and beta gam K after phase 1
-    const int tid = threadIdx.x, w = tid >> 6;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
     const int tg = c * C + t;
@@ -745,7 +746,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     // F..G: MA and MP are stored transposed only; phase G reads them both ways.
     uint16_t *MAt = sm.slot[4], *MPt = sm.slot[7], *MPtl = sm.slot[10];
     uint16_t *dQt = sm.slot[2], *dKt = sm.slot[8], *dVt = sm.slot[11];  // gradients, G..end
-    const int tid = threadIdx.x, w = tid >> 6;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
     const int tg = c * C + t;

@@ -142,7 +142,7 @@ __global__ void __launch_bounds__(NT) wide_prep_kernel(ChunkArgs a) {
     uint16_t *Ks = sm.ks, *KLs = sm.kl, *KBGs = sm.kbg, *VBs = sm.vbt;
     uint16_t *Tb = sm.ks;  // over K once A is formed
     uint16_t *Wt = sm.u.wu[0], *Wtl = sm.u.wu[1], *Ut = sm.u.wu[2], *Utl = sm.u.wu[3];
-    const int tid = threadIdx.x, w = tid >> 6;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tg = c * C + t;
     const int tm = w >> 1, tn0 = 2 * (w & 1);
@@ -349,7 +349,7 @@ __device__ __forceinline__ void wscan_step(int s, const WScanArgs &p, int bh, in
 // indices with equal residue mod 8, so they share one XCD's L2.
 __global__ void __launch_bounds__(64 * SW) wide_scan_kernel(WScanArgs p) {
     __shared__ uint16_t xs[2][2][16 * LDX];
-    const int x = blockIdx.x, w = threadIdx.x >> 6, l = lane_id();
+    const int x = blockIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
     const int cg = (x >> 3) % NCG, bh = (x & 7) + 8 * (x / (8 * NCG));
     if (bh >= p.B * p.H) return;
     const int b = bh / p.H, h = bh % p.H;
@@ -427,7 +427,7 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a) {
     uint16_t *Pt = sm.pt, *Ptl = sm.ptl;
     uint16_t *Dt = sm.q, *Dl = sm.k;  // over Q/K after phase 1
     uint16_t *Os = sm.st;             // over S0^T after phase 2
-    const int tid = threadIdx.x, w = tid >> 6;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, t0 = c * C, tg = t0 + t;
     const int tm = w >> 1, tn0 = 2 * (w & 1);
@@ -596,7 +596,7 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a) {
     uint16_t *dOs = sm.dos, *Pt = sm.pt, *Ptl = sm.ptl;
     uint16_t *Xt = sm.q, *Xtl = sm.k;                  // over Q/K after phase 1
     uint16_t *Wt = sm.u.wt[0], *Wtl = sm.u.wt[1];      // over the phase-1 operands
-    const int tid = threadIdx.x, w = tid >> 6;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
     const int tg = c * C + t;
@@ -759,7 +759,7 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
     uint16_t *dQt = sm.dh, *dKt = sm.s0t, *dVt = sm.vr;
     static_assert(sizeof(sm.dh) + sizeof(sm.dlo) >= KD * LDB * 2, "dQ^T over dh, dlo");
     static_assert(sizeof(sm.s0t) + sizeof(sm.dos) >= KD * LDB * 2, "dK^T over s0t, dos");
-    const int tid = threadIdx.x, w = tid >> 6;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
     const int tg = c * C + t;

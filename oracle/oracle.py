@@ -166,3 +166,49 @@ def doc_limits_to_masks(doc_start, doc_end):
     valid = doc_end >= doc_start
     reset = valid & (doc_start == t)
     return valid.astype(np.uint8), reset.astype(np.uint8)
+
+
+# --- f32 chunked CPU scan (oracle/chunk_cpu.c) ------------------------------------
+# The reference's CPU tensor solver chunk::scan (crates/mixers/src/chunk.rs:129-250)
+# restated in f32; the "f32 chunked CPU scan" leg of bench.py's cpu_baseline.
+# Pinned against scan() (f64) by tests/test_chunk_cpu.py.
+
+_SO_CHUNK = os.path.join(_HERE, "_build", "libgdn2_chunk_cpu.so")
+_chunk_lib = None
+_fp = ctypes.POINTER(ctypes.c_float)
+
+
+def _chunk():
+    global _chunk_lib
+    if _chunk_lib is None:
+        if not os.path.exists(_SO_CHUNK):
+            build()
+        L = ctypes.CDLL(_SO_CHUNK)
+        L.gdn2_chunk_cpu_f32.argtypes = [ctypes.c_int64] * 5 + [ctypes.c_int] + [_fp] * 12
+        L.gdn2_chunk_cpu_f32.restype = ctypes.c_int
+        L.gdn2_chunk_cpu_threads.restype = ctypes.c_int
+        _chunk_lib = L
+    return _chunk_lib
+
+
+def chunk_threads() -> int:
+    return _chunk().gdn2_chunk_cpu_threads()
+
+
+def chunk_scan_f32(q, k, v, alpha, erase, write, valid, reset, initial=None, chunk=64):
+    """f32 chunked forward (chunk.rs:129-250).  Returns (output, final_state, scores)."""
+    f = lambda x: None if x is None else np.ascontiguousarray(np.asarray(x, dtype=np.float32))  # noqa
+    q, k, v, alpha, erase, write, valid, reset, initial = map(
+        f, (q, k, v, alpha, erase, write, valid, reset, initial))
+    B, T, H, K = q.shape
+    V = v.shape[3]
+    out = np.empty((B, T, H, V), np.float32)
+    fin = np.empty((B, H, K, V), np.float32)
+    sc = np.empty((B, T, H), np.float32)
+    p = lambda x: None if x is None else x.ctypes.data_as(_fp)  # noqa
+    rc = _chunk().gdn2_chunk_cpu_f32(B, T, H, K, V, chunk, p(q), p(k), p(v), p(alpha), p(erase),
+                                     p(write), p(valid), p(reset), p(initial), p(out), p(fin),
+                                     p(sc))
+    if rc != 0:
+        raise RuntimeError(f"gdn2_chunk_cpu_f32 failed ({rc})")
+    return out, fin, sc
