@@ -207,6 +207,60 @@ static int scalar_backward_impl(const gdn2_shape *shape, int chunk, const gdn2_v
                                 void *dk, void *dv, float *dbeta, float *dg, float *d_initial,
                                 void *workspace, size_t workspace_bytes, void *stream);
 
+// The chunk kernels take bf16 q/k/v with unit channel stride and 16-byte
+// aligned token rows (every stride a multiple of 8 elements).
+static bool rows_aligned(const gdn2_view *v) {
+    return v->stride[3] == 1 && ((uintptr_t)v->data & 15) == 0 && v->stride[0] % 8 == 0 &&
+           v->stride[1] % 8 == 0 && v->stride[2] % 8 == 0;
+}
+
+// The channel-wise op runs the 16-token chunk-WY MFMA kernels
+// (gdn2_chunk_cw.hip) for bf16 q/k/v with d_k = d_v = 64 and aligned rows,
+// whatever the chunk argument (the chunking changes no result); everything
+// else runs the token-sequential kernels.  Forward and backward apply the
+// same rule, so the checkpoint format always matches.
+static bool use_cw_path(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k,
+                        const gdn2_view *v) {
+    return cw_eligible_shape(shape) && q->dtype == GDN2_BF16 && rows_aligned(q) &&
+           rows_aligned(k) && rows_aligned(v);
+}
+
+static size_t training_checkpoint_bytes(const gdn2_shape *s) {
+    const size_t c = cw_eligible_shape(s) ? cw_checkpoint_bytes(s->batch, s->time, s->heads) : 0;
+    const size_t q = seq_checkpoint_bytes(s);
+    return c > q ? c : q;
+}
+
+static size_t training_workspace_bytes(const gdn2_shape *s) {
+    const size_t c = cw_eligible_shape(s) ? cw_workspace_bytes(s->batch, s->time, s->heads) : 0;
+    const size_t q = seq_workspace_bytes(s);
+    return c > q ? c : q;
+}
+
+static ChunkArgs cw_args(const gdn2_shape *s, const gdn2_view *q, const gdn2_view *k,
+                         const gdn2_view *v, const gdn2_view *alpha, const gdn2_view *erase,
+                         const gdn2_view *write, const gdn2_view *valid, const gdn2_view *reset) {
+    ChunkArgs a{};
+    a.B = (int)s->batch;
+    a.T = (int)s->time;
+    a.H = (int)s->heads;
+    a.nc = (a.T + CW_C - 1) / CW_C;
+    a.q = (const uint16_t *)q->data;
+    a.k = (const uint16_t *)k->data;
+    a.v = (const uint16_t *)v->data;
+    for (int d = 0; d < 3; ++d) {
+        a.qs[d] = q->stride[d];
+        a.ks[d] = k->stride[d];
+        a.vs[d] = v->stride[d];
+    }
+    a.alpha = make_view(alpha);
+    a.erase = make_view(erase);
+    a.write = make_view(write);
+    a.valid = make_view(valid);
+    a.reset = make_view(reset);
+    return a;
+}
+
 extern "C" {
 
 int gdn2_abi_version(void) { return 100; }
@@ -215,12 +269,12 @@ const char *gdn2_last_error(void) { return gdn2::last_error(); }
 
 size_t gdn2_training_checkpoint_bytes(const gdn2_shape *shape, int chunk) {
     if (check_shape(shape) || check_chunk(chunk)) return 0;
-    return seq_checkpoint_bytes(shape);
+    return training_checkpoint_bytes(shape);  // large enough for either kernel family
 }
 
 size_t gdn2_training_workspace_bytes(const gdn2_shape *shape, int chunk) {
     if (check_shape(shape) || check_chunk(chunk)) return 0;
-    return seq_workspace_bytes(shape);
+    return training_workspace_bytes(shape);
 }
 
 int gdn2_training_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q,
@@ -237,9 +291,20 @@ int gdn2_training_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q,
     if (!output || !final_state || !scores)
         return fail(GDN2_ERR_ARGUMENT, "output, final_state and scores must be non-null");
     if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
-    if (checkpoint_bytes < seq_checkpoint_bytes(shape))
+    if (checkpoint_bytes < training_checkpoint_bytes(shape))
         return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
-                    seq_checkpoint_bytes(shape), checkpoint_bytes);
+                    training_checkpoint_bytes(shape), checkpoint_bytes);
+    if (use_cw_path(shape, q, k, v)) {
+        ChunkArgs c = cw_args(shape, q, k, v, alpha, erase, write, valid, reset);
+        c.initial = make_view(initial);
+        c.out = output;
+        c.out_bf16 = output_dtype == GDN2_BF16;
+        c.final_state = final_state;
+        c.scores = scores;
+        cw_bind_checkpoint(c, checkpoint);
+        const hipEvent_t *ev = stage_events(0, (hipStream_t)stream);
+        return launch_status(launch_cw_fwd(c, (hipStream_t)stream, ev), "gdn2_training_scan");
+    }
     SeqArgs a = seq_args(shape, q, k, v, alpha, erase, write, valid, reset);
     a.initial = make_view(initial);
     a.out = output;
@@ -265,13 +330,37 @@ int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gdn2_view *
     GDN2_TRY(check_channel_inputs(shape, q, k, v, alpha, erase, write, valid, reset));
     if (d_output) GDN2_TRY(check_view(d_output, "d_output", q->dtype, true));
     if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
-    if (checkpoint_bytes < seq_checkpoint_bytes(shape))
+    if (checkpoint_bytes < training_checkpoint_bytes(shape))
         return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
-                    seq_checkpoint_bytes(shape), checkpoint_bytes);
+                    training_checkpoint_bytes(shape), checkpoint_bytes);
     if (!workspace) return fail(GDN2_ERR_ARGUMENT, "workspace is null");
-    if (workspace_bytes < seq_workspace_bytes(shape))
+    if (workspace_bytes < training_workspace_bytes(shape))
         return fail(GDN2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
-                    seq_workspace_bytes(shape), workspace_bytes);
+                    training_workspace_bytes(shape), workspace_bytes);
+    if (use_cw_path(shape, q, k, v)) {
+        if (d_output && d_output->data && !rows_aligned(d_output))
+            return fail(GDN2_ERR_ARGUMENT,
+                        "d_output needs unit channel stride and 16-byte aligned rows on the "
+                        "chunked path (bf16, d_k = d_v = 64)");
+        ChunkArgs c = cw_args(shape, q, k, v, alpha, erase, write, valid, reset);
+        cw_bind_checkpoint(c, const_cast<void *>(checkpoint));
+        cw_bind_workspace(c, workspace);
+        if (d_output && d_output->data) {
+            c.dout = (const uint16_t *)d_output->data;
+            for (int d = 0; d < 3; ++d) c.ds[d] = d_output->stride[d];
+        }
+        c.dfinal = d_final_state;
+        c.dscores = d_scores;
+        c.dq = dq;
+        c.dk = dk;
+        c.dv = dv;
+        c.dalpha = dalpha;
+        c.derase = derase;
+        c.dwrite = dwrite;
+        c.dinitial = d_initial;
+        const hipEvent_t *ev = stage_events(3, (hipStream_t)stream);
+        return launch_status(launch_cw_bwd(c, (hipStream_t)stream, ev), "gdn2_training_backward");
+    }
     SeqArgs a = seq_args(shape, q, k, v, alpha, erase, write, valid, reset);
     seq_bind_checkpoint(a, checkpoint);
     if (d_output) a.dout = make_view(d_output);
@@ -384,10 +473,6 @@ size_t gdn_scalar_workspace_bytes(const gdn2_shape *shape, int chunk) {
 // aligned token rows; everything else runs the token-sequential kernels.
 // Forward and backward apply the same rule, so the checkpoint format always
 // matches.
-static bool rows_aligned(const gdn2_view *v) {
-    return v->stride[3] == 1 && ((uintptr_t)v->data & 15) == 0 && v->stride[0] % 8 == 0 &&
-           v->stride[1] % 8 == 0 && v->stride[2] % 8 == 0;
-}
 
 static bool use_chunk_path(const gdn2_shape *shape, int chunk, const gdn2_view *q,
                            const gdn2_view *k, const gdn2_view *v) {

@@ -70,6 +70,17 @@ struct ChunkArgs {
     float *ck_kk, *ck_ddp;
     float *ws_gq, *ws_gk, *ws_gb, *ws_gg;
     int pass;  // value block of a bgrad launch
+    // Channel-wise path (16-token chunks): the gates alpha, erase [B,T,H,K] and
+    // write [B,T,H,V] (f32 views), the chunk-local cumulative log decay checkpoint,
+    // and the per-channel gate gradients.
+    View alpha, erase, write;
+    struct CwGate *ck_cwg;
+    float *ck_lam;
+    float *ck_tf;  // T = (I + A)^-1 per 16-token chunk, f32
+    // Lo parts (x - bf16(x)) of the chunk-start states and the chunk-end state
+    // adjoints, kept by the scan when non-null.
+    uint16_t *ck_state_lo, *ws_dstate_lo;
+    float *dalpha, *derase, *dwrite;
 };
 
 inline bool chunk_eligible_shape(const gdn2_shape *s, int chunk) {
@@ -114,6 +125,79 @@ inline void chunk_bind_workspace(ChunkArgs &a, void *ws) {
     a.ws_dstate = reinterpret_cast<uint16_t *>(p);
     a.ws_n = reinterpret_cast<float *>(p + n * CK_STATE_BYTES);
 }
+
+// ---- channel-wise path: per-channel gates, 16-token chunks, d_k = d_v = 64 ------
+constexpr int CW_C = 16;  // tokens per chunk
+struct CwGate {
+    float val[CW_C];
+    int seg[CW_C];  // resets at or before the token within the chunk
+};
+
+inline bool cw_eligible_shape(const gdn2_shape *s) {
+    return s->keys == CHUNK_D && s->values == CHUNK_D;
+}
+
+inline int64_t cw_chunk_count(int64_t B, int64_t T, int64_t H) {
+    return B * H * ((T + CW_C - 1) / CW_C);
+}
+
+// Checkpoint per chunk: S0^T (bf16 hi/lo, 64x64), T (f32 16x16), CwGate, the
+// cumulative log decay Lambda (f32 16x64), delta (f32 16x64), M = A_c^T and A_c
+// (bf16 64x64), B_c^T (f32 64x64).
+constexpr size_t CWK_STATE = (size_t)CHUNK_D * CHUNK_D * 2;
+constexpr size_t CWK_T = (size_t)CW_C * CW_C * 4;
+constexpr size_t CWK_GATE = sizeof(CwGate);
+constexpr size_t CWK_LAM = (size_t)CW_C * CHUNK_D * 4;
+constexpr size_t CWK_DELTA = (size_t)CW_C * CHUNK_D * 4;
+constexpr size_t CWK_MAPM = (size_t)CHUNK_D * CHUNK_D * 2;
+constexpr size_t CWK_MAPN = (size_t)CHUNK_D * CHUNK_D * 4;
+constexpr size_t CWK_CHUNK =
+    2 * CWK_STATE + CWK_T + CWK_GATE + CWK_LAM + CWK_DELTA + 2 * CWK_MAPM + CWK_MAPN;
+constexpr size_t CWW_CHUNK = 2 * CWK_STATE + CWK_MAPN;  // backward: dS^T (bf16 hi/lo), N^T (f32)
+
+inline size_t cw_checkpoint_bytes(int64_t B, int64_t T, int64_t H) {
+    return (size_t)cw_chunk_count(B, T, H) * CWK_CHUNK;
+}
+inline size_t cw_workspace_bytes(int64_t B, int64_t T, int64_t H) {
+    return (size_t)cw_chunk_count(B, T, H) * CWW_CHUNK;
+}
+
+inline void cw_bind_checkpoint(ChunkArgs &a, void *ck) {
+    const int64_t n = (int64_t)a.B * a.H * a.nc;
+    char *p = static_cast<char *>(ck);
+    a.ck_state = reinterpret_cast<uint16_t *>(p);
+    p += n * CWK_STATE;
+    a.ck_state_lo = reinterpret_cast<uint16_t *>(p);
+    p += n * CWK_STATE;
+    a.ck_tf = reinterpret_cast<float *>(p);
+    p += n * CWK_T;
+    a.ck_cwg = reinterpret_cast<CwGate *>(p);
+    p += n * CWK_GATE;
+    a.ck_lam = reinterpret_cast<float *>(p);
+    p += n * CWK_LAM;
+    a.ck_delta = reinterpret_cast<float *>(p);
+    p += n * CWK_DELTA;
+    a.ck_mt = reinterpret_cast<uint16_t *>(p);
+    p += n * CWK_MAPM;
+    a.map_m = reinterpret_cast<uint16_t *>(p);
+    p += n * CWK_MAPM;
+    a.map_n = reinterpret_cast<float *>(p);
+}
+
+inline void cw_bind_workspace(ChunkArgs &a, void *ws) {
+    const int64_t n = (int64_t)a.B * a.H * a.nc;
+    char *p = static_cast<char *>(ws);
+    a.ws_dstate = reinterpret_cast<uint16_t *>(p);
+    a.ws_dstate_lo = reinterpret_cast<uint16_t *>(p + n * CWK_STATE);
+    a.ws_n = reinterpret_cast<float *>(p + 2 * n * CWK_STATE);
+}
+
+// The affine scan over a.nc chunks of per-chunk 64 x 64 maps (gdn2_chunk.hip),
+// forward (state) or reverse (adjoint); shared with the channel-wise path.
+hipError_t launch_chunk_affine_scan(const ChunkArgs &a, bool reverse, hipStream_t stream);
+
+hipError_t launch_cw_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
+hipError_t launch_cw_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
 
 // ---- wide path: d_k = d_v = WIDE_D, value blocks of 64 -------------------------
 constexpr int WIDE_D = 128;

@@ -218,6 +218,7 @@ struct AffineArgs {
     const uint16_t *m;
     const float *n;
     uint16_t *ckpt;  // X^T per chunk, bf16
+    uint16_t *ckpt_lo;  // X^T - bf16(X^T) per chunk, bf16 (null: not kept)
     View x0;          // [B,H,64,64] strided (data may be null: zero)
     float *xout;      // [B,H,64,64] dense (may be null)
     int reverse;
@@ -234,6 +235,14 @@ __device__ __forceinline__ void affine_step(int s, const AffineArgs &p, int bh, 
     for (int tm = 0; tm < 4; ++tm) {
         *reinterpret_cast<uint2 *>(&ck[j * D + 16 * tm + acc_row(0)]) =
             make_uint2(bf16_pack2(X[tm][0], X[tm][1]), bf16_pack2(X[tm][2], X[tm][3]));
+        if (p.ckpt_lo) {
+            float r[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r[i] = X[tm][i] - bf16_val(bf16_bits(X[tm][i]));
+            *reinterpret_cast<uint2 *>(&p.ckpt_lo[((int64_t)bh * p.nc + c) * D * D + j * D + 16 * tm +
+                                                  acc_row(0)]) =
+                make_uint2(bf16_pack2(r[0], r[1]), bf16_pack2(r[2], r[3]));
+        }
         store_tile_t_split(xh + 16 * tm, xl + 16 * tm, LDB, X[tm]);  // [col][row]
     }
     __syncthreads();
@@ -486,12 +495,38 @@ static void launch_affine_scan(const AffineArgs &p, hipStream_t stream) {
     }
 }
 
-static AffineArgs affine_args(const ChunkArgs &a) {
+// The scan over a.nc chunks of 64 x 64 maps held in ChunkArgs' per-chunk
+// layout: forward (A_c, B_c^T; X0 = initial; chunk-start states to ck_state)
+// or reverse (M = A_c^T, N^T; X0 = the final-state adjoint, dense; chunk-end
+// adjoints to ws_dstate).  Shared by the scalar and channel-wise paths.
+hipError_t launch_chunk_affine_scan(const ChunkArgs &a, bool reverse, hipStream_t stream) {
     AffineArgs p{};
     p.nc = a.nc;
     p.B = a.B;
     p.H = a.H;
-    return p;
+    if (!reverse) {
+        p.m = a.map_m;
+        p.n = a.map_n;
+        p.ckpt = a.ck_state;
+        p.ckpt_lo = a.ck_state_lo;
+        p.x0 = a.initial;
+        p.xout = a.final_state;
+        p.reverse = 0;
+    } else {
+        p.m = a.ck_mt;
+        p.n = a.ws_n;
+        p.ckpt = a.ws_dstate;
+        p.ckpt_lo = a.ws_dstate_lo;
+        p.x0.data = a.dfinal;
+        p.x0.s0 = (int64_t)a.H * D * D;
+        p.x0.s1 = D * D;
+        p.x0.s2 = D;
+        p.x0.s3 = 1;
+        p.xout = a.dinitial;
+        p.reverse = 1;
+    }
+    launch_affine_scan(p, stream);
+    return hipSuccess;
 }
 
 static inline void mark(const hipEvent_t *ev, int i, hipStream_t stream) {
@@ -503,15 +538,8 @@ hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream, const hipEve
     mark(ev, 0, stream);
     hipLaunchKernelGGL(chunk_prep_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
     mark(ev, 1, stream);
-    AffineArgs p = affine_args(a);
-    p.m = a.map_m;
-    p.n = a.map_n;
-    p.ckpt = a.ck_state;
-    p.x0 = a.initial;
-    p.xout = a.final_state;
-    p.reverse = 0;
     mark(ev, 2, stream);
-    launch_affine_scan(p, stream);
+    (void)launch_chunk_affine_scan(a, false, stream);
     mark(ev, 3, stream);
     mark(ev, 4, stream);
     hipLaunchKernelGGL(chunk_out_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
@@ -1084,19 +1112,8 @@ hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream, const hipEve
     mark(ev, 0, stream);
     hipLaunchKernelGGL(chunk_bprep_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
     mark(ev, 1, stream);
-    AffineArgs p = affine_args(a);
-    p.m = a.ck_mt;
-    p.n = a.ws_n;
-    p.ckpt = a.ws_dstate;
-    p.x0.data = a.dfinal;
-    p.x0.s0 = (int64_t)a.H * D * D;
-    p.x0.s1 = D * D;
-    p.x0.s2 = D;
-    p.x0.s3 = 1;
-    p.xout = a.dinitial;
-    p.reverse = 1;
     mark(ev, 2, stream);
-    launch_affine_scan(p, stream);
+    (void)launch_chunk_affine_scan(a, true, stream);
     mark(ev, 3, stream);
     mark(ev, 4, stream);
     hipLaunchKernelGGL(chunk_bgrad_kernel, dim3(nchunks), dim3(NT), 0, stream, a);

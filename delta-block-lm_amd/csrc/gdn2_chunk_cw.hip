@@ -1,0 +1,1051 @@
+// Chunk-WY channel-wise GDN-2 (the reference's GdnTrainingOps recurrence) on
+// gfx950 MFMA, d_k = d_v = 64, bf16 q/k/v, f32 gates.
+//
+// Recurrence per valid token t (crates/mixers/src/reference.rs:68-111):
+//   bar = diag(alpha_t) S;  delta_t = w_t.v_t - bar^T (e_t.k_t);
+//   S_t = bar + k_t delta_t^T;  o_t = S_t^T q_t;  score_t = |k_t| |delta_t|.
+// Per chunk of CC = 16 tokens (the reference's own chunk for this op,
+// crates/kernels/src/gdn2.rs) with start state S0, per key channel i:
+//   Lambda_t = sum_{u <= t} log alpha_u           (chunk-local, padding: 0)
+//   D_ts     = exp(Lambda_t - Lambda_s), s <= t   (decay over tokens s+1..t, <= 1)
+//   b_t = exp(Lambda_t) [segment 0],  lam_s = exp(Lambda_15 - Lambda_s) [last segment]
+//   ehat = e.k,  Ahat = b.ehat,  Qhat = b.q,  Ktil = lam.k,  wv = w.v
+//   A_ts = sum_i ehat_t D_ts k_s   (s < t, same segment),  T = (I + A)^-1
+//   P_ts = sum_i q_t D_ts k_s      (s <= t, same segment)
+//   R = wv - Ahat S0,  delta = T R,  O = Qhat S0 + P delta
+//   S_16 = A_c S0 + B_c,  A_c = diag(b_15) - Ktil^T W',  W' = T Ahat,
+//                          B_c = Ktil^T U,  U = T wv.
+// Segments split the chunk at valid resets, as in gdn2_chunk.hip.  The decay
+// factors are elementwise per channel, so A and P (16 x 16, one exponential
+// per channel and token pair) are formed on the VALU; every product with the
+// state (R, delta, O, the maps and, in the backward, every state-sized
+// adjoint) runs on v_mfma_f32_16x16x32_bf16 with the 16-token reduction padded
+// to 32 by zero rows or columns.  The chunk maps feed the scalar path's affine
+// scan (gdn2_chunk.hip) over the T / 16 chunks.
+//
+// log alpha is floored at -80 (exp(-80) ~ 2e-35): below that the decay is
+// taken as exp(-80) and the alpha gradient is zero.  The alpha gradient is the
+// log-domain adjoint divided by alpha, so its absolute error grows as 1/alpha.
+#include "gdn2_chunk_tile.h"
+
+namespace gdn2 {
+
+namespace {
+
+constexpr int CC = CW_C;           // tokens per chunk
+constexpr int NW4 = 4, NT4 = 256;  // four waves per workgroup
+constexpr float LOG_FLOOR = -80.f;
+constexpr int LDL = 68;            // f32 row stride of [token][channel] tiles
+constexpr int LDW = 40;            // bf16 row stride of [channel][token] tiles (32 used)
+constexpr int LDI = 17;            // f32 row stride of 16 x 16 tiles
+constexpr int RT32 = 32 * LDB;     // [token][channel] bf16 tile with rows 16..31 zero
+constexpr int RT16 = CC * LDB;     // [token][channel] bf16 tile, 16 rows
+constexpr int CT64 = 64 * LDW;     // [channel][token] bf16 tile, columns 16..31 zero
+
+__device__ __forceinline__ void zero_lds(uint16_t *p, int n, int tid) {
+    for (int i = tid; i < n; i += NT4) p[i] = 0;
+}
+
+// Token t's channels [c0, c0 + 4) of a bf16 sequence (unit channel stride).
+__device__ __forceinline__ void load4_bf16(const uint16_t *base, const int64_t *s, int b, int tg,
+                                           int h, int c0, bool inb, float (&o)[4]) {
+    uint2 r = make_uint2(0, 0);
+    if (inb) r = *reinterpret_cast<const uint2 *>(base + (int64_t)b * s[0] + (int64_t)tg * s[1] +
+                                                  (int64_t)h * s[2] + c0);
+    o[0] = bf16_val((uint16_t)(r.x & 0xffff));
+    o[1] = bf16_val((uint16_t)(r.x >> 16));
+    o[2] = bf16_val((uint16_t)(r.y & 0xffff));
+    o[3] = bf16_val((uint16_t)(r.y >> 16));
+}
+
+__device__ __forceinline__ void load4_f32(const View &v, int b, int tg, int h, int c0, bool inb,
+                                          float fill, float (&o)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = inb ? ld4<float>(v, b, tg, h, c0 + e) : fill;
+}
+
+__device__ __forceinline__ void put4_bf16(uint16_t *p, const float (&x)[4]) {
+    *reinterpret_cast<uint2 *>(p) = make_uint2(bf16_pack2(x[0], x[1]), bf16_pack2(x[2], x[3]));
+}
+
+// Four values as bf16 hi/lo pairs (x ~= hi + lo, ~16 mantissa bits over both).
+__device__ __forceinline__ void put4_split(uint16_t *hi, uint16_t *lo, const float (&x)[4]) {
+    uint16_t h[4], o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) split_bf16(x[e], h[e], o[e]);
+    *reinterpret_cast<uint2 *>(hi) =
+        make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+    *reinterpret_cast<uint2 *>(lo) =
+        make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+}
+
+// T (f32 checkpoint, 16 x 16) into hi/lo LDS rows; thread (r = tid/16, s = tid%16).
+__device__ __forceinline__ void load_t_split(const float *ckt, uint16_t *th, uint16_t *tl, int tid) {
+    const int r = tid >> 4, s = tid & 15;
+    uint16_t hi, lo;
+    split_bf16(ckt[r * CC + s], hi, lo);
+    th[r * LDB + s] = hi;
+    tl[r * LDB + s] = lo;
+}
+
+__device__ __forceinline__ void put4_f32(float *p, const float (&x)[4]) {
+    *reinterpret_cast<float4 *>(p) = make_float4(x[0], x[1], x[2], x[3]);
+}
+
+__device__ __forceinline__ void get4_f32(const float *p, float (&x)[4]) {
+    const float4 v = *reinterpret_cast<const float4 *>(p);
+    x[0] = v.x, x[1] = v.y, x[2] = v.z, x[3] = v.w;
+}
+
+// (I + A)^-1 of a strictly lower 16 x 16 A (f32, row stride lda) into T (row
+// stride ldt) by forward substitution; one wave.  Lane (col = l/4, part = l%4)
+// holds rows part, part + 4, part + 8, part + 12 of column col, and the four
+// parts of a column (one DPP quad) split each row's dot product.
+__device__ __forceinline__ void inv16(const float *A, int lda, float *T, int ldt) {
+    const int l = lane_id(), col = l >> 2, part = l & 3;
+    float Tq[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < CC; ++r) {
+        float acc = 0.f;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int s = part + 4 * m;
+            if (s < r) acc += A[r * lda + s] * Tq[m];
+        }
+        acc += dpp<0xB1>(acc);  // lane ^ 1
+        acc += dpp<0x4E>(acc);  // lane ^ 2
+        if ((r & 3) == part) Tq[r >> 2] = (r == col ? 1.f : 0.f) - acc;
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) T[(part + 4 * m) * ldt + col] = Tq[m];
+}
+
+// Token pair p (0 <= p < n) of a 16-token chunk: strictly lower pairs
+// (t, s), s < t (n = 120) or lower pairs s <= t (n = 136).
+__device__ __forceinline__ void pair_of(int p, bool strict, int &t, int &s) {
+    // the largest r with r (r + 1) / 2 <= p, by the inverse triangular number
+    const int q = p;
+    int r = (int)((sqrtf(8.f * (float)q + 1.f) - 1.f) * 0.5f);
+    // row r covers [r (r + 1) / 2, (r + 1)(r + 2) / 2): fix float rounding
+    while ((r + 1) * (r + 2) / 2 <= q) ++r;
+    while (r * (r + 1) / 2 > q) --r;
+    const int off = q - r * (r + 1) / 2;
+    if (strict) {  // pairs (r + 1, off), off <= r
+        t = r + 1;
+        s = off;
+    } else {  // pairs (r, off), off <= r
+        t = r;
+        s = off;
+    }
+}
+
+// Elementwise decay product of a token pair over 32 channels [32 half, +32):
+// sum_i x_t[i] exp(L_t[i] - L_s[i]) y_s[i] (f32 tiles, row stride LDL).
+__device__ __forceinline__ float pair_dot32(const float *x, const float *y, const float *L, int t,
+                                            int s, int half) {
+    float acc = 0.f;
+#pragma unroll 8
+    for (int i = 32 * half; i < 32 * half + 32; ++i)
+        acc += x[t * LDL + i] * __expf(L[t * LDL + i] - L[s * LDL + i]) * y[s * LDL + i];
+    return acc;
+}
+
+struct CwPrepSmem {
+    float lam[CC * LDL];   // log alpha, then Lambda
+    float eh[CC * LDL];    // e.k (f32)
+    float kf[CC * LDL];    // k (bf16 values)
+    uint16_t ah[RT32];     // Ahat rows hi (rows 16..31 zero); with wv: A_c^T staging
+    uint16_t wv[RT32];     // w.v rows hi (rows 16..31 zero)
+    uint16_t ahl[RT32], wvl[RT32];  // lo parts
+    uint16_t kl[RT32], kll[RT32];   // Ktil rows hi/lo (rows 16..31 zero)
+    uint16_t tb[RT16], tbl[RT16];   // T rows hi/lo (columns 16..31 zero)
+    uint16_t wt[4][CT64];  // W'^T hi/lo, U^T hi/lo ([channel][token])
+    float af[CC * LDI], tf[CC * LDI];
+    float bc[64];
+    float val[CC];
+    int rs[CC], seg[CC];
+};
+
+}  // namespace
+
+// ---- prep: gates, A, T and the state map of every 16-token chunk --------------
+__global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a) {
+    __shared__ CwPrepSmem sm;
+    static_assert(sizeof(sm.ah) + sizeof(sm.wv) >= 64 * LDB * 2, "A_c^T staging over ah, wv");
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = lane_id();
+    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = tid >> 4, c0 = 4 * (tid & 15), tg = c * CC + t;
+    const bool inb = tg < a.T;
+    zero_lds(sm.ah + RT16, RT32 - RT16, tid);
+    zero_lds(sm.wv + RT16, RT32 - RT16, tid);
+    zero_lds(sm.ahl + RT16, RT32 - RT16, tid);
+    zero_lds(sm.wvl + RT16, RT32 - RT16, tid);
+    zero_lds(sm.kl + RT16, RT32 - RT16, tid);
+    zero_lds(sm.kll + RT16, RT32 - RT16, tid);
+    for (int i = tid; i < CC * 16; i += NT4) {
+        sm.tb[(i >> 4) * LDB + 16 + (i & 15)] = 0;
+        sm.tbl[(i >> 4) * LDB + 16 + (i & 15)] = 0;
+    }
+    for (int i = tid; i < 4 * 64 * 16; i += NT4)
+        sm.wt[i >> 10][((i >> 4) & 63) * LDW + 16 + (i & 15)] = 0;
+    // Loads: token t, channels c0 .. c0 + 3.
+    const float vld = inb ? ld4<float>(a.valid, b, tg, 0, 0) : 0.f;
+    const float rst = inb ? ld4<float>(a.reset, b, tg, 0, 0) : 0.f;
+    const bool on = vld != 0.f;
+    float kv[4], vv[4], al[4], er[4], wr[4];
+    load4_bf16(a.k, a.ks, b, tg, h, c0, inb && on, kv);
+    load4_bf16(a.v, a.vs, b, tg, h, c0, inb && on, vv);
+    load4_f32(a.alpha, b, tg, h, c0, inb && on, 1.f, al);
+    load4_f32(a.erase, b, tg, h, c0, inb && on, 0.f, er);
+    load4_f32(a.write, b, tg, h, c0, inb && on, 0.f, wr);
+    {
+        float la[4], eh[4], wv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            la[e] = on ? fmaxf(__logf(al[e]), LOG_FLOOR) : 0.f;
+            eh[e] = er[e] * kv[e];
+            wv[e] = wr[e] * vv[e];
+        }
+        put4_f32(&sm.lam[t * LDL + c0], la);
+        put4_f32(&sm.eh[t * LDL + c0], eh);
+        put4_f32(&sm.kf[t * LDL + c0], kv);
+        put4_split(&sm.wv[t * LDB + c0], &sm.wvl[t * LDB + c0], wv);
+        if (c0 == 0) {
+            sm.val[t] = on ? 1.f : 0.f;
+            sm.rs[t] = (on && rst != 0.f) ? 1 : 0;
+        }
+    }
+    __syncthreads();
+    // Lambda: running sums over the chunk's tokens, one channel per thread;
+    // segment index of every token.
+    if (tid < 64) {
+        float acc = 0.f;
+#pragma unroll
+        for (int tt = 0; tt < CC; ++tt) {
+            acc += sm.lam[tt * LDL + tid];
+            sm.lam[tt * LDL + tid] = acc;
+        }
+    } else if (tid == 64) {
+        int s = 0;
+#pragma unroll
+        for (int tt = 0; tt < CC; ++tt) {
+            s += sm.rs[tt];
+            sm.seg[tt] = s;
+        }
+    }
+    __syncthreads();
+    {  // Ahat and Ktil rows, b at the chunk end
+        const int sgt = sm.seg[t], sg15 = sm.seg[CC - 1];
+        float ah[4], kl[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float L = sm.lam[t * LDL + c0 + e], L15 = sm.lam[(CC - 1) * LDL + c0 + e];
+            ah[e] = (sgt == 0 ? __expf(L) : 0.f) * sm.eh[t * LDL + c0 + e];
+            kl[e] = (sgt == sg15 ? __expf(L15 - L) : 0.f) * kv[e];
+            if (t == CC - 1) sm.bc[c0 + e] = sg15 == 0 ? __expf(L15) : 0.f;
+        }
+        put4_split(&sm.ah[t * LDB + c0], &sm.ahl[t * LDB + c0], ah);
+        put4_split(&sm.kl[t * LDB + c0], &sm.kll[t * LDB + c0], kl);
+    }
+    {  // A (strictly lower, same segment): pair p on lanes 2p, 2p + 1 (channel halves)
+        const int p = tid >> 1, half = tid & 1;
+        int tt = 0, ss = 0;
+        if (p < 120) pair_of(p, true, tt, ss);
+        float acc = p < 120 ? pair_dot32(sm.eh, sm.kf, sm.lam, tt, ss, half) : 0.f;
+        acc += dpp<0xB1>(acc);
+        if (p < 120 && half == 0) sm.af[tt * LDI + ss] = sm.seg[tt] == sm.seg[ss] ? acc : 0.f;
+    }
+    __syncthreads();
+    if (w == 0) inv16(sm.af, LDI, sm.tf, LDI);
+    __syncthreads();
+    {  // T (unit lower): hi/lo LDS operands and the f32 checkpoint; gates and Lambda out
+        const int r = tid >> 4, s = tid & 15;
+        const float x = s <= r ? sm.tf[r * LDI + s] : 0.f;
+        uint16_t hi, lo;
+        split_bf16(x, hi, lo);
+        sm.tb[r * LDB + s] = hi;
+        sm.tbl[r * LDB + s] = lo;
+        a.ck_tf[(int64_t)ci * CC * CC + r * CC + s] = x;
+        if (tid < CC) {
+            a.ck_cwg[ci].val[tid] = sm.val[tid];
+            a.ck_cwg[ci].seg[tid] = sm.seg[tid];
+        }
+        float x4[4];
+        get4_f32(&sm.lam[t * LDL + c0], x4);
+        put4_f32(a.ck_lam + (int64_t)ci * CC * 64 + t * 64 + c0, x4);
+    }
+    __syncthreads();
+    // W' = T Ahat, U = T wv (wave w: channel tile w), transposed hi/lo; products of
+    // hi/lo pairs keep three terms (hi hi, hi lo, lo hi).
+    {
+        const bf16x8_t ta = frag(sm.tb, LDB, 0), tal = frag(sm.tbl, LDB, 0);
+        const bf16x8_t ab = frag_tr(sm.ah, 0, 16 * w), abl = frag_tr(sm.ahl, 0, 16 * w);
+        const bf16x8_t vb = frag_tr(sm.wv, 0, 16 * w), vbl = frag_tr(sm.wvl, 0, 16 * w);
+        f32x4 x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, ab, zero4(), 0, 0, 0);
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, abl, x, 0, 0, 0);
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tal, ab, x, 0, 0, 0);
+        f32x4 y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, vb, zero4(), 0, 0, 0);
+        y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, vbl, y, 0, 0, 0);
+        y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tal, vb, y, 0, 0, 0);
+        store_tile_t_split(&sm.wt[0][(16 * w) * LDW], &sm.wt[1][(16 * w) * LDW], LDW, x);
+        store_tile_t_split(&sm.wt[2][(16 * w) * LDW], &sm.wt[3][(16 * w) * LDW], LDW, y);
+    }
+    __syncthreads();
+    // A_c = diag(b_15) - Ktil^T W', B_c = Ktil^T U: wave w owns row tile w.
+    f32x4 am[4];
+    {
+        const bf16x8_t ka = frag_tr(sm.kl, 0, 16 * w);  // A[i][s] = Ktil[s][16 w + i]
+        const bf16x8_t kal = frag_tr(sm.kll, 0, 16 * w);
+        float *Bt = a.map_n + (int64_t)ci * 64 * 64;     // B_c^T [col][row]
+#pragma unroll
+        for (int tn = 0; tn < 4; ++tn) {
+            f32x4 x = zero4(), y = zero4();
+            const bf16x8_t wh = frag(&sm.wt[0][(16 * tn) * LDW], LDW, 0);
+            const bf16x8_t uh = frag(&sm.wt[2][(16 * tn) * LDW], LDW, 0);
+            x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, wh, x, 0, 0, 0);
+            x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, frag(&sm.wt[1][(16 * tn) * LDW], LDW, 0), x, 0, 0, 0);
+            x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kal, wh, x, 0, 0, 0);
+            y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, uh, y, 0, 0, 0);
+            y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, frag(&sm.wt[3][(16 * tn) * LDW], LDW, 0), y, 0, 0, 0);
+            y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kal, uh, y, 0, 0, 0);
+            const int cc = 16 * tn + acc_col();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) am[tn][i] = (16 * w + acc_row(i) == cc ? sm.bc[cc] : 0.f) - x[i];
+            *reinterpret_cast<float4 *>(&Bt[cc * 64 + 16 * w + acc_row(0)]) = make_float4(y[0], y[1], y[2], y[3]);
+        }
+    }
+    __syncthreads();  // operand reads done: A_c^T goes over ah, wv
+    uint16_t *Mt = sm.ah;
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) store_tile_t(&Mt[(16 * tn) * LDB + 16 * w], LDB, am[tn]);
+    __syncthreads();
+    {  // M = A_c^T rows, and A_c rows read across them
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int p = tid + NT4 * i, r = p >> 3, cb = 8 * (p & 7);
+            *reinterpret_cast<uint4 *>(a.ck_mt + (int64_t)ci * 64 * 64 + r * 64 + cb) =
+                *reinterpret_cast<const uint4 *>(&Mt[r * LDB + cb]);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int cr = 16 * w, r0 = 32 * i;
+            const bf16x8_t ar = frag_tr(Mt, r0, cr);  // A_c[cr + n][r0 + 8 g + e]
+            *reinterpret_cast<bf16x8_t *>(a.map_m + (int64_t)ci * 64 * 64 + (cr + (l & 15)) * 64 +
+                                          r0 + 8 * (l >> 4)) = ar;
+        }
+    }
+}
+
+// ---- out: outputs, edits and scores of every chunk ------------------------------
+namespace {
+struct CwOutSmem {
+    float lam[CC * LDL];   // Lambda
+    float qf[CC * LDL];    // q (bf16 values)
+    float kf[CC * LDL];    // k
+    float wvf[CC * LDL];   // w.v (f32)
+    uint16_t qh[RT16], qhl[RT16];  // Qhat rows hi/lo;  O rows (bf16) over qh at the end
+    uint16_t ah[RT16], ahl[RT16];  // Ahat rows hi/lo
+    uint16_t st[64 * LDB], stl[64 * LDB];  // S0^T rows [v][k] hi/lo
+    uint16_t tb[RT16], tbl[RT16];  // T rows hi/lo (columns 16..31 zero)
+    uint16_t pr[RT16], prl[RT16];  // P rows hi/lo (columns 16..31 zero)
+    uint16_t rt[CT64], rtl[CT64];  // R^T hi/lo
+    uint16_t dt[CT64], dtl[CT64];  // delta^T hi/lo
+    float dd[NW4][CC];
+    float kk[CC];
+    float val[CC];
+    int seg[CC];
+};
+}  // namespace
+
+__global__ void __launch_bounds__(NT4) cw_out_kernel(ChunkArgs a) {
+    __shared__ CwOutSmem sm;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = tid >> 4, c0 = 4 * (tid & 15), t0 = c * CC, tg = t0 + t;
+    const bool inb = tg < a.T;
+    for (int i = tid; i < CC * 16; i += NT4) {
+        const int r = i >> 4, cc = 16 + (i & 15);
+        sm.tb[r * LDB + cc] = 0;
+        sm.tbl[r * LDB + cc] = 0;
+        sm.pr[r * LDB + cc] = 0;
+        sm.prl[r * LDB + cc] = 0;
+    }
+    for (int i = tid; i < 4 * 64 * 16; i += NT4) {
+        uint16_t *tl = (i >> 10) == 0 ? sm.rt : (i >> 10) == 1 ? sm.rtl : (i >> 10) == 2 ? sm.dt : sm.dtl;
+        tl[((i >> 4) & 63) * LDW + 16 + (i & 15)] = 0;
+    }
+    const CwGate *gb = a.ck_cwg + ci;
+    const float va = gb->val[t];
+    const int sg = gb->seg[t];
+    const bool on = va != 0.f;
+    float qv[4], kv[4], vv[4], er[4], wr[4], L[4];
+    load4_bf16(a.q, a.qs, b, tg, h, c0, inb && on, qv);
+    load4_bf16(a.k, a.ks, b, tg, h, c0, inb && on, kv);
+    load4_bf16(a.v, a.vs, b, tg, h, c0, inb && on, vv);
+    load4_f32(a.erase, b, tg, h, c0, inb && on, 0.f, er);
+    load4_f32(a.write, b, tg, h, c0, inb && on, 0.f, wr);
+    get4_f32(a.ck_lam + (int64_t)ci * CC * 64 + t * 64 + c0, L);
+    {
+        const uint16_t *S0 = a.ck_state + (int64_t)ci * 64 * 64;
+        const uint16_t *S0l = a.ck_state_lo + (int64_t)ci * 64 * 64;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int p = tid + NT4 * i, r = p >> 3, cb = 8 * (p & 7);
+            *reinterpret_cast<uint4 *>(&sm.st[r * LDB + cb]) =
+                *reinterpret_cast<const uint4 *>(S0 + r * 64 + cb);
+            *reinterpret_cast<uint4 *>(&sm.stl[r * LDB + cb]) =
+                *reinterpret_cast<const uint4 *>(S0l + r * 64 + cb);
+        }
+        load_t_split(a.ck_tf + (int64_t)ci * CC * CC, sm.tb, sm.tbl, tid);
+    }
+    {
+        float b4[4], qh[4], ah[4], wv[4];
+        float ksq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            b4[e] = sg == 0 ? __expf(L[e]) : 0.f;
+            qh[e] = b4[e] * qv[e];
+            ah[e] = b4[e] * er[e] * kv[e];
+            wv[e] = wr[e] * vv[e];
+            ksq += kv[e] * kv[e];
+        }
+        put4_f32(&sm.lam[t * LDL + c0], L);
+        put4_f32(&sm.qf[t * LDL + c0], qv);
+        put4_f32(&sm.kf[t * LDL + c0], kv);
+        put4_f32(&sm.wvf[t * LDL + c0], wv);
+        put4_split(&sm.qh[t * LDB + c0], &sm.qhl[t * LDB + c0], qh);
+        put4_split(&sm.ah[t * LDB + c0], &sm.ahl[t * LDB + c0], ah);
+        // |k_t|^2: sum over the 16 threads of token t (lanes 16 r .. 16 r + 15)
+        ksq = row16_sum(ksq);
+        if ((tid & 15) == 0) {
+            sm.kk[t] = ksq;
+            sm.val[t] = va;
+            sm.seg[t] = sg;
+        }
+    }
+    __syncthreads();
+    // P (lower, same segment), elementwise; pair p on lanes 2p, 2p + 1.
+    for (int base = 0; base < 2 * 136; base += NT4) {
+        const int task = base + tid, p = task >> 1, half = task & 1;
+        int tt = 0, ss = 0;
+        if (p < 136) pair_of(p, false, tt, ss);
+        float acc = p < 136 ? pair_dot32(sm.qf, sm.kf, sm.lam, tt, ss, half) : 0.f;
+        acc += dpp<0xB1>(acc);
+        if (p < 136 && half == 0) {
+            uint16_t hi, lo;
+            split_bf16(sm.seg[tt] == sm.seg[ss] ? acc : 0.f, hi, lo);
+            sm.pr[tt * LDB + ss] = hi;
+            sm.prl[tt * LDB + ss] = lo;
+        }
+    }
+    for (int i = tid; i < 120; i += NT4) {  // zero the strict upper triangle of P
+        int tt, ss;
+        pair_of(i, true, tt, ss);
+        sm.pr[ss * LDB + tt] = 0;
+        sm.prl[ss * LDB + tt] = 0;
+    }
+    // R = w.v - Ahat S0 and Qhat S0 for value tile w.
+    f32x4 qs = zero4();
+    {
+        f32x4 x = zero4();
+#pragma unroll
+        for (int r = 0; r < 64; r += 32) {
+            const bf16x8_t sb = frag(&sm.st[(16 * w) * LDB], LDB, r);
+            const bf16x8_t sbl = frag(&sm.stl[(16 * w) * LDB], LDB, r);
+            const bf16x8_t ab = frag(sm.ah, LDB, r), qb = frag(sm.qh, LDB, r);
+            x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, sb, x, 0, 0, 0);
+            x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.ahl, LDB, r), sb, x, 0, 0, 0);
+            x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, sbl, x, 0, 0, 0);
+            qs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qb, sb, qs, 0, 0, 0);
+            qs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.qhl, LDB, r), sb, qs, 0, 0, 0);
+            qs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qb, sbl, qs, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = sm.wvf[acc_row(i) * LDL + 16 * w + acc_col()] - x[i];
+        store_tile_t_split(&sm.rt[(16 * w) * LDW], &sm.rtl[(16 * w) * LDW], LDW, x);
+    }
+    __syncthreads();
+    // delta = T R; |delta_t|^2 partials; delta^T hi/lo; delta to the checkpoint.
+    f32x4 dl = zero4();
+    {
+        const bf16x8_t ta = frag(sm.tb, LDB, 0), tal = frag(sm.tbl, LDB, 0);
+        const bf16x8_t rb = frag(&sm.rt[(16 * w) * LDW], LDW, 0);
+        dl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, rb, dl, 0, 0, 0);
+        dl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, frag(&sm.rtl[(16 * w) * LDW], LDW, 0), dl, 0, 0, 0);
+        dl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tal, rb, dl, 0, 0, 0);
+        float p4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p4[i] = dl[i] * dl[i];
+        row_reduce_store(p4, sm.dd[w], 0);
+        store_tile_t_split(&sm.dt[(16 * w) * LDW], &sm.dtl[(16 * w) * LDW], LDW, dl);
+        float *dck = a.ck_delta + (int64_t)ci * CC * 64;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dck[acc_row(i) * 64 + 16 * w + acc_col()] = dl[i];
+    }
+    __syncthreads();
+    // O = Qhat S0 + P delta (P hi/lo x delta hi/lo, three terms).
+    {
+        f32x4 x = qs;
+        const bf16x8_t ph = frag(sm.pr, LDB, 0), pl = frag(sm.prl, LDB, 0);
+        const bf16x8_t dh = frag(&sm.dt[(16 * w) * LDW], LDW, 0), dlo = frag(&sm.dtl[(16 * w) * LDW], LDW, 0);
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, dh, x, 0, 0, 0);
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, dlo, x, 0, 0, 0);
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, dh, x, 0, 0, 0);
+        if (a.out_bf16) {
+            store_tile_rm(&sm.qh[16 * w], LDB, x);  // O rows over Qhat (read in phase 1)
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tq = t0 + acc_row(i);
+                if (tq < a.T)
+                    reinterpret_cast<float *>(a.out)[(((int64_t)b * a.T + tq) * a.H + h) * 64 + 16 * w +
+                                                     acc_col()] = x[i];
+            }
+        }
+    }
+    __syncthreads();
+    if (a.out_bf16 && tid < CC * 8) {
+        const int r = tid >> 3, cb = 8 * (tid & 7), tq = t0 + r;
+        if (tq < a.T)
+            *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.out) +
+                                       (((int64_t)b * a.T + tq) * a.H + h) * 64 + cb) =
+                *reinterpret_cast<const uint4 *>(&sm.qh[r * LDB + cb]);
+    }
+    if (tid < CC && t0 + tid < a.T) {
+        const float dd = sm.dd[0][tid] + sm.dd[1][tid] + sm.dd[2][tid] + sm.dd[3][tid];
+        a.scores[((int64_t)b * a.T + t0 + tid) * a.H + h] =
+            sm.val[tid] != 0.f ? sqrtf(sm.kk[tid] * dd) : 0.f;
+    }
+}
+
+// ---- backward prep: N of the adjoint map dS0 = A_c^T dS_16 + N -----------------
+// N = Y - W'^T X with Y = Qhat^T dO, X = P^T dO + diag(c) delta, W' = T Ahat
+// (formed again with prep's operands), c_s = dscore_s |k_s| / |delta_s|.
+namespace {
+struct CwBPrepSmem {
+    float lam[CC * LDL], qf[CC * LDL], kf[CC * LDL];
+    uint16_t qh[RT32], qhl[RT32];  // Qhat rows hi/lo (rows 16..31 zero)
+    uint16_t ah[RT32], ahl[RT32];  // Ahat rows hi/lo (rows 16..31 zero)
+    uint16_t dor[RT32];   // dO rows (rows 16..31 zero)
+    uint16_t tb[RT16], tbl[RT16];  // T rows hi/lo (columns 16..31 zero)
+    uint16_t ptr[RT16], ptrl[RT16];  // P^T rows hi/lo ([s][t], columns 16..31 zero)
+    uint16_t wt[CT64], wtl[CT64];    // W'^T hi/lo
+    uint16_t xt[CT64], xtl[CT64];    // X^T hi/lo
+    float cs[CC];
+    int seg[CC];
+};
+}  // namespace
+
+__global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a) {
+    __shared__ CwBPrepSmem sm;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = tid >> 4, c0 = 4 * (tid & 15), tg = c * CC + t;
+    const bool inb = tg < a.T;
+    zero_lds(sm.qh + RT16, RT32 - RT16, tid);
+    zero_lds(sm.qhl + RT16, RT32 - RT16, tid);
+    zero_lds(sm.ah + RT16, RT32 - RT16, tid);
+    zero_lds(sm.ahl + RT16, RT32 - RT16, tid);
+    zero_lds(sm.dor + RT16, RT32 - RT16, tid);
+    for (int i = tid; i < CC * 16; i += NT4) {
+        const int r = i >> 4, cc = 16 + (i & 15);
+        sm.tb[r * LDB + cc] = 0;
+        sm.tbl[r * LDB + cc] = 0;
+        sm.ptr[r * LDB + cc] = 0;
+        sm.ptrl[r * LDB + cc] = 0;
+    }
+    for (int i = tid; i < 4 * 64 * 16; i += NT4) {
+        uint16_t *tl = (i >> 10) == 0 ? sm.wt : (i >> 10) == 1 ? sm.wtl : (i >> 10) == 2 ? sm.xt : sm.xtl;
+        tl[((i >> 4) & 63) * LDW + 16 + (i & 15)] = 0;
+    }
+    const CwGate *gb = a.ck_cwg + ci;
+    const float va = gb->val[t];
+    const int sg = gb->seg[t];
+    const bool on = va != 0.f;
+    float qv[4], kv[4], dov[4], er[4], L[4];
+    load4_bf16(a.q, a.qs, b, tg, h, c0, inb && on, qv);
+    load4_bf16(a.k, a.ks, b, tg, h, c0, inb && on, kv);
+    if (a.dout) load4_bf16(a.dout, a.ds, b, tg, h, c0, inb && on, dov);
+    else dov[0] = dov[1] = dov[2] = dov[3] = 0.f;
+    load4_f32(a.erase, b, tg, h, c0, inb && on, 0.f, er);
+    get4_f32(a.ck_lam + (int64_t)ci * CC * 64 + t * 64 + c0, L);
+    const float *dck = a.ck_delta + (int64_t)ci * CC * 64;
+    float dl4[4];
+    get4_f32(dck + t * 64 + c0, dl4);
+    load_t_split(a.ck_tf + (int64_t)ci * CC * CC, sm.tb, sm.tbl, tid);
+    {
+        float qh[4], ah[4], ksq = 0.f, dsq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float bt = sg == 0 ? __expf(L[e]) : 0.f;
+            qh[e] = bt * qv[e];
+            ah[e] = bt * er[e] * kv[e];
+            ksq += kv[e] * kv[e];
+            dsq += dl4[e] * dl4[e];
+        }
+        put4_f32(&sm.lam[t * LDL + c0], L);
+        put4_f32(&sm.qf[t * LDL + c0], qv);
+        put4_f32(&sm.kf[t * LDL + c0], kv);
+        put4_split(&sm.qh[t * LDB + c0], &sm.qhl[t * LDB + c0], qh);
+        put4_split(&sm.ah[t * LDB + c0], &sm.ahl[t * LDB + c0], ah);
+        put4_bf16(&sm.dor[t * LDB + c0], dov);
+        ksq = row16_sum(ksq);
+        dsq = row16_sum(dsq);
+        if ((tid & 15) == 0) {
+            const float dsc = (a.dscores && inb) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
+            const float nk = sqrtf(ksq), nd = sqrtf(dsq);
+            sm.cs[t] = (nk > 0.f && nd > 0.f) ? dsc * nk / nd : 0.f;
+            sm.seg[t] = sg;
+        }
+    }
+    __syncthreads();
+    // P (lower, same segment), stored transposed: ptr[s][t] = P[t][s].
+    for (int base = 0; base < 2 * 136; base += NT4) {
+        const int task = base + tid, p = task >> 1, half = task & 1;
+        int tt = 0, ss = 0;
+        if (p < 136) pair_of(p, false, tt, ss);
+        float acc = p < 136 ? pair_dot32(sm.qf, sm.kf, sm.lam, tt, ss, half) : 0.f;
+        acc += dpp<0xB1>(acc);
+        if (p < 136 && half == 0) {
+            uint16_t hi, lo;
+            split_bf16(sm.seg[tt] == sm.seg[ss] ? acc : 0.f, hi, lo);
+            sm.ptr[ss * LDB + tt] = hi;
+            sm.ptrl[ss * LDB + tt] = lo;
+        }
+    }
+    for (int i = tid; i < 120; i += NT4) {  // P^T is upper triangular: zero its strict lower part
+        int tt, ss;
+        pair_of(i, true, tt, ss);
+        sm.ptr[tt * LDB + ss] = 0;
+        sm.ptrl[tt * LDB + ss] = 0;
+    }
+    // Y = Qhat^T dO (row tile w of keys, all value tiles) and W' = T Ahat (tile w).
+    f32x4 y[4];
+    {
+        const bf16x8_t qa = frag_tr(sm.qh, 0, 16 * w);  // A[k][t] = Qhat[t][16 w + k]
+        const bf16x8_t qal = frag_tr(sm.qhl, 0, 16 * w);
+#pragma unroll
+        for (int tn = 0; tn < 4; ++tn) {
+            const bf16x8_t db = frag_tr(sm.dor, 0, 16 * tn);
+            y[tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa, db, zero4(), 0, 0, 0);
+            y[tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qal, db, y[tn], 0, 0, 0);
+        }
+        const bf16x8_t ta = frag(sm.tb, LDB, 0), tal = frag(sm.tbl, LDB, 0);
+        const bf16x8_t ab = frag_tr(sm.ah, 0, 16 * w);
+        f32x4 x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, ab, zero4(), 0, 0, 0);
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, frag_tr(sm.ahl, 0, 16 * w), x, 0, 0, 0);
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tal, ab, x, 0, 0, 0);
+        store_tile_t_split(&sm.wt[(16 * w) * LDW], &sm.wtl[(16 * w) * LDW], LDW, x);
+    }
+    __syncthreads();
+    // X = P^T dO + c delta (value tile w), stored transposed hi/lo.
+    {
+        const bf16x8_t db = frag_tr(sm.dor, 0, 16 * w);  // B[t][v] = dO[t][16 w + v]
+        f32x4 x = zero4();
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.ptr, LDB, 0), db, x, 0, 0, 0);
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.ptrl, LDB, 0), db, x, 0, 0, 0);
+        if (a.dscores) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                x[i] += sm.cs[acc_row(i)] * dck[acc_row(i) * 64 + 16 * w + acc_col()];
+        }
+        store_tile_t_split(&sm.xt[(16 * w) * LDW], &sm.xtl[(16 * w) * LDW], LDW, x);
+    }
+    __syncthreads();
+    // N = Y - W'^T X: key row tile w, value tiles 0..3; stored transposed (f32).
+    {
+        const bf16x8_t wa = frag(&sm.wt[(16 * w) * LDW], LDW, 0), wal = frag(&sm.wtl[(16 * w) * LDW], LDW, 0);
+        float *Nt = a.ws_n + (int64_t)ci * 64 * 64;
+#pragma unroll
+        for (int tn = 0; tn < 4; ++tn) {
+            const bf16x8_t xb = frag(&sm.xt[(16 * tn) * LDW], LDW, 0), xbl = frag(&sm.xtl[(16 * tn) * LDW], LDW, 0);
+            f32x4 x = zero4();
+            x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xb, x, 0, 0, 0);
+            x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xbl, x, 0, 0, 0);
+            x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wal, xb, x, 0, 0, 0);
+            *reinterpret_cast<float4 *>(&Nt[(16 * tn + acc_col()) * 64 + 16 * w + acc_row(0)]) =
+                make_float4(y[tn][0] - x[0], y[tn][1] - x[1], y[tn][2] - x[2], y[tn][3] - x[3]);
+        }
+    }
+}
+
+// ---- bgrad: every gradient of one chunk -----------------------------------------
+// Given S0, delta (forward checkpoint) and dS at the chunk end (adjoint scan):
+//   ddelta = P^T dO + Ktil dS + diag(c) delta;   dR = T^T ddelta
+//   dw = dR.v,  dv = dR.w;   dAhat = -dR S0^T;  dQhat = dO S0^T;  dKtil = delta dS^T
+//   dA = -strict_lower(dR delta^T),  dP = lower(dO delta^T)   (same segment)
+//   through the decays D_ts (elementwise, per channel i):
+//     eA_t = sum_s dA_ts D_ts k_s,  qP_t = sum_s dP_ts D_ts k_s,
+//     kAP_s = sum_t (dA_ts D_ts ehat_t + dP_ts D_ts q_t)
+//   dq = b dQhat + qP;  dehat = b dAhat + eA;  de = k dehat
+//   dk = lam dKtil + kAP + e dehat + c' k
+//   dLambda_t = ehat eA + q qP - k kAP + Ahat dAhat + Qhat dQhat - Ktil dKtil
+//               [t = 15: + sum_s Ktil dKtil + b_15 rowsum(S0 . dS)]
+//   dlog alpha_u = sum_{t >= u} dLambda_t,  dalpha = dlog alpha / alpha
+// (zero on padding and on valid reset tokens, where the reference's alpha' is
+// alpha (1 - reset) and carries no gradient).
+namespace {
+struct CwBGradSmem {
+    float lam[CC * LDL], qf[CC * LDL], kf[CC * LDL], ehf[CC * LDL], ef[CC * LDL];
+    float seA[CC * LDL], sqP[CC * LDL], skAP[CC * LDL];
+    float dRf[CC * LDL];   // dR (f32) for dw, dv; dLambda afterwards
+    uint16_t dor[RT32];    // dO rows (rows 16..31 zero)
+    uint16_t kl[RT16], kll[RT16];    // Ktil rows hi/lo
+    uint16_t st[64 * LDB], dst[64 * LDB];    // S0^T, dS^T rows [v][k] hi
+    uint16_t stl[64 * LDB], dstl[64 * LDB];  // lo parts
+    uint16_t tb[RT32], tbl[RT32];    // T rows hi/lo (rows and columns 16..31 zero)
+    uint16_t dh[RT16], dlo[RT16];    // delta rows hi/lo
+    uint16_t ptr[RT16], ptrl[RT16];  // P^T rows hi/lo; dq, dk rows (bf16) at the end
+    uint16_t ddt[CT64], ddtl[CT64];  // ddelta^T hi/lo
+    uint16_t drr[RT16], drrl[RT16];  // dR rows hi/lo
+    float dA[CC * LDI], dP[CC * LDI];
+    float cs[CC], ck[CC], val[CC];
+    int seg[CC];
+    float tail[64], fr[64], bc[64];
+};
+}  // namespace
+
+__global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
+    __shared__ CwBGradSmem sm;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = lane_id();
+    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = tid >> 4, c0 = 4 * (tid & 15), t0 = c * CC, tg = t0 + t;
+    const bool inb = tg < a.T;
+    zero_lds(sm.dor + RT16, RT32 - RT16, tid);
+    zero_lds(sm.tb + RT16, RT32 - RT16, tid);
+    zero_lds(sm.tbl + RT16, RT32 - RT16, tid);
+    for (int i = tid; i < CC * 16; i += NT4) {
+        const int r = i >> 4, cc = 16 + (i & 15);
+        sm.tb[r * LDB + cc] = 0;
+        sm.tbl[r * LDB + cc] = 0;
+        sm.ptr[r * LDB + cc] = 0;
+        sm.ptrl[r * LDB + cc] = 0;
+    }
+    for (int i = tid; i < 2 * 64 * 16; i += NT4)
+        ((i >> 10) == 0 ? sm.ddt : sm.ddtl)[((i >> 4) & 63) * LDW + 16 + (i & 15)] = 0;
+    const CwGate *gb = a.ck_cwg + ci;
+    const float va = gb->val[t];
+    const int sg = gb->seg[t], sg15 = gb->seg[CC - 1];
+    const bool on = va != 0.f;
+    float qv[4], kv[4], vv[4], dov[4], er[4], wr[4], L[4], dl4[4];
+    load4_bf16(a.q, a.qs, b, tg, h, c0, inb && on, qv);
+    load4_bf16(a.k, a.ks, b, tg, h, c0, inb && on, kv);
+    load4_bf16(a.v, a.vs, b, tg, h, c0, inb && on, vv);
+    if (a.dout) load4_bf16(a.dout, a.ds, b, tg, h, c0, inb && on, dov);
+    else dov[0] = dov[1] = dov[2] = dov[3] = 0.f;
+    load4_f32(a.erase, b, tg, h, c0, inb && on, 0.f, er);
+    load4_f32(a.write, b, tg, h, c0, inb && on, 0.f, wr);
+    const float *lck = a.ck_lam + (int64_t)ci * CC * 64;
+    get4_f32(lck + t * 64 + c0, L);
+    const float *dck = a.ck_delta + (int64_t)ci * CC * 64;
+    get4_f32(dck + t * 64 + c0, dl4);
+    {
+        const int64_t so = (int64_t)ci * 64 * 64;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int p = tid + NT4 * i, r = p >> 3, cb = 8 * (p & 7), o = r * 64 + cb;
+            *reinterpret_cast<uint4 *>(&sm.st[r * LDB + cb]) = *reinterpret_cast<const uint4 *>(a.ck_state + so + o);
+            *reinterpret_cast<uint4 *>(&sm.stl[r * LDB + cb]) = *reinterpret_cast<const uint4 *>(a.ck_state_lo + so + o);
+            *reinterpret_cast<uint4 *>(&sm.dst[r * LDB + cb]) = *reinterpret_cast<const uint4 *>(a.ws_dstate + so + o);
+            *reinterpret_cast<uint4 *>(&sm.dstl[r * LDB + cb]) = *reinterpret_cast<const uint4 *>(a.ws_dstate_lo + so + o);
+        }
+        load_t_split(a.ck_tf + (int64_t)ci * CC * CC, sm.tb, sm.tbl, tid);
+    }
+    {
+        float eh[4], klv[4], ksq = 0.f, dsq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float L15 = lck[(CC - 1) * 64 + c0 + e];
+            eh[e] = er[e] * kv[e];
+            klv[e] = (sg == sg15 ? __expf(L15 - L[e]) : 0.f) * kv[e];
+            ksq += kv[e] * kv[e];
+            dsq += dl4[e] * dl4[e];
+            if (t == CC - 1) sm.bc[c0 + e] = sg15 == 0 ? __expf(L15) : 0.f;
+        }
+        put4_f32(&sm.lam[t * LDL + c0], L);
+        put4_f32(&sm.qf[t * LDL + c0], qv);
+        put4_f32(&sm.kf[t * LDL + c0], kv);
+        put4_f32(&sm.ehf[t * LDL + c0], eh);
+        put4_f32(&sm.ef[t * LDL + c0], er);
+        put4_bf16(&sm.dor[t * LDB + c0], dov);
+        put4_split(&sm.kl[t * LDB + c0], &sm.kll[t * LDB + c0], klv);
+        put4_split(&sm.dh[t * LDB + c0], &sm.dlo[t * LDB + c0], dl4);
+        ksq = row16_sum(ksq);
+        dsq = row16_sum(dsq);
+        if ((tid & 15) == 0) {
+            const float dsc = (a.dscores && inb) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
+            const float nk = sqrtf(ksq), nd = sqrtf(dsq);
+            const bool ok = nk > 0.f && nd > 0.f;
+            sm.cs[t] = ok ? dsc * nk / nd : 0.f;
+            sm.ck[t] = ok ? dsc * nd / nk : 0.f;
+            sm.val[t] = va;
+            sm.seg[t] = sg;
+        }
+    }
+    __syncthreads();
+    // Phase 1: dQhat (key tile w), Ktil dS (value tile w), dKtil = delta dS^T (key
+    // tile w); P^T hi/lo (elementwise); rowsum(S0 . dS) per key channel.
+    f32x4 gqh = zero4(), kds = zero4(), gkt = zero4();
+#pragma unroll
+    for (int r = 0; r < 64; r += 32) {
+        const bf16x8_t sb = frag_tr(sm.st, r, 16 * w), db = frag_tr(sm.dst, r, 16 * w);
+        const bf16x8_t sbl = frag_tr(sm.stl, r, 16 * w), dbl = frag_tr(sm.dstl, r, 16 * w);
+        const bf16x8_t ob = frag(sm.dor, LDB, r);
+        gqh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ob, sb, gqh, 0, 0, 0);
+        gqh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ob, sbl, gqh, 0, 0, 0);
+        const bf16x8_t dsb = frag(&sm.dst[(16 * w) * LDB], LDB, r), kb = frag(sm.kl, LDB, r);
+        kds = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, dsb, kds, 0, 0, 0);
+        kds = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.kll, LDB, r), dsb, kds, 0, 0, 0);
+        kds = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, frag(&sm.dstl[(16 * w) * LDB], LDB, r), kds, 0, 0, 0);
+        const bf16x8_t hb = frag(sm.dh, LDB, r);
+        gkt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hb, db, gkt, 0, 0, 0);
+        gkt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.dlo, LDB, r), db, gkt, 0, 0, 0);
+        gkt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hb, dbl, gkt, 0, 0, 0);
+    }
+    for (int base = 0; base < 2 * 136; base += NT4) {
+        const int task = base + tid, p = task >> 1, half = task & 1;
+        int tt = 0, ss = 0;
+        if (p < 136) pair_of(p, false, tt, ss);
+        float acc = p < 136 ? pair_dot32(sm.qf, sm.kf, sm.lam, tt, ss, half) : 0.f;
+        acc += dpp<0xB1>(acc);
+        if (p < 136 && half == 0) {
+            uint16_t hi, lo;
+            split_bf16(sm.seg[tt] == sm.seg[ss] ? acc : 0.f, hi, lo);
+            sm.ptr[ss * LDB + tt] = hi;
+            sm.ptrl[ss * LDB + tt] = lo;
+        }
+    }
+    for (int i = tid; i < 120; i += NT4) {
+        int tt, ss;
+        pair_of(i, true, tt, ss);
+        sm.ptr[tt * LDB + ss] = 0;
+        sm.ptrl[tt * LDB + ss] = 0;
+    }
+    if (tid < 64) {  // rowsum_v S0[i][v] dS[i][v] for key channel i = tid
+        float f = 0.f;
+#pragma unroll 8
+        for (int v = 0; v < 64; ++v)
+            f += (bf16_val(sm.st[v * LDB + tid]) + bf16_val(sm.stl[v * LDB + tid])) *
+                 (bf16_val(sm.dst[v * LDB + tid]) + bf16_val(sm.dstl[v * LDB + tid]));
+        sm.fr[tid] = f;
+    }
+    {  // sum_s Ktil_s dKtil_s per key channel (f32 Ktil)
+        const int i = 16 * w + acc_col();
+        const float L15 = sm.lam[(CC - 1) * LDL + i];
+        f32x4 z;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int s = acc_row(e);
+            const float kt = sm.seg[s] == sm.seg[CC - 1] ? __expf(L15 - sm.lam[s * LDL + i]) * sm.kf[s * LDL + i] : 0.f;
+            z[e] = kt * gkt[e];
+        }
+        const float cz = col_reduce(z);
+        if ((l >> 4) == 0) sm.tail[i] = cz;
+    }
+    __syncthreads();
+    // Phase 2: ddelta = P^T dO + Ktil dS + c delta (value tile w) -> ddelta^T hi/lo.
+    {
+        const bf16x8_t db = frag_tr(sm.dor, 0, 16 * w);
+        f32x4 x = kds;
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.ptr, LDB, 0), db, x, 0, 0, 0);
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.ptrl, LDB, 0), db, x, 0, 0, 0);
+        if (a.dscores) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] += sm.cs[acc_row(e)] * dck[acc_row(e) * 64 + 16 * w + acc_col()];
+        }
+        store_tile_t_split(&sm.ddt[(16 * w) * LDW], &sm.ddtl[(16 * w) * LDW], LDW, x);
+    }
+    __syncthreads();
+    // Phase 3: dR = T^T ddelta (value tile w) -> dR rows (bf16) and f32.
+    {
+        const bf16x8_t ta = frag_tr(sm.tb, 0, 0), tal = frag_tr(sm.tbl, 0, 0);  // A[s][t] = T[t][s]
+        const bf16x8_t db = frag(&sm.ddt[(16 * w) * LDW], LDW, 0);
+        f32x4 x = zero4();
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, db, x, 0, 0, 0);
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, frag(&sm.ddtl[(16 * w) * LDW], LDW, 0), x, 0, 0, 0);
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tal, db, x, 0, 0, 0);
+        store_tile_rm_split(&sm.drr[16 * w], &sm.drrl[16 * w], LDB, x);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sm.dRf[acc_row(e) * LDL + 16 * w + acc_col()] = x[e];
+    }
+    __syncthreads();
+    // Phase 4: dAhat = -dR S0^T (key tile w); dA (wave 0) and dP (wave 1); dw, dv.
+    f32x4 gah = zero4();
+#pragma unroll
+    for (int r = 0; r < 64; r += 32) {
+        const bf16x8_t sb = frag_tr(sm.st, r, 16 * w), rb = frag(sm.drr, LDB, r);
+        gah = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rb, sb, gah, 0, 0, 0);
+        gah = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.drrl, LDB, r), sb, gah, 0, 0, 0);
+        gah = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rb, frag_tr(sm.stl, r, 16 * w), gah, 0, 0, 0);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) gah[e] = -gah[e];
+    if (w < 2) {
+        f32x4 x = zero4();
+        const uint16_t *lhs = w == 0 ? sm.drr : sm.dor;
+#pragma unroll
+        for (int r = 0; r < 64; r += 32) {
+            const bf16x8_t la = frag(lhs, LDB, r), dhb = frag(sm.dh, LDB, r);
+            x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(la, dhb, x, 0, 0, 0);
+            x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(la, frag(sm.dlo, LDB, r), x, 0, 0, 0);
+            if (w == 0) x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.drrl, LDB, r), dhb, x, 0, 0, 0);
+        }
+        const int ss = acc_col();
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int tt = acc_row(e);
+            const bool same = sm.seg[tt] == sm.seg[ss];
+            if (w == 0) sm.dA[tt * LDI + ss] = (ss < tt && same) ? -x[e] : 0.f;
+            else sm.dP[tt * LDI + ss] = (ss <= tt && same) ? x[e] : 0.f;
+        }
+    }
+    if (inb) {  // dw = dR.v, dv = dR.w (token t, channels c0 .. c0 + 3)
+        float dr[4], dw4[4], dv4[4];
+        get4_f32(&sm.dRf[t * LDL + c0], dr);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            dw4[e] = on ? dr[e] * vv[e] : 0.f;
+            dv4[e] = on ? dr[e] * wr[e] : 0.f;
+        }
+        const int64_t row = ((int64_t)b * a.T + tg) * a.H + h;
+        if (a.dwrite) put4_f32(a.dwrite + row * 64 + c0, dw4);
+        if (a.dv) put4_bf16(reinterpret_cast<uint16_t *>(a.dv) + row * 64 + c0, dv4);
+    }
+    __syncthreads();
+    // Phase 5: the decay-weighted sums, elementwise.  Thread (channel i = tid/4,
+    // part = tid%4) takes the rows t = part, part + 4, part + 8, part + 12 and every
+    // s <= t: eA_t, qP_t are its own; kAP_s is summed over the four parts (a DPP
+    // quad).
+    {
+        const int i = tid >> 2, part = tid & 3;
+        float eA[4] = {0.f, 0.f, 0.f, 0.f}, qP[4] = {0.f, 0.f, 0.f, 0.f};
+        float kAP[CC];
+#pragma unroll
+        for (int s = 0; s < CC; ++s) kAP[s] = 0.f;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int tt = part + 4 * m;
+            const float Lt = sm.lam[tt * LDL + i], et = sm.ehf[tt * LDL + i], qt = sm.qf[tt * LDL + i];
+#pragma unroll
+            for (int s = 0; s < CC; ++s) {
+                if (s > tt) continue;
+                const float D = s == tt ? 1.f : __expf(Lt - sm.lam[s * LDL + i]);
+                const float dA = sm.dA[tt * LDI + s], dP = sm.dP[tt * LDI + s];
+                const float ks = sm.kf[s * LDL + i] * D;
+                eA[m] += dA * ks;
+                qP[m] += dP * ks;
+                kAP[s] += (dA * et + dP * qt) * D;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < CC; ++s) {
+            float x = kAP[s];
+            x += dpp<0xB1>(x);
+            x += dpp<0x4E>(x);
+            kAP[s] = x;
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            sm.seA[(part + 4 * m) * LDL + i] = eA[m];
+            sm.sqP[(part + 4 * m) * LDL + i] = qP[m];
+        }
+        if (part == 0) {
+#pragma unroll
+            for (int s = 0; s < CC; ++s) sm.skAP[s * LDL + i] = kAP[s];
+        }
+    }
+    __syncthreads();
+    // Phase 6: assemble dq, dk, de and dLambda at key tile w (accumulator layout).
+    {
+        const int i = 16 * w + acc_col();
+        const float L15 = sm.lam[(CC - 1) * LDL + i];
+        f32x4 gq, gk;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int tt = acc_row(e);
+            const bool von = sm.val[tt] != 0.f;
+            const float Lt = sm.lam[tt * LDL + i];
+            const float bt = sm.seg[tt] == 0 ? __expf(Lt) : 0.f;
+            const float lt = sm.seg[tt] == sm.seg[CC - 1] ? __expf(L15 - Lt) : 0.f;
+            const float q = sm.qf[tt * LDL + i], k = sm.kf[tt * LDL + i];
+            const float eh = sm.ehf[tt * LDL + i], ee = sm.ef[tt * LDL + i];
+            const float eA = sm.seA[tt * LDL + i], qP = sm.sqP[tt * LDL + i], kAP = sm.skAP[tt * LDL + i];
+            const float dq = bt * gqh[e] + qP;
+            const float deh = bt * gah[e] + eA;
+            const float dk = lt * gkt[e] + kAP + ee * deh + sm.ck[tt] * k;
+            float dlam = eh * eA + q * qP - k * kAP + bt * eh * gah[e] + bt * q * gqh[e] - lt * k * gkt[e];
+            if (tt == CC - 1) dlam += sm.tail[i] + sm.bc[i] * sm.fr[i];
+            gq[e] = von ? dq : 0.f;
+            gk[e] = von ? dk : 0.f;
+            sm.dRf[tt * LDL + i] = dlam;  // dR is dead: dLambda takes its place
+            const int tq = t0 + tt;
+            if (a.derase && tq < a.T)
+                a.derase[(((int64_t)b * a.T + tq) * a.H + h) * 64 + i] = von ? k * deh : 0.f;
+        }
+        store_tile_rm(&sm.ptr[16 * w], LDB, gq);   // dq rows over P^T (dead)
+        store_tile_rm(&sm.ptrl[16 * w], LDB, gk);  // dk rows
+    }
+    __syncthreads();
+    if (tid < CC * 8) {  // dq, dk rows: 16-byte pieces
+        const int r = tid >> 3, cb = 8 * (tid & 7), tq = t0 + r;
+        if (tq < a.T) {
+            const int64_t o = (((int64_t)b * a.T + tq) * a.H + h) * 64 + cb;
+            if (a.dq) *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.dq) + o) =
+                *reinterpret_cast<const uint4 *>(&sm.ptr[r * LDB + cb]);
+            if (a.dk) *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.dk) + o) =
+                *reinterpret_cast<const uint4 *>(&sm.ptrl[r * LDB + cb]);
+        }
+    } else if (tid >= 192 && a.dalpha) {  // dalpha: reverse running sums of dLambda, channel i
+        // A token's log alpha reaches only the Lambda of later tokens in its own
+        // segment (differences across a reset vanish), so the sum restarts at
+        // every reset; the reset token's own alpha carries no gradient.
+        const int i = tid - 192;
+        float acc = 0.f;
+        for (int tt = CC - 1; tt >= 0; --tt) {
+            acc += sm.dRf[tt * LDL + i];
+            const int tq = t0 + tt;
+            const bool von = sm.val[tt] != 0.f;
+            const bool rs = von && (tt == 0 ? sm.seg[0] == 1 : sm.seg[tt] != sm.seg[tt - 1]);
+            if (tq < a.T) {
+                const float al = von ? ld4<float>(a.alpha, b, tq, h, i) : 1.f;
+                const bool live = von && !rs && __logf(al) > LOG_FLOOR;
+                a.dalpha[(((int64_t)b * a.T + tq) * a.H + h) * 64 + i] = live ? acc / al : 0.f;
+            }
+            if (rs) acc = 0.f;
+        }
+    }
+}
+
+static inline void cmark(const hipEvent_t *ev, int i, hipStream_t stream) {
+    if (ev) (void)hipEventRecord(ev[i], stream);
+}
+
+hipError_t launch_cw_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
+    const int nch = a.B * a.H * a.nc;
+    cmark(ev, 0, stream);
+    hipLaunchKernelGGL(cw_prep_kernel, dim3(nch), dim3(NT4), 0, stream, a);
+    cmark(ev, 1, stream);
+    cmark(ev, 2, stream);
+    (void)launch_chunk_affine_scan(a, false, stream);
+    cmark(ev, 3, stream);
+    cmark(ev, 4, stream);
+    hipLaunchKernelGGL(cw_out_kernel, dim3(nch), dim3(NT4), 0, stream, a);
+    cmark(ev, 5, stream);
+    return hipGetLastError();
+}
+
+hipError_t launch_cw_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
+    const int nch = a.B * a.H * a.nc;
+    cmark(ev, 0, stream);
+    hipLaunchKernelGGL(cw_bprep_kernel, dim3(nch), dim3(NT4), 0, stream, a);
+    cmark(ev, 1, stream);
+    cmark(ev, 2, stream);
+    (void)launch_chunk_affine_scan(a, true, stream);
+    cmark(ev, 3, stream);
+    cmark(ev, 4, stream);
+    hipLaunchKernelGGL(cw_bgrad_kernel, dim3(nch), dim3(NT4), 0, stream, a);
+    cmark(ev, 5, stream);
+    return hipGetLastError();
+}
+
+}  // namespace gdn2

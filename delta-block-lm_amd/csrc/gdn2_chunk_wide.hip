@@ -86,16 +86,6 @@ __device__ __forceinline__ float sq8(uint4 v) {
     return s;
 }
 
-// A [64 x KD] bf16 matrix stored densely per chunk (row stride KD) into a
-// [64 x LDK] LDS tile: two 16-byte pieces per thread.
-__device__ __forceinline__ void stage_mat(uint16_t *tile, const uint16_t *src, int tid) {
-#pragma unroll
-    for (int i = 0; i < NKB; ++i) {
-        const int p = tid + NT * i, r = p / (KD / 8), c0 = 8 * (p % (KD / 8));
-        *reinterpret_cast<uint4 *>(&tile[r * LDK + c0]) =
-            *reinterpret_cast<const uint4 *>(src + r * KD + c0);
-    }
-}
 struct Mat2 {
     uint4 p[NKB];
 };

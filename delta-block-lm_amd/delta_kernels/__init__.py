@@ -150,8 +150,12 @@ def gdn_training_backward(q, k, v, alpha, erase, write, valid, reset, checkpoint
     dinit = torch.empty((B, H, K, V), dtype=torch.float32, device=dev)
     nws = L.gdn2_training_workspace_bytes(ctypes.byref(shape), chunk)
     ws = torch.empty((nws,), dtype=torch.uint8, device=dev)
-    if d_output is not None and d_output.dtype != q.dtype:
-        d_output = d_output.to(q.dtype)
+    if d_output is not None:
+        if d_output.dtype != q.dtype:
+            d_output = d_output.to(q.dtype)
+        if not _rows_aligned(d_output):
+            # The chunk kernels read 16-byte row pieces of the upstream gradient.
+            d_output = d_output.contiguous()
     dfin = None if d_final_state is None else d_final_state.to(torch.float32).contiguous()
     dsc = None if d_scores is None else d_scores.to(torch.float32).contiguous()
     views = [_view(x) for x in (q, k, v, alpha, erase, write, valid, reset)]

@@ -29,7 +29,7 @@ def problem(seed, B, T, H, masks=True, initial=True, K=64, V=64, reset_every=0):
         p["valid"][0, 5] = 0
         p["valid"][0, min(70, T - 2):min(75, T - 1)] = 0
         p["valid"][-1, T - 9:] = 0
-        p["reset"][0, 40] = 1
+        p["reset"][0, 40 if T > 40 else T // 2] = 1
         p["reset"][0, min(72, T - 2)] = 1  # reset on padding: ignored
         if T > 130:
             p["reset"][-1, 129] = 1
@@ -65,3 +65,25 @@ def run_bwd(dk, p, chunk=64, use_final=True, use_scores=True):
                                   dev(p["dO"], torch.bfloat16),
                                   dev(p["dF"]) if use_final else None,
                                   dev(p["dS"]) if use_scores else None)
+
+
+def cw_problem(seed, B, T, H, masks=True, initial=True, alpha_lo=0.5, reset_every=0, D=64):
+    """A channel-wise gate problem: bf16-rounded q/k/v/dO (q, k unit rows),
+    f32 per-channel gates alpha in (alpha_lo, 1), erase in (0, 1), write in
+    (-0.5, 1), with the masks of problem()."""
+    p = problem(seed, B, T, H, masks=masks, initial=initial, K=D, V=D, reset_every=reset_every)
+    rng = np.random.default_rng(seed + 7919)
+    p["alpha"] = rng.uniform(alpha_lo, 1.0, size=(B, T, H, D)).astype(np.float32)
+    p["erase"] = rng.uniform(0.0, 1.0, size=(B, T, H, D)).astype(np.float32)
+    p["write"] = rng.uniform(-0.5, 1.0, size=(B, T, H, D)).astype(np.float32)
+    return p
+
+
+def cw_oracle(p, use_final=True, use_scores=True):
+    """f64 forward outputs and gradients of a cw_problem."""
+    out, fin, sc = oracle.scan(p["q"], p["k"], p["v"], p["alpha"], p["erase"], p["write"],
+                               p["valid"], p["reset"], p["initial"])
+    g = oracle.backward(p["q"], p["k"], p["v"], p["alpha"], p["erase"], p["write"], p["valid"],
+                        p["reset"], p["initial"], p["dO"], p["dF"] if use_final else None,
+                        p["dS"] if use_scores else None)
+    return (out, fin, sc), g

@@ -1,0 +1,211 @@
+"""GPU parity of the channel-wise chunk-WY MFMA path (the training op
+gdn_training_scan with bf16 q/k/v and d_k = d_v = 64; csrc/gdn2_chunk_cw.hip)
+against the f64 oracle: per-channel gates, masks, resets (on valid and on
+padded tokens, at chunk starts), an initial state, every adjoint (output,
+final state, scores), ragged lengths, several heads, sequences past 16 chunks
+(the scan's rolled loop), broadcast gate views and strong decays.  The stage
+timers show that the chunk kernels, not the token-sequential kernels,
+produced each result."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from chunk_util import cw_oracle, cw_problem  # noqa: E402
+from gpu_util import TOL_BF16, dev, gate  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+FWD_STAGES = {"chunk_prep", "state_scan", "chunk_out"}
+BWD_STAGES = {"chunk_bprep", "adjoint_scan", "chunk_bgrad"}
+GATES = ("alpha", "erase", "write")
+
+
+@pytest.fixture(scope="module")
+def dk():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import delta_kernels
+    delta_kernels.lib()
+    return delta_kernels
+
+
+def _inputs(p, grad=True):
+    x = {n: dev(p[n], torch.bfloat16) for n in ("q", "k", "v")}
+    x.update({n: dev(p[n]) for n in GATES})
+    if grad:
+        for t in x.values():
+            t.requires_grad_(True)
+    init = dev(p["initial"])
+    if init is not None and grad:
+        init.requires_grad_(True)
+    return x, init
+
+
+def _run(dk, p, use_final=True, use_scores=True, chunk=16, gates=None):
+    """Forward and backward through delta_kernels.gdn_training_scan with the
+    stage timers on; returns (outputs, grads, stages that ran)."""
+    x, init = _inputs(p)
+    g = gates(x) if gates else [x[n] for n in GATES]
+    dk.stage_timing(True)
+    try:
+        r = dk.gdn_training_scan(x["q"], x["k"], x["v"], *g, dev(p["valid"]), dev(p["reset"]),
+                                 init, chunk)
+        loss = (r.output.float() * dev(p["dO"])).sum()
+        if use_final:
+            loss = loss + (r.final_state * dev(p["dF"])).sum()
+        if use_scores:
+            loss = loss + (r.scores[..., 0] * dev(p["dS"])).sum()
+        loss.backward()
+        torch.cuda.synchronize()
+        ran = set(dk.stage_times())
+    finally:
+        dk.stage_timing(False)
+    grads = {n: x[n].grad for n in x}
+    if init is not None:
+        grads["initial"] = init.grad
+    return r, grads, ran
+
+
+def _check(p, r, grads, use_final=True, use_scores=True, skip=()):
+    (o_out, o_fin, o_sc), og = cw_oracle(p, use_final, use_scores)
+    pad = (p["valid"] == 0)[:, :, None]
+    gate("output", r.output, o_out, TOL_BF16, exact_zero=pad[..., None])
+    gate("final_state", r.final_state, o_fin, TOL_BF16)
+    gate("scores", r.scores[..., 0], o_sc, TOL_BF16, exact_zero=pad)
+    for n in ("q", "k", "v") + GATES:
+        if n not in skip:
+            gate(f"d{n}", grads[n], og[n], TOL_BF16, exact_zero=pad[..., None])
+    if "initial" in grads:
+        gate("d_initial", grads["initial"], og["initial"], TOL_BF16)
+    return og
+
+
+@pytest.mark.parametrize("B,T,H", [(1, 16, 1), (2, 37, 2), (1, 200, 3), (2, 64, 1)])
+@pytest.mark.parametrize("masks", [False, True])
+def test_cw_matches_oracle(dk, B, T, H, masks):
+    p = cw_problem(B * 100 + T + masks, B, T, H, masks=masks)
+    print(f"cw: B={B} T={T} H={H} masks={masks}", flush=True)
+    r, grads, ran = _run(dk, p)
+    assert FWD_STAGES | BWD_STAGES <= ran, sorted(ran)
+    _check(p, r, grads)
+
+
+def test_cw_output_adjoint_only_no_initial(dk):
+    p = cw_problem(3, 2, 150, 2, masks=True, initial=False)
+    r, grads, ran = _run(dk, p, use_final=False, use_scores=False)
+    assert BWD_STAGES <= ran
+    _check(p, r, grads, use_final=False, use_scores=False)
+
+
+def test_cw_resets_at_chunk_edges(dk):
+    """Resets on the first token of a chunk, on token 0, on the last token of a
+    chunk and on a padded token; a chunk that is all padding."""
+    p = cw_problem(17, 2, 96, 1, masks=False)
+    p["reset"][0, [0, 16, 31, 47]] = 1
+    p["valid"][0, 64:80] = 0
+    p["reset"][0, 70] = 1  # on padding: ignored
+    p["reset"][1, [15, 17, 33]] = 1
+    r, grads, ran = _run(dk, p)
+    assert FWD_STAGES | BWD_STAGES <= ran
+    _check(p, r, grads)
+
+
+@pytest.mark.parametrize("T,reset_every", [(256, 0), (1000, 300), (2048, 700)])
+def test_cw_long(dk, T, reset_every):
+    """16, 63 and 128 chunks of 16 tokens: the scan's straight-line form and
+    its rolled loop, with bf16 chunk maps chained over the whole sequence."""
+    p = cw_problem(T, 1, T, 2, masks=True, reset_every=reset_every)
+    print(f"cw long: T={T} chunks={-(-T // 16)}", flush=True)
+    r, grads, ran = _run(dk, p)
+    assert FWD_STAGES | BWD_STAGES <= ran
+    _check(p, r, grads)
+
+
+def test_cw_strong_decay(dk):
+    """alpha down to 1e-3: the decays underflow the chunk within a few tokens.
+    The alpha gradient is gated in the log domain (alpha * dalpha), the
+    quantity the kernels form before the division by alpha."""
+    p = cw_problem(29, 1, 80, 2, masks=True, alpha_lo=1e-3)
+    r, grads, ran = _run(dk, p)
+    og = _check(p, r, grads, skip=("alpha",))
+    pad = (p["valid"] == 0)[:, :, None, None]
+    gate("alpha * dalpha", grads["alpha"].double().cpu().numpy() * p["alpha"],
+         og["alpha"] * p["alpha"], TOL_BF16, exact_zero=np.broadcast_to(pad, p["alpha"].shape))
+
+
+def test_cw_broadcast_gates(dk):
+    """Gates handed over as stride-0 views: alpha and erase shared by the
+    channels of a head ([B,T,H,1] expanded), write shared by the heads."""
+    B, T, H = 1, 70, 2
+    p = cw_problem(41, B, T, H, masks=True)
+    p["alpha"] = np.broadcast_to(p["alpha"][..., :1], p["alpha"].shape).copy()
+    p["erase"] = np.broadcast_to(p["erase"][..., :1], p["erase"].shape).copy()
+    p["write"] = np.broadcast_to(p["write"][:, :, :1], p["write"].shape).copy()
+
+    def views(x):
+        return [x["alpha"][..., :1].expand(B, T, H, 64), x["erase"][..., :1].expand(B, T, H, 64),
+                x["write"][:, :, :1].expand(B, T, H, 64)]
+    r, grads, ran = _run(dk, p, gates=views)
+    assert FWD_STAGES | BWD_STAGES <= ran
+    (o_out, o_fin, o_sc), og = cw_oracle(p)
+    gate("output", r.output, o_out, TOL_BF16)
+    gate("final_state", r.final_state, o_fin, TOL_BF16)
+    # the leaf gradients are the sums over the broadcast axes
+    gate("dalpha (summed)", grads["alpha"][..., :1], og["alpha"].sum(-1, keepdims=True), TOL_BF16)
+    gate("derase (summed)", grads["erase"][..., :1], og["erase"].sum(-1, keepdims=True), TOL_BF16)
+    gate("dwrite (summed)", grads["write"][:, :, :1], og["write"].sum(2, keepdims=True), TOL_BF16)
+    for n in ("q", "k", "v"):
+        gate(f"d{n}", grads[n], og[n], TOL_BF16)
+
+
+def test_cw_split_continuation(dk):
+    """T = 96 scanned whole equals [0, 40) then [40, 96) from the carried state
+    (a split inside a 16-token chunk); the two halves' backward, chained through
+    the state adjoint, equals the whole sequence's backward."""
+    T, cut = 96, 40
+    p = cw_problem(53, 2, T, 2, masks=True)
+    r, grads, _ = _run(dk, p)
+    seq = ("q", "k", "v", "alpha", "erase", "write", "valid", "reset", "dO", "dS")
+    first = {n: (p[n][:, :cut] if n in seq else p[n]) for n in p}
+    second = {n: (p[n][:, cut:] if n in seq else p[n]) for n in p}
+    x1, i1 = _inputs(first, grad=False)
+    x2, _ = _inputs(second, grad=False)
+    f = dk._training_forward(x1["q"], x1["k"], x1["v"], x1["alpha"], x1["erase"], x1["write"],
+                             dev(first["valid"]), dev(first["reset"]), i1, 16)
+    s = dk._training_forward(x2["q"], x2["k"], x2["v"], x2["alpha"], x2["erase"], x2["write"],
+                             dev(second["valid"]), dev(second["reset"]), f[1], 16)
+    gate("output (split)", torch.cat([f[0], s[0]], 1), r.output.detach().float().cpu().numpy(),
+         TOL_BF16)
+    gate("final_state (split)", s[1], r.final_state.detach().cpu().numpy(), TOL_BF16)
+    g2 = dk.gdn_training_backward(x2["q"], x2["k"], x2["v"], x2["alpha"], x2["erase"],
+                                  x2["write"], dev(second["valid"]), dev(second["reset"]), s[3],
+                                  16, dev(second["dO"], torch.bfloat16), dev(p["dF"]),
+                                  dev(second["dS"]))
+    g1 = dk.gdn_training_backward(x1["q"], x1["k"], x1["v"], x1["alpha"], x1["erase"],
+                                  x1["write"], dev(first["valid"]), dev(first["reset"]), f[3],
+                                  16, dev(first["dO"], torch.bfloat16), g2[6], dev(first["dS"]))
+    for i, n in enumerate(("q", "k", "v") + GATES):
+        gate(f"d{n} (split)", torch.cat([g1[i], g2[i]], 1), grads[n].float().cpu().numpy(),
+             TOL_BF16)
+    gate("d_initial (split)", g1[6], grads["initial"].cpu().numpy(), TOL_BF16)
+
+
+def test_scan_selected_reaches_mfma(dk):
+    """The reference's mixer entry (scan_selected with the fused GDN-2
+    backend) runs the chunk kernels for bf16 d = 64 inputs."""
+    from delta_mixers import MixerKind, ScanBackend, ScanInput, scan_selected
+    p = cw_problem(61, 1, 48, 2, masks=True)
+    x, init = _inputs(p, grad=False)
+    dk.stage_timing(True)
+    try:
+        r = scan_selected(ScanBackend.FUSED_GDN2, MixerKind.GDN2,
+                          ScanInput(*(x[n] for n in ("q", "k", "v") + GATES)), dev(p["valid"]),
+                          dev(p["reset"]), 16, init)
+        torch.cuda.synchronize()
+        ran = set(dk.stage_times())
+    finally:
+        dk.stage_timing(False)
+    assert FWD_STAGES <= ran, sorted(ran)
+    (o_out, _, _), _ = cw_oracle(p)
+    gate("scan_selected output", r.output, o_out, TOL_BF16)
