@@ -380,12 +380,12 @@ int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gdn2_view *
 
 size_t gdn2_scan_checkpoint_bytes(const gdn2_shape *shape) {
     if (check_shape(shape)) return 0;
-    return seq_checkpoint_bytes(shape);
+    return training_checkpoint_bytes(shape);
 }
 
 size_t gdn2_scan_workspace_bytes(const gdn2_shape *shape) {
     if (check_shape(shape)) return 0;
-    return seq_workspace_bytes(shape);
+    return training_workspace_bytes(shape);
 }
 
 int gdn2_scan(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k, const gdn2_view *v,
@@ -397,9 +397,20 @@ int gdn2_scan(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k, c
     GDN2_TRY(check_out_dtype(output_dtype));
     if (!output) return fail(GDN2_ERR_ARGUMENT, "output is null");
     if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
-    if (checkpoint_bytes < seq_checkpoint_bytes(shape))
+    if (checkpoint_bytes < training_checkpoint_bytes(shape))
         return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
-                    seq_checkpoint_bytes(shape), checkpoint_bytes);
+                    training_checkpoint_bytes(shape), checkpoint_bytes);
+    if (use_cw_path(shape, q, k, v)) {
+        ChunkArgs c = cw_args(shape, q, k, v, alpha, erase, write, nullptr, nullptr);
+        c.doc = 1;
+        c.doc_start = make_view(doc_start);
+        c.doc_end = make_view(doc_end);
+        c.out = output;
+        c.out_bf16 = output_dtype == GDN2_BF16;
+        cw_bind_checkpoint(c, checkpoint);
+        const hipEvent_t *ev = stage_events(0, (hipStream_t)stream);
+        return launch_status(launch_cw_fwd(c, (hipStream_t)stream, ev), "gdn2_scan");
+    }
     SeqArgs a = seq_args(shape, q, k, v, alpha, erase, write, nullptr, nullptr);
     a.doc = 1;
     a.doc_start = make_view(doc_start);
@@ -421,13 +432,37 @@ int gdn2_backward(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *
     GDN2_TRY(check_doc_inputs(q, k, v, alpha, erase, write, doc_start, doc_end));
     if (d_output) GDN2_TRY(check_view(d_output, "d_output", q->dtype, true));
     if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
-    if (checkpoint_bytes < seq_checkpoint_bytes(shape))
+    if (checkpoint_bytes < training_checkpoint_bytes(shape))
         return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
-                    seq_checkpoint_bytes(shape), checkpoint_bytes);
+                    training_checkpoint_bytes(shape), checkpoint_bytes);
     if (!workspace) return fail(GDN2_ERR_ARGUMENT, "workspace is null");
-    if (workspace_bytes < seq_workspace_bytes(shape))
+    if (workspace_bytes < training_workspace_bytes(shape))
         return fail(GDN2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
-                    seq_workspace_bytes(shape), workspace_bytes);
+                    training_workspace_bytes(shape), workspace_bytes);
+    if (use_cw_path(shape, q, k, v)) {
+        if (d_output && d_output->data && !rows_aligned(d_output))
+            return fail(GDN2_ERR_ARGUMENT,
+                        "d_output needs unit channel stride and 16-byte aligned rows on the "
+                        "chunked path (bf16, d_k = d_v = 64)");
+        ChunkArgs c = cw_args(shape, q, k, v, alpha, erase, write, nullptr, nullptr);
+        c.doc = 1;
+        c.doc_start = make_view(doc_start);
+        c.doc_end = make_view(doc_end);
+        cw_bind_checkpoint(c, const_cast<void *>(checkpoint));
+        cw_bind_workspace(c, workspace);
+        if (d_output && d_output->data) {
+            c.dout = (const uint16_t *)d_output->data;
+            for (int d = 0; d < 3; ++d) c.ds[d] = d_output->stride[d];
+        }
+        c.dq = dq;
+        c.dk = dk;
+        c.dv = dv;
+        c.dalpha = dalpha;
+        c.derase = derase;
+        c.dwrite = dwrite;
+        const hipEvent_t *ev = stage_events(3, (hipStream_t)stream);
+        return launch_status(launch_cw_bwd(c, (hipStream_t)stream, ev), "gdn2_backward");
+    }
     SeqArgs a = seq_args(shape, q, k, v, alpha, erase, write, nullptr, nullptr);
     a.doc = 1;
     a.doc_start = make_view(doc_start);

@@ -80,6 +80,10 @@ struct ChunkArgs {
     // Lo parts (x - bf16(x)) of the chunk-start states and the chunk-end state
     // adjoints, kept by the scan when non-null.
     uint16_t *ck_state_lo, *ws_dstate_lo;
+    // Document limits (int32 [B,T] views, inclusive) in place of valid/reset:
+    // a token is live when end >= start and resets the state when start == t.
+    int doc;
+    View doc_start, doc_end;
     float *dalpha, *derase, *dwrite;
 };
 

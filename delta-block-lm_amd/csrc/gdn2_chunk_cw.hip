@@ -23,6 +23,11 @@
 // to 32 by zero rows or columns.  The chunk maps feed the scalar path's affine
 // scan (gdn2_chunk.hip) over the T / 16 chunks.
 //
+// With document limits (the doc-limit op) a token is live when end >= start and
+// resets the state when start == t; the backward is the exact VJP of that
+// forward, whose adjoint never crosses a reset, as the reference's chunked
+// kernels compute it (crates/kernels/src/gdn2.rs:24-65, :288-490).
+//
 // log alpha is floored at -80 (exp(-80) ~ 2e-35): below that the decay is
 // taken as exp(-80) and the alpha gradient is zero.  The alpha gradient is the
 // log-domain adjoint divided by alpha, so its absolute error grows as 1/alpha.
@@ -189,8 +194,16 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a) {
     for (int i = tid; i < 4 * 64 * 16; i += NT4)
         sm.wt[i >> 10][((i >> 4) & 63) * LDW + 16 + (i & 15)] = 0;
     // Loads: token t, channels c0 .. c0 + 3.
-    const float vld = inb ? ld4<float>(a.valid, b, tg, 0, 0) : 0.f;
-    const float rst = inb ? ld4<float>(a.reset, b, tg, 0, 0) : 0.f;
+    float vld = 0.f, rst = 0.f;
+    if (inb && a.doc) {
+        const int32_t st = reinterpret_cast<const int32_t *>(a.doc_start.data)[b * a.doc_start.s0 + tg * a.doc_start.s1];
+        const int32_t en = reinterpret_cast<const int32_t *>(a.doc_end.data)[b * a.doc_end.s0 + tg * a.doc_end.s1];
+        vld = en >= st ? 1.f : 0.f;
+        rst = st == tg ? 1.f : 0.f;
+    } else if (inb) {
+        vld = ld4<float>(a.valid, b, tg, 0, 0);
+        rst = ld4<float>(a.reset, b, tg, 0, 0);
+    }
     const bool on = vld != 0.f;
     float kv[4], vv[4], al[4], er[4], wr[4];
     load4_bf16(a.k, a.ks, b, tg, h, c0, inb && on, kv);
@@ -511,7 +524,7 @@ __global__ void __launch_bounds__(NT4) cw_out_kernel(ChunkArgs a) {
                                        (((int64_t)b * a.T + tq) * a.H + h) * 64 + cb) =
                 *reinterpret_cast<const uint4 *>(&sm.qh[r * LDB + cb]);
     }
-    if (tid < CC && t0 + tid < a.T) {
+    if (a.scores && tid < CC && t0 + tid < a.T) {
         const float dd = sm.dd[0][tid] + sm.dd[1][tid] + sm.dd[2][tid] + sm.dd[3][tid];
         a.scores[((int64_t)b * a.T + t0 + tid) * a.H + h] =
             sm.val[tid] != 0.f ? sqrtf(sm.kk[tid] * dd) : 0.f;

@@ -11,9 +11,8 @@ struct SeqArgs {
     int B, T, H, K, V;
     View q, k, v, alpha, erase, write, valid, reset, initial;
     // Document limits (int32 [batch, time] views, inclusive; end < start marks
-    // padding).  When set they replace valid/reset, and the backward follows
-    // the reference's doc-limit VJP: the adjoint is cleared at tokens with
-    // end == t and passes through resets.
+    // padding, start == t resets the state).  When set they replace
+    // valid/reset; the backward is the exact VJP, as with masks.
     int doc;
     View doc_start, doc_end;
     // Scalar-gate mode: alpha[i] = exp(g), erase[i] = write[j] = beta, with

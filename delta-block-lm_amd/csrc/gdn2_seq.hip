@@ -2,7 +2,11 @@
 //
 // Semantics follow crates/mixers/src/reference.rs:41-257 (forward and VJP),
 // the stateful fused kernels crates/kernels/src/gdn_training.rs:12-284 and,
-// with document limits, crates/mixers/src/gdn2_reference.rs:84-226.
+// with document limits, the forward of crates/mixers/src/gdn2_reference.rs:51-103
+// (a token is live when end >= start and resets the state when start == t)
+// with the exact VJP of that forward, as the reference's chunked kernels
+// compute it (crates/kernels/src/gdn2.rs:24-65, :288-490): the adjoint never
+// crosses a reset.
 //
 // One workgroup per (batch, head).  Value columns evolve independently in the
 // recurrence, so each wave owns a block of value columns and walks the tokens
@@ -283,17 +287,16 @@ __device__ __forceinline__ void load_tokens(const TokenSrc &src, const BlockCtx 
     }
 }
 
-// Token flags (valid, reset, adjoint clear) from a thread's per-token words.
+// Token flags (valid, reset) from a thread's per-token words.
 template <int KP, int VP, int NT, bool BWD>
 __device__ __forceinline__ void token_flags(const SeqArgs &a, const TokenRegs<KP, VP, NT, BWD> &r,
-                                            int t, float &val, float &rst, float &clr) {
-    val = rst = clr = 0.f;
+                                            int t, float &val, float &rst) {
+    val = rst = 0.f;
     if (!r.in) return;
     if (a.doc) {
         const int32_t st = (int32_t)r.f0, en = (int32_t)r.f1;
         val = en >= st ? 1.f : 0.f;
         rst = st == t ? 1.f : 0.f;
-        clr = en == t ? 1.f : 0.f;
     } else {
         val = __uint_as_float(r.f0);
         rst = __uint_as_float(r.f1);
@@ -344,8 +347,8 @@ __device__ __forceinline__ void store_fwd_flags(const SeqArgs &a,
                                                 const TokenRegs<KP, VP, NT, false> &r,
                                                 FwdTokens<KP, VP> &s, int t0, int tid) {
     if (tid < SEQ_CT) {
-        float val, rst, clr;
-        token_flags(a, r, t0 + tid, val, rst, clr);
+        float val, rst;
+        token_flags(a, r, t0 + tid, val, rst);
         s.val[tid] = val;
         s.rst[tid] = rst;
     }
@@ -561,7 +564,7 @@ struct alignas(16) SeqBwdSmem {
     float q[SEQ_CT][KP], k[SEQ_CT][KP], a[SEQ_CT][KP], e[SEQ_CT][KP];
     float v[SEQ_CT][VP], w[SEQ_CT][VP], dy[SEQ_CT][VP], d[SEQ_CT][VP];
     float dd[SEQ_CT][VP];  // edit adjoint of every token (zero on padding)
-    float val[SEQ_CT], rst[SEQ_CT], clr[SEQ_CT], cs[SEQ_CT], ks[SEQ_CT];
+    float val[SEQ_CT], rst[SEQ_CT], cs[SEQ_CT], ks[SEQ_CT];
     // red[slot][wave][quantity][key]: per-wave sums over the wave's value
     // columns of the q-gradient, adj.delta, bar.ddelta and dalpha terms.
     float red[Cfg::FT][Cfg::NW][4][Cfg::RP];
@@ -571,18 +574,16 @@ struct alignas(16) SeqBwdSmem {
 // per-token flags and score-VJP coefficients, then the operands.  Padded
 // tokens get a = 1 and zero q, k, e, dy (their delta is zero): the adjoint
 // passes unchanged and every gradient but dalpha comes out zero (the flush
-// zeroes dalpha).  With masks, a reset token gets a = 0, which cuts the
-// adjoint; with document limits its own a stays (the adjoint crosses resets).
+// zeroes dalpha).  A reset token gets a = 0, which cuts the adjoint.
 template <int KP, int VP, int NT, typename TIN>
 __device__ __forceinline__ void store_bwd_flags(const SeqArgs &a,
                                                 const TokenRegs<KP, VP, NT, true> &r,
                                                 SeqBwdSmem<KP, VP> &s, int t0, int tid) {
     if (tid < SEQ_CT) {
-        float val, rst, clr;
-        token_flags(a, r, t0 + tid, val, rst, clr);
+        float val, rst;
+        token_flags(a, r, t0 + tid, val, rst);
         s.val[tid] = val;
         s.rst[tid] = rst;
-        s.clr[tid] = clr;
         // Score VJP (zero subgradient at |k| |delta| = 0): ddelta += cs delta,
         // dk += ks k.
         const float sa = __uint_as_float(r.sa), nk = __uint_as_float(r.nk), nd = __uint_as_float(r.nd);
@@ -600,7 +601,7 @@ __device__ __forceinline__ void store_bwd_data(const SeqArgs &a,
 #pragma unroll
     for (int n = 0; n < R::NK; ++n) {
         const int idx = tid + n * NT, tt = idx / KP, c = idx % KP;
-        const bool on = s.val[tt] != 0.f, cut = s.rst[tt] != 0.f && !a.doc;
+        const bool on = s.val[tt] != 0.f, cut = s.rst[tt] != 0.f;
         const float af = __uint_as_float(r.a[n]);
         s.q[tt][c] = on ? raw_f<TIN>(r.q[n]) : 0.f;
         s.k[tt][c] = on ? raw_f<TIN>(r.k[n]) : 0.f;
@@ -729,10 +730,8 @@ __global__ void __launch_bounds__((SeqBwdCfg<KP, VP>::NT)) seq_bwd_kernel(SeqArg
 
     for (int blk = a.nck - 1; blk >= 0; --blk) {
         const int t0 = blk * CT, nt = min(CT, a.T - t0);
-        // Resets and adjoint clears as wave-uniform bit masks.
+        // Resets as a wave-uniform bit mask.
         const uint64_t rm = __ballot(lane < CT && s.rst[lane & (CT - 1)] != 0.f &&
-                                     s.val[lane & (CT - 1)] != 0.f);
-        const uint64_t cm = __ballot(lane < CT && s.clr[lane & (CT - 1)] != 0.f &&
                                      s.val[lane & (CT - 1)] != 0.f);
         if (!AHEAD) load_ck<KP, VP, RL, CL>(a, bh, blk, r0, c0, ckn);
         float S[RL][CL];
@@ -776,13 +775,6 @@ __global__ void __launch_bounds__((SeqBwdCfg<KP, VP>::NT)) seq_bwd_kernel(SeqArg
             if (!AHEAD) fetch_bwd<KP, VP, RL, CL>(s, tt, r0, c0, xl);
             const BwdTok<RL, CL> &x = AHEAD ? xin : xl;
             const int slot = tt % FT;
-            // Document limits: the adjoint is cleared where a document ends.
-            if ((cm >> tt) & 1) {
-#pragma unroll
-                for (int ri = 0; ri < RL; ++ri)
-#pragma unroll
-                    for (int cj = 0; cj < CL; ++cj) adj[ri][cj] = 0.f;
-            }
 #pragma unroll
             for (int ri = 0; ri < RL; ++ri)
 #pragma unroll

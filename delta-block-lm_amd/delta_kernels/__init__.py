@@ -259,8 +259,11 @@ def gdn2_backward(q, k, v, alpha, erase, write, d_output, checkpoint, doc_start,
     dw = torch.empty((B, T, H, V), dtype=torch.float32, device=dev)
     nws = L.gdn2_scan_workspace_bytes(ctypes.byref(shape))
     ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=dev)
-    if d_output is not None and d_output.dtype != q.dtype:
-        d_output = d_output.to(q.dtype)
+    if d_output is not None:
+        if d_output.dtype != q.dtype:
+            d_output = d_output.to(q.dtype)
+        if not _rows_aligned(d_output):
+            d_output = d_output.contiguous()
     views = [_view(x) for x in (q, k, v, alpha, erase, write, doc_start, doc_end)]
     dov = _view(d_output)
     with torch.cuda.device(dev):

@@ -87,8 +87,13 @@ GDN2_API const char *gdn2_last_error(void);
  *
  * q, k, v: F32 or BF16 (same dtype); alpha, erase, write, valid, reset,
  * initial: F32.  initial.data may be NULL (zero state).  chunk: 1..64, the
- * checkpoint interval in tokens (the reference allows 1..16,
- * gdn_training.rs:370-373); results do not depend on it. */
+ * checkpoint interval in tokens of the token-sequential kernels (the
+ * reference allows 1..16, gdn_training.rs:370-373); results do not depend on
+ * it.  bf16 q/k/v with keys = values = 64, unit channel stride and 16-byte
+ * aligned token rows run the 16-token chunk-WY MFMA kernels whatever the
+ * chunk argument (alpha >= 0; log alpha is floored at -80, below which the
+ * alpha gradient is zero); everything else runs the token-sequential
+ * kernels.  On the chunk kernels d_output must have aligned rows too. */
 GDN2_API size_t gdn2_training_checkpoint_bytes(const gdn2_shape *shape, int chunk);
 
 GDN2_API int gdn2_training_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q,
@@ -120,17 +125,23 @@ GDN2_API int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gd
 /* ---- Document-limit GDN-2 scan -------------------------------------------- */
 /* Replaces Gdn2Ops::gdn2_scan / gdn2_backward (reference
  * crates/kernels/src/ops.rs:17-276, CubeCL launches crates/kernels/src/gdn2.rs);
- * semantics of the f64 oracle crates/mixers/src/gdn2_reference.rs:84-226.
+ * forward semantics of the f64 oracle crates/mixers/src/gdn2_reference.rs:51-103.
  * Packed documents are described per token by inclusive int32 limits
  * doc_start[b,t], doc_end[b,t] (I32 views, strides [batch, time]):
  *   end < start      padding: zero output, state kept
  *   start == t       the state is zeroed before the token's update
- * The backward is the reference's doc-limit VJP: the state adjoint is cleared
- * at tokens with end == t (before that token's output gradient is added) and
- * passes unchanged through padding.  For documents whose tokens all carry the
- * same (start, end) this is the exact gradient.  Zero initial state; no final
- * state or score outputs.  q, k, v: F32 or BF16 (same dtype); alpha, erase,
- * write: F32.  The checkpoint (opaque) replaces the reference's
+ * The backward is the exact VJP of that forward, as the reference's chunked
+ * kernels compute it (gdn2.rs:24-65 decay products that vanish across a
+ * reset, :288-490): the state adjoint never crosses a reset and passes
+ * unchanged through padding.  The reference's f64 oracle
+ * (gdn2_reference.rs:107-226) instead clears the adjoint at tokens with
+ * end == t; the two agree whenever each reset follows a document end (the
+ * limits every packed batch carries) and differ only for limits where a reset
+ * has no preceding end or an end no following reset.  Zero initial state; no
+ * final state or score outputs.  q, k, v: F32 or BF16 (same dtype); alpha,
+ * erase, write: F32.  bf16 q/k/v with keys = values = 64 and 16-byte aligned
+ * rows run the 16-token chunk-WY MFMA kernels, everything else the
+ * token-sequential kernels.  The checkpoint (opaque) replaces the reference's
  * [B, H, T/16, 48, 64] checkpoint tensor. */
 GDN2_API size_t gdn2_scan_checkpoint_bytes(const gdn2_shape *shape);
 

@@ -1,8 +1,8 @@
 """f64 restatement of the document-limit GDN-2 scan and its VJP.
 
 TEST INFRASTRUCTURE ONLY: the checker for gdn2_scan / gdn2_backward in
-delta-block-lm_amd/csrc (the document-limit mode of the token-sequential
-kernels).  Nothing in the product imports it.
+delta-block-lm_amd/csrc (the document-limit mode of the token-sequential and
+chunk kernels).  Nothing in the product imports it.
 
 What it restates (read as text from the reference, never executed):
   doc_scan       crates/mixers/src/gdn2_reference.rs:51-103 (step and scan):
@@ -20,8 +20,12 @@ Pinned by tests/test_doc_oracle.py: for documents whose tokens share their
 valid/reset oracle (oracle/oracle.py scan and exact VJP); the reference's own
 padding test (gdn2_reference.rs:229-268) with its assertions and central
 differences; and central differences of doc_backward on consistent documents.
-For inconsistent limits (a reset not preceded by a document end) the backward
-is the reference's rule, pinned by restatement only.
+For inconsistent limits (a reset not preceded by a document end) doc_backward
+is the f64 oracle's rule, pinned by restatement only.  The reference's GPU op
+(crates/kernels/src/gdn2.rs:24-65, :288-490) computes the exact VJP of the
+forward instead, whose adjoint never crosses a reset: oracle.backward with the
+masks of oracle.doc_limits_to_masks.  The kernels here follow the GPU op; the two rules agree
+whenever each reset follows a document end.
 """
 from __future__ import annotations
 

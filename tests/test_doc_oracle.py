@@ -93,8 +93,9 @@ def test_reference_internal_padding_case():
 
 def test_inconsistent_limits_follow_the_reference_rule():
     """A reset at t = 3 whose previous token does not end its document: the
-    forward restarts the state, and the backward (reference rule) keeps the
-    adjoint flowing into tokens 0-2, unlike the exact VJP."""
+    forward restarts the state, and the f64 oracle's backward
+    (gdn2_reference.rs:107-226) keeps the adjoint flowing into tokens 0-2,
+    unlike the exact VJP that the reference's GPU kernels compute."""
     rng = np.random.default_rng(2)
     B, T, H, K, V = 1, 6, 1, 3, 2
     x = _inputs(rng, B, T, H, K, V)

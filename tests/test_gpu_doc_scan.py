@@ -11,8 +11,11 @@
 2. Packed documents at the lm512 head shape (K = V = 64) and K = V = 128, f32
    (1e-4 rms-floored) and bf16 (2e-2) against the f64 doc-limit oracle.
 3. Inconsistent limits (a reset whose previous token does not end its
-   document): the backward follows the reference's rule, which lets the
-   adjoint cross the reset (oracle/doc_oracle.py).
+   document): the backward is the exact VJP of the forward, as the reference's
+   GPU kernels compute it (crates/kernels/src/gdn2.rs:24-65, :288-490); the
+   reference's f64 oracle lets the adjoint cross that reset instead.
+4. bf16 with K = V = 64 runs the 16-token chunk-WY MFMA kernels (stage
+   timers), f32 and other widths the token-sequential kernels.
 """
 import numpy as np
 import pytest
@@ -172,19 +175,44 @@ def test_packed_documents_match_doc_oracle(dk, kv, dtype):
         gate(f"d{name}", t.grad, ref[name], tol, exact_zero=padg)
 
 
-def test_inconsistent_limits_follow_reference_rule(dk):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_inconsistent_limits_follow_reference_kernels(dk, dtype):
     x, _, _, up = _packed_problem(1, 40, 2, 64, 64, 3)
     start = np.zeros((1, 40), np.int32)
     end = np.full((1, 40), 39, np.int32)
     start[0, 20:] = 20  # a reset at 20 without a document end at 19
-    xs = [dev(a).requires_grad_(True) for a in x]
+    start[0, 33:], end[0, 25:33] = 33, 29  # an end at 29 without a reset at 30
+    xs = [dev(a, dtype if i < 3 else torch.float32).requires_grad_(True) for i, a in enumerate(x)]
+    xr = [a.detach().double().cpu().numpy() for a in xs]
     out = dk.gdn2_scan(*xs, dev(start, torch.int32), dev(end, torch.int32))
-    out.backward(dev(up))
-    ref_out, _ = do.doc_scan(*x, start, end)
-    gate("output", out, ref_out, TOL_F32)
-    ref = do.doc_backward(*x, start, end, up)
+    out.backward(dev(up, dtype))
+    upr = dev(up, dtype).double().cpu().numpy()
+    tol = TOL_F32 if dtype == torch.float32 else TOL_BF16
+    ref_out, _ = do.doc_scan(*xr, start, end)
+    gate("output", out, ref_out, tol)
+    valid, reset = oracle.doc_limits_to_masks(start, end)
+    exact = oracle.backward(*xr, valid, reset, upstream=upr)
     for name, t in zip(FIELDS, xs):
-        gate(f"d{name}", t.grad, ref[name], TOL_F32)
+        gate(f"d{name}", t.grad, exact[name], tol)
+    # the f64 oracle's rule differs here: its adjoint crosses the reset at 20
+    cpu_rule = do.doc_backward(*xr, start, end, upr)
+    assert np.abs(cpu_rule["k"][0, :20] - exact["k"][0, :20]).max() > 1e-2
+
+
+def test_bf16_d64_runs_chunk_kernels(dk):
+    x, start, end, up = _packed_problem(2, 100, 3, 64, 64, 9)
+    xs = [dev(a, torch.bfloat16 if i < 3 else torch.float32).requires_grad_(True)
+          for i, a in enumerate(x)]
+    dk.stage_timing(True)
+    try:
+        out = dk.gdn2_scan(*xs, dev(start, torch.int32), dev(end, torch.int32))
+        out.backward(dev(up, torch.bfloat16))
+        torch.cuda.synchronize()
+        ran = set(dk.stage_times())
+    finally:
+        dk.stage_timing(False)
+    assert {"chunk_prep", "state_scan", "chunk_out", "chunk_bprep", "adjoint_scan",
+            "chunk_bgrad"} <= ran, sorted(ran)
 
 
 def test_rejects_bad_limits(dk):
