@@ -77,6 +77,7 @@ struct ChunkArgs {
     struct CwGate *ck_cwg;
     float *ck_lam;
     float *ck_tf;  // T = (I + A)^-1 per 16-token chunk, f32
+    float *ck_p;   // P (decay-weighted q.k overlaps, lower, same segment) per chunk, f32
     // Lo parts (x - bf16(x)) of the chunk-start states and the chunk-end state
     // adjoints, kept by the scan when non-null.
     uint16_t *ck_state_lo, *ws_dstate_lo;
@@ -145,9 +146,9 @@ inline int64_t cw_chunk_count(int64_t B, int64_t T, int64_t H) {
     return B * H * ((T + CW_C - 1) / CW_C);
 }
 
-// Checkpoint per chunk: S0^T (bf16 hi/lo, 64x64), T (f32 16x16), CwGate, the
-// cumulative log decay Lambda (f32 16x64), delta (f32 16x64), M = A_c^T and A_c
-// (bf16 64x64), B_c^T (f32 64x64).
+// Checkpoint per chunk: S0^T (bf16 hi/lo, 64x64), T and P (f32 16x16), CwGate,
+// the cumulative log decay Lambda (f32 16x64), delta (f32 16x64), M = A_c^T and
+// A_c (bf16 64x64), B_c^T (f32 64x64).
 constexpr size_t CWK_STATE = (size_t)CHUNK_D * CHUNK_D * 2;
 constexpr size_t CWK_T = (size_t)CW_C * CW_C * 4;
 constexpr size_t CWK_GATE = sizeof(CwGate);
@@ -156,7 +157,7 @@ constexpr size_t CWK_DELTA = (size_t)CW_C * CHUNK_D * 4;
 constexpr size_t CWK_MAPM = (size_t)CHUNK_D * CHUNK_D * 2;
 constexpr size_t CWK_MAPN = (size_t)CHUNK_D * CHUNK_D * 4;
 constexpr size_t CWK_CHUNK =
-    2 * CWK_STATE + CWK_T + CWK_GATE + CWK_LAM + CWK_DELTA + 2 * CWK_MAPM + CWK_MAPN;
+    2 * CWK_STATE + 2 * CWK_T + CWK_GATE + CWK_LAM + CWK_DELTA + 2 * CWK_MAPM + CWK_MAPN;
 constexpr size_t CWW_CHUNK = 2 * CWK_STATE + CWK_MAPN;  // backward: dS^T (bf16 hi/lo), N^T (f32)
 
 inline size_t cw_checkpoint_bytes(int64_t B, int64_t T, int64_t H) {
@@ -174,6 +175,8 @@ inline void cw_bind_checkpoint(ChunkArgs &a, void *ck) {
     a.ck_state_lo = reinterpret_cast<uint16_t *>(p);
     p += n * CWK_STATE;
     a.ck_tf = reinterpret_cast<float *>(p);
+    p += n * CWK_T;
+    a.ck_p = reinterpret_cast<float *>(p);
     p += n * CWK_T;
     a.ck_cwg = reinterpret_cast<CwGate *>(p);
     p += n * CWK_GATE;

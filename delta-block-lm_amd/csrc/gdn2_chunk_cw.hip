@@ -93,6 +93,16 @@ __device__ __forceinline__ void load_t_split(const float *ckt, uint16_t *th, uin
     tl[r * LDB + s] = lo;
 }
 
+// P^T (from the f32 P checkpoint, 16 x 16) into hi/lo LDS rows [s][t];
+// thread (s = tid/16, t = tid%16).
+__device__ __forceinline__ void load_pt_split(const float *ckp, uint16_t *ph, uint16_t *pl, int tid) {
+    const int s = tid >> 4, t = tid & 15;
+    uint16_t hi, lo;
+    split_bf16(ckp[t * CC + s], hi, lo);
+    ph[s * LDB + t] = hi;
+    pl[s * LDB + t] = lo;
+}
+
 __device__ __forceinline__ void put4_f32(float *p, const float (&x)[4]) {
     *reinterpret_cast<float4 *>(p) = make_float4(x[0], x[1], x[2], x[3]);
 }
@@ -445,10 +455,12 @@ __global__ void __launch_bounds__(NT4) cw_out_kernel(ChunkArgs a) {
         float acc = p < 136 ? pair_dot32(sm.qf, sm.kf, sm.lam, tt, ss, half) : 0.f;
         acc += dpp<0xB1>(acc);
         if (p < 136 && half == 0) {
+            const float pv = sm.seg[tt] == sm.seg[ss] ? acc : 0.f;
             uint16_t hi, lo;
-            split_bf16(sm.seg[tt] == sm.seg[ss] ? acc : 0.f, hi, lo);
+            split_bf16(pv, hi, lo);
             sm.pr[tt * LDB + ss] = hi;
             sm.prl[tt * LDB + ss] = lo;
+            a.ck_p[(int64_t)ci * CC * CC + tt * CC + ss] = pv;  // for the backward
         }
     }
     for (int i = tid; i < 120; i += NT4) {  // zero the strict upper triangle of P
@@ -456,6 +468,7 @@ __global__ void __launch_bounds__(NT4) cw_out_kernel(ChunkArgs a) {
         pair_of(i, true, tt, ss);
         sm.pr[ss * LDB + tt] = 0;
         sm.prl[ss * LDB + tt] = 0;
+        a.ck_p[(int64_t)ci * CC * CC + ss * CC + tt] = 0.f;
     }
     // R = w.v - Ahat S0 and Qhat S0 for value tile w.
     f32x4 qs = zero4();
@@ -533,10 +546,10 @@ __global__ void __launch_bounds__(NT4) cw_out_kernel(ChunkArgs a) {
 
 // ---- backward prep: N of the adjoint map dS0 = A_c^T dS_16 + N -----------------
 // N = Y - W'^T X with Y = Qhat^T dO, X = P^T dO + diag(c) delta, W' = T Ahat
-// (formed again with prep's operands), c_s = dscore_s |k_s| / |delta_s|.
+// (formed again with prep's operands, P from the forward's checkpoint),
+// c_s = dscore_s |k_s| / |delta_s|.
 namespace {
 struct CwBPrepSmem {
-    float lam[CC * LDL], qf[CC * LDL], kf[CC * LDL];
     uint16_t qh[RT32], qhl[RT32];  // Qhat rows hi/lo (rows 16..31 zero)
     uint16_t ah[RT32], ahl[RT32];  // Ahat rows hi/lo (rows 16..31 zero)
     uint16_t dor[RT32];   // dO rows (rows 16..31 zero)
@@ -545,7 +558,6 @@ struct CwBPrepSmem {
     uint16_t wt[CT64], wtl[CT64];    // W'^T hi/lo
     uint16_t xt[CT64], xtl[CT64];    // X^T hi/lo
     float cs[CC];
-    int seg[CC];
 };
 }  // namespace
 
@@ -586,6 +598,7 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a) {
     float dl4[4];
     get4_f32(dck + t * 64 + c0, dl4);
     load_t_split(a.ck_tf + (int64_t)ci * CC * CC, sm.tb, sm.tbl, tid);
+    load_pt_split(a.ck_p + (int64_t)ci * CC * CC, sm.ptr, sm.ptrl, tid);
     {
         float qh[4], ah[4], ksq = 0.f, dsq = 0.f;
 #pragma unroll
@@ -596,9 +609,6 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a) {
             ksq += kv[e] * kv[e];
             dsq += dl4[e] * dl4[e];
         }
-        put4_f32(&sm.lam[t * LDL + c0], L);
-        put4_f32(&sm.qf[t * LDL + c0], qv);
-        put4_f32(&sm.kf[t * LDL + c0], kv);
         put4_split(&sm.qh[t * LDB + c0], &sm.qhl[t * LDB + c0], qh);
         put4_split(&sm.ah[t * LDB + c0], &sm.ahl[t * LDB + c0], ah);
         put4_bf16(&sm.dor[t * LDB + c0], dov);
@@ -608,30 +618,9 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a) {
             const float dsc = (a.dscores && inb) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
             const float nk = sqrtf(ksq), nd = sqrtf(dsq);
             sm.cs[t] = (nk > 0.f && nd > 0.f) ? dsc * nk / nd : 0.f;
-            sm.seg[t] = sg;
         }
     }
     __syncthreads();
-    // P (lower, same segment), stored transposed: ptr[s][t] = P[t][s].
-    for (int base = 0; base < 2 * 136; base += NT4) {
-        const int task = base + tid, p = task >> 1, half = task & 1;
-        int tt = 0, ss = 0;
-        if (p < 136) pair_of(p, false, tt, ss);
-        float acc = p < 136 ? pair_dot32(sm.qf, sm.kf, sm.lam, tt, ss, half) : 0.f;
-        acc += dpp<0xB1>(acc);
-        if (p < 136 && half == 0) {
-            uint16_t hi, lo;
-            split_bf16(sm.seg[tt] == sm.seg[ss] ? acc : 0.f, hi, lo);
-            sm.ptr[ss * LDB + tt] = hi;
-            sm.ptrl[ss * LDB + tt] = lo;
-        }
-    }
-    for (int i = tid; i < 120; i += NT4) {  // P^T is upper triangular: zero its strict lower part
-        int tt, ss;
-        pair_of(i, true, tt, ss);
-        sm.ptr[tt * LDB + ss] = 0;
-        sm.ptrl[tt * LDB + ss] = 0;
-    }
     // Y = Qhat^T dO (row tile w of keys, all value tiles) and W' = T Ahat (tile w).
     f32x4 y[4];
     {
@@ -683,7 +672,8 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a) {
 }
 
 // ---- bgrad: every gradient of one chunk -----------------------------------------
-// Given S0, delta (forward checkpoint) and dS at the chunk end (adjoint scan):
+// Given S0, delta and P (forward checkpoint) and dS at the chunk end (adjoint
+// scan):
 //   ddelta = P^T dO + Ktil dS + diag(c) delta;   dR = T^T ddelta
 //   dw = dR.v,  dv = dR.w;   dAhat = -dR S0^T;  dQhat = dO S0^T;  dKtil = delta dS^T
 //   dA = -strict_lower(dR delta^T),  dP = lower(dO delta^T)   (same segment)
@@ -698,44 +688,63 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a) {
 // (zero on padding and on valid reset tokens, where the reference's alpha' is
 // alpha (1 - reset) and carries no gradient).
 namespace {
+constexpr int BG_STATE = 64 * LDB;  // bf16 elements of a staged 64 x 64 tile
+
+// Two LDS regions change hands at barriers, so that two workgroups fit a CU:
+// region A holds dS^T (hi/lo) through phase 1, then ddelta^T, dR and dA/dP;
+// region B holds S0^T (hi/lo) through phase 4, then the sums of phase 5.
 struct CwBGradSmem {
-    float lam[CC * LDL], qf[CC * LDL], kf[CC * LDL], ehf[CC * LDL], ef[CC * LDL];
-    float seA[CC * LDL], sqP[CC * LDL], skAP[CC * LDL];
+    float lam[CC * LDL], ehf[CC * LDL];
     float dRf[CC * LDL];   // dR (f32) for dw, dv; dLambda afterwards
+    uint16_t qb[RT16], kb[RT16];     // q, k rows (bf16)
     uint16_t dor[RT32];    // dO rows (rows 16..31 zero)
     uint16_t kl[RT16], kll[RT16];    // Ktil rows hi/lo
-    uint16_t st[64 * LDB], dst[64 * LDB];    // S0^T, dS^T rows [v][k] hi
-    uint16_t stl[64 * LDB], dstl[64 * LDB];  // lo parts
-    uint16_t tb[RT32], tbl[RT32];    // T rows hi/lo (rows and columns 16..31 zero)
+    uint16_t ttr[RT16], ttrl[RT16];  // T^T rows hi/lo ([s][t], columns 16..31 zero)
     uint16_t dh[RT16], dlo[RT16];    // delta rows hi/lo
     uint16_t ptr[RT16], ptrl[RT16];  // P^T rows hi/lo; dq, dk rows (bf16) at the end
-    uint16_t ddt[CT64], ddtl[CT64];  // ddelta^T hi/lo
-    uint16_t drr[RT16], drrl[RT16];  // dR rows hi/lo
-    float dA[CC * LDI], dP[CC * LDI];
+    union {
+        uint16_t ds[2][BG_STATE];  // dS^T rows [v][k], hi and lo
+        struct {
+            uint16_t ddt[CT64], ddtl[CT64];    // ddelta^T hi/lo
+            uint16_t drr[RT16], drrl[RT16];    // dR rows hi/lo
+            float dA[CC * LDI], dP[CC * LDI];  // 16 x 16, same segment
+        } g;
+    } ra;
+    union {
+        uint16_t st[2][BG_STATE];  // S0^T rows [v][k], hi and lo
+        float sums[3][CC * LDL];   // eA, qP, kAP [token][channel]
+    } rb;
     float cs[CC], ck[CC], val[CC];
     int seg[CC];
     float tail[64], fr[64], bc[64];
 };
+
+// T^T (from the f32 T checkpoint) into hi/lo LDS rows [s][t]; thread
+// (t = tid/16, s = tid%16).
+__device__ __forceinline__ void load_tt_split(const float *ckt, uint16_t *th, uint16_t *tl, int tid) {
+    const int t = tid >> 4, s = tid & 15;
+    uint16_t hi, lo;
+    split_bf16(ckt[t * CC + s], hi, lo);
+    th[s * LDB + t] = hi;
+    tl[s * LDB + t] = lo;
+}
 }  // namespace
 
 __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
     __shared__ CwBGradSmem sm;
+    static_assert(sizeof(CwBGradSmem) <= 80 * 1024, "two workgroups per CU");
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = lane_id();
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid >> 4, c0 = 4 * (tid & 15), t0 = c * CC, tg = t0 + t;
     const bool inb = tg < a.T;
     zero_lds(sm.dor + RT16, RT32 - RT16, tid);
-    zero_lds(sm.tb + RT16, RT32 - RT16, tid);
-    zero_lds(sm.tbl + RT16, RT32 - RT16, tid);
     for (int i = tid; i < CC * 16; i += NT4) {
         const int r = i >> 4, cc = 16 + (i & 15);
-        sm.tb[r * LDB + cc] = 0;
-        sm.tbl[r * LDB + cc] = 0;
+        sm.ttr[r * LDB + cc] = 0;
+        sm.ttrl[r * LDB + cc] = 0;
         sm.ptr[r * LDB + cc] = 0;
         sm.ptrl[r * LDB + cc] = 0;
     }
-    for (int i = tid; i < 2 * 64 * 16; i += NT4)
-        ((i >> 10) == 0 ? sm.ddt : sm.ddtl)[((i >> 4) & 63) * LDW + 16 + (i & 15)] = 0;
     const CwGate *gb = a.ck_cwg + ci;
     const float va = gb->val[t];
     const int sg = gb->seg[t], sg15 = gb->seg[CC - 1];
@@ -757,12 +766,13 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int p = tid + NT4 * i, r = p >> 3, cb = 8 * (p & 7), o = r * 64 + cb;
-            *reinterpret_cast<uint4 *>(&sm.st[r * LDB + cb]) = *reinterpret_cast<const uint4 *>(a.ck_state + so + o);
-            *reinterpret_cast<uint4 *>(&sm.stl[r * LDB + cb]) = *reinterpret_cast<const uint4 *>(a.ck_state_lo + so + o);
-            *reinterpret_cast<uint4 *>(&sm.dst[r * LDB + cb]) = *reinterpret_cast<const uint4 *>(a.ws_dstate + so + o);
-            *reinterpret_cast<uint4 *>(&sm.dstl[r * LDB + cb]) = *reinterpret_cast<const uint4 *>(a.ws_dstate_lo + so + o);
+            *reinterpret_cast<uint4 *>(&sm.rb.st[0][r * LDB + cb]) = *reinterpret_cast<const uint4 *>(a.ck_state + so + o);
+            *reinterpret_cast<uint4 *>(&sm.rb.st[1][r * LDB + cb]) = *reinterpret_cast<const uint4 *>(a.ck_state_lo + so + o);
+            *reinterpret_cast<uint4 *>(&sm.ra.ds[0][r * LDB + cb]) = *reinterpret_cast<const uint4 *>(a.ws_dstate + so + o);
+            *reinterpret_cast<uint4 *>(&sm.ra.ds[1][r * LDB + cb]) = *reinterpret_cast<const uint4 *>(a.ws_dstate_lo + so + o);
         }
-        load_t_split(a.ck_tf + (int64_t)ci * CC * CC, sm.tb, sm.tbl, tid);
+        load_tt_split(a.ck_tf + (int64_t)ci * CC * CC, sm.ttr, sm.ttrl, tid);
+        load_pt_split(a.ck_p + (int64_t)ci * CC * CC, sm.ptr, sm.ptrl, tid);
     }
     {
         float eh[4], klv[4], ksq = 0.f, dsq = 0.f;
@@ -776,10 +786,9 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
             if (t == CC - 1) sm.bc[c0 + e] = sg15 == 0 ? __expf(L15) : 0.f;
         }
         put4_f32(&sm.lam[t * LDL + c0], L);
-        put4_f32(&sm.qf[t * LDL + c0], qv);
-        put4_f32(&sm.kf[t * LDL + c0], kv);
         put4_f32(&sm.ehf[t * LDL + c0], eh);
-        put4_f32(&sm.ef[t * LDL + c0], er);
+        put4_bf16(&sm.qb[t * LDB + c0], qv);  // exact: q, k are bf16 values
+        put4_bf16(&sm.kb[t * LDB + c0], kv);
         put4_bf16(&sm.dor[t * LDB + c0], dov);
         put4_split(&sm.kl[t * LDB + c0], &sm.kll[t * LDB + c0], klv);
         put4_split(&sm.dh[t * LDB + c0], &sm.dlo[t * LDB + c0], dl4);
@@ -797,50 +806,35 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
     }
     __syncthreads();
     // Phase 1: dQhat (key tile w), Ktil dS (value tile w), dKtil = delta dS^T (key
-    // tile w); P^T hi/lo (elementwise); rowsum(S0 . dS) per key channel.
+    // tile w); rowsum(S0 . dS) per key channel.
+    const uint16_t *st = sm.rb.st[0], *stl = sm.rb.st[1];
     f32x4 gqh = zero4(), kds = zero4(), gkt = zero4();
+    {
+        const uint16_t *dst = sm.ra.ds[0], *dstl = sm.ra.ds[1];
 #pragma unroll
-    for (int r = 0; r < 64; r += 32) {
-        const bf16x8_t sb = frag_tr(sm.st, r, 16 * w), db = frag_tr(sm.dst, r, 16 * w);
-        const bf16x8_t sbl = frag_tr(sm.stl, r, 16 * w), dbl = frag_tr(sm.dstl, r, 16 * w);
-        const bf16x8_t ob = frag(sm.dor, LDB, r);
-        gqh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ob, sb, gqh, 0, 0, 0);
-        gqh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ob, sbl, gqh, 0, 0, 0);
-        const bf16x8_t dsb = frag(&sm.dst[(16 * w) * LDB], LDB, r), kb = frag(sm.kl, LDB, r);
-        kds = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, dsb, kds, 0, 0, 0);
-        kds = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.kll, LDB, r), dsb, kds, 0, 0, 0);
-        kds = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, frag(&sm.dstl[(16 * w) * LDB], LDB, r), kds, 0, 0, 0);
-        const bf16x8_t hb = frag(sm.dh, LDB, r);
-        gkt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hb, db, gkt, 0, 0, 0);
-        gkt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.dlo, LDB, r), db, gkt, 0, 0, 0);
-        gkt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hb, dbl, gkt, 0, 0, 0);
-    }
-    for (int base = 0; base < 2 * 136; base += NT4) {
-        const int task = base + tid, p = task >> 1, half = task & 1;
-        int tt = 0, ss = 0;
-        if (p < 136) pair_of(p, false, tt, ss);
-        float acc = p < 136 ? pair_dot32(sm.qf, sm.kf, sm.lam, tt, ss, half) : 0.f;
-        acc += dpp<0xB1>(acc);
-        if (p < 136 && half == 0) {
-            uint16_t hi, lo;
-            split_bf16(sm.seg[tt] == sm.seg[ss] ? acc : 0.f, hi, lo);
-            sm.ptr[ss * LDB + tt] = hi;
-            sm.ptrl[ss * LDB + tt] = lo;
+        for (int r = 0; r < 64; r += 32) {
+            const bf16x8_t sb = frag_tr(st, r, 16 * w), db = frag_tr(dst, r, 16 * w);
+            const bf16x8_t sbl = frag_tr(stl, r, 16 * w), dbl = frag_tr(dstl, r, 16 * w);
+            const bf16x8_t ob = frag(sm.dor, LDB, r);
+            gqh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ob, sb, gqh, 0, 0, 0);
+            gqh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ob, sbl, gqh, 0, 0, 0);
+            const bf16x8_t dsb = frag(&dst[(16 * w) * LDB], LDB, r), kb = frag(sm.kl, LDB, r);
+            kds = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, dsb, kds, 0, 0, 0);
+            kds = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.kll, LDB, r), dsb, kds, 0, 0, 0);
+            kds = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, frag(&dstl[(16 * w) * LDB], LDB, r), kds, 0, 0, 0);
+            const bf16x8_t hb = frag(sm.dh, LDB, r);
+            gkt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hb, db, gkt, 0, 0, 0);
+            gkt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.dlo, LDB, r), db, gkt, 0, 0, 0);
+            gkt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hb, dbl, gkt, 0, 0, 0);
         }
-    }
-    for (int i = tid; i < 120; i += NT4) {
-        int tt, ss;
-        pair_of(i, true, tt, ss);
-        sm.ptr[tt * LDB + ss] = 0;
-        sm.ptrl[tt * LDB + ss] = 0;
-    }
-    if (tid < 64) {  // rowsum_v S0[i][v] dS[i][v] for key channel i = tid
-        float f = 0.f;
+        if (tid < 64) {  // rowsum_v S0[i][v] dS[i][v] for key channel i = tid
+            float f = 0.f;
 #pragma unroll 8
-        for (int v = 0; v < 64; ++v)
-            f += (bf16_val(sm.st[v * LDB + tid]) + bf16_val(sm.stl[v * LDB + tid])) *
-                 (bf16_val(sm.dst[v * LDB + tid]) + bf16_val(sm.dstl[v * LDB + tid]));
-        sm.fr[tid] = f;
+            for (int v = 0; v < 64; ++v)
+                f += (bf16_val(st[v * LDB + tid]) + bf16_val(stl[v * LDB + tid])) *
+                     (bf16_val(dst[v * LDB + tid]) + bf16_val(dstl[v * LDB + tid]));
+            sm.fr[tid] = f;
+        }
     }
     {  // sum_s Ktil_s dKtil_s per key channel (f32 Ktil)
         const int i = 16 * w + acc_col();
@@ -849,13 +843,18 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int s = acc_row(e);
-            const float kt = sm.seg[s] == sm.seg[CC - 1] ? __expf(L15 - sm.lam[s * LDL + i]) * sm.kf[s * LDL + i] : 0.f;
+            const float kt = sm.seg[s] == sm.seg[CC - 1]
+                                 ? __expf(L15 - sm.lam[s * LDL + i]) * bf16_val(sm.kb[s * LDB + i])
+                                 : 0.f;
             z[e] = kt * gkt[e];
         }
         const float cz = col_reduce(z);
         if ((l >> 4) == 0) sm.tail[i] = cz;
     }
-    __syncthreads();
+    __syncthreads();  // dS is dead: region A takes ddelta^T, dR, dA, dP
+    auto &g = sm.ra.g;
+    for (int i = tid; i < 2 * 64 * 16; i += NT4)
+        ((i >> 10) == 0 ? g.ddt : g.ddtl)[((i >> 4) & 63) * LDW + 16 + (i & 15)] = 0;
     // Phase 2: ddelta = P^T dO + Ktil dS + c delta (value tile w) -> ddelta^T hi/lo.
     {
         const bf16x8_t db = frag_tr(sm.dor, 0, 16 * w);
@@ -866,18 +865,18 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) x[e] += sm.cs[acc_row(e)] * dck[acc_row(e) * 64 + 16 * w + acc_col()];
         }
-        store_tile_t_split(&sm.ddt[(16 * w) * LDW], &sm.ddtl[(16 * w) * LDW], LDW, x);
+        store_tile_t_split(&g.ddt[(16 * w) * LDW], &g.ddtl[(16 * w) * LDW], LDW, x);
     }
     __syncthreads();
-    // Phase 3: dR = T^T ddelta (value tile w) -> dR rows (bf16) and f32.
+    // Phase 3: dR = T^T ddelta (value tile w) -> dR rows (hi/lo) and f32.
     {
-        const bf16x8_t ta = frag_tr(sm.tb, 0, 0), tal = frag_tr(sm.tbl, 0, 0);  // A[s][t] = T[t][s]
-        const bf16x8_t db = frag(&sm.ddt[(16 * w) * LDW], LDW, 0);
+        const bf16x8_t ta = frag(sm.ttr, LDB, 0), tal = frag(sm.ttrl, LDB, 0);  // A[s][t] = T[t][s]
+        const bf16x8_t db = frag(&g.ddt[(16 * w) * LDW], LDW, 0);
         f32x4 x = zero4();
         x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, db, x, 0, 0, 0);
-        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, frag(&sm.ddtl[(16 * w) * LDW], LDW, 0), x, 0, 0, 0);
+        x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, frag(&g.ddtl[(16 * w) * LDW], LDW, 0), x, 0, 0, 0);
         x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tal, db, x, 0, 0, 0);
-        store_tile_rm_split(&sm.drr[16 * w], &sm.drrl[16 * w], LDB, x);
+        store_tile_rm_split(&g.drr[16 * w], &g.drrl[16 * w], LDB, x);
 #pragma unroll
         for (int e = 0; e < 4; ++e) sm.dRf[acc_row(e) * LDL + 16 * w + acc_col()] = x[e];
     }
@@ -886,30 +885,30 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
     f32x4 gah = zero4();
 #pragma unroll
     for (int r = 0; r < 64; r += 32) {
-        const bf16x8_t sb = frag_tr(sm.st, r, 16 * w), rb = frag(sm.drr, LDB, r);
+        const bf16x8_t sb = frag_tr(st, r, 16 * w), rb = frag(g.drr, LDB, r);
         gah = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rb, sb, gah, 0, 0, 0);
-        gah = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.drrl, LDB, r), sb, gah, 0, 0, 0);
-        gah = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rb, frag_tr(sm.stl, r, 16 * w), gah, 0, 0, 0);
+        gah = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(g.drrl, LDB, r), sb, gah, 0, 0, 0);
+        gah = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rb, frag_tr(stl, r, 16 * w), gah, 0, 0, 0);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) gah[e] = -gah[e];
     if (w < 2) {
         f32x4 x = zero4();
-        const uint16_t *lhs = w == 0 ? sm.drr : sm.dor;
+        const uint16_t *lhs = w == 0 ? g.drr : sm.dor;
 #pragma unroll
         for (int r = 0; r < 64; r += 32) {
             const bf16x8_t la = frag(lhs, LDB, r), dhb = frag(sm.dh, LDB, r);
             x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(la, dhb, x, 0, 0, 0);
             x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(la, frag(sm.dlo, LDB, r), x, 0, 0, 0);
-            if (w == 0) x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.drrl, LDB, r), dhb, x, 0, 0, 0);
+            if (w == 0) x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(g.drrl, LDB, r), dhb, x, 0, 0, 0);
         }
         const int ss = acc_col();
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int tt = acc_row(e);
             const bool same = sm.seg[tt] == sm.seg[ss];
-            if (w == 0) sm.dA[tt * LDI + ss] = (ss < tt && same) ? -x[e] : 0.f;
-            else sm.dP[tt * LDI + ss] = (ss <= tt && same) ? x[e] : 0.f;
+            if (w == 0) g.dA[tt * LDI + ss] = (ss < tt && same) ? -x[e] : 0.f;
+            else g.dP[tt * LDI + ss] = (ss <= tt && same) ? x[e] : 0.f;
         }
     }
     if (inb) {  // dw = dR.v, dv = dR.w (token t, channels c0 .. c0 + 3)
@@ -924,29 +923,35 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
         if (a.dwrite) put4_f32(a.dwrite + row * 64 + c0, dw4);
         if (a.dv) put4_bf16(reinterpret_cast<uint16_t *>(a.dv) + row * 64 + c0, dv4);
     }
-    __syncthreads();
+    __syncthreads();  // S0 is dead: region B takes the sums of phase 5
     // Phase 5: the decay-weighted sums, elementwise.  Thread (channel i = tid/4,
     // part = tid%4) takes the rows t = part, part + 4, part + 8, part + 12 and every
     // s <= t: eA_t, qP_t are its own; kAP_s is summed over the four parts (a DPP
     // quad).
+    float *seA = sm.rb.sums[0], *sqP = sm.rb.sums[1], *skAP = sm.rb.sums[2];
     {
         const int i = tid >> 2, part = tid & 3;
         float eA[4] = {0.f, 0.f, 0.f, 0.f}, qP[4] = {0.f, 0.f, 0.f, 0.f};
-        float kAP[CC];
+        float kAP[CC], Ls[CC], ks[CC];
 #pragma unroll
-        for (int s = 0; s < CC; ++s) kAP[s] = 0.f;
+        for (int s = 0; s < CC; ++s) {
+            kAP[s] = 0.f;
+            Ls[s] = sm.lam[s * LDL + i];
+            ks[s] = bf16_val(sm.kb[s * LDB + i]);
+        }
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const int tt = part + 4 * m;
-            const float Lt = sm.lam[tt * LDL + i], et = sm.ehf[tt * LDL + i], qt = sm.qf[tt * LDL + i];
+            const float Lt = sm.lam[tt * LDL + i], et = sm.ehf[tt * LDL + i];
+            const float qt = bf16_val(sm.qb[tt * LDB + i]);
 #pragma unroll
             for (int s = 0; s < CC; ++s) {
                 if (s > tt) continue;
-                const float D = s == tt ? 1.f : __expf(Lt - sm.lam[s * LDL + i]);
-                const float dA = sm.dA[tt * LDI + s], dP = sm.dP[tt * LDI + s];
-                const float ks = sm.kf[s * LDL + i] * D;
-                eA[m] += dA * ks;
-                qP[m] += dP * ks;
+                const float D = s == tt ? 1.f : __expf(Lt - Ls[s]);
+                const float dA = g.dA[tt * LDI + s], dP = g.dP[tt * LDI + s];
+                const float kd = ks[s] * D;
+                eA[m] += dA * kd;
+                qP[m] += dP * kd;
                 kAP[s] += (dA * et + dP * qt) * D;
             }
         }
@@ -959,12 +964,12 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
         }
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            sm.seA[(part + 4 * m) * LDL + i] = eA[m];
-            sm.sqP[(part + 4 * m) * LDL + i] = qP[m];
+            seA[(part + 4 * m) * LDL + i] = eA[m];
+            sqP[(part + 4 * m) * LDL + i] = qP[m];
         }
         if (part == 0) {
 #pragma unroll
-            for (int s = 0; s < CC; ++s) sm.skAP[s * LDL + i] = kAP[s];
+            for (int s = 0; s < CC; ++s) skAP[s * LDL + i] = kAP[s];
         }
     }
     __syncthreads();
@@ -975,14 +980,15 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
         f32x4 gq, gk;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int tt = acc_row(e);
+            const int tt = acc_row(e), tq = t0 + tt;
             const bool von = sm.val[tt] != 0.f;
             const float Lt = sm.lam[tt * LDL + i];
             const float bt = sm.seg[tt] == 0 ? __expf(Lt) : 0.f;
             const float lt = sm.seg[tt] == sm.seg[CC - 1] ? __expf(L15 - Lt) : 0.f;
-            const float q = sm.qf[tt * LDL + i], k = sm.kf[tt * LDL + i];
-            const float eh = sm.ehf[tt * LDL + i], ee = sm.ef[tt * LDL + i];
-            const float eA = sm.seA[tt * LDL + i], qP = sm.sqP[tt * LDL + i], kAP = sm.skAP[tt * LDL + i];
+            const float q = bf16_val(sm.qb[tt * LDB + i]), k = bf16_val(sm.kb[tt * LDB + i]);
+            const float eh = sm.ehf[tt * LDL + i];
+            const float ee = (von && tq < a.T) ? ld4<float>(a.erase, b, tq, h, i) : 0.f;
+            const float eA = seA[tt * LDL + i], qP = sqP[tt * LDL + i], kAP = skAP[tt * LDL + i];
             const float dq = bt * gqh[e] + qP;
             const float deh = bt * gah[e] + eA;
             const float dk = lt * gkt[e] + kAP + ee * deh + sm.ck[tt] * k;
@@ -991,7 +997,6 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
             gq[e] = von ? dq : 0.f;
             gk[e] = von ? dk : 0.f;
             sm.dRf[tt * LDL + i] = dlam;  // dR is dead: dLambda takes its place
-            const int tq = t0 + tt;
             if (a.derase && tq < a.T)
                 a.derase[(((int64_t)b * a.T + tq) * a.H + h) * 64 + i] = von ? k * deh : 0.f;
         }
