@@ -283,6 +283,8 @@ constexpr int SRT = KD / 16 / SW;   // row tiles per wave
 constexpr int SKS = KD / 32;        // reduction steps of a 16x16x32 product
 constexpr int LDX = KD + 8;
 constexpr int NCG = KD / 16;        // 16-column groups per state
+constexpr int CPW = 2;              // column groups per workgroup (one M load serves both)
+constexpr int NWG = NCG / CPW;      // workgroups per head
 }  // namespace
 
 struct WScanArgs {
@@ -296,58 +298,71 @@ struct WScanArgs {
 };
 
 template <int SL, typename F, typename Gt>
-__device__ __forceinline__ void wscan_step(int s, const WScanArgs &p, int bh, int j, int w,
-                                           f32x4 (&X)[SRT], bf16x8_t (&mf)[3][SRT][SKS],
-                                           f32x4 (&nf)[3][SRT], uint16_t (*xs)[2][16 * LDX],
-                                           F &fetch, Gt &chunk_of) {
+__device__ __forceinline__ void wscan_step(int s, const WScanArgs &p, int bh, int j0, int w,
+                                           f32x4 (&X)[CPW][SRT], bf16x8_t (&mf)[3][SRT][SKS],
+                                           f32x4 (&nf)[3][CPW][SRT],
+                                           uint16_t (*xs)[CPW][2][16 * LDX], F &fetch,
+                                           Gt &chunk_of) {
     const int c = chunk_of(s);
     uint16_t *ck = p.ckpt + ((int64_t)bh * p.nc + c) * KD * KD;
-    uint16_t *xh = xs[s & 1][0], *xl = xs[s & 1][1];
 #pragma unroll
-    for (int rt = 0; rt < SRT; ++rt) {
-        const int mt = SRT * w + rt;
-        *reinterpret_cast<uint2 *>(&ck[j * KD + 16 * mt + acc_row(0)]) =
-            make_uint2(bf16_pack2(X[rt][0], X[rt][1]), bf16_pack2(X[rt][2], X[rt][3]));
-        store_tile_t_split(xh + 16 * mt, xl + 16 * mt, LDX, X[rt]);  // [col][row]
+    for (int g = 0; g < CPW; ++g) {
+        const int j = j0 + 16 * g;
+#pragma unroll
+        for (int rt = 0; rt < SRT; ++rt) {
+            const int mt = SRT * w + rt;
+            *reinterpret_cast<uint2 *>(&ck[j * KD + 16 * mt + acc_row(0)]) =
+                make_uint2(bf16_pack2(X[g][rt][0], X[g][rt][1]), bf16_pack2(X[g][rt][2], X[g][rt][3]));
+            store_tile_t_split(xs[s & 1][g][0] + 16 * mt, xs[s & 1][g][1] + 16 * mt, LDX, X[g][rt]);
+        }
     }
     __syncthreads();
     // Y = M X from zero, then X = Y + N: N stays an ordinary operand that is
     // waited for only at the end of the step.
-    f32x4 Y[SRT];
+    f32x4 Y[CPW][SRT];
 #pragma unroll
-    for (int rt = 0; rt < SRT; ++rt) Y[rt] = zero4();
+    for (int g = 0; g < CPW; ++g)
+#pragma unroll
+        for (int rt = 0; rt < SRT; ++rt) Y[g][rt] = zero4();
 #pragma unroll
     for (int kk = 0; kk < SKS; ++kk) {
-        const bf16x8_t bh_ = frag(xh, LDX, 32 * kk), bl_ = frag(xl, LDX, 32 * kk);
 #pragma unroll
-        for (int rt = 0; rt < SRT; ++rt) {
-            Y[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][rt][kk], bh_, Y[rt], 0, 0, 0);
-            Y[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][rt][kk], bl_, Y[rt], 0, 0, 0);
+        for (int g = 0; g < CPW; ++g) {
+            const bf16x8_t bh_ = frag(xs[s & 1][g][0], LDX, 32 * kk), bl_ = frag(xs[s & 1][g][1], LDX, 32 * kk);
+#pragma unroll
+            for (int rt = 0; rt < SRT; ++rt) {
+                Y[g][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][rt][kk], bh_, Y[g][rt], 0, 0, 0);
+                Y[g][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][rt][kk], bl_, Y[g][rt], 0, 0, 0);
+            }
         }
     }
 #pragma unroll
-    for (int rt = 0; rt < SRT; ++rt)
+    for (int g = 0; g < CPW; ++g)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) X[rt][i] = Y[rt][i] + nf[SL][rt][i];
+        for (int rt = 0; rt < SRT; ++rt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) X[g][rt][i] = Y[g][rt][i] + nf[SL][g][rt][i];
     // Unconditional (the last chunk again past the end): every step issues the
     // same loads, so the wait for a ring slot counts only the later steps' loads
     // and stores instead of draining the whole queue.
     fetch(chunk_of(min(s + 3, p.nc - 1)), mf[SL], nf[SL]);
 }
 
-// Workgroup x -> (head bh, column group cg); the NCG groups of a head take
-// indices with equal residue mod 8, so they share one XCD's L2.
+// Workgroup x -> (head bh, column groups CPW g0 .. CPW g0 + CPW - 1); the NWG
+// workgroups of a head take indices with equal residue mod 8, so they share
+// one XCD's L2.  Each wave holds SRT row tiles of M for the whole step and
+// applies them to the workgroup's CPW column groups.
 __global__ void __launch_bounds__(64 * SW) wide_scan_kernel(WScanArgs p) {
-    __shared__ uint16_t xs[2][2][16 * LDX];
+    __shared__ uint16_t xs[2][CPW][2][16 * LDX];
     const int x = blockIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
-    const int cg = (x >> 3) % NCG, bh = (x & 7) + 8 * (x / (8 * NCG));
+    const int g0 = (x >> 3) % NWG, bh = (x & 7) + 8 * (x / (8 * NWG));
     if (bh >= p.B * p.H) return;
     const int b = bh / p.H, h = bh % p.H;
-    const int j = 16 * cg + (l & 15);  // this lane's state column
+    const int j0 = 16 * CPW * g0 + (l & 15);  // this lane's column in group 0
     bf16x8_t mf[3][SRT][SKS];
-    f32x4 nf[3][SRT];
+    f32x4 nf[3][CPW][SRT];
     auto chunk_of = [&](int s) { return p.reverse ? p.nc - 1 - s : s; };
-    auto fetch = [&](int c, bf16x8_t (&m)[SRT][SKS], f32x4 (&n)[SRT]) {
+    auto fetch = [&](int c, bf16x8_t (&m)[SRT][SKS], f32x4 (&n)[CPW][SRT]) {
         const int64_t cix = (int64_t)bh * p.nc + c;
         const uint16_t *M = p.m + cix * KD * KD;
         const float *N = p.n + cix * KD * KD;
@@ -359,37 +374,44 @@ __global__ void __launch_bounds__(64 * SW) wide_scan_kernel(WScanArgs p) {
                 m[rt][kk] = __builtin_bit_cast(
                     bf16x8_t, *reinterpret_cast<const uint4 *>(M + (16 * mt + (l & 15)) * KD +
                                                                32 * kk + 8 * (l >> 4)));
-            const float4 nv = *reinterpret_cast<const float4 *>(&N[j * KD + 16 * mt + acc_row(0)]);
-            n[rt] = f32x4{nv.x, nv.y, nv.z, nv.w};
+#pragma unroll
+            for (int g = 0; g < CPW; ++g) {
+                const float4 nv = *reinterpret_cast<const float4 *>(&N[(j0 + 16 * g) * KD + 16 * mt + acc_row(0)]);
+                n[g][rt] = f32x4{nv.x, nv.y, nv.z, nv.w};
+            }
         }
     };
     fetch(chunk_of(0), mf[0], nf[0]);
-    f32x4 X[SRT];
+    f32x4 X[CPW][SRT];
 #pragma unroll
-    for (int rt = 0; rt < SRT; ++rt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            X[rt][i] = p.x0.data ? ld4<float>(p.x0, b, h, 16 * (SRT * w + rt) + acc_row(i), j) : 0.f;
-    fetch(chunk_of(min(1, p.nc - 1)), mf[1], nf[1]);
-    fetch(chunk_of(min(2, p.nc - 1)), mf[2], nf[2]);
-    int s = 0;
-    for (; s + 2 < p.nc; s += 3) {  // whole ring turns
-        wscan_step<0>(s, p, bh, j, w, X, mf, nf, xs, fetch, chunk_of);
-        wscan_step<1>(s + 1, p, bh, j, w, X, mf, nf, xs, fetch, chunk_of);
-        wscan_step<2>(s + 2, p, bh, j, w, X, mf, nf, xs, fetch, chunk_of);
-    }
-    if (s < p.nc) wscan_step<0>(s, p, bh, j, w, X, mf, nf, xs, fetch, chunk_of);
-    if (s + 1 < p.nc) wscan_step<1>(s + 1, p, bh, j, w, X, mf, nf, xs, fetch, chunk_of);
-    if (p.xout)
+    for (int g = 0; g < CPW; ++g)
 #pragma unroll
         for (int rt = 0; rt < SRT; ++rt)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                p.xout[((int64_t)bh * KD + 16 * (SRT * w + rt) + acc_row(i)) * KD + j] = X[rt][i];
+                X[g][rt][i] = p.x0.data ? ld4<float>(p.x0, b, h, 16 * (SRT * w + rt) + acc_row(i), j0 + 16 * g) : 0.f;
+    fetch(chunk_of(min(1, p.nc - 1)), mf[1], nf[1]);
+    fetch(chunk_of(min(2, p.nc - 1)), mf[2], nf[2]);
+    int s = 0;
+    for (; s + 2 < p.nc; s += 3) {  // whole ring turns
+        wscan_step<0>(s, p, bh, j0, w, X, mf, nf, xs, fetch, chunk_of);
+        wscan_step<1>(s + 1, p, bh, j0, w, X, mf, nf, xs, fetch, chunk_of);
+        wscan_step<2>(s + 2, p, bh, j0, w, X, mf, nf, xs, fetch, chunk_of);
+    }
+    if (s < p.nc) wscan_step<0>(s, p, bh, j0, w, X, mf, nf, xs, fetch, chunk_of);
+    if (s + 1 < p.nc) wscan_step<1>(s + 1, p, bh, j0, w, X, mf, nf, xs, fetch, chunk_of);
+    if (p.xout)
+#pragma unroll
+        for (int g = 0; g < CPW; ++g)
+#pragma unroll
+            for (int rt = 0; rt < SRT; ++rt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    p.xout[((int64_t)bh * KD + 16 * (SRT * w + rt) + acc_row(i)) * KD + j0 + 16 * g] = X[g][rt][i];
 }
 
 static void launch_wide_scan(const WScanArgs &p, hipStream_t stream) {
-    const dim3 grid(8 * NCG * ((p.B * p.H + 7) / 8)), block(64 * SW);
+    const dim3 grid(8 * NWG * ((p.B * p.H + 7) / 8)), block(64 * SW);
     hipLaunchKernelGGL(wide_scan_kernel, grid, block, 0, stream, p);
 }
 
