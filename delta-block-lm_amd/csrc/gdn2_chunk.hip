@@ -224,42 +224,55 @@ struct AffineArgs {
     int reverse;
 };
 
+constexpr int ACG = 1;            // column groups of 16 per scan wave (2 measured slower)
+constexpr int ANW = D / 16 / ACG;  // scan waves (workgroups) per head
+
 template <int SL, typename F, typename Gt>
-__device__ __forceinline__ void affine_step(int s, const AffineArgs &p, int bh, int j,
-                                            f32x4 (&X)[4], bf16x8_t (&mf)[3][4][2],
-                                            f32x4 (&nf)[3][4], uint16_t *xh, uint16_t *xl,
+__device__ __forceinline__ void affine_step(int s, const AffineArgs &p, int bh, int j0,
+                                            f32x4 (&X)[ACG][4], bf16x8_t (&mf)[3][4][2],
+                                            f32x4 (&nf)[3][ACG][4], uint16_t (*xs)[2][16 * LDB],
                                             F &fetch, Gt &chunk_of) {
     const int c = chunk_of(s);
-    uint16_t *ck = p.ckpt + ((int64_t)bh * p.nc + c) * D * D;  // X^T, bf16
+    const int64_t co = ((int64_t)bh * p.nc + c) * D * D;
 #pragma unroll
-    for (int tm = 0; tm < 4; ++tm) {
-        *reinterpret_cast<uint2 *>(&ck[j * D + 16 * tm + acc_row(0)]) =
-            make_uint2(bf16_pack2(X[tm][0], X[tm][1]), bf16_pack2(X[tm][2], X[tm][3]));
-        if (p.ckpt_lo) {
-            float r[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) r[i] = X[tm][i] - bf16_val(bf16_bits(X[tm][i]));
-            *reinterpret_cast<uint2 *>(&p.ckpt_lo[((int64_t)bh * p.nc + c) * D * D + j * D + 16 * tm +
-                                                  acc_row(0)]) =
-                make_uint2(bf16_pack2(r[0], r[1]), bf16_pack2(r[2], r[3]));
-        }
-        store_tile_t_split(xh + 16 * tm, xl + 16 * tm, LDB, X[tm]);  // [col][row]
-    }
-    __syncthreads();
-    f32x4 Y[4];
-#pragma unroll
-    for (int tm = 0; tm < 4; ++tm) Y[tm] = nf[SL][tm];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-        const bf16x8_t bh_ = frag(xh, LDB, 32 * kk), bl_ = frag(xl, LDB, 32 * kk);
+    for (int g = 0; g < ACG; ++g) {
+        const int j = j0 + 16 * g;
 #pragma unroll
         for (int tm = 0; tm < 4; ++tm) {
-            Y[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][tm][kk], bh_, Y[tm], 0, 0, 0);
-            Y[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][tm][kk], bl_, Y[tm], 0, 0, 0);
+            *reinterpret_cast<uint2 *>(&p.ckpt[co + j * D + 16 * tm + acc_row(0)]) =
+                make_uint2(bf16_pack2(X[g][tm][0], X[g][tm][1]), bf16_pack2(X[g][tm][2], X[g][tm][3]));
+            if (p.ckpt_lo) {
+                float r[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) r[i] = X[g][tm][i] - bf16_val(bf16_bits(X[g][tm][i]));
+                *reinterpret_cast<uint2 *>(&p.ckpt_lo[co + j * D + 16 * tm + acc_row(0)]) =
+                    make_uint2(bf16_pack2(r[0], r[1]), bf16_pack2(r[2], r[3]));
+            }
+            store_tile_t_split(xs[g][0] + 16 * tm, xs[g][1] + 16 * tm, LDB, X[g][tm]);  // [col][row]
+        }
+    }
+    __syncthreads();
+    f32x4 Y[ACG][4];
+#pragma unroll
+    for (int g = 0; g < ACG; ++g)
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) Y[g][tm] = nf[SL][g][tm];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+        for (int g = 0; g < ACG; ++g) {
+            const bf16x8_t bh_ = frag(xs[g][0], LDB, 32 * kk), bl_ = frag(xs[g][1], LDB, 32 * kk);
+#pragma unroll
+            for (int tm = 0; tm < 4; ++tm) {
+                Y[g][tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][tm][kk], bh_, Y[g][tm], 0, 0, 0);
+                Y[g][tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][tm][kk], bl_, Y[g][tm], 0, 0, 0);
+            }
         }
     }
 #pragma unroll
-    for (int tm = 0; tm < 4; ++tm) X[tm] = Y[tm];
+    for (int g = 0; g < ACG; ++g)
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) X[g][tm] = Y[g][tm];
     // Unconditional (the last chunk again past the end), so that in the rolled
     // loop every step issues the same loads and a slot's wait counts only the
     // later steps' memory operations.
@@ -267,29 +280,30 @@ __device__ __forceinline__ void affine_step(int s, const AffineArgs &p, int bh, 
     __syncthreads();
 }
 
-// One wave per workgroup: wave w of head bh owns state columns 16w..16w+15,
-// which evolve independently (Y = M X acts on columns), so the four column
-// groups of a head run as four workgroups spread over the CUs (the scan is
-// bound by the loads each CU can stream per step: a four-wave workgroup per
-// head, sharing M through L1, measured twice as slow).  Workgroups are dealt
-// to the 8 XCDs round-robin by index; the four column groups of a head take
-// indices with equal residue mod 8, so they share one XCD's L2.
+// One wave per workgroup: wave w of head bh owns the ACG groups of 16 state
+// columns from 16 ACG w, which evolve independently (Y = M X acts on
+// columns); one load of M's fragments serves all of them.  The ANW workgroups
+// of a head are spread over the CUs (the scan is bound by the loads each CU can
+// stream per step: a four-wave workgroup per head, sharing M through L1,
+// measured twice as slow).  Workgroups are dealt to the 8 XCDs round-robin by
+// index; the groups of a head take indices with equal residue mod 8, so they
+// share one XCD's L2.
 // NC > 0: the chunk count is a compile-time constant and the chunk loop is
 // straight-line code, so the loads of the three-deep (M, N) ring are waited
 // for one by one; NC == 0 runs any count in a rolled loop.
 template <int NC>
 __global__ void __launch_bounds__(64) affine_scan_kernel(AffineArgs p) {
-    __shared__ uint16_t xs[1][2][16 * LDB];
+    __shared__ uint16_t xs[ACG][2][16 * LDB];
     const int x = blockIdx.x, l = lane_id();
-    const int w = (x >> 3) & 3, bh = (x & 7) + 8 * (x >> 5);
+    const int w = (x >> 3) % ANW, bh = (x & 7) + 8 * (x / (8 * ANW));
     if (bh >= p.B * p.H) return;
     const int b = bh / p.H, h = bh % p.H;
-    const int j = 16 * w + (l & 15);  // this lane's state column
+    const int j0 = 16 * ACG * w + (l & 15);  // this lane's column in group 0
     // Three chunks of (M, N) in flight: one global latency spans three steps.
     bf16x8_t mf[3][4][2];
-    f32x4 nf[3][4];
+    f32x4 nf[3][ACG][4];
     auto chunk_of = [&](int s) { return p.reverse ? p.nc - 1 - s : s; };
-    auto fetch = [&](int c, bf16x8_t (&m)[4][2], f32x4 (&n)[4]) {
+    auto fetch = [&](int c, bf16x8_t (&m)[4][2], f32x4 (&n)[ACG][4]) {
         const int64_t ci = (int64_t)bh * p.nc + c;
         const uint16_t *M = p.m + ci * D * D;
         const float *N = p.n + ci * D * D;
@@ -300,45 +314,51 @@ __global__ void __launch_bounds__(64) affine_scan_kernel(AffineArgs p) {
                 m[tm][kk] = __builtin_bit_cast(
                     bf16x8_t, *reinterpret_cast<const uint4 *>(M + (16 * tm + (l & 15)) * D +
                                                                32 * kk + 8 * (l >> 4)));
-            const float4 nv = *reinterpret_cast<const float4 *>(&N[j * D + 16 * tm + acc_row(0)]);
-            n[tm] = f32x4{nv.x, nv.y, nv.z, nv.w};
+#pragma unroll
+            for (int g = 0; g < ACG; ++g) {
+                const float4 nv = *reinterpret_cast<const float4 *>(&N[(j0 + 16 * g) * D + 16 * tm + acc_row(0)]);
+                n[g][tm] = f32x4{nv.x, nv.y, nv.z, nv.w};
+            }
         }
     };
     fetch(chunk_of(0), mf[0], nf[0]);
     // X loads sit between the first and later fetches so that waiting for
     // them stays within the 63 outstanding loads the wait counter tracks.
-    f32x4 X[4];
+    f32x4 X[ACG][4];
 #pragma unroll
-    for (int tm = 0; tm < 4; ++tm)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            X[tm][i] = p.x0.data ? ld4<float>(p.x0, b, h, 16 * tm + acc_row(i), j) : 0.f;
-    fetch(chunk_of(min(1, p.nc - 1)), mf[1], nf[1]);
-    fetch(chunk_of(min(2, p.nc - 1)), mf[2], nf[2]);
-    uint16_t *xh = xs[0][0], *xl = xs[0][1];
-    if constexpr (NC > 0) {
-#pragma unroll
-        for (int s = 0; s < NC; ++s) {
-            if (s % 3 == 0) affine_step<0>(s, p, bh, j, X, mf, nf, xh, xl, fetch, chunk_of);
-            if (s % 3 == 1) affine_step<1>(s, p, bh, j, X, mf, nf, xh, xl, fetch, chunk_of);
-            if (s % 3 == 2) affine_step<2>(s, p, bh, j, X, mf, nf, xh, xl, fetch, chunk_of);
-        }
-    } else {
-        int s = 0;
-        for (; s + 2 < p.nc; s += 3) {  // whole ring turns
-            affine_step<0>(s, p, bh, j, X, mf, nf, xh, xl, fetch, chunk_of);
-            affine_step<1>(s + 1, p, bh, j, X, mf, nf, xh, xl, fetch, chunk_of);
-            affine_step<2>(s + 2, p, bh, j, X, mf, nf, xh, xl, fetch, chunk_of);
-        }
-        if (s < p.nc) affine_step<0>(s, p, bh, j, X, mf, nf, xh, xl, fetch, chunk_of);
-        if (s + 1 < p.nc) affine_step<1>(s + 1, p, bh, j, X, mf, nf, xh, xl, fetch, chunk_of);
-    }
-    if (p.xout)
+    for (int g = 0; g < ACG; ++g)
 #pragma unroll
         for (int tm = 0; tm < 4; ++tm)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                p.xout[((int64_t)bh * D + 16 * tm + acc_row(i)) * D + j] = X[tm][i];
+                X[g][tm][i] = p.x0.data ? ld4<float>(p.x0, b, h, 16 * tm + acc_row(i), j0 + 16 * g) : 0.f;
+    fetch(chunk_of(min(1, p.nc - 1)), mf[1], nf[1]);
+    fetch(chunk_of(min(2, p.nc - 1)), mf[2], nf[2]);
+    if constexpr (NC > 0) {
+#pragma unroll
+        for (int s = 0; s < NC; ++s) {
+            if (s % 3 == 0) affine_step<0>(s, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
+            if (s % 3 == 1) affine_step<1>(s, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
+            if (s % 3 == 2) affine_step<2>(s, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
+        }
+    } else {
+        int s = 0;
+        for (; s + 2 < p.nc; s += 3) {  // whole ring turns
+            affine_step<0>(s, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
+            affine_step<1>(s + 1, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
+            affine_step<2>(s + 2, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
+        }
+        if (s < p.nc) affine_step<0>(s, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
+        if (s + 1 < p.nc) affine_step<1>(s + 1, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
+    }
+    if (p.xout)
+#pragma unroll
+        for (int g = 0; g < ACG; ++g)
+#pragma unroll
+            for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    p.xout[((int64_t)bh * D + 16 * tm + acc_row(i)) * D + j0 + 16 * g] = X[g][tm][i];
 }
 
 // ---- out: outputs and scores of every chunk --------------------------------------
@@ -482,7 +502,7 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
 
 // Straight-line instantiations cover sequences up to 16 chunks (1024 tokens).
 static void launch_affine_scan(const AffineArgs &p, hipStream_t stream) {
-    const dim3 grid(32 * ((p.B * p.H + 7) / 8)), block(64);  // see affine_scan_kernel
+    const dim3 grid(8 * ANW * ((p.B * p.H + 7) / 8)), block(64);  // see affine_scan_kernel
     switch (p.nc) {
 #define GDN2_AFFINE_CASE(n) \
     case n: hipLaunchKernelGGL(affine_scan_kernel<n>, grid, block, 0, stream, p); return;
