@@ -10,8 +10,9 @@
 // columns, one workgroup each (grid = chunks x 2):
 //   prep   block vb: gates, A, T (block 0 writes them), W and U of block vb,
 //          and block vb's 64 columns of A_c and of B_c
-//   scan   four waves per (batch, head, 16 state columns); each wave owns a
-//          quarter of the 128 rows and the column block is shared through LDS
+//   scan   four waves per (batch, head, 32 state columns); each wave owns a
+//          quarter of the 128 rows of the map and applies them to both 16-column
+//          groups, whose bf16 operands are shared through LDS
 //   out    block vb: delta, O and |delta|^2 of the block's 64 value columns;
 //          a small kernel then forms the scores from both blocks' partials
 //   bprep  block vb: N of the adjoint map for the block's 64 value columns
