@@ -104,7 +104,8 @@ class _HolaRead(torch.autograd.Function):
         ds = torch.empty((q.shape[2],), dtype=torch.float32, device=q.device)
         nws = L.gdn2_hola_workspace_bytes(ctypes.byref(shape))
         ws = torch.empty((nws,), dtype=torch.uint8, device=q.device)
-        dov = _view(d_out.float() if d_out is not None else None)
+        d_out = d_out.float() if d_out is not None else None  # held until the launch
+        dov = _view(d_out)
         views = [_view(x) for x in (q, k, v, valid, documents, sink)]
         with torch.cuda.device(q.device):
             rc = L.gdn2_hola_backward(ctypes.byref(shape), *[ctypes.byref(x) for x in views],
