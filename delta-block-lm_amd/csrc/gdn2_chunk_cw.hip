@@ -155,13 +155,22 @@ __device__ __forceinline__ void pair_of(int p, bool strict, int &t, int &s) {
 }
 
 // Elementwise decay product of a token pair over 32 channels [32 half, +32):
-// sum_i x_t[i] exp(L_t[i] - L_s[i]) y_s[i] (f32 tiles, row stride LDL).
+// sum_i x_t[i] exp(L_t[i] - L_s[i]) y_s[i] (f32 tiles, row stride LDL).  Each
+// lane walks its 32 channels from its own starting offset (lane mod 32), so the
+// lanes of a half-wave, which read rows t and s of different pairs, spread over
+// the LDS banks instead of meeting in one (the two halves of a pair would
+// otherwise read words 32 apart: the same bank).
 __device__ __forceinline__ float pair_dot32(const float *x, const float *y, const float *L, int t,
                                             int s, int half) {
+    const int rot = lane_id() & 31;
+    const float *xt = x + t * LDL + 32 * half, *lt = L + t * LDL + 32 * half;
+    const float *ys = y + s * LDL + 32 * half, *ls = L + s * LDL + 32 * half;
     float acc = 0.f;
 #pragma unroll 8
-    for (int i = 32 * half; i < 32 * half + 32; ++i)
-        acc += x[t * LDL + i] * __expf(L[t * LDL + i] - L[s * LDL + i]) * y[s * LDL + i];
+    for (int j = 0; j < 32; ++j) {
+        const int i = (j + rot) & 31;
+        acc += xt[i] * __expf(lt[i] - ls[i]) * ys[i];
+    }
     return acc;
 }
 
