@@ -69,6 +69,13 @@ __device__ __forceinline__ void load4_f32(const View &v, int b, int tg, int h, i
     for (int e = 0; e < 4; ++e) o[e] = inb ? ld4<float>(v, b, tg, h, c0 + e) : fill;
 }
 
+// Padding tokens read as fill (the loads themselves are unconditional, so
+// they need not wait for the token's flags).
+__device__ __forceinline__ void mask4(float (&x)[4], bool on, float fill) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = on ? x[e] : fill;
+}
+
 __device__ __forceinline__ void put4_bf16(uint16_t *p, const float (&x)[4]) {
     *reinterpret_cast<uint2 *>(p) = make_uint2(bf16_pack2(x[0], x[1]), bf16_pack2(x[2], x[3]));
 }
@@ -225,11 +232,12 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a) {
     }
     const bool on = vld != 0.f;
     float kv[4], vv[4], al[4], er[4], wr[4];
-    load4_bf16(a.k, a.ks, b, tg, h, c0, inb && on, kv);
-    load4_bf16(a.v, a.vs, b, tg, h, c0, inb && on, vv);
-    load4_f32(a.alpha, b, tg, h, c0, inb && on, 1.f, al);
-    load4_f32(a.erase, b, tg, h, c0, inb && on, 0.f, er);
-    load4_f32(a.write, b, tg, h, c0, inb && on, 0.f, wr);
+    load4_bf16(a.k, a.ks, b, tg, h, c0, inb, kv);
+    load4_bf16(a.v, a.vs, b, tg, h, c0, inb, vv);
+    load4_f32(a.alpha, b, tg, h, c0, inb, 1.f, al);
+    load4_f32(a.erase, b, tg, h, c0, inb, 0.f, er);
+    load4_f32(a.write, b, tg, h, c0, inb, 0.f, wr);
+    mask4(kv, on, 0.f), mask4(vv, on, 0.f), mask4(al, on, 1.f), mask4(er, on, 0.f), mask4(wr, on, 0.f);
     {
         float la[4], eh[4], wv[4];
 #pragma unroll
@@ -411,11 +419,12 @@ __global__ void __launch_bounds__(NT4) cw_out_kernel(ChunkArgs a) {
     const int sg = gb->seg[t];
     const bool on = va != 0.f;
     float qv[4], kv[4], vv[4], er[4], wr[4], L[4];
-    load4_bf16(a.q, a.qs, b, tg, h, c0, inb && on, qv);
-    load4_bf16(a.k, a.ks, b, tg, h, c0, inb && on, kv);
-    load4_bf16(a.v, a.vs, b, tg, h, c0, inb && on, vv);
-    load4_f32(a.erase, b, tg, h, c0, inb && on, 0.f, er);
-    load4_f32(a.write, b, tg, h, c0, inb && on, 0.f, wr);
+    load4_bf16(a.q, a.qs, b, tg, h, c0, inb, qv);
+    load4_bf16(a.k, a.ks, b, tg, h, c0, inb, kv);
+    load4_bf16(a.v, a.vs, b, tg, h, c0, inb, vv);
+    load4_f32(a.erase, b, tg, h, c0, inb, 0.f, er);
+    load4_f32(a.write, b, tg, h, c0, inb, 0.f, wr);
+    mask4(qv, on, 0.f), mask4(kv, on, 0.f), mask4(vv, on, 0.f), mask4(er, on, 0.f), mask4(wr, on, 0.f);
     get4_f32(a.ck_lam + (int64_t)ci * CC * 64 + t * 64 + c0, L);
     {
         const uint16_t *S0 = a.ck_state + (int64_t)ci * 64 * 64;
@@ -597,15 +606,19 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a) {
     const int sg = gb->seg[t];
     const bool on = va != 0.f;
     float qv[4], kv[4], dov[4], er[4], L[4];
-    load4_bf16(a.q, a.qs, b, tg, h, c0, inb && on, qv);
-    load4_bf16(a.k, a.ks, b, tg, h, c0, inb && on, kv);
-    if (a.dout) load4_bf16(a.dout, a.ds, b, tg, h, c0, inb && on, dov);
+    load4_bf16(a.q, a.qs, b, tg, h, c0, inb, qv);
+    load4_bf16(a.k, a.ks, b, tg, h, c0, inb, kv);
+    if (a.dout) load4_bf16(a.dout, a.ds, b, tg, h, c0, inb, dov);
     else dov[0] = dov[1] = dov[2] = dov[3] = 0.f;
-    load4_f32(a.erase, b, tg, h, c0, inb && on, 0.f, er);
+    load4_f32(a.erase, b, tg, h, c0, inb, 0.f, er);
+    mask4(qv, on, 0.f), mask4(kv, on, 0.f), mask4(dov, on, 0.f), mask4(er, on, 0.f);
     get4_f32(a.ck_lam + (int64_t)ci * CC * 64 + t * 64 + c0, L);
     const float *dck = a.ck_delta + (int64_t)ci * CC * 64;
-    float dl4[4];
+    float dl4[4], dacc[4];
     get4_f32(dck + t * 64 + c0, dl4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)  // delta at this lane's accumulator positions (value tile w)
+        dacc[i] = a.dscores ? dck[acc_row(i) * 64 + 16 * w + acc_col()] : 0.f;
     load_t_split(a.ck_tf + (int64_t)ci * CC * CC, sm.tb, sm.tbl, tid);
     load_pt_split(a.ck_p + (int64_t)ci * CC * CC, sm.ptr, sm.ptrl, tid);
     {
@@ -657,8 +670,7 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a) {
         x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.ptrl, LDB, 0), db, x, 0, 0, 0);
         if (a.dscores) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                x[i] += sm.cs[acc_row(i)] * dck[acc_row(i) * 64 + 16 * w + acc_col()];
+            for (int i = 0; i < 4; ++i) x[i] += sm.cs[acc_row(i)] * dacc[i];
         }
         store_tile_t_split(&sm.xt[(16 * w) * LDW], &sm.xtl[(16 * w) * LDW], LDW, x);
     }
@@ -759,17 +771,34 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
     const int sg = gb->seg[t], sg15 = gb->seg[CC - 1];
     const bool on = va != 0.f;
     float qv[4], kv[4], vv[4], dov[4], er[4], wr[4], L[4], dl4[4];
-    load4_bf16(a.q, a.qs, b, tg, h, c0, inb && on, qv);
-    load4_bf16(a.k, a.ks, b, tg, h, c0, inb && on, kv);
-    load4_bf16(a.v, a.vs, b, tg, h, c0, inb && on, vv);
-    if (a.dout) load4_bf16(a.dout, a.ds, b, tg, h, c0, inb && on, dov);
+    load4_bf16(a.q, a.qs, b, tg, h, c0, inb, qv);
+    load4_bf16(a.k, a.ks, b, tg, h, c0, inb, kv);
+    load4_bf16(a.v, a.vs, b, tg, h, c0, inb, vv);
+    if (a.dout) load4_bf16(a.dout, a.ds, b, tg, h, c0, inb, dov);
     else dov[0] = dov[1] = dov[2] = dov[3] = 0.f;
-    load4_f32(a.erase, b, tg, h, c0, inb && on, 0.f, er);
-    load4_f32(a.write, b, tg, h, c0, inb && on, 0.f, wr);
+    load4_f32(a.erase, b, tg, h, c0, inb, 0.f, er);
+    load4_f32(a.write, b, tg, h, c0, inb, 0.f, wr);
+    mask4(qv, on, 0.f), mask4(kv, on, 0.f), mask4(vv, on, 0.f), mask4(dov, on, 0.f);
+    mask4(er, on, 0.f), mask4(wr, on, 0.f);
     const float *lck = a.ck_lam + (int64_t)ci * CC * 64;
     get4_f32(lck + t * 64 + c0, L);
     const float *dck = a.ck_delta + (int64_t)ci * CC * 64;
     get4_f32(dck + t * 64 + c0, dl4);
+    // Loads of phases 6 and 7, issued with the rest so that their latency is
+    // not exposed after a barrier: erase at this lane's accumulator positions
+    // (key tile w), and for wave 3 the alpha of channel tid - 192 at every token.
+    float eacc[4], dacc[4], alr[CC];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int tq = t0 + acc_row(e);
+        eacc[e] = tq < a.T ? ld4<float>(a.erase, b, tq, h, 16 * w + acc_col()) : 0.f;
+        dacc[e] = a.dscores ? dck[acc_row(e) * 64 + 16 * w + acc_col()] : 0.f;
+    }
+    if (w == 3 && a.dalpha) {
+#pragma unroll
+        for (int tt = 0; tt < CC; ++tt)
+            alr[tt] = t0 + tt < a.T ? ld4<float>(a.alpha, b, t0 + tt, h, tid - 192) : 1.f;
+    }
     {
         const int64_t so = (int64_t)ci * 64 * 64;
 #pragma unroll
@@ -872,7 +901,7 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
         x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.ptrl, LDB, 0), db, x, 0, 0, 0);
         if (a.dscores) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) x[e] += sm.cs[acc_row(e)] * dck[acc_row(e) * 64 + 16 * w + acc_col()];
+            for (int e = 0; e < 4; ++e) x[e] += sm.cs[acc_row(e)] * dacc[e];
         }
         store_tile_t_split(&g.ddt[(16 * w) * LDW], &g.ddtl[(16 * w) * LDW], LDW, x);
     }
@@ -996,7 +1025,7 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
             const float lt = sm.seg[tt] == sm.seg[CC - 1] ? __expf(L15 - Lt) : 0.f;
             const float q = bf16_val(sm.qb[tt * LDB + i]), k = bf16_val(sm.kb[tt * LDB + i]);
             const float eh = sm.ehf[tt * LDL + i];
-            const float ee = (von && tq < a.T) ? ld4<float>(a.erase, b, tq, h, i) : 0.f;
+            const float ee = von ? eacc[e] : 0.f;
             const float eA = seA[tt * LDL + i], qP = sqP[tt * LDL + i], kAP = skAP[tt * LDL + i];
             const float dq = bt * gqh[e] + qP;
             const float deh = bt * gah[e] + eA;
@@ -1028,13 +1057,14 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
         // every reset; the reset token's own alpha carries no gradient.
         const int i = tid - 192;
         float acc = 0.f;
+#pragma unroll
         for (int tt = CC - 1; tt >= 0; --tt) {
             acc += sm.dRf[tt * LDL + i];
             const int tq = t0 + tt;
             const bool von = sm.val[tt] != 0.f;
             const bool rs = von && (tt == 0 ? sm.seg[0] == 1 : sm.seg[tt] != sm.seg[tt - 1]);
             if (tq < a.T) {
-                const float al = von ? ld4<float>(a.alpha, b, tq, h, i) : 1.f;
+                const float al = von ? alr[tt] : 1.f;
                 const bool live = von && !rs && __logf(al) > LOG_FLOOR;
                 a.dalpha[(((int64_t)b * a.T + tq) * a.H + h) * 64 + i] = live ? acc / al : 0.f;
             }
