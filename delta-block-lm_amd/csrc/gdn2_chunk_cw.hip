@@ -737,7 +737,7 @@ struct CwBGradSmem {
     } rb;
     float cs[CC], ck[CC], val[CC];
     int seg[CC];
-    float tail[64], fr[64], bc[64];
+    float tail[64], fr[NW4][64], bc[64];
 };
 
 // T^T (from the f32 T checkpoint) into hi/lo LDS rows [s][t]; thread
@@ -865,13 +865,14 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
             gkt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.dlo, LDB, r), db, gkt, 0, 0, 0);
             gkt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hb, dbl, gkt, 0, 0, 0);
         }
-        if (tid < 64) {  // rowsum_v S0[i][v] dS[i][v] for key channel i = tid
+        {  // rowsum_v S0[i][v] dS[i][v], key channel i = tid % 64, rows v of quarter w
+            const int i = tid & 63;
             float f = 0.f;
 #pragma unroll 8
-            for (int v = 0; v < 64; ++v)
-                f += (bf16_val(st[v * LDB + tid]) + bf16_val(stl[v * LDB + tid])) *
-                     (bf16_val(dst[v * LDB + tid]) + bf16_val(dstl[v * LDB + tid]));
-            sm.fr[tid] = f;
+            for (int v = 16 * w; v < 16 * w + 16; ++v)
+                f += (bf16_val(st[v * LDB + i]) + bf16_val(stl[v * LDB + i])) *
+                     (bf16_val(dst[v * LDB + i]) + bf16_val(dstl[v * LDB + i]));
+            sm.fr[w][i] = f;
         }
     }
     {  // sum_s Ktil_s dKtil_s per key channel (f32 Ktil)
@@ -1031,7 +1032,8 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
             const float deh = bt * gah[e] + eA;
             const float dk = lt * gkt[e] + kAP + ee * deh + sm.ck[tt] * k;
             float dlam = eh * eA + q * qP - k * kAP + bt * eh * gah[e] + bt * q * gqh[e] - lt * k * gkt[e];
-            if (tt == CC - 1) dlam += sm.tail[i] + sm.bc[i] * sm.fr[i];
+            if (tt == CC - 1)
+                dlam += sm.tail[i] + sm.bc[i] * (sm.fr[0][i] + sm.fr[1][i] + sm.fr[2][i] + sm.fr[3][i]);
             gq[e] = von ? dq : 0.f;
             gk[e] = von ? dk : 0.f;
             sm.dRf[tt * LDL + i] = dlam;  // dR is dead: dLambda takes its place
