@@ -209,10 +209,10 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
 // (S_C = A S0 + B, c ascending, X0 = initial state) or backward
 // (dS0 = M dS_C + N, c descending, X0 = adjoint of the final state).  X before
 // each step goes to ckpt[c], transposed (X^T row-major) and rounded to bf16
-// (every consumer uses it as a bf16 MFMA operand).  Columns of X evolve independently, so each of the
-// four waves owns 16 columns; M fragments come straight from global memory
-// (prefetched one chunk ahead), X is re-packed through a wave-private LDS tile
-// into the bf16 hi/lo operand of the next product.
+// (every consumer uses it as a bf16 MFMA operand), with its lo part to ckpt_lo
+// when that is kept.  Columns of X evolve independently, so each of four
+// compute waves owns 16 columns; X is re-packed through LDS into the bf16
+// hi/lo operand of the next product.
 struct AffineArgs {
     int nc, B, H;
     const uint16_t *m;
@@ -223,143 +223,6 @@ struct AffineArgs {
     float *xout;      // [B,H,64,64] dense (may be null)
     int reverse;
 };
-
-constexpr int ACG = 1;            // column groups of 16 per scan wave (2 measured slower)
-constexpr int ANW = D / 16 / ACG;  // scan waves (workgroups) per head
-
-template <int SL, typename F, typename Gt>
-__device__ __forceinline__ void affine_step(int s, const AffineArgs &p, int bh, int j0,
-                                            f32x4 (&X)[ACG][4], bf16x8_t (&mf)[3][4][2],
-                                            f32x4 (&nf)[3][ACG][4], uint16_t (*xs)[2][16 * LDB],
-                                            F &fetch, Gt &chunk_of) {
-    const int c = chunk_of(s);
-    const int64_t co = ((int64_t)bh * p.nc + c) * D * D;
-#pragma unroll
-    for (int g = 0; g < ACG; ++g) {
-        const int j = j0 + 16 * g;
-#pragma unroll
-        for (int tm = 0; tm < 4; ++tm) {
-            *reinterpret_cast<uint2 *>(&p.ckpt[co + j * D + 16 * tm + acc_row(0)]) =
-                make_uint2(bf16_pack2(X[g][tm][0], X[g][tm][1]), bf16_pack2(X[g][tm][2], X[g][tm][3]));
-            if (p.ckpt_lo) {
-                float r[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) r[i] = X[g][tm][i] - bf16_val(bf16_bits(X[g][tm][i]));
-                *reinterpret_cast<uint2 *>(&p.ckpt_lo[co + j * D + 16 * tm + acc_row(0)]) =
-                    make_uint2(bf16_pack2(r[0], r[1]), bf16_pack2(r[2], r[3]));
-            }
-            store_tile_t_split(xs[g][0] + 16 * tm, xs[g][1] + 16 * tm, LDB, X[g][tm]);  // [col][row]
-        }
-    }
-    __syncthreads();
-    f32x4 Y[ACG][4];
-#pragma unroll
-    for (int g = 0; g < ACG; ++g)
-#pragma unroll
-        for (int tm = 0; tm < 4; ++tm) Y[g][tm] = nf[SL][g][tm];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-        for (int g = 0; g < ACG; ++g) {
-            const bf16x8_t bh_ = frag(xs[g][0], LDB, 32 * kk), bl_ = frag(xs[g][1], LDB, 32 * kk);
-#pragma unroll
-            for (int tm = 0; tm < 4; ++tm) {
-                Y[g][tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][tm][kk], bh_, Y[g][tm], 0, 0, 0);
-                Y[g][tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][tm][kk], bl_, Y[g][tm], 0, 0, 0);
-            }
-        }
-    }
-#pragma unroll
-    for (int g = 0; g < ACG; ++g)
-#pragma unroll
-        for (int tm = 0; tm < 4; ++tm) X[g][tm] = Y[g][tm];
-    // Unconditional (the last chunk again past the end), so that in the rolled
-    // loop every step issues the same loads and a slot's wait counts only the
-    // later steps' memory operations.
-    fetch(chunk_of(min(s + 3, p.nc - 1)), mf[SL], nf[SL]);
-    __syncthreads();
-}
-
-// One wave per workgroup: wave w of head bh owns the ACG groups of 16 state
-// columns from 16 ACG w, which evolve independently (Y = M X acts on
-// columns); one load of M's fragments serves all of them.  The ANW workgroups
-// of a head are spread over the CUs (the scan is bound by the loads each CU can
-// stream per step: a four-wave workgroup per head, sharing M through L1,
-// measured twice as slow).  Workgroups are dealt to the 8 XCDs round-robin by
-// index; the groups of a head take indices with equal residue mod 8, so they
-// share one XCD's L2.
-// NC > 0: the chunk count is a compile-time constant and the chunk loop is
-// straight-line code, so the loads of the three-deep (M, N) ring are waited
-// for one by one; NC == 0 runs any count in a rolled loop.
-template <int NC>
-__global__ void __launch_bounds__(64) affine_scan_kernel(AffineArgs p) {
-    __shared__ uint16_t xs[ACG][2][16 * LDB];
-    const int x = blockIdx.x, l = lane_id();
-    const int w = (x >> 3) % ANW, bh = (x & 7) + 8 * (x / (8 * ANW));
-    if (bh >= p.B * p.H) return;
-    const int b = bh / p.H, h = bh % p.H;
-    const int j0 = 16 * ACG * w + (l & 15);  // this lane's column in group 0
-    // Three chunks of (M, N) in flight: one global latency spans three steps.
-    bf16x8_t mf[3][4][2];
-    f32x4 nf[3][ACG][4];
-    auto chunk_of = [&](int s) { return p.reverse ? p.nc - 1 - s : s; };
-    auto fetch = [&](int c, bf16x8_t (&m)[4][2], f32x4 (&n)[ACG][4]) {
-        const int64_t ci = (int64_t)bh * p.nc + c;
-        const uint16_t *M = p.m + ci * D * D;
-        const float *N = p.n + ci * D * D;
-#pragma unroll
-        for (int tm = 0; tm < 4; ++tm) {
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk)
-                m[tm][kk] = __builtin_bit_cast(
-                    bf16x8_t, *reinterpret_cast<const uint4 *>(M + (16 * tm + (l & 15)) * D +
-                                                               32 * kk + 8 * (l >> 4)));
-#pragma unroll
-            for (int g = 0; g < ACG; ++g) {
-                const float4 nv = *reinterpret_cast<const float4 *>(&N[(j0 + 16 * g) * D + 16 * tm + acc_row(0)]);
-                n[g][tm] = f32x4{nv.x, nv.y, nv.z, nv.w};
-            }
-        }
-    };
-    fetch(chunk_of(0), mf[0], nf[0]);
-    // X loads sit between the first and later fetches so that waiting for
-    // them stays within the 63 outstanding loads the wait counter tracks.
-    f32x4 X[ACG][4];
-#pragma unroll
-    for (int g = 0; g < ACG; ++g)
-#pragma unroll
-        for (int tm = 0; tm < 4; ++tm)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                X[g][tm][i] = p.x0.data ? ld4<float>(p.x0, b, h, 16 * tm + acc_row(i), j0 + 16 * g) : 0.f;
-    fetch(chunk_of(min(1, p.nc - 1)), mf[1], nf[1]);
-    fetch(chunk_of(min(2, p.nc - 1)), mf[2], nf[2]);
-    if constexpr (NC > 0) {
-#pragma unroll
-        for (int s = 0; s < NC; ++s) {
-            if (s % 3 == 0) affine_step<0>(s, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
-            if (s % 3 == 1) affine_step<1>(s, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
-            if (s % 3 == 2) affine_step<2>(s, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
-        }
-    } else {
-        int s = 0;
-        for (; s + 2 < p.nc; s += 3) {  // whole ring turns
-            affine_step<0>(s, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
-            affine_step<1>(s + 1, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
-            affine_step<2>(s + 2, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
-        }
-        if (s < p.nc) affine_step<0>(s, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
-        if (s + 1 < p.nc) affine_step<1>(s + 1, p, bh, j0, X, mf, nf, xs, fetch, chunk_of);
-    }
-    if (p.xout)
-#pragma unroll
-        for (int g = 0; g < ACG; ++g)
-#pragma unroll
-            for (int tm = 0; tm < 4; ++tm)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    p.xout[((int64_t)bh * D + 16 * tm + acc_row(i)) * D + j0 + 16 * g] = X[g][tm][i];
-}
 
 // ---- out: outputs and scores of every chunk --------------------------------------
 __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
@@ -500,19 +363,168 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
     }
 }
 
-// Straight-line instantiations cover sequences up to 16 chunks (1024 tokens).
-static void launch_affine_scan(const AffineArgs &p, hipStream_t stream) {
-    const dim3 grid(8 * ANW * ((p.B * p.H + 7) / 8)), block(64);  // see affine_scan_kernel
-    switch (p.nc) {
-#define GDN2_AFFINE_CASE(n) \
-    case n: hipLaunchKernelGGL(affine_scan_kernel<n>, grid, block, 0, stream, p); return;
-        GDN2_AFFINE_CASE(1) GDN2_AFFINE_CASE(2) GDN2_AFFINE_CASE(3) GDN2_AFFINE_CASE(4)
-        GDN2_AFFINE_CASE(5) GDN2_AFFINE_CASE(6) GDN2_AFFINE_CASE(7) GDN2_AFFINE_CASE(8)
-        GDN2_AFFINE_CASE(9) GDN2_AFFINE_CASE(10) GDN2_AFFINE_CASE(11) GDN2_AFFINE_CASE(12)
-        GDN2_AFFINE_CASE(13) GDN2_AFFINE_CASE(14) GDN2_AFFINE_CASE(15) GDN2_AFFINE_CASE(16)
-#undef GDN2_AFFINE_CASE
-    default: hipLaunchKernelGGL(affine_scan_kernel<0>, grid, block, 0, stream, p);
+// One workgroup per (batch, head), seven waves:
+//   waves 0-3  compute: wave w owns state columns 16 w .. 16 w + 15;
+//   wave 4     streams the chunk maps M into an LDS ring with LDS-DMA loads
+//              (global_load_lds_dwordx4: lane L's 16 bytes land at the slot
+//              base + 16 L), PC_RING - 1 chunks ahead;
+//   wave 6     streams N the same way, PC_NRING - 1 chunks ahead;
+//   wave 5     copies each step's X^T tiles (hi, and lo when kept) from LDS to
+//              the checkpoint.
+// A wave's memory counter completes in order, so a scan wave that loaded its
+// own operands and stored its own checkpoint would wait for older checkpoint
+// stores whenever it waited for a prefetched operand, and could keep only
+// three chunks in flight within the counter's 63 operations.  Here the
+// compute waves issue no memory operations inside the loop, and each head's
+// map is read once per step instead of once per column group.  One workgroup
+// barrier per step: the producers pass it once that step's operands have
+// landed, the compute waves once their X^T tiles for the step are in LDS
+// (double-buffered by step parity, so the writer reads one buffer while the
+// next step fills the other).
+namespace {
+constexpr int PC_RING = 4;                 // LDS slots of M
+constexpr int PC_MOPS = D * D * 2 / 1024;  // LDS-DMA instructions per map (1 KiB each)
+constexpr int PC_NRING = 5;                // LDS slots of N
+constexpr int PC_NOPS = D * D * 4 / 1024;  // LDS-DMA instructions per N (1 KiB each)
+constexpr int PC_THREADS = 7 * 64;
+
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+struct PcSmem {
+    uint4 m[PC_RING][D * D / 8];      // M rows: 16-byte chunk x of row r holds chunk x ^ (r & 7)
+    uint4 n[PC_NRING][D * D / 4];     // N^T rows (f32): chunk x of column row j holds x ^ (j & 15)
+    uint16_t xs[2][4][2][16 * LDB];   // [step parity][compute wave][hi, lo]: X^T [col][row]
+};
+
+__device__ __forceinline__ void pc_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ void pc_step(int s, int j, int w, f32x4 (&X)[4], PcSmem &sm) {
+    const int l = lane_id();
+    uint16_t *xh = sm.xs[s & 1][w][0], *xl = sm.xs[s & 1][w][1];
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) store_tile_t_split(xh + 16 * tm, xl + 16 * tm, LDB, X[tm]);
+    pc_barrier();  // this step's map is in its slot; the writer may read X^T
+    const uint4 *slot = sm.m[s % PC_RING], *nslot = sm.n[s % PC_NRING];
+    f32x4 Y[4];
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+        const float4 nv = __builtin_bit_cast(float4, nslot[j * 16 + ((4 * tm + (l >> 4)) ^ (j & 15))]);
+        Y[tm] = f32x4{nv.x, nv.y, nv.z, nv.w};
     }
+    // hi and lo products accumulate separately: two dependent MFMAs per tile
+    f32x4 Z[4] = {zero4(), zero4(), zero4(), zero4()};
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+        const bf16x8_t bh_ = frag(xh, LDB, 32 * kk), bl_ = frag(xl, LDB, 32 * kk);
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) {
+            const int r = 16 * tm + (l & 15), q = 4 * kk + (l >> 4);
+            const bf16x8_t mf = __builtin_bit_cast(bf16x8_t, slot[r * 8 + (q ^ (r & 7))]);
+            Y[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf, bh_, Y[tm], 0, 0, 0);
+            Z[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf, bl_, Z[tm], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) X[tm][i] = Y[tm][i] + Z[tm][i];
+}
+}  // namespace
+
+__global__ void __launch_bounds__(PC_THREADS) affine_scan_pc_kernel(AffineArgs p) {
+    __shared__ PcSmem sm;
+    const int bh = blockIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
+    if (w == 4) {  // producer: the maps, PC_RING - 1 chunks ahead
+        typedef __attribute__((address_space(1))) const void *gptr;
+        typedef __attribute__((address_space(3))) void *lptr;
+        auto issue = [&](int s) {
+            const int sc = min(s, p.nc - 1), c = p.reverse ? p.nc - 1 - sc : sc;
+            const uint16_t *M = p.m + ((int64_t)bh * p.nc + c) * D * D;
+            uint4 *slot = sm.m[s % PC_RING];
+#pragma unroll
+            for (int i = 0; i < PC_MOPS; ++i) {
+                const int q = 64 * i + l, r = q >> 3, x = q & 7;
+                __builtin_amdgcn_global_load_lds((gptr)(M + r * D + 8 * (x ^ (r & 7))),
+                                                 (lptr)(slot + 64 * i), 16, 0, 0);
+            }
+        };
+        for (int s = 0; s < PC_RING - 1; ++s) issue(s);
+        for (int s = 0; s < p.nc; ++s) {
+            // map s has landed once no more than the PC_RING - 2 later maps are in flight
+            __builtin_amdgcn_s_waitcnt(vmcnt_only((PC_RING - 2) * PC_MOPS));
+            pc_barrier();
+            issue(s + PC_RING - 1);  // into the slot that step s - 1 read
+        }
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+        return;
+    }
+    if (w == 6) {  // producer: N, PC_NRING - 1 chunks ahead
+        typedef __attribute__((address_space(1))) const void *gptr;
+        typedef __attribute__((address_space(3))) void *lptr;
+        auto issue = [&](int s) {
+            const int sc = min(s, p.nc - 1), c = p.reverse ? p.nc - 1 - sc : sc;
+            const float *N = p.n + ((int64_t)bh * p.nc + c) * D * D;
+            uint4 *slot = sm.n[s % PC_NRING];
+#pragma unroll
+            for (int i = 0; i < PC_NOPS; ++i) {
+                const int q = 64 * i + l, jj = q >> 4, x = q & 15;
+                __builtin_amdgcn_global_load_lds((gptr)(N + jj * D + 4 * (x ^ (jj & 15))),
+                                                 (lptr)(slot + 64 * i), 16, 0, 0);
+            }
+        };
+        for (int s = 0; s < PC_NRING - 1; ++s) issue(s);
+        for (int s = 0; s < p.nc; ++s) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_only((PC_NRING - 2) * PC_NOPS));
+            pc_barrier();
+            issue(s + PC_NRING - 1);
+        }
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+        return;
+    }
+    if (w == 5) {  // writer: X^T before step s -> checkpoint of chunk c(s)
+        for (int s = 0; s < p.nc; ++s) {
+            pc_barrier();
+            const int c = p.reverse ? p.nc - 1 - s : s;
+            const int64_t co = ((int64_t)bh * p.nc + c) * D * D;
+#pragma unroll
+            for (int part = 0; part < 2; ++part) {
+                uint16_t *ck = part == 0 ? p.ckpt : p.ckpt_lo;
+                if (!ck) continue;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {  // 4 compute waves x 16 columns x 64 rows
+                    const int q = 64 * i + l, cw = q >> 7, col = (q >> 3) & 15, r8 = 8 * (q & 7);
+                    const uint4 v = *reinterpret_cast<const uint4 *>(&sm.xs[s & 1][cw][part][col * LDB + r8]);
+                    *reinterpret_cast<uint4 *>(&ck[co + (16 * cw + col) * D + r8]) = v;
+                }
+            }
+        }
+        return;
+    }
+    const int b = bh / p.H, h = bh % p.H;
+    const int j = 16 * w + (l & 15);  // this lane's state column
+    f32x4 X[4];
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            X[tm][i] = p.x0.data ? ld4<float>(p.x0, b, h, 16 * tm + acc_row(i), j) : 0.f;
+    for (int s = 0; s < p.nc; ++s) pc_step(s, j, w, X, sm);
+    if (p.xout)
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                p.xout[((int64_t)bh * D + 16 * tm + acc_row(i)) * D + j] = X[tm][i];
+}
+
+static void launch_affine_scan(const AffineArgs &p, hipStream_t stream) {
+    hipLaunchKernelGGL(affine_scan_pc_kernel, dim3(p.B * p.H), dim3(PC_THREADS), 0, stream, p);
 }
 
 // The scan over a.nc chunks of 64 x 64 maps held in ChunkArgs' per-chunk
