@@ -92,8 +92,9 @@ GDN2_API const char *gdn2_last_error(void);
  * it.  bf16 q/k/v with keys = values = 64, unit channel stride and 16-byte
  * aligned token rows run the 16-token chunk-WY MFMA kernels whatever the
  * chunk argument (alpha >= 0; log alpha is floored at -80, below which the
- * alpha gradient is zero); everything else runs the token-sequential
- * kernels.  On the chunk kernels d_output must have aligned rows too. */
+ * alpha gradient is zero: an underflowed gate alpha = 0 gets d_alpha = 0
+ * where the token-sequential kernels give the adjoint of the decayed state
+ * times that state); everything else runs the token-sequential kernels.  On the chunk kernels d_output must have aligned rows too. */
 GDN2_API size_t gdn2_training_checkpoint_bytes(const gdn2_shape *shape, int chunk);
 
 GDN2_API int gdn2_training_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q,

@@ -209,3 +209,48 @@ def test_scan_selected_reaches_mfma(dk):
     assert FWD_STAGES <= ran, sorted(ran)
     (o_out, _, _), _ = cw_oracle(p)
     gate("scan_selected output", r.output, o_out, TOL_BF16)
+
+
+@pytest.mark.parametrize("T", [1, 15, 17])
+def test_cw_short_sequences(dk, T):
+    """Fewer tokens than one chunk, and one token past it."""
+    p = cw_problem(300 + T, 2, T, 2, masks=False)
+    r, grads, ran = _run(dk, p)
+    assert FWD_STAGES | BWD_STAGES <= ran
+    _check(p, r, grads)
+
+
+def test_cw_all_padding_row_and_zero_keys(dk):
+    """A sequence that is padding throughout keeps its initial state and gets
+    zero gradients; zero key rows give zero scores (the zero subgradient of
+    |k| |delta|); alpha exactly 1 (no decay) on some channels."""
+    p = cw_problem(77, 2, 40, 2, masks=False)
+    p["valid"][1, :] = 0
+    p["k"][0, 5] = 0.0
+    p["k"][0, 21, 1] = 0.0
+    p["alpha"][0, 11, 1, 8:16] = 1.0
+    r, grads, ran = _run(dk, p)
+    assert FWD_STAGES | BWD_STAGES <= ran
+    og = _check(p, r, grads)
+    fin = r.final_state.detach().cpu().numpy()
+    # the scan carries states as a bf16 hi/lo pair: 16 significant bits
+    np.testing.assert_allclose(fin[1], p["initial"][1], rtol=2.0 ** -15, atol=1e-7)
+    assert np.all(r.scores.detach().cpu().numpy()[0, 5] == 0)
+    gate("d_initial (padded row passes dF)", grads["initial"][1], og["initial"][1], TOL_BF16)
+
+
+def test_cw_alpha_zero_is_floored(dk):
+    """alpha exactly 0 (an underflowed gate) on some channels: outputs, states
+    and every gradient but dalpha match the oracle; dalpha there is 0, the
+    documented floor of the log-domain gradient (log alpha < -80), where the
+    exact gradient is the pre-decay state adjoint times the state."""
+    p = cw_problem(78, 1, 40, 2, masks=False)
+    p["alpha"][0, 10, 0, :8] = 0.0
+    r, grads, ran = _run(dk, p)
+    assert FWD_STAGES | BWD_STAGES <= ran
+    og = _check(p, r, grads, skip=("alpha",))
+    da = grads["alpha"].double().cpu().numpy()
+    assert np.all(da[0, 10, 0, :8] == 0)
+    keep = np.ones(da.shape, bool)
+    keep[0, 10, 0, :8] = False
+    gate("dalpha (alpha > 0)", da[keep], og["alpha"][keep], TOL_BF16)
