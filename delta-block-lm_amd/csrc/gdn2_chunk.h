@@ -86,6 +86,10 @@ struct ChunkArgs {
     int doc;
     View doc_start, doc_end;
     float *dalpha, *derase, *dwrite;
+    // Factored chunk map (the scan of gdn2_chunk_lr.hip): -W'^T [D][C] and
+    // Ktil = lam K [C][D] (bf16), U^T [D][C] and the map's diagonal [D] (f32).
+    uint16_t *lr_wt, *lr_kt;
+    float *lr_u, *lr_gv;
 };
 
 inline bool chunk_eligible_shape(const gdn2_shape *s, int chunk) {
@@ -147,17 +151,19 @@ inline int64_t cw_chunk_count(int64_t B, int64_t T, int64_t H) {
 }
 
 // Checkpoint per chunk: S0^T (bf16 hi/lo, 64x64), T and P (f32 16x16), CwGate,
-// the cumulative log decay Lambda (f32 16x64), delta (f32 16x64), M = A_c^T and
-// A_c (bf16 64x64), B_c^T (f32 64x64).
+// the cumulative log decay Lambda (f32 16x64), delta (f32 16x64), and the
+// factored chunk map: -W'^T and Ktil (bf16 16x64), U^T (f32 16x64), b_15 (f32 64).
 constexpr size_t CWK_STATE = (size_t)CHUNK_D * CHUNK_D * 2;
 constexpr size_t CWK_T = (size_t)CW_C * CW_C * 4;
 constexpr size_t CWK_GATE = sizeof(CwGate);
 constexpr size_t CWK_LAM = (size_t)CW_C * CHUNK_D * 4;
 constexpr size_t CWK_DELTA = (size_t)CW_C * CHUNK_D * 4;
-constexpr size_t CWK_MAPM = (size_t)CHUNK_D * CHUNK_D * 2;
+constexpr size_t CWK_LRW = (size_t)CW_C * CHUNK_D * 2;
+constexpr size_t CWK_LRU = (size_t)CW_C * CHUNK_D * 4;
+constexpr size_t CWK_LRG = (size_t)CHUNK_D * 4;
 constexpr size_t CWK_MAPN = (size_t)CHUNK_D * CHUNK_D * 4;
-constexpr size_t CWK_CHUNK =
-    2 * CWK_STATE + 2 * CWK_T + CWK_GATE + CWK_LAM + CWK_DELTA + 2 * CWK_MAPM + CWK_MAPN;
+constexpr size_t CWK_CHUNK = 2 * CWK_STATE + 2 * CWK_T + CWK_GATE + CWK_LAM + CWK_DELTA + 2 * CWK_LRW +
+                             CWK_LRU + CWK_LRG;
 constexpr size_t CWW_CHUNK = 2 * CWK_STATE + CWK_MAPN;  // backward: dS^T (bf16 hi/lo), N^T (f32)
 
 inline size_t cw_checkpoint_bytes(int64_t B, int64_t T, int64_t H) {
@@ -184,11 +190,13 @@ inline void cw_bind_checkpoint(ChunkArgs &a, void *ck) {
     p += n * CWK_LAM;
     a.ck_delta = reinterpret_cast<float *>(p);
     p += n * CWK_DELTA;
-    a.ck_mt = reinterpret_cast<uint16_t *>(p);
-    p += n * CWK_MAPM;
-    a.map_m = reinterpret_cast<uint16_t *>(p);
-    p += n * CWK_MAPM;
-    a.map_n = reinterpret_cast<float *>(p);
+    a.lr_wt = reinterpret_cast<uint16_t *>(p);
+    p += n * CWK_LRW;
+    a.lr_kt = reinterpret_cast<uint16_t *>(p);
+    p += n * CWK_LRW;
+    a.lr_u = reinterpret_cast<float *>(p);
+    p += n * CWK_LRU;
+    a.lr_gv = reinterpret_cast<float *>(p);
 }
 
 inline void cw_bind_workspace(ChunkArgs &a, void *ws) {
@@ -200,7 +208,7 @@ inline void cw_bind_workspace(ChunkArgs &a, void *ws) {
 }
 
 // The affine scan over a.nc chunks of per-chunk 64 x 64 maps (gdn2_chunk.hip),
-// forward (state) or reverse (adjoint); shared with the channel-wise path.
+// forward (state) or reverse (adjoint).
 hipError_t launch_chunk_affine_scan(const ChunkArgs &a, bool reverse, hipStream_t stream);
 
 hipError_t launch_cw_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
@@ -215,17 +223,19 @@ inline bool wide_eligible_shape(const gdn2_shape *s, int chunk) {
 }
 
 // Checkpoint per chunk: S0^T (bf16 D x D), T (bf16 C x C), GateBlock, delta (f32
-// C x D), M = A_c^T and A_c (bf16 D x D), B_c^T (f32 D x D), |k|^2 and the value
-// blocks' |delta|^2 (f32 C each).
+// C x D), the factored chunk map (-W'^T and Ktil bf16 C x D, U^T f32 C x D, the
+// diagonal f32 D), |k|^2 and the value blocks' |delta|^2 (f32 C each).
 constexpr size_t WCK_STATE = (size_t)WIDE_D * WIDE_D * 2;
 constexpr size_t WCK_T = CK_T_BYTES;
 constexpr size_t WCK_GATE = CK_GATE_BYTES;
 constexpr size_t WCK_DELTA = (size_t)CHUNK * WIDE_D * 4;
-constexpr size_t WCK_MAPM = (size_t)WIDE_D * WIDE_D * 2;
+constexpr size_t WCK_LRW = (size_t)CHUNK * WIDE_D * 2;
+constexpr size_t WCK_LRU = (size_t)CHUNK * WIDE_D * 4;
+constexpr size_t WCK_LRG = (size_t)WIDE_D * 4;
 constexpr size_t WCK_MAPN = (size_t)WIDE_D * WIDE_D * 4;
 constexpr size_t WCK_NORM = (size_t)CHUNK * (1 + WIDE_NVB) * 4;
 constexpr size_t WCK_CHUNK =
-    WCK_STATE + WCK_T + WCK_GATE + WCK_DELTA + 2 * WCK_MAPM + WCK_MAPN + WCK_NORM;
+    WCK_STATE + WCK_T + WCK_GATE + WCK_DELTA + 2 * WCK_LRW + WCK_LRU + WCK_LRG + WCK_NORM;
 // Backward workspace per chunk: dS^T (bf16), N^T (f32), and the first value
 // block's dq/dk (f32 C x D each) and dbeta/dG (f32 C each) partials.
 constexpr size_t WWS_CHUNK = WCK_STATE + WCK_MAPN + 2 * (size_t)CHUNK * WIDE_D * 4 +
@@ -250,12 +260,14 @@ inline void wide_bind_checkpoint(ChunkArgs &a, void *ck) {
     p += n * WCK_GATE;
     a.ck_delta = reinterpret_cast<float *>(p);
     p += n * WCK_DELTA;
-    a.ck_mt = reinterpret_cast<uint16_t *>(p);
-    p += n * WCK_MAPM;
-    a.map_m = reinterpret_cast<uint16_t *>(p);
-    p += n * WCK_MAPM;
-    a.map_n = reinterpret_cast<float *>(p);
-    p += n * WCK_MAPN;
+    a.lr_wt = reinterpret_cast<uint16_t *>(p);
+    p += n * WCK_LRW;
+    a.lr_kt = reinterpret_cast<uint16_t *>(p);
+    p += n * WCK_LRW;
+    a.lr_u = reinterpret_cast<float *>(p);
+    p += n * WCK_LRU;
+    a.lr_gv = reinterpret_cast<float *>(p);
+    p += n * WCK_LRG;
     a.ck_kk = reinterpret_cast<float *>(p);
     a.ck_ddp = a.ck_kk + n * CHUNK;
 }
@@ -275,6 +287,25 @@ inline void wide_bind_workspace(ChunkArgs &a, void *ws) {
 
 hipError_t launch_wide_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
 hipError_t launch_wide_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
+
+// Factored affine scan (gdn2_chunk_lr.hip) over chunks of one (batch, head):
+//   forward  X_next = diag(gv) X + Ktil^T (U - W' X),   X0 = initial state
+//   reverse  X_prev = diag(gv) X + N - W'^T (Ktil X),   X0 = final-state adjoint
+// with X before each step to ckpt[c] (X^T, bf16 hi and, when ckpt_lo is set, lo).
+struct LrScanArgs {
+    int nc, B, H, vd;      // chunks per head, batch, heads, state columns
+    const uint16_t *wt;    // -W'^T per chunk [kd][ct] bf16
+    const uint16_t *kt;    // Ktil per chunk [ct][kd] bf16
+    const float *u;        // U^T per chunk [vd][ct] f32 (forward)
+    const float *n;        // N^T per chunk [vd][kd] f32 (reverse)
+    const float *gv;       // diagonal of the map per chunk [kd] f32
+    uint16_t *ckpt, *ckpt_lo;  // X^T per chunk [vd][kd] bf16
+    View x0;               // [B,H,kd,vd] strided (data may be null: zero)
+    float *xout;           // [B,H,kd,vd] dense (may be null)
+    int reverse;
+};
+// kd x ct in {128 x 64, 64 x 16}; hipErrorInvalidValue for other shapes.
+hipError_t launch_lr_scan(const LrScanArgs &p, int kd, int ct, hipStream_t stream);
 
 hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
 hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);

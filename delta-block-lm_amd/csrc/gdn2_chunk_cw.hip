@@ -18,10 +18,12 @@
 // Segments split the chunk at valid resets, as in gdn2_chunk.hip.  The decay
 // factors are elementwise per channel, so A and P (16 x 16, one exponential
 // per channel and token pair) are formed on the VALU; every product with the
-// state (R, delta, O, the maps and, in the backward, every state-sized
-// adjoint) runs on v_mfma_f32_16x16x32_bf16 with the 16-token reduction padded
-// to 32 by zero rows or columns.  The chunk maps feed the scalar path's affine
-// scan (gdn2_chunk.hip) over the T / 16 chunks.
+// state (R, delta, O, W', U and, in the backward, every state-sized adjoint)
+// runs on v_mfma_f32_16x16x32_bf16 with the 16-token reduction padded to 32 by
+// zero rows or columns.  The chunk map is rank 16 beside its diagonal, so it
+// leaves prep as its factors (-W'^T, Ktil, U^T, b_15: 8.25 KiB per chunk
+// against 24 KiB for A_c and B_c) for the factored scan of gdn2_chunk_lr.hip
+// over the T / 16 chunks.
 //
 // With document limits (the doc-limit op) a token is live when end >= start and
 // resets the state when start == t; the backward is the exact VJP of that
@@ -185,25 +187,23 @@ struct CwPrepSmem {
     float lam[CC * LDL];   // log alpha, then Lambda
     float eh[CC * LDL];    // e.k (f32)
     float kf[CC * LDL];    // k (bf16 values)
-    uint16_t ah[RT32];     // Ahat rows hi (rows 16..31 zero); with wv: A_c^T staging
+    uint16_t ah[RT32];     // Ahat rows hi (rows 16..31 zero)
     uint16_t wv[RT32];     // w.v rows hi (rows 16..31 zero)
     uint16_t ahl[RT32], wvl[RT32];  // lo parts
-    uint16_t kl[RT32], kll[RT32];   // Ktil rows hi/lo (rows 16..31 zero)
     uint16_t tb[RT16], tbl[RT16];   // T rows hi/lo (columns 16..31 zero)
-    uint16_t wt[4][CT64];  // W'^T hi/lo, U^T hi/lo ([channel][token])
     float af[CC * LDI], tf[CC * LDI];
-    float bc[64];
     float val[CC];
     int rs[CC], seg[CC];
 };
 
 }  // namespace
 
-// ---- prep: gates, A, T and the state map of every 16-token chunk --------------
+// ---- prep: gates, A, T and the factored state map of every 16-token chunk ------
+// The map S_16 = diag(b_15) S0 + Ktil^T (U - W' S0) leaves as its factors:
+// -W'^T and Ktil (bf16), U^T and b_15 (f32), for the scan of gdn2_chunk_lr.hip.
 __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a) {
     __shared__ CwPrepSmem sm;
-    static_assert(sizeof(sm.ah) + sizeof(sm.wv) >= 64 * LDB * 2, "A_c^T staging over ah, wv");
-    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = lane_id();
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid >> 4, c0 = 4 * (tid & 15), tg = c * CC + t;
     const bool inb = tg < a.T;
@@ -211,14 +211,10 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a) {
     zero_lds(sm.wv + RT16, RT32 - RT16, tid);
     zero_lds(sm.ahl + RT16, RT32 - RT16, tid);
     zero_lds(sm.wvl + RT16, RT32 - RT16, tid);
-    zero_lds(sm.kl + RT16, RT32 - RT16, tid);
-    zero_lds(sm.kll + RT16, RT32 - RT16, tid);
     for (int i = tid; i < CC * 16; i += NT4) {
         sm.tb[(i >> 4) * LDB + 16 + (i & 15)] = 0;
         sm.tbl[(i >> 4) * LDB + 16 + (i & 15)] = 0;
     }
-    for (int i = tid; i < 4 * 64 * 16; i += NT4)
-        sm.wt[i >> 10][((i >> 4) & 63) * LDW + 16 + (i & 15)] = 0;
     // Loads: token t, channels c0 .. c0 + 3.
     float vld = 0.f, rst = 0.f;
     if (inb && a.doc) {
@@ -274,7 +270,7 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a) {
         }
     }
     __syncthreads();
-    {  // Ahat and Ktil rows, b at the chunk end
+    {  // Ahat rows; Ktil rows and b at the chunk end (the map's diagonal) out
         const int sgt = sm.seg[t], sg15 = sm.seg[CC - 1];
         float ah[4], kl[4];
 #pragma unroll
@@ -282,10 +278,16 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a) {
             const float L = sm.lam[t * LDL + c0 + e], L15 = sm.lam[(CC - 1) * LDL + c0 + e];
             ah[e] = (sgt == 0 ? __expf(L) : 0.f) * sm.eh[t * LDL + c0 + e];
             kl[e] = (sgt == sg15 ? __expf(L15 - L) : 0.f) * kv[e];
-            if (t == CC - 1) sm.bc[c0 + e] = sg15 == 0 ? __expf(L15) : 0.f;
         }
         put4_split(&sm.ah[t * LDB + c0], &sm.ahl[t * LDB + c0], ah);
-        put4_split(&sm.kl[t * LDB + c0], &sm.kll[t * LDB + c0], kl);
+        *reinterpret_cast<uint2 *>(a.lr_kt + ((int64_t)ci * CC + t) * 64 + c0) =
+            make_uint2(bf16_pack2(kl[0], kl[1]), bf16_pack2(kl[2], kl[3]));
+        if (t == CC - 1) {
+            float bc[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bc[e] = sg15 == 0 ? __expf(sm.lam[(CC - 1) * LDL + c0 + e]) : 0.f;
+            put4_f32(a.lr_gv + (int64_t)ci * 64 + c0, bc);
+        }
     }
     {  // A (strictly lower, same segment): pair p on lanes 2p, 2p + 1 (channel halves)
         const int p = tid >> 1, half = tid & 1;
@@ -315,8 +317,9 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a) {
         put4_f32(a.ck_lam + (int64_t)ci * CC * 64 + t * 64 + c0, x4);
     }
     __syncthreads();
-    // W' = T Ahat, U = T wv (wave w: channel tile w), transposed hi/lo; products of
-    // hi/lo pairs keep three terms (hi hi, hi lo, lo hi).
+    // W' = T Ahat, U = T wv (wave w: channel tile w); products of hi/lo pairs keep
+    // three terms (hi hi, hi lo, lo hi).  Out from the accumulators: -W'^T (bf16)
+    // and U^T (f32), [channel][token].
     {
         const bf16x8_t ta = frag(sm.tb, LDB, 0), tal = frag(sm.tbl, LDB, 0);
         const bf16x8_t ab = frag_tr(sm.ah, 0, 16 * w), abl = frag_tr(sm.ahl, 0, 16 * w);
@@ -327,52 +330,9 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a) {
         f32x4 y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, vb, zero4(), 0, 0, 0);
         y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, vbl, y, 0, 0, 0);
         y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tal, vb, y, 0, 0, 0);
-        store_tile_t_split(&sm.wt[0][(16 * w) * LDW], &sm.wt[1][(16 * w) * LDW], LDW, x);
-        store_tile_t_split(&sm.wt[2][(16 * w) * LDW], &sm.wt[3][(16 * w) * LDW], LDW, y);
-    }
-    __syncthreads();
-    // A_c = diag(b_15) - Ktil^T W', B_c = Ktil^T U: wave w owns row tile w.
-    f32x4 am[4];
-    {
-        const bf16x8_t ka = frag_tr(sm.kl, 0, 16 * w);  // A[i][s] = Ktil[s][16 w + i]
-        const bf16x8_t kal = frag_tr(sm.kll, 0, 16 * w);
-        float *Bt = a.map_n + (int64_t)ci * 64 * 64;     // B_c^T [col][row]
-#pragma unroll
-        for (int tn = 0; tn < 4; ++tn) {
-            f32x4 x = zero4(), y = zero4();
-            const bf16x8_t wh = frag(&sm.wt[0][(16 * tn) * LDW], LDW, 0);
-            const bf16x8_t uh = frag(&sm.wt[2][(16 * tn) * LDW], LDW, 0);
-            x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, wh, x, 0, 0, 0);
-            x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, frag(&sm.wt[1][(16 * tn) * LDW], LDW, 0), x, 0, 0, 0);
-            x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kal, wh, x, 0, 0, 0);
-            y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, uh, y, 0, 0, 0);
-            y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, frag(&sm.wt[3][(16 * tn) * LDW], LDW, 0), y, 0, 0, 0);
-            y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kal, uh, y, 0, 0, 0);
-            const int cc = 16 * tn + acc_col();
-#pragma unroll
-            for (int i = 0; i < 4; ++i) am[tn][i] = (16 * w + acc_row(i) == cc ? sm.bc[cc] : 0.f) - x[i];
-            *reinterpret_cast<float4 *>(&Bt[cc * 64 + 16 * w + acc_row(0)]) = make_float4(y[0], y[1], y[2], y[3]);
-        }
-    }
-    __syncthreads();  // operand reads done: A_c^T goes over ah, wv
-    uint16_t *Mt = sm.ah;
-#pragma unroll
-    for (int tn = 0; tn < 4; ++tn) store_tile_t(&Mt[(16 * tn) * LDB + 16 * w], LDB, am[tn]);
-    __syncthreads();
-    {  // M = A_c^T rows, and A_c rows read across them
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int p = tid + NT4 * i, r = p >> 3, cb = 8 * (p & 7);
-            *reinterpret_cast<uint4 *>(a.ck_mt + (int64_t)ci * 64 * 64 + r * 64 + cb) =
-                *reinterpret_cast<const uint4 *>(&Mt[r * LDB + cb]);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int cr = 16 * w, r0 = 32 * i;
-            const bf16x8_t ar = frag_tr(Mt, r0, cr);  // A_c[cr + n][r0 + 8 g + e]
-            *reinterpret_cast<bf16x8_t *>(a.map_m + (int64_t)ci * 64 * 64 + (cr + (l & 15)) * 64 +
-                                          r0 + 8 * (l >> 4)) = ar;
-        }
+        const int64_t o = ((int64_t)ci * 64 + 16 * w + acc_col()) * CC + acc_row(0);
+        *reinterpret_cast<uint2 *>(a.lr_wt + o) = make_uint2(bf16_pack2(-x[0], -x[1]), bf16_pack2(-x[2], -x[3]));
+        *reinterpret_cast<float4 *>(a.lr_u + o) = make_float4(y[0], y[1], y[2], y[3]);
     }
 }
 
@@ -1079,13 +1039,47 @@ static inline void cmark(const hipEvent_t *ev, int i, hipStream_t stream) {
     if (ev) (void)hipEventRecord(ev[i], stream);
 }
 
+// The factored scan over a head's 16-token chunks: forward (states and their
+// lo parts, U of prep) or reverse (state adjoints and their lo parts, N of
+// bprep).
+static hipError_t cw_scan(const ChunkArgs &a, bool reverse, hipStream_t stream) {
+    LrScanArgs p{};
+    p.nc = a.nc;
+    p.B = a.B;
+    p.H = a.H;
+    p.vd = 64;
+    p.wt = a.lr_wt;
+    p.kt = a.lr_kt;
+    p.gv = a.lr_gv;
+    p.reverse = reverse ? 1 : 0;
+    if (!reverse) {
+        p.u = a.lr_u;
+        p.ckpt = a.ck_state;
+        p.ckpt_lo = a.ck_state_lo;
+        p.x0 = a.initial;
+        p.xout = a.final_state;
+    } else {
+        p.n = a.ws_n;
+        p.ckpt = a.ws_dstate;
+        p.ckpt_lo = a.ws_dstate_lo;
+        p.x0.data = a.dfinal;
+        p.x0.s0 = (int64_t)a.H * 64 * 64;
+        p.x0.s1 = 64 * 64;
+        p.x0.s2 = 64;
+        p.x0.s3 = 1;
+        p.xout = a.dinitial;
+    }
+    return launch_lr_scan(p, 64, CC, stream);
+}
+
 hipError_t launch_cw_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
     const int nch = a.B * a.H * a.nc;
     cmark(ev, 0, stream);
     hipLaunchKernelGGL(cw_prep_kernel, dim3(nch), dim3(NT4), 0, stream, a);
     cmark(ev, 1, stream);
     cmark(ev, 2, stream);
-    (void)launch_chunk_affine_scan(a, false, stream);
+    const hipError_t e = cw_scan(a, false, stream);
+    if (e != hipSuccess) return e;
     cmark(ev, 3, stream);
     cmark(ev, 4, stream);
     hipLaunchKernelGGL(cw_out_kernel, dim3(nch), dim3(NT4), 0, stream, a);
@@ -1099,7 +1093,8 @@ hipError_t launch_cw_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_
     hipLaunchKernelGGL(cw_bprep_kernel, dim3(nch), dim3(NT4), 0, stream, a);
     cmark(ev, 1, stream);
     cmark(ev, 2, stream);
-    (void)launch_chunk_affine_scan(a, true, stream);
+    const hipError_t e = cw_scan(a, true, stream);
+    if (e != hipSuccess) return e;
     cmark(ev, 3, stream);
     cmark(ev, 4, stream);
     hipLaunchKernelGGL(cw_bgrad_kernel, dim3(nch), dim3(NT4), 0, stream, a);

@@ -1,0 +1,365 @@
+// Factored affine scan over chunks on gfx950 MFMA.
+//
+// Every chunk-WY path here has a chunk map of the form
+//   S_next = diag(gv) S + Ktil^T (U - W' S)            (forward state)
+//   dS_prev = diag(gv) dS + N - W'^T (Ktil dS)         (state adjoint)
+// with Ktil = lam K and W' the chunk's CT x KD factors (A_c = diag(gv) -
+// Ktil^T W' has rank CT beside its diagonal), U = T (scaled V) the chunk's
+// CT x VD update and N the adjoint's additive term.  Streaming the factors
+// instead of the dense KD x KD map moves (2 KD CT + 4 VD CT) bytes per chunk
+// and head in place of (2 KD KD + 4 KD VD): for d = 128, C = 64 that is 64 KiB
+// instead of 96 KiB, and for the channel-wise 16-token chunks 8 KiB instead of
+// 24 KiB.  Both directions run two products per step,
+//   phase 1  V = Ad - Qm X        (CT x 16 per wave, reduction over KD)
+//   phase 2  X = gv X + Pm^T V + N (KD x 16 per wave, reduction over CT)
+// forward: Qm = -W', Pm = Ktil, Ad = U, N = 0; reverse: Qm = Ktil, Pm = -W',
+// Ad = 0, N from the backward prep (the checkpoint keeps -W', so no sign flips).
+//
+// Layout of the work: a workgroup owns NCW 16-column groups of one (batch,
+// head); its compute waves (one per group) keep their 16 columns of X in
+// MFMA accumulators for the whole scan.  An accumulator tile (lane (n, g)
+// holds rows 4g .. 4g + 3 of column n) is already a B operand of
+// v_mfma_f32_16x16x32_bf16 once two row tiles are paired into one reduction
+// slice (slot e < 4 -> row 4g + e of the first tile, e >= 4 -> row 4g + e - 4
+// of the second; the A operand reads the same rows), so X and V never leave
+// the registers: no LDS exchange and no barrier between the phases.  X and V
+// enter their products as bf16 hi/lo pairs.  Producer waves stream each
+// chunk's -W'^T [KD][CT], Ktil [CT][KD], U^T or N^T (the group's columns) and
+// gv into an LDS ring with LDS-DMA (global_load_lds_dwordx4: lane L's 16 bytes
+// land at the slot base + 16 L), R - 1 chunks ahead; one workgroup barrier per
+// step hands a slot from the producers to the compute waves.  The compute
+// waves issue no loads inside the loop, only their checkpoint stores (X before
+// each step, bf16 hi and optionally lo, transposed), so their memory counter
+// never holds them back.  Those stores pass through the wave's own LDS rows
+// [16 columns][KD] (written in accumulator layout, read back as 16-byte row
+// pieces), so each store instruction writes whole lines of eight columns
+// instead of 32-byte pieces of sixteen.
+//
+// LDS rows are swizzled by 16-byte chunk (chunk x of row r at x ^ lr_swz(r)),
+// so that the direct 8-byte fragment reads, the transpose reads and the
+// 16-byte f32 reads of every phase touch each bank once per pass.
+#include "gdn2_chunk.h"
+#include "gdn2_mfma.h"
+
+namespace gdn2 {
+
+namespace {
+
+typedef short lr_v4s __attribute__((ext_vector_type(4)));
+typedef short lr_v8s __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(1))) const void *lr_gptr;
+typedef __attribute__((address_space(3))) void *lr_lptr;
+
+// Stored chunk of logical 16-byte chunk x in row r of a tile with nch chunks
+// per row: x ^ lr_swz(r, nch).  With 64 four-byte banks, rows per 256 bytes
+// rpb = 16 / nch (1 for nch >= 16); the swizzle spreads 16 consecutive rows
+// (direct and 16-byte reads) and aligned groups of 8 rows x 32 bytes (transpose
+// reads) over distinct bank slots.
+__host__ __device__ constexpr int lr_swz(int r, int nch) {
+    return 2 * ((r / (nch >= 16 ? 1 : 16 / nch)) & ((nch < 16 ? nch : 16) / 2 - 1)) + ((r >> 3) & 1);
+}
+
+// Byte offset of element e (size es bytes) of row r in a swizzled tile.
+__device__ __forceinline__ int lr_off(int r, int e, int es, int nch) {
+    const int b = e * es;
+    return r * nch * 16 + (((b >> 4) ^ lr_swz(r, nch)) << 4) + (b & 15);
+}
+
+__device__ __forceinline__ void lr_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// s_waitcnt immediate that waits for vmcnt <= n only.
+constexpr int lr_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+__device__ __forceinline__ lr_v4s lr_tr16(const char *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) lr_v4s *)p);
+}
+
+__device__ __forceinline__ lr_v4s lr_ld8(const char *p) {
+    return __builtin_bit_cast(lr_v4s, *reinterpret_cast<const uint2 *>(p));
+}
+
+__device__ __forceinline__ bf16x8_t lr_cat(lr_v4s a, lr_v4s b) {
+    const lr_v8s v = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// hi and lo bf16 terms of the four values of an accumulator tile.
+__device__ __forceinline__ void lr_split(const f32x4 &x, lr_v4s &hi, lr_v4s &lo) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint16_t h, o;
+        split_bf16(x[i], h, o);
+        hi[i] = (short)h;
+        lo[i] = (short)o;
+    }
+}
+
+template <int KD_, int CT_, int NCW_, int NPROD_, int R_, bool BWD_, bool LO_>
+struct LrCfg {
+    static constexpr int KD = KD_, CT = CT_, NCW = NCW_, NPROD = NPROD_, R = R_;
+    static constexpr bool BWD = BWD_, LO = LO_;  // LO: the checkpoint keeps lo parts
+    static constexpr int WT_NCH = CT * 2 / 16;              // -W'^T [KD][CT] bf16
+    static constexpr int KT_NCH = KD * 2 / 16;              // Ktil [CT][KD] bf16
+    static constexpr int AUX_NCH = (BWD ? KD : CT) * 4 / 16;  // N^T [cols][KD] or U^T [cols][CT] f32
+    static constexpr int WT_BYTES = KD * CT * 2;
+    static constexpr int KT_BYTES = CT * KD * 2;
+    static constexpr int AUX_BYTES = NCW * 16 * AUX_NCH * 16;
+    static constexpr int GV_BYTES = 1024;                   // KD f32 (KD <= 256)
+    static constexpr int WT_OPS = WT_BYTES / 1024, KT_OPS = KT_BYTES / 1024, AUX_OPS = AUX_BYTES / 1024;
+    static constexpr int SLOT = WT_BYTES + KT_BYTES + AUX_BYTES + GV_BYTES;
+    static constexpr int XS_NCH = KD * 2 / 16;                  // X^T staging rows [16 cols][KD] bf16
+    static constexpr int XS_BYTES = 16 * KD * 2;                // one term (hi or lo)
+    static constexpr int LDS_BYTES = R * SLOT + NCW * (LO ? 2 : 1) * XS_BYTES;
+    // LDS-DMA operations each producer issues per chunk
+    static constexpr int OPS0 = NPROD == 1 ? WT_OPS + KT_OPS + AUX_OPS + 1 : WT_OPS;
+    static constexpr int OPS1 = NPROD == 1 ? 0 : KT_OPS;
+    static constexpr int OPS2 = NPROD == 1 ? 0 : AUX_OPS + 1;
+    static_assert(WT_BYTES % 1024 == 0 && KT_BYTES % 1024 == 0 && AUX_BYTES % 1024 == 0, "1 KiB DMA units");
+    static_assert(KD * 4 <= GV_BYTES, "gv fits one DMA unit");
+    static_assert(NPROD == 1 || NPROD == 3, "one producer, or one per stream");
+    static_assert((R - 1) * OPS0 <= 63 && (R - 1) * OPS1 <= 63 && (R - 1) * OPS2 <= 63,
+                  "prefetched chunks fit the memory counter");
+    static_assert(LDS_BYTES <= 160 * 1024, "ring and staging fit LDS");
+    static_assert(KD % 32 == 0 && (CT == 16 || CT % 32 == 0), "tile shapes");
+};
+
+}  // namespace
+
+template <class Cfg>
+__global__ void __launch_bounds__(64 * (Cfg::NCW + Cfg::NPROD)) lr_scan_kernel(LrScanArgs p) {
+    constexpr int KD = Cfg::KD, CT = Cfg::CT, NCW = Cfg::NCW, R = Cfg::R;
+    constexpr bool BWD = Cfg::BWD;
+    extern __shared__ __align__(1024) char lr_ring[];
+    const int x = blockIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
+    const int nwg = p.vd / (16 * NCW);
+    // Workgroup x -> (head bh, column block cg); the workgroups of a head take
+    // indices with equal residue mod 8, so they share one XCD's L2.
+    const int cg = (x >> 3) % nwg, bh = (x & 7) + 8 * (x / (8 * nwg));
+    if (bh >= p.B * p.H) return;
+    const int colbase = 16 * NCW * cg;
+    auto chunk_of = [&](int s) { return p.reverse ? p.nc - 1 - s : s; };
+    if (w >= NCW) {  // producers
+        const int pw = w - NCW;
+        auto dma_tile = [&](const char *src, int ops, int nch, char *dst) {
+#pragma unroll 4
+            for (int i = 0; i < ops; ++i) {
+                const int q = 64 * i + l, r = q / nch, y = q % nch;
+                __builtin_amdgcn_global_load_lds((lr_gptr)(src + r * nch * 16 + ((y ^ lr_swz(r, nch)) << 4)),
+                                                 (lr_lptr)(dst + 1024 * i), 16, 0, 0);
+            }
+        };
+        auto issue = [&](int s) {
+            const int sc = min(s, p.nc - 1);
+            const int64_t cix = (int64_t)bh * p.nc + chunk_of(sc);
+            char *slot = lr_ring + (s % R) * Cfg::SLOT;
+            if (Cfg::NPROD == 1 || pw == 0)
+                dma_tile(reinterpret_cast<const char *>(p.wt + cix * KD * CT), Cfg::WT_OPS, Cfg::WT_NCH, slot);
+            if (Cfg::NPROD == 1 || pw == 1)
+                dma_tile(reinterpret_cast<const char *>(p.kt + cix * CT * KD), Cfg::KT_OPS, Cfg::KT_NCH,
+                         slot + Cfg::WT_BYTES);
+            if (Cfg::NPROD == 1 || pw == 2) {
+                const float *aux = BWD ? p.n + (cix * p.vd + colbase) * KD : p.u + (cix * p.vd + colbase) * CT;
+                char *ax = slot + Cfg::WT_BYTES + Cfg::KT_BYTES;
+                dma_tile(reinterpret_cast<const char *>(aux), Cfg::AUX_OPS, Cfg::AUX_NCH, ax);
+                if (l < KD / 4)
+                    __builtin_amdgcn_global_load_lds((lr_gptr)(p.gv + cix * KD + 4 * l),
+                                                     (lr_lptr)(ax + Cfg::AUX_BYTES), 16, 0, 0);
+            }
+        };
+        for (int s = 0; s < R - 1; ++s) issue(s);
+        for (int s = 0; s < p.nc; ++s) {
+            // chunk s has landed once no more than the R - 2 later chunks are in flight
+            if (pw == 0) __builtin_amdgcn_s_waitcnt(lr_vmcnt(Cfg::OPS0 * (R - 2)));
+            else if (pw == 1) __builtin_amdgcn_s_waitcnt(lr_vmcnt(Cfg::OPS1 * (R - 2)));
+            else __builtin_amdgcn_s_waitcnt(lr_vmcnt(Cfg::OPS2 * (R - 2)));
+            lr_barrier();
+            issue(s + R - 1);  // into the slot that step s - 1 read
+        }
+        __builtin_amdgcn_s_waitcnt(lr_vmcnt(0));
+        return;
+    }
+    // compute wave w: state columns colbase + 16 w .. + 15
+    const int b = bh / p.H, h = bh % p.H, g = l >> 4, n = l & 15, j = colbase + 16 * w + n;
+    f32x4 X[KD / 16];
+#pragma unroll
+    for (int rt = 0; rt < KD / 16; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            X[rt][i] = p.x0.data ? ld4<float>(p.x0, b, h, 16 * rt + 4 * g + i, j) : 0.f;
+    for (int s = 0; s < p.nc; ++s) {
+        const int64_t cix = (int64_t)bh * p.nc + chunk_of(s);
+        // X before the step: B operands of phase 1, and X^T (bf16 hi, lo) through this
+        // wave's LDS rows [16 columns][KD] to the checkpoint in whole 16-byte pieces
+        // (eight lanes per column row), so each store instruction writes full lines.
+        bf16x8_t xh[KD / 32], xl[KD / 32];
+        char *xsw = lr_ring + R * Cfg::SLOT + w * (Cfg::LO ? 2 : 1) * Cfg::XS_BYTES;
+        constexpr bool lo_out = Cfg::LO;
+#pragma unroll
+        for (int kk = 0; kk < KD / 32; ++kk) {
+            lr_v4s h0, l0, h1, l1;
+            lr_split(X[2 * kk], h0, l0);
+            lr_split(X[2 * kk + 1], h1, l1);
+            xh[kk] = lr_cat(h0, h1);
+            xl[kk] = lr_cat(l0, l1);
+            *reinterpret_cast<lr_v4s *>(xsw + lr_off(n, 32 * kk + 4 * g, 2, Cfg::XS_NCH)) = h0;
+            *reinterpret_cast<lr_v4s *>(xsw + lr_off(n, 32 * kk + 16 + 4 * g, 2, Cfg::XS_NCH)) = h1;
+            if (lo_out) {
+                *reinterpret_cast<lr_v4s *>(xsw + Cfg::XS_BYTES + lr_off(n, 32 * kk + 4 * g, 2, Cfg::XS_NCH)) = l0;
+                *reinterpret_cast<lr_v4s *>(xsw + Cfg::XS_BYTES + lr_off(n, 32 * kk + 16 + 4 * g, 2, Cfg::XS_NCH)) = l1;
+            }
+        }
+        {
+            uint16_t *ck = p.ckpt + (cix * p.vd + colbase + 16 * w) * KD;
+            uint16_t *cl = lo_out ? p.ckpt_lo + (cix * p.vd + colbase + 16 * w) * KD : nullptr;
+#pragma unroll
+            for (int i = 0; i < Cfg::XS_BYTES / 1024; ++i) {
+                const int q = 64 * i + l, r = q / Cfg::XS_NCH, x = q % Cfg::XS_NCH;
+                const int off = r * Cfg::XS_NCH * 16 + ((x ^ lr_swz(r, Cfg::XS_NCH)) << 4);
+                *reinterpret_cast<uint4 *>(ck + 8 * q) = *reinterpret_cast<const uint4 *>(xsw + off);
+                if (lo_out)
+                    *reinterpret_cast<uint4 *>(cl + 8 * q) = *reinterpret_cast<const uint4 *>(xsw + Cfg::XS_BYTES + off);
+            }
+        }
+        lr_barrier();  // slot s has landed
+        const char *slot = lr_ring + (s % R) * Cfg::SLOT;
+        const char *wt = slot, *kt = slot + Cfg::WT_BYTES, *ax = kt + Cfg::KT_BYTES;
+        const float *gv = reinterpret_cast<const float *>(ax + Cfg::AUX_BYTES);
+        // Every LDS read of the step first (none depends on X or V), so their
+        // latencies overlap each other and the products.
+        constexpr int NP = CT >= 32 ? CT / 32 : 1;
+        bf16x8_t qa[CT / 16][KD / 32];  // phase 1 A operands (Qm)
+        bf16x8_t pa[KD / 16][NP];       // phase 2 A operands (Pm^T), CT >= 32
+        lr_v4s pa4[KD / 16];            // phase 2 A operands, CT = 16
+        f32x4 ad[CT / 16], nb[KD / 16], gq[KD / 16];
+#pragma unroll
+        for (int tt = 0; tt < CT / 16; ++tt)
+#pragma unroll
+            for (int kk = 0; kk < KD / 32; ++kk) {
+                if (BWD) {  // Qm = Ktil rows: token 16 tt + n, keys 32 kk + 4 g (+ 16)
+                    qa[tt][kk] = lr_cat(lr_ld8(kt + lr_off(16 * tt + n, 32 * kk + 4 * g, 2, Cfg::KT_NCH)),
+                                        lr_ld8(kt + lr_off(16 * tt + n, 32 * kk + 16 + 4 * g, 2, Cfg::KT_NCH)));
+                } else {  // Qm = -W' read across -W'^T rows (keys 32 kk + 4 g + e (+ 16), token 16 tt + n)
+                    const int r = 32 * kk + 4 * g + (n >> 2), e = 16 * tt + 4 * (n & 3);
+                    qa[tt][kk] = lr_cat(lr_tr16(wt + lr_off(r, e, 2, Cfg::WT_NCH)),
+                                        lr_tr16(wt + lr_off(r + 16, e, 2, Cfg::WT_NCH)));
+                }
+            }
+#pragma unroll
+        for (int rt = 0; rt < KD / 16; ++rt) {
+            if constexpr (CT >= 32) {
+#pragma unroll
+                for (int q = 0; q < NP; ++q) {
+                    if (BWD) {  // Pm = -W': -W'^T rows 16 rt + n, tokens 32 q + 4 g (+ 16)
+                        pa[rt][q] = lr_cat(lr_ld8(wt + lr_off(16 * rt + n, 32 * q + 4 * g, 2, Cfg::WT_NCH)),
+                                           lr_ld8(wt + lr_off(16 * rt + n, 32 * q + 16 + 4 * g, 2, Cfg::WT_NCH)));
+                    } else {  // Pm = Ktil read across its rows (tokens 32 q + 4 g + e (+ 16), key 16 rt + n)
+                        const int r = 32 * q + 4 * g + (n >> 2), e = 16 * rt + 4 * (n & 3);
+                        pa[rt][q] = lr_cat(lr_tr16(kt + lr_off(r, e, 2, Cfg::KT_NCH)),
+                                           lr_tr16(kt + lr_off(r + 16, e, 2, Cfg::KT_NCH)));
+                    }
+                }
+            } else {
+                if (BWD) pa4[rt] = lr_ld8(wt + lr_off(16 * rt + n, 4 * g, 2, Cfg::WT_NCH));
+                else pa4[rt] = lr_tr16(kt + lr_off(4 * g + (n >> 2), 16 * rt + 4 * (n & 3), 2, Cfg::KT_NCH));
+            }
+            const float4 gv4 = *reinterpret_cast<const float4 *>(gv + 16 * rt + 4 * g);
+            gq[rt] = f32x4{gv4.x, gv4.y, gv4.z, gv4.w};
+            if (BWD) {
+                const float4 nv = *reinterpret_cast<const float4 *>(ax + lr_off(16 * w + n, 16 * rt + 4 * g, 4,
+                                                                                Cfg::AUX_NCH));
+                nb[rt] = f32x4{nv.x, nv.y, nv.z, nv.w};
+            }
+        }
+        if (!BWD)
+#pragma unroll
+            for (int tt = 0; tt < CT / 16; ++tt) {
+                const float4 u = *reinterpret_cast<const float4 *>(ax + lr_off(16 * w + n, 16 * tt + 4 * g, 4,
+                                                                               Cfg::AUX_NCH));
+                ad[tt] = f32x4{u.x, u.y, u.z, u.w};
+            }
+        // phase 1: V = Ad - Qm X (token tiles tt)
+        f32x4 V[CT / 16];
+#pragma unroll
+        for (int tt = 0; tt < CT / 16; ++tt) V[tt] = BWD ? zero4() : ad[tt];
+#pragma unroll
+        for (int kk = 0; kk < KD / 32; ++kk)
+#pragma unroll
+            for (int tt = 0; tt < CT / 16; ++tt) {
+                V[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[tt][kk], xh[kk], V[tt], 0, 0, 0);
+                V[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[tt][kk], xl[kk], V[tt], 0, 0, 0);
+            }
+        // phase 2: X = gv X + Pm^T V + N (row tiles rt)
+        bf16x8_t vh[NP], vl[NP];
+        lr_v4s vh4 = {0, 0, 0, 0}, vl4 = {0, 0, 0, 0};
+        if constexpr (CT >= 32) {
+#pragma unroll
+            for (int q = 0; q < NP; ++q) {
+                lr_v4s h0, l0, h1, l1;
+                lr_split(V[2 * q], h0, l0);
+                lr_split(V[2 * q + 1], h1, l1);
+                vh[q] = lr_cat(h0, h1);
+                vl[q] = lr_cat(l0, l1);
+            }
+        } else {
+            lr_split(V[0], vh4, vl4);
+        }
+#pragma unroll
+        for (int rt = 0; rt < KD / 16; ++rt) {
+            f32x4 acc;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = gq[rt][i] * X[rt][i] + (BWD ? nb[rt][i] : 0.f);
+            if constexpr (CT >= 32) {
+#pragma unroll
+                for (int q = 0; q < NP; ++q) {
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[rt][q], vh[q], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[rt][q], vl[q], acc, 0, 0, 0);
+                }
+            } else {  // 16 tokens: one 16x16x16 product per term
+                acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa4[rt], vh4, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa4[rt], vl4, acc, 0, 0, 0);
+            }
+            X[rt] = acc;
+        }
+    }
+    if (p.xout)
+#pragma unroll
+        for (int rt = 0; rt < KD / 16; ++rt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                p.xout[((int64_t)bh * KD + 16 * rt + 4 * g + i) * p.vd + j] = X[rt][i];
+}
+
+template <class Cfg>
+static hipError_t launch_lr(const LrScanArgs &p, hipStream_t stream) {
+    const int nwg = p.vd / (16 * Cfg::NCW);
+    const dim3 grid(8 * nwg * ((p.B * p.H + 7) / 8)), block(64 * (Cfg::NCW + Cfg::NPROD));
+    const size_t lds = (size_t)Cfg::LDS_BYTES;
+    static bool attr_set = false;  // the kernel's dynamic LDS limit, set once per process
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute((const void *)lr_scan_kernel<Cfg>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(lr_scan_kernel<Cfg>, grid, block, lds, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_lr_scan(const LrScanArgs &p, int kd, int ct, hipStream_t stream) {
+    if (p.vd % 16 != 0) return hipErrorInvalidValue;
+    // d = 128 keeps bf16 hi only, the 16-token chunks hi and lo
+    if ((kd == 128) != (p.ckpt_lo == nullptr)) return hipErrorInvalidValue;
+    if (kd == 128 && ct == 64 && p.vd % 32 == 0)
+        return p.reverse ? launch_lr<LrCfg<128, 64, 2, 3, 3, true, false>>(p, stream)
+                         : launch_lr<LrCfg<128, 64, 2, 3, 3, false, false>>(p, stream);
+    if (kd == 64 && ct == 16 && p.vd % 16 == 0)
+        return p.reverse ? launch_lr<LrCfg<64, 16, 1, 1, 6, true, true>>(p, stream)
+                         : launch_lr<LrCfg<64, 16, 1, 1, 8, false, true>>(p, stream);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace gdn2

@@ -3,23 +3,25 @@
 // The chunk form is that of gdn2_chunk.hip (per chunk of C = 64 tokens with
 // start state S0: A = strict_lower(beta_t Gam_ts k_t.k_s), T = (I + A)^-1,
 // R = diag(beta)(V - diag(gam) K S0), delta = T R, O = diag(gam) Q S0 +
-// (Gam .* Q K^T) delta, S_C = A_c S0 + B_c with A_c = gam_63 I - (lam K)^T W,
-// B_c = (lam K)^T U, W = T diag(beta gam) K, U = T diag(beta) V).  Key-side
-// products reduce over all D = 128 key channels; value columns evolve
-// independently, so every value-side product is cut into value blocks of 64
-// columns, one workgroup each (grid = chunks x 2):
-//   prep   block vb: gates, A, T (block 0 writes them), W and U of block vb,
-//          and block vb's 64 columns of A_c and of B_c
-//   scan   four waves per (batch, head, 32 state columns); each wave owns a
-//          quarter of the 128 rows of the map and applies them to both 16-column
-//          groups, whose bf16 operands are shared through LDS
+// (Gam .* Q K^T) delta, S_C = gam_63 S0 + Ktil^T (U - W S0) with Ktil = lam K,
+// W = T diag(beta gam) K, U = T diag(beta) V).  Key-side products reduce over
+// all D = 128 key channels; value columns evolve independently, so every
+// value-side product is cut into value blocks of 64 columns, one workgroup
+// each (grid = chunks x 2):
+//   prep   block vb: gates, A, T (block 0 writes them), and the chunk map's
+//          factors: block vb's 64 key columns of -W^T and Ktil, 64 value
+//          columns of U^T
+//   scan   the factored scan of gdn2_chunk_lr.hip (the map is rank 64 beside
+//          its diagonal, so its factors are 64 KiB per chunk against 96 KiB
+//          for A_c and B_c)
 //   out    block vb: delta, O and |delta|^2 of the block's 64 value columns;
 //          a small kernel then forms the scores from both blocks' partials
 //   bprep  block vb: N of the adjoint map for the block's 64 value columns
 //   bgrad  two launches: block 0 leaves its dq, dk, dbeta, dG partials in the
 //          workspace, block 1 adds its own and writes the gradients
 // Precision follows gdn2_chunk.hip: R, delta, P, dd, dP, W, U and the scan's X
-// enter their products as bf16 hi + lo pairs; S0, T, Q, K, V, dS as bf16.
+// and V enter their products as bf16 hi + lo pairs; S0, T, Q, K, V, dS and the
+// scan's -W and Ktil as bf16, U as f32.
 #include "gdn2_chunk_tile.h"
 
 namespace gdn2 {
@@ -108,31 +110,29 @@ __device__ __forceinline__ void put_mat2(uint16_t *tile, const Mat2 &m, int tid)
 }
 
 struct WPrepSmem {
-    uint16_t ks[KTILE];    // K rows; T (bf16, row stride LDB) once A is formed; then the
-                           // block's A_c^T rows [64][KD] for the row stores
-    uint16_t kl[KTILE];    // lam K rows
+    uint16_t ks[KTILE];    // K rows; T (bf16, row stride LDB) once A is formed
     uint16_t kbg[TILE];    // beta gam K rows, key columns of block vb
     uint16_t vbt[TILE];    // beta V rows, value columns of block vb
-    union {
-        struct {
-            float Af[C * LDF];
-            float Tf[C * LDF];
-        } inv;
-        uint16_t wu[4][TILE];  // W^T hi/lo, U^T hi/lo of block vb
-    } u;
+    struct {
+        float Af[C * LDF];
+        float Tf[C * LDF];
+    } inv;
     GateLds gl;
 };
 
 }  // namespace
 
-// ---- prep: gates, the UT inverse and block vb of the chunk's state map ---------
+// ---- prep: gates, the UT inverse and block vb of the chunk's factored map -------
+// The chunk map S_C = gam_63 S0 + Ktil^T (U - W S0) (Ktil = lam K, W = T diag(beta
+// gam) K, U = T diag(beta) V) leaves as its factors: block vb writes its 64 key
+// columns of -W^T and of Ktil, its 64 value columns of U^T, and block 0 the gate
+// block, T and the diagonal gam_63.
 __global__ void __launch_bounds__(NT) wide_prep_kernel(ChunkArgs a) {
     __shared__ WPrepSmem sm;
     int ci, vb;
     if (!chunk_block(blockIdx.x, a.B * a.H * a.nc, ci, vb)) return;
-    uint16_t *Ks = sm.ks, *KLs = sm.kl, *KBGs = sm.kbg, *VBs = sm.vbt;
+    uint16_t *Ks = sm.ks, *KBGs = sm.kbg, *VBs = sm.vbt;
     uint16_t *Tb = sm.ks;  // over K once A is formed
-    uint16_t *Wt = sm.u.wu[0], *Wtl = sm.u.wu[1], *Ut = sm.u.wu[2], *Utl = sm.u.wu[3];
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tg = c * C + t;
@@ -165,11 +165,12 @@ __global__ void __launch_bounds__(NT) wide_prep_kernel(ChunkArgs a) {
         }
     }
     __syncthreads();
-    {  // scaled rows: lam K (all key channels), beta gam K (key block vb)
-        const float bg = sm.gl.beta[t] * sm.gl.gam[t], la = sm.gl.lam[t];
-#pragma unroll
-        for (int i = 0; i < NKB; ++i) put_row8(KLs, t, cb + 8 * i, scale8(k8.p[i], la), LDK);
+    {  // beta gam K (key block vb) staged; Ktil = lam K (key block vb) and the diagonal out
+        const float bg = sm.gl.beta[t] * sm.gl.gam[t];
         put_row8(KBGs, t, cb, scale8(piece(k8, vb), bg));
+        *reinterpret_cast<uint4 *>(a.lr_kt + ((int64_t)ci * C + t) * KD + 64 * vb + 8 * cb) =
+            scale8(piece(k8, vb), sm.gl.lam[t]);
+        if (vb == 0 && tid < KD) a.lr_gv[(int64_t)ci * KD + tid] = sm.gl.gamC;
     }
     // A = strict_lower(beta_t Gam_ts k_t.k_s) in f32 (tiles with tn <= tm only).
     if (tn0 <= tm) {
@@ -184,22 +185,22 @@ __global__ void __launch_bounds__(NT) wide_prep_kernel(ChunkArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tt = 16 * tm + acc_row(i);
-                sm.u.inv.Af[tt * LDF + ss] = (ss < tt && rg.seg[i] == sgs)
-                                                 ? rg.beta[i] * __expf(rg.G[i] - Gs) * kk[j][i]
-                                                 : 0.f;
+                sm.inv.Af[tt * LDF + ss] = (ss < tt && rg.seg[i] == sgs)
+                                               ? rg.beta[i] * __expf(rg.G[i] - Gs) * kk[j][i]
+                                               : 0.f;
             }
         }
     }
     __syncthreads();
-    ut_inverse(sm.u.inv.Af, sm.u.inv.Tf, w);
+    ut_inverse(sm.inv.Af, sm.inv.Tf, w);
     {  // T (bf16, row-major, zero above the diagonal): LDS operand and checkpoint
         const int r = tid >> 3, c0 = 8 * (tid & 7);
         uint32_t pk[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int s0 = c0 + 2 * e;
-            pk[e] = bf16_pack2(s0 <= r ? sm.u.inv.Tf[r * LDF + s0] : 0.f,
-                               s0 + 1 <= r ? sm.u.inv.Tf[r * LDF + s0 + 1] : 0.f);
+            pk[e] = bf16_pack2(s0 <= r ? sm.inv.Tf[r * LDF + s0] : 0.f,
+                               s0 + 1 <= r ? sm.inv.Tf[r * LDF + s0 + 1] : 0.f);
         }
         const uint4 v = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         if (vb == 0) *reinterpret_cast<uint4 *>(a.ck_t + (int64_t)ci * C * C + r * C + c0) = v;
@@ -207,213 +208,20 @@ __global__ void __launch_bounds__(NT) wide_prep_kernel(ChunkArgs a) {
     }
     put_row8(VBs, t, cb, scale8(v8, sm.gl.beta[t]));
     __syncthreads();
-    // W_vb = T (beta gam K)[:, block vb], U_vb = T (beta V_vb): transposed hi/lo.
+    // W_vb = T (beta gam K)[:, block vb], U_vb = T (beta V_vb), straight from the
+    // accumulators: -W^T (bf16) and U^T (f32), [column][token].
     {
         f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
         gemm2_tr(x, &Tb[(16 * tm) * LDB], KBGs, tn0);
         gemm2_tr(y, &Tb[(16 * tm) * LDB], VBs, tn0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            store_tile_t_split(&Wt[(16 * (tn0 + j)) * LDB + 16 * tm],
-                               &Wtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
-            store_tile_t_split(&Ut[(16 * (tn0 + j)) * LDB + 16 * tm],
-                               &Utl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, y[j]);
+            const int64_t o = ((int64_t)ci * KD + 64 * vb + 16 * (tn0 + j) + acc_col()) * C + 16 * tm + acc_row(0);
+            *reinterpret_cast<uint2 *>(a.lr_wt + o) =
+                make_uint2(bf16_pack2(-x[j][0], -x[j][1]), bf16_pack2(-x[j][2], -x[j][3]));
+            *reinterpret_cast<float4 *>(a.lr_u + o) = make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
         }
     }
-    __syncthreads();
-    // Columns of block vb: A_c[:, vb] = gam_63 I[:, vb] - (lam K)^T W_vb (bf16; its
-    // transpose staged in LDS), B_c[:, vb] = (lam K)^T U_vb (f32, stored transposed).
-    {
-        const float gC = sm.gl.gamC;
-        uint16_t *Mt = sm.ks;  // [64 block columns][KD rows]; T is dead
-        float *Bt = a.map_n + (int64_t)ci * KD * KD;
-#pragma unroll
-        for (int rb = 0; rb < NKB; ++rb) {
-            const int mt = tm + 4 * rb;  // row tile of A_c / B_c (key channel)
-            f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
-            gemm2_atr<64, LDK, LDB>(x, KLs, 16 * mt, Wt, tn0);  // A[k][t] = (lam K)[t][k]
-            gemm2_atr<64, LDK, LDB>(x, KLs, 16 * mt, Wtl, tn0);
-            gemm2_atr<64, LDK, LDB>(y, KLs, 16 * mt, Ut, tn0);
-            gemm2_atr<64, LDK, LDB>(y, KLs, 16 * mt, Utl, tn0);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int cl = 16 * (tn0 + j) + acc_col();  // column within the block
-                f32x4 am;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    am[i] = (16 * mt + acc_row(i) == 64 * vb + cl ? gC : 0.f) - x[j][i];
-                store_tile_t(&Mt[(16 * (tn0 + j)) * LDK + 16 * mt], LDK, am);
-                *reinterpret_cast<float4 *>(&Bt[(64 * vb + cl) * KD + 16 * mt + acc_row(0)]) =
-                    make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
-            }
-        }
-    }
-    __syncthreads();
-    // Rows out: M = A_c^T rows 64 vb .. 64 vb + 63 (whole rows), and A_c's block
-    // columns read across them (16-byte pieces of A_c rows).
-    {
-        const uint16_t *Mt = sm.ks;
-        const int l = lane_id();
-#pragma unroll
-        for (int i = 0; i < NKB; ++i) {
-            const int p = tid + NT * i, r = p / (KD / 8), c0 = 8 * (p % (KD / 8));
-            *reinterpret_cast<uint4 *>(a.ck_mt + (int64_t)ci * KD * KD + (64 * vb + r) * KD + c0) =
-                *reinterpret_cast<const uint4 *>(&Mt[r * LDK + c0]);
-        }
-#pragma unroll
-        for (int i = 0; i < NKB; ++i) {
-            const int c0 = 16 * ((w & 3) + 4 * i), r0 = 32 * (w >> 2);
-            const bf16x8_t ar = frag_tr<LDK>(Mt, r0, c0);  // A_c[c0 + n][64 vb + r0 + 8 g + e]
-            *reinterpret_cast<bf16x8_t *>(a.map_m + (int64_t)ci * KD * KD + (c0 + (l & 15)) * KD +
-                                          64 * vb + r0 + 8 * (l >> 4)) = ar;
-        }
-    }
-}
-
-// ---- affine scan over chunks (d = 128) -------------------------------------------
-// X_next = M_c X + N_c per chunk of one (batch, head), forward (states, M = A_c,
-// N = B_c) or reverse (state adjoints, M = A_c^T, N from bprep).  Columns of X
-// evolve independently: a workgroup owns 16 of them, and its four waves own a
-// quarter of the 128 rows each.  Per step every wave writes its rows of X
-// (bf16 hi/lo, transposed) to a double-buffered LDS block, one barrier, then
-// multiplies its rows of M (registers, three chunks ahead) against the whole
-// 128 x 16 block.  X before each step goes to ckpt[c] as X^T in bf16.
-namespace {
-constexpr int SW = 4;               // waves per scan workgroup
-constexpr int SRT = KD / 16 / SW;   // row tiles per wave
-constexpr int SKS = KD / 32;        // reduction steps of a 16x16x32 product
-constexpr int LDX = KD + 8;
-constexpr int NCG = KD / 16;        // 16-column groups per state
-constexpr int CPW = 2;              // column groups per workgroup (one M load serves both)
-constexpr int NWG = NCG / CPW;      // workgroups per head
-}  // namespace
-
-struct WScanArgs {
-    int nc, B, H;
-    const uint16_t *m;   // [chunk][KD][KD] bf16 row-major
-    const float *n;      // [chunk][KD cols][KD rows] f32 (N^T)
-    uint16_t *ckpt;      // [chunk][KD cols][KD rows] bf16 (X^T)
-    View x0;             // [B,H,KD,KD] strided (data may be null: zero)
-    float *xout;         // [B,H,KD,KD] dense (may be null)
-    int reverse;
-};
-
-template <int SL, typename F, typename Gt>
-__device__ __forceinline__ void wscan_step(int s, const WScanArgs &p, int bh, int j0, int w,
-                                           f32x4 (&X)[CPW][SRT], bf16x8_t (&mf)[3][SRT][SKS],
-                                           f32x4 (&nf)[3][CPW][SRT],
-                                           uint16_t (*xs)[CPW][2][16 * LDX], F &fetch,
-                                           Gt &chunk_of) {
-    const int c = chunk_of(s);
-    uint16_t *ck = p.ckpt + ((int64_t)bh * p.nc + c) * KD * KD;
-#pragma unroll
-    for (int g = 0; g < CPW; ++g) {
-        const int j = j0 + 16 * g;
-#pragma unroll
-        for (int rt = 0; rt < SRT; ++rt) {
-            const int mt = SRT * w + rt;
-            *reinterpret_cast<uint2 *>(&ck[j * KD + 16 * mt + acc_row(0)]) =
-                make_uint2(bf16_pack2(X[g][rt][0], X[g][rt][1]), bf16_pack2(X[g][rt][2], X[g][rt][3]));
-            store_tile_t_split(xs[s & 1][g][0] + 16 * mt, xs[s & 1][g][1] + 16 * mt, LDX, X[g][rt]);
-        }
-    }
-    __syncthreads();
-    // Y = M X from zero, then X = Y + N: N stays an ordinary operand that is
-    // waited for only at the end of the step.
-    f32x4 Y[CPW][SRT];
-#pragma unroll
-    for (int g = 0; g < CPW; ++g)
-#pragma unroll
-        for (int rt = 0; rt < SRT; ++rt) Y[g][rt] = zero4();
-#pragma unroll
-    for (int kk = 0; kk < SKS; ++kk) {
-#pragma unroll
-        for (int g = 0; g < CPW; ++g) {
-            const bf16x8_t bh_ = frag(xs[s & 1][g][0], LDX, 32 * kk), bl_ = frag(xs[s & 1][g][1], LDX, 32 * kk);
-#pragma unroll
-            for (int rt = 0; rt < SRT; ++rt) {
-                Y[g][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][rt][kk], bh_, Y[g][rt], 0, 0, 0);
-                Y[g][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf[SL][rt][kk], bl_, Y[g][rt], 0, 0, 0);
-            }
-        }
-    }
-#pragma unroll
-    for (int g = 0; g < CPW; ++g)
-#pragma unroll
-        for (int rt = 0; rt < SRT; ++rt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) X[g][rt][i] = Y[g][rt][i] + nf[SL][g][rt][i];
-    // Unconditional (the last chunk again past the end): every step issues the
-    // same loads, so the wait for a ring slot counts only the later steps' loads
-    // and stores instead of draining the whole queue.
-    fetch(chunk_of(min(s + 3, p.nc - 1)), mf[SL], nf[SL]);
-}
-
-// Workgroup x -> (head bh, column groups CPW g0 .. CPW g0 + CPW - 1); the NWG
-// workgroups of a head take indices with equal residue mod 8, so they share
-// one XCD's L2.  Each wave holds SRT row tiles of M for the whole step and
-// applies them to the workgroup's CPW column groups.
-__global__ void __launch_bounds__(64 * SW) wide_scan_kernel(WScanArgs p) {
-    __shared__ uint16_t xs[2][CPW][2][16 * LDX];
-    const int x = blockIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
-    const int g0 = (x >> 3) % NWG, bh = (x & 7) + 8 * (x / (8 * NWG));
-    if (bh >= p.B * p.H) return;
-    const int b = bh / p.H, h = bh % p.H;
-    const int j0 = 16 * CPW * g0 + (l & 15);  // this lane's column in group 0
-    bf16x8_t mf[3][SRT][SKS];
-    f32x4 nf[3][CPW][SRT];
-    auto chunk_of = [&](int s) { return p.reverse ? p.nc - 1 - s : s; };
-    auto fetch = [&](int c, bf16x8_t (&m)[SRT][SKS], f32x4 (&n)[CPW][SRT]) {
-        const int64_t cix = (int64_t)bh * p.nc + c;
-        const uint16_t *M = p.m + cix * KD * KD;
-        const float *N = p.n + cix * KD * KD;
-#pragma unroll
-        for (int rt = 0; rt < SRT; ++rt) {
-            const int mt = SRT * w + rt;
-#pragma unroll
-            for (int kk = 0; kk < SKS; ++kk)
-                m[rt][kk] = __builtin_bit_cast(
-                    bf16x8_t, *reinterpret_cast<const uint4 *>(M + (16 * mt + (l & 15)) * KD +
-                                                               32 * kk + 8 * (l >> 4)));
-#pragma unroll
-            for (int g = 0; g < CPW; ++g) {
-                const float4 nv = *reinterpret_cast<const float4 *>(&N[(j0 + 16 * g) * KD + 16 * mt + acc_row(0)]);
-                n[g][rt] = f32x4{nv.x, nv.y, nv.z, nv.w};
-            }
-        }
-    };
-    fetch(chunk_of(0), mf[0], nf[0]);
-    f32x4 X[CPW][SRT];
-#pragma unroll
-    for (int g = 0; g < CPW; ++g)
-#pragma unroll
-        for (int rt = 0; rt < SRT; ++rt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                X[g][rt][i] = p.x0.data ? ld4<float>(p.x0, b, h, 16 * (SRT * w + rt) + acc_row(i), j0 + 16 * g) : 0.f;
-    fetch(chunk_of(min(1, p.nc - 1)), mf[1], nf[1]);
-    fetch(chunk_of(min(2, p.nc - 1)), mf[2], nf[2]);
-    int s = 0;
-    for (; s + 2 < p.nc; s += 3) {  // whole ring turns
-        wscan_step<0>(s, p, bh, j0, w, X, mf, nf, xs, fetch, chunk_of);
-        wscan_step<1>(s + 1, p, bh, j0, w, X, mf, nf, xs, fetch, chunk_of);
-        wscan_step<2>(s + 2, p, bh, j0, w, X, mf, nf, xs, fetch, chunk_of);
-    }
-    if (s < p.nc) wscan_step<0>(s, p, bh, j0, w, X, mf, nf, xs, fetch, chunk_of);
-    if (s + 1 < p.nc) wscan_step<1>(s + 1, p, bh, j0, w, X, mf, nf, xs, fetch, chunk_of);
-    if (p.xout)
-#pragma unroll
-        for (int g = 0; g < CPW; ++g)
-#pragma unroll
-            for (int rt = 0; rt < SRT; ++rt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    p.xout[((int64_t)bh * KD + 16 * (SRT * w + rt) + acc_row(i)) * KD + j0 + 16 * g] = X[g][rt][i];
-}
-
-static void launch_wide_scan(const WScanArgs &p, hipStream_t stream) {
-    const dim3 grid(8 * NWG * ((p.B * p.H + 7) / 8)), block(64 * SW);
-    hipLaunchKernelGGL(wide_scan_kernel, grid, block, 0, stream, p);
 }
 
 // ---- out: value block vb of the outputs, the edits and their norms -------------
@@ -1144,23 +952,44 @@ static inline void wmark(const hipEvent_t *ev, int i, hipStream_t stream) {
     if (ev) (void)hipEventRecord(ev[i], stream);
 }
 
+// The factored scan over a head's chunks: forward (states, U of prep) or
+// reverse (state adjoints, N of bprep).
+static hipError_t wide_scan(const ChunkArgs &a, bool reverse, hipStream_t stream) {
+    LrScanArgs p{};
+    p.nc = a.nc;
+    p.B = a.B;
+    p.H = a.H;
+    p.vd = KD;
+    p.wt = a.lr_wt;
+    p.kt = a.lr_kt;
+    p.gv = a.lr_gv;
+    p.reverse = reverse ? 1 : 0;
+    if (!reverse) {
+        p.u = a.lr_u;
+        p.ckpt = a.ck_state;
+        p.x0 = a.initial;
+        p.xout = a.final_state;
+    } else {
+        p.n = a.ws_n;
+        p.ckpt = a.ws_dstate;
+        p.x0.data = a.dfinal;
+        p.x0.s0 = (int64_t)a.H * KD * KD;
+        p.x0.s1 = (int64_t)KD * KD;
+        p.x0.s2 = KD;
+        p.x0.s3 = 1;
+        p.xout = a.dinitial;
+    }
+    return launch_lr_scan(p, KD, C, stream);
+}
+
 hipError_t launch_wide_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
     const int nch = a.B * a.H * a.nc;
     wmark(ev, 0, stream);
     hipLaunchKernelGGL(wide_prep_kernel, chunk_block_grid(nch), dim3(NT), 0, stream, a);
     wmark(ev, 1, stream);
-    WScanArgs p{};
-    p.nc = a.nc;
-    p.B = a.B;
-    p.H = a.H;
-    p.m = a.map_m;
-    p.n = a.map_n;
-    p.ckpt = a.ck_state;
-    p.x0 = a.initial;
-    p.xout = a.final_state;
-    p.reverse = 0;
     wmark(ev, 2, stream);
-    launch_wide_scan(p, stream);
+    const hipError_t e = wide_scan(a, false, stream);
+    if (e != hipSuccess) return e;
     wmark(ev, 3, stream);
     wmark(ev, 4, stream);
     hipLaunchKernelGGL(wide_out_kernel, chunk_block_grid(nch), dim3(NT), 0, stream, a);
@@ -1175,22 +1004,9 @@ hipError_t launch_wide_bwd(const ChunkArgs &a, hipStream_t stream, const hipEven
     wmark(ev, 0, stream);
     hipLaunchKernelGGL(wide_bprep_kernel, chunk_block_grid(nch), dim3(NT), 0, stream, a);
     wmark(ev, 1, stream);
-    WScanArgs p{};
-    p.nc = a.nc;
-    p.B = a.B;
-    p.H = a.H;
-    p.m = a.ck_mt;
-    p.n = a.ws_n;
-    p.ckpt = a.ws_dstate;
-    p.x0.data = a.dfinal;
-    p.x0.s0 = (int64_t)a.H * KD * KD;
-    p.x0.s1 = (int64_t)KD * KD;
-    p.x0.s2 = KD;
-    p.x0.s3 = 1;
-    p.xout = a.dinitial;
-    p.reverse = 1;
     wmark(ev, 2, stream);
-    launch_wide_scan(p, stream);
+    const hipError_t e = wide_scan(a, true, stream);
+    if (e != hipSuccess) return e;
     wmark(ev, 3, stream);
     wmark(ev, 4, stream);
     for (int pass = 0; pass < NVB; ++pass) {
