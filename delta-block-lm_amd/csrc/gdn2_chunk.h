@@ -65,11 +65,8 @@ struct ChunkArgs {
     uint16_t *ws_dstate;  // [B*H*nc] adjoint of the state at each chunk end
     float *ws_n;       // N of the adjoint map dS_start = M dS_end + N
     // Wide path (d_k = d_v = 128, value blocks of 64): per-chunk |k_t|^2 and the
-    // value blocks' partial |delta_t|^2 (forward checkpoint), and the gradient
-    // partials the first value block hands to the second (backward workspace).
+    // value blocks' partial |delta_t|^2 (forward checkpoint).
     float *ck_kk, *ck_ddp;
-    float *ws_gq, *ws_gk, *ws_gb, *ws_gg;
-    int pass;  // value block of a bgrad launch
     // Channel-wise path (16-token chunks): the gates alpha, erase [B,T,H,K] and
     // write [B,T,H,V] (f32 views), the chunk-local cumulative log decay checkpoint,
     // and the per-channel gate gradients.
@@ -236,10 +233,8 @@ constexpr size_t WCK_MAPN = (size_t)WIDE_D * WIDE_D * 4;
 constexpr size_t WCK_NORM = (size_t)CHUNK * (1 + WIDE_NVB) * 4;
 constexpr size_t WCK_CHUNK =
     WCK_STATE + WCK_T + WCK_GATE + WCK_DELTA + 2 * WCK_LRW + WCK_LRU + WCK_LRG + WCK_NORM;
-// Backward workspace per chunk: dS^T (bf16), N^T (f32), and the first value
-// block's dq/dk (f32 C x D each) and dbeta/dG (f32 C each) partials.
-constexpr size_t WWS_CHUNK = WCK_STATE + WCK_MAPN + 2 * (size_t)CHUNK * WIDE_D * 4 +
-                             2 * (size_t)CHUNK * 4;
+// Backward workspace per chunk: dS^T (bf16) and N^T (f32).
+constexpr size_t WWS_CHUNK = WCK_STATE + WCK_MAPN;
 
 inline size_t wide_checkpoint_bytes(int64_t B, int64_t T, int64_t H) {
     return (size_t)chunk_count(B, T, H) * WCK_CHUNK;
@@ -278,11 +273,6 @@ inline void wide_bind_workspace(ChunkArgs &a, void *ws) {
     a.ws_dstate = reinterpret_cast<uint16_t *>(p);
     p += n * WCK_STATE;
     a.ws_n = reinterpret_cast<float *>(p);
-    p += n * WCK_MAPN;
-    a.ws_gq = reinterpret_cast<float *>(p);
-    a.ws_gk = a.ws_gq + n * CHUNK * WIDE_D;
-    a.ws_gb = a.ws_gk + n * CHUNK * WIDE_D;
-    a.ws_gg = a.ws_gb + n * CHUNK;
 }
 
 hipError_t launch_wide_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);

@@ -118,6 +118,21 @@ __device__ __forceinline__ void row_reduce_store(const float (&p)[4], float *dst
     if ((n & 3) == 0) dst[16 * tm + 4 * (lane_id() >> 4) + 2 * b3 + b2] = x;
 }
 
+// As row_reduce_store, adding to dst when add is set (the lane that stores a
+// row's sum is the same for every call with the same tm).
+__device__ __forceinline__ void row_reduce_accum(const float (&p)[4], float *dst, int tm, bool add) {
+    const int n = lane_id() & 15;
+    const bool b3 = (n & 8) != 0, b2 = (n & 4) != 0;
+    const float s0 = b3 ? p[0] : p[2], s1 = b3 ? p[1] : p[3];
+    const float a0 = (b3 ? p[2] : p[0]) + dpp<0x128>(s0);
+    const float a1 = (b3 ? p[3] : p[1]) + dpp<0x128>(s1);
+    float x = (b2 ? a1 : a0) + dpp<0x141>(b2 ? a0 : a1);
+    x += dpp<0x4E>(x);
+    x += dpp<0xB1>(x);
+    float *d = &dst[16 * tm + 4 * (lane_id() >> 4) + 2 * b3 + b2];
+    if ((n & 3) == 0) *d = add ? *d + x : x;
+}
+
 // Wave 0 (lane == token): decays derived from a gate block.
 __device__ __forceinline__ void gates_derive(GateLds &gl, float G, float beta, float val, int seg) {
     const int t = lane_id();

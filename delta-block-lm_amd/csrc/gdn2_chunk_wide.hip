@@ -17,8 +17,8 @@
 //   out    block vb: delta, O and |delta|^2 of the block's 64 value columns;
 //          a small kernel then forms the scores from both blocks' partials
 //   bprep  block vb: N of the adjoint map for the block's 64 value columns
-//   bgrad  two launches: block 0 leaves its dq, dk, dbeta, dG partials in the
-//          workspace, block 1 adds its own and writes the gradients
+//   bgrad  one workgroup per chunk walks both value blocks, summing what each
+//          contributes to dq, dk, dbeta and dG in registers and LDS
 // Precision follows gdn2_chunk.hip: R, delta, P, dd, dP, W, U and the scan's X
 // and V enter their products as bf16 hi + lo pairs; S0, T, Q, K, V, dS and the
 // scan's -W and Ktil as bf16, U as f32.
@@ -544,40 +544,52 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a) {
     }
 }
 
-// ---- bgrad: every gradient of one chunk, value block a.pass --------------------
-// The phases of gdn2_chunk.hip's gradient kernel with dO, S0, dS, delta, V and
-// dV cut to value block vb.  Everything a value block contributes to dq, dk,
-// dbeta and dG is a sum over its value columns, so block 0 leaves its
-// contributions in the workspace (f32, accumulator layout) and block 1 adds
-// its own before the masks, the dG reverse scan and the stores.
+// ---- bgrad: every gradient of one chunk ------------------------------------------
+// The phases of gdn2_chunk.hip's gradient kernel with the value side cut into
+// the two value blocks of 64 columns, which one workgroup walks in turn.  What
+// does not depend on the values (gates, T, KK^T, QK^T and P) is formed once.
+// What a value block contributes to dq, dk, dbeta and dG is a sum over its
+// columns and stays in registers across the blocks: dO S0^T, the dK terms, dA
+// and dP before their masks, and the row-sum partials.  The masked dA and dP,
+// their products with K and Q (phase G), the dG reverse scan and the dq/dk
+// stores then run once.
 namespace {
 struct WBGradSmem {
     uint16_t q[KTILE];    // Q rows
     uint16_t k[KTILE];    // K rows
-    uint16_t s0t[KTILE];  // S0^T rows of block vb (..F); with dos: dK^T [KD][LDB] (G..)
-    uint16_t dos[TILE];   // dO rows of block vb (..F)
+    uint16_t s0t[KTILE];  // S0^T rows of block vb; with dos: dK^T [KD][LDB] after the blocks
+    uint16_t dos[TILE];   // dO rows of block vb
     uint16_t dst[KTILE];  // dS^T rows of block vb (A..D); dR rows (E..F)
-    uint16_t vr[TILE];    // V rows of block vb (..E); dV^T (G..)
-    uint16_t tr[TILE];    // T rows (..E); MA^T (F..G)
-    uint16_t dh[TILE], dlo[TILE];  // delta rows hi/lo (..F); dQ^T [KD][LDB] over both (G..)
-    uint16_t pt[TILE], ptl[TILE];  // P^T hi/lo (A..D); ddelta^T (D..E); MP^T (F..G)
+    uint16_t vr[TILE];    // V rows of block vb (..E); the last block's dV^T (F..)
+    uint16_t tr[TILE];    // T rows; MA^T (F..G)
+    uint16_t dh[TILE], dlo[TILE];  // delta rows hi/lo of block vb (..F); dQ^T [KD][LDB] over both at the end
+    uint16_t pt[TILE], ptl[TILE];  // P^T hi/lo (until read into registers); ddelta^T (D..E);
+                                   // block 0's dV^T (its F .. block 1's D); MP^T (after the blocks)
     GateLds gl;
     float dsc[C];
     float g1[2][C], ku[2][C], b1[2][C], b2[2][C], zr[2][C], zc[4][C], dlam[2][C];
     float frob[NW];
 };
+
+// A value block's inputs as loaded: dO, S0^T and dS^T rows, V, delta (f32).
+struct VbRaw {
+    uint4 dor, vr;
+    Mat2 s0, ds;
+    float4 d0, d1;
+};
 }  // namespace
 
 __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
     __shared__ WBGradSmem sm;
-    const int vb = a.pass;
-    const bool first = vb == 0, last = vb == NVB - 1;
     uint16_t *Qs = sm.q, *Ks = sm.k, *dOs = sm.dos, *S0t = sm.s0t, *dSt = sm.dst;
     uint16_t *Vr = sm.vr, *Tr = sm.tr, *Dh = sm.dh, *Dlo = sm.dlo, *Pt = sm.pt, *Ptl = sm.ptl;
     uint16_t *Dd = sm.pt, *Ddl = sm.ptl;  // ddelta^T, D..E
     uint16_t *dRr = sm.dst;               // dR rows, E..F
     uint16_t *MAt = sm.tr, *MPt = sm.pt, *MPtl = sm.ptl;
-    uint16_t *dQt = sm.dh, *dKt = sm.s0t, *dVt = sm.vr;
+    uint16_t *dQt = sm.dh, *dKt = sm.s0t;
+    // dV^T of a block ([value][token]): block 0 over P^T's tiles (free from its
+    // phase F until block 1's phase D), block 1 over its V rows (free after E).
+    auto dVt = [&](int vb) { return vb == 0 ? sm.pt : sm.vr; };
     static_assert(sizeof(sm.dh) + sizeof(sm.dlo) >= KD * LDB * 2, "dQ^T over dh, dlo");
     static_assert(sizeof(sm.s0t) + sizeof(sm.dos) >= KD * LDB * 2, "dK^T over s0t, dos");
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -586,105 +598,66 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
     const int tg = c * C + t;
     const bool inb = tg < a.T;
     const GateBlock *gb = a.ck_gate + ci;
-    const float *dck = a.ck_delta + (int64_t)ci * C * KD + 64 * vb;
     const int r0 = 16 * tm + 4 * (lane_id() >> 4);
+    auto load_vb = [&](int vb, VbRaw &r) {
+        const float *dck = a.ck_delta + (int64_t)ci * C * KD + 64 * vb;
+        r.dor = a.dout ? load8(a.dout + 64 * vb, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
+        r.s0 = load_mat2(a.ck_state + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
+        r.ds = load_mat2(a.ws_dstate + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
+        r.vr = load8(a.v + 64 * vb, a.vs, b, tg, h, cb, inb);
+        r.d0 = *reinterpret_cast<const float4 *>(dck + t * KD + 8 * cb);
+        r.d1 = *reinterpret_cast<const float4 *>(dck + t * KD + 8 * cb + 4);
+    };
     const Row2 qr = load_row2(a.q, a.qs, b, tg, h, cb, inb);
     const Row2 kr = load_row2(a.k, a.ks, b, tg, h, cb, inb);
-    const uint4 dor =
-        a.dout ? load8(a.dout + 64 * vb, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
-    const Mat2 s0 = load_mat2(a.ck_state + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
-    const Mat2 ds = load_mat2(a.ws_dstate + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
+    VbRaw raw;
+    load_vb(0, raw);
     const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
     const int sg = gb->seg[t];
     const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
     const bool score_adj = a.dscores != nullptr;
-    const uint4 vr = load8(a.v + 64 * vb, a.vs, b, tg, h, cb, inb);
     const uint4 trw = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C +
                                                       (tid >> 3) * C + 8 * (tid & 7));
-    const float4 d0 = *reinterpret_cast<const float4 *>(dck + t * KD + 8 * cb);
-    const float4 d1 = *reinterpret_cast<const float4 *>(dck + t * KD + 8 * cb + 4);
     const bool on = va != 0.f;
-    {
-        put_row2(Qs, t, cb, mask_row2(qr, on));
-        put_row2(Ks, t, cb, mask_row2(kr, on));
-        put_row8(dOs, t, cb, mask8(dor, on));
-        put_mat2(S0t, s0, tid);
-        put_mat2(dSt, ds, tid);
-        float fr = 0.f;
+    float frob = 0.f;  // this thread's part of <S0, dS> over both blocks
+    // A block's dO, S0^T and dS^T rows into LDS (the first stage of each block).
+    auto stage_vb_a = [&](const VbRaw &r) {
+        put_row8(dOs, t, cb, mask8(r.dor, on));
+        put_mat2(S0t, r.s0, tid);
+        put_mat2(dSt, r.ds, tid);
 #pragma unroll
-        for (int i = 0; i < NKB; ++i) fr += dot8_bf16(s0.p[i], ds.p[i]);
-        fr = wave_sum(fr);
-        if (lane_id() == 0) sm.frob[w] = fr;
-        if (w == 0) {
-            gates_derive(sm.gl, G, be, va, sg);
-            sm.dsc[t] = dsc;
-        }
-    }
-    __syncthreads();
-    const RowGates rg = row_gates(sm.gl, tm);
-    float lmv[4];
-    {
-        const float4 lm = lds_f4(&sm.gl.lam[r0]);
-        lmv[0] = lm.x, lmv[1] = lm.y, lmv[2] = lm.z, lmv[3] = lm.w;
-    }
-    // Phase A: dO S0^T (key tiles of both key blocks), lam K dS, KK^T, QK^T;
-    // P^T (hi/lo) -> LDS.
-    float gmA[2][4];
-    f32x4 dos[NKB][2], kds[2] = {zero4(), zero4()};
-    f32x4 kk[2] = {zero4(), zero4()}, qk[2] = {zero4(), zero4()};
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-        dos[kb][0] = dos[kb][1] = zero4();
-        gemm2_tr<64, LDB, LDK>(dos[kb], &dOs[(16 * tm) * LDB], S0t, tn0 + 4 * kb);
-    }
-    gemm2<KD, LDK, LDK>(kds, &Ks[(16 * tm) * LDK], dSt, tn0);
-    if (tn0 <= tm) {
-        gemm2<KD, LDK, LDK>(kk, &Ks[(16 * tm) * LDK], Ks, tn0);
-        gemm2<KD, LDK, LDK>(qk, &Qs[(16 * tm) * LDK], Ks, tn0);
-    }
-    {
-        float p[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                float qv[4];
-                ld4_rm_tr<LDK>(Qs, 16 * tm, 16 * (tn0 + 4 * kb + j), qv);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) p[i] += qv[i] * dos[kb][j][i];  // q_t . (dO S0^T)_t
-            }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int ss = 16 * (tn0 + j) + acc_col();
-            const float Gs = sm.gl.G[ss];
-            const int sgs = sm.gl.seg[ss];
-            f32x4 pq = qk[j];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int tt = 16 * tm + acc_row(i);
-                kds[j][i] *= lmv[i];
-                gmA[j][i] = (ss <= tt && rg.seg[i] == sgs) ? __expf(rg.G[i] - Gs) : 0.f;
-                pq[i] *= gmA[j][i];
-            }
-            store_tile_t_split(&Pt[(16 * (tn0 + j)) * LDB + 16 * tm],
-                               &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq);
-        }
-        row_reduce_store(p, sm.g1[w & 1], tm);
-    }
-    {  // second half of the staging: V, T and delta (hi/lo) of the block
-        put_row8(Vr, t, cb, mask8(vr, on));
-        *reinterpret_cast<uint4 *>(&Tr[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
-        const float x[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+        for (int i = 0; i < NKB; ++i) frob += dot8_bf16(r.s0.p[i], r.ds.p[i]);
+    };
+    // A block's V rows and delta rows (hi/lo): read from phase D on.
+    auto stage_vb_b = [&](const VbRaw &r) {
+        put_row8(Vr, t, cb, mask8(r.vr, on));
+        const float x[8] = {r.d0.x, r.d0.y, r.d0.z, r.d0.w, r.d1.x, r.d1.y, r.d1.z, r.d1.w};
         Pack8 ph, pl;
 #pragma unroll
         for (int e = 0; e < 8; ++e) split_bf16(x[e], ph.h[e], pl.h[e]);
         put_row8(Dh, t, cb, ph.u);
         put_row8(Dlo, t, cb, pl.u);
+    };
+    put_row2(Qs, t, cb, mask_row2(qr, on));
+    put_row2(Ks, t, cb, mask_row2(kr, on));
+    *reinterpret_cast<uint4 *>(&Tr[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
+    stage_vb_a(raw);
+    stage_vb_b(raw);
+    if (w == 0) {
+        gates_derive(sm.gl, G, be, va, sg);
+        sm.dsc[t] = dsc;
     }
     __syncthreads();
-    // Phase D: delta dS^T (-> dlam), ddelta = P^T dO + lam K dS + c delta.
+    float lmv[4], bt[4], bg[4];  // lam, beta, beta gam at this lane's rows
+    {
+        const RowGates rg = row_gates(sm.gl, tm);
+        const float4 lm = lds_f4(&sm.gl.lam[r0]);
+        lmv[0] = lm.x, lmv[1] = lm.y, lmv[2] = lm.z, lmv[3] = lm.w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bt[i] = rg.beta[i], bg[i] = rg.beta[i] * rg.gam[i];
+    }
     float cs[4] = {0.f, 0.f, 0.f, 0.f}, ck[4] = {0.f, 0.f, 0.f, 0.f};
-    if (score_adj) {
+    if (score_adj) {  // c and c' from the forward's |k|^2 and both blocks' |delta|^2
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int ss = r0 + i;
@@ -697,29 +670,125 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
             ck[i] = ok ? sm.dsc[ss] * nd / nk : 0.f;
         }
     }
-    f32x4 dka[NKB][2];
-    f32x4 xd[2] = {kds[0], kds[1]};
+    // The Gam mask at this wave's tiles (formed here and again after the blocks).
+    auto gam_mask = [&](float (&gm)[2][4]) {
+        const RowGates rg = row_gates(sm.gl, tm);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int ss = 16 * (tn0 + j) + acc_col();
+            const float Gs = sm.gl.G[ss];
+            const int sgs = sm.gl.seg[ss];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tt = 16 * tm + acc_row(i);
+                gm[j][i] = (ss <= tt && rg.seg[i] == sgs) ? __expf(rg.G[i] - Gs) : 0.f;
+            }
+        }
+    };
+    // Once for both blocks: P = Gam . QK^T, transposed (hi/lo) -> LDS, then this
+    // wave's rows of P^T (the A operand of P^T dO) into registers.
+    bf16x8_t pf[2][2];  // [hi, lo][reduction half]
     {
-        float p[4] = {0.f, 0.f, 0.f, 0.f};
+        float gm[2][4];
+        gam_mask(gm);
+        f32x4 qk[2] = {zero4(), zero4()};
+        if (tn0 <= tm) gemm2<KD, LDK, LDK>(qk, &Qs[(16 * tm) * LDK], Ks, tn0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            f32x4 pq;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pq[i] = qk[j][i] * gm[j][i];
+            store_tile_t_split(&Pt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+        pf[0][k2] = frag(&Pt[(16 * tm) * LDB], LDB, 32 * k2);
+        pf[1][k2] = frag(&Ptl[(16 * tm) * LDB], LDB, 32 * k2);
+    }
+    // Sums over both blocks, in registers: dO S0^T (-> dQ), the dK terms, dA and
+    // dP before their masks, and the row-sum partials of the gate gradients.
+    f32x4 dos[NKB][2], dka[NKB][2], da[2], dp[2];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) dos[kb][0] = dos[kb][1] = dka[kb][0] = dka[kb][1] = zero4();
+    da[0] = da[1] = dp[0] = dp[1] = zero4();
+    // A block's dV rows out of its staged transposed tile: lane (token 16 (w%4) +
+    // l%16, values 32 (w/4) + 8 (l/16) ..) stores one 16-byte piece.
+    auto dv_out = [&](int vb) {
+        const int l = lane_id(), tq = c * C + 16 * (w & 3) + (l & 15);
+        const bf16x8_t gv = frag_tr(dVt(vb), 32 * (w >> 2), 16 * (w & 3));
+        if (tq < a.T && a.dv)
+            *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dv) +
+                                          (((int64_t)b * a.T + tq) * a.H + h) * KD + 64 * vb +
+                                          32 * (w >> 2) + 8 * (l >> 4)) = gv;
+    };
+    // Rolled: unrolled, the second block's loads are hoisted into the first
+    // block's phases and the registers spill.
+#pragma unroll 1
+    for (int vb = 0; vb < NVB; ++vb) {
+        if (vb > 0) {
+            load_vb(vb, raw);
+            __syncthreads();  // the previous block's phase F has read dO, S0^T, dR and delta
+            dv_out(vb - 1);
+            stage_vb_a(raw);
+            stage_vb_b(raw);
+            __syncthreads();
+        }
+        // Phase A: dO S0^T (key tiles of both key blocks), lam K dS.  Row-sum
+        // partials of the gate gradients add into their LDS rows block by block.
+        f32x4 kds[2] = {zero4(), zero4()};
+        float pg1[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
-            dka[kb][0] = dka[kb][1] = zero4();
-            gemm2_tr<64, LDB, LDK>(dka[kb], &Dh[(16 * tm) * LDB], dSt, tn0 + 4 * kb);
-            gemm2_tr<64, LDB, LDK>(dka[kb], &Dlo[(16 * tm) * LDB], dSt, tn0 + 4 * kb);
+            f32x4 x[2] = {zero4(), zero4()};
+            gemm2_tr<64, LDB, LDK>(x, &dOs[(16 * tm) * LDB], S0t, tn0 + 4 * kb);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float qv[4];
+                ld4_rm_tr<LDK>(Qs, 16 * tm, 16 * (tn0 + 4 * kb + j), qv);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    pg1[i] += qv[i] * x[j][i];  // q_t . (dO S0^T)_t
+                    dos[kb][j][i] += x[j][i];
+                }
+            }
+        }
+        row_reduce_accum(pg1, sm.g1[w & 1], tm, vb > 0);
+        gemm2<KD, LDK, LDK>(kds, &Ks[(16 * tm) * LDK], dSt, tn0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kds[j][i] *= lmv[i];
+        // Phase D: delta dS^T (-> dlam, dK), ddelta = P^T dO + lam K dS + c delta.
+        f32x4 xd[2] = {kds[0], kds[1]};
+        float pdl[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+            f32x4 x[2] = {zero4(), zero4()};
+            gemm2_tr<64, LDB, LDK>(x, &Dh[(16 * tm) * LDB], dSt, tn0 + 4 * kb);
+            gemm2_tr<64, LDB, LDK>(x, &Dlo[(16 * tm) * LDB], dSt, tn0 + 4 * kb);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 float kv[4];
                 ld4_rm_tr<LDK>(Ks, 16 * tm, 16 * (tn0 + 4 * kb + j), kv);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    p[i] += kv[i] * dka[kb][j][i];
-                    dka[kb][j][i] *= lmv[i];
+                    pdl[i] += kv[i] * x[j][i];
+                    dka[kb][j][i] += lmv[i] * x[j][i];
                 }
             }
         }
-        row_reduce_store(p, sm.dlam[w & 1], tm);
-        gemm2_tr(xd, &Pt[(16 * tm) * LDB], dOs, tn0);  // B[v][t] = dO[t][v]
-        gemm2_tr(xd, &Ptl[(16 * tm) * LDB], dOs, tn0);
+        row_reduce_accum(pdl, sm.dlam[w & 1], tm, vb > 0);
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const bf16x8_t ob = frag_tr(dOs, 32 * k2, 16 * (tn0 + j));  // B[v][t] = dO[t][v]
+                xd[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf[0][k2], ob, xd[j], 0, 0, 0);
+                xd[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf[1][k2], ob, xd[j], 0, 0, 0);
+            }
         if (score_adj) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
@@ -730,45 +799,45 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
                 for (int i = 0; i < 4; ++i) xd[j][i] += cs[i] * (dh[i] + dlo[i]);
             }
         }
-    }
-    __syncthreads();  // P^T read by every wave before ddelta^T takes its tiles
+        __syncthreads();  // P^T and delta read by every wave before ddelta^T takes P's tiles
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-        store_tile_t_split(&Dd[(16 * (tn0 + j)) * LDB + 16 * tm],
-                           &Ddl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, xd[j]);
-    __syncthreads();
-    // Phase E: dR = T^T ddelta -> dV, the sum_v dR v part of dbeta, dR rows.
-    f32x4 dvv[2];
-    {
-        f32x4 x[2] = {zero4(), zero4()};
+        for (int j = 0; j < 2; ++j)
+            store_tile_t_split(&Dd[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Ddl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, xd[j]);
+        __syncthreads();
+        // Phase E: dR = T^T ddelta -> dV, the sum_v dR v part of dbeta, dR rows.
+        {
+            f32x4 x[2] = {zero4(), zero4()};
 #pragma unroll
-        for (int r = 0; r < 64; r += 32) {
-            const bf16x8_t tt = frag_tr(Tr, r, 16 * tm);  // A[s][t] = T[t][s]
+            for (int r = 0; r < 64; r += 32) {
+                const bf16x8_t tt = frag_tr(Tr, r, 16 * tm);  // A[s][t] = T[t][s]
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const uint16_t *Yh = &Dd[(16 * (tn0 + j)) * LDB], *Yl = &Ddl[(16 * (tn0 + j)) * LDB];
+                    x[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tt, frag(Yh, LDB, r), x[j], 0, 0, 0);
+                    x[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tt, frag(Yl, LDB, r), x[j], 0, 0, 0);
+                }
+            }
+            f32x4 dvv[2];
+            float pb2[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const uint16_t *Yh = &Dd[(16 * (tn0 + j)) * LDB], *Yl = &Ddl[(16 * (tn0 + j)) * LDB];
-                x[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tt, frag(Yh, LDB, r), x[j], 0, 0, 0);
-                x[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tt, frag(Yl, LDB, r), x[j], 0, 0, 0);
-            }
-        }
-        float p[4] = {0.f, 0.f, 0.f, 0.f};
+                float vv[4];
+                ld4_rm_tr(Vr, 16 * tm, 16 * (tn0 + j), vv);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            float vv[4];
-            ld4_rm_tr(Vr, 16 * tm, 16 * (tn0 + j), vv);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                p[i] += x[j][i] * vv[i];
-                dvv[j][i] = sm.gl.val[r0 + i] != 0.f ? rg.beta[i] * x[j][i] : 0.f;
+                for (int i = 0; i < 4; ++i) {
+                    pb2[i] += x[j][i] * vv[i];
+                    dvv[j][i] = sm.gl.val[r0 + i] != 0.f ? bt[i] * x[j][i] : 0.f;
+                }
+                store_tile_rm(&dRr[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, x[j]);
             }
-            store_tile_rm(&dRr[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, x[j]);
+            row_reduce_accum(pb2, sm.b2[w & 1], tm, vb > 0);
+            __syncthreads();  // V and ddelta^T read: their tiles take this block's dV^T
+#pragma unroll
+            for (int j = 0; j < 2; ++j) store_tile_t(&dVt(vb)[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, dvv[j]);
         }
-        row_reduce_store(p, sm.b2[w & 1], tm);
-    }
-    __syncthreads();
-    // Phase F: dR S0^T (-> dK, dbeta, dgam), dA and dP (masked) -> MA^T, MP^T.
-    {
-        float p2[4] = {0.f, 0.f, 0.f, 0.f};
+        // Phase F: dR S0^T (-> dK, dbeta, dgam); dR delta^T and dO delta^T summed.
+        float pku[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
             f32x4 drs[2] = {zero4(), zero4()};
@@ -779,20 +848,31 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
                 ld4_rm_tr<LDK>(Ks, 16 * tm, 16 * (tn0 + 4 * kb + j), kv);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    p2[i] += kv[i] * drs[j][i];
-                    dka[kb][j][i] -= rg.beta[i] * rg.gam[i] * drs[j][i];
+                    pku[i] += kv[i] * drs[j][i];
+                    dka[kb][j][i] -= bg[i] * drs[j][i];
                 }
             }
         }
-        row_reduce_store(p2, sm.ku[w & 1], tm);
-    }
-    {
-        f32x4 da[2] = {zero4(), zero4()}, dp[2] = {zero4(), zero4()};
+        row_reduce_accum(pku, sm.ku[w & 1], tm, vb > 0);
         if (tn0 <= tm) {
             gemm2(da, &dRr[(16 * tm) * LDB], Dh, tn0);
             gemm2(da, &dRr[(16 * tm) * LDB], Dlo, tn0);
             gemm2(dp, &dOs[(16 * tm) * LDB], Dh, tn0);
             gemm2(dp, &dOs[(16 * tm) * LDB], Dlo, tn0);
+        }
+    }
+    frob = wave_sum(frob);
+    if (lane_id() == 0) sm.frob[w] = frob;
+    const RowGates rg = row_gates(sm.gl, tm);
+    // dA and dP masked -> MA^T, MP^T, and the gate-gradient partial sums (KK^T,
+    // QK^T and the mask formed again here rather than held through the blocks).
+    {
+        float gmA[2][4];
+        gam_mask(gmA);
+        f32x4 kk[2] = {zero4(), zero4()}, qk[2] = {zero4(), zero4()};
+        if (tn0 <= tm) {
+            gemm2<KD, LDK, LDK>(kk, &Ks[(16 * tm) * LDK], Ks, tn0);
+            gemm2<KD, LDK, LDK>(qk, &Qs[(16 * tm) * LDK], Ks, tn0);
         }
         float pb[4] = {0.f, 0.f, 0.f, 0.f}, pz[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -821,9 +901,8 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
         row_reduce_store(pz, sm.zr[w & 1], tm);
     }
     __syncthreads();
-    // Phase G: this block's dQ = MP K + gam dO S0^T and dK = (MA + MA^T) K + MP^T Q
-    // + lam delta dS^T - beta gam dR S0^T; block 0 leaves them in the workspace,
-    // block 1 adds them, masks and stages the rows.
+    // Phase G: dQ = MP K + gam dO S0^T and dK = (MA + MA^T) K + MP^T Q + lam delta
+    // dS^T - beta gam dR S0^T (+ c' k), masked, staged transposed with dV.
     {
         f32x4 x[NKB][2], y[NKB][2];
 #pragma unroll
@@ -848,66 +927,39 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
                     y[kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ptl, qbf, y[kb][j], 0, 0, 0);
                 }
         }
-        // Partials in accumulator layout: one float4 per lane and tile.
-        const int64_t pbase = (((int64_t)ci * NW + w) * NKB * 2) * 64 + lane_id();
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 float kv[4] = {0.f, 0.f, 0.f, 0.f};
-                if (score_adj && last) ld4_rm_tr<LDK>(Ks, 16 * tm, 16 * (tn0 + 4 * kb + j), kv);
+                if (score_adj) ld4_rm_tr<LDK>(Ks, 16 * tm, 16 * (tn0 + 4 * kb + j), kv);
                 f32x4 gq, gk;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    gq[i] = x[kb][j][i] + rg.gam[i] * dos[kb][j][i];
-                    gk[i] = y[kb][j][i] + dka[kb][j][i] + ck[i] * kv[i];
+                    const bool von = sm.gl.val[r0 + i] != 0.f;
+                    gq[i] = von ? x[kb][j][i] + rg.gam[i] * dos[kb][j][i] : 0.f;
+                    gk[i] = von ? y[kb][j][i] + dka[kb][j][i] + ck[i] * kv[i] : 0.f;
                 }
-                const int64_t pi = pbase + (kb * 2 + j) * 64;
-                float4 *wq = reinterpret_cast<float4 *>(a.ws_gq) + pi;
-                float4 *wk = reinterpret_cast<float4 *>(a.ws_gk) + pi;
-                if (!last) {
-                    *wq = make_float4(gq[0], gq[1], gq[2], gq[3]);
-                    *wk = make_float4(gk[0], gk[1], gk[2], gk[3]);
-                } else {
-                    if (!first) {
-                        const float4 pq = *wq, pk = *wk;
-                        gq[0] += pq.x, gq[1] += pq.y, gq[2] += pq.z, gq[3] += pq.w;
-                        gk[0] += pk.x, gk[1] += pk.y, gk[2] += pk.z, gk[3] += pk.w;
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const bool von = sm.gl.val[r0 + i] != 0.f;
-                        gq[i] = von ? gq[i] : 0.f;
-                        gk[i] = von ? gk[i] : 0.f;
-                    }
-                    // Transposed gradient tiles ([channel][token]) in dead slots.
-                    store_tile_t(&dQt[(16 * (tn0 + 4 * kb + j)) * LDB + 16 * tm], LDB, gq);
-                    store_tile_t(&dKt[(16 * (tn0 + 4 * kb + j)) * LDB + 16 * tm], LDB, gk);
-                }
+                // Transposed gradient tiles ([channel][token]) in slots phase G does not read.
+                store_tile_t(&dQt[(16 * (tn0 + 4 * kb + j)) * LDB + 16 * tm], LDB, gq);
+                store_tile_t(&dKt[(16 * (tn0 + 4 * kb + j)) * LDB + 16 * tm], LDB, gk);
             }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) store_tile_t(&dVt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, dvv[j]);
     }
     __syncthreads();
+    dv_out(NVB - 1);
     // Rows out: lane (token 16 (w%4) + l%16, channels 32 (w/4) + 8 (l/16) ..) of
     // every 64-channel block stores one 16-byte piece per gradient.
     {
         const int l = lane_id();
         const int tq = c * C + 16 * (w & 3) + (l & 15);
         const int64_t row = ((int64_t)b * a.T + tq) * a.H + h;
-        const bf16x8_t gv = frag_tr(dVt, 32 * (w >> 2), 16 * (w & 3));
-        if (tq < a.T && a.dv)
-            *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dv) + row * KD + 64 * vb +
-                                          32 * (w >> 2) + 8 * (l >> 4)) = gv;
-        if (last) {
 #pragma unroll
-            for (int kb = 0; kb < NKB; ++kb) {
-                const bf16x8_t gq = frag_tr(dQt, 64 * kb + 32 * (w >> 2), 16 * (w & 3));
-                const bf16x8_t gk = frag_tr(dKt, 64 * kb + 32 * (w >> 2), 16 * (w & 3));
-                const int64_t o = row * KD + 64 * kb + 32 * (w >> 2) + 8 * (l >> 4);
-                if (tq < a.T && a.dq) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dq) + o) = gq;
-                if (tq < a.T && a.dk) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dk) + o) = gk;
-            }
+        for (int kb = 0; kb < NKB; ++kb) {
+            const bf16x8_t gq = frag_tr(dQt, 64 * kb + 32 * (w >> 2), 16 * (w & 3));
+            const bf16x8_t gk = frag_tr(dKt, 64 * kb + 32 * (w >> 2), 16 * (w & 3));
+            const int64_t o = row * KD + 64 * kb + 32 * (w >> 2) + 8 * (l >> 4);
+            if (tq < a.T && a.dq) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dq) + o) = gq;
+            if (tq < a.T && a.dk) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dk) + o) = gk;
         }
     }
     // Phase H: gate gradients (wave 0, lane == token; lane t holds token 63 - t).
@@ -926,24 +978,14 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
             for (int q = 0; q < NW; ++q) fr += sm.frob[q];
             dG += tail + sm.gl.gamC * fr;
         }
-        float db = sm.b1[0][s] + sm.b1[1][s] + sm.b2[0][s] + sm.b2[1][s] - gam * u;
-        const int64_t gi = (int64_t)ci * C + s;
-        if (!last) {
-            a.ws_gg[gi] = dG;
-            a.ws_gb[gi] = db;
-        } else {
-            if (!first) {
-                dG += a.ws_gg[gi];
-                db += a.ws_gb[gi];
-            }
-            const float x = wave_scan_add(dG);
-            const bool von = sm.gl.val[s] != 0.f;
-            const bool rs = von && (s == 0 ? sm.gl.seg[0] == 1 : sm.gl.seg[s] != sm.gl.seg[s - 1]);
-            if (ts < a.T) {
-                const int64_t o = ((int64_t)b * a.T + ts) * a.H + h;
-                if (a.dg) a.dg[o] = (von && !rs) ? x : 0.f;
-                if (a.dbeta) a.dbeta[o] = von ? db : 0.f;
-            }
+        const float db = sm.b1[0][s] + sm.b1[1][s] + sm.b2[0][s] + sm.b2[1][s] - gam * u;
+        const float x = wave_scan_add(dG);
+        const bool von = sm.gl.val[s] != 0.f;
+        const bool rs = von && (s == 0 ? sm.gl.seg[0] == 1 : sm.gl.seg[s] != sm.gl.seg[s - 1]);
+        if (ts < a.T) {
+            const int64_t o = ((int64_t)b * a.T + ts) * a.H + h;
+            if (a.dg) a.dg[o] = (von && !rs) ? x : 0.f;
+            if (a.dbeta) a.dbeta[o] = von ? db : 0.f;
         }
     }
 }
@@ -1009,11 +1051,7 @@ hipError_t launch_wide_bwd(const ChunkArgs &a, hipStream_t stream, const hipEven
     if (e != hipSuccess) return e;
     wmark(ev, 3, stream);
     wmark(ev, 4, stream);
-    for (int pass = 0; pass < NVB; ++pass) {
-        ChunkArgs q = a;
-        q.pass = pass;
-        hipLaunchKernelGGL(wide_bgrad_kernel, dim3(nch), dim3(NT), 0, stream, q);
-    }
+    hipLaunchKernelGGL(wide_bgrad_kernel, dim3(nch), dim3(NT), 0, stream, a);
     wmark(ev, 5, stream);
     return hipGetLastError();
 }
