@@ -6,19 +6,18 @@
 // (Gam .* Q K^T) delta, S_C = gam_63 S0 + Ktil^T (U - W S0) with Ktil = lam K,
 // W = T diag(beta gam) K, U = T diag(beta) V).  Key-side products reduce over
 // all D = 128 key channels; value columns evolve independently, so every
-// value-side product is cut into value blocks of 64 columns, one workgroup
-// each (grid = chunks x 2):
-//   prep   block vb: gates, A, T (block 0 writes them), and the chunk map's
-//          factors: block vb's 64 key columns of -W^T and Ktil, 64 value
-//          columns of U^T
+// value-side product is cut into two value blocks of 64 columns, which one
+// workgroup per chunk walks in turn after forming the block-independent
+// products (gates, A, T, P = Gam . QK^T, W) once:
+//   prep   gates, A, T, and the chunk map's factors -W^T, Ktil, U^T, gam_63
 //   scan   the factored scan of gdn2_chunk_lr.hip (the map is rank 64 beside
 //          its diagonal, so its factors are 64 KiB per chunk against 96 KiB
 //          for A_c and B_c)
-//   out    block vb: delta, O and |delta|^2 of the block's 64 value columns;
-//          a small kernel then forms the scores from both blocks' partials
-//   bprep  block vb: N of the adjoint map for the block's 64 value columns
-//   bgrad  one workgroup per chunk walks both value blocks, summing what each
-//          contributes to dq, dk, dbeta and dG in registers and LDS
+//   out    per block: delta, O and |delta|^2; then the scores
+//   bprep  per block: N of the adjoint map
+//   bgrad  per block: the block's contributions to dq, dk, dbeta and dG,
+//          summed in registers and LDS; then the masked products, dg and the
+//          stores
 // Precision follows gdn2_chunk.hip: R, delta, P, dd, dP, W, U and the scan's X
 // and V enter their products as bf16 hi + lo pairs; S0, T, Q, K, V, dS and the
 // scan's -W and Ktil as bf16, U as f32.
@@ -35,17 +34,6 @@ constexpr int LDK = KD + 8;     // bf16 row stride of a 64 x KD tile
 constexpr int KTILE = 64 * LDK;
 static_assert(NVB == 2 && NKB == 2, "the wide kernels cut D into two blocks of 64");
 
-// Workgroup x -> (chunk, value block): both blocks of a chunk share x mod 8
-// and so one XCD (workgroups go to the XCDs round-robin by index).
-__device__ __forceinline__ bool chunk_block(int x, int nch, int &ci, int &vb) {
-    const int g = x / (8 * NVB), r = x % (8 * NVB);
-    vb = r >> 3;
-    ci = 8 * g + (r & 7);
-    return ci < nch;
-}
-
-inline dim3 chunk_block_grid(int nch) { return dim3(8 * NVB * ((nch + 7) / 8)); }
-
 // Token t's channel pieces [8 cb, 8 cb + 8) and [64 + 8 cb, 72 + 8 cb).
 struct Row2 {
     uint4 p[NKB];
@@ -61,9 +49,6 @@ __device__ __forceinline__ void put_row2(uint16_t *tile, int t, int cb, const Ro
 #pragma unroll
     for (int i = 0; i < NKB; ++i) put_row8(tile, t, cb + 8 * i, r.p[i], LDK);
 }
-// Piece i of a row, i uniform but not a compile-time constant (no dynamic
-// register indexing).
-__device__ __forceinline__ uint4 piece(const Row2 &r, int i) { return i == 0 ? r.p[0] : r.p[1]; }
 __device__ __forceinline__ Row2 mask_row2(Row2 r, bool on) {
 #pragma unroll
     for (int i = 0; i < NKB; ++i) r.p[i] = mask8(r.p[i], on);
@@ -110,36 +95,37 @@ __device__ __forceinline__ void put_mat2(uint16_t *tile, const Mat2 &m, int tid)
 }
 
 struct WPrepSmem {
-    uint16_t ks[KTILE];    // K rows; T (bf16, row stride LDB) once A is formed
-    uint16_t kbg[TILE];    // beta gam K rows, key columns of block vb
-    uint16_t vbt[TILE];    // beta V rows, value columns of block vb
-    struct {
-        float Af[C * LDF];
-        float Tf[C * LDF];
-    } inv;
+    uint16_t ks[KTILE];  // K rows; T (bf16, row stride LDB) once A is formed
+    union {
+        struct {
+            float Af[C * LDF];
+            float Tf[C * LDF];
+        } inv;
+        struct {
+            uint16_t kbg[NKB][TILE];  // beta gam K rows, key block kb
+            uint16_t vbt[NVB][TILE];  // beta V rows, value block vb
+        } wu;                          // once the inverse is done
+    } u;
     GateLds gl;
 };
 
 }  // namespace
 
-// ---- prep: gates, the UT inverse and block vb of the chunk's factored map -------
+// ---- prep: gates, the UT inverse and the chunk's factored map ------------------
 // The chunk map S_C = gam_63 S0 + Ktil^T (U - W S0) (Ktil = lam K, W = T diag(beta
-// gam) K, U = T diag(beta) V) leaves as its factors: block vb writes its 64 key
-// columns of -W^T and of Ktil, its 64 value columns of U^T, and block 0 the gate
-// block, T and the diagonal gam_63.
+// gam) K, U = T diag(beta) V) leaves as its factors: -W^T and Ktil (bf16), U^T
+// (f32) and the diagonal gam_63, with the gate block and T.  One workgroup per
+// chunk forms A and T once and W, U for both key and value blocks.
 __global__ void __launch_bounds__(NT) wide_prep_kernel(ChunkArgs a) {
     __shared__ WPrepSmem sm;
-    int ci, vb;
-    if (!chunk_block(blockIdx.x, a.B * a.H * a.nc, ci, vb)) return;
-    uint16_t *Ks = sm.ks, *KBGs = sm.kbg, *VBs = sm.vbt;
-    uint16_t *Tb = sm.ks;  // over K once A is formed
+    uint16_t *Ks = sm.ks, *Tb = sm.ks;  // T over K once A is formed
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tg = c * C + t;
     const int tm = w >> 1, tn0 = 2 * (w & 1);
     const bool inb = tg < a.T;
     const Row2 kraw = load_row2(a.k, a.ks, b, tg, h, cb, inb);
-    const uint4 vraw = load8(a.v + 64 * vb, a.vs, b, tg, h, cb, inb);
+    const Row2 vraw = load_row2(a.v, a.vs, b, tg, h, cb, inb);
     const float vld = inb ? ld4<float>(a.valid, b, tg, 0, 0) : 0.f;
     float rst = 0.f, gt = 0.f, bt = 0.f;
     if (w == 0 && inb) {
@@ -148,29 +134,27 @@ __global__ void __launch_bounds__(NT) wide_prep_kernel(ChunkArgs a) {
         bt = ld4<float>(a.beta, b, tg, h, 0);
     }
     const bool on = vld != 0.f;
-    const Row2 k8 = mask_row2(kraw, on);
-    const uint4 v8 = mask8(vraw, on);
+    const Row2 k8 = mask_row2(kraw, on), v8 = mask_row2(vraw, on);
     put_row2(Ks, t, cb, k8);
     if (w == 0) {
         const float G = wave_scan_add(on ? gt : 0.f);
         const int seg = wave_scan_add((on && rst != 0.f) ? 1 : 0);
         const float bm = on ? bt : 0.f;
         gates_derive(sm.gl, G, bm, on ? 1.f : 0.f, seg);
-        if (vb == 0) {
-            GateBlock *gb = a.ck_gate + ci;
-            gb->G[t] = G;
-            gb->beta[t] = bm;
-            gb->val[t] = on ? 1.f : 0.f;
-            gb->seg[t] = seg;
-        }
+        GateBlock *gb = a.ck_gate + ci;
+        gb->G[t] = G;
+        gb->beta[t] = bm;
+        gb->val[t] = on ? 1.f : 0.f;
+        gb->seg[t] = seg;
     }
     __syncthreads();
-    {  // beta gam K (key block vb) staged; Ktil = lam K (key block vb) and the diagonal out
-        const float bg = sm.gl.beta[t] * sm.gl.gam[t];
-        put_row8(KBGs, t, cb, scale8(piece(k8, vb), bg));
-        *reinterpret_cast<uint4 *>(a.lr_kt + ((int64_t)ci * C + t) * KD + 64 * vb + 8 * cb) =
-            scale8(piece(k8, vb), sm.gl.lam[t]);
-        if (vb == 0 && tid < KD) a.lr_gv[(int64_t)ci * KD + tid] = sm.gl.gamC;
+    {  // Ktil = lam K rows and the map's diagonal out
+        const float la = sm.gl.lam[t];
+#pragma unroll
+        for (int i = 0; i < NKB; ++i)
+            *reinterpret_cast<uint4 *>(a.lr_kt + ((int64_t)ci * C + t) * KD + 64 * i + 8 * cb) =
+                scale8(k8.p[i], la);
+        if (tid < KD) a.lr_gv[(int64_t)ci * KD + tid] = sm.gl.gamC;
     }
     // A = strict_lower(beta_t Gam_ts k_t.k_s) in f32 (tiles with tn <= tm only).
     if (tn0 <= tm) {
@@ -185,38 +169,47 @@ __global__ void __launch_bounds__(NT) wide_prep_kernel(ChunkArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tt = 16 * tm + acc_row(i);
-                sm.inv.Af[tt * LDF + ss] = (ss < tt && rg.seg[i] == sgs)
-                                               ? rg.beta[i] * __expf(rg.G[i] - Gs) * kk[j][i]
-                                               : 0.f;
+                sm.u.inv.Af[tt * LDF + ss] = (ss < tt && rg.seg[i] == sgs)
+                                                 ? rg.beta[i] * __expf(rg.G[i] - Gs) * kk[j][i]
+                                                 : 0.f;
             }
         }
     }
     __syncthreads();
-    ut_inverse(sm.inv.Af, sm.inv.Tf, w);
+    ut_inverse(sm.u.inv.Af, sm.u.inv.Tf, w);
     {  // T (bf16, row-major, zero above the diagonal): LDS operand and checkpoint
         const int r = tid >> 3, c0 = 8 * (tid & 7);
         uint32_t pk[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int s0 = c0 + 2 * e;
-            pk[e] = bf16_pack2(s0 <= r ? sm.inv.Tf[r * LDF + s0] : 0.f,
-                               s0 + 1 <= r ? sm.inv.Tf[r * LDF + s0 + 1] : 0.f);
+            pk[e] = bf16_pack2(s0 <= r ? sm.u.inv.Tf[r * LDF + s0] : 0.f,
+                               s0 + 1 <= r ? sm.u.inv.Tf[r * LDF + s0 + 1] : 0.f);
         }
         const uint4 v = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        if (vb == 0) *reinterpret_cast<uint4 *>(a.ck_t + (int64_t)ci * C * C + r * C + c0) = v;
+        *reinterpret_cast<uint4 *>(a.ck_t + (int64_t)ci * C * C + r * C + c0) = v;
         *reinterpret_cast<uint4 *>(&Tb[r * LDB + c0]) = v;
     }
-    put_row8(VBs, t, cb, scale8(v8, sm.gl.beta[t]));
-    __syncthreads();
-    // W_vb = T (beta gam K)[:, block vb], U_vb = T (beta V_vb), straight from the
-    // accumulators: -W^T (bf16) and U^T (f32), [column][token].
+    __syncthreads();  // T read out of the inverse's scratch: beta gam K and beta V take it
     {
+        const float bg = sm.gl.beta[t] * sm.gl.gam[t], be = sm.gl.beta[t];
+#pragma unroll
+        for (int i = 0; i < NKB; ++i) {
+            put_row8(sm.u.wu.kbg[i], t, cb, scale8(k8.p[i], bg));
+            put_row8(sm.u.wu.vbt[i], t, cb, scale8(v8.p[i], be));
+        }
+    }
+    __syncthreads();
+    // W = T (beta gam K), U = T (beta V), block by block, straight from the
+    // accumulators: -W^T (bf16) and U^T (f32), [column][token].
+#pragma unroll
+    for (int i = 0; i < NKB; ++i) {
         f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
-        gemm2_tr(x, &Tb[(16 * tm) * LDB], KBGs, tn0);
-        gemm2_tr(y, &Tb[(16 * tm) * LDB], VBs, tn0);
+        gemm2_tr(x, &Tb[(16 * tm) * LDB], sm.u.wu.kbg[i], tn0);
+        gemm2_tr(y, &Tb[(16 * tm) * LDB], sm.u.wu.vbt[i], tn0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int64_t o = ((int64_t)ci * KD + 64 * vb + 16 * (tn0 + j) + acc_col()) * C + 16 * tm + acc_row(0);
+            const int64_t o = ((int64_t)ci * KD + 64 * i + 16 * (tn0 + j) + acc_col()) * C + 16 * tm + acc_row(0);
             *reinterpret_cast<uint2 *>(a.lr_wt + o) =
                 make_uint2(bf16_pack2(-x[j][0], -x[j][1]), bf16_pack2(-x[j][2], -x[j][3]));
             *reinterpret_cast<float4 *>(a.lr_u + o) = make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
@@ -224,51 +217,54 @@ __global__ void __launch_bounds__(NT) wide_prep_kernel(ChunkArgs a) {
     }
 }
 
-// ---- out: value block vb of the outputs, the edits and their norms -------------
+// ---- out: outputs, edits, their norms and the scores -----------------------------
+// One workgroup per chunk: Q, K, T and P = Gam . QK^T once; R, delta and O for
+// each value block in turn; the scores from both blocks' |delta|^2.
 namespace {
 struct WOutSmem {
-    uint16_t q[KTILE];   // Q rows; delta^T hi (row stride LDB) from phase 2
-    uint16_t k[KTILE];   // K rows; delta^T lo from phase 2
+    uint16_t q[KTILE];   // Q rows
+    uint16_t k[KTILE];   // K rows
     uint16_t st[KTILE];  // S0^T rows of block vb ([v][k]); O rows (LDB) in phase 3
-    uint16_t vt[TILE];   // V_vb^T, then R^T lo; with tb: delta f32 rows from phase 3
-    uint16_t tb[TILE];   // T rows
+    uint16_t vt[TILE];   // V_vb^T, then R^T lo; with rt: delta f32 rows in phase 3
     uint16_t rt[TILE];   // R^T hi
+    uint16_t tb[TILE];   // T rows
     uint16_t pt[TILE], ptl[TILE];  // P^T hi/lo
+    uint16_t dt[TILE], dl[TILE];   // delta^T hi/lo of block vb
     GateLds gl;
     float kk[NW][C];
-    float dd[2][C];
+    float dd[NVB][2][C];
 };
 }  // namespace
 
 __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a) {
     __shared__ WOutSmem sm;
-    int ci, vb;
-    if (!chunk_block(blockIdx.x, a.B * a.H * a.nc, ci, vb)) return;
     uint16_t *Qs = sm.q, *Ks = sm.k, *Vt = sm.vt, *Tb = sm.tb, *St = sm.st, *Rt = sm.rt;
-    uint16_t *Pt = sm.pt, *Ptl = sm.ptl;
-    uint16_t *Dt = sm.q, *Dl = sm.k;  // over Q/K after phase 1
-    uint16_t *Os = sm.st;             // over S0^T after phase 2
+    uint16_t *Pt = sm.pt, *Ptl = sm.ptl, *Dt = sm.dt, *Dl = sm.dl;
+    uint16_t *Os = sm.st;  // over S0^T after phase 2
+    float *Df = reinterpret_cast<float *>(sm.vt);  // over V^T/R^T lo and R^T hi after phase 2
+    static_assert(C * LDF * sizeof(float) <= 2 * TILE * sizeof(uint16_t), "delta over vt+rt");
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, t0 = c * C, tg = t0 + t;
     const int tm = w >> 1, tn0 = 2 * (w & 1);
     const GateBlock *gb = a.ck_gate + ci;
     const bool inb = tg < a.T;
     const Row2 qr = load_row2(a.q, a.qs, b, tg, h, cb, inb);
     const Row2 kr = load_row2(a.k, a.ks, b, tg, h, cb, inb);
-    const uint4 vr = load8(a.v + 64 * vb, a.vs, b, tg, h, cb, inb);
-    const Mat2 s0r = load_mat2(a.ck_state + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
+    uint4 vr = load8(a.v, a.vs, b, tg, h, cb, inb);
+    Mat2 s0r = load_mat2(a.ck_state + (int64_t)ci * KD * KD, tid);
     const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
     const int sg = gb->seg[t];
     const uint4 trw =
         *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C + (tid >> 3) * C + 8 * (tid & 7));
+    const bool on = va != 0.f;
     {
-        const bool on = va != 0.f;
         const Row2 k8 = mask_row2(kr, on);
         put_row2(Qs, t, cb, mask_row2(qr, on));
         put_row2(Ks, t, cb, k8);
         put_col8(Vt, t, cb, mask8(vr, on));
         put_mat2(St, s0r, tid);
+        *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
         float ksq = 0.f;
 #pragma unroll
         for (int i = 0; i < NKB; ++i) ksq += sq8(k8.p[i]);
@@ -276,124 +272,132 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a) {
         if (w == 0) gates_derive(sm.gl, G, be, va, sg);
     }
     __syncthreads();
-    // Phase 1: R (-> Rt, lo over Vt), P (hi/lo), and gam Q S0 kept in registers.
-    f32x4 qs[2] = {zero4(), zero4()};
-    {
-        f32x4 x[2] = {zero4(), zero4()};
-        gemm2<KD, LDK, LDK>(x, &Ks[(16 * tm) * LDK], St, tn0);
-        gemm2<KD, LDK, LDK>(qs, &Qs[(16 * tm) * LDK], St, tn0);
+    const RowGates rg = row_gates(sm.gl, tm);
+    {  // P = Gam . QK^T (causal tiles) -> P^T hi/lo, once for both blocks
         f32x4 pq[2] = {zero4(), zero4()};
         if (tn0 <= tm) gemm2<KD, LDK, LDK>(pq, &Qs[(16 * tm) * LDK], Ks, tn0);
-        const RowGates rg = row_gates(sm.gl, tm);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int ss = 16 * (tn0 + j) + acc_col();
             const float Gs = sm.gl.G[ss];
             const int sgs = sm.gl.seg[ss];
-            uint16_t *vt = &Vt[(16 * (tn0 + j)) * LDB + 16 * tm];
-            float vv[4];
-            ld4_bf16(vt + acc_col() * LDB + 4 * (lane_id() >> 4), vv);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tt = 16 * tm + acc_row(i);
-                x[j][i] = rg.beta[i] * (vv[i] - rg.gam[i] * x[j][i]);
-                qs[j][i] *= rg.gam[i];
                 pq[j][i] *= (ss <= tt && rg.seg[i] == sgs) ? __expf(rg.G[i] - Gs) : 0.f;
             }
-            store_tile_t_split(&Rt[(16 * (tn0 + j)) * LDB + 16 * tm], vt, LDB, x[j]);
             store_tile_t_split(&Pt[(16 * (tn0 + j)) * LDB + 16 * tm],
                                &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq[j]);
         }
     }
-    *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
-    __syncthreads();
-    // Phase 2: delta = T R (-> Dt/Dl over the Q/K tiles) and |delta_t|^2 of the block.
-    f32x4 dlt[2] = {zero4(), zero4()};
-    {
-        gemm2(dlt, &Tb[(16 * tm) * LDB], Rt, tn0);
-        gemm2(dlt, &Tb[(16 * tm) * LDB], Vt, tn0);
-        float p[4];
+#pragma unroll 1
+    for (int vb = 0; vb < NVB; ++vb) {
+        if (vb > 0) {
+            vr = load8(a.v + 64 * vb, a.vs, b, tg, h, cb, inb);
+            s0r = load_mat2(a.ck_state + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
+            __syncthreads();  // the previous block's O and delta rows are stored
+            put_col8(Vt, t, cb, mask8(vr, on));
+            put_mat2(St, s0r, tid);
+            __syncthreads();
+        }
+        // Phase 1: R (-> Rt, lo over Vt) and gam Q S0 kept in registers.
+        f32x4 qs[2] = {zero4(), zero4()};
+        {
+            f32x4 x[2] = {zero4(), zero4()};
+            gemm2<KD, LDK, LDK>(x, &Ks[(16 * tm) * LDK], St, tn0);
+            gemm2<KD, LDK, LDK>(qs, &Qs[(16 * tm) * LDK], St, tn0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p[i] = dlt[0][i] * dlt[0][i] + dlt[1][i] * dlt[1][i];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            store_tile_t_split(&Dt[(16 * (tn0 + j)) * LDB + 16 * tm],
-                               &Dl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, dlt[j]);
-        row_reduce_store(p, sm.dd[w & 1], tm);
-    }
-    __syncthreads();
-    float *Df = reinterpret_cast<float *>(sm.vt);  // over V^T/R^T-lo and T, dead from here on
-    static_assert(C * LDF * sizeof(float) <= 2 * TILE * sizeof(uint16_t), "delta over vt+tb");
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            Df[(16 * tm + acc_row(i)) * LDF + 16 * (tn0 + j) + acc_col()] = dlt[j][i];
-    // Phase 3: O = gam Q S0 + P delta, staged through LDS for coalesced stores.
-    {
-        f32x4 x[2] = {qs[0], qs[1]};
-        gemm2_atr(x, Pt, 16 * tm, Dt, tn0);
-        gemm2_atr(x, Pt, 16 * tm, Dl, tn0);
-        gemm2_atr(x, Ptl, 16 * tm, Dt, tn0);
-        if (a.out_bf16) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) store_tile_rm(&Os[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, x[j]);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 2; ++j) {
+                uint16_t *vt = &Vt[(16 * (tn0 + j)) * LDB + 16 * tm];
+                float vv[4];
+                ld4_bf16(vt + acc_col() * LDB + 4 * (lane_id() >> 4), vv);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int tq = t0 + 16 * tm + acc_row(i);
-                    if (tq < a.T)
-                        reinterpret_cast<float *>(a.out)[(((int64_t)b * a.T + tq) * a.H + h) * KD +
-                                                         64 * vb + 16 * (tn0 + j) + acc_col()] = x[j][i];
+                    x[j][i] = rg.beta[i] * (vv[i] - rg.gam[i] * x[j][i]);
+                    qs[j][i] *= rg.gam[i];
                 }
+                store_tile_t_split(&Rt[(16 * (tn0 + j)) * LDB + 16 * tm], vt, LDB, x[j]);
+            }
+        }
+        __syncthreads();
+        // Phase 2: delta = T R (-> Dt/Dl) and |delta_t|^2 of the block.
+        f32x4 dlt[2] = {zero4(), zero4()};
+        {
+            gemm2(dlt, &Tb[(16 * tm) * LDB], Rt, tn0);
+            gemm2(dlt, &Tb[(16 * tm) * LDB], Vt, tn0);
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p[i] = dlt[0][i] * dlt[0][i] + dlt[1][i] * dlt[1][i];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                store_tile_t_split(&Dt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                                   &Dl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, dlt[j]);
+            row_reduce_store(p, sm.dd[vb][w & 1], tm);
+        }
+        __syncthreads();
+        // delta (f32 rows) over the dead R^T tiles; O = gam Q S0 + P delta over S0^T.
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                Df[(16 * tm + acc_row(i)) * LDF + 16 * (tn0 + j) + acc_col()] = dlt[j][i];
+        {
+            f32x4 x[2] = {qs[0], qs[1]};
+            gemm2_atr(x, Pt, 16 * tm, Dt, tn0);
+            gemm2_atr(x, Pt, 16 * tm, Dl, tn0);
+            gemm2_atr(x, Ptl, 16 * tm, Dt, tn0);
+            if (a.out_bf16) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) store_tile_rm(&Os[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, x[j]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int tq = t0 + 16 * tm + acc_row(i);
+                        if (tq < a.T)
+                            reinterpret_cast<float *>(a.out)[(((int64_t)b * a.T + tq) * a.H + h) * KD +
+                                                             64 * vb + 16 * (tn0 + j) + acc_col()] = x[j][i];
+                    }
+            }
+        }
+        __syncthreads();
+        {
+            const int r = tid >> 3, c0 = 8 * (tid & 7), tq = t0 + r;
+            float *dck = a.ck_delta + (int64_t)ci * C * KD + r * KD + 64 * vb + c0;
+            *reinterpret_cast<float4 *>(dck) = *reinterpret_cast<const float4 *>(&Df[r * LDF + c0]);
+            *reinterpret_cast<float4 *>(dck + 4) = *reinterpret_cast<const float4 *>(&Df[r * LDF + c0 + 4]);
+            if (a.out_bf16 && tq < a.T)
+                *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.out) +
+                                           (((int64_t)b * a.T + tq) * a.H + h) * KD + 64 * vb + c0) =
+                    *reinterpret_cast<const uint4 *>(&Os[r * LDB + c0]);
         }
     }
-    if (tid < 64) {  // |k_t|^2 (block 0) and this block's |delta_t|^2 for the scores
-        float kk = 0.f;
+    // |k_t|^2 and each block's |delta_t|^2 (the backward's score terms) and the
+    // scores score_t = |k_t| |delta_t| (0 on padding).
+    if (tid < 64) {
+        float kk = 0.f, dd = 0.f;
 #pragma unroll
         for (int q = 0; q < NW; ++q) kk += sm.kk[q][t];
-        if (vb == 0) a.ck_kk[(int64_t)ci * C + t] = kk;
-        a.ck_ddp[((int64_t)ci * NVB + vb) * C + t] = sm.dd[0][t] + sm.dd[1][t];
-    }
-    __syncthreads();
-    {
-        const int r = tid >> 3, c0 = 8 * (tid & 7), tq = t0 + r;
-        float *dck = a.ck_delta + (int64_t)ci * C * KD + r * KD + 64 * vb + c0;
-        *reinterpret_cast<float4 *>(dck) = *reinterpret_cast<const float4 *>(&Df[r * LDF + c0]);
-        *reinterpret_cast<float4 *>(dck + 4) = *reinterpret_cast<const float4 *>(&Df[r * LDF + c0 + 4]);
-        if (a.out_bf16 && tq < a.T)
-            *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.out) +
-                                       (((int64_t)b * a.T + tq) * a.H + h) * KD + 64 * vb + c0) =
-                *reinterpret_cast<const uint4 *>(&Os[r * LDB + c0]);
-    }
-}
-
-// Scores from the blocks' partial norms: score_t = |k_t| |delta_t| on valid
-// tokens, 0 on padding.
-__global__ void __launch_bounds__(256) wide_score_kernel(ChunkArgs a) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t nch = (int64_t)a.B * a.H * a.nc;
-    if (i >= nch * C) return;
-    const int64_t ci = i / C;
-    const int t = (int)(i % C), bh = (int)(ci / a.nc), c = (int)(ci % a.nc);
-    const int b = bh / a.H, h = bh % a.H, tg = c * C + t;
-    if (tg >= a.T) return;
-    float dd = 0.f;
+        a.ck_kk[(int64_t)ci * C + t] = kk;
 #pragma unroll
-    for (int vb = 0; vb < NVB; ++vb) dd += a.ck_ddp[(ci * NVB + vb) * C + t];
-    const float kk = a.ck_kk[ci * C + t];
-    a.scores[((int64_t)b * a.T + tg) * a.H + h] = a.ck_gate[ci].val[t] != 0.f ? sqrtf(kk * dd) : 0.f;
+        for (int vb = 0; vb < NVB; ++vb) {
+            const float d = sm.dd[vb][0][t] + sm.dd[vb][1][t];
+            a.ck_ddp[((int64_t)ci * NVB + vb) * C + t] = d;
+            dd += d;
+        }
+        if (tg < a.T) a.scores[((int64_t)b * a.T + tg) * a.H + h] = sm.gl.val[t] != 0.f ? sqrtf(kk * dd) : 0.f;
+    }
 }
 
-// ---- backward prep: N of the adjoint map, value block vb -------------------------
+// ---- backward prep: N of the adjoint map ---------------------------------------
 // dS0 = M dS_C + N with M = A_c^T and N = Y - W^T X, Y = (gam Q)^T dO,
 // X = P^T dO + diag(c) delta, W = T diag(beta gam) K (formed again from T and K
-// with prep's operands and products); the block's 64 columns of N per workgroup.
+// with prep's operands and products).  One workgroup per chunk: W and P once,
+// Y, X and N for both value blocks.
 namespace {
 struct WBPrepSmem {
-    uint16_t q[KTILE], k[KTILE];  // Q, K rows; X^T hi/lo (row stride LDB) from phase 2
+    uint16_t q[KTILE], k[KTILE];  // Q, K rows; X^T hi/lo of block 0 (row stride LDB) from phase 2
     union {
         struct {
             uint16_t qg[KTILE];   // gam Q rows
@@ -402,7 +406,7 @@ struct WBPrepSmem {
         } p1;
         uint16_t wt[2][KD * LDB];  // W^T hi/lo ([k][t]) from phase 2
     } u;
-    uint16_t dos[TILE];            // dO rows of block vb
+    uint16_t dos[NVB][TILE];       // dO rows of each block; X^T hi/lo of block 1 from phase 2
     uint16_t pt[TILE], ptl[TILE];  // P^T hi/lo
     GateLds gl;
     float dsc[C];
@@ -411,44 +415,39 @@ struct WBPrepSmem {
 
 __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a) {
     __shared__ WBPrepSmem sm;
-    int ci, vb;
-    if (!chunk_block(blockIdx.x, a.B * a.H * a.nc, ci, vb)) return;
     uint16_t *Qs = sm.q, *Ks = sm.k, *QGs = sm.u.p1.qg, *Tb = sm.u.p1.tb, *KBGs = sm.u.p1.kbg;
-    uint16_t *dOs = sm.dos, *Pt = sm.pt, *Ptl = sm.ptl;
-    uint16_t *Xt = sm.q, *Xtl = sm.k;                  // over Q/K after phase 1
-    uint16_t *Wt = sm.u.wt[0], *Wtl = sm.u.wt[1];      // over the phase-1 operands
+    uint16_t *Pt = sm.pt, *Ptl = sm.ptl;
+    uint16_t *Wt = sm.u.wt[0], *Wtl = sm.u.wt[1];  // over the phase-1 operands
+    // X^T hi/lo of each block, over Q/K (block 0) and the dO rows (block 1) after phase 2
+    uint16_t *Xt[NVB] = {sm.q, sm.dos[0]}, *Xtl[NVB] = {sm.k, sm.dos[1]};
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
     const int tg = c * C + t;
     const bool inb = tg < a.T;
     const GateBlock *gb = a.ck_gate + ci;
-    const float *dck = a.ck_delta + (int64_t)ci * C * KD + 64 * vb;
+    const float *dck = a.ck_delta + (int64_t)ci * C * KD;
     const int r0 = 16 * tm + 4 * (lane_id() >> 4);
     const Row2 qr = load_row2(a.q, a.qs, b, tg, h, cb, inb);
     const Row2 kr = load_row2(a.k, a.ks, b, tg, h, cb, inb);
-    const uint4 dor =
-        a.dout ? load8(a.dout + 64 * vb, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
+    uint4 dor[NVB];
+#pragma unroll
+    for (int vb = 0; vb < NVB; ++vb)
+        dor[vb] = a.dout ? load8(a.dout + 64 * vb, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
     const uint4 trow = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C +
                                                          (tid >> 3) * C + 8 * (tid & 7));
     const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
     const int sg = gb->seg[t];
     const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
     const bool score_adj = a.dscores != nullptr;
-    float dl[2][4] = {};  // delta at this wave's X tile
-    if (score_adj) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dl[j][i] = dck[(r0 + i) * KD + 16 * (tn0 + j) + acc_col()];
-    }
     {
         const bool on = va != 0.f;
         const float gam = sg == 0 ? __expf(G) : 0.f, bg = be * gam;
         const Row2 q8 = mask_row2(qr, on), k8 = mask_row2(kr, on);
         put_row2(Qs, t, cb, q8);
         put_row2(Ks, t, cb, k8);
-        put_row8(dOs, t, cb, mask8(dor, on));
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) put_row8(sm.dos[vb], t, cb, mask8(dor[vb], on));
 #pragma unroll
         for (int i = 0; i < NKB; ++i) {
             put_row8(QGs, t, cb + 8 * i, scale8(q8.p[i], gam), LDK);
@@ -462,20 +461,24 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a) {
     }
     __syncthreads();
     const RowGates rg = row_gates(sm.gl, tm);
-    // Phase 1: W = T (beta gam K) and Y = (gam Q)^T dO_vb in registers; P^T hi/lo.
-    f32x4 wacc[NKB][2], yacc[NKB][2];
+    // Phase 1: W = T (beta gam K) and both blocks' Y = (gam Q)^T dO in registers; P^T hi/lo.
+    f32x4 wacc[NKB][2], yacc[NVB][NKB][2];
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-        wacc[kb][0] = wacc[kb][1] = yacc[kb][0] = yacc[kb][1] = zero4();
+        wacc[kb][0] = wacc[kb][1] = zero4();
         gemm2_tr<64, LDB, LDK>(wacc[kb], &Tb[(16 * tm) * LDB], KBGs, tn0 + 4 * kb);
         const int mt = tm + 4 * kb;  // row tile of Y (key channel)
 #pragma unroll
-        for (int r = 0; r < 64; r += 32) {  // Y[k][v] = sum_t (gam Q)[t][k] dO[t][v]
-            const bf16x8_t x = frag_tr<LDK>(QGs, r, 16 * mt);
+        for (int vb = 0; vb < NVB; ++vb) {
+            yacc[vb][kb][0] = yacc[vb][kb][1] = zero4();
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                yacc[kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    x, frag_tr(dOs, r, 16 * (tn0 + j)), yacc[kb][j], 0, 0, 0);
+            for (int r = 0; r < 64; r += 32) {  // Y[k][v] = sum_t (gam Q)[t][k] dO[t][v]
+                const bf16x8_t x = frag_tr<LDK>(QGs, r, 16 * mt);
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    yacc[vb][kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        x, frag_tr(sm.dos[vb], r, 16 * (tn0 + j)), yacc[vb][kb][j], 0, 0, 0);
+            }
         }
     }
     {
@@ -496,52 +499,66 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a) {
         }
     }
     __syncthreads();
-    // Phase 2: W^T hi/lo; X = P^T dO_vb + diag(c) delta_vb, stored transposed (hi/lo).
+    // Phase 2: W^T hi/lo; both blocks' X = P^T dO + diag(c) delta in registers, then
+    // stored transposed (hi/lo) once every wave has read the dO rows.
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
             store_tile_t_split(&Wt[(16 * (tn0 + 4 * kb + j)) * LDB + 16 * tm],
                                &Wtl[(16 * (tn0 + 4 * kb + j)) * LDB + 16 * tm], LDB, wacc[kb][j]);
-    {
-        f32x4 x[2] = {zero4(), zero4()};
-        gemm2_tr(x, &Pt[(16 * tm) * LDB], dOs, tn0);  // B[v][t] = dO[t][v]
-        gemm2_tr(x, &Ptl[(16 * tm) * LDB], dOs, tn0);
+    f32x4 xx[NVB][2];
+    float cs[4] = {0.f, 0.f, 0.f, 0.f};
+    if (score_adj) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ss = r0 + i;
+            float dq = 0.f;
+#pragma unroll
+            for (int v2 = 0; v2 < NVB; ++v2) dq += a.ck_ddp[((int64_t)ci * NVB + v2) * C + ss];
+            const float nk = sqrtf(a.ck_kk[(int64_t)ci * C + ss]), nd = sqrtf(dq);
+            cs[i] = (nk > 0.f && nd > 0.f) ? sm.dsc[ss] * nk / nd : 0.f;
+        }
+    }
+#pragma unroll
+    for (int vb = 0; vb < NVB; ++vb) {
+        xx[vb][0] = xx[vb][1] = zero4();
+        gemm2_tr(xx[vb], &Pt[(16 * tm) * LDB], sm.dos[vb], tn0);  // B[v][t] = dO[t][v]
+        gemm2_tr(xx[vb], &Ptl[(16 * tm) * LDB], sm.dos[vb], tn0);
         if (score_adj) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int ss = r0 + i;
-                float dq = 0.f;
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int v2 = 0; v2 < NVB; ++v2) dq += a.ck_ddp[((int64_t)ci * NVB + v2) * C + ss];
-                const float nk = sqrtf(a.ck_kk[(int64_t)ci * C + ss]), nd = sqrtf(dq);
-                const float cs = (nk > 0.f && nd > 0.f) ? sm.dsc[ss] * nk / nd : 0.f;
-#pragma unroll
-                for (int j = 0; j < 2; ++j) x[j][i] += cs * dl[j][i];
-            }
+                for (int i = 0; i < 4; ++i)
+                    xx[vb][j][i] += cs[i] * dck[(r0 + i) * KD + 64 * vb + 16 * (tn0 + j) + acc_col()];
         }
+    }
+    __syncthreads();  // Q, K and dO rows read: X^T takes their tiles
+#pragma unroll
+    for (int vb = 0; vb < NVB; ++vb)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-            store_tile_t_split(&Xt[(16 * (tn0 + j)) * LDB + 16 * tm],
-                               &Xtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
-    }
+            store_tile_t_split(&Xt[vb][(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &Xtl[vb][(16 * (tn0 + j)) * LDB + 16 * tm], LDB, xx[vb][j]);
     __syncthreads();
-    // Phase 3: N = Y - W^T X for the block's 64 columns, all KD rows.
+    // Phase 3: N = Y - W^T X, both blocks' 64 columns, all KD rows.
     float *Nt = a.ws_n + (int64_t)ci * KD * KD;  // N transposed: Nt[col][row]
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-        const int mt = tm + 4 * kb;
-        f32x4 x[2] = {zero4(), zero4()};
-        gemm2(x, &Wt[(16 * mt) * LDB], Xt, tn0);
-        gemm2(x, &Wt[(16 * mt) * LDB], Xtl, tn0);
-        gemm2(x, &Wtl[(16 * mt) * LDB], Xt, tn0);
+    for (int vb = 0; vb < NVB; ++vb)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-            *reinterpret_cast<float4 *>(&Nt[(64 * vb + 16 * (tn0 + j) + acc_col()) * KD + 16 * mt +
-                                            acc_row(0)]) =
-                make_float4(yacc[kb][j][0] - x[j][0], yacc[kb][j][1] - x[j][1],
-                            yacc[kb][j][2] - x[j][2], yacc[kb][j][3] - x[j][3]);
-    }
+        for (int kb = 0; kb < NKB; ++kb) {
+            const int mt = tm + 4 * kb;
+            f32x4 x[2] = {zero4(), zero4()};
+            gemm2(x, &Wt[(16 * mt) * LDB], Xt[vb], tn0);
+            gemm2(x, &Wt[(16 * mt) * LDB], Xtl[vb], tn0);
+            gemm2(x, &Wtl[(16 * mt) * LDB], Xt[vb], tn0);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                *reinterpret_cast<float4 *>(&Nt[(64 * vb + 16 * (tn0 + j) + acc_col()) * KD + 16 * mt +
+                                                acc_row(0)]) =
+                    make_float4(yacc[vb][kb][j][0] - x[j][0], yacc[vb][kb][j][1] - x[j][1],
+                                yacc[vb][kb][j][2] - x[j][2], yacc[vb][kb][j][3] - x[j][3]);
+        }
 }
 
 // ---- bgrad: every gradient of one chunk ------------------------------------------
@@ -1027,16 +1044,14 @@ static hipError_t wide_scan(const ChunkArgs &a, bool reverse, hipStream_t stream
 hipError_t launch_wide_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
     const int nch = a.B * a.H * a.nc;
     wmark(ev, 0, stream);
-    hipLaunchKernelGGL(wide_prep_kernel, chunk_block_grid(nch), dim3(NT), 0, stream, a);
+    hipLaunchKernelGGL(wide_prep_kernel, dim3(nch), dim3(NT), 0, stream, a);
     wmark(ev, 1, stream);
     wmark(ev, 2, stream);
     const hipError_t e = wide_scan(a, false, stream);
     if (e != hipSuccess) return e;
     wmark(ev, 3, stream);
     wmark(ev, 4, stream);
-    hipLaunchKernelGGL(wide_out_kernel, chunk_block_grid(nch), dim3(NT), 0, stream, a);
-    hipLaunchKernelGGL(wide_score_kernel, dim3((unsigned)(((int64_t)nch * C + 255) / 256)), dim3(256),
-                       0, stream, a);
+    hipLaunchKernelGGL(wide_out_kernel, dim3(nch), dim3(NT), 0, stream, a);
     wmark(ev, 5, stream);
     return hipGetLastError();
 }
@@ -1044,7 +1059,7 @@ hipError_t launch_wide_fwd(const ChunkArgs &a, hipStream_t stream, const hipEven
 hipError_t launch_wide_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
     const int nch = a.B * a.H * a.nc;
     wmark(ev, 0, stream);
-    hipLaunchKernelGGL(wide_bprep_kernel, chunk_block_grid(nch), dim3(NT), 0, stream, a);
+    hipLaunchKernelGGL(wide_bprep_kernel, dim3(nch), dim3(NT), 0, stream, a);
     wmark(ev, 1, stream);
     wmark(ev, 2, stream);
     const hipError_t e = wide_scan(a, true, stream);
