@@ -217,8 +217,8 @@ __global__ void __launch_bounds__(64 * (Cfg::NCW + Cfg::NPROD)) lr_scan_kernel(L
             uint16_t *cl = lo_out ? p.ckpt_lo + (cix * p.vd + colbase + 16 * w) * KD : nullptr;
 #pragma unroll
             for (int i = 0; i < Cfg::XS_BYTES / 1024; ++i) {
-                const int q = 64 * i + l, r = q / Cfg::XS_NCH, x = q % Cfg::XS_NCH;
-                const int off = r * Cfg::XS_NCH * 16 + ((x ^ lr_swz(r, Cfg::XS_NCH)) << 4);
+                const int q = 64 * i + l, r = q / Cfg::XS_NCH, y = q % Cfg::XS_NCH;
+                const int off = r * Cfg::XS_NCH * 16 + ((y ^ lr_swz(r, Cfg::XS_NCH)) << 4);
                 *reinterpret_cast<uint4 *>(ck + 8 * q) = *reinterpret_cast<const uint4 *>(xsw + off);
                 if (lo_out)
                     *reinterpret_cast<uint4 *>(cl + 8 * q) = *reinterpret_cast<const uint4 *>(xsw + Cfg::XS_BYTES + off);
@@ -338,13 +338,11 @@ static hipError_t launch_lr(const LrScanArgs &p, hipStream_t stream) {
     const int nwg = p.vd / (16 * Cfg::NCW);
     const dim3 grid(8 * nwg * ((p.B * p.H + 7) / 8)), block(64 * (Cfg::NCW + Cfg::NPROD));
     const size_t lds = (size_t)Cfg::LDS_BYTES;
-    static bool attr_set = false;  // the kernel's dynamic LDS limit, set once per process
-    if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute((const void *)lr_scan_kernel<Cfg>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    // The kernel's dynamic LDS limit, raised once per process (a function-local
+    // static: initialised exactly once even with concurrent first callers).
+    static const hipError_t attr = hipFuncSetAttribute((const void *)lr_scan_kernel<Cfg>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
     hipLaunchKernelGGL(lr_scan_kernel<Cfg>, grid, block, lds, stream, p);
     return hipGetLastError();
 }
