@@ -602,7 +602,7 @@ hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream, const hipEve
 namespace {
 
 struct BPrepSmem {  // fits twice in one CU's LDS
-    uint16_t slot[8][TILE];
+    uint16_t slot[7][TILE];
     GateLds gl;
     float kk[NW][C];
     float dd[NW][C];
@@ -634,12 +634,12 @@ __device__ __forceinline__ uint4 load_mat(const uint16_t *src, int tid) {
 // products as prep, so the same bits) and builds N for every chunk in parallel.
 __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     __shared__ BPrepSmem sm;
-    // Tiles are staged as rows (gam Q scaled per token) and read across with
-    // transpose reads where a product needs them transposed.
-    uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *QGs = sm.slot[2], *dOs = sm.slot[3];
-    uint16_t *Tb = sm.slot[4], *KBGs = sm.slot[5], *Pt = sm.slot[6], *Ptl = sm.slot[7];
+    // Tiles are staged as rows and read across with transpose reads where a
+    // product needs them transposed.
+    uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *dOs = sm.slot[2];
+    uint16_t *Tb = sm.slot[3], *KBGs = sm.slot[4], *Pt = sm.slot[5], *Ptl = sm.slot[6];
     uint16_t *Xt = sm.slot[0], *Xtl = sm.slot[1];  // over Q/K after phase 1
-    uint16_t *Wt = sm.slot[4], *Wtl = sm.slot[5];  // over T and beta gam K after phase 1
+    uint16_t *Wt = sm.slot[3], *Wtl = sm.slot[4];  // over T and beta gam K after phase 1
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
@@ -681,16 +681,13 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
         put_row8(Ks, t, cb, kp.u);
         put_row8(dOs, t, cb, mask8(dor, on));
         float ksq = 0.f;
-        uint32_t qg[4], kb[4];
+        uint32_t kb[4];
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-            const float q0 = bf16_val(qp.h[e]), q1 = bf16_val(qp.h[e + 1]);
             const float k0 = bf16_val(kp.h[e]), k1 = bf16_val(kp.h[e + 1]);
-            qg[e / 2] = bf16_pack2(gam * q0, gam * q1);
             kb[e / 2] = bf16_pack2(bg * k0, bg * k1);
             ksq += k0 * k0 + k1 * k1;
         }
-        put_row8(QGs, t, cb, make_uint4(qg[0], qg[1], qg[2], qg[3]));
         put_row8(KBGs, t, cb, make_uint4(kb[0], kb[1], kb[2], kb[3]));
         *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trow;
         if (score_adj) sm.kk[cb][t] = ksq;
@@ -708,12 +705,15 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     {
         f32x4 pq[2] = {zero4(), zero4()};
 #pragma unroll
-        for (int r = 0; r < 64; r += 32) {  // Y[k][v] = sum_t (gam Q)[t][k] dO[t][v]
-            const bf16x8_t x = frag_tr(QGs, r, 16 * tm);
+        for (int r = 0; r < 64; r += 32) {  // Y[k][v] = sum_t (gam Q)[t][k] dO[t][v], gam Q hi/lo
+            bf16x8_t x, xl;
+            frag_tr_scaled_split(Qs, sm.gl.gam, r, 16 * tm, x, xl);
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                yacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, frag_tr(dOs, r, 16 * (tn0 + j)),
-                                                                  yacc[j], 0, 0, 0);
+            for (int j = 0; j < 2; ++j) {
+                const bf16x8_t ob = frag_tr(dOs, r, 16 * (tn0 + j));
+                yacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, ob, yacc[j], 0, 0, 0);
+                yacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, ob, yacc[j], 0, 0, 0);
+            }
         }
         if (tn0 <= tm) gemm2(pq, &Qs[(16 * tm) * LDB], Ks, tn0);
 #pragma unroll

@@ -258,6 +258,31 @@ __device__ __forceinline__ void gemm2_atr(f32x4 (&acc)[2], const uint16_t *Z, in
     }
 }
 
+// frag_tr(Z, r0, c0) with row r of Z scaled by s[r], as a two-term bf16 split
+// (hi + lo carries ~16 mantissa bits of s[r] Z[r][c]).  Lane (n, g) holds rows
+// r0 + 8g .. r0 + 8g + 7, so it reads those eight scales (s 16-byte aligned,
+// r0 a multiple of 8).  Used where a per-token scale falls on the reduction
+// index, so it cannot be applied to the product's accumulator instead.
+template <int LDZ = LDB>
+__device__ __forceinline__ void frag_tr_scaled_split(const uint16_t *Z, const float *s, int r0, int c0,
+                                                     bf16x8_t &hi, bf16x8_t &lo) {
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    const v8s z = __builtin_bit_cast(v8s, frag_tr<LDZ>(Z, r0, c0));
+    const float *sr = s + r0 + 8 * (lane_id() >> 4);
+    const float4 s0 = *reinterpret_cast<const float4 *>(sr), s1 = *reinterpret_cast<const float4 *>(sr + 4);
+    const float sc[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    v8s h, o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        uint16_t hh, ll;
+        split_bf16(sc[e] * bf16_val((uint16_t)z[e]), hh, ll);
+        h[e] = (short)hh;
+        o[e] = (short)ll;
+    }
+    hi = __builtin_bit_cast(bf16x8_t, h);
+    lo = __builtin_bit_cast(bf16x8_t, o);
+}
+
 // T = (I + A)^-1 for the strictly lower 64x64 A in Af; result in Tf (lower
 // blocks).  Called by all waves; ends with a barrier.  Blocks are 16x16:
 //   1. diagonal blocks T_bb = (I + A_bb)^-1 by forward substitution (waves 0-3,

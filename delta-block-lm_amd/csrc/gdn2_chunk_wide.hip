@@ -400,7 +400,6 @@ struct WBPrepSmem {
     uint16_t q[KTILE], k[KTILE];  // Q, K rows; X^T hi/lo of block 0 (row stride LDB) from phase 2
     union {
         struct {
-            uint16_t qg[KTILE];   // gam Q rows
             uint16_t tb[TILE];    // T rows
             uint16_t kbg[KTILE];  // beta gam K rows
         } p1;
@@ -415,7 +414,7 @@ struct WBPrepSmem {
 
 __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a) {
     __shared__ WBPrepSmem sm;
-    uint16_t *Qs = sm.q, *Ks = sm.k, *QGs = sm.u.p1.qg, *Tb = sm.u.p1.tb, *KBGs = sm.u.p1.kbg;
+    uint16_t *Qs = sm.q, *Ks = sm.k, *Tb = sm.u.p1.tb, *KBGs = sm.u.p1.kbg;
     uint16_t *Pt = sm.pt, *Ptl = sm.ptl;
     uint16_t *Wt = sm.u.wt[0], *Wtl = sm.u.wt[1];  // over the phase-1 operands
     // X^T hi/lo of each block, over Q/K (block 0) and the dO rows (block 1) after phase 2
@@ -449,10 +448,7 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a) {
 #pragma unroll
         for (int vb = 0; vb < NVB; ++vb) put_row8(sm.dos[vb], t, cb, mask8(dor[vb], on));
 #pragma unroll
-        for (int i = 0; i < NKB; ++i) {
-            put_row8(QGs, t, cb + 8 * i, scale8(q8.p[i], gam), LDK);
-            put_row8(KBGs, t, cb + 8 * i, scale8(k8.p[i], bg), LDK);
-        }
+        for (int i = 0; i < NKB; ++i) put_row8(KBGs, t, cb + 8 * i, scale8(k8.p[i], bg), LDK);
         *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trow;
         if (w == 0) {
             gates_derive(sm.gl, G, be, va, sg);
@@ -469,16 +465,19 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a) {
         gemm2_tr<64, LDB, LDK>(wacc[kb], &Tb[(16 * tm) * LDB], KBGs, tn0 + 4 * kb);
         const int mt = tm + 4 * kb;  // row tile of Y (key channel)
 #pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) {
-            yacc[vb][kb][0] = yacc[vb][kb][1] = zero4();
+        for (int vb = 0; vb < NVB; ++vb) yacc[vb][kb][0] = yacc[vb][kb][1] = zero4();
 #pragma unroll
-            for (int r = 0; r < 64; r += 32) {  // Y[k][v] = sum_t (gam Q)[t][k] dO[t][v]
-                const bf16x8_t x = frag_tr<LDK>(QGs, r, 16 * mt);
+        for (int r = 0; r < 64; r += 32) {  // Y[k][v] = sum_t (gam Q)[t][k] dO[t][v], gam Q hi/lo
+            bf16x8_t x, xl;
+            frag_tr_scaled_split<LDK>(Qs, sm.gl.gam, r, 16 * mt, x, xl);
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    yacc[vb][kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        x, frag_tr(sm.dos[vb], r, 16 * (tn0 + j)), yacc[vb][kb][j], 0, 0, 0);
-            }
+            for (int vb = 0; vb < NVB; ++vb)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const bf16x8_t ob = frag_tr(sm.dos[vb], r, 16 * (tn0 + j));
+                    yacc[vb][kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, ob, yacc[vb][kb][j], 0, 0, 0);
+                    yacc[vb][kb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, ob, yacc[vb][kb][j], 0, 0, 0);
+                }
         }
     }
     {

@@ -254,3 +254,46 @@ def test_cw_alpha_zero_is_floored(dk):
     keep = np.ones(da.shape, bool)
     keep[0, 10, 0, :8] = False
     gate("dalpha (alpha > 0)", da[keep], og["alpha"][keep], TOL_BF16)
+
+
+def test_cw_many_heads(dk):
+    """Twelve (batch, head) sequences: more than one group of eight heads in the
+    scan's workgroup mapping, the last group partly empty."""
+    p = cw_problem(91, 3, 100, 4, masks=True)
+    r, grads, ran = _run(dk, p)
+    assert FWD_STAGES | BWD_STAGES <= ran
+    _check(p, r, grads)
+
+
+def _cw_slice(p, b, h):
+    """Sequence (b, h) of a cw_problem as a B = 1, H = 1 problem."""
+    out = {}
+    for n, x in p.items():
+        if x is None:
+            out[n] = None
+        elif n in ("initial", "dF"):      # [B, H, K, V]
+            out[n] = x[b:b + 1, h:h + 1]
+        elif x.ndim == 2:                 # [B, T]
+            out[n] = x[b:b + 1]
+        else:                             # [B, T, H, ...]
+            out[n] = x[b:b + 1, :, h:h + 1]
+    return out
+
+
+def test_cw_full_shape_oracle_slices(dk):
+    """The document-scan benchmark's head shape (B16 T512 H8: 128 heads, 32
+    chunks each) with masks, resets and an initial state; whole sequences cut
+    out of the batch against the f64 oracle."""
+    p = cw_problem(97, 16, 512, 8, masks=True)
+    r, grads, ran = _run(dk, p)
+    assert FWD_STAGES | BWD_STAGES <= ran
+    for b, h in [(0, 0), (15, 7), (9, 3)]:
+        s = _cw_slice(p, b, h)
+        (o_out, o_fin, o_sc), og = cw_oracle(s)
+        pad = (s["valid"] == 0)[:, :, None]
+        gate(f"output ({b},{h})", r.output[b:b + 1, :, h:h + 1], o_out, TOL_BF16, exact_zero=pad[..., None])
+        gate(f"final_state ({b},{h})", r.final_state[b:b + 1, h:h + 1], o_fin, TOL_BF16)
+        gate(f"scores ({b},{h})", r.scores[b:b + 1, :, h:h + 1, 0], o_sc, TOL_BF16, exact_zero=pad)
+        for n in ("q", "k", "v") + GATES:
+            gate(f"d{n} ({b},{h})", grads[n][b:b + 1, :, h:h + 1], og[n], TOL_BF16, exact_zero=pad[..., None])
+        gate(f"d_initial ({b},{h})", grads["initial"][b:b + 1, h:h + 1], og["initial"], TOL_BF16)

@@ -36,7 +36,7 @@ def _timed(dk, fn):
     return r, ran
 
 
-@pytest.mark.parametrize("B,T,H", [(1, 64, 1), (2, 200, 2), (1, 130, 3)])
+@pytest.mark.parametrize("B,T,H", [(1, 64, 1), (2, 200, 2), (1, 130, 3), (3, 130, 3)])
 @pytest.mark.parametrize("masks", [False, True])
 def test_wide_forward_matches_oracle(dk, B, T, H, masks):
     p = problem(B * 1000 + T + masks, B, T, H, masks=masks, K=D, V=D)
@@ -51,7 +51,7 @@ def test_wide_forward_matches_oracle(dk, B, T, H, masks):
     gate("scores", sc, o_sc, TOL_BF16, exact_zero=pad)
 
 
-@pytest.mark.parametrize("B,T,H", [(1, 64, 1), (2, 200, 2), (1, 130, 3)])
+@pytest.mark.parametrize("B,T,H", [(1, 64, 1), (2, 200, 2), (1, 130, 3), (3, 130, 3)])
 @pytest.mark.parametrize("masks", [False, True])
 def test_wide_backward_matches_oracle(dk, B, T, H, masks):
     p = problem(7 * B + T + masks, B, T, H, masks=masks, K=D, V=D)
