@@ -297,6 +297,10 @@ struct LrScanArgs {
 // kd x ct in {128 x 64, 64 x 16}; hipErrorInvalidValue for other shapes.
 hipError_t launch_lr_scan(const LrScanArgs &p, int kd, int ct, hipStream_t stream);
 
+// Compute units of the current device (queried once per device); sizes the
+// grids of the kernels that walk several chunks per workgroup.
+int device_cus();
+
 hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
 hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
 

@@ -28,6 +28,9 @@
 // as two-term bf16 splits (hi + lo); S0, T, Q, K, V as single bf16 terms.
 #include "gdn2_chunk_tile.h"
 
+#include <algorithm>
+#include <atomic>
+
 namespace gdn2 {
 
 namespace {
@@ -617,10 +620,71 @@ struct BGradSmem {
     float dsc[C];
     float g1[2][C], ku[2][C], b1[2][C], b2[2][C], zr[2][C], zc[4][C], dlam[2][C];
     float frob[NW];
+    // Per token, from phase G: dG without the chunk-end term, dbeta, lam dlam, and
+    // 1 where dg is kept (valid, not a reset); the |S0 dS| total.
+    float hdg[C], hdb[C], hld[C], hkeep[C];
+    float frs;
 };
 
 __device__ __forceinline__ uint4 load_mat(const uint16_t *src, int tid) {
     return *reinterpret_cast<const uint4 *>(src + (tid >> 3) * D + 8 * (tid & 7));
+}
+
+// One chunk's global inputs to bgrad, held in registers.  A workgroup walks
+// several chunks and loads the next chunk's inputs while it computes the
+// current one, in five parts spread over the phases so that no phase issues
+// more than a few memory instructions per wave (a burst of them stalls issue
+// for the whole CU).
+struct BgradIn {
+    uint4 q, k, dO, s0, ds;
+    float G, be, va, dsc;
+    int sg;
+    uint4 v, t;
+    float4 d0, d1;
+};
+
+struct ChunkPos {
+    int b, h, c;
+};
+__device__ __forceinline__ ChunkPos chunk_pos(const ChunkArgs &a, int ci) {
+    const int bh = ci / a.nc;
+    return ChunkPos{bh / a.H, bh % a.H, ci % a.nc};
+}
+
+// Part P of chunk ci's inputs: 0 q, k; 1 dO, S0^T; 2 dS^T, the gates, the score
+// adjoint; 3 V, T; 4 delta.  The loads take no branch, so that the compiler's
+// memory-counter waits stay exact across the chunk loop: a row past the
+// sequence end reads the last row (the gate block marks such tokens invalid,
+// and the staging zeroes invalid rows), a missing dO reads q (zeroed at the
+// staging) and a missing score adjoint reads the delta checkpoint, which holds
+// more than B*T*H floats (the value is then never used).
+template <int P>
+__device__ __forceinline__ void bgrad_load(const ChunkArgs &a, int ci, const ChunkPos &p, int tid,
+                                           BgradIn &x) {
+    const int t = tid & 63, cb = tid >> 6, tg = p.c * C + t;
+    const int tr = tg < a.T ? tg : a.T - 1;
+    if constexpr (P == 0) {
+        x.q = *reinterpret_cast<const uint4 *>(row_ptr(a.q, a.qs, p.b, tr, p.h) + 8 * cb);
+        x.k = *reinterpret_cast<const uint4 *>(row_ptr(a.k, a.ks, p.b, tr, p.h) + 8 * cb);
+    } else if constexpr (P == 1) {
+        const uint16_t *dop = a.dout ? a.dout : a.q;
+        const int64_t *dos = a.dout ? a.ds : a.qs;
+        x.dO = *reinterpret_cast<const uint4 *>(row_ptr(dop, dos, p.b, tr, p.h) + 8 * cb);
+        x.s0 = load_mat(a.ck_state + (int64_t)ci * D * D, tid);
+    } else if constexpr (P == 2) {
+        x.ds = load_mat(a.ws_dstate + (int64_t)ci * D * D, tid);
+        const GateBlock *gb = a.ck_gate + ci;
+        x.G = gb->G[t], x.be = gb->beta[t], x.va = gb->val[t];
+        x.sg = gb->seg[t];
+        x.dsc = (a.dscores ? a.dscores : a.ck_delta)[((int64_t)p.b * a.T + tr) * a.H + p.h];
+    } else if constexpr (P == 3) {
+        x.v = *reinterpret_cast<const uint4 *>(row_ptr(a.v, a.vs, p.b, tr, p.h) + 8 * cb);
+        x.t = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C + (tid >> 3) * C + 8 * (tid & 7));
+    } else {
+        const float *dck = a.ck_delta + (int64_t)ci * C * D + t * D + 8 * cb;
+        x.d0 = *reinterpret_cast<const float4 *>(dck);
+        x.d1 = *reinterpret_cast<const float4 *>(dck + 4);
+    }
 }
 
 }  // namespace
@@ -782,6 +846,34 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     }
 }
 
+// The stores of one bgrad chunk.  dq, dk, dv: lane (token 16 (w%4) + l%16,
+// channels 32 (w/4) + 8 (l/16) ..) reads its eight channels across the
+// transposed gradient tile (every lane runs the transpose reads) and stores one
+// 16-byte row piece; dg, dbeta from wave 0's registers (lane l: token 63 - l).
+__device__ __forceinline__ bf16x8_t bgrad_grad_frag(const uint16_t *tile, int w) {
+    return frag_tr(tile, 32 * (w >> 2), 16 * (w & 3));
+}
+__device__ __forceinline__ void bgrad_store_rows(const ChunkArgs &a, const ChunkPos &p, int w,
+                                                 bf16x8_t gq, bf16x8_t gk, bf16x8_t gv) {
+    const int l = lane_id();
+    const int tq = p.c * C + 16 * (w & 3) + (l & 15);
+    if (tq < a.T) {
+        const int64_t o = (((int64_t)p.b * a.T + tq) * a.H + p.h) * D + 32 * (w >> 2) + 8 * (l >> 4);
+        if (a.dq) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dq) + o) = gq;
+        if (a.dk) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dk) + o) = gk;
+        if (a.dv) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dv) + o) = gv;
+    }
+}
+__device__ __forceinline__ void bgrad_store_gates(const ChunkArgs &a, const ChunkPos &p, int w,
+                                                  float dg, float db) {
+    const int ts = p.c * C + 63 - lane_id();
+    if (w == 0 && ts < a.T) {
+        const int64_t o = ((int64_t)p.b * a.T + ts) * a.H + p.h;
+        if (a.dg) a.dg[o] = dg;
+        if (a.dbeta) a.dbeta[o] = db;
+    }
+}
+
 // bgrad: every gradient of one chunk, given S0, the edits delta (forward
 // checkpoint) and dS at the chunk end (adjoint scan).  Phases between barriers:
 //   A  dO S0^T, K dS, KK^T, QK^T (registers); P^T -> LDS
@@ -790,7 +882,13 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
 //   F  dR S0^T (-> dK, dbeta, dgam); dA, dP masked -> MA^T, MP^T
 //   G  dQ = MP K + gam dO S0^T;  dK = (MA + MA^T) K + MP^T Q + ...
 //   H  gate gradients: dbeta, and dg by a reverse scan of dG (wave 0)
-__global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
+// The grid holds one workgroup per CU (the LDS allows no more), each walking
+// chunks blockIdx.x, blockIdx.x + gridDim.x, ...: the next chunk's inputs are
+// loaded into registers while the current chunk computes, so the load latency
+// that starts every chunk is paid once per workgroup instead of once per chunk.
+// A chunk's stores are issued after the next chunk's staging, so that the
+// staging's wait on its (older) loads never waits on stores.
+__global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunks) {
     __shared__ BGradSmem sm;
     // Every input tile is staged once, in the orientation it is stored in (rows
     // of Q, K, dO, V, T; S0^T and dS^T as checkpointed), and read the other way
@@ -805,39 +903,43 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
     uint16_t *dRr = sm.slot[9];                    // dR rows, E..F
     // F..G: MA and MP are stored transposed only; phase G reads them both ways.
     uint16_t *MAt = sm.slot[4], *MPt = sm.slot[7], *MPtl = sm.slot[10];
-    uint16_t *dQt = sm.slot[2], *dKt = sm.slot[8], *dVt = sm.slot[11];  // gradients, G..end
-    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
-    const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
-    const int tg = c * C + t;
-    const bool inb = tg < a.T;
-    const GateBlock *gb = a.ck_gate + ci;
-    const float *dck = a.ck_delta + (int64_t)ci * C * D;
-    const int r0 = 16 * tm + 4 * (lane_id() >> 4);
-    // Every load is issued here, phase A's operands first.  Phase A's tiles go
-    // to LDS before the first barrier; the rest (V, T, delta and the transposed
-    // copies phase A does not read) are written after phase A, so phase A runs
-    // while the tail of the loads is still arriving.
-    const uint4 qr = load8(a.q, a.qs, b, tg, h, cb, inb);
-    const uint4 kr = load8(a.k, a.ks, b, tg, h, cb, inb);
-    const uint4 dor = a.dout ? load8(a.dout, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
-    const uint4 s0 = load_mat(a.ck_state + (int64_t)ci * D * D, tid);
-    const uint4 ds = load_mat(a.ws_dstate + (int64_t)ci * D * D, tid);
-    const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
-    const int sg = gb->seg[t];
-    const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
+    // Gradients, G to the next chunk's staging: slots that phase G does not read and
+    // the staging does not write.
+    uint16_t *dQt = sm.slot[3], *dKt = sm.slot[5], *dVt = sm.slot[13];
     // The score adjoint's terms (c delta in ddelta, c' k in dk, and the norms
     // behind them) only exist when a score adjoint is given (uniform branches).
     const bool score_adj = a.dscores != nullptr;
-    const uint4 vr = load8(a.v, a.vs, b, tg, h, cb, inb);
-    const uint4 trw = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C +
-                                                      (tid >> 3) * C + 8 * (tid & 7));
-    const float4 d0 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb);
-    const float4 d1 = *reinterpret_cast<const float4 *>(dck + t * D + 8 * cb + 4);
-    const bool on = va != 0.f;
-    const uint4 k8 = mask8(kr, on), d8 = mask8(dor, on);
+    BgradIn in;
     {
-        const uint4 q8 = mask8(qr, on);
+        const ChunkPos p0 = chunk_pos(a, blockIdx.x);
+        bgrad_load<0>(a, blockIdx.x, p0, threadIdx.x, in);
+        bgrad_load<1>(a, blockIdx.x, p0, threadIdx.x, in);
+        bgrad_load<2>(a, blockIdx.x, p0, threadIdx.x, in);
+        bgrad_load<3>(a, blockIdx.x, p0, threadIdx.x, in);
+        bgrad_load<4>(a, blockIdx.x, p0, threadIdx.x, in);
+    }
+    float pdg = 0.f, pdb = 0.f;  // wave 0: the previous chunk's dg, dbeta (lane t: token 63 - t)
+    for (int ci = blockIdx.x; ci < nchunks; ci += gridDim.x) {
+    // An opaque zero keeps the wave- and lane-dependent address arithmetic of
+    // the body inside the loop: hoisted out, it would stay live across it and
+    // exhaust the registers.
+    int zero;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+    const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
+    const int r0 = 16 * tm + 4 * (lane_id() >> 4);
+    // The next chunk of this workgroup; past the end this chunk is loaded again,
+    // so the loads need no branch.
+    const int cn = ci + (int)gridDim.x < nchunks ? ci + (int)gridDim.x : ci;
+    const ChunkPos pn = chunk_pos(a, cn);
+    // The previous chunk (stored during this one) and whether there is one.
+    const bool prev = ci != (int)blockIdx.x;
+    const ChunkPos pp = chunk_pos(a, prev ? ci - (int)gridDim.x : ci);
+    // Phase A's tiles go to LDS before the first barrier; the rest (V, T, delta)
+    // after phase A.  Each part's registers then take the next chunk's loads.
+    const bool on = in.va != 0.f;
+    {
+        const uint4 q8 = mask8(in.q, on), k8 = mask8(in.k, on), d8 = mask8(in.dO, on && a.dout);
         put_row8(Qs, t, cb, q8);
         put_row8(Ks, t, cb, k8);
         put_row8(dOs, t, cb, d8);
@@ -852,16 +954,21 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
             }
             sm.kk[cb][t] = ksq;
         }
-        *reinterpret_cast<uint4 *>(&S0t[(tid >> 3) * LDB + 8 * (tid & 7)]) = s0;
-        *reinterpret_cast<uint4 *>(&dSt[(tid >> 3) * LDB + 8 * (tid & 7)]) = ds;
-        const float fr = wave_sum(dot8_bf16(s0, ds));
-        if (lane_id() == 0) sm.frob[w] = fr;
+        *reinterpret_cast<uint4 *>(&S0t[(tid >> 3) * LDB + 8 * (tid & 7)]) = in.s0;
+        *reinterpret_cast<uint4 *>(&dSt[(tid >> 3) * LDB + 8 * (tid & 7)]) = in.ds;
         if (w == 0) {
-            gates_derive(sm.gl, G, be, va, sg);
-            sm.dsc[t] = dsc;
+            gates_derive(sm.gl, in.G, in.be, in.va, in.sg);
+            sm.dsc[t] = in.dsc;
         }
     }
+    // |S0 dS| partial; written after the barrier, when the previous chunk's phase H
+    // (wave 0) has read the last one.
+    const float fr = wave_sum(dot8_bf16(in.s0, in.ds));
+    // The previous chunk's dv tile is read now: phase A writes P^T over it.
+    const bf16x8_t gv = bgrad_grad_frag(dVt, w);
+    bgrad_load<0>(a, cn, pn, tid, in);
     __syncthreads();
+    if (lane_id() == 0) sm.frob[w] = fr;
     const RowGates rg = row_gates(sm.gl, tm);
     float lmv[4];
     {
@@ -902,9 +1009,9 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         row_reduce_store(p, sm.g1[w & 1], tm);
     }
     {  // second half of the staging: operands of phases D-G that A does not read
-        put_row8(Vr, t, cb, mask8(vr, on));
-        *reinterpret_cast<uint4 *>(&Tr[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
-        const float x[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+        put_row8(Vr, t, cb, mask8(in.v, on));
+        *reinterpret_cast<uint4 *>(&Tr[(tid >> 3) * LDB + 8 * (tid & 7)]) = in.t;
+        const float x[8] = {in.d0.x, in.d0.y, in.d0.z, in.d0.w, in.d1.x, in.d1.y, in.d1.z, in.d1.w};
         Pack8 ph, pl;
         float dsq = 0.f;
 #pragma unroll
@@ -916,7 +1023,12 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         put_row8(Dlo, t, cb, pl.u);
         if (score_adj) sm.dd[cb][t] = dsq;
     }
+    // The previous chunk's dq, dk, dv rows, then the next chunk's V and T.
+    if (prev) bgrad_store_rows(a, pp, w, bgrad_grad_frag(dQt, w), bgrad_grad_frag(dKt, w), gv);
+    bgrad_load<3>(a, cn, pn, tid, in);
     __syncthreads();
+    bgrad_load<1>(a, cn, pn, tid, in);
+    if (prev) bgrad_store_gates(a, pp, w, pdg, pdb);
     // Phase D: delta dS^T (-> dlam), ddelta = P^T dO + lam K dS + c delta (-> ddelta^T).
     float cs[4] = {0.f, 0.f, 0.f, 0.f}, ck[4] = {0.f, 0.f, 0.f, 0.f};
     if (score_adj) {
@@ -969,6 +1081,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         }
     }
     __syncthreads();
+    bgrad_load<2>(a, cn, pn, tid, in);
     // Phase E: dR = T^T ddelta -> dV (kept for the stores), dbeta (sum_v dR v part), dR rows.
     f32x4 dvv[2];
     {
@@ -998,6 +1111,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         row_reduce_store(p, sm.b2[w & 1], tm);
     }
     __syncthreads();
+    bgrad_load<4>(a, cn, pn, tid, in);
     // Phase F: dR S0^T (-> dK; sum_k k dR S0^T -> dbeta and dgam), dA and dP
     // (masked) -> MA^T, MP^T, and the gate-gradient partial sums.
     f32x4 drs[2] = {zero4(), zero4()};
@@ -1051,6 +1165,33 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
         row_reduce_store(pz, sm.zr[w & 1], tm);
     }
     __syncthreads();
+    // Every per-token term of the gate gradients is in LDS now: each wave sums
+    // those of 8 tokens while phase G's products run.  With u_t = k_t . (dR S0^T)_t:
+    //   dbeta_t = sum dA Gam KK^T + sum_v dR v - gam_t u_t,
+    //   dG_t   = row - column sums of Z + gam_t (q_t . (dO S0^T)_t - beta_t u_t) - lam_t dlam_t
+    // (plus, for the last token, the chunk-end term added in phase H).
+    {  // straight-line (every lane computes token 8w + l%8), so it interleaves with phase G
+        const int s = 8 * w + (lane_id() & 7);
+        const float gam = sm.gl.gam[s], lam = sm.gl.lam[s], bet = sm.gl.beta[s];
+        const float dlam = sm.dlam[0][s] + sm.dlam[1][s];
+        const float u = sm.ku[0][s] + sm.ku[1][s];
+        const float dG = sm.zr[0][s] + sm.zr[1][s] - (sm.zc[0][s] + sm.zc[1][s] + sm.zc[2][s] + sm.zc[3][s]) +
+                         gam * (sm.g1[0][s] + sm.g1[1][s] - bet * u) - lam * dlam;
+        const bool on = sm.gl.val[s] != 0.f;
+        const int sgp = sm.gl.seg[s > 0 ? s - 1 : 0];
+        const bool rs = on && (s == 0 ? sm.gl.seg[0] == 1 : sm.gl.seg[s] != sgp);
+        const float db = on ? sm.b1[0][s] + sm.b1[1][s] + sm.b2[0][s] + sm.b2[1][s] - gam * u : 0.f;
+        float fr = 0.f;
+#pragma unroll
+        for (int q = 0; q < NW; ++q) fr += sm.frob[q];
+        if (lane_id() < 8) {
+            sm.hdg[s] = dG;
+            sm.hdb[s] = db;
+            sm.hld[s] = lam * dlam;
+            sm.hkeep[s] = (on && !rs) ? 1.f : 0.f;
+            if (s == 0) sm.frs = fr;
+        }
+    }
     // Phase G: dQ and dK.
     {
         f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
@@ -1089,54 +1230,42 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a) {
             store_tile_t(&dVt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, dvv[j]);
         }
     }
-    __syncthreads();
-    // dq, dk, dv: lane (token 16 (w%4) + l%16, channels 32 (w/4) + 8 (l/16) ..) reads
-    // its eight channels across the transposed tiles and stores one 16-byte row
-    // piece per gradient.  Every lane runs the transpose reads.
-    {
-        const int l = lane_id();
-        const int tq = c * C + 16 * (w & 3) + (l & 15);
-        const bf16x8_t gq = frag_tr(dQt, 32 * (w >> 2), 16 * (w & 3));
-        const bf16x8_t gk = frag_tr(dKt, 32 * (w >> 2), 16 * (w & 3));
-        const bf16x8_t gv = frag_tr(dVt, 32 * (w >> 2), 16 * (w & 3));
-        if (tq < a.T) {
-            const int64_t o = (((int64_t)b * a.T + tq) * a.H + h) * D + 32 * (w >> 2) + 8 * (l >> 4);
-            if (a.dq) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dq) + o) = gq;
-            if (a.dk) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dk) + o) = gk;
-            if (a.dv) *reinterpret_cast<bf16x8_t *>(reinterpret_cast<uint16_t *>(a.dv) + o) = gv;
-        }
-    }
-    // Phase H: gate gradients (wave 0, lane == token).  With u_t = k_t . (dR S0^T)_t:
-    //   dbeta_t = sum dA Gam KK^T + sum_v dR v - gam_t u_t,
-    //   dG_t   = row - column sums of Z + gam_t (q_t . (dO S0^T)_t - beta_t u_t) - lam_t dlam_t.
-    // Lane t holds token s = 63 - t, so a forward scan over lanes sums suffixes:
-    // dg_s = sum_{r >= s} dG_r.
+    __syncthreads();  // gradient tiles complete: the next iteration stores them
+    // Phase H (wave 0): dg by a reverse scan of dG.  Lane t holds token s = 63 - t,
+    // so a forward scan over lanes sums suffixes: dg_s = sum_{r >= s} dG_r.
     if (w == 0) {
-        const int s = 63 - t, ts = c * C + s;
-        const float gam = sm.gl.gam[s], lam = sm.gl.lam[s], bet = sm.gl.beta[s];
-        const float dlam = sm.dlam[0][s] + sm.dlam[1][s];
-        const float u = sm.ku[0][s] + sm.ku[1][s];
-        float dG = sm.zr[0][s] + sm.zr[1][s] -
-                   (sm.zc[0][s] + sm.zc[1][s] + sm.zc[2][s] + sm.zc[3][s]) +
-                   gam * (sm.g1[0][s] + sm.g1[1][s] - bet * u) - lam * dlam;
-        const float tail = wave_sum(lam * dlam);
-        if (s == 63) {
-            float fr = 0.f;
-#pragma unroll
-            for (int q = 0; q < NW; ++q) fr += sm.frob[q];
-            dG += tail + sm.gl.gamC * fr;
-        }
+        const int s = 63 - t;
+        float dG = sm.hdg[s];
+        const float tail = wave_sum(sm.hld[s]);
+        if (s == 63) dG += tail + sm.gl.gamC * sm.frs;
         const float x = wave_scan_add(dG);
-        const bool on = sm.gl.val[s] != 0.f;
-        const bool rs = on && (s == 0 ? sm.gl.seg[0] == 1 : sm.gl.seg[s] != sm.gl.seg[s - 1]);
-        if (ts < a.T) {
-            const int64_t o = ((int64_t)b * a.T + ts) * a.H + h;
-            if (a.dg) a.dg[o] = (on && !rs) ? x : 0.f;
-            if (a.dbeta)
-                a.dbeta[o] = on ? sm.b1[0][s] + sm.b1[1][s] + sm.b2[0][s] + sm.b2[1][s] - gam * u
-                                : 0.f;
-        }
+        pdg = sm.hkeep[s] != 0.f ? x : 0.f;
+        pdb = sm.hdb[s];
     }
+    // No barrier here: the next staging writes no LDS that the stores or phase H
+    // read (the per-token sums phase H reads are rewritten only in the next
+    // chunk's phase G, after a barrier that wave 0 reaches after phase H).
+    }
+    {
+        const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int last = blockIdx.x + (nchunks - 1 - (int)blockIdx.x) / (int)gridDim.x * gridDim.x;
+        const ChunkPos pl = chunk_pos(a, last);
+        bgrad_store_rows(a, pl, w, bgrad_grad_frag(dQt, w), bgrad_grad_frag(dKt, w), bgrad_grad_frag(dVt, w));
+        bgrad_store_gates(a, pl, w, pdg, pdb);
+    }
+}
+
+int device_cus() {
+    static std::atomic<int> cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            return 256;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
 }
 
 hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
@@ -1148,7 +1277,8 @@ hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream, const hipEve
     (void)launch_chunk_affine_scan(a, true, stream);
     mark(ev, 3, stream);
     mark(ev, 4, stream);
-    hipLaunchKernelGGL(chunk_bgrad_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
+    hipLaunchKernelGGL(chunk_bgrad_kernel, dim3(std::min(nchunks, device_cus())), dim3(NT), 0, stream, a,
+                       nchunks);
     mark(ev, 5, stream);
     return hipGetLastError();
 }
