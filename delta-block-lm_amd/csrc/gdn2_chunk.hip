@@ -134,12 +134,16 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
     // T (bf16, row-major, zero above the diagonal): LDS operand and checkpoint.
     {
         const int r = tid >> 3, c0 = 8 * (tid & 7);
+        // Two 16-byte reads; the blocks above the diagonal hold stale data and are
+        // masked after the read.
+        const float4 f0 = *reinterpret_cast<const float4 *>(&sm.u.inv.Tf[r * LDF + c0]);
+        const float4 f1 = *reinterpret_cast<const float4 *>(&sm.u.inv.Tf[r * LDF + c0 + 4]);
+        const float f[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
         uint32_t pk[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int s0 = c0 + 2 * e;
-            pk[e] = bf16_pack2(s0 <= r ? sm.u.inv.Tf[r * LDF + s0] : 0.f,
-                               s0 + 1 <= r ? sm.u.inv.Tf[r * LDF + s0 + 1] : 0.f);
+            pk[e] = bf16_pack2(s0 <= r ? f[2 * e] : 0.f, s0 + 1 <= r ? f[2 * e + 1] : 0.f);
         }
         const uint4 v = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         *reinterpret_cast<uint4 *>(a.ck_t + (int64_t)ci * C * C + r * C + c0) = v;

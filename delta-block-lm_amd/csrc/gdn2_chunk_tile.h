@@ -285,37 +285,32 @@ __device__ __forceinline__ void frag_tr_scaled_split(const uint16_t *Z, const fl
 
 // T = (I + A)^-1 for the strictly lower 64x64 A in Af; result in Tf (lower
 // blocks).  Called by all waves; ends with a barrier.  Blocks are 16x16:
-//   1. diagonal blocks T_bb = (I + A_bb)^-1 by forward substitution (waves 0-3,
-//      four lanes per column share each row's dot product);
+//   1. diagonal blocks T_bb = (I + A_bb)^-1 by forward substitution: wave 0,
+//      lane (block l/16, column l%16) walks its column down the 16 rows with
+//      FMAs on its own registers (the A values are LDS broadcasts);
 //   2. T_10 = -T_11 A_10 T_00 and T_32 = -T_33 A_32 T_22;
 //   3. T_21 (32x32, blocks r = 2,3 x c = 0,1) = -T_22(32) A_21(32) T_11(32).
 // Products chain through registers (the second factor of each step is an
 // accumulator tile), so the three steps take three barriers.
 __device__ __forceinline__ void ut_inverse(const float *Af, float *Tf, int w) {
     const int l = lane_id();
-    if (w < 4) {
-        // Lane (col, part) holds rows part, part+4, part+8, part+12 of column col;
-        // the four parts of a column (one DPP quad) split each row's dot product.
-        const int col = l >> 2, part = l & 3;
-        const float *Ab = Af + (16 * w) * LDF + 16 * w;
-        float Tq[4] = {0.f, 0.f, 0.f, 0.f};
+    if (w == 0) {
+        const int bk = l >> 4, col = l & 15;
+        const float *Ab = Af + (16 * bk) * LDF + 16 * bk;
+        float Tc[16];  // T_bb[r][col]; rows above col come out 0
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            float acc = 0.f;
+            float e0 = 0.f, e1 = 0.f;  // two chains halve the dependent FMA latency
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const int s = part + 4 * m;
-                if (s < r) acc += Ab[r * LDF + s] * Tq[m];
+            for (int q = 0; q < r; ++q) {
+                if (q & 1) e1 += Ab[r * LDF + q] * Tc[q];
+                else e0 += Ab[r * LDF + q] * Tc[q];
             }
-            acc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                       0, __builtin_bit_cast(int, acc), 0xB1, 0xF, 0xF, false));  // lane ^ 1
-            acc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                       0, __builtin_bit_cast(int, acc), 0x4E, 0xF, 0xF, false));  // lane ^ 2
-            if ((r & 3) == part) Tq[r >> 2] = (r == col ? 1.f : 0.f) - acc;
+            Tc[r] = (r == col ? 1.f : 0.f) - (e0 + e1);
         }
-        float *Tb = Tf + (16 * w) * LDF + 16 * w;
+        float *Tb = Tf + (16 * bk) * LDF + 16 * bk;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) Tb[(part + 4 * m) * LDF + col] = Tq[m];
+        for (int r = 0; r < 16; ++r) Tb[r * LDF + col] = Tc[r];
     }
     __syncthreads();
     auto blkA = [&](int r, int c) { return Af + (16 * r) * LDF + 16 * c; };
