@@ -23,6 +23,8 @@
 // scan's -W and Ktil as bf16, U as f32.
 #include "gdn2_chunk_tile.h"
 
+#include <algorithm>
+
 namespace gdn2 {
 
 namespace {
@@ -218,60 +220,130 @@ __global__ void __launch_bounds__(NT) wide_prep_kernel(ChunkArgs a) {
 }
 
 // ---- out: outputs, edits, their norms and the scores -----------------------------
-// One workgroup per chunk: Q, K, T and P = Gam . QK^T once; R, delta and O for
-// each value block in turn; the scores from both blocks' |delta|^2.
+// Q, K, T and P = Gam . QK^T once per chunk; R, delta and O for each value block
+// in turn; the scores from both blocks' |delta|^2.  One workgroup per CU walks
+// chunks blockIdx.x, blockIdx.x + gridDim.x, ...: the next chunk's inputs are
+// loaded into registers while the current one computes, and the last block's
+// stores are issued after the next chunk's staging, so that no chunk waits on
+// its loads (or the previous chunk's stores) but a workgroup's first.
 namespace {
 struct WOutSmem {
     uint16_t q[KTILE];   // Q rows
     uint16_t k[KTILE];   // K rows
-    uint16_t st[KTILE];  // S0^T rows of block vb ([v][k]); O rows (LDB) in phase 3
-    uint16_t vt[TILE];   // V_vb^T, then R^T lo; with rt: delta f32 rows in phase 3
+    uint16_t st[KTILE];  // S0^T rows of block vb ([v][k])
+    uint16_t vt[TILE];   // V_vb^T, then R^T lo
     uint16_t rt[TILE];   // R^T hi
     uint16_t tb[TILE];   // T rows
     uint16_t pt[TILE], ptl[TILE];  // P^T hi/lo
     uint16_t dt[TILE], dl[TILE];   // delta^T hi/lo of block vb
+    float df[C * LDF];             // delta rows (f32) of block vb, for the checkpoint
+    uint16_t os[TILE];             // O rows of block vb (bf16 output)
     GateLds gl;
     float kk[NW][C];
     float dd[NVB][2][C];
 };
+
+// One chunk's inputs: rows past the sequence end read the last row (the gate
+// block marks those tokens invalid and the staging zeroes them), so the loads
+// take no branch and the compiler's memory-counter waits stay exact.
+struct WOutIn {
+    Row2 q, k;
+    uint4 v[NVB];
+    Mat2 s0[NVB];
+    uint4 t;
+    float G, be, va;
+    int sg;
+};
+// Part P: 0 q, k; 1 V and S0 of block 0; 2 T and the gates; 3 V and S0 of block 1.
+template <int P>
+__device__ __forceinline__ void wout_load(const ChunkArgs &a, int ci, int tid, WOutIn &x) {
+    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = tid & 63, cb = tid >> 6, tg = c * C + t;
+    const int tr = tg < a.T ? tg : a.T - 1;
+    if constexpr (P == 0) {
+        x.q = load_row2(a.q, a.qs, b, tr, h, cb, true);
+        x.k = load_row2(a.k, a.ks, b, tr, h, cb, true);
+    } else if constexpr (P == 1 || P == 3) {
+        constexpr int vb = P == 1 ? 0 : 1;
+        x.v[vb] = load8(a.v + 64 * vb, a.vs, b, tr, h, cb, true);
+        x.s0[vb] = load_mat2(a.ck_state + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
+    } else {
+        x.t = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C + (tid >> 3) * C + 8 * (tid & 7));
+        const GateBlock *gb = a.ck_gate + ci;
+        x.G = gb->G[t], x.be = gb->beta[t], x.va = gb->val[t];
+        x.sg = gb->seg[t];
+    }
+}
+
+// Value block vb's delta rows (checkpoint) and, for bf16 output, O rows.
+__device__ __forceinline__ void wout_store(const ChunkArgs &a, int ci, int vb, int tid, const WOutSmem &sm) {
+    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int r = tid >> 3, c0 = 8 * (tid & 7), tq = c * C + r;
+    float *dck = a.ck_delta + (int64_t)ci * C * KD + r * KD + 64 * vb + c0;
+    *reinterpret_cast<float4 *>(dck) = *reinterpret_cast<const float4 *>(&sm.df[r * LDF + c0]);
+    *reinterpret_cast<float4 *>(dck + 4) = *reinterpret_cast<const float4 *>(&sm.df[r * LDF + c0 + 4]);
+    if (a.out_bf16 && tq < a.T)
+        *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.out) + (((int64_t)b * a.T + tq) * a.H + h) * KD +
+                                   64 * vb + c0) = *reinterpret_cast<const uint4 *>(&sm.os[r * LDB + c0]);
+}
+
+// Wave 0's per-token terms of a chunk (lane == token): |k_t|^2, each block's
+// |delta_t|^2 and the score |k_t| |delta_t| (0 on padding).
+struct WOutTok {
+    float kk, dd[NVB], score;
+};
+__device__ __forceinline__ void wout_store_tok(const ChunkArgs &a, int ci, const WOutTok &x) {
+    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = lane_id(), tg = c * C + t;
+    a.ck_kk[(int64_t)ci * C + t] = x.kk;
+#pragma unroll
+    for (int vb = 0; vb < NVB; ++vb) a.ck_ddp[((int64_t)ci * NVB + vb) * C + t] = x.dd[vb];
+    if (tg < a.T) a.scores[((int64_t)b * a.T + tg) * a.H + h] = x.score;
+}
 }  // namespace
 
-__global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a) {
+__global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a, int nchunks) {
     __shared__ WOutSmem sm;
     uint16_t *Qs = sm.q, *Ks = sm.k, *Vt = sm.vt, *Tb = sm.tb, *St = sm.st, *Rt = sm.rt;
     uint16_t *Pt = sm.pt, *Ptl = sm.ptl, *Dt = sm.dt, *Dl = sm.dl;
-    uint16_t *Os = sm.st;  // over S0^T after phase 2
-    float *Df = reinterpret_cast<float *>(sm.vt);  // over V^T/R^T lo and R^T hi after phase 2
-    static_assert(C * LDF * sizeof(float) <= 2 * TILE * sizeof(uint16_t), "delta over vt+rt");
-    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
-    const int t = tid & 63, cb = tid >> 6, t0 = c * C, tg = t0 + t;
+    WOutIn in;
+    wout_load<0>(a, blockIdx.x, threadIdx.x, in);
+    wout_load<1>(a, blockIdx.x, threadIdx.x, in);
+    wout_load<2>(a, blockIdx.x, threadIdx.x, in);
+    wout_load<3>(a, blockIdx.x, threadIdx.x, in);
+    WOutTok tok{};  // wave 0: the previous chunk's per-token terms
+    for (int ci = blockIdx.x; ci < nchunks; ci += gridDim.x) {
+    // An opaque zero keeps the lane- and wave-dependent address arithmetic inside
+    // the loop (hoisted, it would stay live across it and exhaust the registers).
+    int zero;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+    const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = tid & 63, cb = tid >> 6, t0 = c * C;
     const int tm = w >> 1, tn0 = 2 * (w & 1);
-    const GateBlock *gb = a.ck_gate + ci;
-    const bool inb = tg < a.T;
-    const Row2 qr = load_row2(a.q, a.qs, b, tg, h, cb, inb);
-    const Row2 kr = load_row2(a.k, a.ks, b, tg, h, cb, inb);
-    uint4 vr = load8(a.v, a.vs, b, tg, h, cb, inb);
-    Mat2 s0r = load_mat2(a.ck_state + (int64_t)ci * KD * KD, tid);
-    const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
-    const int sg = gb->seg[t];
-    const uint4 trw =
-        *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C + (tid >> 3) * C + 8 * (tid & 7));
-    const bool on = va != 0.f;
+    // The next chunk; past the end this chunk again, so the loads need no branch.
+    const int cn = ci + (int)gridDim.x < nchunks ? ci + (int)gridDim.x : ci;
+    const bool on = in.va != 0.f;
     {
-        const Row2 k8 = mask_row2(kr, on);
-        put_row2(Qs, t, cb, mask_row2(qr, on));
+        const Row2 k8 = mask_row2(in.k, on);
+        put_row2(Qs, t, cb, mask_row2(in.q, on));
         put_row2(Ks, t, cb, k8);
-        put_col8(Vt, t, cb, mask8(vr, on));
-        put_mat2(St, s0r, tid);
-        *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trw;
+        put_col8(Vt, t, cb, mask8(in.v[0], on));
+        put_mat2(St, in.s0[0], tid);
+        *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = in.t;
         float ksq = 0.f;
 #pragma unroll
         for (int i = 0; i < NKB; ++i) ksq += sq8(k8.p[i]);
         sm.kk[cb][t] = ksq;
-        if (w == 0) gates_derive(sm.gl, G, be, va, sg);
+        if (w == 0) gates_derive(sm.gl, in.G, in.be, in.va, in.sg);
     }
+    if (ci != (int)blockIdx.x) {  // the previous chunk's last block and token terms
+        wout_store(a, ci - gridDim.x, NVB - 1, tid, sm);
+        if (w == 0) wout_store_tok(a, ci - gridDim.x, tok);
+    }
+    wout_load<0>(a, cn, tid, in);
     __syncthreads();
+    wout_load<1>(a, cn, tid, in);
     const RowGates rg = row_gates(sm.gl, tm);
     {  // P = Gam . QK^T (causal tiles) -> P^T hi/lo, once for both blocks
         f32x4 pq[2] = {zero4(), zero4()};
@@ -292,14 +364,6 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a) {
     }
 #pragma unroll 1
     for (int vb = 0; vb < NVB; ++vb) {
-        if (vb > 0) {
-            vr = load8(a.v + 64 * vb, a.vs, b, tg, h, cb, inb);
-            s0r = load_mat2(a.ck_state + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
-            __syncthreads();  // the previous block's O and delta rows are stored
-            put_col8(Vt, t, cb, mask8(vr, on));
-            put_mat2(St, s0r, tid);
-            __syncthreads();
-        }
         // Phase 1: R (-> Rt, lo over Vt) and gam Q S0 kept in registers.
         f32x4 qs[2] = {zero4(), zero4()};
         {
@@ -319,6 +383,7 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a) {
                 store_tile_t_split(&Rt[(16 * (tn0 + j)) * LDB + 16 * tm], vt, LDB, x[j]);
             }
         }
+        if (vb == 0) wout_load<2>(a, cn, tid, in);
         __syncthreads();
         // Phase 2: delta = T R (-> Dt/Dl) and |delta_t|^2 of the block.
         f32x4 dlt[2] = {zero4(), zero4()};
@@ -335,12 +400,24 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a) {
             row_reduce_store(p, sm.dd[vb][w & 1], tm);
         }
         __syncthreads();
-        // delta (f32 rows) over the dead R^T tiles; O = gam Q S0 + P delta over S0^T.
+        if (vb == NVB - 1 && w == 0) {  // the chunk's token terms, stored after the next staging
+            float kk = 0.f, dd = 0.f;
+#pragma unroll
+            for (int q = 0; q < NW; ++q) kk += sm.kk[q][t];
+            tok.kk = kk;
+#pragma unroll
+            for (int v2 = 0; v2 < NVB; ++v2) {
+                tok.dd[v2] = sm.dd[v2][0][t] + sm.dd[v2][1][t];
+                dd += tok.dd[v2];
+            }
+            tok.score = sm.gl.val[t] != 0.f ? sqrtf(kk * dd) : 0.f;
+        }
+        // delta (f32 rows) and O = gam Q S0 + P delta into their own tiles.
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                Df[(16 * tm + acc_row(i)) * LDF + 16 * (tn0 + j) + acc_col()] = dlt[j][i];
+                sm.df[(16 * tm + acc_row(i)) * LDF + 16 * (tn0 + j) + acc_col()] = dlt[j][i];
         {
             f32x4 x[2] = {qs[0], qs[1]};
             gemm2_atr(x, Pt, 16 * tm, Dt, tn0);
@@ -348,7 +425,7 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a) {
             gemm2_atr(x, Ptl, 16 * tm, Dt, tn0);
             if (a.out_bf16) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) store_tile_rm(&Os[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, x[j]);
+                for (int j = 0; j < 2; ++j) store_tile_rm(&sm.os[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, x[j]);
             } else {
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
@@ -361,32 +438,22 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a) {
                     }
             }
         }
-        __syncthreads();
-        {
-            const int r = tid >> 3, c0 = 8 * (tid & 7), tq = t0 + r;
-            float *dck = a.ck_delta + (int64_t)ci * C * KD + r * KD + 64 * vb + c0;
-            *reinterpret_cast<float4 *>(dck) = *reinterpret_cast<const float4 *>(&Df[r * LDF + c0]);
-            *reinterpret_cast<float4 *>(dck + 4) = *reinterpret_cast<const float4 *>(&Df[r * LDF + c0 + 4]);
-            if (a.out_bf16 && tq < a.T)
-                *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.out) +
-                                           (((int64_t)b * a.T + tq) * a.H + h) * KD + 64 * vb + c0) =
-                    *reinterpret_cast<const uint4 *>(&Os[r * LDB + c0]);
+        __syncthreads();  // delta and O rows complete; V, S0 and R of the block read
+        if (vb == 0) {
+            // Block 0's stores; block 1's V and S0 (loaded one chunk ahead) staged.
+            wout_store(a, ci, 0, tid, sm);
+            put_col8(Vt, t, cb, mask8(in.v[1], on));
+            put_mat2(St, in.s0[1], tid);
+            wout_load<3>(a, cn, tid, in);
+            __syncthreads();
         }
     }
-    // |k_t|^2 and each block's |delta_t|^2 (the backward's score terms) and the
-    // scores score_t = |k_t| |delta_t| (0 on padding).
-    if (tid < 64) {
-        float kk = 0.f, dd = 0.f;
-#pragma unroll
-        for (int q = 0; q < NW; ++q) kk += sm.kk[q][t];
-        a.ck_kk[(int64_t)ci * C + t] = kk;
-#pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) {
-            const float d = sm.dd[vb][0][t] + sm.dd[vb][1][t];
-            a.ck_ddp[((int64_t)ci * NVB + vb) * C + t] = d;
-            dd += d;
-        }
-        if (tg < a.T) a.scores[((int64_t)b * a.T + tg) * a.H + h] = sm.gl.val[t] != 0.f ? sqrtf(kk * dd) : 0.f;
+    }
+    {
+        const int tid = threadIdx.x;
+        const int last = blockIdx.x + (nchunks - 1 - (int)blockIdx.x) / (int)gridDim.x * gridDim.x;
+        wout_store(a, last, NVB - 1, tid, sm);
+        if ((tid >> 6) == 0) wout_store_tok(a, last, tok);
     }
 }
 
@@ -412,53 +479,107 @@ struct WBPrepSmem {
 };
 }  // namespace
 
-__global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a) {
+// One chunk's inputs to bprep (rows past the sequence end read the last row; a
+// missing dO reads q and a missing score adjoint the delta checkpoint, which
+// holds more than B*T*H floats; the staging zeroes what is not used), so the
+// loads take no branch.  Part P: 0 q, k; 1 dO; 2 T, the gates, the score adjoint.
+struct WBPrepIn {
+    Row2 q, k;
+    uint4 dO[NVB];
+    uint4 t;
+    float G, be, va, dsc;
+    int sg;
+};
+template <int P>
+__device__ __forceinline__ void wbprep_load(const ChunkArgs &a, int ci, int tid, WBPrepIn &x) {
+    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = tid & 63, cb = tid >> 6, tg = c * C + t;
+    const int tr = tg < a.T ? tg : a.T - 1;
+    if constexpr (P == 0) {
+        x.q = load_row2(a.q, a.qs, b, tr, h, cb, true);
+        x.k = load_row2(a.k, a.ks, b, tr, h, cb, true);
+    } else if constexpr (P == 1) {
+        const uint16_t *dop = a.dout ? a.dout : a.q;
+        const int64_t *dos = a.dout ? a.ds : a.qs;
+#pragma unroll
+        for (int vb = 0; vb < NVB; ++vb) x.dO[vb] = load8(dop + 64 * vb, dos, b, tr, h, cb, true);
+    } else {
+        x.t = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C + (tid >> 3) * C + 8 * (tid & 7));
+        const GateBlock *gb = a.ck_gate + ci;
+        x.G = gb->G[t], x.be = gb->beta[t], x.va = gb->val[t];
+        x.sg = gb->seg[t];
+        x.dsc = (a.dscores ? a.dscores : a.ck_delta)[((int64_t)b * a.T + tr) * a.H + h];
+    }
+}
+
+// N of chunk ci from the registers it was formed in (transposed: Nt[col][row]).
+__device__ __forceinline__ void wbprep_store(const ChunkArgs &a, int ci, int tm, int tn0,
+                                             const f32x4 (&n)[NVB][NKB][2]) {
+    float *Nt = a.ws_n + (int64_t)ci * KD * KD;
+#pragma unroll
+    for (int vb = 0; vb < NVB; ++vb)
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                *reinterpret_cast<float4 *>(&Nt[(64 * vb + 16 * (tn0 + j) + acc_col()) * KD + 16 * (tm + 4 * kb) +
+                                                acc_row(0)]) =
+                    make_float4(n[vb][kb][j][0], n[vb][kb][j][1], n[vb][kb][j][2], n[vb][kb][j][3]);
+}
+
+// One workgroup per CU walks chunks blockIdx.x, blockIdx.x + gridDim.x, ...; the
+// next chunk's inputs are loaded into registers while the current one computes,
+// and a chunk's N (formed in the registers of Y) is stored after the next
+// chunk's staging, so that no chunk but a workgroup's first waits on its loads
+// or on the previous chunk's stores.
+__global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a, int nchunks) {
     __shared__ WBPrepSmem sm;
     uint16_t *Qs = sm.q, *Ks = sm.k, *Tb = sm.u.p1.tb, *KBGs = sm.u.p1.kbg;
     uint16_t *Pt = sm.pt, *Ptl = sm.ptl;
     uint16_t *Wt = sm.u.wt[0], *Wtl = sm.u.wt[1];  // over the phase-1 operands
     // X^T hi/lo of each block, over Q/K (block 0) and the dO rows (block 1) after phase 2
     uint16_t *Xt[NVB] = {sm.q, sm.dos[0]}, *Xtl[NVB] = {sm.k, sm.dos[1]};
-    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const bool score_adj = a.dscores != nullptr;
+    WBPrepIn in;
+    wbprep_load<0>(a, blockIdx.x, threadIdx.x, in);
+    wbprep_load<1>(a, blockIdx.x, threadIdx.x, in);
+    wbprep_load<2>(a, blockIdx.x, threadIdx.x, in);
+    // Y, then N = Y - W^T X in place; held until the next chunk's staging is done.
+    f32x4 yacc[NVB][NKB][2];
+    for (int ci = blockIdx.x; ci < nchunks; ci += gridDim.x) {
+    // An opaque zero keeps the lane- and wave-dependent address arithmetic inside
+    // the loop (hoisted, it would stay live across it and exhaust the registers).
+    int zero;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+    const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
-    const int tg = c * C + t;
-    const bool inb = tg < a.T;
-    const GateBlock *gb = a.ck_gate + ci;
     const float *dck = a.ck_delta + (int64_t)ci * C * KD;
     const int r0 = 16 * tm + 4 * (lane_id() >> 4);
-    const Row2 qr = load_row2(a.q, a.qs, b, tg, h, cb, inb);
-    const Row2 kr = load_row2(a.k, a.ks, b, tg, h, cb, inb);
-    uint4 dor[NVB];
-#pragma unroll
-    for (int vb = 0; vb < NVB; ++vb)
-        dor[vb] = a.dout ? load8(a.dout + 64 * vb, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
-    const uint4 trow = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C +
-                                                         (tid >> 3) * C + 8 * (tid & 7));
-    const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
-    const int sg = gb->seg[t];
-    const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
-    const bool score_adj = a.dscores != nullptr;
+    // The next chunk; past the end this chunk again, so the loads need no branch.
+    const int cn = ci + (int)gridDim.x < nchunks ? ci + (int)gridDim.x : ci;
     {
-        const bool on = va != 0.f;
-        const float gam = sg == 0 ? __expf(G) : 0.f, bg = be * gam;
-        const Row2 q8 = mask_row2(qr, on), k8 = mask_row2(kr, on);
+        const bool on = in.va != 0.f;
+        const float gam = in.sg == 0 ? __expf(in.G) : 0.f, bg = in.be * gam;
+        const Row2 q8 = mask_row2(in.q, on), k8 = mask_row2(in.k, on);
         put_row2(Qs, t, cb, q8);
         put_row2(Ks, t, cb, k8);
 #pragma unroll
-        for (int vb = 0; vb < NVB; ++vb) put_row8(sm.dos[vb], t, cb, mask8(dor[vb], on));
+        for (int vb = 0; vb < NVB; ++vb) put_row8(sm.dos[vb], t, cb, mask8(in.dO[vb], on && a.dout));
 #pragma unroll
         for (int i = 0; i < NKB; ++i) put_row8(KBGs, t, cb + 8 * i, scale8(k8.p[i], bg), LDK);
-        *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trow;
+        *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = in.t;
         if (w == 0) {
-            gates_derive(sm.gl, G, be, va, sg);
-            sm.dsc[t] = dsc;
+            gates_derive(sm.gl, in.G, in.be, in.va, in.sg);
+            sm.dsc[t] = score_adj ? in.dsc : 0.f;
         }
     }
+    if (ci != (int)blockIdx.x) wbprep_store(a, ci - gridDim.x, tm, tn0, yacc);  // the previous chunk's N
+    wbprep_load<0>(a, cn, tid, in);
     __syncthreads();
+    wbprep_load<1>(a, cn, tid, in);
     const RowGates rg = row_gates(sm.gl, tm);
     // Phase 1: W = T (beta gam K) and both blocks' Y = (gam Q)^T dO in registers; P^T hi/lo.
-    f32x4 wacc[NKB][2], yacc[NVB][NKB][2];
+    f32x4 wacc[NKB][2];
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
         wacc[kb][0] = wacc[kb][1] = zero4();
@@ -498,6 +619,7 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a) {
         }
     }
     __syncthreads();
+    wbprep_load<2>(a, cn, tid, in);
     // Phase 2: W^T hi/lo; both blocks' X = P^T dO + diag(c) delta in registers, then
     // stored transposed (hi/lo) once every wave has read the dO rows.
 #pragma unroll
@@ -540,8 +662,7 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a) {
             store_tile_t_split(&Xt[vb][(16 * (tn0 + j)) * LDB + 16 * tm],
                                &Xtl[vb][(16 * (tn0 + j)) * LDB + 16 * tm], LDB, xx[vb][j]);
     __syncthreads();
-    // Phase 3: N = Y - W^T X, both blocks' 64 columns, all KD rows.
-    float *Nt = a.ws_n + (int64_t)ci * KD * KD;  // N transposed: Nt[col][row]
+    // Phase 3: N = Y - W^T X, both blocks' 64 columns, all KD rows, in Y's registers.
 #pragma unroll
     for (int vb = 0; vb < NVB; ++vb)
 #pragma unroll
@@ -553,11 +674,16 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a) {
             gemm2(x, &Wtl[(16 * mt) * LDB], Xt[vb], tn0);
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-                *reinterpret_cast<float4 *>(&Nt[(64 * vb + 16 * (tn0 + j) + acc_col()) * KD + 16 * mt +
-                                                acc_row(0)]) =
-                    make_float4(yacc[vb][kb][j][0] - x[j][0], yacc[vb][kb][j][1] - x[j][1],
-                                yacc[vb][kb][j][2] - x[j][2], yacc[vb][kb][j][3] - x[j][3]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) yacc[vb][kb][j][e] -= x[j][e];
         }
+    __syncthreads();  // W^T and X^T read: the next chunk's staging takes their tiles
+    }
+    {
+        const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int last = blockIdx.x + (nchunks - 1 - (int)blockIdx.x) / (int)gridDim.x * gridDim.x;
+        wbprep_store(a, last, w >> 1, 2 * (w & 1), yacc);
+    }
 }
 
 // ---- bgrad: every gradient of one chunk ------------------------------------------
@@ -1050,7 +1176,7 @@ hipError_t launch_wide_fwd(const ChunkArgs &a, hipStream_t stream, const hipEven
     if (e != hipSuccess) return e;
     wmark(ev, 3, stream);
     wmark(ev, 4, stream);
-    hipLaunchKernelGGL(wide_out_kernel, dim3(nch), dim3(NT), 0, stream, a);
+    hipLaunchKernelGGL(wide_out_kernel, dim3(std::min(nch, device_cus())), dim3(NT), 0, stream, a, nch);
     wmark(ev, 5, stream);
     return hipGetLastError();
 }
@@ -1058,7 +1184,7 @@ hipError_t launch_wide_fwd(const ChunkArgs &a, hipStream_t stream, const hipEven
 hipError_t launch_wide_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
     const int nch = a.B * a.H * a.nc;
     wmark(ev, 0, stream);
-    hipLaunchKernelGGL(wide_bprep_kernel, dim3(nch), dim3(NT), 0, stream, a);
+    hipLaunchKernelGGL(wide_bprep_kernel, dim3(std::min(nch, device_cus())), dim3(NT), 0, stream, a, nch);
     wmark(ev, 1, stream);
     wmark(ev, 2, stream);
     const hipError_t e = wide_scan(a, true, stream);
