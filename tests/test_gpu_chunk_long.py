@@ -83,6 +83,33 @@ def test_long_chunk_path_matches_oracle(dk, T, H, reset_every):
 
 
 @pytest.mark.parametrize("D", [64, 128])
+def test_chunk_loops_uneven_split(dk, D):
+    """336 chunks (B3 T1000 H7): the kernels that walk chunks with one workgroup
+    per CU get more chunks than workgroups but not a multiple of them, so some
+    workgroups walk two chunks and others one (the last chunk's stores come
+    after the loop); d_k = d_v = 64 and 128, with masks and resets."""
+    p = problem(77 + D, 3, 1000, 7, masks=True, K=D, V=D, reset_every=300)
+    print(f"chunk loops: B3 T1000 H7 D={D}, 336 chunks", flush=True)
+    (out, fin, sc), grads, ran = _fwd_bwd(dk, p)
+    assert CHUNK_STAGES <= ran, f"chunk kernels did not all run: {sorted(ran)}"
+    a, e, w = oracle.scalar_gates(p["beta"], p["g"], D, D)
+    o_out, o_fin, o_sc = oracle.scan(p["q"], p["k"], p["v"], a, e, w, p["valid"], p["reset"],
+                                     p["initial"])
+    pad = (p["valid"] == 0)[:, :, None]
+    gate("output", out, o_out, TOL_BF16, exact_zero=pad[..., None])
+    gate("final_state", fin, o_fin, TOL_BF16)
+    gate("scores", sc, o_sc, TOL_BF16, exact_zero=pad)
+    og, odb, odg = scalar_oracle_grads(p)
+    dq, dkk, dv, db, dg, dinit = grads
+    gate("dq", dq, og["q"], TOL_BF16, exact_zero=pad[..., None])
+    gate("dk", dkk, og["k"], TOL_BF16, exact_zero=pad[..., None])
+    gate("dv", dv, og["v"], TOL_BF16, exact_zero=pad[..., None])
+    gate("dbeta", db, odb, TOL_BF16, exact_zero=pad)
+    gate("dg", dg, odg, TOL_BF16, exact_zero=pad)
+    gate("d_initial", dinit, og["initial"], TOL_BF16)
+
+
+@pytest.mark.parametrize("D", [64, 128])
 def test_long_split_continuation(dk, D):
     """T = 8192 (128 chunks) scanned whole equals [0, 4096) then [4096, 8192)
     from the carried state; the backward of the two halves, chained through
