@@ -35,6 +35,8 @@
 // log-domain adjoint divided by alpha, so its absolute error grows as 1/alpha.
 #include "gdn2_chunk_tile.h"
 
+#include <algorithm>
+
 namespace gdn2 {
 
 namespace {
@@ -91,15 +93,6 @@ __device__ __forceinline__ void put4_split(uint16_t *hi, uint16_t *lo, const flo
         make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
     *reinterpret_cast<uint2 *>(lo) =
         make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
-}
-
-// T (f32 checkpoint, 16 x 16) into hi/lo LDS rows; thread (r = tid/16, s = tid%16).
-__device__ __forceinline__ void load_t_split(const float *ckt, uint16_t *th, uint16_t *tl, int tid) {
-    const int r = tid >> 4, s = tid & 15;
-    uint16_t hi, lo;
-    split_bf16(ckt[r * CC + s], hi, lo);
-    th[r * LDB + s] = hi;
-    tl[r * LDB + s] = lo;
 }
 
 // P^T (from the f32 P checkpoint, 16 x 16) into hi/lo LDS rows [s][t];
@@ -201,38 +194,102 @@ struct CwPrepSmem {
 // ---- prep: gates, A, T and the factored state map of every 16-token chunk ------
 // The map S_16 = diag(b_15) S0 + Ktil^T (U - W' S0) leaves as its factors:
 // -W'^T and Ktil (bf16), U^T and b_15 (f32), for the scan of gdn2_chunk_lr.hip.
-__global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a) {
+// One chunk's inputs to prep, held in registers: the mask words (valid and reset,
+// or the document limits: both are [B,T] views of 4-byte elements, so one pair
+// of loads serves either) and k, v, alpha, erase, write.  Rows past the
+// sequence end read the last row and are masked at the staging, so the loads
+// take no branch.
+struct CwPrepIn {
+    uint32_t m1, m2;
+    uint2 k, v;
+    float al[4], er[4], wr[4];
+};
+__device__ __forceinline__ void cwprep_load(const ChunkArgs &a, int ci, int tid, CwPrepIn &x) {
+    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = tid >> 4, c0 = 4 * (tid & 15), tg = c * CC + t;
+    const int tr = tg < a.T ? tg : a.T - 1;
+    const View &v1 = a.doc ? a.doc_start : a.valid, &v2 = a.doc ? a.doc_end : a.reset;
+    x.m1 = reinterpret_cast<const uint32_t *>(v1.data)[b * v1.s0 + tr * v1.s1];
+    x.m2 = reinterpret_cast<const uint32_t *>(v2.data)[b * v2.s0 + tr * v2.s1];
+    x.k = *reinterpret_cast<const uint2 *>(row_ptr(a.k, a.ks, b, tr, h) + c0);
+    x.v = *reinterpret_cast<const uint2 *>(row_ptr(a.v, a.vs, b, tr, h) + c0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        x.al[e] = ld4<float>(a.alpha, b, tr, h, c0 + e);
+        x.er[e] = ld4<float>(a.erase, b, tr, h, c0 + e);
+        x.wr[e] = ld4<float>(a.write, b, tr, h, c0 + e);
+    }
+}
+
+// What prep stores once the inverse is done, held until the next chunk's
+// staging: T (f32, this thread's element), the gate block (threads < 16),
+// Lambda (this thread's four), -W'^T (bf16) and U^T (f32) from the accumulators.
+struct CwPrepOut {
+    float tx, val, lam[4];
+    int seg;
+    f32x4 x, y;
+};
+__device__ __forceinline__ void cwprep_store(const ChunkArgs &a, int ci, int tid, int w, const CwPrepOut &o) {
+    const int t = tid >> 4, c0 = 4 * (tid & 15);
+    a.ck_tf[(int64_t)ci * CC * CC + tid] = o.tx;  // (r, s) = (tid / 16, tid % 16)
+    if (tid < CC) {
+        a.ck_cwg[ci].val[tid] = o.val;
+        a.ck_cwg[ci].seg[tid] = o.seg;
+    }
+    put4_f32(a.ck_lam + (int64_t)ci * CC * 64 + t * 64 + c0, o.lam);
+    const int64_t off = ((int64_t)ci * 64 + 16 * w + acc_col()) * CC + acc_row(0);
+    *reinterpret_cast<uint2 *>(a.lr_wt + off) = make_uint2(bf16_pack2(-o.x[0], -o.x[1]), bf16_pack2(-o.x[2], -o.x[3]));
+    *reinterpret_cast<float4 *>(a.lr_u + off) = make_float4(o.y[0], o.y[1], o.y[2], o.y[3]);
+}
+
+// Workgroups walk chunks blockIdx.x, blockIdx.x + gridDim.x, ... (as many
+// workgroups as fit the GPU at once): the next chunk's inputs are loaded into
+// registers while the current one computes, and the stores after the inverse
+// are issued after the next chunk's staging.
+__global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a, int nchunks) {
     __shared__ CwPrepSmem sm;
-    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    {  // zero padding (rows 16..31 of the token-row tiles, columns 16..31 of T), once
+        const int tid = threadIdx.x;
+        zero_lds(sm.ah + RT16, RT32 - RT16, tid);
+        zero_lds(sm.wv + RT16, RT32 - RT16, tid);
+        zero_lds(sm.ahl + RT16, RT32 - RT16, tid);
+        zero_lds(sm.wvl + RT16, RT32 - RT16, tid);
+        for (int i = tid; i < CC * 16; i += NT4) {
+            sm.tb[(i >> 4) * LDB + 16 + (i & 15)] = 0;
+            sm.tbl[(i >> 4) * LDB + 16 + (i & 15)] = 0;
+        }
+    }
+    CwPrepIn in;
+    cwprep_load(a, blockIdx.x, threadIdx.x, in);
+    CwPrepOut po;
+    for (int ci = blockIdx.x; ci < nchunks; ci += gridDim.x) {
+    // An opaque zero keeps the lane- and wave-dependent address arithmetic inside
+    // the loop (hoisted, it would stay live across it).
+    int zero;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+    const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = ci % a.nc;
     const int t = tid >> 4, c0 = 4 * (tid & 15), tg = c * CC + t;
     const bool inb = tg < a.T;
-    zero_lds(sm.ah + RT16, RT32 - RT16, tid);
-    zero_lds(sm.wv + RT16, RT32 - RT16, tid);
-    zero_lds(sm.ahl + RT16, RT32 - RT16, tid);
-    zero_lds(sm.wvl + RT16, RT32 - RT16, tid);
-    for (int i = tid; i < CC * 16; i += NT4) {
-        sm.tb[(i >> 4) * LDB + 16 + (i & 15)] = 0;
-        sm.tbl[(i >> 4) * LDB + 16 + (i & 15)] = 0;
-    }
-    // Loads: token t, channels c0 .. c0 + 3.
-    float vld = 0.f, rst = 0.f;
-    if (inb && a.doc) {
-        const int32_t st = reinterpret_cast<const int32_t *>(a.doc_start.data)[b * a.doc_start.s0 + tg * a.doc_start.s1];
-        const int32_t en = reinterpret_cast<const int32_t *>(a.doc_end.data)[b * a.doc_end.s0 + tg * a.doc_end.s1];
-        vld = en >= st ? 1.f : 0.f;
-        rst = st == tg ? 1.f : 0.f;
-    } else if (inb) {
-        vld = ld4<float>(a.valid, b, tg, 0, 0);
-        rst = ld4<float>(a.reset, b, tg, 0, 0);
+    // The next chunk; past the end this chunk again, so the loads need no branch.
+    const int cn = ci + (int)gridDim.x < nchunks ? ci + (int)gridDim.x : ci;
+    float vld, rst;
+    if (a.doc) {
+        const int st = (int)in.m1, en = (int)in.m2;
+        vld = (inb && en >= st) ? 1.f : 0.f;
+        rst = (inb && st == tg) ? 1.f : 0.f;
+    } else {
+        vld = inb ? __uint_as_float(in.m1) : 0.f;
+        rst = inb ? __uint_as_float(in.m2) : 0.f;
     }
     const bool on = vld != 0.f;
     float kv[4], vv[4], al[4], er[4], wr[4];
-    load4_bf16(a.k, a.ks, b, tg, h, c0, inb, kv);
-    load4_bf16(a.v, a.vs, b, tg, h, c0, inb, vv);
-    load4_f32(a.alpha, b, tg, h, c0, inb, 1.f, al);
-    load4_f32(a.erase, b, tg, h, c0, inb, 0.f, er);
-    load4_f32(a.write, b, tg, h, c0, inb, 0.f, wr);
+    kv[0] = bf16_val((uint16_t)(in.k.x & 0xffff)), kv[1] = bf16_val((uint16_t)(in.k.x >> 16));
+    kv[2] = bf16_val((uint16_t)(in.k.y & 0xffff)), kv[3] = bf16_val((uint16_t)(in.k.y >> 16));
+    vv[0] = bf16_val((uint16_t)(in.v.x & 0xffff)), vv[1] = bf16_val((uint16_t)(in.v.x >> 16));
+    vv[2] = bf16_val((uint16_t)(in.v.y & 0xffff)), vv[3] = bf16_val((uint16_t)(in.v.y >> 16));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) al[e] = in.al[e], er[e] = in.er[e], wr[e] = in.wr[e];
     mask4(kv, on, 0.f), mask4(vv, on, 0.f), mask4(al, on, 1.f), mask4(er, on, 0.f), mask4(wr, on, 0.f);
     {
         float la[4], eh[4], wv[4];
@@ -251,6 +308,8 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a) {
             sm.rs[t] = (on && rst != 0.f) ? 1 : 0;
         }
     }
+    if (ci != (int)blockIdx.x) cwprep_store(a, ci - gridDim.x, tid, w, po);  // the previous chunk's
+    cwprep_load(a, cn, tid, in);
     __syncthreads();
     // Lambda: running sums over the chunk's tokens, one channel per thread;
     // segment index of every token.
@@ -262,11 +321,11 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a) {
             sm.lam[tt * LDL + tid] = acc;
         }
     } else if (tid == 64) {
-        int s = 0;
+        int s2 = 0;
 #pragma unroll
         for (int tt = 0; tt < CC; ++tt) {
-            s += sm.rs[tt];
-            sm.seg[tt] = s;
+            s2 += sm.rs[tt];
+            sm.seg[tt] = s2;
         }
     }
     __syncthreads();
@@ -300,26 +359,24 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a) {
     __syncthreads();
     if (w == 0) inv16(sm.af, LDI, sm.tf, LDI);
     __syncthreads();
-    {  // T (unit lower): hi/lo LDS operands and the f32 checkpoint; gates and Lambda out
-        const int r = tid >> 4, s = tid & 15;
-        const float x = s <= r ? sm.tf[r * LDI + s] : 0.f;
+    {  // T (unit lower): hi/lo LDS operands; T, the gate block and Lambda kept for the stores
+        const int r = tid >> 4, s2 = tid & 15;
+        const float x = s2 <= r ? sm.tf[r * LDI + s2] : 0.f;
         uint16_t hi, lo;
         split_bf16(x, hi, lo);
-        sm.tb[r * LDB + s] = hi;
-        sm.tbl[r * LDB + s] = lo;
-        a.ck_tf[(int64_t)ci * CC * CC + r * CC + s] = x;
+        sm.tb[r * LDB + s2] = hi;
+        sm.tbl[r * LDB + s2] = lo;
+        po.tx = x;
         if (tid < CC) {
-            a.ck_cwg[ci].val[tid] = sm.val[tid];
-            a.ck_cwg[ci].seg[tid] = sm.seg[tid];
+            po.val = sm.val[tid];
+            po.seg = sm.seg[tid];
         }
-        float x4[4];
-        get4_f32(&sm.lam[t * LDL + c0], x4);
-        put4_f32(a.ck_lam + (int64_t)ci * CC * 64 + t * 64 + c0, x4);
+        get4_f32(&sm.lam[t * LDL + c0], po.lam);
     }
     __syncthreads();
     // W' = T Ahat, U = T wv (wave w: channel tile w); products of hi/lo pairs keep
-    // three terms (hi hi, hi lo, lo hi).  Out from the accumulators: -W'^T (bf16)
-    // and U^T (f32), [channel][token].
+    // three terms (hi hi, hi lo, lo hi); -W'^T and U^T leave from the accumulators
+    // after the next chunk's staging.
     {
         const bf16x8_t ta = frag(sm.tb, LDB, 0), tal = frag(sm.tbl, LDB, 0);
         const bf16x8_t ab = frag_tr(sm.ah, 0, 16 * w), abl = frag_tr(sm.ahl, 0, 16 * w);
@@ -330,9 +387,15 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a) {
         f32x4 y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, vb, zero4(), 0, 0, 0);
         y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ta, vbl, y, 0, 0, 0);
         y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tal, vb, y, 0, 0, 0);
-        const int64_t o = ((int64_t)ci * 64 + 16 * w + acc_col()) * CC + acc_row(0);
-        *reinterpret_cast<uint2 *>(a.lr_wt + o) = make_uint2(bf16_pack2(-x[0], -x[1]), bf16_pack2(-x[2], -x[3]));
-        *reinterpret_cast<float4 *>(a.lr_u + o) = make_float4(y[0], y[1], y[2], y[3]);
+        po.x = x;
+        po.y = y;
+    }
+    __syncthreads();  // the next chunk's staging overwrites the tiles read above
+    }
+    {
+        const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int last = blockIdx.x + (nchunks - 1 - (int)blockIdx.x) / (int)gridDim.x * gridDim.x;
+        cwprep_store(a, last, tid, w, po);
     }
 }
 
@@ -357,49 +420,126 @@ struct CwOutSmem {
 };
 }  // namespace
 
-__global__ void __launch_bounds__(NT4) cw_out_kernel(ChunkArgs a) {
-    __shared__ CwOutSmem sm;
-    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
-    const int t = tid >> 4, c0 = 4 * (tid & 15), t0 = c * CC, tg = t0 + t;
-    const bool inb = tg < a.T;
-    for (int i = tid; i < CC * 16; i += NT4) {
-        const int r = i >> 4, cc = 16 + (i & 15);
-        sm.tb[r * LDB + cc] = 0;
-        sm.tbl[r * LDB + cc] = 0;
-        sm.pr[r * LDB + cc] = 0;
-        sm.prl[r * LDB + cc] = 0;
-    }
-    for (int i = tid; i < 4 * 64 * 16; i += NT4) {
-        uint16_t *tl = (i >> 10) == 0 ? sm.rt : (i >> 10) == 1 ? sm.rtl : (i >> 10) == 2 ? sm.dt : sm.dtl;
-        tl[((i >> 4) & 63) * LDW + 16 + (i & 15)] = 0;
-    }
-    const CwGate *gb = a.ck_cwg + ci;
-    const float va = gb->val[t];
-    const int sg = gb->seg[t];
-    const bool on = va != 0.f;
-    float qv[4], kv[4], vv[4], er[4], wr[4], L[4];
-    load4_bf16(a.q, a.qs, b, tg, h, c0, inb, qv);
-    load4_bf16(a.k, a.ks, b, tg, h, c0, inb, kv);
-    load4_bf16(a.v, a.vs, b, tg, h, c0, inb, vv);
-    load4_f32(a.erase, b, tg, h, c0, inb, 0.f, er);
-    load4_f32(a.write, b, tg, h, c0, inb, 0.f, wr);
-    mask4(qv, on, 0.f), mask4(kv, on, 0.f), mask4(vv, on, 0.f), mask4(er, on, 0.f), mask4(wr, on, 0.f);
-    get4_f32(a.ck_lam + (int64_t)ci * CC * 64 + t * 64 + c0, L);
-    {
+// One chunk's inputs to out, held in registers.  Rows past the sequence end read
+// the last row (the gate block marks those tokens invalid and the staging
+// zeroes them), so the loads take no branch.  Part 0: the gate block, q, k, v,
+// erase, write, Lambda; part 1: S0 (hi/lo) and T.
+struct CwOutIn {
+    float va;
+    int sg;
+    uint2 q, k, v;
+    float er[4], wr[4], L[4];
+    uint4 s0[2], s0l[2];
+    float tf;
+};
+template <int P>
+__device__ __forceinline__ void cwout_load(const ChunkArgs &a, int ci, int tid, CwOutIn &x) {
+    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = tid >> 4, c0 = 4 * (tid & 15), tg = c * CC + t;
+    const int tr = tg < a.T ? tg : a.T - 1;
+    if constexpr (P == 0) {
+        const CwGate *gb = a.ck_cwg + ci;
+        x.va = gb->val[t];
+        x.sg = gb->seg[t];
+        x.q = *reinterpret_cast<const uint2 *>(row_ptr(a.q, a.qs, b, tr, h) + c0);
+        x.k = *reinterpret_cast<const uint2 *>(row_ptr(a.k, a.ks, b, tr, h) + c0);
+        x.v = *reinterpret_cast<const uint2 *>(row_ptr(a.v, a.vs, b, tr, h) + c0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x.er[e] = ld4<float>(a.erase, b, tr, h, c0 + e);
+            x.wr[e] = ld4<float>(a.write, b, tr, h, c0 + e);
+        }
+        get4_f32(a.ck_lam + (int64_t)ci * CC * 64 + t * 64 + c0, x.L);
+    } else {
         const uint16_t *S0 = a.ck_state + (int64_t)ci * 64 * 64;
         const uint16_t *S0l = a.ck_state_lo + (int64_t)ci * 64 * 64;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int p = tid + NT4 * i, r = p >> 3, cb = 8 * (p & 7);
-            *reinterpret_cast<uint4 *>(&sm.st[r * LDB + cb]) =
-                *reinterpret_cast<const uint4 *>(S0 + r * 64 + cb);
-            *reinterpret_cast<uint4 *>(&sm.stl[r * LDB + cb]) =
-                *reinterpret_cast<const uint4 *>(S0l + r * 64 + cb);
+            x.s0[i] = *reinterpret_cast<const uint4 *>(S0 + r * 64 + cb);
+            x.s0l[i] = *reinterpret_cast<const uint4 *>(S0l + r * 64 + cb);
         }
-        load_t_split(a.ck_tf + (int64_t)ci * CC * CC, sm.tb, sm.tbl, tid);
+        x.tf = a.ck_tf[(int64_t)ci * CC * CC + tid];
     }
+}
+
+// The last stores of an out chunk, held until the next chunk's staging: the O
+// row piece of threads < 128 (bf16 output) and the score of threads < 16.
+struct CwOutOut {
+    uint4 o;
+    float score;
+};
+__device__ __forceinline__ void cwout_store(const ChunkArgs &a, int ci, int tid, const CwOutOut &x) {
+    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H, t0 = c * CC;
+    if (a.out_bf16 && tid < CC * 8) {
+        const int r = tid >> 3, cb = 8 * (tid & 7), tq = t0 + r;
+        if (tq < a.T)
+            *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.out) + (((int64_t)b * a.T + tq) * a.H + h) * 64 + cb) =
+                x.o;
+    }
+    if (a.scores && tid < CC && t0 + tid < a.T) a.scores[((int64_t)b * a.T + t0 + tid) * a.H + h] = x.score;
+}
+
+// Workgroups walk chunks blockIdx.x, blockIdx.x + gridDim.x, ... (as many
+// workgroups as fit the GPU at once): the next chunk's inputs are loaded into
+// registers while the current one computes, and a chunk's O rows and scores
+// are stored after the next chunk's staging.
+__global__ void __launch_bounds__(NT4) cw_out_kernel(ChunkArgs a, int nchunks) {
+    __shared__ CwOutSmem sm;
+    {  // zero padding (columns 16..31 of T, P, R^T and delta^T), once
+        const int tid = threadIdx.x;
+        for (int i = tid; i < CC * 16; i += NT4) {
+            const int r = i >> 4, cc = 16 + (i & 15);
+            sm.tb[r * LDB + cc] = 0;
+            sm.tbl[r * LDB + cc] = 0;
+            sm.pr[r * LDB + cc] = 0;
+            sm.prl[r * LDB + cc] = 0;
+        }
+        for (int i = tid; i < 4 * 64 * 16; i += NT4) {
+            uint16_t *tl = (i >> 10) == 0 ? sm.rt : (i >> 10) == 1 ? sm.rtl : (i >> 10) == 2 ? sm.dt : sm.dtl;
+            tl[((i >> 4) & 63) * LDW + 16 + (i & 15)] = 0;
+        }
+    }
+    CwOutIn in;
+    cwout_load<0>(a, blockIdx.x, threadIdx.x, in);
+    cwout_load<1>(a, blockIdx.x, threadIdx.x, in);
+    CwOutOut po;
+    for (int ci = blockIdx.x; ci < nchunks; ci += gridDim.x) {
+    // An opaque zero keeps the lane- and wave-dependent address arithmetic inside
+    // the loop (hoisted, it would stay live across it).
+    int zero;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+    const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+    const int t = tid >> 4, c0 = 4 * (tid & 15), t0 = c * CC;
+    // The next chunk; past the end this chunk again, so the loads need no branch.
+    const int cn = ci + (int)gridDim.x < nchunks ? ci + (int)gridDim.x : ci;
     {
+        const float va = in.va;
+        const int sg = in.sg;
+        const bool on = va != 0.f;
+        float qv[4], kv[4], vv[4], er[4], wr[4], L[4];
+        qv[0] = bf16_val((uint16_t)(in.q.x & 0xffff)), qv[1] = bf16_val((uint16_t)(in.q.x >> 16));
+        qv[2] = bf16_val((uint16_t)(in.q.y & 0xffff)), qv[3] = bf16_val((uint16_t)(in.q.y >> 16));
+        kv[0] = bf16_val((uint16_t)(in.k.x & 0xffff)), kv[1] = bf16_val((uint16_t)(in.k.x >> 16));
+        kv[2] = bf16_val((uint16_t)(in.k.y & 0xffff)), kv[3] = bf16_val((uint16_t)(in.k.y >> 16));
+        vv[0] = bf16_val((uint16_t)(in.v.x & 0xffff)), vv[1] = bf16_val((uint16_t)(in.v.x >> 16));
+        vv[2] = bf16_val((uint16_t)(in.v.y & 0xffff)), vv[3] = bf16_val((uint16_t)(in.v.y >> 16));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) er[e] = in.er[e], wr[e] = in.wr[e], L[e] = in.L[e];
+        mask4(qv, on, 0.f), mask4(kv, on, 0.f), mask4(vv, on, 0.f), mask4(er, on, 0.f), mask4(wr, on, 0.f);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int p = tid + NT4 * i, r = p >> 3, cb = 8 * (p & 7);
+            *reinterpret_cast<uint4 *>(&sm.st[r * LDB + cb]) = in.s0[i];
+            *reinterpret_cast<uint4 *>(&sm.stl[r * LDB + cb]) = in.s0l[i];
+        }
+        {
+            uint16_t hi, lo;
+            split_bf16(in.tf, hi, lo);
+            sm.tb[(tid >> 4) * LDB + (tid & 15)] = hi;
+            sm.tbl[(tid >> 4) * LDB + (tid & 15)] = lo;
+        }
         float b4[4], qh[4], ah[4], wv[4];
         float ksq = 0.f;
 #pragma unroll
@@ -424,7 +564,10 @@ __global__ void __launch_bounds__(NT4) cw_out_kernel(ChunkArgs a) {
             sm.seg[t] = sg;
         }
     }
+    if (ci != (int)blockIdx.x) cwout_store(a, ci - gridDim.x, tid, po);  // the previous chunk's
+    cwout_load<0>(a, cn, tid, in);
     __syncthreads();
+    cwout_load<1>(a, cn, tid, in);
     // P (lower, same segment), elementwise; pair p on lanes 2p, 2p + 1.
     for (int base = 0; base < 2 * 136; base += NT4) {
         const int task = base + tid, p = task >> 1, half = task & 1;
@@ -508,17 +651,19 @@ __global__ void __launch_bounds__(NT4) cw_out_kernel(ChunkArgs a) {
         }
     }
     __syncthreads();
-    if (a.out_bf16 && tid < CC * 8) {
-        const int r = tid >> 3, cb = 8 * (tid & 7), tq = t0 + r;
-        if (tq < a.T)
-            *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.out) +
-                                       (((int64_t)b * a.T + tq) * a.H + h) * 64 + cb) =
-                *reinterpret_cast<const uint4 *>(&sm.qh[r * LDB + cb]);
+    // O row pieces and scores into registers (stored after the next staging).
+    po.o = *reinterpret_cast<const uint4 *>(&sm.qh[(tid >> 3 & 15) * LDB + 8 * (tid & 7)]);
+    {
+        const int tk = tid & 15;
+        const float dd = sm.dd[0][tk] + sm.dd[1][tk] + sm.dd[2][tk] + sm.dd[3][tk];
+        po.score = sm.val[tk] != 0.f ? sqrtf(sm.kk[tk] * dd) : 0.f;
     }
-    if (a.scores && tid < CC && t0 + tid < a.T) {
-        const float dd = sm.dd[0][tid] + sm.dd[1][tid] + sm.dd[2][tid] + sm.dd[3][tid];
-        a.scores[((int64_t)b * a.T + t0 + tid) * a.H + h] =
-            sm.val[tid] != 0.f ? sqrtf(sm.kk[tid] * dd) : 0.f;
+    __syncthreads();  // the next chunk's staging overwrites the tiles read above
+    }
+    {
+        const int tid = threadIdx.x;
+        const int last = blockIdx.x + (nchunks - 1 - (int)blockIdx.x) / (int)gridDim.x * gridDim.x;
+        cwout_store(a, last, tid, po);
     }
 }
 
@@ -539,57 +684,125 @@ struct CwBPrepSmem {
 };
 }  // namespace
 
-__global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a) {
-    __shared__ CwBPrepSmem sm;
-    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
+// One chunk's inputs to bprep, held in registers.  Rows past the sequence end
+// read the last row (the gate block marks those tokens invalid and the staging
+// zeroes them), a missing dO reads q (zeroed at the staging) and a missing
+// score adjoint reads the delta checkpoint, so the loads take no branch.
+// Part 0: q, k, dO and the gate block; part 1: erase, Lambda, delta, T, P and
+// the score terms.
+struct CwBpIn {
+    uint2 q, k, dO;
+    float er[4], L[4], dl[4], dacc[4];
+    float tf, pf, va, dsc;
+    int sg;
+};
+template <int P>
+__device__ __forceinline__ void cwbp_load(const ChunkArgs &a, int ci, int tid, int w, CwBpIn &x) {
+    const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid >> 4, c0 = 4 * (tid & 15), tg = c * CC + t;
-    const bool inb = tg < a.T;
-    zero_lds(sm.qh + RT16, RT32 - RT16, tid);
-    zero_lds(sm.qhl + RT16, RT32 - RT16, tid);
-    zero_lds(sm.ah + RT16, RT32 - RT16, tid);
-    zero_lds(sm.ahl + RT16, RT32 - RT16, tid);
-    zero_lds(sm.dor + RT16, RT32 - RT16, tid);
-    for (int i = tid; i < CC * 16; i += NT4) {
-        const int r = i >> 4, cc = 16 + (i & 15);
-        sm.tb[r * LDB + cc] = 0;
-        sm.tbl[r * LDB + cc] = 0;
-        sm.ptr[r * LDB + cc] = 0;
-        sm.ptrl[r * LDB + cc] = 0;
-    }
-    for (int i = tid; i < 4 * 64 * 16; i += NT4) {
-        uint16_t *tl = (i >> 10) == 0 ? sm.wt : (i >> 10) == 1 ? sm.wtl : (i >> 10) == 2 ? sm.xt : sm.xtl;
-        tl[((i >> 4) & 63) * LDW + 16 + (i & 15)] = 0;
-    }
-    const CwGate *gb = a.ck_cwg + ci;
-    const float va = gb->val[t];
-    const int sg = gb->seg[t];
-    const bool on = va != 0.f;
-    float qv[4], kv[4], dov[4], er[4], L[4];
-    load4_bf16(a.q, a.qs, b, tg, h, c0, inb, qv);
-    load4_bf16(a.k, a.ks, b, tg, h, c0, inb, kv);
-    if (a.dout) load4_bf16(a.dout, a.ds, b, tg, h, c0, inb, dov);
-    else dov[0] = dov[1] = dov[2] = dov[3] = 0.f;
-    load4_f32(a.erase, b, tg, h, c0, inb, 0.f, er);
-    mask4(qv, on, 0.f), mask4(kv, on, 0.f), mask4(dov, on, 0.f), mask4(er, on, 0.f);
-    get4_f32(a.ck_lam + (int64_t)ci * CC * 64 + t * 64 + c0, L);
-    const float *dck = a.ck_delta + (int64_t)ci * CC * 64;
-    float dl4[4], dacc[4];
-    get4_f32(dck + t * 64 + c0, dl4);
+    const int tr = tg < a.T ? tg : a.T - 1;
+    if constexpr (P == 0) {
+        x.q = *reinterpret_cast<const uint2 *>(row_ptr(a.q, a.qs, b, tr, h) + c0);
+        x.k = *reinterpret_cast<const uint2 *>(row_ptr(a.k, a.ks, b, tr, h) + c0);
+        x.dO = *reinterpret_cast<const uint2 *>(row_ptr(a.dout ? a.dout : a.q, a.dout ? a.ds : a.qs, b, tr, h) + c0);
+        const CwGate *gb = a.ck_cwg + ci;
+        x.va = gb->val[t];
+        x.sg = gb->seg[t];
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)  // delta at this lane's accumulator positions (value tile w)
-        dacc[i] = a.dscores ? dck[acc_row(i) * 64 + 16 * w + acc_col()] : 0.f;
-    load_t_split(a.ck_tf + (int64_t)ci * CC * CC, sm.tb, sm.tbl, tid);
-    load_pt_split(a.ck_p + (int64_t)ci * CC * CC, sm.ptr, sm.ptrl, tid);
+        for (int e = 0; e < 4; ++e) x.er[e] = ld4<float>(a.erase, b, tr, h, c0 + e);
+        get4_f32(a.ck_lam + (int64_t)ci * CC * 64 + t * 64 + c0, x.L);
+        const float *dck = a.ck_delta + (int64_t)ci * CC * 64;
+        get4_f32(dck + t * 64 + c0, x.dl);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x.dacc[i] = dck[acc_row(i) * 64 + 16 * w + acc_col()];
+        x.tf = a.ck_tf[(int64_t)ci * CC * CC + (tid >> 4) * CC + (tid & 15)];
+        x.pf = a.ck_p[(int64_t)ci * CC * CC + (tid & 15) * CC + (tid >> 4)];
+        x.dsc = (a.dscores ? a.dscores : a.ck_delta)[((int64_t)b * a.T + tr) * a.H + h];
+    }
+}
+
+// N of chunk ci (transposed, f32) from the registers it was formed in.
+__device__ __forceinline__ void cwbp_store(const ChunkArgs &a, int ci, int w, const f32x4 (&n)[4]) {
+    float *Nt = a.ws_n + (int64_t)ci * 64 * 64;
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn)
+        *reinterpret_cast<float4 *>(&Nt[(16 * tn + acc_col()) * 64 + 16 * w + acc_row(0)]) =
+            make_float4(n[tn][0], n[tn][1], n[tn][2], n[tn][3]);
+}
+
+// Workgroups walk chunks blockIdx.x, blockIdx.x + gridDim.x, ... (as many
+// workgroups as fit the GPU at once): the next chunk's inputs are loaded into
+// registers while the current one computes, and a chunk's N is stored after
+// the next chunk's staging, so that no chunk but a workgroup's first waits on
+// its loads or on the previous chunk's stores.
+__global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a, int nchunks) {
+    __shared__ CwBPrepSmem sm;
+    {  // zero padding (rows 16..31 of the token-row tiles, columns 16..31 of the others), once
+        const int tid = threadIdx.x;
+        zero_lds(sm.qh + RT16, RT32 - RT16, tid);
+        zero_lds(sm.qhl + RT16, RT32 - RT16, tid);
+        zero_lds(sm.ah + RT16, RT32 - RT16, tid);
+        zero_lds(sm.ahl + RT16, RT32 - RT16, tid);
+        zero_lds(sm.dor + RT16, RT32 - RT16, tid);
+        for (int i = tid; i < CC * 16; i += NT4) {
+            const int r = i >> 4, cc = 16 + (i & 15);
+            sm.tb[r * LDB + cc] = 0;
+            sm.tbl[r * LDB + cc] = 0;
+            sm.ptr[r * LDB + cc] = 0;
+            sm.ptrl[r * LDB + cc] = 0;
+        }
+        for (int i = tid; i < 4 * 64 * 16; i += NT4) {
+            uint16_t *tl = (i >> 10) == 0 ? sm.wt : (i >> 10) == 1 ? sm.wtl : (i >> 10) == 2 ? sm.xt : sm.xtl;
+            tl[((i >> 4) & 63) * LDW + 16 + (i & 15)] = 0;
+        }
+    }
+    CwBpIn in;
     {
+        const int w0 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        cwbp_load<0>(a, blockIdx.x, threadIdx.x, w0, in);
+        cwbp_load<1>(a, blockIdx.x, threadIdx.x, w0, in);
+    }
+    f32x4 nacc[4];  // N = Y - W'^T X, held until the next chunk's staging is done
+    for (int ci = blockIdx.x; ci < nchunks; ci += gridDim.x) {
+    // An opaque zero keeps the lane- and wave-dependent address arithmetic inside
+    // the loop (hoisted, it would stay live across it).
+    int zero;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+    const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t = tid >> 4, c0 = 4 * (tid & 15);
+    // The next chunk; past the end this chunk again, so the loads need no branch.
+    const int cn = ci + (int)gridDim.x < nchunks ? ci + (int)gridDim.x : ci;
+    {
+        const bool on = in.va != 0.f;
+        float qv[4], kv[4], dov[4], er[4];
+        const uint2 q2 = in.q, k2 = in.k, d2 = in.dO;
+        qv[0] = bf16_val((uint16_t)(q2.x & 0xffff)), qv[1] = bf16_val((uint16_t)(q2.x >> 16));
+        qv[2] = bf16_val((uint16_t)(q2.y & 0xffff)), qv[3] = bf16_val((uint16_t)(q2.y >> 16));
+        kv[0] = bf16_val((uint16_t)(k2.x & 0xffff)), kv[1] = bf16_val((uint16_t)(k2.x >> 16));
+        kv[2] = bf16_val((uint16_t)(k2.y & 0xffff)), kv[3] = bf16_val((uint16_t)(k2.y >> 16));
+        dov[0] = bf16_val((uint16_t)(d2.x & 0xffff)), dov[1] = bf16_val((uint16_t)(d2.x >> 16));
+        dov[2] = bf16_val((uint16_t)(d2.y & 0xffff)), dov[3] = bf16_val((uint16_t)(d2.y >> 16));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) er[e] = in.er[e];
+        mask4(qv, on, 0.f), mask4(kv, on, 0.f), mask4(dov, on && a.dout, 0.f), mask4(er, on, 0.f);
+        {
+            uint16_t hi, lo;
+            split_bf16(in.tf, hi, lo);
+            sm.tb[(tid >> 4) * LDB + (tid & 15)] = hi;
+            sm.tbl[(tid >> 4) * LDB + (tid & 15)] = lo;
+            split_bf16(in.pf, hi, lo);
+            sm.ptr[(tid >> 4) * LDB + (tid & 15)] = hi;
+            sm.ptrl[(tid >> 4) * LDB + (tid & 15)] = lo;
+        }
         float qh[4], ah[4], ksq = 0.f, dsq = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const float bt = sg == 0 ? __expf(L[e]) : 0.f;
+            const float bt = in.sg == 0 ? __expf(in.L[e]) : 0.f;
             qh[e] = bt * qv[e];
             ah[e] = bt * er[e] * kv[e];
             ksq += kv[e] * kv[e];
-            dsq += dl4[e] * dl4[e];
+            dsq += in.dl[e] * in.dl[e];
         }
         put4_split(&sm.qh[t * LDB + c0], &sm.qhl[t * LDB + c0], qh);
         put4_split(&sm.ah[t * LDB + c0], &sm.ahl[t * LDB + c0], ah);
@@ -597,12 +810,17 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a) {
         ksq = row16_sum(ksq);
         dsq = row16_sum(dsq);
         if ((tid & 15) == 0) {
-            const float dsc = (a.dscores && inb) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
             const float nk = sqrtf(ksq), nd = sqrtf(dsq);
-            sm.cs[t] = (nk > 0.f && nd > 0.f) ? dsc * nk / nd : 0.f;
+            sm.cs[t] = (a.dscores && nk > 0.f && nd > 0.f) ? in.dsc * nk / nd : 0.f;
         }
     }
+    float dacc[4];  // delta at this lane's accumulator positions (value tile w)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dacc[i] = in.dacc[i];
+    if (ci != (int)blockIdx.x) cwbp_store(a, ci - gridDim.x, w, nacc);  // the previous chunk's N
+    cwbp_load<0>(a, cn, tid, w, in);
     __syncthreads();
+    cwbp_load<1>(a, cn, tid, w, in);
     // Y = Qhat^T dO (row tile w of keys, all value tiles) and W' = T Ahat (tile w).
     f32x4 y[4];
     {
@@ -635,10 +853,9 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a) {
         store_tile_t_split(&sm.xt[(16 * w) * LDW], &sm.xtl[(16 * w) * LDW], LDW, x);
     }
     __syncthreads();
-    // N = Y - W'^T X: key row tile w, value tiles 0..3; stored transposed (f32).
+    // N = Y - W'^T X: key row tile w, value tiles 0..3, in registers.
     {
         const bf16x8_t wa = frag(&sm.wt[(16 * w) * LDW], LDW, 0), wal = frag(&sm.wtl[(16 * w) * LDW], LDW, 0);
-        float *Nt = a.ws_n + (int64_t)ci * 64 * 64;
 #pragma unroll
         for (int tn = 0; tn < 4; ++tn) {
             const bf16x8_t xb = frag(&sm.xt[(16 * tn) * LDW], LDW, 0), xbl = frag(&sm.xtl[(16 * tn) * LDW], LDW, 0);
@@ -646,9 +863,16 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a) {
             x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xb, x, 0, 0, 0);
             x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xbl, x, 0, 0, 0);
             x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wal, xb, x, 0, 0, 0);
-            *reinterpret_cast<float4 *>(&Nt[(16 * tn + acc_col()) * 64 + 16 * w + acc_row(0)]) =
-                make_float4(y[tn][0] - x[0], y[tn][1] - x[1], y[tn][2] - x[2], y[tn][3] - x[3]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) nacc[tn][e] = y[tn][e] - x[e];
         }
+    }
+    __syncthreads();  // the next chunk's staging overwrites the tiles read above
+    }
+    {
+        const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int last = blockIdx.x + (nchunks - 1 - (int)blockIdx.x) / (int)gridDim.x * gridDim.x;
+        cwbp_store(a, last, w, nacc);
     }
 }
 
@@ -1075,14 +1299,14 @@ static hipError_t cw_scan(const ChunkArgs &a, bool reverse, hipStream_t stream) 
 hipError_t launch_cw_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
     const int nch = a.B * a.H * a.nc;
     cmark(ev, 0, stream);
-    hipLaunchKernelGGL(cw_prep_kernel, dim3(nch), dim3(NT4), 0, stream, a);
+    hipLaunchKernelGGL(cw_prep_kernel, dim3(std::min(nch, 4 * device_cus())), dim3(NT4), 0, stream, a, nch);
     cmark(ev, 1, stream);
     cmark(ev, 2, stream);
     const hipError_t e = cw_scan(a, false, stream);
     if (e != hipSuccess) return e;
     cmark(ev, 3, stream);
     cmark(ev, 4, stream);
-    hipLaunchKernelGGL(cw_out_kernel, dim3(nch), dim3(NT4), 0, stream, a);
+    hipLaunchKernelGGL(cw_out_kernel, dim3(std::min(nch, 2 * device_cus())), dim3(NT4), 0, stream, a, nch);
     cmark(ev, 5, stream);
     return hipGetLastError();
 }
@@ -1090,7 +1314,7 @@ hipError_t launch_cw_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_
 hipError_t launch_cw_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
     const int nch = a.B * a.H * a.nc;
     cmark(ev, 0, stream);
-    hipLaunchKernelGGL(cw_bprep_kernel, dim3(nch), dim3(NT4), 0, stream, a);
+    hipLaunchKernelGGL(cw_bprep_kernel, dim3(std::min(nch, 3 * device_cus())), dim3(NT4), 0, stream, a, nch);
     cmark(ev, 1, stream);
     cmark(ev, 2, stream);
     const hipError_t e = cw_scan(a, true, stream);
