@@ -929,6 +929,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
     // exhaust the registers.
     int zero;
     asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+    const ChunkArgs &a = chunk_args_reloaded();
     const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
     const int r0 = 16 * tm + 4 * (lane_id() >> 4);
@@ -1253,6 +1254,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
     {
         const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         const int last = blockIdx.x + (nchunks - 1 - (int)blockIdx.x) / (int)gridDim.x * gridDim.x;
+        const ChunkArgs &a = chunk_args_reloaded();
         const ChunkPos pl = chunk_pos(a, last);
         bgrad_store_rows(a, pl, w, bgrad_grad_frag(dQt, w), bgrad_grad_frag(dKt, w), bgrad_grad_frag(dVt, w));
         bgrad_store_gates(a, pl, w, pdg, pdb);

@@ -267,6 +267,7 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a, int nchunks) 
     // the loop (hoisted, it would stay live across it).
     int zero;
     asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+    const ChunkArgs &a = chunk_args_reloaded();
     const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = ci % a.nc;
     const int t = tid >> 4, c0 = 4 * (tid & 15), tg = c * CC + t;
@@ -395,6 +396,7 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a, int nchunks) 
     {
         const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         const int last = blockIdx.x + (nchunks - 1 - (int)blockIdx.x) / (int)gridDim.x * gridDim.x;
+        const ChunkArgs &a = chunk_args_reloaded();
         cwprep_store(a, last, tid, w, po);
     }
 }
@@ -509,6 +511,7 @@ __global__ void __launch_bounds__(NT4) cw_out_kernel(ChunkArgs a, int nchunks) {
     // the loop (hoisted, it would stay live across it).
     int zero;
     asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+    const ChunkArgs &a = chunk_args_reloaded();
     const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid >> 4, c0 = 4 * (tid & 15), t0 = c * CC;
@@ -663,6 +666,7 @@ __global__ void __launch_bounds__(NT4) cw_out_kernel(ChunkArgs a, int nchunks) {
     {
         const int tid = threadIdx.x;
         const int last = blockIdx.x + (nchunks - 1 - (int)blockIdx.x) / (int)gridDim.x * gridDim.x;
+        const ChunkArgs &a = chunk_args_reloaded();
         cwout_store(a, last, tid, po);
     }
 }
@@ -769,6 +773,7 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a, int nchunks)
     // the loop (hoisted, it would stay live across it).
     int zero;
     asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+    const ChunkArgs &a = chunk_args_reloaded();
     const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t = tid >> 4, c0 = 4 * (tid & 15);
     // The next chunk; past the end this chunk again, so the loads need no branch.
@@ -872,6 +877,7 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a, int nchunks)
     {
         const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         const int last = blockIdx.x + (nchunks - 1 - (int)blockIdx.x) / (int)gridDim.x * gridDim.x;
+        const ChunkArgs &a = chunk_args_reloaded();
         cwbp_store(a, last, w, nacc);
     }
 }

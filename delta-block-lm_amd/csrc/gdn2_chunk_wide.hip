@@ -317,6 +317,7 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a, int nchunks) 
     // the loop (hoisted, it would stay live across it and exhaust the registers).
     int zero;
     asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+    const ChunkArgs &a = chunk_args_reloaded();
     const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, t0 = c * C;
@@ -452,6 +453,7 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a, int nchunks) 
     {
         const int tid = threadIdx.x;
         const int last = blockIdx.x + (nchunks - 1 - (int)blockIdx.x) / (int)gridDim.x * gridDim.x;
+        const ChunkArgs &a = chunk_args_reloaded();
         wout_store(a, last, NVB - 1, tid, sm);
         if ((tid >> 6) == 0) wout_store_tok(a, last, tok);
     }
@@ -551,6 +553,7 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a, int nchunks
     // the loop (hoisted, it would stay live across it and exhaust the registers).
     int zero;
     asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+    const ChunkArgs &a = chunk_args_reloaded();
     const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
     const float *dck = a.ck_delta + (int64_t)ci * C * KD;
@@ -682,6 +685,7 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a, int nchunks
     {
         const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         const int last = blockIdx.x + (nchunks - 1 - (int)blockIdx.x) / (int)gridDim.x * gridDim.x;
+        const ChunkArgs &a = chunk_args_reloaded();
         wbprep_store(a, last, w >> 1, 2 * (w & 1), yacc);
     }
 }
