@@ -398,6 +398,8 @@ constexpr int PC_THREADS = 7 * 64;
 // s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in
 // bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+// s_waitcnt immediate that waits for lgkmcnt == 0 only (vmcnt 63, expcnt 7).
+constexpr int LGKMCNT_ZERO = 15 | (3 << 14) | (7 << 4);
 
 struct PcSmem {
     uint4 m[PC_RING][D * D / 8];      // M rows: 16-byte chunk x of row r holds chunk x ^ (r & 7)
@@ -416,6 +418,9 @@ __device__ __forceinline__ void pc_step(int s, int j, int w, f32x4 (&X)[4], PcSm
     uint16_t *xh = sm.xs[s & 1][w][0], *xl = sm.xs[s & 1][w][1];
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm) store_tile_t_split(xh + 16 * tm, xl + 16 * tm, LDB, X[tm]);
+    // The writer wave reads these tiles after the barrier, and the LDS operations
+    // of different waves may complete out of issue order: wait until they landed.
+    __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);
     pc_barrier();  // this step's map is in its slot; the writer may read X^T
     const uint4 *slot = sm.m[s % PC_RING], *nslot = sm.n[s % PC_NRING];
     f32x4 Y[4];
