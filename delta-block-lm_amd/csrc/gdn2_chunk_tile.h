@@ -297,14 +297,29 @@ __device__ __forceinline__ void ut_inverse(const float *Af, float *Tf, int w) {
     if (w == 0) {
         const int bk = l >> 4, col = l & 15;
         const float *Ab = Af + (16 * bk) * LDF + 16 * bk;
+        // Row r of the block, L[r][0..r-1], as (r + 3) / 4 float4 reads (the entries
+        // at and above the diagonal are zero), issued PD rows ahead of its use so
+        // that the LDS latency overlaps the substitution instead of preceding each row.
+        constexpr int PD = 4;
+        float4 Lr[16][4];
+        auto load_row = [&](int r) {
+#pragma unroll
+            for (int v = 0; v < (r + 3) / 4; ++v) Lr[r][v] = *reinterpret_cast<const float4 *>(Ab + r * LDF + 4 * v);
+        };
+#pragma unroll
+        for (int r = 1; r <= PD; ++r) load_row(r);
         float Tc[16];  // T_bb[r][col]; rows above col come out 0
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
+            if (r >= 1 && r + PD < 16) load_row(r + PD);
+            __builtin_amdgcn_sched_barrier(0);  // keeps the reads ahead of this row's FMAs
             float e0 = 0.f, e1 = 0.f;  // two chains halve the dependent FMA latency
 #pragma unroll
             for (int q = 0; q < r; ++q) {
-                if (q & 1) e1 += Ab[r * LDF + q] * Tc[q];
-                else e0 += Ab[r * LDF + q] * Tc[q];
+                const float4 &v4 = Lr[r][q >> 2];
+                const float a = (q & 3) == 0 ? v4.x : (q & 3) == 1 ? v4.y : (q & 3) == 2 ? v4.z : v4.w;
+                if (q & 1) e1 += a * Tc[q];
+                else e0 += a * Tc[q];
             }
             Tc[r] = (r == col ? 1.f : 0.f) - (e0 + e1);
         }
