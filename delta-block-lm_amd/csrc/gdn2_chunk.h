@@ -23,19 +23,19 @@ struct GateBlock {
 //   gate   GateBlock
 //   delta  the chunk's edits delta[t][v], f32 row-major
 //   Mt     the adjoint map M = A_c^T, bf16 row-major
-// plus the forward state map S_next = A_c S + B_c (A_c bf16 row-major, B_c f32
-// transposed), read only by the forward state scan.  Transposed f32 matrices
-// let each MFMA lane move its four accumulator rows with one 16-byte access.
+// plus the forward state map S_next = A_c S + B_c (A_c bf16 row-major, B_c bf16
+// transposed), read only by the forward state scan.  Transposed matrices let
+// each MFMA lane move its four accumulator rows with one 8-byte access.
 constexpr size_t CK_STATE_BYTES = CHUNK_D * CHUNK_D * sizeof(uint16_t);
 constexpr size_t CK_T_BYTES = CHUNK * CHUNK * sizeof(uint16_t);
 constexpr size_t CK_GATE_BYTES = sizeof(GateBlock);
 constexpr size_t CK_DELTA_BYTES = CHUNK * CHUNK_D * sizeof(float);
 constexpr size_t CK_MAP_M_BYTES = CHUNK_D * CHUNK_D * sizeof(uint16_t);
-constexpr size_t CK_MAP_N_BYTES = CHUNK_D * CHUNK_D * sizeof(float);
+constexpr size_t CK_MAP_N_BYTES = CHUNK_D * CHUNK_D * sizeof(uint16_t);
 constexpr size_t CK_CHUNK_BYTES = CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES + CK_DELTA_BYTES +
                                   2 * CK_MAP_M_BYTES + CK_MAP_N_BYTES;
-// Backward workspace per chunk: dS at the chunk end (bf16, transposed) and N of
-// the adjoint map (f32, transposed).
+// Backward workspace per chunk: dS at the chunk end and N of the adjoint map
+// (both bf16, transposed).
 constexpr size_t WS_CHUNK_BYTES = CK_STATE_BYTES + CK_MAP_N_BYTES;
 
 struct ChunkArgs {
@@ -55,7 +55,7 @@ struct ChunkArgs {
     float *ck_delta;
     uint16_t *ck_mt;   // adjoint map M = A_c^T
     uint16_t *map_m;   // forward state map A_c
-    float *map_n;      // forward state map B_c^T
+    uint16_t *map_n;   // forward state map B_c^T (bf16)
     // backward
     const uint16_t *dout;
     int64_t ds[3];
@@ -63,7 +63,8 @@ struct ChunkArgs {
     void *dq, *dk, *dv;
     float *dbeta, *dg, *dinitial;
     uint16_t *ws_dstate;  // [B*H*nc] adjoint of the state at each chunk end
-    float *ws_n;       // N of the adjoint map dS_start = M dS_end + N
+    float *ws_n;       // N of the adjoint map dS_start = M dS_end + N (f32; wide and channel-wise)
+    uint16_t *ws_nb;   // N^T of the adjoint map, bf16 (d = 64 chunk path)
     // Wide path (d_k = d_v = 128, value blocks of 64): per-chunk |k_t|^2 and the
     // value blocks' partial |delta_t|^2 (forward checkpoint).
     float *ck_kk, *ck_ddp;
@@ -134,7 +135,7 @@ inline void chunk_bind_checkpoint(ChunkArgs &a, void *ck) {
     p += n * CK_MAP_M_BYTES;
     a.map_m = reinterpret_cast<uint16_t *>(p);
     p += n * CK_MAP_M_BYTES;
-    a.map_n = reinterpret_cast<float *>(p);
+    a.map_n = reinterpret_cast<uint16_t *>(p);
 }
 
 // Carve the backward workspace.
@@ -142,7 +143,7 @@ inline void chunk_bind_workspace(ChunkArgs &a, void *ws) {
     const int64_t n = (int64_t)a.B * a.H * a.nc;
     char *p = static_cast<char *>(ws);
     a.ws_dstate = reinterpret_cast<uint16_t *>(p);
-    a.ws_n = reinterpret_cast<float *>(p + n * CK_STATE_BYTES);
+    a.ws_nb = reinterpret_cast<uint16_t *>(p + n * CK_STATE_BYTES);
 }
 
 // ---- channel-wise path: per-channel gates, 16-token chunks, d_k = d_v = 64 ------

@@ -183,7 +183,7 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         gemm2_atr(y, KLs, 16 * tm, Utl, tn0);
         const float gC = sm.gl.gamC;
         uint16_t *Mt = sm.slot[1];  // A_c^T over beta gam K, which is dead
-        float *Bt = a.map_n + (int64_t)ci * D * D;    // B transposed: Bt[col][row]
+        uint16_t *Bt = a.map_n + (int64_t)ci * D * D;  // B transposed: Bt[col][row], bf16
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int cc = 16 * (tn0 + j) + acc_col();
@@ -191,8 +191,8 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) am[i] = (16 * tm + acc_row(i) == cc ? gC : 0.f) - x[j][i];
             store_tile_t(&Mt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, am);
-            *reinterpret_cast<float4 *>(&Bt[cc * D + 16 * tm + acc_row(0)]) =
-                make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
+            *reinterpret_cast<uint2 *>(&Bt[cc * D + 16 * tm + acc_row(0)]) =
+                make_uint2(bf16_pack2(y[j][0], y[j][1]), bf16_pack2(y[j][2], y[j][3]));
         }
     }
     __syncthreads();
@@ -223,7 +223,7 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
 struct AffineArgs {
     int nc, B, H;
     const uint16_t *m;
-    const float *n;
+    const uint16_t *n;  // N^T (bf16)
     uint16_t *ckpt;  // X^T per chunk, bf16
     uint16_t *ckpt_lo;  // X^T - bf16(X^T) per chunk, bf16 (null: not kept)
     View x0;          // [B,H,64,64] strided (data may be null: zero)
@@ -392,7 +392,7 @@ namespace {
 constexpr int PC_RING = 4;                 // LDS slots of M
 constexpr int PC_MOPS = D * D * 2 / 1024;  // LDS-DMA instructions per map (1 KiB each)
 constexpr int PC_NRING = 5;                // LDS slots of N
-constexpr int PC_NOPS = D * D * 4 / 1024;  // LDS-DMA instructions per N (1 KiB each)
+constexpr int PC_NOPS = D * D * 2 / 1024;  // LDS-DMA instructions per N (1 KiB each)
 constexpr int PC_THREADS = 7 * 64;
 
 // s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in
@@ -403,7 +403,7 @@ constexpr int LGKMCNT_ZERO = 15 | (3 << 14) | (7 << 4);
 
 struct PcSmem {
     uint4 m[PC_RING][D * D / 8];      // M rows: 16-byte chunk x of row r holds chunk x ^ (r & 7)
-    uint4 n[PC_NRING][D * D / 4];     // N^T rows (f32): chunk x of column row j holds x ^ (j & 15)
+    uint4 n[PC_NRING][D * D / 8];     // N^T rows (bf16): chunk x of column row j holds x ^ (j & 7)
     uint16_t xs[2][4][2][16 * LDB];   // [step parity][compute wave][hi, lo]: X^T [col][row]
 };
 
@@ -422,12 +422,15 @@ __device__ __forceinline__ void pc_step(int s, int j, int w, f32x4 (&X)[4], PcSm
     // of different waves may complete out of issue order: wait until they landed.
     __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);
     pc_barrier();  // this step's map is in its slot; the writer may read X^T
-    const uint4 *slot = sm.m[s % PC_RING], *nslot = sm.n[s % PC_NRING];
+    const uint4 *slot = sm.m[s % PC_RING];
+    const uint2 *nslot = reinterpret_cast<const uint2 *>(sm.n[s % PC_NRING]);
     f32x4 Y[4];
 #pragma unroll
-    for (int tm = 0; tm < 4; ++tm) {
-        const float4 nv = __builtin_bit_cast(float4, nslot[j * 16 + ((4 * tm + (l >> 4)) ^ (j & 15))]);
-        Y[tm] = f32x4{nv.x, nv.y, nv.z, nv.w};
+    for (int tm = 0; tm < 4; ++tm) {  // N[16 tm + 4 g + i][j]: half g & 1 of chunk 2 tm + g / 2 of row j
+        const int g = l >> 4;
+        const uint2 nv = nslot[(j * 8 + ((2 * tm + (g >> 1)) ^ (j & 7))) * 2 + (g & 1)];
+        Y[tm] = f32x4{bf16_val((uint16_t)nv.x), bf16_val((uint16_t)(nv.x >> 16)), bf16_val((uint16_t)nv.y),
+                      bf16_val((uint16_t)(nv.y >> 16))};
     }
     // hi and lo products accumulate separately: two dependent MFMAs per tile
     f32x4 Z[4] = {zero4(), zero4(), zero4(), zero4()};
@@ -481,12 +484,12 @@ __global__ void __launch_bounds__(PC_THREADS) affine_scan_pc_kernel(AffineArgs p
         typedef __attribute__((address_space(3))) void *lptr;
         auto issue = [&](int s) {
             const int sc = min(s, p.nc - 1), c = p.reverse ? p.nc - 1 - sc : sc;
-            const float *N = p.n + ((int64_t)bh * p.nc + c) * D * D;
+            const uint16_t *N = p.n + ((int64_t)bh * p.nc + c) * D * D;
             uint4 *slot = sm.n[s % PC_NRING];
 #pragma unroll
             for (int i = 0; i < PC_NOPS; ++i) {
-                const int q = 64 * i + l, jj = q >> 4, x = q & 15;
-                __builtin_amdgcn_global_load_lds((gptr)(N + jj * D + 4 * (x ^ (jj & 15))),
+                const int q = 64 * i + l, jj = q >> 3, x = q & 7;
+                __builtin_amdgcn_global_load_lds((gptr)(N + jj * D + 8 * (x ^ (jj & 7))),
                                                  (lptr)(slot + 64 * i), 16, 0, 0);
             }
         };
@@ -558,7 +561,7 @@ hipError_t launch_chunk_affine_scan(const ChunkArgs &a, bool reverse, hipStream_
         p.reverse = 0;
     } else {
         p.m = a.ck_mt;
-        p.n = a.ws_n;
+        p.n = a.ws_nb;
         p.ckpt = a.ws_dstate;
         p.ckpt_lo = a.ws_dstate_lo;
         p.x0.data = a.dfinal;
@@ -845,13 +848,12 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
         gemm2(x, &Wt[(16 * tm) * LDB], Xt, tn0);
         gemm2(x, &Wt[(16 * tm) * LDB], Xtl, tn0);
         gemm2(x, &Wtl[(16 * tm) * LDB], Xt, tn0);
-        float *Nt = a.ws_n + (int64_t)ci * D * D;  // N transposed: Nt[col][row]
+        uint16_t *Nt = a.ws_nb + (int64_t)ci * D * D;  // N transposed: Nt[col][row], bf16
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-            *reinterpret_cast<float4 *>(&Nt[(16 * (tn0 + j) + acc_col()) * D + 16 * tm +
-                                            acc_row(0)]) =
-                make_float4(yacc[j][0] - x[j][0], yacc[j][1] - x[j][1], yacc[j][2] - x[j][2],
-                            yacc[j][3] - x[j][3]);
+            *reinterpret_cast<uint2 *>(&Nt[(16 * (tn0 + j) + acc_col()) * D + 16 * tm + acc_row(0)]) =
+                make_uint2(bf16_pack2(yacc[j][0] - x[j][0], yacc[j][1] - x[j][1]),
+                           bf16_pack2(yacc[j][2] - x[j][2], yacc[j][3] - x[j][3]));
     }
 }
 
