@@ -18,25 +18,25 @@ struct GateBlock {
 };
 
 // Per-chunk private storage handed from the forward to the backward:
-//   state  S at the chunk start, bf16, transposed (S^T row-major)
+//   state, state_lo  S at the chunk start, bf16 hi and lo, transposed (S^T rows)
 //   T      (I + A)^-1, bf16 row-major
 //   gate   GateBlock
 //   delta  the chunk's edits delta[t][v], f32 row-major
-//   Mt     the adjoint map M = A_c^T, bf16 row-major
-// plus the forward state map S_next = A_c S + B_c (A_c bf16 row-major, B_c bf16
-// transposed), read only by the forward state scan.  Transposed matrices let
-// each MFMA lane move its four accumulator rows with one 8-byte access.
+// plus the factored state map S_C = gam_63 S0 + Ktil^T (U - W S0) that the
+// scans read: -W^T [key][token] and Ktil = lam K [token][key] (bf16 hi, then
+// lo), U^T [value][token] (f32) and gam_63 repeated per key (f32).
 constexpr size_t CK_STATE_BYTES = CHUNK_D * CHUNK_D * sizeof(uint16_t);
 constexpr size_t CK_T_BYTES = CHUNK * CHUNK * sizeof(uint16_t);
 constexpr size_t CK_GATE_BYTES = sizeof(GateBlock);
 constexpr size_t CK_DELTA_BYTES = CHUNK * CHUNK_D * sizeof(float);
-constexpr size_t CK_MAP_M_BYTES = CHUNK_D * CHUNK_D * sizeof(uint16_t);
-constexpr size_t CK_MAP_N_BYTES = CHUNK_D * CHUNK_D * sizeof(uint16_t);
-constexpr size_t CK_CHUNK_BYTES = CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES + CK_DELTA_BYTES +
-                                  2 * CK_MAP_M_BYTES + CK_MAP_N_BYTES;
-// Backward workspace per chunk: dS at the chunk end and N of the adjoint map
-// (both bf16, transposed).
-constexpr size_t WS_CHUNK_BYTES = CK_STATE_BYTES + CK_MAP_N_BYTES;
+constexpr size_t CK_LRW_BYTES = 2 * CHUNK_D * CHUNK * sizeof(uint16_t);  // hi and lo
+constexpr size_t CK_LRU_BYTES = CHUNK_D * CHUNK * sizeof(float);
+constexpr size_t CK_LRG_BYTES = CHUNK_D * sizeof(float);
+constexpr size_t CK_CHUNK_BYTES = 2 * CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES + CK_DELTA_BYTES +
+                                  2 * CK_LRW_BYTES + CK_LRU_BYTES + CK_LRG_BYTES;
+// Backward workspace per chunk: dS at the chunk end (bf16 hi and lo,
+// transposed) and N^T of the adjoint map (f32).
+constexpr size_t WS_CHUNK_BYTES = 2 * CK_STATE_BYTES + CHUNK_D * CHUNK_D * sizeof(float);
 
 struct ChunkArgs {
     int B, T, H, nc;
@@ -53,9 +53,6 @@ struct ChunkArgs {
     uint16_t *ck_t;
     GateBlock *ck_gate;
     float *ck_delta;
-    uint16_t *ck_mt;   // adjoint map M = A_c^T
-    uint16_t *map_m;   // forward state map A_c
-    uint16_t *map_n;   // forward state map B_c^T (bf16)
     // backward
     const uint16_t *dout;
     int64_t ds[3];
@@ -63,8 +60,7 @@ struct ChunkArgs {
     void *dq, *dk, *dv;
     float *dbeta, *dg, *dinitial;
     uint16_t *ws_dstate;  // [B*H*nc] adjoint of the state at each chunk end
-    float *ws_n;       // N of the adjoint map dS_start = M dS_end + N (f32; wide and channel-wise)
-    uint16_t *ws_nb;   // N^T of the adjoint map, bf16 (d = 64 chunk path)
+    float *ws_n;       // N^T of the adjoint map dS_start = M dS_end + N (f32)
     // Wide path (d_k = d_v = 128, value blocks of 64): per-chunk |k_t|^2 and the
     // value blocks' partial |delta_t|^2 (forward checkpoint).
     float *ck_kk, *ck_ddp;
@@ -125,17 +121,21 @@ inline void chunk_bind_checkpoint(ChunkArgs &a, void *ck) {
     char *p = static_cast<char *>(ck);
     a.ck_state = reinterpret_cast<uint16_t *>(p);
     p += n * CK_STATE_BYTES;
+    a.ck_state_lo = reinterpret_cast<uint16_t *>(p);
+    p += n * CK_STATE_BYTES;
     a.ck_t = reinterpret_cast<uint16_t *>(p);
     p += n * CK_T_BYTES;
     a.ck_gate = reinterpret_cast<GateBlock *>(p);
     p += n * CK_GATE_BYTES;
     a.ck_delta = reinterpret_cast<float *>(p);
     p += n * CK_DELTA_BYTES;
-    a.ck_mt = reinterpret_cast<uint16_t *>(p);
-    p += n * CK_MAP_M_BYTES;
-    a.map_m = reinterpret_cast<uint16_t *>(p);
-    p += n * CK_MAP_M_BYTES;
-    a.map_n = reinterpret_cast<uint16_t *>(p);
+    a.lr_wt = reinterpret_cast<uint16_t *>(p);
+    p += n * CK_LRW_BYTES;
+    a.lr_kt = reinterpret_cast<uint16_t *>(p);
+    p += n * CK_LRW_BYTES;
+    a.lr_u = reinterpret_cast<float *>(p);
+    p += n * CK_LRU_BYTES;
+    a.lr_gv = reinterpret_cast<float *>(p);
 }
 
 // Carve the backward workspace.
@@ -143,7 +143,10 @@ inline void chunk_bind_workspace(ChunkArgs &a, void *ws) {
     const int64_t n = (int64_t)a.B * a.H * a.nc;
     char *p = static_cast<char *>(ws);
     a.ws_dstate = reinterpret_cast<uint16_t *>(p);
-    a.ws_nb = reinterpret_cast<uint16_t *>(p + n * CK_STATE_BYTES);
+    p += n * CK_STATE_BYTES;
+    a.ws_dstate_lo = reinterpret_cast<uint16_t *>(p);
+    p += n * CK_STATE_BYTES;
+    a.ws_n = reinterpret_cast<float *>(p);
 }
 
 // ---- channel-wise path: per-channel gates, 16-token chunks, d_k = d_v = 64 ------
@@ -163,13 +166,14 @@ inline int64_t cw_chunk_count(int64_t B, int64_t T, int64_t H) {
 
 // Checkpoint per chunk: S0^T (bf16 hi/lo, 64x64), T and P (f32 16x16), CwGate,
 // the cumulative log decay Lambda (f32 16x64), delta (f32 16x64), and the
-// factored chunk map: -W'^T and Ktil (bf16 16x64), U^T (f32 16x64), b_15 (f32 64).
+// factored chunk map: -W'^T and Ktil (bf16 hi and lo, 16x64 each), U^T (f32
+// 16x64), b_15 (f32 64).
 constexpr size_t CWK_STATE = (size_t)CHUNK_D * CHUNK_D * 2;
 constexpr size_t CWK_T = (size_t)CW_C * CW_C * 4;
 constexpr size_t CWK_GATE = sizeof(CwGate);
 constexpr size_t CWK_LAM = (size_t)CW_C * CHUNK_D * 4;
 constexpr size_t CWK_DELTA = (size_t)CW_C * CHUNK_D * 4;
-constexpr size_t CWK_LRW = (size_t)CW_C * CHUNK_D * 2;
+constexpr size_t CWK_LRW = (size_t)CW_C * CHUNK_D * 2 * 2;  // hi and lo
 constexpr size_t CWK_LRU = (size_t)CW_C * CHUNK_D * 4;
 constexpr size_t CWK_LRG = (size_t)CHUNK_D * 4;
 constexpr size_t CWK_MAPN = (size_t)CHUNK_D * CHUNK_D * 4;
@@ -220,7 +224,7 @@ inline void cw_bind_workspace(ChunkArgs &a, void *ws) {
 
 // The affine scan over a.nc chunks of per-chunk 64 x 64 maps (gdn2_chunk.hip),
 // forward (state) or reverse (adjoint).
-hipError_t launch_chunk_affine_scan(const ChunkArgs &a, bool reverse, hipStream_t stream);
+hipError_t launch_chunk_scan(const ChunkArgs &a, bool reverse, hipStream_t stream);
 
 hipError_t launch_cw_fwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
 hipError_t launch_cw_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev);
@@ -234,19 +238,21 @@ inline bool wide_eligible_shape(const gdn2_shape *s, int chunk) {
 }
 
 // Checkpoint per chunk: S0^T (bf16 D x D), T (bf16 C x C), GateBlock, delta (f32
-// C x D), the factored chunk map (-W'^T and Ktil bf16 C x D, U^T f32 C x D, the
-// diagonal f32 D), |k|^2 and the value blocks' |delta|^2 (f32 C each).
+// C x D), the factored chunk map (-W'^T bf16 C x D, Ktil bf16 hi and lo C x D
+// each, U^T f32 C x D, the diagonal f32 D), |k|^2 and the value blocks'
+// |delta|^2 (f32 C each).
 constexpr size_t WCK_STATE = (size_t)WIDE_D * WIDE_D * 2;
 constexpr size_t WCK_T = CK_T_BYTES;
 constexpr size_t WCK_GATE = CK_GATE_BYTES;
 constexpr size_t WCK_DELTA = (size_t)CHUNK * WIDE_D * 4;
 constexpr size_t WCK_LRW = (size_t)CHUNK * WIDE_D * 2;
+constexpr size_t WCK_LRK = 2 * WCK_LRW;  // Ktil hi and lo
 constexpr size_t WCK_LRU = (size_t)CHUNK * WIDE_D * 4;
 constexpr size_t WCK_LRG = (size_t)WIDE_D * 4;
 constexpr size_t WCK_MAPN = (size_t)WIDE_D * WIDE_D * 4;
 constexpr size_t WCK_NORM = (size_t)CHUNK * (1 + WIDE_NVB) * 4;
 constexpr size_t WCK_CHUNK =
-    WCK_STATE + WCK_T + WCK_GATE + WCK_DELTA + 2 * WCK_LRW + WCK_LRU + WCK_LRG + WCK_NORM;
+    WCK_STATE + WCK_T + WCK_GATE + WCK_DELTA + WCK_LRW + WCK_LRK + WCK_LRU + WCK_LRG + WCK_NORM;
 // Backward workspace per chunk: dS^T (bf16) and N^T (f32).
 constexpr size_t WWS_CHUNK = WCK_STATE + WCK_MAPN;
 
@@ -272,7 +278,7 @@ inline void wide_bind_checkpoint(ChunkArgs &a, void *ck) {
     a.lr_wt = reinterpret_cast<uint16_t *>(p);
     p += n * WCK_LRW;
     a.lr_kt = reinterpret_cast<uint16_t *>(p);
-    p += n * WCK_LRW;
+    p += n * WCK_LRK;
     a.lr_u = reinterpret_cast<float *>(p);
     p += n * WCK_LRU;
     a.lr_gv = reinterpret_cast<float *>(p);

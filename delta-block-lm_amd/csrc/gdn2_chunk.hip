@@ -36,14 +36,11 @@ namespace gdn2 {
 namespace {
 
 struct PrepSmem {
-    uint16_t slot[4][TILE];  // K rows (then T), (beta gam K)^T, (lam K)^T, (beta V)^T
-    union {
-        struct {
-            float Af[C * LDF];
-            float Tf[C * LDF];
-        } inv;
-        uint16_t wu[4][TILE];  // W^T hi/lo, U^T hi/lo once the inverse is done
-    } u;
+    uint16_t slot[4][TILE];  // K rows (then T), beta gam K rows (hi, lo), beta V rows
+    struct {
+        float Af[C * LDF];
+        float Tf[C * LDF];
+    } inv;
     GateLds gl;
 };
 
@@ -56,16 +53,17 @@ struct OutSmem {
 
 }  // namespace
 
-// ---- prep: gates, the UT inverse and the affine state map of every chunk -------
-// W = T diag(beta gam) K, U = T diag(beta) V, and the chunk's state map
-//   S_C = A S0 + B,  A = gam_63 I - (lam K)^T W,  B = (lam K)^T U.
+// ---- prep: gates, the UT inverse and the factored state map of every chunk ----
+// W = T diag(beta gam) K and U = T diag(beta) V give the chunk's state map
+//   S_C = gam_63 S0 + (lam K)^T (U - W S0),
+// which leaves as its factors for the scan: -W^T and Ktil = lam K (bf16 hi and
+// lo), U^T (f32) and gam_63.
 __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
     __shared__ PrepSmem sm;
-    // beta gam K, lam K and beta V are staged as scaled rows; the products that
-    // need them transposed read across them.
-    uint16_t *Ks = sm.slot[0], *KBGs = sm.slot[1], *KLs = sm.slot[2], *VBs = sm.slot[3];
+    // beta gam K and beta V are staged as scaled rows; the products that need
+    // them transposed read across them.
+    uint16_t *Ks = sm.slot[0], *KBGs = sm.slot[1], *KBGl = sm.slot[3], *VBs = sm.slot[2];
     uint16_t *Tb = sm.slot[0];  // over K once A is formed
-    uint16_t *Wt = sm.u.wu[0], *Wtl = sm.u.wu[1], *Ut = sm.u.wu[2], *Utl = sm.u.wu[3];
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, tg = c * C + t;
@@ -96,19 +94,30 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         gb->seg[t] = seg;
     }
     __syncthreads();
-    {  // scaled rows of K for the W/A products
+    {  // beta gam K rows (hi, lo) for the W product; Ktil = lam K rows (hi, lo) and gam_63 out
         const float bg = sm.gl.beta[t] * sm.gl.gam[t], la = sm.gl.lam[t];
         Pack8 kp;
         kp.u = k8;
-        uint32_t kb[4], kl[4];
+        uint32_t kb[4], kbl[4], kh[4], kl[4];
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
             const float k0 = bf16_val(kp.h[e]), k1 = bf16_val(kp.h[e + 1]);
-            kb[e / 2] = bf16_pack2(bg * k0, bg * k1);
-            kl[e / 2] = bf16_pack2(la * k0, la * k1);
+            uint16_t h0, l0, h1, l1;
+            split_bf16(bg * k0, h0, l0);
+            split_bf16(bg * k1, h1, l1);
+            kb[e / 2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+            kbl[e / 2] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+            split_bf16(la * k0, h0, l0);
+            split_bf16(la * k1, h1, l1);
+            kh[e / 2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+            kl[e / 2] = (uint32_t)l0 | ((uint32_t)l1 << 16);
         }
         put_row8(KBGs, t, cb, make_uint4(kb[0], kb[1], kb[2], kb[3]));
-        put_row8(KLs, t, cb, make_uint4(kl[0], kl[1], kl[2], kl[3]));
+        put_row8(KBGl, t, cb, make_uint4(kbl[0], kbl[1], kbl[2], kbl[3]));
+        uint16_t *kt = a.lr_kt + ((int64_t)ci * 2 * C + t) * D + 8 * cb;
+        *reinterpret_cast<uint4 *>(kt) = make_uint4(kh[0], kh[1], kh[2], kh[3]);
+        *reinterpret_cast<uint4 *>(kt + C * D) = make_uint4(kl[0], kl[1], kl[2], kl[3]);
+        if (tid < D) a.lr_gv[(int64_t)ci * D + tid] = sm.gl.gamC;
     }
     // A = strict_lower(beta_t Gam_ts k_t.k_s) in f32 (tiles with tn <= tm only).
     if (tn0 <= tm) {
@@ -123,21 +132,21 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tt = 16 * tm + acc_row(i);
-                sm.u.inv.Af[tt * LDF + ss] = (ss < tt && rg.seg[i] == sgs)
+                sm.inv.Af[tt * LDF + ss] = (ss < tt && rg.seg[i] == sgs)
                                                  ? rg.beta[i] * __expf(rg.G[i] - Gs) * kk[j][i]
                                                  : 0.f;
             }
         }
     }
     __syncthreads();
-    ut_inverse(sm.u.inv.Af, sm.u.inv.Tf, w);
+    ut_inverse(sm.inv.Af, sm.inv.Tf, w);
     // T (bf16, row-major, zero above the diagonal): LDS operand and checkpoint.
     {
         const int r = tid >> 3, c0 = 8 * (tid & 7);
         // Two 16-byte reads; the blocks above the diagonal hold stale data and are
         // masked after the read.
-        const float4 f0 = *reinterpret_cast<const float4 *>(&sm.u.inv.Tf[r * LDF + c0]);
-        const float4 f1 = *reinterpret_cast<const float4 *>(&sm.u.inv.Tf[r * LDF + c0 + 4]);
+        const float4 f0 = *reinterpret_cast<const float4 *>(&sm.inv.Tf[r * LDF + c0]);
+        const float4 f1 = *reinterpret_cast<const float4 *>(&sm.inv.Tf[r * LDF + c0 + 4]);
         const float f[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
         uint32_t pk[4];
 #pragma unroll
@@ -160,76 +169,30 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         put_row8(VBs, t, cb, make_uint4(vb[0], vb[1], vb[2], vb[3]));
     }
     __syncthreads();
-    // W = T (beta gam K), U = T (beta V): stored transposed as hi/lo pairs.
+    // W = T (beta gam K), U = T (beta V), straight from the accumulators: -W^T
+    // (bf16 hi and lo) and U^T (f32), [column][token].  bprep forms W again
+    // from T and K with the same operands and products.
     {
         f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
         gemm2_tr(x, &Tb[(16 * tm) * LDB], KBGs, tn0);  // B[k][t] = (beta gam K)[t][k]
+        gemm2_tr(x, &Tb[(16 * tm) * LDB], KBGl, tn0);
         gemm2_tr(y, &Tb[(16 * tm) * LDB], VBs, tn0);   // B[v][t] = (beta V)[t][v]
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            store_tile_t_split(&Wt[(16 * (tn0 + j)) * LDB + 16 * tm],
-                               &Wtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
-            store_tile_t_split(&Ut[(16 * (tn0 + j)) * LDB + 16 * tm],
-                               &Utl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, y[j]);
-        }
-    }
-    __syncthreads();
-    // A = gam_63 I - (lam K)^T W (bf16, row-major), B = (lam K)^T U (f32).
-    {
-        f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
-        gemm2_atr(x, KLs, 16 * tm, Wt, tn0);  // A[k][t] = (lam K)[t][k]
-        gemm2_atr(x, KLs, 16 * tm, Wtl, tn0);
-        gemm2_atr(y, KLs, 16 * tm, Ut, tn0);
-        gemm2_atr(y, KLs, 16 * tm, Utl, tn0);
-        const float gC = sm.gl.gamC;
-        uint16_t *Mt = sm.slot[1];  // A_c^T over beta gam K, which is dead
-        uint16_t *Bt = a.map_n + (int64_t)ci * D * D;  // B transposed: Bt[col][row], bf16
+            const int64_t row = (int64_t)(16 * (tn0 + j) + acc_col()) * C + 16 * tm + acc_row(0);
+            uint16_t *wt = a.lr_wt + (int64_t)ci * 2 * D * C + row;
+            uint16_t h[4], o[4];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int cc = 16 * (tn0 + j) + acc_col();
-            f32x4 am;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) am[i] = (16 * tm + acc_row(i) == cc ? gC : 0.f) - x[j][i];
-            store_tile_t(&Mt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, am);
-            *reinterpret_cast<uint2 *>(&Bt[cc * D + 16 * tm + acc_row(0)]) =
-                make_uint2(bf16_pack2(y[j][0], y[j][1]), bf16_pack2(y[j][2], y[j][3]));
+            for (int i = 0; i < 4; ++i) split_bf16(-x[j][i], h[i], o[i]);
+            *reinterpret_cast<uint2 *>(wt) =
+                make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+            *reinterpret_cast<uint2 *>(wt + D * C) =
+                make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+            *reinterpret_cast<float4 *>(a.lr_u + (int64_t)ci * D * C + row) =
+                make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
         }
-    }
-    __syncthreads();
-    // Rows out: M = A_c^T (adjoint map) row by row, and A_c (forward state map)
-    // read across it: lane (row 16 (w%4) + l%16, columns 32 (w/4) + 8 (l/16) ..)
-    // stores one 16-byte row piece.  Every lane runs the transpose reads.  W is
-    // not checkpointed: bprep forms it again from T and K.
-    {
-        const int r = tid >> 3, c0 = 8 * (tid & 7), l = lane_id();
-        const uint16_t *Mt = sm.slot[1];
-        const bf16x8_t ar = frag_tr(Mt, 32 * (w >> 2), 16 * (w & 3));
-        *reinterpret_cast<uint4 *>(a.ck_mt + (int64_t)ci * D * D + r * D + c0) =
-            *reinterpret_cast<const uint4 *>(&Mt[r * LDB + c0]);
-        *reinterpret_cast<bf16x8_t *>(a.map_m + (int64_t)ci * D * D + (16 * (w & 3) + (l & 15)) * D +
-                                      32 * (w >> 2) + 8 * (l >> 4)) = ar;
     }
 }
-
-// ---- affine scan: the only sequential part -----------------------------------
-// X_{next} = M_c X + N_c over the chunks of one (batch, head): forward
-// (S_C = A S0 + B, c ascending, X0 = initial state) or backward
-// (dS0 = M dS_C + N, c descending, X0 = adjoint of the final state).  X before
-// each step goes to ckpt[c], transposed (X^T row-major) and rounded to bf16
-// (every consumer uses it as a bf16 MFMA operand), with its lo part to ckpt_lo
-// when that is kept.  Columns of X evolve independently, so each of four
-// compute waves owns 16 columns; X is re-packed through LDS into the bf16
-// hi/lo operand of the next product.
-struct AffineArgs {
-    int nc, B, H;
-    const uint16_t *m;
-    const uint16_t *n;  // N^T (bf16)
-    uint16_t *ckpt;  // X^T per chunk, bf16
-    uint16_t *ckpt_lo;  // X^T - bf16(X^T) per chunk, bf16 (null: not kept)
-    View x0;          // [B,H,64,64] strided (data may be null: zero)
-    float *xout;      // [B,H,64,64] dense (may be null)
-    int reverse;
-};
 
 // ---- out: outputs and scores of every chunk --------------------------------------
 __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
@@ -251,6 +214,16 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
     const uint4 vr = load8(a.v, a.vs, b, tg, h, cb, inb);
     const uint4 s0r = *reinterpret_cast<const uint4 *>(a.ck_state + (int64_t)ci * D * D +
                                                        (tid >> 3) * D + 8 * (tid & 7));
+    // S0's lo part enters the K S0 and Q S0 products straight from the
+    // checkpoint as B fragments: S0^T row 16 (tn0 + j) + l % 16, keys 32 i + 8 (l / 16).
+    bf16x8_t s0l[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            s0l[j][i] = *reinterpret_cast<const bf16x8_t *>(
+                a.ck_state_lo + (int64_t)ci * D * D + (16 * (tn0 + j) + (tid & 15)) * D + 32 * i +
+                8 * ((tid & 63) >> 4));
     const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
     const int sg = gb->seg[t];
     const uint4 trw =
@@ -280,6 +253,16 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
         f32x4 x[2] = {zero4(), zero4()};
         gemm2(x, &Ks[(16 * tm) * LDB], St, tn0);
         gemm2(qs, &Qs[(16 * tm) * LDB], St, tn0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const bf16x8_t kf = frag(&Ks[(16 * tm) * LDB], LDB, 32 * i);
+            const bf16x8_t qf = frag(&Qs[(16 * tm) * LDB], LDB, 32 * i);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                x[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, s0l[j][i], x[j], 0, 0, 0);
+                qs[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf, s0l[j][i], qs[j], 0, 0, 0);
+            }
+        }
         f32x4 pq[2] = {zero4(), zero4()};
         if (tn0 <= tm) gemm2(pq, &Qs[(16 * tm) * LDB], Ks, tn0);
         const RowGates rg = row_gates(sm.gl, tm);
@@ -370,198 +353,27 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
     }
 }
 
-// One workgroup per (batch, head), seven waves:
-//   waves 0-3  compute: wave w owns state columns 16 w .. 16 w + 15;
-//   wave 4     streams the chunk maps M into an LDS ring with LDS-DMA loads
-//              (global_load_lds_dwordx4: lane L's 16 bytes land at the slot
-//              base + 16 L), PC_RING - 1 chunks ahead;
-//   wave 6     streams N the same way, PC_NRING - 1 chunks ahead;
-//   wave 5     copies each step's X^T tiles (hi, and lo when kept) from LDS to
-//              the checkpoint.
-// A wave's memory counter completes in order, so a scan wave that loaded its
-// own operands and stored its own checkpoint would wait for older checkpoint
-// stores whenever it waited for a prefetched operand, and could keep only
-// three chunks in flight within the counter's 63 operations.  Here the
-// compute waves issue no memory operations inside the loop, and each head's
-// map is read once per step instead of once per column group.  One workgroup
-// barrier per step: the producers pass it once that step's operands have
-// landed, the compute waves once their X^T tiles for the step are in LDS
-// (double-buffered by step parity, so the writer reads one buffer while the
-// next step fills the other).
-namespace {
-constexpr int PC_RING = 4;                 // LDS slots of M
-constexpr int PC_MOPS = D * D * 2 / 1024;  // LDS-DMA instructions per map (1 KiB each)
-constexpr int PC_NRING = 5;                // LDS slots of N
-constexpr int PC_NOPS = D * D * 2 / 1024;  // LDS-DMA instructions per N (1 KiB each)
-constexpr int PC_THREADS = 7 * 64;
-
-// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in
-// bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
-constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-// s_waitcnt immediate that waits for lgkmcnt == 0 only (vmcnt 63, expcnt 7).
-constexpr int LGKMCNT_ZERO = 15 | (3 << 14) | (7 << 4);
-
-struct PcSmem {
-    uint4 m[PC_RING][D * D / 8];      // M rows: 16-byte chunk x of row r holds chunk x ^ (r & 7)
-    uint4 n[PC_NRING][D * D / 8];     // N^T rows (bf16): chunk x of column row j holds x ^ (j & 7)
-    uint16_t xs[2][4][2][16 * LDB];   // [step parity][compute wave][hi, lo]: X^T [col][row]
-};
-
-__device__ __forceinline__ void pc_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-__device__ __forceinline__ void pc_step(int s, int j, int w, f32x4 (&X)[4], PcSmem &sm) {
-    const int l = lane_id();
-    uint16_t *xh = sm.xs[s & 1][w][0], *xl = sm.xs[s & 1][w][1];
-#pragma unroll
-    for (int tm = 0; tm < 4; ++tm) store_tile_t_split(xh + 16 * tm, xl + 16 * tm, LDB, X[tm]);
-    // The writer wave reads these tiles after the barrier, and the LDS operations
-    // of different waves may complete out of issue order: wait until they landed.
-    __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);
-    pc_barrier();  // this step's map is in its slot; the writer may read X^T
-    const uint4 *slot = sm.m[s % PC_RING];
-    const uint2 *nslot = reinterpret_cast<const uint2 *>(sm.n[s % PC_NRING]);
-    f32x4 Y[4];
-#pragma unroll
-    for (int tm = 0; tm < 4; ++tm) {  // N[16 tm + 4 g + i][j]: half g & 1 of chunk 2 tm + g / 2 of row j
-        const int g = l >> 4;
-        const uint2 nv = nslot[(j * 8 + ((2 * tm + (g >> 1)) ^ (j & 7))) * 2 + (g & 1)];
-        Y[tm] = f32x4{bf16_val((uint16_t)nv.x), bf16_val((uint16_t)(nv.x >> 16)), bf16_val((uint16_t)nv.y),
-                      bf16_val((uint16_t)(nv.y >> 16))};
-    }
-    // hi and lo products accumulate separately: two dependent MFMAs per tile
-    f32x4 Z[4] = {zero4(), zero4(), zero4(), zero4()};
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-        const bf16x8_t bh_ = frag(xh, LDB, 32 * kk), bl_ = frag(xl, LDB, 32 * kk);
-#pragma unroll
-        for (int tm = 0; tm < 4; ++tm) {
-            const int r = 16 * tm + (l & 15), q = 4 * kk + (l >> 4);
-            const bf16x8_t mf = __builtin_bit_cast(bf16x8_t, slot[r * 8 + (q ^ (r & 7))]);
-            Y[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf, bh_, Y[tm], 0, 0, 0);
-            Z[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mf, bl_, Z[tm], 0, 0, 0);
-        }
-    }
-#pragma unroll
-    for (int tm = 0; tm < 4; ++tm)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) X[tm][i] = Y[tm][i] + Z[tm][i];
-}
-}  // namespace
-
-__global__ void __launch_bounds__(PC_THREADS) affine_scan_pc_kernel(AffineArgs p) {
-    __shared__ PcSmem sm;
-    const int bh = blockIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
-    if (w == 4) {  // producer: the maps, PC_RING - 1 chunks ahead
-        typedef __attribute__((address_space(1))) const void *gptr;
-        typedef __attribute__((address_space(3))) void *lptr;
-        auto issue = [&](int s) {
-            const int sc = min(s, p.nc - 1), c = p.reverse ? p.nc - 1 - sc : sc;
-            const uint16_t *M = p.m + ((int64_t)bh * p.nc + c) * D * D;
-            uint4 *slot = sm.m[s % PC_RING];
-#pragma unroll
-            for (int i = 0; i < PC_MOPS; ++i) {
-                const int q = 64 * i + l, r = q >> 3, x = q & 7;
-                __builtin_amdgcn_global_load_lds((gptr)(M + r * D + 8 * (x ^ (r & 7))),
-                                                 (lptr)(slot + 64 * i), 16, 0, 0);
-            }
-        };
-        for (int s = 0; s < PC_RING - 1; ++s) issue(s);
-        for (int s = 0; s < p.nc; ++s) {
-            // map s has landed once no more than the PC_RING - 2 later maps are in flight
-            __builtin_amdgcn_s_waitcnt(vmcnt_only((PC_RING - 2) * PC_MOPS));
-            pc_barrier();
-            issue(s + PC_RING - 1);  // into the slot that step s - 1 read
-        }
-        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-        return;
-    }
-    if (w == 6) {  // producer: N, PC_NRING - 1 chunks ahead
-        typedef __attribute__((address_space(1))) const void *gptr;
-        typedef __attribute__((address_space(3))) void *lptr;
-        auto issue = [&](int s) {
-            const int sc = min(s, p.nc - 1), c = p.reverse ? p.nc - 1 - sc : sc;
-            const uint16_t *N = p.n + ((int64_t)bh * p.nc + c) * D * D;
-            uint4 *slot = sm.n[s % PC_NRING];
-#pragma unroll
-            for (int i = 0; i < PC_NOPS; ++i) {
-                const int q = 64 * i + l, jj = q >> 3, x = q & 7;
-                __builtin_amdgcn_global_load_lds((gptr)(N + jj * D + 8 * (x ^ (jj & 7))),
-                                                 (lptr)(slot + 64 * i), 16, 0, 0);
-            }
-        };
-        for (int s = 0; s < PC_NRING - 1; ++s) issue(s);
-        for (int s = 0; s < p.nc; ++s) {
-            __builtin_amdgcn_s_waitcnt(vmcnt_only((PC_NRING - 2) * PC_NOPS));
-            pc_barrier();
-            issue(s + PC_NRING - 1);
-        }
-        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-        return;
-    }
-    if (w == 5) {  // writer: X^T before step s -> checkpoint of chunk c(s)
-        for (int s = 0; s < p.nc; ++s) {
-            pc_barrier();
-            const int c = p.reverse ? p.nc - 1 - s : s;
-            const int64_t co = ((int64_t)bh * p.nc + c) * D * D;
-#pragma unroll
-            for (int part = 0; part < 2; ++part) {
-                uint16_t *ck = part == 0 ? p.ckpt : p.ckpt_lo;
-                if (!ck) continue;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {  // 4 compute waves x 16 columns x 64 rows
-                    const int q = 64 * i + l, cw = q >> 7, col = (q >> 3) & 15, r8 = 8 * (q & 7);
-                    const uint4 v = *reinterpret_cast<const uint4 *>(&sm.xs[s & 1][cw][part][col * LDB + r8]);
-                    *reinterpret_cast<uint4 *>(&ck[co + (16 * cw + col) * D + r8]) = v;
-                }
-            }
-        }
-        return;
-    }
-    const int b = bh / p.H, h = bh % p.H;
-    const int j = 16 * w + (l & 15);  // this lane's state column
-    f32x4 X[4];
-#pragma unroll
-    for (int tm = 0; tm < 4; ++tm)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            X[tm][i] = p.x0.data ? ld4<float>(p.x0, b, h, 16 * tm + acc_row(i), j) : 0.f;
-    for (int s = 0; s < p.nc; ++s) pc_step(s, j, w, X, sm);
-    if (p.xout)
-#pragma unroll
-        for (int tm = 0; tm < 4; ++tm)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                p.xout[((int64_t)bh * D + 16 * tm + acc_row(i)) * D + j] = X[tm][i];
-}
-
-static void launch_affine_scan(const AffineArgs &p, hipStream_t stream) {
-    hipLaunchKernelGGL(affine_scan_pc_kernel, dim3(p.B * p.H), dim3(PC_THREADS), 0, stream, p);
-}
-
-// The scan over a.nc chunks of 64 x 64 maps held in ChunkArgs' per-chunk
-// layout: forward (A_c, B_c^T; X0 = initial; chunk-start states to ck_state)
-// or reverse (M = A_c^T, N^T; X0 = the final-state adjoint, dense; chunk-end
-// adjoints to ws_dstate).  Shared by the scalar and channel-wise paths.
-hipError_t launch_chunk_affine_scan(const ChunkArgs &a, bool reverse, hipStream_t stream) {
-    AffineArgs p{};
+// The state scan over a head's chunks (gdn2_chunk_lr.hip): forward (chunk-start
+// states and their lo parts, from prep's factors) or reverse (chunk-end state
+// adjoints and their lo parts, N from bprep).
+hipError_t launch_chunk_scan(const ChunkArgs &a, bool reverse, hipStream_t stream) {
+    LrScanArgs p{};
     p.nc = a.nc;
     p.B = a.B;
     p.H = a.H;
+    p.vd = D;
+    p.wt = a.lr_wt;
+    p.kt = a.lr_kt;
+    p.gv = a.lr_gv;
+    p.reverse = reverse ? 1 : 0;
     if (!reverse) {
-        p.m = a.map_m;
-        p.n = a.map_n;
+        p.u = a.lr_u;
         p.ckpt = a.ck_state;
         p.ckpt_lo = a.ck_state_lo;
         p.x0 = a.initial;
         p.xout = a.final_state;
-        p.reverse = 0;
     } else {
-        p.m = a.ck_mt;
-        p.n = a.ws_nb;
+        p.n = a.ws_n;
         p.ckpt = a.ws_dstate;
         p.ckpt_lo = a.ws_dstate_lo;
         p.x0.data = a.dfinal;
@@ -570,10 +382,8 @@ hipError_t launch_chunk_affine_scan(const ChunkArgs &a, bool reverse, hipStream_
         p.x0.s2 = D;
         p.x0.s3 = 1;
         p.xout = a.dinitial;
-        p.reverse = 1;
     }
-    launch_affine_scan(p, stream);
-    return hipSuccess;
+    return launch_lr_scan(p, D, C, stream);
 }
 
 static inline void mark(const hipEvent_t *ev, int i, hipStream_t stream) {
@@ -586,7 +396,7 @@ hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream, const hipEve
     hipLaunchKernelGGL(chunk_prep_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
     mark(ev, 1, stream);
     mark(ev, 2, stream);
-    (void)launch_chunk_affine_scan(a, false, stream);
+    (void)launch_chunk_scan(a, false, stream);
     mark(ev, 3, stream);
     mark(ev, 4, stream);
     hipLaunchKernelGGL(chunk_out_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
@@ -617,7 +427,7 @@ hipError_t launch_chunk_fwd(const ChunkArgs &a, hipStream_t stream, const hipEve
 namespace {
 
 struct BPrepSmem {  // fits twice in one CU's LDS
-    uint16_t slot[7][TILE];
+    uint16_t slot[8][TILE];
     GateLds gl;
     float kk[NW][C];
     float dd[NW][C];
@@ -625,7 +435,7 @@ struct BPrepSmem {  // fits twice in one CU's LDS
 };
 
 struct BGradSmem {
-    uint16_t slot[15][TILE];
+    uint16_t slot[16][TILE];
     GateLds gl;
     float kk[NW][C];
     float dd[NW][C];
@@ -648,7 +458,7 @@ __device__ __forceinline__ uint4 load_mat(const uint16_t *src, int tid) {
 // more than a few memory instructions per wave (a burst of them stalls issue
 // for the whole CU).
 struct BgradIn {
-    uint4 q, k, dO, s0, ds;
+    uint4 q, k, dO, s0, ds, s0l, dsl;  // S0^T and dS^T rows: bf16 hi and lo
     float G, be, va, dsc;
     int sg;
     uint4 v, t;
@@ -683,8 +493,10 @@ __device__ __forceinline__ void bgrad_load(const ChunkArgs &a, int ci, const Chu
         const int64_t *dos = a.dout ? a.ds : a.qs;
         x.dO = *reinterpret_cast<const uint4 *>(row_ptr(dop, dos, p.b, tr, p.h) + 8 * cb);
         x.s0 = load_mat(a.ck_state + (int64_t)ci * D * D, tid);
+        x.s0l = load_mat(a.ck_state_lo + (int64_t)ci * D * D, tid);
     } else if constexpr (P == 2) {
         x.ds = load_mat(a.ws_dstate + (int64_t)ci * D * D, tid);
+        x.dsl = load_mat(a.ws_dstate_lo + (int64_t)ci * D * D, tid);
         const GateBlock *gb = a.ck_gate + ci;
         x.G = gb->G[t], x.be = gb->beta[t], x.va = gb->val[t];
         x.sg = gb->seg[t];
@@ -714,6 +526,7 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     // product needs them transposed.
     uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *dOs = sm.slot[2];
     uint16_t *Tb = sm.slot[3], *KBGs = sm.slot[4], *Pt = sm.slot[5], *Ptl = sm.slot[6];
+    uint16_t *KBGl = sm.slot[7];  // beta gam K lo rows
     uint16_t *Xt = sm.slot[0], *Xtl = sm.slot[1];  // over Q/K after phase 1
     uint16_t *Wt = sm.slot[3], *Wtl = sm.slot[4];  // over T and beta gam K after phase 1
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -757,14 +570,19 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
         put_row8(Ks, t, cb, kp.u);
         put_row8(dOs, t, cb, mask8(dor, on));
         float ksq = 0.f;
-        uint32_t kb[4];
+        uint32_t kb[4], kbl[4];
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
             const float k0 = bf16_val(kp.h[e]), k1 = bf16_val(kp.h[e + 1]);
-            kb[e / 2] = bf16_pack2(bg * k0, bg * k1);
+            uint16_t h0, l0, h1, l1;
+            split_bf16(bg * k0, h0, l0);
+            split_bf16(bg * k1, h1, l1);
+            kb[e / 2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+            kbl[e / 2] = (uint32_t)l0 | ((uint32_t)l1 << 16);
             ksq += k0 * k0 + k1 * k1;
         }
         put_row8(KBGs, t, cb, make_uint4(kb[0], kb[1], kb[2], kb[3]));
+        put_row8(KBGl, t, cb, make_uint4(kbl[0], kbl[1], kbl[2], kbl[3]));
         *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = trow;
         if (score_adj) sm.kk[cb][t] = ksq;
         if (w == 0) {
@@ -778,6 +596,7 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
     // W = T (beta gam K) in registers.
     f32x4 yacc[2] = {zero4(), zero4()}, wacc[2] = {zero4(), zero4()};
     gemm2_tr(wacc, &Tb[(16 * tm) * LDB], KBGs, tn0);  // B[k][t] = (beta gam K)[t][k]
+    gemm2_tr(wacc, &Tb[(16 * tm) * LDB], KBGl, tn0);
     {
         f32x4 pq[2] = {zero4(), zero4()};
 #pragma unroll
@@ -848,12 +667,12 @@ __global__ void __launch_bounds__(NT) chunk_bprep_kernel(ChunkArgs a) {
         gemm2(x, &Wt[(16 * tm) * LDB], Xt, tn0);
         gemm2(x, &Wt[(16 * tm) * LDB], Xtl, tn0);
         gemm2(x, &Wtl[(16 * tm) * LDB], Xt, tn0);
-        uint16_t *Nt = a.ws_nb + (int64_t)ci * D * D;  // N transposed: Nt[col][row], bf16
+        float *Nt = a.ws_n + (int64_t)ci * D * D;  // N transposed: Nt[col][row], f32
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-            *reinterpret_cast<uint2 *>(&Nt[(16 * (tn0 + j) + acc_col()) * D + 16 * tm + acc_row(0)]) =
-                make_uint2(bf16_pack2(yacc[j][0] - x[j][0], yacc[j][1] - x[j][1]),
-                           bf16_pack2(yacc[j][2] - x[j][2], yacc[j][3] - x[j][3]));
+            *reinterpret_cast<float4 *>(&Nt[(16 * (tn0 + j) + acc_col()) * D + 16 * tm + acc_row(0)]) =
+                make_float4(yacc[j][0] - x[j][0], yacc[j][1] - x[j][1], yacc[j][2] - x[j][2],
+                            yacc[j][3] - x[j][3]);
     }
 }
 
@@ -906,14 +725,16 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
     // with transpose reads.
     uint16_t *Qs = sm.slot[0], *Ks = sm.slot[1], *dOs = sm.slot[2];
     uint16_t *Vr = sm.slot[6], *Tr = sm.slot[7];     // V rows, T rows (T[t][s])
-    uint16_t *S0t = sm.slot[8], *dSt = sm.slot[9];   // S0^T, dS^T rows
+    uint16_t *S0t = sm.slot[8], *dSt = sm.slot[9];   // S0^T, dS^T rows (bf16 hi)
+    uint16_t *S0lt = sm.slot[15];                    // S0^T lo, staging..F
+    uint16_t *dSlt = sm.slot[10];                    // dS^T lo, staging..D
     uint16_t *Dh = sm.slot[11], *Dlo = sm.slot[12];  // delta rows (hi/lo)
     uint16_t *Pt = sm.slot[13], *Ptl = sm.slot[14];  // A..D
     // Later tenants of free or dead slots.
     uint16_t *Dd = sm.slot[3], *Ddl = sm.slot[4];  // ddelta^T, D..E
-    uint16_t *dRr = sm.slot[9];                    // dR rows, E..F
+    uint16_t *dRr = sm.slot[9], *dRl = sm.slot[14];  // dR rows (hi, lo), E..F
     // F..G: MA and MP are stored transposed only; phase G reads them both ways.
-    uint16_t *MAt = sm.slot[4], *MPt = sm.slot[7], *MPtl = sm.slot[10];
+    uint16_t *MAt = sm.slot[4], *MAtl = sm.slot[6], *MPt = sm.slot[7], *MPtl = sm.slot[10];
     // Gradients, G to the next chunk's staging: slots that phase G does not read and
     // the staging does not write.
     uint16_t *dQt = sm.slot[3], *dKt = sm.slot[5], *dVt = sm.slot[13];
@@ -968,6 +789,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
         }
         *reinterpret_cast<uint4 *>(&S0t[(tid >> 3) * LDB + 8 * (tid & 7)]) = in.s0;
         *reinterpret_cast<uint4 *>(&dSt[(tid >> 3) * LDB + 8 * (tid & 7)]) = in.ds;
+        *reinterpret_cast<uint4 *>(&S0lt[(tid >> 3) * LDB + 8 * (tid & 7)]) = in.s0l;
+        *reinterpret_cast<uint4 *>(&dSlt[(tid >> 3) * LDB + 8 * (tid & 7)]) = in.dsl;
         if (w == 0) {
             gates_derive(sm.gl, in.G, in.be, in.va, in.sg);
             sm.dsc[t] = in.dsc;
@@ -975,7 +798,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
     }
     // |S0 dS| partial; written after the barrier, when the previous chunk's phase H
     // (wave 0) has read the last one.
-    const float fr = wave_sum(dot8_bf16(in.s0, in.ds));
+    const float fr = wave_sum(dot8_bf16(in.s0, in.ds) + dot8_bf16(in.s0l, in.ds) + dot8_bf16(in.s0, in.dsl));
     // The previous chunk's dv tile is read now: phase A writes P^T over it.
     const bf16x8_t gv = bgrad_grad_frag(dVt, w);
     bgrad_load<0>(a, cn, pn, tid, in);
@@ -992,7 +815,9 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
     f32x4 dos[2] = {zero4(), zero4()}, kds[2] = {zero4(), zero4()};
     f32x4 kk[2] = {zero4(), zero4()}, qk[2] = {zero4(), zero4()};
     gemm2_tr(dos, &dOs[(16 * tm) * LDB], S0t, tn0);  // B[k][v] = S0^T[v][k]
+    gemm2_tr(dos, &dOs[(16 * tm) * LDB], S0lt, tn0);
     gemm2(kds, &Ks[(16 * tm) * LDB], dSt, tn0);
+    gemm2(kds, &Ks[(16 * tm) * LDB], dSlt, tn0);
     if (tn0 <= tm) {
         gemm2(kk, &Ks[(16 * tm) * LDB], Ks, tn0);
         gemm2(qk, &Qs[(16 * tm) * LDB], Ks, tn0);
@@ -1064,6 +889,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
     {
         gemm2_tr(dka, &Dh[(16 * tm) * LDB], dSt, tn0);  // B[k][v] = dS^T[v][k]
         gemm2_tr(dka, &Dlo[(16 * tm) * LDB], dSt, tn0);
+        gemm2_tr(dka, &Dh[(16 * tm) * LDB], dSlt, tn0);
         float p[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -1118,7 +944,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
                 p[i] += x[j][i] * vv[i];
                 dvv[j][i] = sm.gl.val[r0 + i] != 0.f ? rg.beta[i] * x[j][i] : 0.f;
             }
-            store_tile_rm(&dRr[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, x[j]);
+            store_tile_rm_split(&dRr[(16 * tm) * LDB + 16 * (tn0 + j)], &dRl[(16 * tm) * LDB + 16 * (tn0 + j)],
+                                LDB, x[j]);
         }
         row_reduce_store(p, sm.b2[w & 1], tm);
     }
@@ -1128,6 +955,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
     // (masked) -> MA^T, MP^T, and the gate-gradient partial sums.
     f32x4 drs[2] = {zero4(), zero4()};
     gemm2_tr(drs, &dRr[(16 * tm) * LDB], S0t, tn0);  // B[k][v] = S0^T[v][k]
+    gemm2_tr(drs, &dRr[(16 * tm) * LDB], S0lt, tn0);
+    gemm2_tr(drs, &dRl[(16 * tm) * LDB], S0t, tn0);
     {
         float p2[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1147,6 +976,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
         if (tn0 <= tm) {
             gemm2(da, &dRr[(16 * tm) * LDB], Dh, tn0);
             gemm2(da, &dRr[(16 * tm) * LDB], Dlo, tn0);
+            gemm2(da, &dRl[(16 * tm) * LDB], Dh, tn0);
             gemm2(dp, &dOs[(16 * tm) * LDB], Dh, tn0);
             gemm2(dp, &dOs[(16 * tm) * LDB], Dlo, tn0);
         }
@@ -1167,7 +997,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
                 z[i] = (dA * rg.beta[i] * kk[j][i] + dP * qk[j][i]) * gm;
                 pz[i] += z[i];
             }
-            store_tile_t(&MAt[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, ma);
+            store_tile_t_split(&MAt[(16 * (tn0 + j)) * LDB + 16 * tm],
+                               &MAtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, ma);
             store_tile_t_split(&MPt[(16 * (tn0 + j)) * LDB + 16 * tm],
                                &MPtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, mp);
             const float zc = col_reduce(z);
@@ -1212,6 +1043,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
             // MP and MA rows, read across their transposes.
             const bf16x8_t mp = frag_tr(MPt, r, 16 * tm), mpl = frag_tr(MPtl, r, 16 * tm);
             const bf16x8_t ma = frag_tr(MAt, r, 16 * tm), mat = frag(&MAt[(16 * tm) * LDB], LDB, r);
+            const bf16x8_t mal = frag_tr(MAtl, r, 16 * tm), matl = frag(&MAtl[(16 * tm) * LDB], LDB, r);
             const bf16x8_t pt = frag(&MPt[(16 * tm) * LDB], LDB, r), ptl = frag(&MPtl[(16 * tm) * LDB], LDB, r);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
@@ -1221,6 +1053,8 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
                 x[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mpl, kb, x[j], 0, 0, 0);
                 y[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ma, kb, y[j], 0, 0, 0);
                 y[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mat, kb, y[j], 0, 0, 0);
+                y[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mal, kb, y[j], 0, 0, 0);
+                y[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(matl, kb, y[j], 0, 0, 0);
                 y[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pt, qb, y[j], 0, 0, 0);
                 y[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ptl, qb, y[j], 0, 0, 0);
             }
@@ -1287,7 +1121,7 @@ hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream, const hipEve
     hipLaunchKernelGGL(chunk_bprep_kernel, dim3(nchunks), dim3(NT), 0, stream, a);
     mark(ev, 1, stream);
     mark(ev, 2, stream);
-    (void)launch_chunk_affine_scan(a, true, stream);
+    (void)launch_chunk_scan(a, true, stream);
     mark(ev, 3, stream);
     mark(ev, 4, stream);
     hipLaunchKernelGGL(chunk_bgrad_kernel, dim3(std::min(nchunks, device_cus())), dim3(NT), 0, stream, a,

@@ -237,9 +237,11 @@ __device__ __forceinline__ void cwprep_store(const ChunkArgs &a, int ci, int tid
         a.ck_cwg[ci].seg[tid] = o.seg;
     }
     put4_f32(a.ck_lam + (int64_t)ci * CC * 64 + t * 64 + c0, o.lam);
-    const int64_t off = ((int64_t)ci * 64 + 16 * w + acc_col()) * CC + acc_row(0);
-    *reinterpret_cast<uint2 *>(a.lr_wt + off) = make_uint2(bf16_pack2(-o.x[0], -o.x[1]), bf16_pack2(-o.x[2], -o.x[3]));
-    *reinterpret_cast<float4 *>(a.lr_u + off) = make_float4(o.y[0], o.y[1], o.y[2], o.y[3]);
+    const int64_t row = (int64_t)(16 * w + acc_col()) * CC + acc_row(0);
+    const float nw[4] = {-o.x[0], -o.x[1], -o.x[2], -o.x[3]};
+    uint16_t *wt = a.lr_wt + (int64_t)ci * 2 * 64 * CC + row;  // -W'^T hi, then lo
+    put4_split(wt, wt + 64 * CC, nw);
+    *reinterpret_cast<float4 *>(a.lr_u + (int64_t)ci * 64 * CC + row) = make_float4(o.y[0], o.y[1], o.y[2], o.y[3]);
 }
 
 // Workgroups walk chunks blockIdx.x, blockIdx.x + gridDim.x, ... (as many
@@ -340,8 +342,8 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a, int nchunks) 
             kl[e] = (sgt == sg15 ? __expf(L15 - L) : 0.f) * kv[e];
         }
         put4_split(&sm.ah[t * LDB + c0], &sm.ahl[t * LDB + c0], ah);
-        *reinterpret_cast<uint2 *>(a.lr_kt + ((int64_t)ci * CC + t) * 64 + c0) =
-            make_uint2(bf16_pack2(kl[0], kl[1]), bf16_pack2(kl[2], kl[3]));
+        uint16_t *kt = a.lr_kt + ((int64_t)ci * 2 * CC + t) * 64 + c0;  // Ktil hi, then lo
+        put4_split(kt, kt + CC * 64, kl);
         if (t == CC - 1) {
             float bc[4];
 #pragma unroll

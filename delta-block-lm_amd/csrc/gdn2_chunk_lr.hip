@@ -98,19 +98,24 @@ __device__ __forceinline__ void lr_split(const f32x4 &x, lr_v4s &hi, lr_v4s &lo)
     }
 }
 
-template <int KD_, int CT_, int NCW_, int NPROD_, int R_, bool BWD_, bool LO_>
+template <int KD_, int CT_, int NCW_, int NPROD_, int R_, bool BWD_, bool LO_, bool WHL_>
 struct LrCfg {
     static constexpr int KD = KD_, CT = CT_, NCW = NCW_, NPROD = NPROD_, R = R_;
     static constexpr bool BWD = BWD_, LO = LO_;  // LO: the checkpoint keeps lo parts
+    static constexpr bool WHL = WHL_;            // -W'^T comes as hi and lo (Ktil always does)
     static constexpr int WT_NCH = CT * 2 / 16;              // -W'^T [KD][CT] bf16
     static constexpr int KT_NCH = KD * 2 / 16;              // Ktil [CT][KD] bf16
     static constexpr int AUX_NCH = (BWD ? KD : CT) * 4 / 16;  // N^T [cols][KD] or U^T [cols][CT] f32
-    static constexpr int WT_BYTES = KD * CT * 2;
+    // The factors arrive as bf16 hi and lo tiles, the lo tile right after the hi
+    // tile in memory and in the LDS slot (rows KD.. of -W'^T, CT.. of Ktil).
+    static constexpr int WT_BYTES = KD * CT * 2;            // one term
     static constexpr int KT_BYTES = CT * KD * 2;
+    static constexpr int WT_TERMS = WHL ? 2 : 1;
     static constexpr int AUX_BYTES = NCW * 16 * AUX_NCH * 16;
     static constexpr int GV_BYTES = 1024;                   // KD f32 (KD <= 256)
-    static constexpr int WT_OPS = WT_BYTES / 1024, KT_OPS = KT_BYTES / 1024, AUX_OPS = AUX_BYTES / 1024;
-    static constexpr int SLOT = WT_BYTES + KT_BYTES + AUX_BYTES + GV_BYTES;
+    static constexpr int WT_OPS = WT_TERMS * WT_BYTES / 1024, KT_OPS = 2 * KT_BYTES / 1024,
+                         AUX_OPS = AUX_BYTES / 1024;
+    static constexpr int SLOT = WT_TERMS * WT_BYTES + 2 * KT_BYTES + AUX_BYTES + GV_BYTES;
     static constexpr int XS_NCH = KD * 2 / 16;                  // X^T staging rows [16 cols][KD] bf16
     static constexpr int XS_BYTES = 16 * KD * 2;                // one term (hi or lo)
     static constexpr int LDS_BYTES = R * SLOT + NCW * (LO ? 2 : 1) * XS_BYTES;
@@ -125,6 +130,8 @@ struct LrCfg {
                   "prefetched chunks fit the memory counter");
     static_assert(LDS_BYTES <= 160 * 1024, "ring and staging fit LDS");
     static_assert(KD % 32 == 0 && (CT == 16 || CT % 32 == 0), "tile shapes");
+    // The lo tile reuses the hi tile's swizzle: lr_swz repeats every 16 rows.
+    static_assert(KD % 16 == 0 && CT % 16 == 0, "lo tiles start on a swizzle period");
 };
 
 }  // namespace
@@ -157,13 +164,14 @@ __global__ void __launch_bounds__(64 * (Cfg::NCW + Cfg::NPROD)) lr_scan_kernel(L
             const int64_t cix = (int64_t)bh * p.nc + chunk_of(sc);
             char *slot = lr_ring + (s % R) * Cfg::SLOT;
             if (Cfg::NPROD == 1 || pw == 0)
-                dma_tile(reinterpret_cast<const char *>(p.wt + cix * KD * CT), Cfg::WT_OPS, Cfg::WT_NCH, slot);
+                dma_tile(reinterpret_cast<const char *>(p.wt + cix * Cfg::WT_TERMS * KD * CT), Cfg::WT_OPS,
+                         Cfg::WT_NCH, slot);
             if (Cfg::NPROD == 1 || pw == 1)
-                dma_tile(reinterpret_cast<const char *>(p.kt + cix * CT * KD), Cfg::KT_OPS, Cfg::KT_NCH,
-                         slot + Cfg::WT_BYTES);
+                dma_tile(reinterpret_cast<const char *>(p.kt + cix * 2 * CT * KD), Cfg::KT_OPS, Cfg::KT_NCH,
+                         slot + Cfg::WT_TERMS * Cfg::WT_BYTES);
             if (Cfg::NPROD == 1 || pw == 2) {
                 const float *aux = BWD ? p.n + (cix * p.vd + colbase) * KD : p.u + (cix * p.vd + colbase) * CT;
-                char *ax = slot + Cfg::WT_BYTES + Cfg::KT_BYTES;
+                char *ax = slot + Cfg::WT_TERMS * Cfg::WT_BYTES + 2 * Cfg::KT_BYTES;
                 dma_tile(reinterpret_cast<const char *>(aux), Cfg::AUX_OPS, Cfg::AUX_NCH, ax);
                 if (l < KD / 4)
                     __builtin_amdgcn_global_load_lds((lr_gptr)(p.gv + cix * KD + 4 * l),
@@ -226,46 +234,40 @@ __global__ void __launch_bounds__(64 * (Cfg::NCW + Cfg::NPROD)) lr_scan_kernel(L
         }
         lr_barrier();  // slot s has landed
         const char *slot = lr_ring + (s % R) * Cfg::SLOT;
-        const char *wt = slot, *kt = slot + Cfg::WT_BYTES, *ax = kt + Cfg::KT_BYTES;
+        const char *wt = slot, *kt = slot + Cfg::WT_TERMS * Cfg::WT_BYTES, *ax = kt + 2 * Cfg::KT_BYTES;
+        constexpr bool WHL = Cfg::WHL;
         const float *gv = reinterpret_cast<const float *>(ax + Cfg::AUX_BYTES);
-        // Every LDS read of the step first (none depends on X or V), so their
+        constexpr int WL = Cfg::WT_BYTES, KL = Cfg::KT_BYTES;  // offsets of the lo tiles
+        // Phase 1's LDS reads first (none depends on X), then phase 2's, so their
         // latencies overlap each other and the products.
         constexpr int NP = CT >= 32 ? CT / 32 : 1;
-        bf16x8_t qa[CT / 16][KD / 32];  // phase 1 A operands (Qm)
-        bf16x8_t pa[KD / 16][NP];       // phase 2 A operands (Pm^T), CT >= 32
-        lr_v4s pa4[KD / 16];            // phase 2 A operands, CT = 16
+        bf16x8_t qa[CT / 16][KD / 32], qal[CT / 16][KD / 32] = {};  // phase 1 A operands (Qm hi, lo)
         f32x4 ad[CT / 16], nb[KD / 16], gq[KD / 16];
 #pragma unroll
         for (int tt = 0; tt < CT / 16; ++tt)
 #pragma unroll
             for (int kk = 0; kk < KD / 32; ++kk) {
                 if (BWD) {  // Qm = Ktil rows: token 16 tt + n, keys 32 kk + 4 g (+ 16)
-                    qa[tt][kk] = lr_cat(lr_ld8(kt + lr_off(16 * tt + n, 32 * kk + 4 * g, 2, Cfg::KT_NCH)),
-                                        lr_ld8(kt + lr_off(16 * tt + n, 32 * kk + 16 + 4 * g, 2, Cfg::KT_NCH)));
+                    const int o0 = lr_off(16 * tt + n, 32 * kk + 4 * g, 2, Cfg::KT_NCH);
+                    const int o1 = lr_off(16 * tt + n, 32 * kk + 16 + 4 * g, 2, Cfg::KT_NCH);
+                    qa[tt][kk] = lr_cat(lr_ld8(kt + o0), lr_ld8(kt + o1));
+                    qal[tt][kk] = lr_cat(lr_ld8(kt + KL + o0), lr_ld8(kt + KL + o1));
                 } else {  // Qm = -W' read across -W'^T rows (keys 32 kk + 4 g + e (+ 16), token 16 tt + n)
                     const int r = 32 * kk + 4 * g + (n >> 2), e = 16 * tt + 4 * (n & 3);
-                    qa[tt][kk] = lr_cat(lr_tr16(wt + lr_off(r, e, 2, Cfg::WT_NCH)),
-                                        lr_tr16(wt + lr_off(r + 16, e, 2, Cfg::WT_NCH)));
+                    const int o0 = lr_off(r, e, 2, Cfg::WT_NCH), o1 = lr_off(r + 16, e, 2, Cfg::WT_NCH);
+                    qa[tt][kk] = lr_cat(lr_tr16(wt + o0), lr_tr16(wt + o1));
+                    if (WHL) qal[tt][kk] = lr_cat(lr_tr16(wt + WL + o0), lr_tr16(wt + WL + o1));
                 }
+            }
+        if (!BWD)
+#pragma unroll
+            for (int tt = 0; tt < CT / 16; ++tt) {
+                const float4 u = *reinterpret_cast<const float4 *>(ax + lr_off(16 * w + n, 16 * tt + 4 * g, 4,
+                                                                               Cfg::AUX_NCH));
+                ad[tt] = f32x4{u.x, u.y, u.z, u.w};
             }
 #pragma unroll
         for (int rt = 0; rt < KD / 16; ++rt) {
-            if constexpr (CT >= 32) {
-#pragma unroll
-                for (int q = 0; q < NP; ++q) {
-                    if (BWD) {  // Pm = -W': -W'^T rows 16 rt + n, tokens 32 q + 4 g (+ 16)
-                        pa[rt][q] = lr_cat(lr_ld8(wt + lr_off(16 * rt + n, 32 * q + 4 * g, 2, Cfg::WT_NCH)),
-                                           lr_ld8(wt + lr_off(16 * rt + n, 32 * q + 16 + 4 * g, 2, Cfg::WT_NCH)));
-                    } else {  // Pm = Ktil read across its rows (tokens 32 q + 4 g + e (+ 16), key 16 rt + n)
-                        const int r = 32 * q + 4 * g + (n >> 2), e = 16 * rt + 4 * (n & 3);
-                        pa[rt][q] = lr_cat(lr_tr16(kt + lr_off(r, e, 2, Cfg::KT_NCH)),
-                                           lr_tr16(kt + lr_off(r + 16, e, 2, Cfg::KT_NCH)));
-                    }
-                }
-            } else {
-                if (BWD) pa4[rt] = lr_ld8(wt + lr_off(16 * rt + n, 4 * g, 2, Cfg::WT_NCH));
-                else pa4[rt] = lr_tr16(kt + lr_off(4 * g + (n >> 2), 16 * rt + 4 * (n & 3), 2, Cfg::KT_NCH));
-            }
             const float4 gv4 = *reinterpret_cast<const float4 *>(gv + 16 * rt + 4 * g);
             gq[rt] = f32x4{gv4.x, gv4.y, gv4.z, gv4.w};
             if (BWD) {
@@ -274,14 +276,7 @@ __global__ void __launch_bounds__(64 * (Cfg::NCW + Cfg::NPROD)) lr_scan_kernel(L
                 nb[rt] = f32x4{nv.x, nv.y, nv.z, nv.w};
             }
         }
-        if (!BWD)
-#pragma unroll
-            for (int tt = 0; tt < CT / 16; ++tt) {
-                const float4 u = *reinterpret_cast<const float4 *>(ax + lr_off(16 * w + n, 16 * tt + 4 * g, 4,
-                                                                               Cfg::AUX_NCH));
-                ad[tt] = f32x4{u.x, u.y, u.z, u.w};
-            }
-        // phase 1: V = Ad - Qm X (token tiles tt)
+        // phase 1: V = Ad - Qm X (token tiles tt), three terms of the hi/lo pairs
         f32x4 V[CT / 16];
 #pragma unroll
         for (int tt = 0; tt < CT / 16; ++tt) V[tt] = BWD ? zero4() : ad[tt];
@@ -290,6 +285,8 @@ __global__ void __launch_bounds__(64 * (Cfg::NCW + Cfg::NPROD)) lr_scan_kernel(L
 #pragma unroll
             for (int tt = 0; tt < CT / 16; ++tt) {
                 V[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[tt][kk], xh[kk], V[tt], 0, 0, 0);
+                if (BWD || WHL)
+                    V[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qal[tt][kk], xh[kk], V[tt], 0, 0, 0);
                 V[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[tt][kk], xl[kk], V[tt], 0, 0, 0);
             }
         // phase 2: X = gv X + Pm^T V + N (row tiles rt)
@@ -315,12 +312,36 @@ __global__ void __launch_bounds__(64 * (Cfg::NCW + Cfg::NPROD)) lr_scan_kernel(L
             if constexpr (CT >= 32) {
 #pragma unroll
                 for (int q = 0; q < NP; ++q) {
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[rt][q], vh[q], acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[rt][q], vl[q], acc, 0, 0, 0);
+                    bf16x8_t pa, pal = {};
+                    if (BWD) {  // Pm = -W': -W'^T rows 16 rt + n, tokens 32 q + 4 g (+ 16)
+                        const int o0 = lr_off(16 * rt + n, 32 * q + 4 * g, 2, Cfg::WT_NCH);
+                        const int o1 = lr_off(16 * rt + n, 32 * q + 16 + 4 * g, 2, Cfg::WT_NCH);
+                        pa = lr_cat(lr_ld8(wt + o0), lr_ld8(wt + o1));
+                        if (WHL) pal = lr_cat(lr_ld8(wt + WL + o0), lr_ld8(wt + WL + o1));
+                    } else {  // Pm = Ktil read across its rows (tokens 32 q + 4 g + e (+ 16), key 16 rt + n)
+                        const int r = 32 * q + 4 * g + (n >> 2), e = 16 * rt + 4 * (n & 3);
+                        const int o0 = lr_off(r, e, 2, Cfg::KT_NCH), o1 = lr_off(r + 16, e, 2, Cfg::KT_NCH);
+                        pa = lr_cat(lr_tr16(kt + o0), lr_tr16(kt + o1));
+                        pal = lr_cat(lr_tr16(kt + KL + o0), lr_tr16(kt + KL + o1));
+                    }
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vh[q], acc, 0, 0, 0);
+                    if (!BWD || WHL) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pal, vh[q], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vl[q], acc, 0, 0, 0);
                 }
             } else {  // 16 tokens: one 16x16x16 product per term
-                acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa4[rt], vh4, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa4[rt], vl4, acc, 0, 0, 0);
+                lr_v4s pa4, pal4 = {0, 0, 0, 0};
+                if (BWD) {
+                    const int o = lr_off(16 * rt + n, 4 * g, 2, Cfg::WT_NCH);
+                    pa4 = lr_ld8(wt + o);
+                    if (WHL) pal4 = lr_ld8(wt + WL + o);
+                } else {
+                    const int o = lr_off(4 * g + (n >> 2), 16 * rt + 4 * (n & 3), 2, Cfg::KT_NCH);
+                    pa4 = lr_tr16(kt + o);
+                    pal4 = lr_tr16(kt + KL + o);
+                }
+                acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa4, vh4, acc, 0, 0, 0);
+                if (!BWD || WHL) acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pal4, vh4, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa4, vl4, acc, 0, 0, 0);
             }
             X[rt] = acc;
         }
@@ -352,11 +373,14 @@ hipError_t launch_lr_scan(const LrScanArgs &p, int kd, int ct, hipStream_t strea
     // d = 128 keeps bf16 hi only, the 16-token chunks hi and lo
     if ((kd == 128) != (p.ckpt_lo == nullptr)) return hipErrorInvalidValue;
     if (kd == 128 && ct == 64 && p.vd % 32 == 0)
-        return p.reverse ? launch_lr<LrCfg<128, 64, 2, 3, 3, true, false>>(p, stream)
-                         : launch_lr<LrCfg<128, 64, 2, 3, 3, false, false>>(p, stream);
+        return p.reverse ? launch_lr<LrCfg<128, 64, 2, 3, 2, true, false, false>>(p, stream)
+                         : launch_lr<LrCfg<128, 64, 2, 3, 2, false, false, false>>(p, stream);
+    if (kd == 64 && ct == 64 && p.vd % 32 == 0)
+        return p.reverse ? launch_lr<LrCfg<64, 64, 2, 3, 3, true, true, true>>(p, stream)
+                         : launch_lr<LrCfg<64, 64, 2, 3, 3, false, true, true>>(p, stream);
     if (kd == 64 && ct == 16 && p.vd % 16 == 0)
-        return p.reverse ? launch_lr<LrCfg<64, 16, 1, 1, 6, true, true>>(p, stream)
-                         : launch_lr<LrCfg<64, 16, 1, 1, 8, false, true>>(p, stream);
+        return p.reverse ? launch_lr<LrCfg<64, 16, 1, 1, 5, true, true, true>>(p, stream)
+                         : launch_lr<LrCfg<64, 16, 1, 1, 7, false, true, true>>(p, stream);
     return hipErrorInvalidValue;
 }
 

@@ -206,7 +206,7 @@ GDN2_API int gdn_scalar_backward(const gdn2_shape *shape, int chunk, const gdn2_
  * shares that device's array, so calls that overlap in time on one device
  * (other streams, other threads) race; calls in order on one stream do not.
  * Arguments and results are those of gdn_scalar_backward. */
-#define GDN2_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+#define GDN2_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 
 GDN2_API int gdn_scalar_backward_noalloc(const gdn2_shape *shape, int chunk, const gdn2_view *q,
                         const gdn2_view *k, const gdn2_view *v, const gdn2_view *beta,

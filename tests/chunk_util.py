@@ -67,13 +67,24 @@ def run_bwd(dk, p, chunk=64, use_final=True, use_scores=True):
                                   dev(p["dS"]) if use_scores else None)
 
 
-def cw_problem(seed, B, T, H, masks=True, initial=True, alpha_lo=0.5, reset_every=0, D=64):
+def slow_decay(p, lo, hi, seed):
+    """Replace a problem's scalar log gates by g = log(alpha) with alpha drawn
+    uniformly from [lo, hi] (the reference benchmark draws alpha in
+    [0.90, 0.99], crates/experiment/src/kron_benchmark.rs:89)."""
+    rng = np.random.default_rng(seed + 104729)
+    alpha = rng.uniform(lo, hi, size=p["g"].shape)
+    p["g"] = np.log(alpha).astype(np.float32)
+    return p
+
+
+def cw_problem(seed, B, T, H, masks=True, initial=True, alpha_lo=0.5, reset_every=0, D=64,
+               alpha_hi=1.0):
     """A channel-wise gate problem: bf16-rounded q/k/v/dO (q, k unit rows),
-    f32 per-channel gates alpha in (alpha_lo, 1), erase in (0, 1), write in
-    (-0.5, 1), with the masks of problem()."""
+    f32 per-channel gates alpha in (alpha_lo, alpha_hi), erase in (0, 1), write
+    in (-0.5, 1), with the masks of problem()."""
     p = problem(seed, B, T, H, masks=masks, initial=initial, K=D, V=D, reset_every=reset_every)
     rng = np.random.default_rng(seed + 7919)
-    p["alpha"] = rng.uniform(alpha_lo, 1.0, size=(B, T, H, D)).astype(np.float32)
+    p["alpha"] = rng.uniform(alpha_lo, alpha_hi, size=(B, T, H, D)).astype(np.float32)
     p["erase"] = rng.uniform(0.0, 1.0, size=(B, T, H, D)).astype(np.float32)
     p["write"] = rng.uniform(-0.5, 1.0, size=(B, T, H, D)).astype(np.float32)
     return p
@@ -87,3 +98,18 @@ def cw_oracle(p, use_final=True, use_scores=True):
                         p["reset"], p["initial"], p["dO"], p["dF"] if use_final else None,
                         p["dS"] if use_scores else None)
     return (out, fin, sc), g
+
+
+def fixture_problem(f, bf16=True):
+    """A restated reference fixture (tests/fixtures.py) as a cw_problem-style
+    dict, with q/k/v and the output adjoint rounded to bf16 when the problem
+    is meant for the bf16 chunk kernels (the oracle then sees the rounded
+    values)."""
+    bf = (lambda x: torch.tensor(np.ascontiguousarray(x), dtype=torch.float32)
+          .to(torch.bfloat16).float().numpy()) if bf16 else (lambda x: np.asarray(x, np.float32))
+    return dict(q=bf(f.q), k=bf(f.k), v=bf(f.v), alpha=np.array(f.alpha, np.float32),
+                erase=np.array(f.erase, np.float32), write=np.array(f.write, np.float32),
+                valid=np.array(f.valid, np.float32), reset=np.array(f.reset, np.float32),
+                initial=None if f.initial is None else np.array(f.initial, np.float32),
+                dO=bf(f.upstream), dF=np.array(f.final_adjoint, np.float32),
+                dS=np.array(f.score_adjoint, np.float32))

@@ -36,8 +36,9 @@ class Fixture(dict):
     __getattr__ = dict.__getitem__
 
 
-def gdn_fixture(t: int) -> Fixture:
-    b, h, k, v = 2, 4, 32, 64
+def gdn_fixture(t: int, k: int = 32, v: int = 64, b: int = 2, h: int = 4) -> Fixture:
+    """The reference's widths are K = 32, V = 64 with B = 2, H = 4; other
+    widths and sizes apply the same per-element formulas to a larger array."""
     widths = [k, k, v, k, k, v]
     data = []
     for field, width in enumerate(widths):
@@ -79,13 +80,16 @@ def aligned_fixture(t: int) -> Fixture:
     return f
 
 
-def gate_fixture(t: int, mode: int = 0) -> Fixture:
+def gate_fixture(t: int, mode: int = 0, K: int = 32, V: int = 64, b: int = 2,
+                 h: int = 4) -> Fixture:
     """GDN gate fixture with the edits of kron_checks.rs:132-188.
 
     mode 0: output + final state + score objectives; 1: output only;
-    2: final state only; 3: score only (kron_checks.rs:190-192)."""
-    f = gdn_fixture(t)
-    b, h, K = 2, 4, 32
+    2: final state only; 3: score only (kron_checks.rs:190-192).  K, V, b and h
+    default to the reference's; other values apply the same formulas and
+    edits (alpha zero on key channel 0 at p = 2, on every key channel at
+    p = 16) to a larger problem."""
+    f = gdn_fixture(t, K, V, b, h)
     valid = f.valid.astype(bool).reshape(-1)
     reset = f.reset.astype(bool).reshape(-1)
     reset[0] = False
@@ -117,9 +121,9 @@ def gate_fixture(t: int, mode: int = 0) -> Fixture:
                     f.alpha[row, p, hh, :K] = 0.0
     f["valid"] = valid.reshape(b, t).astype(np.uint8)
     f["reset"] = reset.reshape(b, t).astype(np.uint8)
-    ii = np.arange(b * h * K * 64).astype(F32)
+    ii = np.arange(b * h * K * V).astype(F32)
     f["initial"] = (F32(0.03) * np.sin((ii * F32(11) + F32(7)) * F32(0.017)).astype(F32)).reshape(
-        b, h, K, 64)
+        b, h, K, V)
     isd = np.arange(b * t * h).astype(F32)
     score_seed = (F32(0.07) * np.cos((isd * F32(7) + F32(2)) * F32(0.13)).astype(F32)).reshape(
         b, t, h)

@@ -1,6 +1,8 @@
 """Helpers for the GPU parity tests: device upload and the tolerance gates."""
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import torch
 
@@ -35,6 +37,15 @@ def gate(name, got, ref, tol, exact_zero=None, ref_gate=False):
         ez = np.broadcast_to(exact_zero, got.shape)
         assert np.all(got[ez] == 0), f"{name}: padding entries are not exactly zero"
         bad &= ~ez
+    ratio = err / bound
+    if exact_zero is not None:
+        ratio = np.where(ez, 0.0, ratio)
+    log = os.environ.get("GDN2_GATE_LOG")
+    if log and ratio.size:
+        # worst error-to-gate ratio per gated output, for the precision tables
+        test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+        with open(log, "a") as fh:
+            fh.write(f"{test}\t{name}\t{float(ratio.max()):.4f}\n")
     if bad.any():
         i = np.unravel_index(np.argmax(err / bound), err.shape)
         raise AssertionError(
