@@ -8,6 +8,14 @@ from gpu_util import dev
 from oracle import oracle
 
 
+def chunk_stages(D):
+    """Stage-timer names of the chunk-WY path at d_k = d_v = D (64 or 128):
+    prep, state scan and output forward; prep, adjoint scan and gradients
+    backward."""
+    assert D in (64, 128)
+    return {"chunk_prep", "state_scan", "chunk_out", "chunk_bprep", "adjoint_scan", "chunk_bgrad"}
+
+
 def problem(seed, B, T, H, masks=True, initial=True, K=64, V=64, reset_every=0):
     """reset_every > 0 adds a valid reset every reset_every tokens of the
     first sequence and a padded run before each (long sequences)."""

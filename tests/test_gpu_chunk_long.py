@@ -14,14 +14,12 @@ import pytest
 
 torch = pytest.importorskip("torch")
 
-from chunk_util import problem, scalar_oracle_grads  # noqa: E402
+from chunk_util import chunk_stages, problem, scalar_oracle_grads  # noqa: E402
 from gpu_util import TOL_BF16, dev, gate  # noqa: E402
 from oracle import oracle  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
-CHUNK_STAGES = {"chunk_prep", "state_scan", "chunk_out", "chunk_bprep", "adjoint_scan",
-                "chunk_bgrad"}
 
 
 @pytest.fixture(scope="module")
@@ -64,7 +62,7 @@ def test_long_chunk_path_matches_oracle(dk, T, H, reset_every):
     p = problem(T + H, 1, T, H, masks=True, reset_every=reset_every)
     print(f"chunk long: T={T} H={H} chunks={-(-T // 64)}", flush=True)
     (out, fin, sc), grads, ran = _fwd_bwd(dk, p)
-    assert CHUNK_STAGES <= ran, f"chunk kernels did not all run: {sorted(ran)}"
+    assert chunk_stages(64) <= ran, f"chunk kernels did not all run: {sorted(ran)}"
     a, e, w = oracle.scalar_gates(p["beta"], p["g"], 64, 64)
     o_out, o_fin, o_sc = oracle.scan(p["q"], p["k"], p["v"], a, e, w, p["valid"], p["reset"],
                                      p["initial"])
@@ -91,7 +89,7 @@ def test_chunk_loops_uneven_split(dk, D):
     p = problem(77 + D, 3, 1000, 7, masks=True, K=D, V=D, reset_every=300)
     print(f"chunk loops: B3 T1000 H7 D={D}, 336 chunks", flush=True)
     (out, fin, sc), grads, ran = _fwd_bwd(dk, p)
-    assert CHUNK_STAGES <= ran, f"chunk kernels did not all run: {sorted(ran)}"
+    assert chunk_stages(D) <= ran, f"chunk kernels did not all run: {sorted(ran)}"
     a, e, w = oracle.scalar_gates(p["beta"], p["g"], D, D)
     o_out, o_fin, o_sc = oracle.scan(p["q"], p["k"], p["v"], a, e, w, p["valid"], p["reset"],
                                      p["initial"])
@@ -118,7 +116,7 @@ def test_long_split_continuation(dk, D):
     T, half = 8192, 4096
     p = problem(11, 2, T, 2, masks=False, K=D, V=D)
     whole_fwd, whole_grads, ran = _fwd_bwd(dk, p)
-    assert CHUNK_STAGES <= ran
+    assert chunk_stages(D) <= ran
     first = {n: (x[:, :half] if x is not None and x.ndim in (2, 3, 4) and x.shape[1] == T else x)
              for n, x in p.items()}
     second = {n: (x[:, half:] if x is not None and x.ndim in (2, 3, 4) and x.shape[1] == T
