@@ -263,7 +263,7 @@ static ChunkArgs cw_args(const gdn2_shape *s, const gdn2_view *q, const gdn2_vie
 
 extern "C" {
 
-int gdn2_abi_version(void) { return 100; }
+int gdn2_abi_version(void) { return 101; }
 
 const char *gdn2_last_error(void) { return gdn2::last_error(); }
 

@@ -30,9 +30,14 @@
 // forward, whose adjoint never crosses a reset, as the reference's chunked
 // kernels compute it (crates/kernels/src/gdn2.rs:24-65, :288-490).
 //
-// log alpha is floored at -80 (exp(-80) ~ 2e-35): below that the decay is
-// taken as exp(-80) and the alpha gradient is zero.  The alpha gradient is the
-// log-domain adjoint divided by alpha, so its absolute error grows as 1/alpha.
+// log alpha is floored at -80 (exp(-80) ~ 2e-35) in the decays: below that a
+// decay is taken as exp(-80).  These kernels need alpha >= 0 on valid tokens:
+// a negative alpha turns its chunk's log decay into NaN, which then reaches the
+// outputs, the state and every gradient of the sequence (the token-sequential
+// kernels take any alpha).  The alpha gradient does not go through the log:
+// it sums each gradient pair's coefficient times the product of the other
+// alphas of the pair's span (cw_bgrad phase 7), so alpha = 0 and small alphas
+// get their exact gradient.
 #include "gdn2_chunk_tile.h"
 
 #include <algorithm>
@@ -298,7 +303,9 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a, int nchunks) 
         float la[4], eh[4], wv[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            la[e] = on ? fmaxf(__logf(al[e]), LOG_FLOOR) : 0.f;
+            // a negative alpha is outside these kernels' log-domain decays: it
+            // poisons the chunk (NaN), so the caller sees it instead of a wrong value
+            la[e] = on ? (al[e] < 0.f ? __builtin_nanf("") : fmaxf(__logf(al[e]), LOG_FLOOR)) : 0.f;
             eh[e] = er[e] * kv[e];
             wv[e] = wr[e] * vv[e];
         }
@@ -895,9 +902,11 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a, int nchunks)
 //     kAP_s = sum_t (dA_ts D_ts ehat_t + dP_ts D_ts q_t)
 //   dq = b dQhat + qP;  dehat = b dAhat + eA;  de = k dehat
 //   dk = lam dKtil + kAP + e dehat + c' k
-//   dLambda_t = ehat eA + q qP - k kAP + Ahat dAhat + Qhat dQhat - Ktil dKtil
-//               [t = 15: + sum_s Ktil dKtil + b_15 rowsum(S0 . dS)]
-//   dlog alpha_u = sum_{t >= u} dLambda_t,  dalpha = dlog alpha / alpha
+//   dalpha_u = sum over the pairs (hi, lo) with lo < u <= hi of the pair's
+//              coefficient times the product of alpha over (lo, hi] without u:
+//              interior pairs (dA_ts ehat_t + dP_ts q_t) k_s, start pairs
+//              ehat_t dAhat_t + q_t dQhat_t (through b_t), end pairs k_s dKtil_s
+//              (through lam_s) and rowsum(S0 . dS) (through b_15)
 // (zero on padding and on valid reset tokens, where the reference's alpha' is
 // alpha (1 - reset) and carries no gradient).
 namespace {
@@ -929,7 +938,7 @@ struct CwBGradSmem {
     } rb;
     float cs[CC], ck[CC], val[CC];
     int seg[CC];
-    float tail[64], fr[NW4][64], bc[64];
+    float fr[NW4][64];
 };
 
 // T^T (from the f32 T checkpoint) into hi/lo LDS rows [s][t]; thread
@@ -978,19 +987,15 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
     get4_f32(dck + t * 64 + c0, dl4);
     // Loads of phases 6 and 7, issued with the rest so that their latency is
     // not exposed after a barrier: erase at this lane's accumulator positions
-    // (key tile w), and for wave 3 the alpha of channel tid - 192 at every token.
-    float eacc[4], dacc[4], alr[CC];
+    // (key tile w), and alpha at this thread's token and channels.
+    float eacc[4], dacc[4], alv4[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int tq = t0 + acc_row(e);
         eacc[e] = tq < a.T ? ld4<float>(a.erase, b, tq, h, 16 * w + acc_col()) : 0.f;
         dacc[e] = a.dscores ? dck[acc_row(e) * 64 + 16 * w + acc_col()] : 0.f;
     }
-    if (w == 3 && a.dalpha) {
-#pragma unroll
-        for (int tt = 0; tt < CC; ++tt)
-            alr[tt] = t0 + tt < a.T ? ld4<float>(a.alpha, b, t0 + tt, h, tid - 192) : 1.f;
-    }
+    if (a.dalpha) load4_f32(a.alpha, b, tg, h, c0, inb, 1.f, alv4);
     {
         const int64_t so = (int64_t)ci * 64 * 64;
 #pragma unroll
@@ -1013,7 +1018,6 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
             klv[e] = (sg == sg15 ? __expf(L15 - L[e]) : 0.f) * kv[e];
             ksq += kv[e] * kv[e];
             dsq += dl4[e] * dl4[e];
-            if (t == CC - 1) sm.bc[c0 + e] = sg15 == 0 ? __expf(L15) : 0.f;
         }
         put4_f32(&sm.lam[t * LDL + c0], L);
         put4_f32(&sm.ehf[t * LDL + c0], eh);
@@ -1066,21 +1070,6 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
                      (bf16_val(dst[v * LDB + i]) + bf16_val(dstl[v * LDB + i]));
             sm.fr[w][i] = f;
         }
-    }
-    {  // sum_s Ktil_s dKtil_s per key channel (f32 Ktil)
-        const int i = 16 * w + acc_col();
-        const float L15 = sm.lam[(CC - 1) * LDL + i];
-        f32x4 z;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int s = acc_row(e);
-            const float kt = sm.seg[s] == sm.seg[CC - 1]
-                                 ? __expf(L15 - sm.lam[s * LDL + i]) * bf16_val(sm.kb[s * LDB + i])
-                                 : 0.f;
-            z[e] = kt * gkt[e];
-        }
-        const float cz = col_reduce(z);
-        if ((l >> 4) == 0) sm.tail[i] = cz;
     }
     __syncthreads();  // dS is dead: region A takes ddelta^T, dR, dA, dP
     auto &g = sm.ra.g;
@@ -1204,7 +1193,19 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
         }
     }
     __syncthreads();
-    // Phase 6: assemble dq, dk, de and dLambda at key tile w (accumulator layout).
+    // Phase 6: assemble dq, dk, de at key tile w (accumulator layout), and the
+    // alpha gradient's start- and end-pair coefficients (phase 7) over the dead
+    // ddelta^T, alpha (1 on padding) over the dead dR rows.
+    float *stc = reinterpret_cast<float *>(g.ddt), *enc = stc + CC * LDL;
+    float *alf = reinterpret_cast<float *>(g.drr);
+    static_assert(2 * CC * LDL * sizeof(float) <= 2 * sizeof(g.ddt), "pair coefficients over ddelta^T");
+    static_assert(CC * LDL * sizeof(float) <= 2 * sizeof(g.drr), "alpha over the dR rows");
+    if (a.dalpha) {
+        float ae[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ae[e] = on ? alv4[e] : 1.f;
+        put4_f32(&alf[t * LDL + c0], ae);
+    }
     {
         const int i = 16 * w + acc_col();
         const float L15 = sm.lam[(CC - 1) * LDL + i];
@@ -1223,12 +1224,10 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
             const float dq = bt * gqh[e] + qP;
             const float deh = bt * gah[e] + eA;
             const float dk = lt * gkt[e] + kAP + ee * deh + sm.ck[tt] * k;
-            float dlam = eh * eA + q * qP - k * kAP + bt * eh * gah[e] + bt * q * gqh[e] - lt * k * gkt[e];
-            if (tt == CC - 1)
-                dlam += sm.tail[i] + sm.bc[i] * (sm.fr[0][i] + sm.fr[1][i] + sm.fr[2][i] + sm.fr[3][i]);
             gq[e] = von ? dq : 0.f;
             gk[e] = von ? dk : 0.f;
-            sm.dRf[tt * LDL + i] = dlam;  // dR is dead: dLambda takes its place
+            stc[tt * LDL + i] = sm.seg[tt] == 0 ? eh * gah[e] + q * gqh[e] : 0.f;
+            enc[tt * LDL + i] = sm.seg[tt] == sm.seg[CC - 1] ? k * gkt[e] : 0.f;
             if (a.derase && tq < a.T)
                 a.derase[(((int64_t)b * a.T + tq) * a.H + h) * 64 + i] = von ? k * deh : 0.f;
         }
@@ -1245,24 +1244,72 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
             if (a.dk) *reinterpret_cast<uint4 *>(reinterpret_cast<uint16_t *>(a.dk) + o) =
                 *reinterpret_cast<const uint4 *>(&sm.ptrl[r * LDB + cb]);
         }
-    } else if (tid >= 192 && a.dalpha) {  // dalpha: reverse running sums of dLambda, channel i
-        // A token's log alpha reaches only the Lambda of later tokens in its own
-        // segment (differences across a reset vanish), so the sum restarts at
-        // every reset; the reset token's own alpha carries no gradient.
-        const int i = tid - 192;
-        float acc = 0.f;
+    }
+    if (a.dalpha) {
+        // Phase 7: dalpha without dividing by alpha.  Every gradient term that
+        // alpha_u enters is a pair (hi, lo) of the chunk with lo < u <= hi whose
+        // decay is the product of alpha over (lo, hi]: interior pairs of tokens
+        // (s < t), start pairs (t, start) through b_t, end pairs (end, s) through
+        // lam_s and the pair (end, start) through b_15 (end acts as token 15,
+        // start as token -1).  With C the pair coefficients,
+        //   dalpha_u = sum_{lo < u <= hi} C[hi][lo] prod_{lo < u' <= hi, u' != u} alpha_u'
+        //            = sum_{lo < u} L(lo, u) Y(u, lo),
+        //   L(lo, u) = prod_{lo < u' < u} alpha_u',
+        //   Y(u, lo) = C[u][lo] + alpha_{u+1} Y(u + 1, lo),
+        // so alpha = 0 gets its exact gradient and a small alpha loses no
+        // precision.  Pairs never cross a reset (their coefficients are zero), and
+        // padding has alpha 1.  Thread (channel i = tid / 4, part p = tid % 4)
+        // takes lo = p - 1, p + 3, p + 7, p + 11; the four parts are summed by a
+        // DPP quad.
+        const int i = tid >> 2, p = tid & 3;
+        const int sg15 = sm.seg[CC - 1];
+        const float fs = sg15 == 0 ? sm.fr[0][i] + sm.fr[1][i] + sm.fr[2][i] + sm.fr[3][i] : 0.f;
+        float alv[CC], ehv[CC], qv16[CC], acc[CC];
 #pragma unroll
-        for (int tt = CC - 1; tt >= 0; --tt) {
-            acc += sm.dRf[tt * LDL + i];
-            const int tq = t0 + tt;
-            const bool von = sm.val[tt] != 0.f;
-            const bool rs = von && (tt == 0 ? sm.seg[0] == 1 : sm.seg[tt] != sm.seg[tt - 1]);
-            if (tq < a.T) {
-                const float al = von ? alr[tt] : 1.f;
-                const bool live = von && !rs && __logf(al) > LOG_FLOOR;
-                a.dalpha[(((int64_t)b * a.T + tq) * a.H + h) * 64 + i] = live ? acc / al : 0.f;
+        for (int u = 0; u < CC; ++u) {
+            alv[u] = alf[u * LDL + i];
+            ehv[u] = sm.ehf[u * LDL + i];
+            qv16[u] = bf16_val(sm.qb[u * LDB + i]);
+            acc[u] = 0.f;
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int lo = p - 1 + 4 * m;  // -1 .. 14
+            const float klo = lo >= 0 ? bf16_val(sm.kb[lo * LDB + i]) : 0.f;
+            const float elo = lo >= 0 ? enc[lo * LDL + i] : fs;  // end pair with lo
+            float Yr[CC], Y = 0.f;
+#pragma unroll
+            for (int u = CC - 1; u >= 0; --u) {
+                const int lc = lo >= 0 ? lo : 0;
+                const float inner = (g.dA[u * LDI + lc] * ehv[u] + g.dP[u * LDI + lc] * qv16[u]) * klo;
+                float cf = lo < 0 ? stc[u * LDL + i] : (u > lo ? inner : 0.f);
+                if (u == CC - 1) cf += elo;
+                Y = u == CC - 1 ? cf : cf + alv[u + 1] * Y;
+                Yr[u] = Y;
             }
-            if (rs) acc = 0.f;
+            float L = 1.f;
+#pragma unroll
+            for (int u = 0; u < CC; ++u)
+                if (u > lo) {
+                    acc[u] += L * Yr[u];
+                    L *= alv[u];
+                }
+        }
+#pragma unroll
+        for (int u = 0; u < CC; ++u) {
+            float x = acc[u];
+            x += dpp<0xB1>(x);
+            x += dpp<0x4E>(x);
+            acc[u] = x;
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int u = p + 4 * m, tq = t0 + u;
+            const float da = p == 0 ? acc[4 * m] : p == 1 ? acc[4 * m + 1] : p == 2 ? acc[4 * m + 2] : acc[4 * m + 3];
+            const bool von = sm.val[u] != 0.f;
+            // the reset token's own alpha (applied to a zeroed state) carries no gradient
+            const bool rs = von && (u == 0 ? sm.seg[0] == 1 : sm.seg[u] != sm.seg[u - 1]);
+            if (tq < a.T) a.dalpha[(((int64_t)b * a.T + tq) * a.H + h) * 64 + i] = von && !rs ? da : 0.f;
         }
     }
 }

@@ -91,10 +91,11 @@ GDN2_API const char *gdn2_last_error(void);
  * reference allows 1..16, gdn_training.rs:370-373); results do not depend on
  * it.  bf16 q/k/v with keys = values = 64, unit channel stride and 16-byte
  * aligned token rows run the 16-token chunk-WY MFMA kernels whatever the
- * chunk argument (alpha >= 0; log alpha is floored at -80, below which the
- * alpha gradient is zero: an underflowed gate alpha = 0 gets d_alpha = 0
- * where the token-sequential kernels give the adjoint of the decayed state
- * times that state); everything else runs the token-sequential kernels.  On the chunk kernels d_output must have aligned rows too. */
+ * chunk argument; everything else runs the token-sequential kernels.  The
+ * chunk kernels need alpha >= 0 on valid tokens: a negative alpha gives NaN
+ * outputs, state and gradients for its sequence (the token-sequential kernels
+ * accept any alpha).  alpha = 0 and tiny alphas get their exact gradient on
+ * both.  On the chunk kernels d_output must have aligned rows too. */
 GDN2_API size_t gdn2_training_checkpoint_bytes(const gdn2_shape *shape, int chunk);
 
 GDN2_API int gdn2_training_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q,
@@ -142,7 +143,9 @@ GDN2_API int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gd
  * final state or score outputs.  q, k, v: F32 or BF16 (same dtype); alpha,
  * erase, write: F32.  bf16 q/k/v with keys = values = 64 and 16-byte aligned
  * rows run the 16-token chunk-WY MFMA kernels, everything else the
- * token-sequential kernels.  The checkpoint (opaque) replaces the reference's
+ * token-sequential kernels.  The chunk kernels need alpha >= 0 on live tokens
+ * (a negative alpha gives NaN results for its sequence); the token-sequential
+ * kernels accept any alpha.  The checkpoint (opaque) replaces the reference's
  * [B, H, T/16, 48, 64] checkpoint tensor. */
 GDN2_API size_t gdn2_scan_checkpoint_bytes(const gdn2_shape *shape);
 

@@ -38,7 +38,7 @@ def test_library_exports_all_declared_symbols(L):
 
 
 def test_abi_version(L):
-    assert L.gdn2_abi_version() == 100
+    assert L.gdn2_abi_version() == 101
 
 
 def _shape(B=2, T=8, H=2, K=32, V=64):

@@ -124,14 +124,81 @@ def test_cw_long(dk, T, reset_every):
 
 def test_cw_strong_decay(dk):
     """alpha down to 1e-3: the decays underflow the chunk within a few tokens.
-    The alpha gradient is gated in the log domain (alpha * dalpha), the
-    quantity the kernels form before the division by alpha."""
+    The alpha gradient itself is gated (it is formed without dividing by
+    alpha)."""
     p = cw_problem(29, 1, 80, 2, masks=True, alpha_lo=1e-3)
     r, grads, ran = _run(dk, p)
-    og = _check(p, r, grads, skip=("alpha",))
-    pad = (p["valid"] == 0)[:, :, None, None]
-    gate("alpha * dalpha", grads["alpha"].double().cpu().numpy() * p["alpha"],
-         og["alpha"] * p["alpha"], TOL_BF16, exact_zero=np.broadcast_to(pad, p["alpha"].shape))
+    assert FWD_STAGES | BWD_STAGES <= ran
+    _check(p, r, grads)
+
+
+@pytest.mark.parametrize("tiny", [1e-4, 1e-6, 1e-20])
+def test_cw_tiny_alpha_gradient(dk, tiny):
+    """alpha at 1e-4, 1e-6 and 1e-20 on a scattering of tokens and channels
+    (and in [1e-3, 1e-2] elsewhere on some rows): dalpha is finite and matches
+    the oracle, where dividing a log-domain gradient by alpha would blow up."""
+    p = cw_problem(31, 2, 70, 2, masks=True)
+    rng = np.random.default_rng(7)
+    pick = rng.random(p["alpha"].shape) < 0.08
+    p["alpha"][pick] = tiny
+    p["alpha"][0, 20:40] = rng.uniform(1e-3, 1e-2, size=p["alpha"][0, 20:40].shape).astype(np.float32)
+    print(f"cw tiny alpha {tiny}", flush=True)
+    r, grads, ran = _run(dk, p)
+    assert BWD_STAGES <= ran
+    assert torch.isfinite(grads["alpha"]).all()
+    _check(p, r, grads)
+
+
+def test_cw_alpha_zero_exact_gradient(dk):
+    """alpha exactly 0 (an underflowed gate) on one channel of a token and on
+    every channel of another: outputs, states and every gradient, dalpha
+    included, match the oracle (whose dalpha there is the pre-decay state
+    adjoint times the state, nonzero)."""
+    p = cw_problem(78, 1, 40, 2, masks=False)
+    p["alpha"][0, 10, 0, :8] = 0.0
+    p["alpha"][0, 27, 1, :] = 0.0
+    r, grads, ran = _run(dk, p)
+    assert FWD_STAGES | BWD_STAGES <= ran
+    og = _check(p, r, grads)
+    assert np.abs(og["alpha"][0, 10, 0, :8]).max() > 0  # the exact gradient is not zero there
+
+
+def test_cw_negative_alpha_fails_loudly(dk):
+    """A negative alpha is outside the chunk kernels' log-domain decays: the
+    sequence that holds it gets NaN outputs (never finite wrong values), the
+    other sequences are untouched, and the f32 token-sequential kernels give
+    the oracle's values for the same inputs."""
+    p = cw_problem(83, 2, 40, 1, masks=False)
+    p["alpha"][1, 12, 0, 5] = -0.5
+    x, init = _inputs(p, grad=False)
+    r = dk.gdn_training_scan(x["q"], x["k"], x["v"], x["alpha"], x["erase"], x["write"],
+                             dev(p["valid"]), dev(p["reset"]), init, 16)
+    torch.cuda.synchronize()
+    out = r.output.float().cpu().numpy()
+    assert np.isnan(out[1, 12:]).any(), "a negative alpha must not give finite outputs"
+    (o_out, o_fin, _), _ = cw_oracle(p)
+    gate("output of the sequence without a negative alpha", r.output[0], o_out[0], TOL_BF16)
+    xf = {n: dev(p[n]) for n in ("q", "k", "v")}
+    rf = dk.gdn_training_scan(xf["q"], xf["k"], xf["v"], x["alpha"], x["erase"], x["write"],
+                              dev(p["valid"]), dev(p["reset"]), init, 16)
+    gate("f32 (token-sequential) output with a negative alpha", rf.output, o_out, 1e-4)
+    gate("f32 (token-sequential) final state with a negative alpha", rf.final_state, o_fin, 1e-4)
+
+
+@pytest.mark.parametrize("t,mode", [(7, 0), (35, 0), (35, 1), (35, 2), (35, 3)])
+def test_cw_gate_fixture_k64(dk, t, mode):
+    """The reference GDN gate fixture with all its edits (crates/mixers/src/
+    kron_checks.rs:124-188: reset on padding, an all-padding chunk, a zero edit,
+    a negative write, zero key and value norms, alpha zero on one channel at
+    p = 2 and on every channel at p = 16, a nonzero initial state, the four
+    objectives) at K = V = 64 in bf16 through the channel-wise chunk kernels."""
+    import fixtures as fx
+    from chunk_util import fixture_problem
+    p = fixture_problem(fx.gate_fixture(t, mode, K=64, V=64))
+    print(f"cw gate fixture K=V=64 T={t} mode={mode}", flush=True)
+    r, grads, ran = _run(dk, p)
+    assert FWD_STAGES | BWD_STAGES <= ran
+    _check(p, r, grads)
 
 
 def test_cw_broadcast_gates(dk):
@@ -237,23 +304,6 @@ def test_cw_all_padding_row_and_zero_keys(dk):
     np.testing.assert_allclose(fin[1], p["initial"][1], rtol=2.0 ** -15, atol=1e-7)
     assert np.all(r.scores.detach().cpu().numpy()[0, 5] == 0)
     gate("d_initial (padded row passes dF)", grads["initial"][1], og["initial"][1], TOL_BF16)
-
-
-def test_cw_alpha_zero_is_floored(dk):
-    """alpha exactly 0 (an underflowed gate) on some channels: outputs, states
-    and every gradient but dalpha match the oracle; dalpha there is 0, the
-    documented floor of the log-domain gradient (log alpha < -80), where the
-    exact gradient is the pre-decay state adjoint times the state."""
-    p = cw_problem(78, 1, 40, 2, masks=False)
-    p["alpha"][0, 10, 0, :8] = 0.0
-    r, grads, ran = _run(dk, p)
-    assert FWD_STAGES | BWD_STAGES <= ran
-    og = _check(p, r, grads, skip=("alpha",))
-    da = grads["alpha"].double().cpu().numpy()
-    assert np.all(da[0, 10, 0, :8] == 0)
-    keep = np.ones(da.shape, bool)
-    keep[0, 10, 0, :8] = False
-    gate("dalpha (alpha > 0)", da[keep], og["alpha"][keep], TOL_BF16)
 
 
 def test_cw_many_heads(dk):
