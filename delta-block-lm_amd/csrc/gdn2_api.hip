@@ -4,6 +4,7 @@
 // anything, mirroring the reference's fail-fast asserts
 // (crates/kernels/src/gdn_training.rs:286-342, :356-390; chunk.rs:110-124):
 // an unsupported shape, dtype or buffer size is an error, never a fallback.
+#include <algorithm>
 #include <climits>
 #include <cstdarg>
 #include <cstdio>
@@ -11,6 +12,7 @@
 #include <string>
 
 #include "gdn2_chunk.h"
+#include "gdn2_chunk_f32.h"
 #include "gdn2_seq.h"
 #include "gdn2_status.h"
 
@@ -225,16 +227,39 @@ static bool use_cw_path(const gdn2_shape *shape, const gdn2_view *q, const gdn2_
            rows_aligned(k) && rows_aligned(v);
 }
 
+// f32 q/k/v with d_k, d_v <= 64 run the f32 chunk kernels (gdn2_chunk_f32.hip;
+// any element strides), again whatever the chunk argument.
+static bool use_fc_path(const gdn2_shape *shape, const gdn2_view *q) {
+    return fc_eligible_shape(shape) && q->dtype == GDN2_F32;
+}
+
+// The checkpoint and workspace sizes do not depend on the dtype: each is the
+// largest that any kernel family eligible for the shape needs.
 static size_t training_checkpoint_bytes(const gdn2_shape *s) {
     const size_t c = cw_eligible_shape(s) ? cw_checkpoint_bytes(s->batch, s->time, s->heads) : 0;
+    const size_t f = fc_eligible_shape(s) ? fc_checkpoint_bytes(s->batch, s->time, s->heads,
+                                                                (int)s->keys, (int)s->values)
+                                          : 0;
     const size_t q = seq_checkpoint_bytes(s);
-    return c > q ? c : q;
+    return std::max(c, std::max(f, q));
 }
 
 static size_t training_workspace_bytes(const gdn2_shape *s) {
     const size_t c = cw_eligible_shape(s) ? cw_workspace_bytes(s->batch, s->time, s->heads) : 0;
+    const size_t f = fc_eligible_shape(s) ? fc_workspace_bytes(s->batch, s->time, s->heads,
+                                                               (int)s->keys, (int)s->values)
+                                          : 0;
     const size_t q = seq_workspace_bytes(s);
-    return c > q ? c : q;
+    return std::max(c, std::max(f, q));
+}
+
+// The f32 chunk path's argument block over the token-sequential one.
+static FcArgs fc_args(const SeqArgs &s, void *checkpoint, void *workspace) {
+    FcArgs f{};
+    f.s = s;
+    f.nc = (s.T + FC_C - 1) / FC_C;
+    fc_bind(f, checkpoint, workspace);
+    return f;
 }
 
 static ChunkArgs cw_args(const gdn2_shape *s, const gdn2_view *q, const gdn2_view *k,
@@ -311,6 +336,11 @@ int gdn2_training_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q,
     a.out_bf16 = output_dtype == GDN2_BF16;
     a.final_state = final_state;
     a.scores = scores;
+    if (use_fc_path(shape, q)) {
+        const FcArgs f = fc_args(a, checkpoint, nullptr);
+        const hipEvent_t *ev = stage_events(0, (hipStream_t)stream);
+        return launch_status(launch_fc_fwd(f, (hipStream_t)stream, ev), "gdn2_training_scan");
+    }
     seq_bind_checkpoint(a, checkpoint);
     return launch_status(launch_seq_fwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
                          "gdn2_training_scan");
@@ -362,7 +392,6 @@ int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gdn2_view *
         return launch_status(launch_cw_bwd(c, (hipStream_t)stream, ev), "gdn2_training_backward");
     }
     SeqArgs a = seq_args(shape, q, k, v, alpha, erase, write, valid, reset);
-    seq_bind_checkpoint(a, checkpoint);
     if (d_output) a.dout = make_view(d_output);
     a.dfinal = d_final_state;
     a.dscores = d_scores;
@@ -373,6 +402,12 @@ int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gdn2_view *
     a.derase = derase;
     a.dwrite = dwrite;
     a.dinitial = d_initial;
+    if (use_fc_path(shape, q)) {
+        const FcArgs f = fc_args(a, const_cast<void *>(checkpoint), workspace);
+        const hipEvent_t *ev = stage_events(3, (hipStream_t)stream);
+        return launch_status(launch_fc_bwd(f, (hipStream_t)stream, ev), "gdn2_training_backward");
+    }
+    seq_bind_checkpoint(a, checkpoint);
     a.replay = (float *)workspace;
     return launch_status(launch_seq_bwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
                          "gdn2_training_backward");
@@ -417,6 +452,11 @@ int gdn2_scan(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k, c
     a.doc_end = make_view(doc_end);
     a.out = output;
     a.out_bf16 = output_dtype == GDN2_BF16;
+    if (use_fc_path(shape, q)) {
+        const FcArgs f = fc_args(a, checkpoint, nullptr);
+        const hipEvent_t *ev = stage_events(0, (hipStream_t)stream);
+        return launch_status(launch_fc_fwd(f, (hipStream_t)stream, ev), "gdn2_scan");
+    }
     seq_bind_checkpoint(a, checkpoint);
     return launch_status(launch_seq_fwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
                          "gdn2_scan");
@@ -467,7 +507,6 @@ int gdn2_backward(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *
     a.doc = 1;
     a.doc_start = make_view(doc_start);
     a.doc_end = make_view(doc_end);
-    seq_bind_checkpoint(a, checkpoint);
     if (d_output) a.dout = make_view(d_output);
     a.dq = dq;
     a.dk = dk;
@@ -475,6 +514,12 @@ int gdn2_backward(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *
     a.dalpha = dalpha;
     a.derase = derase;
     a.dwrite = dwrite;
+    if (use_fc_path(shape, q)) {
+        const FcArgs f = fc_args(a, const_cast<void *>(checkpoint), workspace);
+        const hipEvent_t *ev = stage_events(3, (hipStream_t)stream);
+        return launch_status(launch_fc_bwd(f, (hipStream_t)stream, ev), "gdn2_backward");
+    }
+    seq_bind_checkpoint(a, checkpoint);
     a.replay = (float *)workspace;
     return launch_status(launch_seq_bwd(a, q->dtype == GDN2_BF16, (hipStream_t)stream),
                          "gdn2_backward");

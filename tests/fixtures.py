@@ -12,6 +12,8 @@ the GPU path consume identical numbers.
                           initial_data, score_seed, objectives 0..3)
   reset_padding_fixture() crates/mixers/src/chunk_tests.rs:25-75 (B2/T5/H2/K3/V4)
   dre_tokens(n, seed)     reuse/crates/dre-gdn2/src/tests.rs:35-51 (SplitMix tokens)
+  kron_raw(b, t, seed)    crates/experiment/src/kron_benchmark.rs:73-116 (the isolated-scan
+                          benchmark fixture, GDN-2 widths)
 """
 from __future__ import annotations
 
@@ -200,3 +202,43 @@ def dre_tokens(n: int, seed: int = 7, K: int = 32, V: int = 64):
         for name, width, center, spread in spec:
             fields[name].append([center + spread * rng.signed() for _ in range(width)])
     return {name: np.asarray(x, dtype=F32).reshape(1, n, 1, -1) for name, x in fields.items()}
+
+
+def splitmix_block(seed: int, n: int) -> np.ndarray:
+    """The first n outputs of SplitMix64 from seed (data.rs:13-21), vectorized:
+    the state after step j is seed + j * 0x9E3779B97F4A7C15 (mod 2^64)."""
+    with np.errstate(over="ignore"):
+        j = np.arange(1, n + 1, dtype=np.uint64)
+        z = np.uint64(seed) + j * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def kron_raw(b: int, t: int, seed: int = 1, h: int = 4) -> Fixture:
+    """The reference's isolated-scan benchmark fixture (kron_benchmark.rs:73-116,
+    GDN-2 widths K32/V64): one SplitMix64 stream drawn field by field; x = the top
+    24 bits / 2^24; q, k, v = x - 0.5 with every row scaled to unit norm; alpha =
+    0.90 + 0.09 x; erase and write = 0.1 + 0.8 x; all valid, no resets, zero
+    initial state, all-ones upstream gradient."""
+    widths = [32, 32, 64, 32, 32, 64]
+    n = b * t * h * sum(widths)
+    x = ((splitmix_block(seed, n) >> np.uint64(40)).astype(np.float32)
+         / np.float32(1 << 24))
+    out, off = [], 0
+    for field, w in enumerate(widths):
+        f = x[off:off + b * t * h * w].reshape(b, t, h, w)
+        off += b * t * h * w
+        if field == 3:
+            f = np.float32(0.90) + np.float32(0.09) * f
+        elif field >= 4:
+            f = np.float32(0.1) + np.float32(0.8) * f
+        else:
+            f = f - np.float32(0.5)
+            f = f / np.sqrt((f * f).sum(-1, keepdims=True, dtype=np.float32))
+        out.append(f.astype(np.float32))
+    return Fixture(q=out[0], k=out[1], v=out[2], alpha=out[3], erase=out[4], write=out[5],
+                   valid=np.ones((b, t), np.uint8), reset=np.zeros((b, t), np.uint8),
+                   initial=np.zeros((b, h, 32, 64), np.float32),
+                   upstream=np.ones((b, t, h, 64), np.float32), final_adjoint=None,
+                   score_adjoint=None)

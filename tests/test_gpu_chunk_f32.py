@@ -1,0 +1,145 @@
+"""The f32 chunk kernels (csrc/gdn2_chunk_f32.hip): channel-wise GDN-2 with f32
+q/k/v and d_k, d_v <= 64, in 16-token chunks, against the f64 oracle.
+
+1. The reference's isolated-scan benchmark workload (kron_benchmark.rs:73-116:
+   B8 T512 H4 K32 V64, alpha in [0.90, 0.99], erase/write in [0.1, 0.9], unit
+   rows, all-ones upstream gradient) with the stage timers on: the six chunk
+   stages run, and every output and gradient passes the 1e-4 gate and the
+   reference's own gate 2e-5 + 3e-4|ref| (kron_checks.rs:34-35).
+2. The reference's GDN gate fixture (kron_checks.rs:89-524) at T = 35, all
+   four objectives, through the chunk kernels (stage timers), at both gates.
+   The fixture zeroes alpha on one channel at p = 2 and on every channel at
+   p = 16, so the exact alpha gradient at alpha = 0 is gated too.
+3. Gates the chunk kernels handle with no special case, because they form every
+   decay as a product of the gates: negative alpha, alpha = 0 on a whole
+   chunk, tiny alpha; and ragged widths (d_k, d_v in 1..64) with padding and
+   resets inside chunks and sequence ends off the chunk grid.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import fixtures as fx  # noqa: E402
+from gpu_util import TOL_F32, dev, gate  # noqa: E402
+from oracle import oracle  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+GROUPS = ("q", "k", "v", "alpha", "erase", "write")
+STAGES = {"chunk_prep", "state_scan", "chunk_out", "chunk_bprep", "adjoint_scan", "chunk_bgrad"}
+
+
+@pytest.fixture(scope="module")
+def dk():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import delta_kernels
+    delta_kernels.lib()
+    return delta_kernels
+
+
+def run_and_check(dk, f, ref_gate=True, chunk=16):
+    """Forward + backward through gdn_training_scan with the stage timers on,
+    every output and gradient gated against the f64 oracle; returns the stages
+    that ran."""
+    xs = {n: dev(f[n]).requires_grad_(True) for n in GROUPS}
+    init = dev(f.initial).requires_grad_(True) if f.initial is not None else None
+    dk.stage_timing(True)
+    try:
+        r = dk.gdn_training_scan(xs["q"], xs["k"], xs["v"], xs["alpha"], xs["erase"],
+                                 xs["write"], dev(f.valid), dev(f.reset), init, chunk)
+        loss = (r.output * dev(f.upstream)).sum()
+        if f.final_adjoint is not None:
+            loss = loss + (r.final_state * dev(f.final_adjoint)).sum()
+        if f.score_adjoint is not None:
+            loss = loss + (r.scores[..., 0] * dev(f.score_adjoint)).sum()
+        loss.backward()
+        torch.cuda.synchronize()
+        ran = set(dk.stage_times())
+    finally:
+        dk.stage_timing(False)
+    out, fin, sc = oracle.scan(f.q, f.k, f.v, f.alpha, f.erase, f.write, f.valid, f.reset,
+                               f.initial)
+    g = oracle.backward(f.q, f.k, f.v, f.alpha, f.erase, f.write, f.valid, f.reset, f.initial,
+                        f.upstream, f.final_adjoint, f.score_adjoint)
+    pad = (f.valid == 0)[:, :, None, None]
+    gate("output", r.output, out, TOL_F32, exact_zero=pad, ref_gate=ref_gate)
+    gate("final_state", r.final_state, fin, TOL_F32, ref_gate=ref_gate)
+    gate("scores", r.scores[..., 0], sc, TOL_F32, exact_zero=pad[..., 0], ref_gate=ref_gate)
+    for n in GROUPS:
+        gate(f"d{n}", xs[n].grad, g[n], TOL_F32, exact_zero=pad, ref_gate=ref_gate)
+    if init is not None:
+        gate("d_initial", init.grad, g["initial"], TOL_F32, ref_gate=ref_gate)
+    return ran, g
+
+
+def test_reference_benchmark_workload(dk):
+    f = fx.kron_raw(8, 512)
+    print("f32 chunk: kron_raw B8 T512 H4 K32 V64", flush=True)
+    ran, _ = run_and_check(dk, f)
+    assert STAGES <= ran, sorted(ran)
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+def test_gate_fixture_runs_chunk_kernels(dk, mode):
+    f = fx.gate_fixture(35, mode)
+    assert (f.alpha[:, 2, :, 0] == 0).all() and (f.alpha[:, 16] == 0).all()
+    ran, g = run_and_check(dk, f)
+    assert STAGES <= ran, sorted(ran)
+    if mode != 2:  # the final state does not depend on p = 16 (resets at 19, padding from 16)
+        assert np.abs(g["alpha"][:, 16]).max() > 0  # the gradient at alpha = 0 is not zero
+
+
+def _random(seed, B, T, H, K, V, alpha=(0.8, 1.0), masks=True):
+    rng = np.random.default_rng(seed)
+    k = rng.normal(size=(B, T, H, K))
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    valid = np.ones((B, T), np.uint8)
+    reset = np.zeros((B, T), np.uint8)
+    if masks:
+        valid[0, 5:9] = 0
+        valid[-1, T - 3:] = 0
+        reset[0, [p for p in (0, 13, 40) if p < T]] = 1
+        reset[-1, [p for p in (2, 17, 18) if p < T]] = 1
+        if T > 18:
+            valid[-1, 18] = 0  # a reset on a padding token does nothing
+    return fx.Fixture(
+        q=(rng.normal(size=(B, T, H, K)) * 0.3).astype(np.float32), k=k.astype(np.float32),
+        v=rng.normal(size=(B, T, H, V)).astype(np.float32),
+        alpha=rng.uniform(*alpha, size=(B, T, H, K)).astype(np.float32),
+        erase=rng.uniform(0.2, 0.9, size=(B, T, H, K)).astype(np.float32),
+        write=rng.uniform(0.2, 0.9, size=(B, T, H, V)).astype(np.float32),
+        valid=valid, reset=reset,
+        initial=(rng.normal(size=(B, H, K, V)) * 0.1).astype(np.float32),
+        upstream=rng.normal(size=(B, T, H, V)).astype(np.float32),
+        final_adjoint=(rng.normal(size=(B, H, K, V)) * 0.1).astype(np.float32),
+        score_adjoint=(rng.normal(size=(B, T, H)) * 0.1).astype(np.float32))
+
+
+@pytest.mark.parametrize("K,V,T", [(1, 1, 19), (3, 4, 33), (17, 64, 50), (64, 33, 64),
+                                   (64, 64, 77), (32, 64, 130)])
+def test_ragged_widths(dk, K, V, T):
+    f = _random(K * 100 + V, 2, T, 3, K, V)
+    print(f"f32 chunk: widths K{K} V{V} T{T}", flush=True)
+    ran, _ = run_and_check(dk, f, ref_gate=False)
+    assert STAGES <= ran, sorted(ran)
+
+
+def test_negative_alpha(dk):
+    """alpha in [-1, 1]: the decays are signed products; the f32 chunk kernels
+    take them exactly (the bf16 chunk kernels refuse them with NaN)."""
+    f = _random(5, 2, 70, 2, 32, 64, alpha=(-1.0, 1.0))
+    ran, _ = run_and_check(dk, f, ref_gate=False)
+    assert STAGES <= ran
+
+
+def test_zero_and_tiny_alpha(dk):
+    """alpha = 0 over a whole chunk of one head, one channel at 1e-30 over
+    another chunk, 1e-3..1e-2 elsewhere in that sequence."""
+    f = _random(6, 2, 64, 2, 32, 64)
+    f.alpha[0, 16:32, 0] = 0.0
+    f.alpha[0, 32:48, 1, 3] = 1e-30
+    f.alpha[1, :, 0] = np.random.default_rng(1).uniform(1e-3, 1e-2, size=(64, 32))
+    _, g = run_and_check(dk, f, ref_gate=False)
+    assert np.abs(g["alpha"][0, 16:32, 0]).max() > 0

@@ -15,7 +15,9 @@
    GPU kernels compute it (crates/kernels/src/gdn2.rs:24-65, :288-490); the
    reference's f64 oracle lets the adjoint cross that reset instead.
 4. bf16 with K = V = 64 runs the 16-token chunk-WY MFMA kernels (stage
-   timers), f32 and other widths the token-sequential kernels.
+   timers); f32 with K, V <= 64 (items 1 and 2 at K32/V64 and K = V = 64) the
+   f32 chunk kernels; bf16 at other widths and K = V = 128 the
+   token-sequential kernels.
 """
 import numpy as np
 import pytest
