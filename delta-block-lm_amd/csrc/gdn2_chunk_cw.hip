@@ -955,7 +955,7 @@ __device__ __forceinline__ void load_tt_split(const float *ckt, uint16_t *th, ui
 __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
     __shared__ CwBGradSmem sm;
     static_assert(sizeof(CwBGradSmem) <= 80 * 1024, "two workgroups per CU");
-    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = lane_id();
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid >> 4, c0 = 4 * (tid & 15), t0 = c * CC, tg = t0 + t;
     const bool inb = tg < a.T;

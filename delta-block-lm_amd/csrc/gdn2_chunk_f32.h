@@ -18,8 +18,10 @@ inline bool fc_eligible_shape(const gdn2_shape *s) {
 //   st     S at the chunk start, [K][V]                 (forward scan -> out, bgrad)
 //   tm     T = (I + A)^-1, [16][16]                       (prep -> out, bgrad)
 //   dl     the edits delta, [16][V]                       (out -> bprep, bgrad)
-//   fw, fk the factored map: W' = T (b . e . k) and Ktil = lam . k, [16][K] each
-//   fu     U = T (w . v), [16][V];  gv  b_15 (the map's diagonal), [K]
+//   fw, fk the factored map: W' = T (b . e . k) and Ktil = lam . k, [16][KP] each
+//   fu     U = T (w . v), [16][V];  gv  b_15 (the map's diagonal), [KP]
+// KP = d_k rounded up to 16: the key axis of the map's factors is padded with
+// zeros to whole 16-row MFMA tiles for the scans.
 // Backward workspace: ds, the state adjoint at each chunk end, and n, the
 // adjoint map's additive term, [K][V] each.
 struct FcArgs {
@@ -30,9 +32,10 @@ struct FcArgs {
 };
 
 inline int64_t fc_chunks(int64_t B, int64_t T, int64_t H) { return B * H * ((T + FC_C - 1) / FC_C); }
+__host__ __device__ inline int fc_kp(int K) { return (K + 15) & ~15; }
 
 inline size_t fc_chunk_floats(int K, int V) {
-    return (size_t)K * V + FC_C * FC_C + FC_C * V + 2 * FC_C * K + FC_C * V + K;
+    return (size_t)K * V + FC_C * FC_C + FC_C * V + 2 * FC_C * fc_kp(K) + FC_C * V + fc_kp(K);
 }
 
 inline size_t fc_checkpoint_bytes(int64_t B, int64_t T, int64_t H, int K, int V) {
@@ -54,9 +57,9 @@ inline void fc_bind(FcArgs &a, void *ck, void *ws) {
     a.dl = p;
     p += n * FC_C * V;
     a.fw = p;
-    p += n * FC_C * K;
+    p += n * FC_C * fc_kp(K);
     a.fk = p;
-    p += n * FC_C * K;
+    p += n * FC_C * fc_kp(K);
     a.fu = p;
     p += n * FC_C * V;
     a.gv = p;

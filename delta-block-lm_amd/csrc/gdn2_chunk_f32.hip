@@ -25,6 +25,7 @@
 // one 256-thread workgroup per chunk, thread (token t = tid / 16, channels
 // 4 (tid % 16) .. + 3) for the [token][channel] tiles.
 #include "gdn2_chunk_f32.h"
+#include "gdn2_mfma.h"
 
 #include <algorithm>
 
@@ -221,16 +222,19 @@ __global__ void __launch_bounds__(NT) fc_prep_kernel(FcArgs a) {
         for (int r = 0; r < C; ++r) sm.T[r * LT + j] = tc[r];
     }
     __syncthreads();
-    // W' = T (b . ehat), U = T wv, Ktil = lam . k: token t, channels 4g .. 4g + 3.
+    // W' = T (b . ehat), U = T wv, Ktil = lam . k: token t, channels 4g .. 4g + 3;
+    // W', Ktil and gv zero on the key padding up to KP.
+    const int KP = fc_kp(K);
     const int64_t fo = (int64_t)ci * C;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int i = 4 * g + e;
-        if (i < K) {
+        if (i < KP) {
             float wsum = 0.f;
-            for (int q = 0; q <= t; ++q) wsum += sm.T[t * LT + q] * sm.bt[q * LQ + i] * sm.eh[q * LQ + i];
-            a.fw[(fo + t) * K + i] = wsum;
-            a.fk[(fo + t) * K + i] = sm.lam[t * LQ + i] * sm.k[t * LQ + i];
+            if (i < K)
+                for (int q = 0; q <= t; ++q) wsum += sm.T[t * LT + q] * sm.bt[q * LQ + i] * sm.eh[q * LQ + i];
+            a.fw[(fo + t) * KP + i] = wsum;
+            a.fk[(fo + t) * KP + i] = i < K ? sm.lam[t * LQ + i] * sm.k[t * LQ + i] : 0.f;
         }
         if (i < V) {
             float usum = 0.f;
@@ -238,121 +242,125 @@ __global__ void __launch_bounds__(NT) fc_prep_kernel(FcArgs a) {
             a.fu[(fo + t) * V + i] = usum;
         }
     }
-    if (tid < K) a.gv[(int64_t)ci * K + tid] = sm.bt[(C - 1) * LQ + tid];
+    if (tid < KP) a.gv[(int64_t)ci * KP + tid] = tid < K ? sm.bt[(C - 1) * LQ + tid] : 0.f;
     a.tm[(int64_t)ci * C * C + tid] = sm.T[(tid >> 4) * LT + (tid & 15)];
 }
 
 // ---- the scan over the chunks of one (batch, head) -----------------------------
-// One wave per (batch, head, group of 16 value columns): lane (column jl = l % 16,
-// quarter kq = l / 16) holds the state rows i = 4 r + kq of its column.  Per
-// chunk, forward:   v_t = U_t - W'_t . S,      S <- diag(gv) S + Ktil^T v
-//         reverse:  v_t = Ktil_t . X,          X <- diag(gv) X + N - W'^T v
-// (the sums over i across the four quarters by two lane shuffles).  The state
-// before each chunk (forward) or after it (reverse) goes to the checkpoint or
-// workspace.  The next chunk's factors are loaded into registers while the
-// current one computes.
-template <bool REV>
+// One wave per (batch, head, 16 value columns j = 16 cg + l % 16), on
+// v_mfma_f32_16x16x4f32 (exact f32 products).  The state's key axis is cut
+// into KT tiles of 16 rows; tile tau lives in the accumulator layout: lane l
+// (g = l / 16, n = l % 16) holds S[16 tau + 4 g + r][16 cg + n] in register r.
+// Per chunk, forward:  v = U - W' S,          S <- diag(gv) S + Ktil^T v
+//            reverse:  v = Ktil X,            X <- diag(gv) X + N - W'^T v
+// Each product's 16-long reduction runs as four k = 4 MFMA steps s whose
+// k-slice is {4 g + s}: the B operand of step s is then register s of the
+// lane's own accumulator tile (rows 4 g + s of S or X, rows 4 g + s of v), so
+// no value changes lanes; the A operand is the matching element of W' or Ktil,
+// read from global memory into registers one chunk ahead.
+template <int KT>
+struct FcScanOps {
+    float w[KT][4], k[KT][4], g[KT][4], a[KT][4];  // A operands, gv rows, U or N
+};
+
+template <int KT, bool REV>
+__device__ __forceinline__ void fc_scan_load(const FcArgs &a, int64_t ci, int cg, FcScanOps<KT> &o) {
+    const int K = a.s.K, V = a.s.V, KP = 16 * KT, l = lane_id(), g = l >> 4, n = l & 15, j = 16 * cg + n;
+    const float *fw = a.fw + ci * C * KP, *fk = a.fk + ci * C * KP;
+#pragma unroll
+    for (int tau = 0; tau < KT; ++tau)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            // the operand (token l % 16, key 16 tau + 4 g + s) and (token 4 g + s, key 16 tau + l % 16)
+            const float rowk = (REV ? fk : fw)[n * KP + 16 * tau + 4 * g + s];
+            const float colk = (REV ? fw : fk)[(4 * g + s) * KP + 16 * tau + n];
+            o.w[tau][s] = REV ? rowk : -rowk;
+            o.k[tau][s] = REV ? -colk : colk;
+            o.g[tau][s] = a.gv[ci * KP + 16 * tau + 4 * g + s];
+            if (REV) {
+                const int i = 16 * tau + 4 * g + s;
+                o.a[tau][s] = (i < K && j < V) ? a.n[(ci * K + i) * V + j] : 0.f;
+            } else {
+                o.a[tau][s] = (tau == 0 && j < V) ? a.fu[(ci * C + 4 * g + s) * V + j] : 0.f;
+            }
+        }
+}
+
+template <int KT, bool REV>
 __global__ void __launch_bounds__(64) fc_scan_kernel(FcArgs a) {
-    __shared__ float fw[C * FK], fk[C * FK], gv[FK];
     const SeqArgs &s = a.s;
     const int K = s.K, V = s.V, ng = (V + 15) / 16;
     const int wg = blockIdx.x, bh = wg / ng, cg = wg % ng, b = bh / s.H, h = bh % s.H;
-    const int l = threadIdx.x, jl = l & 15, kq = l >> 4, j = 16 * cg + jl;
+    const int l = lane_id(), g = l >> 4, n = l & 15, j = 16 * cg + n;
     const bool jv = j < V;
-    const int nf = C * K;  // floats of one factor per chunk
-    float X[16];
+    f32x4 X[KT];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int i = 4 * r + kq;
-        float x = 0.f;
-        if (i < K && jv) {
-            if (!REV) x = s.initial.data ? ld4<float>(s.initial, b, h, i, j) : 0.f;
-            else x = s.dfinal ? s.dfinal[((int64_t)bh * K + i) * V + j] : 0.f;
-        }
-        X[r] = x;
-    }
-    // prefetch registers: this lane's share of W', Ktil (up to 16 + 16 floats),
-    // gv (1), and the column's U (forward) or N (reverse) rows
-    float pw[16], pk[16], pg = 0.f, pa[16];
-    auto fetch = [&](int step) {
-        const int c = REV ? a.nc - 1 - step : step;
-        const int64_t ci = (int64_t)bh * a.nc + c;
+    for (int tau = 0; tau < KT; ++tau)
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int e = l + 64 * q;
-            pw[q] = e < nf ? a.fw[ci * nf + e] : 0.f;
-            pk[q] = e < nf ? a.fk[ci * nf + e] : 0.f;
-        }
-        pg = l < K ? a.gv[ci * K + l] : 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            if (!REV) pa[r] = (r < C && jv) ? a.fu[(ci * C + r) * V + j] : 0.f;
-            else {
-                const int i = 4 * r + kq;
-                pa[r] = (i < K && jv) ? a.n[(ci * K + i) * V + j] : 0.f;
+        for (int r = 0; r < 4; ++r) {
+            const int i = 16 * tau + 4 * g + r;
+            float x = 0.f;
+            if (i < K && jv) {
+                if (!REV) x = s.initial.data ? ld4<float>(s.initial, b, h, i, j) : 0.f;
+                else x = s.dfinal ? s.dfinal[((int64_t)bh * K + i) * V + j] : 0.f;
             }
+            X[tau][r] = x;
         }
-    };
-    fetch(0);
+    FcScanOps<KT> cur, nxt;
+    fc_scan_load<KT, REV>(a, (int64_t)bh * a.nc + (REV ? a.nc - 1 : 0), cg, cur);
+    float *keep = REV ? a.ds : a.st;
     for (int step = 0; step < a.nc; ++step) {
         const int c = REV ? a.nc - 1 - step : step;
         const int64_t ci = (int64_t)bh * a.nc + c;
-        __syncthreads();  // the previous step's reads of the factor tiles are done
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int e = l + 64 * q;
-            if (e < nf) {
-                fw[e] = pw[q];
-                fk[e] = pk[q];
-            }
-        }
-        if (l < K) gv[l] = pg;
-        float ad[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) ad[r] = pa[r];
-        __syncthreads();
-        if (step + 1 < a.nc) fetch(step + 1);
+        if (step + 1 < a.nc) fc_scan_load<KT, REV>(a, ci + (REV ? -1 : 1), cg, nxt);
         // the state before (forward) / the adjoint after (reverse) this chunk
-        float *out = REV ? a.ds : a.st;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = 4 * r + kq;
-            if (i < K && jv) out[(ci * K + i) * V + j] = X[r];
-        }
-        float vt[C];
+        for (int tau = 0; tau < KT; ++tau)
 #pragma unroll
-        for (int t = 0; t < C; ++t) {
-            const float *row = REV ? fk : fw;
-            float p = 0.f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int i = 4 * r + kq;
-                if (i < K) p += row[t * K + i] * X[r];
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * tau + 4 * g + r;
+                if (i < K && jv) keep[(ci * K + i) * V + j] = X[tau][r];
             }
-            p += __shfl_xor(p, 16);
-            p += __shfl_xor(p, 32);
-            vt[t] = REV ? p : ad[t] - p;
-        }
+        // v[t][j], t = 4 g + r: U - W' S (forward) or Ktil X (reverse)
+        f32x4 v = REV ? zero4() : f32x4{cur.a[0][0], cur.a[0][1], cur.a[0][2], cur.a[0][3]};
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = 4 * r + kq;
-            if (i < K) {
-                float x = gv[i] * X[r] + (REV ? ad[r] : 0.f);
-                const float *col = REV ? fw : fk;
-                float u = 0.f;
+        for (int tau = 0; tau < KT; ++tau)
 #pragma unroll
-                for (int t = 0; t < C; ++t) u += col[t * K + i] * vt[t];
-                X[r] = REV ? x - u : x + u;
-            }
+            for (int q = 0; q < 4; ++q)
+                v = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.w[tau][q], X[tau][q], v, 0, 0, 0);
+        // S <- diag(gv) S (+ N) + Ktil^T v, or X <- diag(gv) X + N - W'^T v
+#pragma unroll
+        for (int tau = 0; tau < KT; ++tau) {
+            f32x4 x;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x[r] = cur.g[tau][r] * X[tau][r] + (REV ? cur.a[tau][r] : 0.f);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                x = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.k[tau][q], v[q], x, 0, 0, 0);
+            X[tau] = x;
         }
+        cur = nxt;
     }
     float *fin = REV ? s.dinitial : s.final_state;
     if (fin)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = 4 * r + kq;
-            if (i < K && jv) fin[((int64_t)bh * K + i) * V + j] = X[r];
-        }
+        for (int tau = 0; tau < KT; ++tau)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * tau + 4 * g + r;
+                if (i < K && jv) fin[((int64_t)bh * K + i) * V + j] = X[tau][r];
+            }
+}
+
+template <bool REV>
+static void launch_fc_scan(const FcArgs &a, hipStream_t stream) {
+    const dim3 grid(a.s.B * a.s.H * ((a.s.V + 15) / 16)), block(64);
+    switch (fc_kp(a.s.K) / 16) {
+        case 1: hipLaunchKernelGGL((fc_scan_kernel<1, REV>), grid, block, 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((fc_scan_kernel<2, REV>), grid, block, 0, stream, a); break;
+        case 3: hipLaunchKernelGGL((fc_scan_kernel<3, REV>), grid, block, 0, stream, a); break;
+        default: hipLaunchKernelGGL((fc_scan_kernel<4, REV>), grid, block, 0, stream, a); break;
+    }
 }
 
 // ---- out: edits, outputs, scores ----------------------------------------------
@@ -470,7 +478,7 @@ __global__ void __launch_bounds__(NT) fc_bprep_kernel(FcArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int i = 4 * g + e;
-        sm.w[t * LQ + i] = i < K ? a.fw[((int64_t)ci * C + t) * K + i] : 0.f;
+        sm.w[t * LQ + i] = i < K ? a.fw[((int64_t)ci * C + t) * fc_kp(K) + i] : 0.f;
     }
     __syncthreads();
     // X = P^T dO + c delta (token t, columns 4g ..)
@@ -704,12 +712,12 @@ static inline void fmark(const hipEvent_t *ev, int i, hipStream_t stream) {
 }
 
 hipError_t launch_fc_fwd(const FcArgs &a, hipStream_t stream, const hipEvent_t *ev) {
-    const int n = a.s.B * a.s.H * a.nc, ng = (a.s.V + 15) / 16;
+    const int n = a.s.B * a.s.H * a.nc;
     fmark(ev, 0, stream);
     hipLaunchKernelGGL(fc_prep_kernel, dim3(n), dim3(NT), 0, stream, a);
     fmark(ev, 1, stream);
     fmark(ev, 2, stream);
-    hipLaunchKernelGGL(fc_scan_kernel<false>, dim3(a.s.B * a.s.H * ng), dim3(64), 0, stream, a);
+    launch_fc_scan<false>(a, stream);
     fmark(ev, 3, stream);
     fmark(ev, 4, stream);
     hipLaunchKernelGGL(fc_out_kernel, dim3(n), dim3(NT), 0, stream, a);
@@ -718,12 +726,12 @@ hipError_t launch_fc_fwd(const FcArgs &a, hipStream_t stream, const hipEvent_t *
 }
 
 hipError_t launch_fc_bwd(const FcArgs &a, hipStream_t stream, const hipEvent_t *ev) {
-    const int n = a.s.B * a.s.H * a.nc, ng = (a.s.V + 15) / 16;
+    const int n = a.s.B * a.s.H * a.nc;
     fmark(ev, 0, stream);
     hipLaunchKernelGGL(fc_bprep_kernel, dim3(n), dim3(NT), 0, stream, a);
     fmark(ev, 1, stream);
     fmark(ev, 2, stream);
-    hipLaunchKernelGGL(fc_scan_kernel<true>, dim3(a.s.B * a.s.H * ng), dim3(64), 0, stream, a);
+    launch_fc_scan<true>(a, stream);
     fmark(ev, 3, stream);
     fmark(ev, 4, stream);
     hipLaunchKernelGGL(fc_bgrad_kernel, dim3(n), dim3(NT), 0, stream, a);

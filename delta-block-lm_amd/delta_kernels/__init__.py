@@ -20,8 +20,8 @@ import torch
 
 from ._lib import GDN2_BF16, GDN2_F32, GDN2_I32, Gdn2Shape, Gdn2View, check, lib
 
-__all__ = ["GdnTrainingOutput", "gdn_training_scan", "gdn_training_backward", "gdn2_scan",
-           "gdn2_scan_forward", "gdn2_backward",
+__all__ = ["GdnTrainingOutput", "gdn_training_scan", "gdn_training_forward",
+           "gdn_training_backward", "gdn2_scan", "gdn2_scan_forward", "gdn2_backward",
            "gdn_scalar_scan", "gdn_scalar_forward", "gdn_scalar_backward", "gdn_decode_step",
            "stage_timing", "stage_times", "lib"]
 
@@ -108,6 +108,13 @@ def _check_shapes(q, k, v, gates, valid, reset, initial):
 
 
 # ---- channel-wise training scan ---------------------------------------------------
+
+
+def gdn_training_forward(q, k, v, alpha, erase, write, valid, reset, initial, chunk):
+    """Raw forward (crates/kernels/src/gdn_training_ops.rs:27-48).  Returns
+    (output, final_state, scores, checkpoint); the checkpoint feeds
+    gdn_training_backward."""
+    return _training_forward(q, k, v, alpha, erase, write, valid, reset, initial, chunk)
 
 
 def _training_forward(q, k, v, alpha, erase, write, valid, reset, initial, chunk):

@@ -109,3 +109,32 @@ def generate(cfg: Config, seed: int = 0) -> dict:
             out["d_output"] = round_bf16(out["d_output"])
     out["q"], out["k"], out["v"] = q, k, v
     return out
+
+
+def kron_benchmark_inputs(batch: int, time: int, seed: int = 1, heads: int = 4) -> dict:
+    """The reference's isolated-scan benchmark inputs for GDN-2
+    (crates/experiment/src/kron_benchmark.rs:73-116; default seed 1,
+    crates/experiment/src/config.rs:405): one SplitMix64 stream drawn field by
+    field, widths q, k 32, v 64, alpha, erase 32, write 64; x = (output >> 40) /
+    2^24; q, k, v = x - 0.5 with every row scaled to unit norm; alpha = 0.90 +
+    0.09 x; erase, write = 0.1 + 0.8 x.  All tokens valid, no resets, zero
+    initial state [B, H, 32, 64] and an all-ones upstream gradient.  f32."""
+    widths = (32, 32, 64, 32, 32, 64)
+    names = ("q", "k", "v", "alpha", "erase", "write")
+    total = batch * time * heads * sum(widths)
+    x = (splitmix_outputs(seed, 0, total) >> np.uint64(40)).astype(np.float32) / np.float32(1 << 24)
+    out, off = {}, 0
+    for field, (name, w) in enumerate(zip(names, widths)):
+        f = x[off:off + batch * time * heads * w].reshape(batch, time, heads, w)
+        off += batch * time * heads * w
+        if field == 3:
+            f = np.float32(0.90) + np.float32(0.09) * f
+        elif field >= 4:
+            f = np.float32(0.1) + np.float32(0.8) * f
+        else:
+            f = f - np.float32(0.5)
+            f = f / np.sqrt((f * f).sum(-1, keepdims=True, dtype=np.float32))
+        out[name] = np.ascontiguousarray(f, dtype=np.float32)
+    out["initial"] = np.zeros((batch, heads, 32, 64), np.float32)
+    out["d_output"] = np.ones((batch, time, heads, 64), np.float32)
+    return out
