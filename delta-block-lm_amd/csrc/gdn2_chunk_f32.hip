@@ -174,10 +174,17 @@ struct FcBPrepSmem {
 
 struct FcBGradSmem {
     Masks m;
-    float q[C * LQ], k[C * LQ], v[C * LQ], al[C * LQ], e[C * LQ], w[C * LQ], eh[C * LQ], dO[C * LQ];
-    float dl[C * LQ], dd[C * LQ], dr[C * LQ], bt[C * LQ], lam[C * LQ];
-    float ga[C * LQ], gq[C * LQ], gk[C * LQ];  // dAhat, dQhat, dKtil [token][key]
-    float s0[FK * LS], ds[FK * LS];
+    float q[C * LQ], k[C * LQ], e[C * LQ], al[C * LQ], dO[C * LQ], dl[C * LQ], dr[C * LQ];
+    float bt[C * LQ], lam[C * LQ];
+    union {
+        struct {
+            float s0[FK * LS], ds[FK * LS];  // S0 and dS, zero-padded to whole 16 x 16 tiles
+        } st;
+        struct {
+            float ga[C * LQ], gq[C * LQ], gk[C * LQ];  // dAhat, dQhat, dKtil [token][key]
+            float part[4 * C * 64];  // dalpha partials: 4 rpw groups x C rows x 64 / rpw channels
+        } gr;
+    } u;
     float T[C * LT], P[C * LT], dA[C * LT], dP[C * LT];
     float cs[C], ck[C], fs[FK];
 };
@@ -515,6 +522,8 @@ __global__ void __launch_bounds__(NT) fc_bprep_kernel(FcArgs a) {
 //   ddelta = P^T dO + Ktil dS + c delta,  dR = T^T ddelta,  dw = dR.v,  dv = dR.w
 //   dAhat = -dR S0^T,  dQhat = dO S0^T,  dKtil = delta dS^T
 //   dA = -strict_lower(dR delta^T),  dP = lower(dO delta^T)   (same segment)
+// on v_mfma_f32_16x16x4f32 (wave w takes value tile w in the first group, the
+// 16 x 16 output tiles in turn in the second); then per key channel on the VALU
 //   eA_t = sum_s dA_ts D_ts k_s,  qP_t = sum_s dP_ts D_ts k_s,
 //   kAP_s = sum_t (dA_ts ehat_t + dP_ts q_t) D_ts
 //   dq = b dQhat + qP;  dehat = b dAhat + eA;  de = k dehat;
@@ -523,12 +532,15 @@ __global__ void __launch_bounds__(NT) fc_bprep_kernel(FcArgs a) {
 // coefficient times the product of the gates over (lo, hi] without u (interior
 // pairs (dA_ts ehat_t + dP_ts q_t) k_s; start pairs ehat_t dAhat_t + q_t dQhat_t
 // through b_t; end pairs k_s dKtil_s through lam_s; rowsum(S0 . dS) through
-// b_15): exact for zero and negative gates.
+// b_15): sum_{lo < u} L(lo, u) Y(u, lo) with L the gates over (lo, u) and Y by
+// Horner over hi, exact for zero and negative gates.
 __global__ void __launch_bounds__(NT) fc_bgrad_kernel(FcArgs a) {
     __shared__ FcBGradSmem sm;
     const SeqArgs &s = a.s;
     const int tid = threadIdx.x, ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / s.H, h = bh % s.H;
     const int K = s.K, V = s.V, t = tid >> 4, g = tid & 15, tg = c * C + t;
+    const int KT = (K + 15) >> 4, VT = (V + 15) >> 4, VP = 16 * VT;
+    const int w = tid >> 6, l = tid & 63, lg = l >> 4, ln = l & 15;
     fc_masks(s, b, c, sm.m, tid);
     const bool on = sm.m.val[t] != 0.f;
     const bool score_adj = s.dscores != nullptr;
@@ -537,14 +549,10 @@ __global__ void __launch_bounds__(NT) fc_bgrad_kernel(FcArgs a) {
     for (int e = 0; e < 4; ++e) {
         const int i = 4 * g + e;
         const float kv = fc_in(s.k, b, tg, h, i, s.T, K, on);
-        const float ev = fc_in(s.erase, b, tg, h, i, s.T, K, on);
         sm.q[t * LQ + i] = fc_in(s.q, b, tg, h, i, s.T, K, on);
         sm.k[t * LQ + i] = kv;
-        sm.e[t * LQ + i] = ev;
-        sm.eh[t * LQ + i] = ev * kv;
+        sm.e[t * LQ + i] = fc_in(s.erase, b, tg, h, i, s.T, K, on);
         sm.al[t * LQ + i] = (on && i < K) ? ld4<float>(s.alpha, b, tg, h, i) : 1.f;
-        sm.v[t * LQ + i] = fc_in(s.v, b, tg, h, i, s.T, V, on);
-        sm.w[t * LQ + i] = fc_in(s.write, b, tg, h, i, s.T, V, on);
         sm.dO[t * LQ + i] = (s.dout.data && on && tg < s.T && i < V) ? ld4<float>(s.dout, b, tg, h, i) : 0.f;
         const float d = i < V ? a.dl[((int64_t)ci * C + t) * V + i] : 0.f;
         sm.dl[t * LQ + i] = d;
@@ -562,148 +570,203 @@ __global__ void __launch_bounds__(NT) fc_bgrad_kernel(FcArgs a) {
     }
     {
         const float *st = a.st + (int64_t)ci * K * V, *ds = a.ds + (int64_t)ci * K * V;
-        for (int e = tid; e < K * V; e += NT) {
-            sm.s0[(e / V) * LS + e % V] = st[e];
-            sm.ds[(e / V) * LS + e % V] = ds[e];
+        const int KP = 16 * KT;
+        for (int e = tid; e < KP * VP; e += NT) {
+            const int i = e / VP, j = e - i * VP;
+            const bool in = i < K && j < V;
+            sm.u.st.s0[i * LS + j] = in ? st[i * V + j] : 0.f;
+            sm.u.st.ds[i * LS + j] = in ? ds[i * V + j] : 0.f;
         }
     }
     sm.T[(tid >> 4) * LT + (tid & 15)] = a.tm[(int64_t)ci * C * C + tid];
     __syncthreads();
     fc_decay_rows(sm.al, sm.m, sm.bt, sm.lam, K, tid);
     fc_tri<false>(sm.q, sm.k, sm.al, sm.m, sm.P, K, tid);
-    if (tid < K) {  // rowsum(S0 . dS) of key channel i
+    {  // rowsum(S0 . dS) of key channel i = tid / 4, in four column quarters
+        const int i = tid >> 2, j0 = 16 * (tid & 3);
         float f = 0.f;
-        for (int j = 0; j < V; ++j) f += sm.s0[tid * LS + j] * sm.ds[tid * LS + j];
-        sm.fs[tid] = f;
+        if (i < 16 * KT && j0 < VP)  // inside the zero-padded tiles
+#pragma unroll
+            for (int j = 0; j < 16; ++j) f += sm.u.st.s0[i * LS + j0 + j] * sm.u.st.ds[i * LS + j0 + j];
+        f += __shfl_xor(f, 1);
+        f += __shfl_xor(f, 2);
+        if ((tid & 3) == 0) sm.fs[i] = f;
     }
     __syncthreads();
-    // ddelta = P^T dO + Ktil dS + c delta
+    // ddelta and dR of value tile w (lane (lg, ln): rows 4 lg + r, column 16 w + ln)
+    if (w < VT) {
+        const int j = 16 * w + ln;
+        f32x4 dd;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int j = 4 * g + e;
-        float x = sm.cs[t] * sm.dl[t * LQ + j];
-        if (j < V) {
-            for (int q = t; q < C; ++q) x += sm.P[q * LT + t] * sm.dO[q * LQ + j];
-            for (int i = 0; i < K; ++i) x += sm.lam[t * LQ + i] * sm.k[t * LQ + i] * sm.ds[i * LS + j];
+        for (int r = 0; r < 4; ++r) dd[r] = sm.cs[4 * lg + r] * sm.dl[(4 * lg + r) * LQ + j];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            dd = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.P[(4 * lg + q) * LT + ln], sm.dO[(4 * lg + q) * LQ + j], dd,
+                                                      0, 0, 0);
+        for (int tau = 0; tau < KT; ++tau)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int i = 16 * tau + 4 * lg + q;
+                dd = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.lam[ln * LQ + i] * sm.k[ln * LQ + i],
+                                                          sm.u.st.ds[i * LS + j], dd, 0, 0, 0);
+            }
+        f32x4 dr = zero4();
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            dr = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.T[(4 * lg + q) * LT + ln], dd[q], dr, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tt = 4 * lg + r, tq = c * C + tt;
+            sm.dr[tt * LQ + j] = dr[r];
+            if (j < V && tq < s.T) {
+                const bool von = sm.m.val[tt] != 0.f;
+                const int64_t o = (((int64_t)b * s.T + tq) * s.H + h) * V + j;
+                if (s.dwrite) s.dwrite[o] = von ? dr[r] * ld4<float>(s.v, b, tq, h, j) : 0.f;
+                if (s.dv) store_out(s.dv, 0, o, von ? dr[r] * ld4<float>(s.write, b, tq, h, j) : 0.f);
+            }
         }
-        sm.dd[t * LQ + j] = x;
     }
     __syncthreads();
-    // dR = T^T ddelta; dw, dv
+    // The 16 x 16 products over the value axis: tiles 0 .. 3 KT - 1 are dAhat,
+    // dQhat, dKtil of key tile tau = n / 3; tile 3 KT is dA, 3 KT + 1 is dP.
+    const int ntile = 3 * KT + 2;
+    f32x4 res[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int j = 4 * g + e;
-        float x = 0.f;
-        for (int q = t; q < C; ++q) x += sm.T[q * LT + t] * sm.dd[q * LQ + j];
-        sm.dr[t * LQ + j] = x;
-        if (j < V && tg < s.T) {
-            const int64_t o = (((int64_t)b * s.T + tg) * s.H + h) * V + j;
-            if (s.dwrite) s.dwrite[o] = on ? x * sm.v[t * LQ + j] : 0.f;
-            if (s.dv) store_out(s.dv, 0, o, on ? x * sm.w[t * LQ + j] : 0.f);
+    for (int m = 0; m < 4; ++m) {
+        const int n = w + 4 * m;
+        res[m] = zero4();
+        if (n >= ntile) continue;
+        const int kind = n < 3 * KT ? n % 3 : 3 + (n - 3 * KT), tau = n < 3 * KT ? n / 3 : 0;
+        const float *xa = kind == 0 || kind == 3 ? sm.dr : (kind == 2 ? sm.dl : sm.dO);
+        const float *yb = kind == 2 ? sm.u.st.ds : sm.u.st.s0;
+        const int yo = kind >= 3 ? 0 : (16 * tau + ln) * LS, ys = kind >= 3 ? LQ : LS;
+        const float *yy = kind >= 3 ? sm.dl + ln * LQ : yb + yo;
+        (void)ys;
+        f32x4 acc = zero4();
+        for (int kk = 0; kk < VP; kk += 4)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[ln * LQ + kk + lg], yy[kk + lg], acc, 0, 0, 0);
+        res[m] = acc;
+    }
+    __syncthreads();  // S0 and dS are no longer read: their space takes dAhat, dQhat, dKtil
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const int n = w + 4 * m;
+        if (n >= ntile) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tt = 4 * lg + r;
+            if (n < 3 * KT) {
+                const int kind = n % 3, i = 16 * (n / 3) + ln;
+                float *dst = kind == 0 ? sm.u.gr.ga : (kind == 1 ? sm.u.gr.gq : sm.u.gr.gk);
+                dst[tt * LQ + i] = kind == 0 ? -res[m][r] : res[m][r];
+            } else {
+                const bool same = sm.m.seg[tt] == sm.m.seg[ln];
+                if (n == 3 * KT) sm.dA[tt * LT + ln] = (ln < tt && same) ? -res[m][r] : 0.f;
+                else sm.dP[tt * LT + ln] = (ln <= tt && same) ? res[m][r] : 0.f;
+            }
         }
     }
     __syncthreads();
-    // dAhat = -dR S0^T, dQhat = dO S0^T, dKtil = delta dS^T (token t, keys 4g ..)
+    // Per key channel: lane i of a group of cpl lanes, rpw groups per wave; the
+    // lane keeps its channel's gates, k, q and ehat of the whole chunk in
+    // registers.  Group (w, sub) takes the rows u = 4 rpw p + rpw w + sub
+    // (p < 4 / rpw): the token rows of eA, qP, kAP and the outputs, then the
+    // start rows lo = u - 1 of the alpha gradient's pairs, whose partial sums
+    // over lo meet in LDS.
+    const int cpl = K <= 16 ? 16 : (K <= 32 ? 32 : 64), rpw = 64 / cpl;
+    const int i = l % cpl, sub = l / cpl, sg15 = sm.m.seg[C - 1], np = 4 / rpw;
+    const bool iv = i < K;
+    float ra[C], rk[C], rq[C], re[C];
+    int sg[C];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int i = 4 * g + e;
-        float xa = 0.f, xq = 0.f, xk = 0.f;
-        if (i < K)
-            for (int j = 0; j < V; ++j) {
-                xa -= sm.dr[t * LQ + j] * sm.s0[i * LS + j];
-                xq += sm.dO[t * LQ + j] * sm.s0[i * LS + j];
-                xk += sm.dl[t * LQ + j] * sm.ds[i * LS + j];
-            }
-        sm.ga[t * LQ + i] = xa;
-        sm.gq[t * LQ + i] = xq;
-        sm.gk[t * LQ + i] = xk;
+    for (int x = 0; x < C; ++x) {
+        ra[x] = sm.al[x * LQ + i];
+        rk[x] = sm.k[x * LQ + i];
+        rq[x] = sm.q[x * LQ + i];
+        re[x] = sm.e[x * LQ + i] * rk[x];
+        sg[x] = sm.m.seg[x];
     }
-    {  // dA (strict, same segment) and dP (with the diagonal): pair (t, s) = (tid / 16, tid % 16)
-        const int tt = tid >> 4, ss = tid & 15;
-        float xa = 0.f, xp = 0.f;
-        if (ss <= tt && sm.m.seg[tt] == sm.m.seg[ss])
-            for (int j = 0; j < V; ++j) {
-                xa -= sm.dr[tt * LQ + j] * sm.dl[ss * LQ + j];
-                xp += sm.dO[tt * LQ + j] * sm.dl[ss * LQ + j];
-            }
-        sm.dA[tt * LT + ss] = ss < tt ? xa : 0.f;
-        sm.dP[tt * LT + ss] = xp;
-    }
-    __syncthreads();
-    // Per key channel i (threads i < K): the decay-weighted sums through running
-    // products, then dq, dk, de and dalpha for every token of the channel.
-    if (tid < K) {
-        const int i = tid, sg15 = sm.m.seg[C - 1];
-        float eA[C], qP[C], kAP[C], al[C];
+    for (int p = 0; p < np; ++p) {
+        const int u = 4 * rpw * p + rpw * w + sub, su = sm.m.seg[u];
+        // eA, qP of row u (s <= u) and kAP of row u (t >= u); the running
+        // decays stop at u's segment, where dA and dP end as well
+        float eA = 0.f, qP = 0.f, kAP = 0.f, d = 1.f, d2 = 1.f;
 #pragma unroll
-        for (int u = 0; u < C; ++u) {
-            eA[u] = qP[u] = kAP[u] = 0.f;
-            al[u] = sm.al[u * LQ + i];
-        }
-#pragma unroll
-        for (int tt = 0; tt < C; ++tt) {
-            const float et = sm.eh[tt * LQ + i], qt = sm.q[tt * LQ + i];
-            float d = 1.f;  // D_{tt, ss}
-#pragma unroll
-            for (int ss = tt; ss >= 0; --ss) {
-                if (sm.m.seg[ss] != sm.m.seg[tt]) break;
-                const float dA = sm.dA[tt * LT + ss], dP = sm.dP[tt * LT + ss];
-                const float ks = sm.k[ss * LQ + i];
-                eA[tt] += dA * d * ks;
-                qP[tt] += dP * d * ks;
-                kAP[ss] += (dA * et + dP * qt) * d;
-                d *= al[ss];
+        for (int x = C - 1; x >= 0; --x) {
+            if (x <= u) {
+                eA += sm.dA[u * LT + x] * d * rk[x];
+                qP += sm.dP[u * LT + x] * d * rk[x];
+                d = (x > 0 && sg[x - 1] == su) ? d * ra[x] : 0.f;
             }
         }
-        // dalpha by the pair products (see the kernel comment): lo = -1 is the
-        // chunk start, hi = 15 also stands for the chunk end.
-        float dal[C];
 #pragma unroll
-        for (int u = 0; u < C; ++u) dal[u] = 0.f;
-        for (int lo = -1; lo < C - 1; ++lo) {
-            float Y[C], y = 0.f;
-#pragma unroll
-            for (int u = C - 1; u >= 0; --u) {
-                float cf = 0.f;
-                if (u > lo) {
-                    if (lo < 0) {
-                        cf = sm.m.seg[u] == 0 ? sm.eh[u * LQ + i] * sm.ga[u * LQ + i] + sm.q[u * LQ + i] * sm.gq[u * LQ + i] : 0.f;
-                        if (u == C - 1 && sg15 == 0) cf += sm.fs[i];
-                    } else {
-                        cf = (sm.dA[u * LT + lo] * sm.eh[u * LQ + i] + sm.dP[u * LT + lo] * sm.q[u * LQ + i]) *
-                             sm.k[lo * LQ + i];
-                        if (u == C - 1 && sm.m.seg[lo] == sg15) cf += sm.k[lo * LQ + i] * sm.gk[lo * LQ + i];
-                    }
-                }
-                y = u == C - 1 ? cf : cf + al[u + 1] * y;
-                Y[u] = y;
+        for (int x = 0; x < C; ++x) {
+            if (x >= u) {
+                d2 = x == u ? 1.f : (sg[x] == su ? d2 * ra[x] : 0.f);
+                kAP += (sm.dA[x * LT + u] * re[x] + sm.dP[x * LT + u] * rq[x]) * d2;
             }
-            float L = 1.f;
-#pragma unroll
-            for (int u = 0; u < C; ++u)
-                if (u > lo) {
-                    dal[u] += L * Y[u];
-                    L *= al[u];
-                }
         }
-        const int K_ = K;
-#pragma unroll
-        for (int u = 0; u < C; ++u) {
-            const int tq = c * C + u;
-            if (tq >= s.T) continue;
+        const int tq = c * C + u;
+        if (iv && tq < s.T) {
             const bool von = sm.m.val[u] != 0.f;
             const float bt = sm.bt[u * LQ + i], lt = sm.lam[u * LQ + i];
-            const float q = sm.q[u * LQ + i], k = sm.k[u * LQ + i], ev = sm.e[u * LQ + i];
-            const float dq = bt * sm.gq[u * LQ + i] + qP[u];
-            const float deh = bt * sm.ga[u * LQ + i] + eA[u];
-            const float dk = lt * sm.gk[u * LQ + i] + kAP[u] + ev * deh + sm.ck[u] * k;
-            const int64_t o = (((int64_t)b * s.T + tq) * s.H + h) * K_ + i;
+            const float k = sm.k[u * LQ + i], ev = sm.e[u * LQ + i];
+            const float dq = bt * sm.u.gr.gq[u * LQ + i] + qP;
+            const float deh = bt * sm.u.gr.ga[u * LQ + i] + eA;
+            const float dk = lt * sm.u.gr.gk[u * LQ + i] + kAP + ev * deh + sm.ck[u] * k;
+            const int64_t o = (((int64_t)b * s.T + tq) * s.H + h) * K + i;
             if (s.dq) store_out(s.dq, 0, o, von ? dq : 0.f);
             if (s.dk) store_out(s.dk, 0, o, von ? dk : 0.f);
             if (s.derase) s.derase[o] = von ? k * deh : 0.f;
-            if (s.dalpha) s.dalpha[o] = (von && !sm.m.rs[u]) ? dal[u] : 0.f;
-            (void)q;
         }
+    }
+    // dalpha partials: for each start row lo of this group, Y(u, lo) for u > lo
+    // by Horner over u descending, then dal[u] += L(lo, u) Y(u, lo) ascending.
+    float dal[C];
+#pragma unroll
+    for (int x = 0; x < C; ++x) dal[x] = 0.f;
+    for (int p = 0; p < np; ++p) {
+        const int lo = 4 * rpw * p + rpw * w + sub - 1;  // -1 .. 14
+        const float kl = lo >= 0 ? sm.k[lo * LQ + i] : 0.f;
+        const float endc = (lo >= 0 && sm.m.seg[lo] == sg15) ? kl * sm.u.gr.gk[lo * LQ + i] : 0.f;
+        float Y[C], y = 0.f;
+#pragma unroll
+        for (int x = C - 1; x >= 0; --x) {
+            float cf = 0.f;
+            if (x > lo) {
+                if (lo >= 0) {
+                    cf = (sm.dA[x * LT + lo] * re[x] + sm.dP[x * LT + lo] * rq[x]) * kl;
+                    if (x == C - 1) cf += endc;
+                } else {
+                    cf = sg[x] == 0 ? re[x] * sm.u.gr.ga[x * LQ + i] + rq[x] * sm.u.gr.gq[x * LQ + i] : 0.f;
+                    if (x == C - 1 && sg15 == 0) cf += sm.fs[i];
+                }
+            }
+            y = x == C - 1 ? cf : cf + ra[x + 1] * y;
+            Y[x] = y;
+        }
+        float L = 1.f;
+#pragma unroll
+        for (int x = 0; x < C; ++x)
+            if (x > lo) {
+                dal[x] += L * Y[x];
+                L *= ra[x];
+            }
+    }
+    // partials [group][u][channel] (4 rpw groups of C x cpl), then one sum per (u, channel)
+    float *part = sm.u.gr.part + (w * rpw + sub) * (C * cpl);
+#pragma unroll
+    for (int x = 0; x < C; ++x) part[x * cpl + i] = dal[x];
+    __syncthreads();
+    for (int e = tid; e < C * cpl; e += NT) {
+        const int u = e / cpl, ch = e - u * cpl;
+        if (ch >= K) continue;
+        float x = 0.f;
+        for (int gq = 0; gq < 4 * rpw; ++gq) x += sm.u.gr.part[gq * (C * cpl) + e];
+        const int tq = c * C + u;
+        if (tq < s.T && s.dalpha)
+            s.dalpha[(((int64_t)b * s.T + tq) * s.H + h) * K + ch] =
+                (sm.m.val[u] != 0.f && !sm.m.rs[u]) ? x : 0.f;
     }
 }
 
