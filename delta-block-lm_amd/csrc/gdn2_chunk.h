@@ -237,7 +237,7 @@ inline bool wide_eligible_shape(const gdn2_shape *s, int chunk) {
     return chunk == CHUNK && s->keys == WIDE_D && s->values == WIDE_D;
 }
 
-// Checkpoint per chunk: S0^T (bf16 D x D), T (bf16 C x C), GateBlock, delta (f32
+// Checkpoint per chunk: S0^T (bf16 hi and lo, D x D each), T (bf16 C x C), GateBlock, delta (f32
 // C x D), the factored chunk map (-W'^T bf16 C x D, Ktil bf16 hi and lo C x D
 // each, U^T f32 C x D, the diagonal f32 D), |k|^2 and the value blocks'
 // |delta|^2 (f32 C each).
@@ -252,9 +252,9 @@ constexpr size_t WCK_LRG = (size_t)WIDE_D * 4;
 constexpr size_t WCK_MAPN = (size_t)WIDE_D * WIDE_D * 4;
 constexpr size_t WCK_NORM = (size_t)CHUNK * (1 + WIDE_NVB) * 4;
 constexpr size_t WCK_CHUNK =
-    WCK_STATE + WCK_T + WCK_GATE + WCK_DELTA + WCK_LRW + WCK_LRK + WCK_LRU + WCK_LRG + WCK_NORM;
-// Backward workspace per chunk: dS^T (bf16) and N^T (f32).
-constexpr size_t WWS_CHUNK = WCK_STATE + WCK_MAPN;
+    2 * WCK_STATE + WCK_T + WCK_GATE + WCK_DELTA + WCK_LRW + WCK_LRK + WCK_LRU + WCK_LRG + WCK_NORM;
+// Backward workspace per chunk: dS^T (bf16 hi and lo) and N^T (f32).
+constexpr size_t WWS_CHUNK = 2 * WCK_STATE + WCK_MAPN;
 
 inline size_t wide_checkpoint_bytes(int64_t B, int64_t T, int64_t H) {
     return (size_t)chunk_count(B, T, H) * WCK_CHUNK;
@@ -268,6 +268,8 @@ inline void wide_bind_checkpoint(ChunkArgs &a, void *ck) {
     const int64_t n = (int64_t)a.B * a.H * a.nc;
     char *p = static_cast<char *>(ck);
     a.ck_state = reinterpret_cast<uint16_t *>(p);
+    p += n * WCK_STATE;
+    a.ck_state_lo = reinterpret_cast<uint16_t *>(p);
     p += n * WCK_STATE;
     a.ck_t = reinterpret_cast<uint16_t *>(p);
     p += n * WCK_T;
@@ -291,6 +293,8 @@ inline void wide_bind_workspace(ChunkArgs &a, void *ws) {
     const int64_t n = (int64_t)a.B * a.H * a.nc;
     char *p = static_cast<char *>(ws);
     a.ws_dstate = reinterpret_cast<uint16_t *>(p);
+    p += n * WCK_STATE;
+    a.ws_dstate_lo = reinterpret_cast<uint16_t *>(p);
     p += n * WCK_STATE;
     a.ws_n = reinterpret_cast<float *>(p);
 }

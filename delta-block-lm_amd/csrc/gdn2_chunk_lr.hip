@@ -370,11 +370,11 @@ static hipError_t launch_lr(const LrScanArgs &p, hipStream_t stream) {
 
 hipError_t launch_lr_scan(const LrScanArgs &p, int kd, int ct, hipStream_t stream) {
     if (p.vd % 16 != 0) return hipErrorInvalidValue;
-    // d = 128 keeps bf16 hi only, the 16-token chunks hi and lo
-    if ((kd == 128) != (p.ckpt_lo == nullptr)) return hipErrorInvalidValue;
+    // every configuration keeps the checkpoint's lo part; d = 128 streams -W'^T as hi only
+    if (p.ckpt_lo == nullptr) return hipErrorInvalidValue;
     if (kd == 128 && ct == 64 && p.vd % 32 == 0)
-        return p.reverse ? launch_lr<LrCfg<128, 64, 2, 3, 2, true, false, false>>(p, stream)
-                         : launch_lr<LrCfg<128, 64, 2, 3, 2, false, false, false>>(p, stream);
+        return p.reverse ? launch_lr<LrCfg<128, 64, 2, 3, 2, true, true, false>>(p, stream)
+                         : launch_lr<LrCfg<128, 64, 2, 3, 2, false, true, false>>(p, stream);
     if (kd == 64 && ct == 64 && p.vd % 32 == 0)
         return p.reverse ? launch_lr<LrCfg<64, 64, 2, 3, 3, true, true, true>>(p, stream)
                          : launch_lr<LrCfg<64, 64, 2, 3, 3, false, true, true>>(p, stream);

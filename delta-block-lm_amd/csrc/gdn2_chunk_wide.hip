@@ -64,6 +64,15 @@ __device__ __forceinline__ uint4 scale8(uint4 v, float f) {
     for (int e = 0; e < 8; e += 2) o[e / 2] = bf16_pack2(f * bf16_val(p.h[e]), f * bf16_val(p.h[e + 1]));
     return make_uint4(o[0], o[1], o[2], o[3]);
 }
+// f * v as a bf16 hi/lo pair (f * v ~= hi + lo).
+__device__ __forceinline__ void scale8_split(uint4 v, float f, uint4 &hi, uint4 &lo) {
+    Pack8 p, h, l;
+    p.u = v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) split_bf16(f * bf16_val(p.h[e]), h.h[e], l.h[e]);
+    hi = h.u;
+    lo = l.u;
+}
 __device__ __forceinline__ float sq8(uint4 v) {
     Pack8 p;
     p.u = v;
@@ -104,7 +113,8 @@ struct WPrepSmem {
             float Tf[C * LDF];
         } inv;
         struct {
-            uint16_t kbg[NKB][TILE];  // beta gam K rows, key block kb
+            uint16_t kbg[NKB][TILE];   // beta gam K rows (hi), key block kb
+            uint16_t kbgl[NKB][TILE];  // their lo parts
             uint16_t vbt[NVB][TILE];  // beta V rows, value block vb
         } wu;                          // once the inverse is done
     } u;
@@ -210,7 +220,10 @@ __global__ void __launch_bounds__(NT) wide_prep_kernel(ChunkArgs a) {
         const float bg = sm.gl.beta[t] * sm.gl.gam[t], be = sm.gl.beta[t];
 #pragma unroll
         for (int i = 0; i < NKB; ++i) {
-            put_row8(sm.u.wu.kbg[i], t, cb, scale8(k8.p[i], bg));
+            uint4 kh, kl;
+            scale8_split(k8.p[i], bg, kh, kl);
+            put_row8(sm.u.wu.kbg[i], t, cb, kh);
+            put_row8(sm.u.wu.kbgl[i], t, cb, kl);
             put_row8(sm.u.wu.vbt[i], t, cb, scale8(v8.p[i], be));
         }
     }
@@ -221,6 +234,7 @@ __global__ void __launch_bounds__(NT) wide_prep_kernel(ChunkArgs a) {
     for (int i = 0; i < NKB; ++i) {
         f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
         gemm2_tr(x, &Tb[(16 * tm) * LDB], sm.u.wu.kbg[i], tn0);
+        gemm2_tr(x, &Tb[(16 * tm) * LDB], sm.u.wu.kbgl[i], tn0);
         gemm2_tr(y, &Tb[(16 * tm) * LDB], sm.u.wu.vbt[i], tn0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -248,7 +262,7 @@ struct WOutSmem {
     uint16_t rt[TILE];   // R^T hi
     uint16_t tb[TILE];   // T rows
     uint16_t pt[TILE], ptl[TILE];  // P^T hi/lo
-    uint16_t dt[TILE], dl[TILE];   // delta^T hi/lo of block vb
+    uint16_t dt[TILE], dl[TILE];   // delta^T hi/lo of block vb; S0^T lo rows of block vb before phase 2
     float df[C * LDF];             // delta rows (f32) of block vb, for the checkpoint
     uint16_t os[TILE];             // O rows of block vb (bf16 output)
     GateLds gl;
@@ -262,7 +276,7 @@ struct WOutSmem {
 struct WOutIn {
     Row2 q, k;
     uint4 v[NVB];
-    Mat2 s0[NVB];
+    Mat2 s0[NVB], s0l[NVB];  // S0^T rows, bf16 hi and lo
     uint4 t;
     float G, be, va;
     int sg;
@@ -280,6 +294,7 @@ __device__ __forceinline__ void wout_load(const ChunkArgs &a, int ci, int tid, W
         constexpr int vb = P == 1 ? 0 : 1;
         x.v[vb] = load8(a.v + 64 * vb, a.vs, b, tr, h, cb, true);
         x.s0[vb] = load_mat2(a.ck_state + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
+        x.s0l[vb] = load_mat2(a.ck_state_lo + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
     } else {
         x.t = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C + (tid >> 3) * C + 8 * (tid & 7));
         const GateBlock *gb = a.ck_gate + ci;
@@ -319,6 +334,9 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a, int nchunks) 
     __shared__ WOutSmem sm;
     uint16_t *Qs = sm.q, *Ks = sm.k, *Vt = sm.vt, *Tb = sm.tb, *St = sm.st, *Rt = sm.rt;
     uint16_t *Pt = sm.pt, *Ptl = sm.ptl, *Dt = sm.dt, *Dl = sm.dl;
+    // S0^T lo rows of the current block over delta^T's tiles, which phase 1 does not use.
+    uint16_t *Sl = sm.dt;
+    static_assert(sizeof(sm.dt) + sizeof(sm.dl) >= sizeof(sm.st), "S0^T lo over dt, dl");
     WOutIn in;
     wout_load<0>(a, blockIdx.x, threadIdx.x, in);
     wout_load<1>(a, blockIdx.x, threadIdx.x, in);
@@ -344,6 +362,7 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a, int nchunks) 
         put_row2(Ks, t, cb, k8);
         put_col8(Vt, t, cb, mask8(in.v[0], on));
         put_mat2(St, in.s0[0], tid);
+        put_mat2(Sl, in.s0l[0], tid);
         *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = in.t;
         float ksq = 0.f;
 #pragma unroll
@@ -378,12 +397,15 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a, int nchunks) 
     }
 #pragma unroll 1
     for (int vb = 0; vb < NVB; ++vb) {
-        // Phase 1: R (-> Rt, lo over Vt) and gam Q S0 kept in registers.
+        // Phase 1: R (-> Rt, lo over Vt) and gam Q S0 kept in registers; S0 as
+        // hi + lo.
         f32x4 qs[2] = {zero4(), zero4()};
         {
             f32x4 x[2] = {zero4(), zero4()};
             gemm2<KD, LDK, LDK>(x, &Ks[(16 * tm) * LDK], St, tn0);
             gemm2<KD, LDK, LDK>(qs, &Qs[(16 * tm) * LDK], St, tn0);
+            gemm2<KD, LDK, LDK>(x, &Ks[(16 * tm) * LDK], Sl, tn0);
+            gemm2<KD, LDK, LDK>(qs, &Qs[(16 * tm) * LDK], Sl, tn0);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 uint16_t *vt = &Vt[(16 * (tn0 + j)) * LDB + 16 * tm];
@@ -458,6 +480,7 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a, int nchunks) 
             wout_store(a, ci, 0, tid, sm);
             put_col8(Vt, t, cb, mask8(in.v[1], on));
             put_mat2(St, in.s0[1], tid);
+            put_mat2(Sl, in.s0l[1], tid);
             wout_load<3>(a, cn, tid, in);
             __syncthreads();
         }
@@ -483,7 +506,8 @@ struct WBPrepSmem {
     union {
         struct {
             uint16_t tb[TILE];    // T rows
-            uint16_t kbg[KTILE];  // beta gam K rows
+            uint16_t kbg[KTILE];  // beta gam K rows (hi)
+            uint16_t kbgl[KTILE];  // their lo parts
         } p1;
         uint16_t wt[2][KD * LDB];  // W^T hi/lo ([k][t]) from phase 2
     } u;
@@ -549,7 +573,7 @@ __device__ __forceinline__ void wbprep_store(const ChunkArgs &a, int ci, int tm,
 // or on the previous chunk's stores.
 __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a, int nchunks) {
     __shared__ WBPrepSmem sm;
-    uint16_t *Qs = sm.q, *Ks = sm.k, *Tb = sm.u.p1.tb, *KBGs = sm.u.p1.kbg;
+    uint16_t *Qs = sm.q, *Ks = sm.k, *Tb = sm.u.p1.tb, *KBGs = sm.u.p1.kbg, *KBGl = sm.u.p1.kbgl;
     uint16_t *Pt = sm.pt, *Ptl = sm.ptl;
     uint16_t *Wt = sm.u.wt[0], *Wtl = sm.u.wt[1];  // over the phase-1 operands
     // X^T hi/lo of each block, over Q/K (block 0) and the dO rows (block 1) after phase 2
@@ -582,7 +606,12 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a, int nchunks
 #pragma unroll
         for (int vb = 0; vb < NVB; ++vb) put_row8(sm.dos[vb], t, cb, mask8(in.dO[vb], on && a.dout));
 #pragma unroll
-        for (int i = 0; i < NKB; ++i) put_row8(KBGs, t, cb + 8 * i, scale8(k8.p[i], bg), LDK);
+        for (int i = 0; i < NKB; ++i) {
+            uint4 kh, kl;
+            scale8_split(k8.p[i], bg, kh, kl);
+            put_row8(KBGs, t, cb + 8 * i, kh, LDK);
+            put_row8(KBGl, t, cb + 8 * i, kl, LDK);
+        }
         *reinterpret_cast<uint4 *>(&Tb[(tid >> 3) * LDB + 8 * (tid & 7)]) = in.t;
         if (w == 0) {
             gates_derive(sm.gl, in.G, in.be, in.va, in.sg);
@@ -600,6 +629,7 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a, int nchunks
     for (int kb = 0; kb < NKB; ++kb) {
         wacc[kb][0] = wacc[kb][1] = zero4();
         gemm2_tr<64, LDB, LDK>(wacc[kb], &Tb[(16 * tm) * LDB], KBGs, tn0 + 4 * kb);
+        gemm2_tr<64, LDB, LDK>(wacc[kb], &Tb[(16 * tm) * LDB], KBGl, tn0 + 4 * kb);
         const int mt = tm + 4 * kb;  // row tile of Y (key channel)
 #pragma unroll
         for (int vb = 0; vb < NVB; ++vb) yacc[vb][kb][0] = yacc[vb][kb][1] = zero4();
@@ -723,7 +753,9 @@ struct WBGradSmem {
     uint16_t tr[TILE];    // T rows; MA^T (F..G)
     uint16_t dh[TILE], dlo[TILE];  // delta rows hi/lo of block vb (..F); dQ^T [KD][LDB] over both at the end
     uint16_t pt[TILE], ptl[TILE];  // P^T hi/lo (until read into registers); ddelta^T (D..E);
-                                   // block 0's dV^T (its F .. block 1's D); MP^T (after the blocks)
+                                   // block 0's dV^T over pt (its F .. block 1's D) and dR lo
+                                   // rows over ptl (F); MP^T (after the blocks)
+    uint16_t xl[KTILE];            // dS^T lo rows of block vb (A..D); S0^T lo rows (F)
     GateLds gl;
     float dsc[C];
     float g1[2][C], ku[2][C], b1[2][C], b2[2][C], zr[2][C], zc[4][C], dlam[2][C];
@@ -733,7 +765,7 @@ struct WBGradSmem {
 // A value block's inputs as loaded: dO, S0^T and dS^T rows, V, delta (f32).
 struct VbRaw {
     uint4 dor, vr;
-    Mat2 s0, ds;
+    Mat2 s0, ds, dsl;  // S0^T rows (hi), dS^T rows (hi and lo)
     float4 d0, d1;
 };
 }  // namespace
@@ -746,6 +778,8 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
     uint16_t *dRr = sm.dst;               // dR rows, E..F
     uint16_t *MAt = sm.tr, *MPt = sm.pt, *MPtl = sm.ptl;
     uint16_t *dQt = sm.dh, *dKt = sm.s0t;
+    uint16_t *Xl = sm.xl;  // dS^T lo (A..D), then S0^T lo (E..F)
+    uint16_t *dRl = sm.ptl;  // dR rows' lo part (F): ddelta^T lo is read by then
     // dV^T of a block ([value][token]): block 0 over P^T's tiles (free from its
     // phase F until block 1's phase D), block 1 over its V rows (free after E).
     auto dVt = [&](int vb) { return vb == 0 ? sm.pt : sm.vr; };
@@ -763,6 +797,7 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
         r.dor = a.dout ? load8(a.dout + 64 * vb, a.ds, b, tg, h, cb, inb) : make_uint4(0, 0, 0, 0);
         r.s0 = load_mat2(a.ck_state + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
         r.ds = load_mat2(a.ws_dstate + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
+        r.dsl = load_mat2(a.ws_dstate_lo + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
         r.vr = load8(a.v + 64 * vb, a.vs, b, tg, h, cb, inb);
         r.d0 = *reinterpret_cast<const float4 *>(dck + t * KD + 8 * cb);
         r.d1 = *reinterpret_cast<const float4 *>(dck + t * KD + 8 * cb + 4);
@@ -779,13 +814,16 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
                                                       (tid >> 3) * C + 8 * (tid & 7));
     const bool on = va != 0.f;
     float frob = 0.f;  // this thread's part of <S0, dS> over both blocks
-    // A block's dO, S0^T and dS^T rows into LDS (the first stage of each block).
+    // A block's dO, S0^T and dS^T rows (hi; dS^T lo over xl) into LDS (the first
+    // stage of each block); S0^T lo comes in phase E.
     auto stage_vb_a = [&](const VbRaw &r) {
         put_row8(dOs, t, cb, mask8(r.dor, on));
         put_mat2(S0t, r.s0, tid);
         put_mat2(dSt, r.ds, tid);
+        put_mat2(Xl, r.dsl, tid);
 #pragma unroll
-        for (int i = 0; i < NKB; ++i) frob += dot8_bf16(r.s0.p[i], r.ds.p[i]);
+        for (int i = 0; i < NKB; ++i)
+            frob += dot8_bf16(r.s0.p[i], r.ds.p[i]) + dot8_bf16(r.s0.p[i], r.dsl.p[i]);
     };
     // A block's V rows and delta rows (hi/lo): read from phase D on.
     auto stage_vb_b = [&](const VbRaw &r) {
@@ -916,6 +954,7 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
         }
         row_reduce_accum(pg1, sm.g1[w & 1], tm, vb > 0);
         gemm2<KD, LDK, LDK>(kds, &Ks[(16 * tm) * LDK], dSt, tn0);
+        gemm2<KD, LDK, LDK>(kds, &Ks[(16 * tm) * LDK], Xl, tn0);
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -928,6 +967,7 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
             f32x4 x[2] = {zero4(), zero4()};
             gemm2_tr<64, LDB, LDK>(x, &Dh[(16 * tm) * LDB], dSt, tn0 + 4 * kb);
             gemm2_tr<64, LDB, LDK>(x, &Dlo[(16 * tm) * LDB], dSt, tn0 + 4 * kb);
+            gemm2_tr<64, LDB, LDK>(x, &Dh[(16 * tm) * LDB], Xl, tn0 + 4 * kb);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 float kv[4];
@@ -958,11 +998,19 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
                 for (int i = 0; i < 4; ++i) xd[j][i] += cs[i] * (dh[i] + dlo[i]);
             }
         }
+        // S0^T lo rows again (phase F's operand, staged over dS^T lo in phase E;
+        // an L2 hit, issued here so that phase E hides it)
+        const Mat2 s0lr = load_mat2(a.ck_state_lo + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
         __syncthreads();  // P^T and delta read by every wave before ddelta^T takes P's tiles
 #pragma unroll
         for (int j = 0; j < 2; ++j)
             store_tile_t_split(&Dd[(16 * (tn0 + j)) * LDB + 16 * tm],
                                &Ddl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, xd[j]);
+#pragma unroll
+        for (int i = 0; i < NKB; ++i) {  // <S0 lo, dS hi> at this thread's staging positions
+            const int p = tid + NT * i, r = p / (KD / 8), c0 = 8 * (p % (KD / 8));
+            frob += dot8_bf16(s0lr.p[i], *reinterpret_cast<const uint4 *>(&dSt[r * LDK + c0]));
+        }
         __syncthreads();
         // Phase E: dR = T^T ddelta -> dV, the sum_v dR v part of dbeta, dR rows.
         {
@@ -991,9 +1039,17 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
                 store_tile_rm(&dRr[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, x[j]);
             }
             row_reduce_accum(pb2, sm.b2[w & 1], tm, vb > 0);
-            __syncthreads();  // V and ddelta^T read: their tiles take this block's dV^T
+            put_mat2(Xl, s0lr, tid);  // dS^T lo was last read in phase D
+            __syncthreads();  // V and ddelta^T read: their tiles take this block's dV^T and dR's lo rows
 #pragma unroll
-            for (int j = 0; j < 2; ++j) store_tile_t(&dVt(vb)[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, dvv[j]);
+            for (int j = 0; j < 2; ++j) {
+                store_tile_t(&dVt(vb)[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, dvv[j]);
+                f32x4 lo;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) lo[i] = x[j][i] - bf16_val(bf16_bits(x[j][i]));
+                store_tile_rm(&dRl[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, lo);
+            }
+            __syncthreads();
         }
         // Phase F: dR S0^T (-> dK, dbeta, dgam); dR delta^T and dO delta^T summed.
         float pku[4] = {0.f, 0.f, 0.f, 0.f};
@@ -1001,6 +1057,8 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
         for (int kb = 0; kb < NKB; ++kb) {
             f32x4 drs[2] = {zero4(), zero4()};
             gemm2_tr<64, LDB, LDK>(drs, &dRr[(16 * tm) * LDB], S0t, tn0 + 4 * kb);
+            gemm2_tr<64, LDB, LDK>(drs, &dRr[(16 * tm) * LDB], Xl, tn0 + 4 * kb);
+            gemm2_tr<64, LDB, LDK>(drs, &dRl[(16 * tm) * LDB], S0t, tn0 + 4 * kb);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 float kv[4];
@@ -1013,15 +1071,36 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
             }
         }
         row_reduce_accum(pku, sm.ku[w & 1], tm, vb > 0);
+        {  // phase A's dO S0^T with S0's lo part, which xl holds now
+            float pg1l[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+                f32x4 x[2] = {zero4(), zero4()};
+                gemm2_tr<64, LDB, LDK>(x, &dOs[(16 * tm) * LDB], Xl, tn0 + 4 * kb);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    float qv[4];
+                    ld4_rm_tr<LDK>(Qs, 16 * tm, 16 * (tn0 + 4 * kb + j), qv);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        pg1l[i] += qv[i] * x[j][i];
+                        dos[kb][j][i] += x[j][i];
+                    }
+                }
+            }
+            row_reduce_accum(pg1l, sm.g1[w & 1], tm, true);
+        }
         if (tn0 <= tm) {
             gemm2(da, &dRr[(16 * tm) * LDB], Dh, tn0);
             gemm2(da, &dRr[(16 * tm) * LDB], Dlo, tn0);
+            gemm2(da, &dRl[(16 * tm) * LDB], Dh, tn0);
             gemm2(dp, &dOs[(16 * tm) * LDB], Dh, tn0);
             gemm2(dp, &dOs[(16 * tm) * LDB], Dlo, tn0);
         }
     }
     frob = wave_sum(frob);
     if (lane_id() == 0) sm.frob[w] = frob;
+    __syncthreads();  // the last block's phase F has read dR's lo rows: MP^T takes their tile
     const RowGates rg = row_gates(sm.gl, tm);
     // dA and dP masked -> MA^T, MP^T, and the gate-gradient partial sums (KK^T,
     // QK^T and the mask formed again here rather than held through the blocks).
@@ -1168,11 +1247,13 @@ static hipError_t wide_scan(const ChunkArgs &a, bool reverse, hipStream_t stream
     if (!reverse) {
         p.u = a.lr_u;
         p.ckpt = a.ck_state;
+        p.ckpt_lo = a.ck_state_lo;
         p.x0 = a.initial;
         p.xout = a.final_state;
     } else {
         p.n = a.ws_n;
         p.ckpt = a.ws_dstate;
+        p.ckpt_lo = a.ws_dstate_lo;
         p.x0.data = a.dfinal;
         p.x0.s0 = (int64_t)a.H * KD * KD;
         p.x0.s1 = (int64_t)KD * KD;
