@@ -117,8 +117,10 @@ def test_long8k_full_size_oracle_slices(dk, b, h):
 
 def test_decode_full_size_steps_match_scan(dk):
     """Config 3: 256 x 8 fp32 states, 1024 single-token steps.  Every step's
-    output, score and state equal the scan carrying the same initial state,
-    bitwise; one sequence is checked against the f64 oracle."""
+    output and score, and the final state, match the scan carrying the same
+    initial state (the f32 chunk kernels; decode is token-sequential) within the
+    f32 gate; one sequence of both is checked against the f64 oracle at the
+    reference's gate."""
     cfg, p = _cfg(3)
     B, T, H, K, V = cfg.batch, cfg.time, cfg.heads, cfg.keys, cfg.values
     q, k, v = dev(p["q"]), dev(p["k"]), dev(p["v"])
@@ -130,13 +132,17 @@ def test_decode_full_size_steps_match_scan(dk):
     reset = torch.zeros((B, T), device="cuda")
     r = dk.gdn_training_scan(q, k, v, a, e, w, valid, reset, s0, 16)
     state = s0.clone()
+    outs, scs = [], []
     for t in range(T):
         sl = slice(t, t + 1)
         o, sc = dk.gdn_decode_step(state, q[:, sl], k[:, sl], v[:, sl], a[:, sl], e[:, sl],
                                    w[:, sl], valid[:, sl], reset[:, sl])
-        assert torch.equal(o, r.output[:, sl]), f"step {t}: output differs from the scan"
-        assert torch.equal(sc, r.scores[:, sl, :, 0]), f"step {t}: score differs from the scan"
-    assert torch.equal(state, r.final_state)
+        outs.append(o)
+        scs.append(sc)
+    dec_out, dec_sc = torch.cat(outs, 1), torch.cat(scs, 1)
+    gate("decode output vs scan", dec_out, host(r.output), TOL_F32)
+    gate("decode scores vs scan", dec_sc, host(r.scores[..., 0]), TOL_F32)
+    gate("decode state vs scan", state, host(r.final_state), TOL_F32)
     b, h = 17, 5
     s = _slice(p, b, h)
     ah, eh, wh = (host(x[b:b + 1, :, h:h + 1]) for x in (a, e, w))
@@ -147,3 +153,5 @@ def test_decode_full_size_steps_match_scan(dk):
     gate("output", r.output[b:b + 1, :, h:h + 1], o, TOL_F32, ref_gate=True)
     gate("final_state", r.final_state[b:b + 1, h:h + 1], f, TOL_F32, ref_gate=True)
     gate("scores", r.scores[b:b + 1, :, h:h + 1, 0], c, TOL_F32, ref_gate=True)
+    gate("decode output", dec_out[b:b + 1, :, h:h + 1], o, TOL_F32, ref_gate=True)
+    gate("decode state", state[b:b + 1, h:h + 1], f, TOL_F32, ref_gate=True)
