@@ -83,8 +83,11 @@ __device__ __forceinline__ float fc_in(const View &v, int b, int tg, int h, int 
     return (on && tg < T && ch < W) ? ld4<float>(v, b, tg, h, ch) : 0.f;
 }
 
-// b_t and lam_t of channel i (threads i < K): running products of the gates.
+// b_t and lam_t of channel i (threads i < K): running products of the gates;
+// zero on the channels K .. 63, which the MFMA products read as padding.
 __device__ void fc_decay_rows(const float *al, const Masks &m, float *bt, float *lam, int K, int tid) {
+    if (tid >= K && tid < FK)
+        for (int t = 0; t < C; ++t) bt[t * LQ + tid] = lam[t * LQ + tid] = 0.f;
     if (tid < K) {
         const int i = tid, sg15 = m.seg[C - 1];
         float p = 1.f;
@@ -100,8 +103,10 @@ __device__ void fc_decay_rows(const float *al, const Masks &m, float *bt, float 
     }
 }
 
-// b_t alone (threads i < K).
+// b_t alone (threads i < K; zero on the channels K .. 63).
 __device__ void fc_b_row(const float *al, const Masks &m, float *bt, int K, int tid) {
+    if (tid >= K && tid < FK)
+        for (int t = 0; t < C; ++t) bt[t * LQ + tid] = 0.f;
     if (tid < K) {
         float p = 1.f;
         for (int t = 0; t < C; ++t) {
@@ -159,15 +164,15 @@ struct FcPrepSmem {
 
 struct FcOutSmem {
     Masks m;
-    float q[C * LQ], k[C * LQ], al[C * LQ], eh[C * LQ], wv[C * LQ], bt[C * LQ], r[C * LQ], dl[C * LQ];
-    float s0[FK * LS];
+    float q[C * LQ], k[C * LQ], al[C * LQ], eh[C * LQ], wv[C * LQ], bt[C * LQ];
+    float s0[FK * LS];  // S0, zero-padded to whole 16 x 16 tiles
     float T[C * LT], P[C * LT];
-    float kk[C], dd[C];
+    float kk[C], ddp[4][C];
 };
 
 struct FcBPrepSmem {
     Masks m;
-    float q[C * LQ], k[C * LQ], al[C * LQ], bt[C * LQ], dO[C * LQ], dl[C * LQ], x[C * LQ], w[C * LQ];
+    float q[C * LQ], k[C * LQ], al[C * LQ], bt[C * LQ], dO[C * LQ], dl[C * LQ], w[C * LQ];
     float P[C * LT];
     float cs[C];
 };
@@ -229,28 +234,38 @@ __global__ void __launch_bounds__(NT) fc_prep_kernel(FcArgs a) {
         for (int r = 0; r < C; ++r) sm.T[r * LT + j] = tc[r];
     }
     __syncthreads();
-    // W' = T (b . ehat), U = T wv, Ktil = lam . k: token t, channels 4g .. 4g + 3;
-    // W', Ktil and gv zero on the key padding up to KP.
-    const int KP = fc_kp(K);
+    // Ktil = lam . k (token t, channels 4g .. 4g + 3) and gv = b_15; zero on the
+    // key padding up to KP.
+    const int KP = fc_kp(K), KT = KP >> 4, VT = (V + 15) >> 4;
     const int64_t fo = (int64_t)ci * C;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int i = 4 * g + e;
-        if (i < KP) {
-            float wsum = 0.f;
-            if (i < K)
-                for (int q = 0; q <= t; ++q) wsum += sm.T[t * LT + q] * sm.bt[q * LQ + i] * sm.eh[q * LQ + i];
-            a.fw[(fo + t) * KP + i] = wsum;
-            a.fk[(fo + t) * KP + i] = i < K ? sm.lam[t * LQ + i] * sm.k[t * LQ + i] : 0.f;
-        }
-        if (i < V) {
-            float usum = 0.f;
-            for (int q = 0; q <= t; ++q) usum += sm.T[t * LT + q] * sm.wv[q * LQ + i];
-            a.fu[(fo + t) * V + i] = usum;
-        }
+        if (i < KP) a.fk[(fo + t) * KP + i] = i < K ? sm.lam[t * LQ + i] * sm.k[t * LQ + i] : 0.f;
     }
     if (tid < KP) a.gv[(int64_t)ci * KP + tid] = tid < K ? sm.bt[(C - 1) * LQ + tid] : 0.f;
     a.tm[(int64_t)ci * C * C + tid] = sm.T[(tid >> 4) * LT + (tid & 15)];
+    // W' = T (b . ehat) and U = T wv on v_mfma_f32_16x16x4f32: tiles 0 .. KT - 1
+    // of W' (key tiles), then VT tiles of U, taken by the waves in turn (lane
+    // (lg, ln): tokens 4 lg + r, column 16 tile + ln).
+    const int w = tid >> 6, l = tid & 63, lg = l >> 4, ln = l & 15;
+    for (int n = w; n < KT + VT; n += 4) {
+        const bool isw = n < KT;
+        const int col = 16 * (isw ? n : n - KT) + ln;
+        f32x4 x = zero4();
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int ss = 4 * lg + q;
+            const float bv = isw ? sm.bt[ss * LQ + col] * sm.eh[ss * LQ + col] : sm.wv[ss * LQ + col];
+            x = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.T[ln * LT + ss], bv, x, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tt = 4 * lg + r;
+            if (isw) a.fw[(fo + tt) * KP + col] = x[r];
+            else if (col < V) a.fu[(fo + tt) * V + col] = x[r];
+        }
+    }
 }
 
 // ---- the scan over the chunks of one (batch, head) -----------------------------
@@ -272,7 +287,12 @@ struct FcScanOps {
 
 template <int KT, bool REV>
 __device__ __forceinline__ void fc_scan_load(const FcArgs &a, int64_t ci, int cg, FcScanOps<KT> &o) {
+    // Every load is issued (indices past the widths are clamped and their values
+    // dropped by a select), so no load sits behind a branch and the compiler's
+    // memory-counter waits stay exact across the prefetch ring.
     const int K = a.s.K, V = a.s.V, KP = 16 * KT, l = lane_id(), g = l >> 4, n = l & 15, j = 16 * cg + n;
+    const bool jv = j < V;
+    const int jc = jv ? j : 0;
     const float *fw = a.fw + ci * C * KP, *fk = a.fk + ci * C * KP;
 #pragma unroll
     for (int tau = 0; tau < KT; ++tau)
@@ -286,9 +306,14 @@ __device__ __forceinline__ void fc_scan_load(const FcArgs &a, int64_t ci, int cg
             o.g[tau][s] = a.gv[ci * KP + 16 * tau + 4 * g + s];
             if (REV) {
                 const int i = 16 * tau + 4 * g + s;
-                o.a[tau][s] = (i < K && j < V) ? a.n[(ci * K + i) * V + j] : 0.f;
+                const bool in = i < K && jv;
+                const float x = a.n[(ci * K + (i < K ? i : 0)) * V + jc];
+                o.a[tau][s] = in ? x : 0.f;
+            } else if (tau == 0) {
+                const float x = a.fu[(ci * C + 4 * g + s) * V + jc];
+                o.a[tau][s] = jv ? x : 0.f;
             } else {
-                o.a[tau][s] = (tau == 0 && j < V) ? a.fu[(ci * C + 4 * g + s) * V + j] : 0.f;
+                o.a[tau][s] = 0.f;
             }
         }
 }
@@ -313,40 +338,52 @@ __global__ void __launch_bounds__(64) fc_scan_kernel(FcArgs a) {
             }
             X[tau][r] = x;
         }
-    FcScanOps<KT> cur, nxt;
-    fc_scan_load<KT, REV>(a, (int64_t)bh * a.nc + (REV ? a.nc - 1 : 0), cg, cur);
+    // A ring of D chunks' operands in registers: chunk step + D is loaded (the
+    // last chunk again past the end) as soon as step's operands are used.
+    constexpr int D = KT <= 2 ? 3 : 2;
+    FcScanOps<KT> ring[D];
+    auto chunk_at = [&](int step) {
+        const int sc = step < a.nc ? step : a.nc - 1;
+        return (int64_t)bh * a.nc + (REV ? a.nc - 1 - sc : sc);
+    };
+#pragma unroll
+    for (int d = 0; d < D; ++d) fc_scan_load<KT, REV>(a, chunk_at(d), cg, ring[d]);
     float *keep = REV ? a.ds : a.st;
-    for (int step = 0; step < a.nc; ++step) {
-        const int c = REV ? a.nc - 1 - step : step;
-        const int64_t ci = (int64_t)bh * a.nc + c;
-        if (step + 1 < a.nc) fc_scan_load<KT, REV>(a, ci + (REV ? -1 : 1), cg, nxt);
-        // the state before (forward) / the adjoint after (reverse) this chunk
+    for (int s0 = 0; s0 < a.nc; s0 += D) {
 #pragma unroll
-        for (int tau = 0; tau < KT; ++tau)
+        for (int d = 0; d < D; ++d) {
+            const int step = s0 + d;
+            if (step >= a.nc) break;
+            const int64_t ci = chunk_at(step);
+            const FcScanOps<KT> &cur = ring[d];
+            // the state before (forward) / the adjoint after (reverse) this chunk
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = 16 * tau + 4 * g + r;
-                if (i < K && jv) keep[(ci * K + i) * V + j] = X[tau][r];
+            for (int tau = 0; tau < KT; ++tau)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int i = 16 * tau + 4 * g + r;
+                    if (i < K && jv) keep[(ci * K + i) * V + j] = X[tau][r];
+                }
+            // v[t][j], t = 4 g + r: U - W' S (forward) or Ktil X (reverse)
+            f32x4 v = REV ? zero4() : f32x4{cur.a[0][0], cur.a[0][1], cur.a[0][2], cur.a[0][3]};
+#pragma unroll
+            for (int tau = 0; tau < KT; ++tau)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    v = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.w[tau][q], X[tau][q], v, 0, 0, 0);
+            // S <- diag(gv) S + Ktil^T v, or X <- diag(gv) X + N - W'^T v
+#pragma unroll
+            for (int tau = 0; tau < KT; ++tau) {
+                f32x4 x;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) x[r] = cur.g[tau][r] * X[tau][r] + (REV ? cur.a[tau][r] : 0.f);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    x = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.k[tau][q], v[q], x, 0, 0, 0);
+                X[tau] = x;
             }
-        // v[t][j], t = 4 g + r: U - W' S (forward) or Ktil X (reverse)
-        f32x4 v = REV ? zero4() : f32x4{cur.a[0][0], cur.a[0][1], cur.a[0][2], cur.a[0][3]};
-#pragma unroll
-        for (int tau = 0; tau < KT; ++tau)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                v = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.w[tau][q], X[tau][q], v, 0, 0, 0);
-        // S <- diag(gv) S (+ N) + Ktil^T v, or X <- diag(gv) X + N - W'^T v
-#pragma unroll
-        for (int tau = 0; tau < KT; ++tau) {
-            f32x4 x;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) x[r] = cur.g[tau][r] * X[tau][r] + (REV ? cur.a[tau][r] : 0.f);
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                x = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.k[tau][q], v[q], x, 0, 0, 0);
-            X[tau] = x;
+            fc_scan_load<KT, REV>(a, chunk_at(step + D), cg, ring[d]);
         }
-        cur = nxt;
     }
     float *fin = REV ? s.dinitial : s.final_state;
     if (fin)
@@ -376,6 +413,8 @@ __global__ void __launch_bounds__(NT) fc_out_kernel(FcArgs a) {
     const SeqArgs &s = a.s;
     const int tid = threadIdx.x, ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / s.H, h = bh % s.H;
     const int K = s.K, V = s.V, t = tid >> 4, g = tid & 15, tg = c * C + t;
+    const int KP = fc_kp(K), VT = (V + 15) >> 4, VP = 16 * VT;
+    const int w = tid >> 6, l = tid & 63, lg = l >> 4, ln = l & 15;
     fc_masks(s, b, c, sm.m, tid);
     const bool on = sm.m.val[t] != 0.f;
     float ksq = 0.f;
@@ -395,57 +434,61 @@ __global__ void __launch_bounds__(NT) fc_out_kernel(FcArgs a) {
     ksq += __shfl_xor(ksq, 4);
     ksq += __shfl_xor(ksq, 8);
     if (g == 0) sm.kk[t] = ksq;
-    const float *st = a.st + (int64_t)ci * K * V;
-    for (int e = tid; e < K * V; e += NT) sm.s0[(e / V) * LS + e % V] = st[e];
+    {
+        const float *st = a.st + (int64_t)ci * K * V;
+        for (int e = tid; e < KP * VP; e += NT) {
+            const int i = e / VP, j = e - i * VP;
+            sm.s0[i * LS + j] = (i < K && j < V) ? st[i * V + j] : 0.f;
+        }
+    }
     sm.T[(tid >> 4) * LT + (tid & 15)] = a.tm[(int64_t)ci * C * C + tid];
     __syncthreads();
     fc_b_row(sm.al, sm.m, sm.bt, K, tid);
     fc_tri<false>(sm.q, sm.k, sm.al, sm.m, sm.P, K, tid);  // P, lower with the diagonal
     __syncthreads();
-    // R = wv - Ahat S0 (token t, columns 4g ..)
+    // Wave w: value tile w on v_mfma_f32_16x16x4f32 (lane (lg, ln): rows 4 lg + r,
+    // column 16 w + ln).  R = wv - Ahat S0, O = Qhat S0 over the key axis; then
+    // delta = T R and O += P delta with the accumulator rows as the B operand
+    // (step q reduces over the tokens 4 lg + q).
+    if (w < VT) {
+        const int j = 16 * w + ln;
+        f32x4 x = zero4(), o = zero4();
+        for (int kk = 0; kk < KP; kk += 4) {
+            const int i = kk + lg;
+            const float sv = sm.s0[i * LS + j], bti = sm.bt[ln * LQ + i];
+            x = __builtin_amdgcn_mfma_f32_16x16x4f32(bti * sm.eh[ln * LQ + i], sv, x, 0, 0, 0);
+            o = __builtin_amdgcn_mfma_f32_16x16x4f32(bti * sm.q[ln * LQ + i], sv, o, 0, 0, 0);
+        }
+        f32x4 r, d = zero4();
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int j = 4 * g + e;
-        if (j < V) {
-            float x = 0.f;
-            for (int i = 0; i < K; ++i) x += sm.bt[t * LQ + i] * sm.eh[t * LQ + i] * sm.s0[i * LS + j];
-            sm.r[t * LQ + j] = sm.wv[t * LQ + j] - x;
+        for (int q = 0; q < 4; ++q) r[q] = sm.wv[(4 * lg + q) * LQ + j] - x[q];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            d = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.T[ln * LT + 4 * lg + q], r[q], d, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            o = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.P[ln * LT + 4 * lg + q], d[q], o, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float p = d[q] * d[q];
+            p += __shfl_xor(p, 1);
+            p += __shfl_xor(p, 2);
+            p += __shfl_xor(p, 4);
+            p += __shfl_xor(p, 8);
+            const int tt = 4 * lg + q, tq = c * C + tt;
+            if (ln == 0) sm.ddp[w][tt] = p;
+            if (j < V) {
+                a.dl[((int64_t)ci * C + tt) * V + j] = d[q];
+                if (tq < s.T) store_out(s.out, s.out_bf16, (((int64_t)b * s.T + tq) * s.H + h) * V + j, o[q]);
+            }
         }
     }
     __syncthreads();
-    // delta = T R and |delta_t|^2
-    float dsq = 0.f, dlt[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int j = 4 * g + e;
-        float x = 0.f;
-        if (j < V)
-            for (int q = 0; q <= t; ++q) x += sm.T[t * LT + q] * sm.r[q * LQ + j];
-        dlt[e] = x;
-        if (j < V) sm.dl[t * LQ + j] = x;
-        dsq += x * x;
+    if (s.scores && tid < C && c * C + tid < s.T) {
+        float dd = 0.f;
+        for (int x = 0; x < VT; ++x) dd += sm.ddp[x][tid];
+        s.scores[((int64_t)b * s.T + c * C + tid) * s.H + h] = sm.m.val[tid] != 0.f ? sqrtf(sm.kk[tid] * dd) : 0.f;
     }
-    dsq += __shfl_xor(dsq, 1);
-    dsq += __shfl_xor(dsq, 2);
-    dsq += __shfl_xor(dsq, 4);
-    dsq += __shfl_xor(dsq, 8);
-    if (g == 0) sm.dd[t] = dsq;
-    __syncthreads();
-    // O = Qhat S0 + P delta; delta to the checkpoint
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int j = 4 * g + e;
-        if (j < V) {
-            float x = 0.f;
-            for (int i = 0; i < K; ++i) x += sm.bt[t * LQ + i] * sm.q[t * LQ + i] * sm.s0[i * LS + j];
-            for (int q = 0; q <= t; ++q) x += sm.P[t * LT + q] * sm.dl[q * LQ + j];
-            if (tg < s.T) store_out(s.out, s.out_bf16, (((int64_t)b * s.T + tg) * s.H + h) * V + j, x);
-            a.dl[((int64_t)ci * C + t) * V + j] = dlt[e];
-        }
-    }
-    if (s.scores && tid < C && c * C + tid < s.T)
-        s.scores[((int64_t)b * s.T + c * C + tid) * s.H + h] =
-            sm.m.val[tid] != 0.f ? sqrtf(sm.kk[tid] * sm.dd[tid]) : 0.f;
 }
 
 // ---- bprep: N = Qhat^T dO - W'^T X, X = P^T dO + c delta ------------------------
@@ -488,31 +531,34 @@ __global__ void __launch_bounds__(NT) fc_bprep_kernel(FcArgs a) {
         sm.w[t * LQ + i] = i < K ? a.fw[((int64_t)ci * C + t) * fc_kp(K) + i] : 0.f;
     }
     __syncthreads();
-    // X = P^T dO + c delta (token t, columns 4g ..)
+    // Wave w: value tile w on v_mfma_f32_16x16x4f32 (lane (lg, ln): rows 4 lg + r,
+    // column 16 w + ln).  X = P^T dO + c delta, then per key tile tau
+    // N = Qhat^T dO - W'^T X, X's accumulator rows as the B operand.
+    const int w = tid >> 6, l = tid & 63, lg = l >> 4, ln = l & 15, VT = (V + 15) >> 4, KT = fc_kp(K) >> 4;
+    if (w < VT) {
+        const int j = 16 * w + ln;
+        f32x4 x;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int j = 4 * g + e;
-        float x = sm.cs[t] * sm.dl[t * LQ + j];
-        for (int q = t; q < C; ++q) x += sm.P[q * LT + t] * sm.dO[q * LQ + j];
-        sm.x[t * LQ + j] = x;
-    }
-    __syncthreads();
-    // N[i][j] = sum_t Qhat[t][i] dO[t][j] - W'[t][i] X[t][j]: thread (i = tid / 4,
-    // columns 16 (tid % 4) ..)
-    {
-        const int i = tid >> 2, j0 = 16 * (tid & 3);
-        if (i < K) {
-            float nacc[16];
+        for (int q = 0; q < 4; ++q) x[q] = sm.cs[4 * lg + q] * sm.dl[(4 * lg + q) * LQ + j];
 #pragma unroll
-            for (int q = 0; q < 16; ++q) nacc[q] = 0.f;
-            for (int tt = 0; tt < C; ++tt) {
-                const float qh = sm.bt[tt * LQ + i] * sm.q[tt * LQ + i], wq = sm.w[tt * LQ + i];
+        for (int q = 0; q < 4; ++q)
+            x = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.P[(4 * lg + q) * LT + ln], sm.dO[(4 * lg + q) * LQ + j], x,
+                                                     0, 0, 0);
+        for (int tau = 0; tau < KT; ++tau) {
+            const int i = 16 * tau + ln;
+            f32x4 n = zero4();
 #pragma unroll
-                for (int q = 0; q < 16; ++q) nacc[q] += qh * sm.dO[tt * LQ + j0 + q] - wq * sm.x[tt * LQ + j0 + q];
+            for (int q = 0; q < 4; ++q) {
+                const int tt = 4 * lg + q;
+                n = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.bt[tt * LQ + i] * sm.q[tt * LQ + i], sm.dO[tt * LQ + j], n,
+                                                         0, 0, 0);
+                n = __builtin_amdgcn_mfma_f32_16x16x4f32(-sm.w[tt * LQ + i], x[q], n, 0, 0, 0);
             }
 #pragma unroll
-            for (int q = 0; q < 16; ++q)
-                if (j0 + q < V) a.n[((int64_t)ci * K + i) * V + j0 + q] = nacc[q];
+            for (int r = 0; r < 4; ++r) {
+                const int ii = 16 * tau + 4 * lg + r;
+                if (ii < K && j < V) a.n[((int64_t)ci * K + ii) * V + j] = n[r];
+            }
         }
     }
 }
