@@ -22,18 +22,17 @@ struct GateBlock {
 //   T      (I + A)^-1, bf16 row-major
 //   gate   GateBlock
 //   delta  the chunk's edits delta[t][v], f32 row-major
-// plus the factored state map S_C = gam_63 S0 + Ktil^T (U - W S0) that the
-// scans read: -W^T [key][token] and Ktil = lam K [token][key] (bf16 hi, then
-// lo), U^T [value][token] (f32) and gam_63 repeated per key (f32).
+// plus the dense state map S_C = A_c S0 + B_c that the scans read: A_c rows and
+// A_c^T rows (the adjoint map M), each bf16 hi then lo [64][64], and B_c^T
+// [value][key] (f32).
 constexpr size_t CK_STATE_BYTES = CHUNK_D * CHUNK_D * sizeof(uint16_t);
 constexpr size_t CK_T_BYTES = CHUNK * CHUNK * sizeof(uint16_t);
 constexpr size_t CK_GATE_BYTES = sizeof(GateBlock);
 constexpr size_t CK_DELTA_BYTES = CHUNK * CHUNK_D * sizeof(float);
-constexpr size_t CK_LRW_BYTES = 2 * CHUNK_D * CHUNK * sizeof(uint16_t);  // hi and lo
-constexpr size_t CK_LRU_BYTES = CHUNK_D * CHUNK * sizeof(float);
-constexpr size_t CK_LRG_BYTES = CHUNK_D * sizeof(float);
+constexpr size_t CK_MAP_BYTES = 2 * CHUNK_D * CHUNK_D * sizeof(uint16_t);  // hi and lo
+constexpr size_t CK_MAPB_BYTES = CHUNK_D * CHUNK_D * sizeof(float);
 constexpr size_t CK_CHUNK_BYTES = 2 * CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES + CK_DELTA_BYTES +
-                                  2 * CK_LRW_BYTES + CK_LRU_BYTES + CK_LRG_BYTES;
+                                  2 * CK_MAP_BYTES + CK_MAPB_BYTES;
 // Backward workspace per chunk: dS at the chunk end (bf16 hi and lo,
 // transposed) and N^T of the adjoint map (f32).
 constexpr size_t WS_CHUNK_BYTES = 2 * CK_STATE_BYTES + CHUNK_D * CHUNK_D * sizeof(float);
@@ -84,6 +83,10 @@ struct ChunkArgs {
     // Ktil = lam K [C][D] (bf16), U^T [D][C] and the map's diagonal [D] (f32).
     uint16_t *lr_wt, *lr_kt;
     float *lr_u, *lr_gv;
+    // Dense chunk map (d = 64 scalar gates): A_c and M = A_c^T rows (bf16 hi
+    // then lo), B_c^T (f32).
+    uint16_t *map_m, *map_mt;
+    float *map_b;
 };
 
 // The kernel's ChunkArgs argument, read again from the kernel argument segment;
@@ -129,13 +132,11 @@ inline void chunk_bind_checkpoint(ChunkArgs &a, void *ck) {
     p += n * CK_GATE_BYTES;
     a.ck_delta = reinterpret_cast<float *>(p);
     p += n * CK_DELTA_BYTES;
-    a.lr_wt = reinterpret_cast<uint16_t *>(p);
-    p += n * CK_LRW_BYTES;
-    a.lr_kt = reinterpret_cast<uint16_t *>(p);
-    p += n * CK_LRW_BYTES;
-    a.lr_u = reinterpret_cast<float *>(p);
-    p += n * CK_LRU_BYTES;
-    a.lr_gv = reinterpret_cast<float *>(p);
+    a.map_m = reinterpret_cast<uint16_t *>(p);
+    p += n * CK_MAP_BYTES;
+    a.map_mt = reinterpret_cast<uint16_t *>(p);
+    p += n * CK_MAP_BYTES;
+    a.map_b = reinterpret_cast<float *>(p);
 }
 
 // Carve the backward workspace.

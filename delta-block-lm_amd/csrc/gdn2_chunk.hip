@@ -53,11 +53,11 @@ struct OutSmem {
 
 }  // namespace
 
-// ---- prep: gates, the UT inverse and the factored state map of every chunk ----
+// ---- prep: gates, the UT inverse and the dense state map of every chunk -------
 // W = T diag(beta gam) K and U = T diag(beta) V give the chunk's state map
-//   S_C = gam_63 S0 + (lam K)^T (U - W S0),
-// which leaves as its factors for the scan: -W^T and Ktil = lam K (bf16 hi and
-// lo), U^T (f32) and gam_63.
+//   S_C = A_c S0 + B_c,  A_c = gam_63 I - Ktil^T W,  B_c = Ktil^T U  (Ktil = lam K),
+// formed from hi/lo pairs of Ktil, W and U and stored for the scans: A_c rows
+// and A_c^T rows as bf16 hi and lo, B_c^T in f32.
 __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
     __shared__ PrepSmem sm;
     // beta gam K and beta V are staged as scaled rows; the products that need
@@ -94,7 +94,8 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         gb->seg[t] = seg;
     }
     __syncthreads();
-    {  // beta gam K rows (hi, lo) for the W product; Ktil = lam K rows (hi, lo) and gam_63 out
+    uint4 ktil_hi, ktil_lo;  // Ktil = lam K rows (hi, lo), staged once the inverse is done
+    {  // beta gam K rows (hi, lo) for the W product
         const float bg = sm.gl.beta[t] * sm.gl.gam[t], la = sm.gl.lam[t];
         Pack8 kp;
         kp.u = k8;
@@ -114,10 +115,8 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
         }
         put_row8(KBGs, t, cb, make_uint4(kb[0], kb[1], kb[2], kb[3]));
         put_row8(KBGl, t, cb, make_uint4(kbl[0], kbl[1], kbl[2], kbl[3]));
-        uint16_t *kt = a.lr_kt + ((int64_t)ci * 2 * C + t) * D + 8 * cb;
-        *reinterpret_cast<uint4 *>(kt) = make_uint4(kh[0], kh[1], kh[2], kh[3]);
-        *reinterpret_cast<uint4 *>(kt + C * D) = make_uint4(kl[0], kl[1], kl[2], kl[3]);
-        if (tid < D) a.lr_gv[(int64_t)ci * D + tid] = sm.gl.gamC;
+        ktil_hi = make_uint4(kh[0], kh[1], kh[2], kh[3]);
+        ktil_lo = make_uint4(kl[0], kl[1], kl[2], kl[3]);
     }
     // A = strict_lower(beta_t Gam_ts k_t.k_s) in f32 (tiles with tn <= tm only).
     if (tn0 <= tm) {
@@ -168,28 +167,64 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
             vb[e / 2] = bf16_pack2(be * bf16_val(vp.h[e]), be * bf16_val(vp.h[e + 1]));
         put_row8(VBs, t, cb, make_uint4(vb[0], vb[1], vb[2], vb[3]));
     }
+    __syncthreads();  // T staged; the inverse's scratch is free: Ktil rows (hi, lo) take it
+    uint16_t *KLs = reinterpret_cast<uint16_t *>(sm.inv.Af), *KLl = KLs + TILE;
+    static_assert(sizeof(sm.inv) >= 2 * TILE * sizeof(uint16_t), "Ktil hi/lo over the inverse's scratch");
+    put_row8(KLs, t, cb, ktil_hi);
+    put_row8(KLl, t, cb, ktil_lo);
+    // W = T (beta gam K), U = T (beta V) in registers ...
+    f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
+    gemm2_tr(x, &Tb[(16 * tm) * LDB], KBGs, tn0);  // B[k][t] = (beta gam K)[t][k]
+    gemm2_tr(x, &Tb[(16 * tm) * LDB], KBGl, tn0);
+    gemm2_tr(y, &Tb[(16 * tm) * LDB], VBs, tn0);   // B[v][t] = (beta V)[t][v]
+    __syncthreads();  // T, beta gam K and beta V read: W^T and U^T (hi, lo) take their slots
+    uint16_t *Wt = sm.slot[0], *Wtl = sm.slot[1], *Ut = sm.slot[2], *Utl = sm.slot[3];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        store_tile_t_split(&Wt[(16 * (tn0 + j)) * LDB + 16 * tm], &Wtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, x[j]);
+        store_tile_t_split(&Ut[(16 * (tn0 + j)) * LDB + 16 * tm], &Utl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, y[j]);
+    }
     __syncthreads();
-    // W = T (beta gam K), U = T (beta V), straight from the accumulators: -W^T
-    // (bf16 hi and lo) and U^T (f32), [column][token].  bprep forms W again
-    // from T and K with the same operands and products.
+    // ... then A_c = gam_63 I - Ktil^T W and B_c = Ktil^T U over the three terms
+    // of the hi/lo pairs (tile rows: key 16 tm + .., columns 16 (tn0 + j) + ..).
+    f32x4 am[2] = {zero4(), zero4()}, bm[2] = {zero4(), zero4()};
+    gemm2_atr(am, KLs, 16 * tm, Wt, tn0);  // A[k][t] = Ktil[t][k]
+    gemm2_atr(am, KLs, 16 * tm, Wtl, tn0);
+    gemm2_atr(am, KLl, 16 * tm, Wt, tn0);
+    gemm2_atr(bm, KLs, 16 * tm, Ut, tn0);
+    gemm2_atr(bm, KLs, 16 * tm, Utl, tn0);
+    gemm2_atr(bm, KLl, 16 * tm, Ut, tn0);
     {
-        f32x4 x[2] = {zero4(), zero4()}, y[2] = {zero4(), zero4()};
-        gemm2_tr(x, &Tb[(16 * tm) * LDB], KBGs, tn0);  // B[k][t] = (beta gam K)[t][k]
-        gemm2_tr(x, &Tb[(16 * tm) * LDB], KBGl, tn0);
-        gemm2_tr(y, &Tb[(16 * tm) * LDB], VBs, tn0);   // B[v][t] = (beta V)[t][v]
+        const float gC = sm.gl.gamC;
+        float *Bt = a.map_b + (int64_t)ci * D * D;  // B_c^T [value][key]
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int64_t row = (int64_t)(16 * (tn0 + j) + acc_col()) * C + 16 * tm + acc_row(0);
-            uint16_t *wt = a.lr_wt + (int64_t)ci * 2 * D * C + row;
-            uint16_t h[4], o[4];
+            const int cc = 16 * (tn0 + j) + acc_col();
 #pragma unroll
-            for (int i = 0; i < 4; ++i) split_bf16(-x[j][i], h[i], o[i]);
-            *reinterpret_cast<uint2 *>(wt) =
-                make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
-            *reinterpret_cast<uint2 *>(wt + D * C) =
-                make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
-            *reinterpret_cast<float4 *>(a.lr_u + (int64_t)ci * D * C + row) =
-                make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
+            for (int i = 0; i < 4; ++i) am[j][i] = (16 * tm + acc_row(i) == cc ? gC : 0.f) - am[j][i];
+            *reinterpret_cast<float4 *>(&Bt[cc * D + 16 * tm + acc_row(0)]) =
+                make_float4(bm[j][0], bm[j][1], bm[j][2], bm[j][3]);
+        }
+    }
+    __syncthreads();  // W^T and U^T read: A_c^T (hi, lo) takes their slots
+    uint16_t *Mt = sm.slot[0], *Mtl = sm.slot[1];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        store_tile_t_split(&Mt[(16 * (tn0 + j)) * LDB + 16 * tm], &Mtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, am[j]);
+    __syncthreads();
+    // Rows out, hi then lo: M = A_c^T row by row (the adjoint scan's map), and A_c
+    // (the state scan's) read across it: lane (row 16 (w%4) + l%16, columns
+    // 32 (w/4) + 8 (l/16) ..) stores one 16-byte row piece.
+    {
+        const int r = tid >> 3, c0 = 8 * (tid & 7), l = lane_id();
+        uint16_t *mt = a.map_mt + (int64_t)ci * 2 * D * D, *mm = a.map_m + (int64_t)ci * 2 * D * D;
+        const int64_t fo = (int64_t)(16 * (w & 3) + (l & 15)) * D + 32 * (w >> 2) + 8 * (l >> 4);
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+            const uint16_t *src = part == 0 ? Mt : Mtl;
+            *reinterpret_cast<uint4 *>(mt + part * D * D + r * D + c0) =
+                *reinterpret_cast<const uint4 *>(&src[r * LDB + c0]);
+            *reinterpret_cast<bf16x8_t *>(mm + part * D * D + fo) = frag_tr(src, 32 * (w >> 2), 16 * (w & 3));
         }
     }
 }
@@ -353,26 +388,193 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
     }
 }
 
-// The state scan over a head's chunks (gdn2_chunk_lr.hip): forward (chunk-start
-// states and their lo parts, from prep's factors) or reverse (chunk-end state
-// adjoints and their lo parts, N from bprep).
+// ---- affine scan: the sequential part -------------------------------------------
+// X_next = M_c X + N_c over the chunks of one (batch, head): forward (M = A_c,
+// N = B_c; X0 = the initial state; X before each step = the chunk-start state)
+// or reverse (M = A_c^T, N from bprep; X0 = the final-state adjoint; X before
+// each step = the chunk-end state adjoint).  X before each step goes to the
+// checkpoint transposed (X^T rows), as bf16 hi and lo.  One workgroup per head,
+// seven waves:
+//   waves 0-3  compute: wave w owns state columns 16 w .. 16 w + 15 in MFMA
+//              accumulators; per step it writes X^T hi/lo into its LDS tiles
+//              (the B operand of the product and the writer's source), passes
+//              the step's barrier and forms N + M_hi X_hi + M_hi X_lo + M_lo X_hi
+//              (24 MFMAs, four independent accumulator tiles);
+//   wave 4     streams M (hi, then lo) into an LDS ring with LDS-DMA loads,
+//              AS_MRING - 1 chunks ahead;
+//   wave 6     streams N^T (f32) the same way;
+//   wave 5     copies each step's X^T tiles to the checkpoint.
+// The compute waves issue no global memory operations inside the loop.  LDS
+// rows are swizzled by 16-byte chunk against bank conflicts.
+namespace {
+constexpr int AS_MRING = 3;
+constexpr int AS_NRING = 3;
+constexpr int AS_MOPS = 2 * D * D * 2 / 1024;  // LDS-DMA instructions per map (hi + lo, 1 KiB each)
+constexpr int AS_NOPS = D * D * 4 / 1024;      // per N^T (f32)
+constexpr int AS_THREADS = 7 * 64;
+
+struct AsArgs {
+    int nc, B, H;
+    const uint16_t *m;  // per chunk: M rows, bf16 hi [64][64] then lo [64][64]
+    const float *n;     // per chunk: N^T rows, f32 [64][64]
+    uint16_t *ckpt, *ckpt_lo;  // X^T per chunk, bf16 hi and lo
+    View x0;            // [B,H,64,64] strided (data may be null: zero)
+    float *xout;        // [B,H,64,64] dense (may be null)
+    int reverse;
+};
+
+struct AsSmem {
+    uint4 m[AS_MRING][2 * D * D / 8];  // row r (hi rows 0..63, lo rows 64..127): chunk x at x ^ (r & 7)
+    uint4 n[AS_NRING][D * D / 4];      // N^T row j: chunk x (four f32) at x ^ (j & 15)
+    uint16_t xs[2][4][2][16 * LDB];    // [step parity][compute wave][hi, lo]: X^T [col][row]
+};
+
+// s_waitcnt immediates (gfx9 encoding): vmcnt <= n only; lgkmcnt == 0 only.
+constexpr int as_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int AS_LGKMCNT_ZERO = 15 | (3 << 14) | (7 << 4);
+
+__device__ __forceinline__ void as_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+}  // namespace
+
+__global__ void __launch_bounds__(AS_THREADS) affine_scan_kernel(AsArgs p) {
+    extern __shared__ __align__(1024) char as_lds[];
+    AsSmem &sm = *reinterpret_cast<AsSmem *>(as_lds);
+    const int bh = blockIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
+    typedef __attribute__((address_space(1))) const void *gptr;
+    typedef __attribute__((address_space(3))) void *lptr;
+    auto chunk_of = [&](int s) {
+        const int sc = min(s, p.nc - 1);
+        return (int64_t)bh * p.nc + (p.reverse ? p.nc - 1 - sc : sc);
+    };
+    if (w == 4) {  // producer: M (hi and lo), AS_MRING - 1 chunks ahead
+        auto issue = [&](int s) {
+            const uint16_t *M = p.m + chunk_of(s) * 2 * D * D;
+            uint4 *slot = sm.m[s % AS_MRING];
+#pragma unroll
+            for (int i = 0; i < AS_MOPS; ++i) {
+                const int q = 64 * i + l, r = q >> 3, x = q & 7;
+                __builtin_amdgcn_global_load_lds((gptr)(M + r * D + 8 * (x ^ (r & 7))), (lptr)(slot + 64 * i), 16,
+                                                 0, 0);
+            }
+        };
+        for (int s = 0; s < AS_MRING - 1; ++s) issue(s);
+        for (int s = 0; s < p.nc; ++s) {
+            // chunk s has landed once no more than the AS_MRING - 2 later maps are in flight
+            __builtin_amdgcn_s_waitcnt(as_vmcnt((AS_MRING - 2) * AS_MOPS));
+            as_barrier();
+            issue(s + AS_MRING - 1);  // into the slot that step s - 1 read
+        }
+        __builtin_amdgcn_s_waitcnt(as_vmcnt(0));
+        return;
+    }
+    if (w == 6) {  // producer: N^T, AS_NRING - 1 chunks ahead
+        auto issue = [&](int s) {
+            const float *N = p.n + chunk_of(s) * D * D;
+            uint4 *slot = sm.n[s % AS_NRING];
+#pragma unroll
+            for (int i = 0; i < AS_NOPS; ++i) {
+                const int q = 64 * i + l, jj = q >> 4, x = q & 15;
+                __builtin_amdgcn_global_load_lds((gptr)(N + jj * D + 4 * (x ^ (jj & 15))), (lptr)(slot + 64 * i), 16,
+                                                 0, 0);
+            }
+        };
+        for (int s = 0; s < AS_NRING - 1; ++s) issue(s);
+        for (int s = 0; s < p.nc; ++s) {
+            __builtin_amdgcn_s_waitcnt(as_vmcnt((AS_NRING - 2) * AS_NOPS));
+            as_barrier();
+            issue(s + AS_NRING - 1);
+        }
+        __builtin_amdgcn_s_waitcnt(as_vmcnt(0));
+        return;
+    }
+    if (w == 5) {  // writer: X^T before step s -> the checkpoint of chunk c(s)
+        for (int s = 0; s < p.nc; ++s) {
+            as_barrier();
+            const int64_t co = chunk_of(s) * D * D;
+#pragma unroll
+            for (int part = 0; part < 2; ++part) {
+                uint16_t *ck = part == 0 ? p.ckpt : p.ckpt_lo;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {  // 4 compute waves x 16 columns x 64 rows
+                    const int q = 64 * i + l, cw = q >> 7, col = (q >> 3) & 15, r8 = 8 * (q & 7);
+                    const uint4 v = *reinterpret_cast<const uint4 *>(&sm.xs[s & 1][cw][part][col * LDB + r8]);
+                    *reinterpret_cast<uint4 *>(&ck[co + (16 * cw + col) * D + r8]) = v;
+                }
+            }
+        }
+        return;
+    }
+    const int b = bh / p.H, h = bh % p.H, g = l >> 4, n = l & 15;
+    const int j = 16 * w + n;  // this lane's state column
+    f32x4 X[4];
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) X[tm][i] = p.x0.data ? ld4<float>(p.x0, b, h, 16 * tm + 4 * g + i, j) : 0.f;
+    for (int s = 0; s < p.nc; ++s) {
+        uint16_t *xh = sm.xs[s & 1][w][0], *xl = sm.xs[s & 1][w][1];
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) store_tile_t_split(xh + 16 * tm, xl + 16 * tm, LDB, X[tm]);
+        // The writer wave reads these tiles after the barrier, and the LDS writes of
+        // different waves may complete out of issue order: wait until they landed.
+        __builtin_amdgcn_s_waitcnt(AS_LGKMCNT_ZERO);
+        as_barrier();  // this step's M and N are in their slots; the writer may read X^T
+        const uint4 *slot = sm.m[s % AS_MRING];
+        const float4 *nslot = reinterpret_cast<const float4 *>(sm.n[s % AS_NRING]);
+        f32x4 Y[4], Z[4];
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) {  // N[16 tm + 4 g + i][j]: chunk 4 tm + g of N^T row j
+            const float4 nv = nslot[j * 16 + ((4 * tm + g) ^ (j & 15))];
+            Y[tm] = f32x4{nv.x, nv.y, nv.z, nv.w};
+            Z[tm] = zero4();
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const bf16x8_t bh_ = frag(xh, LDB, 32 * kk), bl_ = frag(xl, LDB, 32 * kk);
+#pragma unroll
+            for (int tm = 0; tm < 4; ++tm) {
+                const int r = 16 * tm + n, q = 4 * kk + g;
+                const bf16x8_t mh = __builtin_bit_cast(bf16x8_t, slot[r * 8 + (q ^ (r & 7))]);
+                const bf16x8_t ml = __builtin_bit_cast(bf16x8_t, slot[512 + r * 8 + (q ^ (r & 7))]);
+                Y[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mh, bh_, Y[tm], 0, 0, 0);
+                Z[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mh, bl_, Z[tm], 0, 0, 0);
+                Z[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ml, bh_, Z[tm], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) X[tm][i] = Y[tm][i] + Z[tm][i];
+    }
+    if (p.xout)
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p.xout[((int64_t)bh * D + 16 * tm + 4 * g + i) * D + j] = X[tm][i];
+}
+
+// The scan over a head's chunks: forward (chunk-start states and their lo
+// parts, A_c and B_c^T from prep) or reverse (chunk-end state adjoints and
+// their lo parts, A_c^T and N^T from bprep).
 hipError_t launch_chunk_scan(const ChunkArgs &a, bool reverse, hipStream_t stream) {
-    LrScanArgs p{};
+    AsArgs p{};
     p.nc = a.nc;
     p.B = a.B;
     p.H = a.H;
-    p.vd = D;
-    p.wt = a.lr_wt;
-    p.kt = a.lr_kt;
-    p.gv = a.lr_gv;
     p.reverse = reverse ? 1 : 0;
     if (!reverse) {
-        p.u = a.lr_u;
+        p.m = a.map_m;
+        p.n = a.map_b;
         p.ckpt = a.ck_state;
         p.ckpt_lo = a.ck_state_lo;
         p.x0 = a.initial;
         p.xout = a.final_state;
     } else {
+        p.m = a.map_mt;
         p.n = a.ws_n;
         p.ckpt = a.ws_dstate;
         p.ckpt_lo = a.ws_dstate_lo;
@@ -383,7 +585,15 @@ hipError_t launch_chunk_scan(const ChunkArgs &a, bool reverse, hipStream_t strea
         p.x0.s3 = 1;
         p.xout = a.dinitial;
     }
-    return launch_lr_scan(p, D, C, stream);
+    constexpr size_t lds = sizeof(AsSmem);
+    static_assert(lds <= 160 * 1024, "rings and staging fit LDS");
+    // The kernel's dynamic LDS limit, raised once per process (a function-local
+    // static: initialised exactly once even with concurrent first callers).
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void *)affine_scan_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(affine_scan_kernel, dim3(a.B * a.H), dim3(AS_THREADS), lds, stream, p);
+    return hipGetLastError();
 }
 
 static inline void mark(const hipEvent_t *ev, int i, hipStream_t stream) {

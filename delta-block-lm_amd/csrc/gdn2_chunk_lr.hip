@@ -375,9 +375,6 @@ hipError_t launch_lr_scan(const LrScanArgs &p, int kd, int ct, hipStream_t strea
     if (kd == 128 && ct == 64 && p.vd % 32 == 0)
         return p.reverse ? launch_lr<LrCfg<128, 64, 2, 3, 2, true, true, false>>(p, stream)
                          : launch_lr<LrCfg<128, 64, 2, 3, 2, false, true, false>>(p, stream);
-    if (kd == 64 && ct == 64 && p.vd % 32 == 0)
-        return p.reverse ? launch_lr<LrCfg<64, 64, 2, 3, 3, true, true, true>>(p, stream)
-                         : launch_lr<LrCfg<64, 64, 2, 3, 3, false, true, true>>(p, stream);
     if (kd == 64 && ct == 16 && p.vd % 16 == 0)
         return p.reverse ? launch_lr<LrCfg<64, 16, 1, 1, 5, true, true, true>>(p, stream)
                          : launch_lr<LrCfg<64, 16, 1, 1, 7, false, true, true>>(p, stream);
