@@ -22,9 +22,9 @@ struct GateBlock {
 //   T      (I + A)^-1, bf16 row-major
 //   gate   GateBlock
 //   delta  the chunk's edits delta[t][v], f32 row-major
-// plus the dense state map S_C = A_c S0 + B_c that the scans read: A_c rows,
-// bf16 hi then lo [64][64] (the adjoint scan reads it across, as A_c^T), and
-// B_c^T [value][key] (f32).
+// plus the dense state map S_C = A_c S0 + B_c that the scans read: A_c rows and
+// A_c^T rows (the adjoint map M), each bf16 hi then lo [64][64], and B_c^T
+// [value][key] (f32).
 constexpr size_t CK_STATE_BYTES = CHUNK_D * CHUNK_D * sizeof(uint16_t);
 constexpr size_t CK_T_BYTES = CHUNK * CHUNK * sizeof(uint16_t);
 constexpr size_t CK_GATE_BYTES = sizeof(GateBlock);
@@ -32,7 +32,7 @@ constexpr size_t CK_DELTA_BYTES = CHUNK * CHUNK_D * sizeof(float);
 constexpr size_t CK_MAP_BYTES = 2 * CHUNK_D * CHUNK_D * sizeof(uint16_t);  // hi and lo
 constexpr size_t CK_MAPB_BYTES = CHUNK_D * CHUNK_D * sizeof(float);
 constexpr size_t CK_CHUNK_BYTES = 2 * CK_STATE_BYTES + CK_T_BYTES + CK_GATE_BYTES + CK_DELTA_BYTES +
-                                  CK_MAP_BYTES + CK_MAPB_BYTES;
+                                  2 * CK_MAP_BYTES + CK_MAPB_BYTES;
 // Backward workspace per chunk: dS at the chunk end (bf16 hi and lo,
 // transposed) and N^T of the adjoint map (f32).
 constexpr size_t WS_CHUNK_BYTES = 2 * CK_STATE_BYTES + CHUNK_D * CHUNK_D * sizeof(float);
@@ -83,9 +83,9 @@ struct ChunkArgs {
     // Ktil = lam K [C][D] (bf16), U^T [D][C] and the map's diagonal [D] (f32).
     uint16_t *lr_wt, *lr_kt;
     float *lr_u, *lr_gv;
-    // Dense chunk map (d = 64 scalar gates): A_c rows (bf16 hi then lo), B_c^T
-    // (f32).
-    uint16_t *map_m;
+    // Dense chunk map (d = 64 scalar gates): A_c and M = A_c^T rows (bf16 hi
+    // then lo), B_c^T (f32).
+    uint16_t *map_m, *map_mt;
     float *map_b;
 };
 
@@ -133,6 +133,8 @@ inline void chunk_bind_checkpoint(ChunkArgs &a, void *ck) {
     a.ck_delta = reinterpret_cast<float *>(p);
     p += n * CK_DELTA_BYTES;
     a.map_m = reinterpret_cast<uint16_t *>(p);
+    p += n * CK_MAP_BYTES;
+    a.map_mt = reinterpret_cast<uint16_t *>(p);
     p += n * CK_MAP_BYTES;
     a.map_b = reinterpret_cast<float *>(p);
 }

@@ -57,7 +57,7 @@ struct OutSmem {
 // W = T diag(beta gam) K and U = T diag(beta) V give the chunk's state map
 //   S_C = A_c S0 + B_c,  A_c = gam_63 I - Ktil^T W,  B_c = Ktil^T U  (Ktil = lam K),
 // formed from hi/lo pairs of Ktil, W and U and stored for the scans: A_c rows
-// as bf16 hi and lo (the adjoint scan reads them across), B_c^T in f32.
+// and A_c^T rows as bf16 hi and lo, B_c^T in f32.
 __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
     __shared__ PrepSmem sm;
     // beta gam K and beta V are staged as scaled rows; the products that need
@@ -212,16 +212,20 @@ __global__ void __launch_bounds__(NT) chunk_prep_kernel(ChunkArgs a) {
     for (int j = 0; j < 2; ++j)
         store_tile_t_split(&Mt[(16 * (tn0 + j)) * LDB + 16 * tm], &Mtl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, am[j]);
     __syncthreads();
-    // A_c rows out, hi then lo, read across A_c^T: lane (row 16 (w%4) + l%16,
-    // columns 32 (w/4) + 8 (l/16) ..) stores one 16-byte row piece.
+    // Rows out, hi then lo: M = A_c^T row by row (the adjoint scan's map), and A_c
+    // (the state scan's) read across it: lane (row 16 (w%4) + l%16, columns
+    // 32 (w/4) + 8 (l/16) ..) stores one 16-byte row piece.
     {
-        const int l = lane_id();
-        uint16_t *mm = a.map_m + (int64_t)ci * 2 * D * D;
+        const int r = tid >> 3, c0 = 8 * (tid & 7), l = lane_id();
+        uint16_t *mt = a.map_mt + (int64_t)ci * 2 * D * D, *mm = a.map_m + (int64_t)ci * 2 * D * D;
         const int64_t fo = (int64_t)(16 * (w & 3) + (l & 15)) * D + 32 * (w >> 2) + 8 * (l >> 4);
 #pragma unroll
-        for (int part = 0; part < 2; ++part)
-            *reinterpret_cast<bf16x8_t *>(mm + part * D * D + fo) =
-                frag_tr(part == 0 ? Mt : Mtl, 32 * (w >> 2), 16 * (w & 3));
+        for (int part = 0; part < 2; ++part) {
+            const uint16_t *src = part == 0 ? Mt : Mtl;
+            *reinterpret_cast<uint4 *>(mt + part * D * D + r * D + c0) =
+                *reinterpret_cast<const uint4 *>(&src[r * LDB + c0]);
+            *reinterpret_cast<bf16x8_t *>(mm + part * D * D + fo) = frag_tr(src, 32 * (w >> 2), 16 * (w & 3));
+        }
     }
 }
 
@@ -387,10 +391,10 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
 // ---- affine scan: the sequential part -------------------------------------------
 // X_next = M_c X + N_c over the chunks of one (batch, head): forward (M = A_c,
 // N = B_c; X0 = the initial state; X before each step = the chunk-start state)
-// or reverse (M = A_c^T, read across the A_c rows with transpose reads; N from
-// bprep; X0 = the final-state adjoint; X before each step = the chunk-end state
-// adjoint).  X before each step goes to the checkpoint transposed (X^T rows), as
-// bf16 hi and lo.  One workgroup per head, seven waves:
+// or reverse (M = A_c^T, N from bprep; X0 = the final-state adjoint; X before
+// each step = the chunk-end state adjoint).  X before each step goes to the
+// checkpoint transposed (X^T rows), as bf16 hi and lo.  One workgroup per head,
+// seven waves:
 //   waves 0-3  compute: wave w owns state columns 16 w .. 16 w + 15 in MFMA
 //              accumulators; per step it writes X^T hi/lo into its LDS tiles
 //              (the B operand of the product and the writer's source), passes
@@ -401,9 +405,7 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
 //   wave 6     streams N^T (f32) the same way;
 //   wave 5     copies each step's X^T tiles to the checkpoint.
 // The compute waves issue no global memory operations inside the loop.  LDS
-// rows of M are swizzled by 16-byte chunk (as_swz) so that both the row reads
-// of the forward scan and the transpose reads of the reverse scan are free of
-// bank conflicts.
+// rows are swizzled by 16-byte chunk against bank conflicts.
 namespace {
 constexpr int AS_MRING = 3;
 constexpr int AS_NRING = 3;
@@ -413,46 +415,18 @@ constexpr int AS_THREADS = 7 * 64;
 
 struct AsArgs {
     int nc, B, H;
-    const uint16_t *m;  // per chunk: A_c rows, bf16 hi [64][64] then lo [64][64]
+    const uint16_t *m;  // per chunk: M rows, bf16 hi [64][64] then lo [64][64]
     const float *n;     // per chunk: N^T rows, f32 [64][64]
     uint16_t *ckpt, *ckpt_lo;  // X^T per chunk, bf16 hi and lo
     View x0;            // [B,H,64,64] strided (data may be null: zero)
     float *xout;        // [B,H,64,64] dense (may be null)
 };
 
-// The slot position of 16-byte chunk x of map row r is x ^ as_swz(r).  A row read
-// (lane i of 8 reads row r0 + i, one chunk) meets 8 distinct positions because
-// as_swz is a bijection on every aligned group of 8 rows; a transpose read
-// (16 lanes read rows r0 + 0..3, chunks 2m and 2m + 1, r0 a multiple of 4) meets
-// 8 distinct positions because as_swz(r) / 2 is distinct over those 4 rows.
-__device__ __forceinline__ int as_swz(int r) { return 2 * (r & 3) + ((r >> 2) & 1); }
-
 struct AsSmem {
-    uint4 m[AS_MRING][2 * D * D / 8];  // row r (hi rows 0..63, lo rows 64..127): chunk x at x ^ as_swz(r)
+    uint4 m[AS_MRING][2 * D * D / 8];  // row r (hi rows 0..63, lo rows 64..127): chunk x at x ^ (r & 7)
     uint4 n[AS_NRING][D * D / 4];      // N^T row j: chunk x (four f32) at x ^ (j & 15)
     uint16_t xs[2][4][2][16 * LDB];    // [step parity][compute wave][hi, lo]: X^T [col][row]
 };
-
-// The A-operand fragment of map rows 16 tm + l%16, reduction offset 32 kk:
-// REV false, row pieces of M = A_c; REV true, the same fragment of A_c^T, i.e.
-// lane (n, g) gets A_c[32 kk + 8 g + e][16 tm + n], e < 8, by two transpose
-// reads (one per four rows) of the swizzled rows.  base: the hi or lo rows.
-template <bool REV>
-__device__ __forceinline__ bf16x8_t as_frag(const uint4 *base, int tm, int kk) {
-    const int l = lane_id(), n = l & 15, g = l >> 4;
-    if constexpr (!REV) {
-        const int r = 16 * tm + n, q = 4 * kk + g;
-        return __builtin_bit_cast(bf16x8_t, base[r * 8 + (q ^ as_swz(r))]);
-    } else {
-        const uint16_t *e = reinterpret_cast<const uint16_t *>(base);
-        const int r = 32 * kk + 8 * g + (n >> 2), c = 16 * tm + 4 * (n & 3);
-        const v4s x = lds_tr16(e + r * D + 8 * ((c >> 3) ^ as_swz(r)) + (c & 7));
-        const v4s y = lds_tr16(e + (r + 4) * D + 8 * ((c >> 3) ^ as_swz(r + 4)) + (c & 7));
-        typedef short v8s __attribute__((ext_vector_type(8)));
-        const v8s v = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
-        return __builtin_bit_cast(bf16x8_t, v);
-    }
-}
 
 // s_waitcnt immediates (gfx9 encoding): vmcnt <= n only; lgkmcnt == 0 only.
 constexpr int as_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
@@ -465,6 +439,7 @@ __device__ __forceinline__ void as_barrier() {
 }
 }  // namespace
 
+// REV: the reverse scan (chunks walked from the last).
 template <bool REV>
 __global__ void __launch_bounds__(AS_THREADS) affine_scan_kernel(AsArgs p) {
     extern __shared__ __align__(1024) char as_lds[];
@@ -483,8 +458,8 @@ __global__ void __launch_bounds__(AS_THREADS) affine_scan_kernel(AsArgs p) {
 #pragma unroll
             for (int i = 0; i < AS_MOPS; ++i) {
                 const int q = 64 * i + l, r = q >> 3, x = q & 7;
-                __builtin_amdgcn_global_load_lds((gptr)(M + r * D + 8 * (x ^ as_swz(r))), (lptr)(slot + 64 * i),
-                                                 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((gptr)(M + r * D + 8 * (x ^ (r & 7))), (lptr)(slot + 64 * i), 16,
+                                                 0, 0);
             }
         };
         for (int s = 0; s < AS_MRING - 1; ++s) issue(s);
@@ -563,7 +538,9 @@ __global__ void __launch_bounds__(AS_THREADS) affine_scan_kernel(AsArgs p) {
             const bf16x8_t bh_ = frag(xh, LDB, 32 * kk), bl_ = frag(xl, LDB, 32 * kk);
 #pragma unroll
             for (int tm = 0; tm < 4; ++tm) {
-                const bf16x8_t mh = as_frag<REV>(slot, tm, kk), ml = as_frag<REV>(slot + 512, tm, kk);
+                const int r = 16 * tm + n, q = 4 * kk + g;
+                const bf16x8_t mh = __builtin_bit_cast(bf16x8_t, slot[r * 8 + (q ^ (r & 7))]);
+                const bf16x8_t ml = __builtin_bit_cast(bf16x8_t, slot[512 + r * 8 + (q ^ (r & 7))]);
                 Y[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mh, bh_, Y[tm], 0, 0, 0);
                 Z[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mh, bl_, Z[tm], 0, 0, 0);
                 Z[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ml, bh_, Z[tm], 0, 0, 0);
@@ -583,20 +560,21 @@ __global__ void __launch_bounds__(AS_THREADS) affine_scan_kernel(AsArgs p) {
 
 // The scan over a head's chunks: forward (chunk-start states and their lo
 // parts, A_c and B_c^T from prep) or reverse (chunk-end state adjoints and
-// their lo parts, A_c^T read across prep's A_c rows, and N^T from bprep).
+// their lo parts, A_c^T and N^T from bprep).
 hipError_t launch_chunk_scan(const ChunkArgs &a, bool reverse, hipStream_t stream) {
     AsArgs p{};
     p.nc = a.nc;
     p.B = a.B;
     p.H = a.H;
-    p.m = a.map_m;
     if (!reverse) {
+        p.m = a.map_m;
         p.n = a.map_b;
         p.ckpt = a.ck_state;
         p.ckpt_lo = a.ck_state_lo;
         p.x0 = a.initial;
         p.xout = a.final_state;
     } else {
+        p.m = a.map_mt;
         p.n = a.ws_n;
         p.ckpt = a.ws_dstate;
         p.ckpt_lo = a.ws_dstate_lo;
