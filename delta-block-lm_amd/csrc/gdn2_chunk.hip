@@ -393,25 +393,30 @@ __global__ void __launch_bounds__(NT) chunk_out_kernel(ChunkArgs a) {
 // N = B_c; X0 = the initial state; X before each step = the chunk-start state)
 // or reverse (M = A_c^T, N from bprep; X0 = the final-state adjoint; X before
 // each step = the chunk-end state adjoint).  X before each step goes to the
-// checkpoint transposed (X^T rows), as bf16 hi and lo.  One workgroup per head,
-// seven waves:
-//   waves 0-3  compute: wave w owns state columns 16 w .. 16 w + 15 in MFMA
-//              accumulators; per step it writes X^T hi/lo into its LDS tiles
-//              (the B operand of the product and the writer's source), passes
-//              the step's barrier and forms N + M_hi X_hi + M_hi X_lo + M_lo X_hi
-//              (24 MFMAs, four independent accumulator tiles);
-//   wave 4     streams M (hi, then lo) into an LDS ring with LDS-DMA loads,
+// checkpoint transposed (X^T rows), as bf16 hi and lo.  The state's columns
+// evolve independently, so each head's scan is split over AS_SPLIT workgroups
+// of 16 AS_CW columns each (the workgroups of one head read the same maps; their
+// block indices differ by a multiple of B*H, so with B*H a multiple of the XCD
+// count they share an L2).  AS_CW + 3 waves per workgroup:
+//   waves 0 .. AS_CW-1  compute: wave w owns state columns j0 + 16 w .. + 15 in
+//              MFMA accumulators; per step it writes X^T hi/lo into its LDS
+//              tiles (the B operand of the product and the writer's source),
+//              passes the step's barrier and forms N + M_hi X_hi + M_hi X_lo +
+//              M_lo X_hi (24 MFMAs, four independent accumulator tiles);
+//   wave AS_CW      streams M (hi, then lo) into an LDS ring with LDS-DMA loads,
 //              AS_MRING - 1 chunks ahead;
-//   wave 6     streams N^T (f32) the same way;
-//   wave 5     copies each step's X^T tiles to the checkpoint.
+//   wave AS_CW + 1  streams the workgroup's rows of N^T (f32) the same way;
+//   wave AS_CW + 2  copies each step's X^T tiles to the checkpoint.
 // The compute waves issue no global memory operations inside the loop.  LDS
 // rows are swizzled by 16-byte chunk against bank conflicts.
 namespace {
+constexpr int AS_CW = 2;               // compute waves per workgroup
+constexpr int AS_SPLIT = 4 / AS_CW;    // workgroups per head
 constexpr int AS_MRING = 3;
 constexpr int AS_NRING = 3;
-constexpr int AS_MOPS = 2 * D * D * 2 / 1024;  // LDS-DMA instructions per map (hi + lo, 1 KiB each)
-constexpr int AS_NOPS = D * D * 4 / 1024;      // per N^T (f32)
-constexpr int AS_THREADS = 7 * 64;
+constexpr int AS_MOPS = 2 * D * D * 2 / 1024;       // LDS-DMA instructions per map (hi + lo, 1 KiB each)
+constexpr int AS_NOPS = 16 * AS_CW * D * 4 / 1024;  // per workgroup's rows of N^T (f32)
+constexpr int AS_THREADS = (AS_CW + 3) * 64;
 
 struct AsArgs {
     int nc, B, H;
@@ -423,9 +428,9 @@ struct AsArgs {
 };
 
 struct AsSmem {
-    uint4 m[AS_MRING][2 * D * D / 8];  // row r (hi rows 0..63, lo rows 64..127): chunk x at x ^ (r & 7)
-    uint4 n[AS_NRING][D * D / 4];      // N^T row j: chunk x (four f32) at x ^ (j & 15)
-    uint16_t xs[2][4][2][16 * LDB];    // [step parity][compute wave][hi, lo]: X^T [col][row]
+    uint4 m[AS_MRING][2 * D * D / 8];       // row r (hi rows 0..63, lo rows 64..127): chunk x at x ^ (r & 7)
+    uint4 n[AS_NRING][16 * AS_CW * D / 4];  // N^T row j0 + j: chunk x (four f32) at x ^ (j & 15)
+    uint16_t xs[2][AS_CW][2][16 * LDB];     // [step parity][compute wave][hi, lo]: X^T [col][row]
 };
 
 // s_waitcnt immediates (gfx9 encoding): vmcnt <= n only; lgkmcnt == 0 only.
@@ -444,14 +449,15 @@ template <bool REV>
 __global__ void __launch_bounds__(AS_THREADS) affine_scan_kernel(AsArgs p) {
     extern __shared__ __align__(1024) char as_lds[];
     AsSmem &sm = *reinterpret_cast<AsSmem *>(as_lds);
-    const int bh = blockIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
+    const int nbh = p.B * p.H, bh = blockIdx.x % nbh, j0 = 16 * AS_CW * (blockIdx.x / nbh);
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
     typedef __attribute__((address_space(1))) const void *gptr;
     typedef __attribute__((address_space(3))) void *lptr;
     auto chunk_of = [&](int s) {
         const int sc = min(s, p.nc - 1);
         return (int64_t)bh * p.nc + (REV ? p.nc - 1 - sc : sc);
     };
-    if (w == 4) {  // producer: M (hi and lo), AS_MRING - 1 chunks ahead
+    if (w == AS_CW) {  // producer: M (hi and lo), AS_MRING - 1 chunks ahead
         auto issue = [&](int s) {
             const uint16_t *M = p.m + chunk_of(s) * 2 * D * D;
             uint4 *slot = sm.m[s % AS_MRING];
@@ -472,9 +478,9 @@ __global__ void __launch_bounds__(AS_THREADS) affine_scan_kernel(AsArgs p) {
         __builtin_amdgcn_s_waitcnt(as_vmcnt(0));
         return;
     }
-    if (w == 6) {  // producer: N^T, AS_NRING - 1 chunks ahead
+    if (w == AS_CW + 1) {  // producer: this workgroup's rows of N^T, AS_NRING - 1 chunks ahead
         auto issue = [&](int s) {
-            const float *N = p.n + chunk_of(s) * D * D;
+            const float *N = p.n + chunk_of(s) * D * D + j0 * D;
             uint4 *slot = sm.n[s % AS_NRING];
 #pragma unroll
             for (int i = 0; i < AS_NOPS; ++i) {
@@ -492,7 +498,7 @@ __global__ void __launch_bounds__(AS_THREADS) affine_scan_kernel(AsArgs p) {
         __builtin_amdgcn_s_waitcnt(as_vmcnt(0));
         return;
     }
-    if (w == 5) {  // writer: X^T before step s -> the checkpoint of chunk c(s)
+    if (w == AS_CW + 2) {  // writer: X^T before step s -> the checkpoint of chunk c(s)
         for (int s = 0; s < p.nc; ++s) {
             as_barrier();
             const int64_t co = chunk_of(s) * D * D;
@@ -500,17 +506,17 @@ __global__ void __launch_bounds__(AS_THREADS) affine_scan_kernel(AsArgs p) {
             for (int part = 0; part < 2; ++part) {
                 uint16_t *ck = part == 0 ? p.ckpt : p.ckpt_lo;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {  // 4 compute waves x 16 columns x 64 rows
+                for (int i = 0; i < 2 * AS_CW; ++i) {  // AS_CW compute waves x 16 columns x 64 rows
                     const int q = 64 * i + l, cw = q >> 7, col = (q >> 3) & 15, r8 = 8 * (q & 7);
                     const uint4 v = *reinterpret_cast<const uint4 *>(&sm.xs[s & 1][cw][part][col * LDB + r8]);
-                    *reinterpret_cast<uint4 *>(&ck[co + (16 * cw + col) * D + r8]) = v;
+                    *reinterpret_cast<uint4 *>(&ck[co + (j0 + 16 * cw + col) * D + r8]) = v;
                 }
             }
         }
         return;
     }
     const int b = bh / p.H, h = bh % p.H, g = l >> 4, n = l & 15;
-    const int j = 16 * w + n;  // this lane's state column
+    const int jl = 16 * w + n, j = j0 + jl;  // this lane's state column (in the workgroup, in the state)
     f32x4 X[4];
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm)
@@ -529,7 +535,7 @@ __global__ void __launch_bounds__(AS_THREADS) affine_scan_kernel(AsArgs p) {
         f32x4 Y[4], Z[4];
 #pragma unroll
         for (int tm = 0; tm < 4; ++tm) {  // N[16 tm + 4 g + i][j]: chunk 4 tm + g of N^T row j
-            const float4 nv = nslot[j * 16 + ((4 * tm + g) ^ (j & 15))];
+            const float4 nv = nslot[jl * 16 + ((4 * tm + g) ^ (jl & 15))];
             Y[tm] = f32x4{nv.x, nv.y, nv.z, nv.w};
             Z[tm] = zero4();
         }
@@ -598,9 +604,9 @@ hipError_t launch_chunk_scan(const ChunkArgs &a, bool reverse, hipStream_t strea
     }();
     if (attr != hipSuccess) return attr;
     if (reverse)
-        hipLaunchKernelGGL(affine_scan_kernel<true>, dim3(a.B * a.H), dim3(AS_THREADS), lds, stream, p);
+        hipLaunchKernelGGL(affine_scan_kernel<true>, dim3(a.B * a.H * AS_SPLIT), dim3(AS_THREADS), lds, stream, p);
     else
-        hipLaunchKernelGGL(affine_scan_kernel<false>, dim3(a.B * a.H), dim3(AS_THREADS), lds, stream, p);
+        hipLaunchKernelGGL(affine_scan_kernel<false>, dim3(a.B * a.H * AS_SPLIT), dim3(AS_THREADS), lds, stream, p);
     return hipGetLastError();
 }
 
