@@ -985,9 +985,12 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
     const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
     const int r0 = 16 * tm + 4 * (lane_id() >> 4);
-    // The next chunk of this workgroup; past the end this chunk is loaded again,
-    // so the loads need no branch.
-    const int cn = ci + (int)gridDim.x < nchunks ? ci + (int)gridDim.x : ci;
+    // The next chunk of this workgroup.  Past the end the loads need no branch
+    // either: every lane of a load reads the first element of this chunk's
+    // source (thread index 0 for the addressing), so each load instruction
+    // touches one cache line that the chunk itself has just read.
+    const bool live = ci + (int)gridDim.x < nchunks;
+    const int cn = live ? ci + (int)gridDim.x : ci, tn = live ? tid : 0;
     const ChunkPos pn = chunk_pos(a, cn);
     // The previous chunk (stored during this one) and whether there is one.
     const bool prev = ci != (int)blockIdx.x;
@@ -1025,7 +1028,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
     const float fr = wave_sum(dot8_bf16(in.s0, in.ds) + dot8_bf16(in.s0l, in.ds) + dot8_bf16(in.s0, in.dsl));
     // The previous chunk's dv tile is read now: phase A writes P^T over it.
     const bf16x8_t gv = bgrad_grad_frag(dVt, w);
-    bgrad_load<0>(a, cn, pn, tid, in);
+    bgrad_load<0>(a, cn, pn, tn, in);
     __syncthreads();
     if (lane_id() == 0) sm.frob[w] = fr;
     const RowGates rg = row_gates(sm.gl, tm);
@@ -1086,9 +1089,9 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
     }
     // The previous chunk's dq, dk, dv rows, then the next chunk's V and T.
     if (prev) bgrad_store_rows(a, pp, w, bgrad_grad_frag(dQt, w), bgrad_grad_frag(dKt, w), gv);
-    bgrad_load<3>(a, cn, pn, tid, in);
+    bgrad_load<3>(a, cn, pn, tn, in);
     __syncthreads();
-    bgrad_load<1>(a, cn, pn, tid, in);
+    bgrad_load<1>(a, cn, pn, tn, in);
     if (prev) bgrad_store_gates(a, pp, w, pdg, pdb);
     // Phase D: delta dS^T (-> dlam), ddelta = P^T dO + lam K dS + c delta (-> ddelta^T).
     float cs[4] = {0.f, 0.f, 0.f, 0.f}, ck[4] = {0.f, 0.f, 0.f, 0.f};
@@ -1143,7 +1146,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
         }
     }
     __syncthreads();
-    bgrad_load<2>(a, cn, pn, tid, in);
+    bgrad_load<2>(a, cn, pn, tn, in);
     // Phase E: dR = T^T ddelta -> dV (kept for the stores), dbeta (sum_v dR v part), dR rows.
     f32x4 dvv[2];
     {
@@ -1174,7 +1177,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
         row_reduce_store(p, sm.b2[w & 1], tm);
     }
     __syncthreads();
-    bgrad_load<4>(a, cn, pn, tid, in);
+    bgrad_load<4>(a, cn, pn, tn, in);
     // Phase F: dR S0^T (-> dK; sum_k k dR S0^T -> dbeta and dgam), dA and dP
     // (masked) -> MA^T, MP^T, and the gate-gradient partial sums.
     f32x4 drs[2] = {zero4(), zero4()};
