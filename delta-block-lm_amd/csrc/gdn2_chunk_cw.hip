@@ -279,8 +279,11 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a, int nchunks) 
     const int c = ci % a.nc;
     const int t = tid >> 4, c0 = 4 * (tid & 15), tg = c * CC + t;
     const bool inb = tg < a.T;
-    // The next chunk; past the end this chunk again, so the loads need no branch.
-    const int cn = ci + (int)gridDim.x < nchunks ? ci + (int)gridDim.x : ci;
+    // The next chunk.  Past the end the loads need no branch either: every lane
+    // addresses this chunk as thread 0 would, so each load instruction touches
+    // a line or two that the chunk itself has just read.
+    const bool live = ci + (int)gridDim.x < nchunks;
+    const int cn = live ? ci + (int)gridDim.x : ci, tn = live ? tid : 0;
     float vld, rst;
     if (a.doc) {
         const int st = (int)in.m1, en = (int)in.m2;
@@ -319,7 +322,7 @@ __global__ void __launch_bounds__(NT4) cw_prep_kernel(ChunkArgs a, int nchunks) 
         }
     }
     if (ci != (int)blockIdx.x) cwprep_store(a, ci - gridDim.x, tid, w, po);  // the previous chunk's
-    cwprep_load(a, cn, tid, in);
+    cwprep_load(a, cn, tn, in);
     __syncthreads();
     // Lambda: running sums over the chunk's tokens, one channel per thread;
     // segment index of every token.
@@ -524,8 +527,11 @@ __global__ void __launch_bounds__(NT4) cw_out_kernel(ChunkArgs a, int nchunks) {
     const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid >> 4, c0 = 4 * (tid & 15), t0 = c * CC;
-    // The next chunk; past the end this chunk again, so the loads need no branch.
-    const int cn = ci + (int)gridDim.x < nchunks ? ci + (int)gridDim.x : ci;
+    // The next chunk.  Past the end the loads need no branch either: every lane
+    // addresses this chunk as thread 0 would, so each load instruction touches
+    // a line or two that the chunk itself has just read.
+    const bool live = ci + (int)gridDim.x < nchunks;
+    const int cn = live ? ci + (int)gridDim.x : ci, tn = live ? tid : 0;
     {
         const float va = in.va;
         const int sg = in.sg;
@@ -577,9 +583,9 @@ __global__ void __launch_bounds__(NT4) cw_out_kernel(ChunkArgs a, int nchunks) {
         }
     }
     if (ci != (int)blockIdx.x) cwout_store(a, ci - gridDim.x, tid, po);  // the previous chunk's
-    cwout_load<0>(a, cn, tid, in);
+    cwout_load<0>(a, cn, tn, in);
     __syncthreads();
-    cwout_load<1>(a, cn, tid, in);
+    cwout_load<1>(a, cn, tn, in);
     // P (lower, same segment), elementwise; pair p on lanes 2p, 2p + 1.
     for (int base = 0; base < 2 * 136; base += NT4) {
         const int task = base + tid, p = task >> 1, half = task & 1;
@@ -785,8 +791,11 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a, int nchunks)
     const ChunkArgs &a = chunk_args_reloaded();
     const int tid = threadIdx.x + zero, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t = tid >> 4, c0 = 4 * (tid & 15);
-    // The next chunk; past the end this chunk again, so the loads need no branch.
-    const int cn = ci + (int)gridDim.x < nchunks ? ci + (int)gridDim.x : ci;
+    // The next chunk.  Past the end the loads need no branch either: every lane
+    // addresses this chunk as thread 0 would, so each load instruction touches
+    // a line or two that the chunk itself has just read.
+    const bool live = ci + (int)gridDim.x < nchunks;
+    const int cn = live ? ci + (int)gridDim.x : ci, tn = live ? tid : 0;
     {
         const bool on = in.va != 0.f;
         float qv[4], kv[4], dov[4], er[4];
@@ -832,9 +841,9 @@ __global__ void __launch_bounds__(NT4) cw_bprep_kernel(ChunkArgs a, int nchunks)
 #pragma unroll
     for (int i = 0; i < 4; ++i) dacc[i] = in.dacc[i];
     if (ci != (int)blockIdx.x) cwbp_store(a, ci - gridDim.x, w, nacc);  // the previous chunk's N
-    cwbp_load<0>(a, cn, tid, w, in);
+    cwbp_load<0>(a, cn, tn, w, in);
     __syncthreads();
-    cwbp_load<1>(a, cn, tid, w, in);
+    cwbp_load<1>(a, cn, tn, w, in);
     // Y = Qhat^T dO (row tile w of keys, all value tiles) and W' = T Ahat (tile w).
     f32x4 y[4];
     {

@@ -353,8 +353,11 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a, int nchunks) 
     const int bh = ci / a.nc, c = ci % a.nc, b = bh / a.H, h = bh % a.H;
     const int t = tid & 63, cb = tid >> 6, t0 = c * C;
     const int tm = w >> 1, tn0 = 2 * (w & 1);
-    // The next chunk; past the end this chunk again, so the loads need no branch.
-    const int cn = ci + (int)gridDim.x < nchunks ? ci + (int)gridDim.x : ci;
+    // The next chunk.  Past the end the loads need no branch either: every lane
+    // addresses this chunk as thread 0 would, so each load instruction touches
+    // a line or two that the chunk itself has just read.
+    const bool live = ci + (int)gridDim.x < nchunks;
+    const int cn = live ? ci + (int)gridDim.x : ci, tn = live ? tid : 0;
     const bool on = in.va != 0.f;
     {
         const Row2 k8 = mask_row2(in.k, on);
@@ -374,9 +377,9 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a, int nchunks) 
         wout_store(a, ci - gridDim.x, NVB - 1, tid, sm);
         if (w == 0) wout_store_tok(a, ci - gridDim.x, tok);
     }
-    wout_load<0>(a, cn, tid, in);
+    wout_load<0>(a, cn, tn, in);
     __syncthreads();
-    wout_load<1>(a, cn, tid, in);
+    wout_load<1>(a, cn, tn, in);
     const RowGates rg = row_gates(sm.gl, tm);
     {  // P = Gam . QK^T (causal tiles) -> P^T hi/lo, once for both blocks
         f32x4 pq[2] = {zero4(), zero4()};
@@ -419,7 +422,7 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a, int nchunks) 
                 store_tile_t_split(&Rt[(16 * (tn0 + j)) * LDB + 16 * tm], vt, LDB, x[j]);
             }
         }
-        if (vb == 0) wout_load<2>(a, cn, tid, in);
+        if (vb == 0) wout_load<2>(a, cn, tn, in);
         __syncthreads();
         // Phase 2: delta = T R (-> Dt/Dl) and |delta_t|^2 of the block.
         f32x4 dlt[2] = {zero4(), zero4()};
@@ -481,7 +484,7 @@ __global__ void __launch_bounds__(NT) wide_out_kernel(ChunkArgs a, int nchunks) 
             put_col8(Vt, t, cb, mask8(in.v[1], on));
             put_mat2(St, in.s0[1], tid);
             put_mat2(Sl, in.s0l[1], tid);
-            wout_load<3>(a, cn, tid, in);
+            wout_load<3>(a, cn, tn, in);
             __syncthreads();
         }
     }
@@ -595,8 +598,11 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a, int nchunks
     const int t = tid & 63, cb = tid >> 6, tm = w >> 1, tn0 = 2 * (w & 1);
     const float *dck = a.ck_delta + (int64_t)ci * C * KD;
     const int r0 = 16 * tm + 4 * (lane_id() >> 4);
-    // The next chunk; past the end this chunk again, so the loads need no branch.
-    const int cn = ci + (int)gridDim.x < nchunks ? ci + (int)gridDim.x : ci;
+    // The next chunk.  Past the end the loads need no branch either: every lane
+    // addresses this chunk as thread 0 would, so each load instruction touches
+    // a line or two that the chunk itself has just read.
+    const bool live = ci + (int)gridDim.x < nchunks;
+    const int cn = live ? ci + (int)gridDim.x : ci, tn = live ? tid : 0;
     {
         const bool on = in.va != 0.f;
         const float gam = in.sg == 0 ? __expf(in.G) : 0.f, bg = in.be * gam;
@@ -619,9 +625,9 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a, int nchunks
         }
     }
     if (ci != (int)blockIdx.x) wbprep_store(a, ci - gridDim.x, tm, tn0, yacc);  // the previous chunk's N
-    wbprep_load<0>(a, cn, tid, in);
+    wbprep_load<0>(a, cn, tn, in);
     __syncthreads();
-    wbprep_load<1>(a, cn, tid, in);
+    wbprep_load<1>(a, cn, tn, in);
     const RowGates rg = row_gates(sm.gl, tm);
     // Phase 1: W = T (beta gam K) and both blocks' Y = (gam Q)^T dO in registers; P^T hi/lo.
     f32x4 wacc[NKB][2];
@@ -665,7 +671,7 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a, int nchunks
         }
     }
     __syncthreads();
-    wbprep_load<2>(a, cn, tid, in);
+    wbprep_load<2>(a, cn, tn, in);
     // Phase 2: W^T hi/lo; both blocks' X = P^T dO + diag(c) delta in registers, then
     // stored transposed (hi/lo) once every wave has read the dO rows.
 #pragma unroll
