@@ -14,6 +14,7 @@ q/k/v and d_k, d_v <= 64, in 16-token chunks, against the f64 oracle.
    decay as a product of the gates: negative alpha, alpha = 0 on a whole
    chunk, tiny alpha; and ragged widths (d_k, d_v in 1..64) with padding and
    resets inside chunks and sequence ends off the chunk grid.
+4. Slow decay over 256 chunks (T = 4096), at both gates.
 """
 import numpy as np
 import pytest
@@ -143,3 +144,15 @@ def test_zero_and_tiny_alpha(dk):
     f.alpha[1, :, 0] = np.random.default_rng(1).uniform(1e-3, 1e-2, size=(64, 32))
     _, g = run_and_check(dk, f, ref_gate=False)
     assert np.abs(g["alpha"][0, 16:32, 0]).max() > 0
+
+
+@pytest.mark.parametrize("alpha", [(0.9, 0.99), (0.999, 1.0)])
+def test_slow_decay_long(dk, alpha):
+    """256 chunks of 16 tokens with slow decay (the reference benchmark's law
+    and alpha >= 0.999): the state and its adjoint carry across the whole
+    sequence, so errors of the f32 scans compound; every output and gradient
+    stays within the 1e-4 gate and the reference's own gate."""
+    f = _random(7, 2, 4096, 2, 32, 64, alpha=alpha)
+    print(f"f32 chunk: slow decay alpha {alpha} T4096", flush=True)
+    ran, _ = run_and_check(dk, f)
+    assert STAGES <= ran, sorted(ran)
