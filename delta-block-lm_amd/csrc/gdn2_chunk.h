@@ -239,17 +239,17 @@ inline bool wide_eligible_shape(const gdn2_shape *s, int chunk) {
 }
 
 // Checkpoint per chunk: S0^T (bf16 hi and lo, D x D each), T (bf16 C x C), GateBlock, delta (f32
-// C x D), the factored chunk map (-W'^T bf16 C x D, Ktil bf16 hi and lo C x D
-// each, U^T f32 C x D, the diagonal f32 D), |k|^2 and the value blocks'
-// |delta|^2 (f32 C each).
+// C x D), the factored chunk map (-W'^T bf16 C x D; Ktil = lam K as the masked K
+// rows, bf16 C x D; U^T f32 C x D; the diagonal f32 D followed by lam f32 C),
+// |k|^2 and the value blocks' |delta|^2 (f32 C each).
 constexpr size_t WCK_STATE = (size_t)WIDE_D * WIDE_D * 2;
 constexpr size_t WCK_T = CK_T_BYTES;
 constexpr size_t WCK_GATE = CK_GATE_BYTES;
 constexpr size_t WCK_DELTA = (size_t)CHUNK * WIDE_D * 4;
 constexpr size_t WCK_LRW = (size_t)CHUNK * WIDE_D * 2;
-constexpr size_t WCK_LRK = 2 * WCK_LRW;  // Ktil hi and lo
+constexpr size_t WCK_LRK = WCK_LRW;  // K rows (Ktil = lam K)
 constexpr size_t WCK_LRU = (size_t)CHUNK * WIDE_D * 4;
-constexpr size_t WCK_LRG = (size_t)WIDE_D * 4;
+constexpr size_t WCK_LRG = (size_t)(WIDE_D + CHUNK) * 4;  // diagonal, then lam
 constexpr size_t WCK_MAPN = (size_t)WIDE_D * WIDE_D * 4;
 constexpr size_t WCK_NORM = (size_t)CHUNK * (1 + WIDE_NVB) * 4;
 constexpr size_t WCK_CHUNK =
@@ -309,11 +309,12 @@ hipError_t launch_wide_bwd(const ChunkArgs &a, hipStream_t stream, const hipEven
 // with X before each step to ckpt[c] (X^T, bf16 hi and, when ckpt_lo is set, lo).
 struct LrScanArgs {
     int nc, B, H, vd;      // chunks per head, batch, heads, state columns
-    const uint16_t *wt;    // -W'^T per chunk [kd][ct] bf16
-    const uint16_t *kt;    // Ktil per chunk [ct][kd] bf16
+    const uint16_t *wt;    // -W'^T per chunk [kd][ct] bf16 (kd x ct = 64 x 16: hi, then lo)
+    const uint16_t *kt;    // per chunk: kd = 128, K [ct][kd] bf16 (Ktil = lam K);
+                           // kd = 64, Ktil [ct][kd] bf16 hi, then lo
     const float *u;        // U^T per chunk [vd][ct] f32 (forward)
     const float *n;        // N^T per chunk [vd][kd] f32 (reverse)
-    const float *gv;       // diagonal of the map per chunk [kd] f32
+    const float *gv;       // per chunk: the map's diagonal [kd] f32; kd = 128: then lam [ct]
     uint16_t *ckpt, *ckpt_lo;  // X^T per chunk [vd][kd] bf16
     View x0;               // [B,H,kd,vd] strided (data may be null: zero)
     float *xout;           // [B,H,kd,vd] dense (may be null)

@@ -98,11 +98,16 @@ __device__ __forceinline__ void lr_split(const f32x4 &x, lr_v4s &hi, lr_v4s &lo)
     }
 }
 
-template <int KD_, int CT_, int NCW_, int NPROD_, int R_, bool BWD_, bool LO_, bool WHL_>
+template <int KD_, int CT_, int NCW_, int NPROD_, int R_, bool BWD_, bool LO_, bool WHL_, bool KLAM_>
 struct LrCfg {
     static constexpr int KD = KD_, CT = CT_, NCW = NCW_, NPROD = NPROD_, R = R_;
     static constexpr bool BWD = BWD_, LO = LO_;  // LO: the checkpoint keeps lo parts
-    static constexpr bool WHL = WHL_;            // -W'^T comes as hi and lo (Ktil always does)
+    static constexpr bool WHL = WHL_;            // -W'^T comes as hi and lo
+    // KLAM: Ktil = diag(lam) K with one lam per token (scalar gates) comes as the
+    // bf16 rows of K (exact) and lam (f32, after gv); lam scales the f32 tile V
+    // instead (Ktil^T V = K^T (lam V), Ktil X = lam (K X)).  Otherwise Ktil comes
+    // as bf16 hi and lo.
+    static constexpr bool KLAM = KLAM_;
     static constexpr int WT_NCH = CT * 2 / 16;              // -W'^T [KD][CT] bf16
     static constexpr int KT_NCH = KD * 2 / 16;              // Ktil [CT][KD] bf16
     static constexpr int AUX_NCH = (BWD ? KD : CT) * 4 / 16;  // N^T [cols][KD] or U^T [cols][CT] f32
@@ -113,9 +118,11 @@ struct LrCfg {
     static constexpr int WT_TERMS = WHL ? 2 : 1;
     static constexpr int AUX_BYTES = NCW * 16 * AUX_NCH * 16;
     static constexpr int GV_BYTES = 1024;                   // KD f32 (KD <= 256)
-    static constexpr int WT_OPS = WT_TERMS * WT_BYTES / 1024, KT_OPS = 2 * KT_BYTES / 1024,
+    static constexpr int KT_TERMS = KLAM ? 1 : 2;
+    static constexpr int GV_FLOATS = KD + (KLAM ? CT : 0);  // gv, then lam
+    static constexpr int WT_OPS = WT_TERMS * WT_BYTES / 1024, KT_OPS = KT_TERMS * KT_BYTES / 1024,
                          AUX_OPS = AUX_BYTES / 1024;
-    static constexpr int SLOT = WT_TERMS * WT_BYTES + 2 * KT_BYTES + AUX_BYTES + GV_BYTES;
+    static constexpr int SLOT = WT_TERMS * WT_BYTES + KT_TERMS * KT_BYTES + AUX_BYTES + GV_BYTES;
     static constexpr int XS_NCH = KD * 2 / 16;                  // X^T staging rows [16 cols][KD] bf16
     static constexpr int XS_BYTES = 16 * KD * 2;                // one term (hi or lo)
     static constexpr int LDS_BYTES = R * SLOT + NCW * (LO ? 2 : 1) * XS_BYTES;
@@ -124,7 +131,7 @@ struct LrCfg {
     static constexpr int OPS1 = NPROD == 1 ? 0 : KT_OPS;
     static constexpr int OPS2 = NPROD == 1 ? 0 : AUX_OPS + 1;
     static_assert(WT_BYTES % 1024 == 0 && KT_BYTES % 1024 == 0 && AUX_BYTES % 1024 == 0, "1 KiB DMA units");
-    static_assert(KD * 4 <= GV_BYTES, "gv fits one DMA unit");
+    static_assert(GV_FLOATS * 4 <= GV_BYTES && GV_FLOATS % 4 == 0, "gv and lam fit one DMA unit");
     static_assert(NPROD == 1 || NPROD == 3, "one producer, or one per stream");
     static_assert((R - 1) * OPS0 <= 63 && (R - 1) * OPS1 <= 63 && (R - 1) * OPS2 <= 63,
                   "prefetched chunks fit the memory counter");
@@ -167,14 +174,14 @@ __global__ void __launch_bounds__(64 * (Cfg::NCW + Cfg::NPROD)) lr_scan_kernel(L
                 dma_tile(reinterpret_cast<const char *>(p.wt + cix * Cfg::WT_TERMS * KD * CT), Cfg::WT_OPS,
                          Cfg::WT_NCH, slot);
             if (Cfg::NPROD == 1 || pw == 1)
-                dma_tile(reinterpret_cast<const char *>(p.kt + cix * 2 * CT * KD), Cfg::KT_OPS, Cfg::KT_NCH,
-                         slot + Cfg::WT_TERMS * Cfg::WT_BYTES);
+                dma_tile(reinterpret_cast<const char *>(p.kt + cix * Cfg::KT_TERMS * CT * KD), Cfg::KT_OPS,
+                         Cfg::KT_NCH, slot + Cfg::WT_TERMS * Cfg::WT_BYTES);
             if (Cfg::NPROD == 1 || pw == 2) {
                 const float *aux = BWD ? p.n + (cix * p.vd + colbase) * KD : p.u + (cix * p.vd + colbase) * CT;
-                char *ax = slot + Cfg::WT_TERMS * Cfg::WT_BYTES + 2 * Cfg::KT_BYTES;
+                char *ax = slot + Cfg::WT_TERMS * Cfg::WT_BYTES + Cfg::KT_TERMS * Cfg::KT_BYTES;
                 dma_tile(reinterpret_cast<const char *>(aux), Cfg::AUX_OPS, Cfg::AUX_NCH, ax);
-                if (l < KD / 4)
-                    __builtin_amdgcn_global_load_lds((lr_gptr)(p.gv + cix * KD + 4 * l),
+                if (l < Cfg::GV_FLOATS / 4)
+                    __builtin_amdgcn_global_load_lds((lr_gptr)(p.gv + cix * Cfg::GV_FLOATS + 4 * l),
                                                      (lr_lptr)(ax + Cfg::AUX_BYTES), 16, 0, 0);
             }
         };
@@ -234,9 +241,10 @@ __global__ void __launch_bounds__(64 * (Cfg::NCW + Cfg::NPROD)) lr_scan_kernel(L
         }
         lr_barrier();  // slot s has landed
         const char *slot = lr_ring + (s % R) * Cfg::SLOT;
-        const char *wt = slot, *kt = slot + Cfg::WT_TERMS * Cfg::WT_BYTES, *ax = kt + 2 * Cfg::KT_BYTES;
-        constexpr bool WHL = Cfg::WHL;
+        const char *wt = slot, *kt = slot + Cfg::WT_TERMS * Cfg::WT_BYTES, *ax = kt + Cfg::KT_TERMS * Cfg::KT_BYTES;
+        constexpr bool WHL = Cfg::WHL, KLAM = Cfg::KLAM;
         const float *gv = reinterpret_cast<const float *>(ax + Cfg::AUX_BYTES);
+        const float *lam = gv + KD;  // KLAM: lam of the chunk's tokens
         constexpr int WL = Cfg::WT_BYTES, KL = Cfg::KT_BYTES;  // offsets of the lo tiles
         // Phase 1's LDS reads first (none depends on X), then phase 2's, so their
         // latencies overlap each other and the products.
@@ -247,11 +255,11 @@ __global__ void __launch_bounds__(64 * (Cfg::NCW + Cfg::NPROD)) lr_scan_kernel(L
         for (int tt = 0; tt < CT / 16; ++tt)
 #pragma unroll
             for (int kk = 0; kk < KD / 32; ++kk) {
-                if (BWD) {  // Qm = Ktil rows: token 16 tt + n, keys 32 kk + 4 g (+ 16)
+                if (BWD) {  // Qm = Ktil (KLAM: K) rows: token 16 tt + n, keys 32 kk + 4 g (+ 16)
                     const int o0 = lr_off(16 * tt + n, 32 * kk + 4 * g, 2, Cfg::KT_NCH);
                     const int o1 = lr_off(16 * tt + n, 32 * kk + 16 + 4 * g, 2, Cfg::KT_NCH);
                     qa[tt][kk] = lr_cat(lr_ld8(kt + o0), lr_ld8(kt + o1));
-                    qal[tt][kk] = lr_cat(lr_ld8(kt + KL + o0), lr_ld8(kt + KL + o1));
+                    if (!KLAM) qal[tt][kk] = lr_cat(lr_ld8(kt + KL + o0), lr_ld8(kt + KL + o1));
                 } else {  // Qm = -W' read across -W'^T rows (keys 32 kk + 4 g + e (+ 16), token 16 tt + n)
                     const int r = 32 * kk + 4 * g + (n >> 2), e = 16 * tt + 4 * (n & 3);
                     const int o0 = lr_off(r, e, 2, Cfg::WT_NCH), o1 = lr_off(r + 16, e, 2, Cfg::WT_NCH);
@@ -285,9 +293,17 @@ __global__ void __launch_bounds__(64 * (Cfg::NCW + Cfg::NPROD)) lr_scan_kernel(L
 #pragma unroll
             for (int tt = 0; tt < CT / 16; ++tt) {
                 V[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[tt][kk], xh[kk], V[tt], 0, 0, 0);
-                if (BWD || WHL)
+                if ((BWD && !KLAM) || (!BWD && WHL))
                     V[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qal[tt][kk], xh[kk], V[tt], 0, 0, 0);
                 V[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[tt][kk], xl[kk], V[tt], 0, 0, 0);
+            }
+        // KLAM: V (token rows 16 tt + 4 g + i) times lam, before its split -- the
+        // reverse's K X becomes Ktil X, the forward's V enters Ktil^T V as lam V.
+        if constexpr (KLAM)
+#pragma unroll
+            for (int tt = 0; tt < CT / 16; ++tt) {
+                const float4 lm = *reinterpret_cast<const float4 *>(lam + 16 * tt + 4 * g);
+                V[tt][0] *= lm.x, V[tt][1] *= lm.y, V[tt][2] *= lm.z, V[tt][3] *= lm.w;
             }
         // phase 2: X = gv X + Pm^T V + N (row tiles rt)
         bf16x8_t vh[NP], vl[NP];
@@ -318,14 +334,15 @@ __global__ void __launch_bounds__(64 * (Cfg::NCW + Cfg::NPROD)) lr_scan_kernel(L
                         const int o1 = lr_off(16 * rt + n, 32 * q + 16 + 4 * g, 2, Cfg::WT_NCH);
                         pa = lr_cat(lr_ld8(wt + o0), lr_ld8(wt + o1));
                         if (WHL) pal = lr_cat(lr_ld8(wt + WL + o0), lr_ld8(wt + WL + o1));
-                    } else {  // Pm = Ktil read across its rows (tokens 32 q + 4 g + e (+ 16), key 16 rt + n)
+                    } else {  // Pm = Ktil (KLAM: K) read across its rows (tokens 32 q + 4 g + e (+ 16), key 16 rt + n)
                         const int r = 32 * q + 4 * g + (n >> 2), e = 16 * rt + 4 * (n & 3);
                         const int o0 = lr_off(r, e, 2, Cfg::KT_NCH), o1 = lr_off(r + 16, e, 2, Cfg::KT_NCH);
                         pa = lr_cat(lr_tr16(kt + o0), lr_tr16(kt + o1));
-                        pal = lr_cat(lr_tr16(kt + KL + o0), lr_tr16(kt + KL + o1));
+                        if (!KLAM) pal = lr_cat(lr_tr16(kt + KL + o0), lr_tr16(kt + KL + o1));
                     }
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vh[q], acc, 0, 0, 0);
-                    if (!BWD || WHL) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pal, vh[q], acc, 0, 0, 0);
+                    if ((!BWD && !KLAM) || (BWD && WHL))
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pal, vh[q], acc, 0, 0, 0);
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vl[q], acc, 0, 0, 0);
                 }
             } else {  // 16 tokens: one 16x16x16 product per term
@@ -373,11 +390,11 @@ hipError_t launch_lr_scan(const LrScanArgs &p, int kd, int ct, hipStream_t strea
     // every configuration keeps the checkpoint's lo part; d = 128 streams -W'^T as hi only
     if (p.ckpt_lo == nullptr) return hipErrorInvalidValue;
     if (kd == 128 && ct == 64 && p.vd % 32 == 0)
-        return p.reverse ? launch_lr<LrCfg<128, 64, 2, 3, 2, true, true, false>>(p, stream)
-                         : launch_lr<LrCfg<128, 64, 2, 3, 2, false, true, false>>(p, stream);
+        return p.reverse ? launch_lr<LrCfg<128, 64, 2, 3, 2, true, true, false, true>>(p, stream)
+                         : launch_lr<LrCfg<128, 64, 2, 3, 3, false, true, false, true>>(p, stream);
     if (kd == 64 && ct == 16 && p.vd % 16 == 0)
-        return p.reverse ? launch_lr<LrCfg<64, 16, 1, 1, 5, true, true, true>>(p, stream)
-                         : launch_lr<LrCfg<64, 16, 1, 1, 7, false, true, true>>(p, stream);
+        return p.reverse ? launch_lr<LrCfg<64, 16, 1, 1, 5, true, true, true, false>>(p, stream)
+                         : launch_lr<LrCfg<64, 16, 1, 1, 7, false, true, true, false>>(p, stream);
     return hipErrorInvalidValue;
 }
 

@@ -160,26 +160,13 @@ __global__ void __launch_bounds__(NT) wide_prep_kernel(ChunkArgs a) {
         gb->seg[t] = seg;
     }
     __syncthreads();
-    {  // Ktil = lam K rows (bf16 hi, then lo) and the map's diagonal out
-        const float la = sm.gl.lam[t];
+    {  // the map's Ktil = lam K as the K rows (masked, bf16) and lam (after the diagonal)
 #pragma unroll
-        for (int i = 0; i < NKB; ++i) {
-            Pack8 p;
-            p.u = k8.p[i];
-            uint32_t hi[4], lo[4];
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                uint16_t h0, l0, h1, l1;
-                split_bf16(la * bf16_val(p.h[e]), h0, l0);
-                split_bf16(la * bf16_val(p.h[e + 1]), h1, l1);
-                hi[e / 2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-                lo[e / 2] = (uint32_t)l0 | ((uint32_t)l1 << 16);
-            }
-            uint16_t *kt = a.lr_kt + ((int64_t)ci * 2 * C + t) * KD + 64 * i + 8 * cb;
-            *reinterpret_cast<uint4 *>(kt) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-            *reinterpret_cast<uint4 *>(kt + C * KD) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-        }
-        if (tid < KD) a.lr_gv[(int64_t)ci * KD + tid] = sm.gl.gamC;
+        for (int i = 0; i < NKB; ++i)
+            *reinterpret_cast<uint4 *>(a.lr_kt + ((int64_t)ci * C + t) * KD + 64 * i + 8 * cb) = k8.p[i];
+        float *gv = a.lr_gv + (int64_t)ci * (KD + C);
+        if (tid < KD) gv[tid] = sm.gl.gamC;
+        else if (tid < KD + C) gv[tid] = sm.gl.lam[tid - KD];
     }
     // A = strict_lower(beta_t Gam_ts k_t.k_s) in f32 (tiles with tn <= tm only).
     if (tn0 <= tm) {
