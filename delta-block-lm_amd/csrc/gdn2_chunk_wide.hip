@@ -88,12 +88,19 @@ __device__ __forceinline__ float sq8(uint4 v) {
 struct Mat2 {
     uint4 p[NKB];
 };
+// T at byte offset off (per lane, 32 bits) of a workgroup-uniform base: the
+// load takes the scalar-base + 32-bit vector-offset form, one VGPR of address
+// per load instead of two.
+template <typename Tv>
+__device__ __forceinline__ Tv ld_off(const void *base, uint32_t off) {
+    return *reinterpret_cast<const Tv *>(static_cast<const char *>(base) + off);
+}
 __device__ __forceinline__ Mat2 load_mat2(const uint16_t *src, int tid) {
     Mat2 m;
 #pragma unroll
     for (int i = 0; i < NKB; ++i) {
         const int p = tid + NT * i, r = p / (KD / 8), c0 = 8 * (p % (KD / 8));
-        m.p[i] = *reinterpret_cast<const uint4 *>(src + r * KD + c0);
+        m.p[i] = ld_off<uint4>(src, 2u * (uint32_t)(r * KD + c0));
     }
     return m;
 }
@@ -763,6 +770,10 @@ struct VbRaw {
 };
 }  // namespace
 
+// SCORE: a score adjoint is given (its terms c delta and c' k and the norms
+// behind them are compiled in only then; without it they would hold registers
+// that the kernel has none to spare for).
+template <bool SCORE>
 __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
     __shared__ WBGradSmem sm;
     uint16_t *Qs = sm.q, *Ks = sm.k, *dOs = sm.dos, *S0t = sm.s0t, *dSt = sm.dst;
@@ -792,8 +803,8 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
         r.ds = load_mat2(a.ws_dstate + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
         r.dsl = load_mat2(a.ws_dstate_lo + (int64_t)ci * KD * KD + 64 * vb * KD, tid);
         r.vr = load8(a.v + 64 * vb, a.vs, b, tg, h, cb, inb);
-        r.d0 = *reinterpret_cast<const float4 *>(dck + t * KD + 8 * cb);
-        r.d1 = *reinterpret_cast<const float4 *>(dck + t * KD + 8 * cb + 4);
+        r.d0 = ld_off<float4>(dck, 4u * (uint32_t)(t * KD + 8 * cb));
+        r.d1 = ld_off<float4>(dck, 4u * (uint32_t)(t * KD + 8 * cb + 4));
     };
     const Row2 qr = load_row2(a.q, a.qs, b, tg, h, cb, inb);
     const Row2 kr = load_row2(a.k, a.ks, b, tg, h, cb, inb);
@@ -802,7 +813,7 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
     const float G = gb->G[t], be = gb->beta[t], va = gb->val[t];
     const int sg = gb->seg[t];
     const float dsc = (a.dscores && inb && w == 0) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
-    const bool score_adj = a.dscores != nullptr;
+    constexpr bool score_adj = SCORE;
     const uint4 trw = *reinterpret_cast<const uint4 *>(a.ck_t + (int64_t)ci * C * C +
                                                       (tid >> 3) * C + 8 * (tid & 7));
     const bool on = va != 0.f;
@@ -838,14 +849,12 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
         sm.dsc[t] = dsc;
     }
     __syncthreads();
-    float lmv[4], bt[4], bg[4];  // lam, beta, beta gam at this lane's rows
-    {
-        const RowGates rg = row_gates(sm.gl, tm);
-        const float4 lm = lds_f4(&sm.gl.lam[r0]);
-        lmv[0] = lm.x, lmv[1] = lm.y, lmv[2] = lm.z, lmv[3] = lm.w;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) bt[i] = rg.beta[i], bg[i] = rg.beta[i] * rg.gam[i];
-    }
+    // lam, beta and gam at this lane's rows, read from LDS where they are used (held
+    // in registers across the block loop, they would spill).
+    auto row4 = [&](const float *v) {
+        const float4 x = lds_f4(&v[r0]);
+        return f32x4{x.x, x.y, x.z, x.w};
+    };
     float cs[4] = {0.f, 0.f, 0.f, 0.f}, ck[4] = {0.f, 0.f, 0.f, 0.f};
     if (score_adj) {  // c and c' from the forward's |k|^2 and both blocks' |delta|^2
 #pragma unroll
@@ -919,7 +928,7 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
 #pragma unroll 1
     for (int vb = 0; vb < NVB; ++vb) {
         if (vb > 0) {
-            load_vb(vb, raw);
+            load_vb(1, raw);  // vb == 1: a constant block, so the addresses stay scalar
             __syncthreads();  // the previous block's phase F has read dO, S0^T, dR and delta
             dv_out(vb - 1);
             stage_vb_a(raw);
@@ -948,13 +957,17 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
         row_reduce_accum(pg1, sm.g1[w & 1], tm, vb > 0);
         gemm2<KD, LDK, LDK>(kds, &Ks[(16 * tm) * LDK], dSt, tn0);
         gemm2<KD, LDK, LDK>(kds, &Ks[(16 * tm) * LDK], Xl, tn0);
+        {
+            const f32x4 lmv = row4(sm.gl.lam);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) kds[j][i] *= lmv[i];
+                for (int i = 0; i < 4; ++i) kds[j][i] *= lmv[i];
+        }
         // Phase D: delta dS^T (-> dlam, dK), ddelta = P^T dO + lam K dS + c delta.
         f32x4 xd[2] = {kds[0], kds[1]};
         float pdl[4] = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 lmv = row4(sm.gl.lam);
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
             f32x4 x[2] = {zero4(), zero4()};
@@ -1007,6 +1020,7 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
         __syncthreads();
         // Phase E: dR = T^T ddelta -> dV, the sum_v dR v part of dbeta, dR rows.
         {
+            const f32x4 bt = row4(sm.gl.beta);
             f32x4 x[2] = {zero4(), zero4()};
 #pragma unroll
             for (int r = 0; r < 64; r += 32) {
@@ -1027,7 +1041,7 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     pb2[i] += x[j][i] * vv[i];
-                    dvv[j][i] = sm.gl.val[r0 + i] != 0.f ? bt[i] * x[j][i] : 0.f;
+                    dvv[j][i] = sm.gl.val[r0 + i] != 0.f ? bt[i] * x[j][i] : 0.f;  // bt: beta rows
                 }
                 store_tile_rm(&dRr[(16 * tm) * LDB + 16 * (tn0 + j)], LDB, x[j]);
             }
@@ -1046,6 +1060,7 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
         }
         // Phase F: dR S0^T (-> dK, dbeta, dgam); dR delta^T and dO delta^T summed.
         float pku[4] = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 bt = row4(sm.gl.beta), gm = row4(sm.gl.gam);
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
             f32x4 drs[2] = {zero4(), zero4()};
@@ -1059,7 +1074,7 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     pku[i] += kv[i] * drs[j][i];
-                    dka[kb][j][i] -= bg[i] * drs[j][i];
+                    dka[kb][j][i] -= bt[i] * gm[i] * drs[j][i];  // beta gam
                 }
             }
         }
@@ -1282,7 +1297,10 @@ hipError_t launch_wide_bwd(const ChunkArgs &a, hipStream_t stream, const hipEven
     if (e != hipSuccess) return e;
     wmark(ev, 3, stream);
     wmark(ev, 4, stream);
-    hipLaunchKernelGGL(wide_bgrad_kernel, dim3(nch), dim3(NT), 0, stream, a);
+    if (a.dscores)
+        hipLaunchKernelGGL(wide_bgrad_kernel<true>, dim3(nch), dim3(NT), 0, stream, a);
+    else
+        hipLaunchKernelGGL(wide_bgrad_kernel<false>, dim3(nch), dim3(NT), 0, stream, a);
     wmark(ev, 5, stream);
     return hipGetLastError();
 }
