@@ -884,10 +884,11 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
             }
         }
     };
-    // Once for both blocks: P = Gam . QK^T, transposed (hi/lo) -> LDS, then this
-    // wave's rows of P^T (the A operand of P^T dO) into registers.
-    bf16x8_t pf[2][2];  // [hi, lo][reduction half]
-    {
+    // P = Gam . QK^T, transposed (hi/lo) -> LDS, read by each block's phase D.
+    // Formed again for the second block (its tiles hold the first block's
+    // ddelta^T and dV^T in between): held in registers across the block loop,
+    // its fragments would spill.
+    auto stage_p = [&]() {
         float gm[2][4];
         gam_mask(gm);
         f32x4 qk[2] = {zero4(), zero4()};
@@ -900,13 +901,9 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
             store_tile_t_split(&Pt[(16 * (tn0 + j)) * LDB + 16 * tm],
                                &Ptl[(16 * (tn0 + j)) * LDB + 16 * tm], LDB, pq);
         }
-    }
+    };
+    stage_p();
     __syncthreads();
-#pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-        pf[0][k2] = frag(&Pt[(16 * tm) * LDB], LDB, 32 * k2);
-        pf[1][k2] = frag(&Ptl[(16 * tm) * LDB], LDB, 32 * k2);
-    }
     // Sums over both blocks, in registers: dO S0^T (-> dQ), the dK terms, dA and
     // dP before their masks, and the row-sum partials of the gate gradients.
     f32x4 dos[NKB][2], dka[NKB][2], da[2], dp[2];
@@ -933,6 +930,8 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
             dv_out(vb - 1);
             stage_vb_a(raw);
             stage_vb_b(raw);
+            __syncthreads();  // the first block's dV^T is out of P's tiles
+            stage_p();
             __syncthreads();
         }
         // Phase A: dO S0^T (key tiles of both key blocks), lam K dS.  Row-sum
@@ -987,13 +986,17 @@ __global__ void __launch_bounds__(NT) wide_bgrad_kernel(ChunkArgs a) {
         }
         row_reduce_accum(pdl, sm.dlam[w & 1], tm, vb > 0);
 #pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2)
+        for (int k2 = 0; k2 < 2; ++k2) {
+            // this wave's rows of P^T (hi, lo): the A operand of P^T dO
+            const bf16x8_t ph = frag(&Pt[(16 * tm) * LDB], LDB, 32 * k2);
+            const bf16x8_t pl = frag(&Ptl[(16 * tm) * LDB], LDB, 32 * k2);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const bf16x8_t ob = frag_tr(dOs, 32 * k2, 16 * (tn0 + j));  // B[v][t] = dO[t][v]
-                xd[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf[0][k2], ob, xd[j], 0, 0, 0);
-                xd[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf[1][k2], ob, xd[j], 0, 0, 0);
+                xd[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, ob, xd[j], 0, 0, 0);
+                xd[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, ob, xd[j], 0, 0, 0);
             }
+        }
         if (score_adj) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
