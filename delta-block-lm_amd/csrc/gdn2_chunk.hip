@@ -942,6 +942,9 @@ __device__ __forceinline__ void bgrad_store_gates(const ChunkArgs &a, const Chun
 // that starts every chunk is paid once per workgroup instead of once per chunk.
 // A chunk's stores are issued after the next chunk's staging, so that the
 // staging's wait on its (older) loads never waits on stores.
+// SCORE: a score adjoint is given; its terms (c delta in ddelta, c' k in dk and the
+// norms behind them) are compiled in only then.
+template <bool SCORE>
 __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunks) {
     __shared__ BGradSmem sm;
     // Every input tile is staged once, in the orientation it is stored in (rows
@@ -962,9 +965,7 @@ __global__ void __launch_bounds__(NT) chunk_bgrad_kernel(ChunkArgs a, int nchunk
     // Gradients, G to the next chunk's staging: slots that phase G does not read and
     // the staging does not write.
     uint16_t *dQt = sm.slot[3], *dKt = sm.slot[5], *dVt = sm.slot[13];
-    // The score adjoint's terms (c delta in ddelta, c' k in dk, and the norms
-    // behind them) only exist when a score adjoint is given (uniform branches).
-    const bool score_adj = a.dscores != nullptr;
+    constexpr bool score_adj = SCORE;
     BgradIn in;
     {
         const ChunkPos p0 = chunk_pos(a, blockIdx.x);
@@ -1351,8 +1352,12 @@ hipError_t launch_chunk_bwd(const ChunkArgs &a, hipStream_t stream, const hipEve
     (void)launch_chunk_scan(a, true, stream);
     mark(ev, 3, stream);
     mark(ev, 4, stream);
-    hipLaunchKernelGGL(chunk_bgrad_kernel, dim3(std::min(nchunks, device_cus())), dim3(NT), 0, stream, a,
-                       nchunks);
+    if (a.dscores)
+        hipLaunchKernelGGL(chunk_bgrad_kernel<true>, dim3(std::min(nchunks, device_cus())), dim3(NT), 0, stream, a,
+                           nchunks);
+    else
+        hipLaunchKernelGGL(chunk_bgrad_kernel<false>, dim3(std::min(nchunks, device_cus())), dim3(NT), 0, stream,
+                           a, nchunks);
     mark(ev, 5, stream);
     return hipGetLastError();
 }
