@@ -568,6 +568,9 @@ __device__ __forceinline__ void wbprep_store(const ChunkArgs &a, int ci, int tm,
 // and a chunk's N (formed in the registers of Y) is stored after the next
 // chunk's staging, so that no chunk but a workgroup's first waits on its loads
 // or on the previous chunk's stores.
+// SCORE: a score adjoint is given (the c delta term and its norms are compiled
+// in only then).
+template <bool SCORE>
 __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a, int nchunks) {
     __shared__ WBPrepSmem sm;
     uint16_t *Qs = sm.q, *Ks = sm.k, *Tb = sm.u.p1.tb, *KBGs = sm.u.p1.kbg, *KBGl = sm.u.p1.kbgl;
@@ -575,7 +578,7 @@ __global__ void __launch_bounds__(NT) wide_bprep_kernel(ChunkArgs a, int nchunks
     uint16_t *Wt = sm.u.wt[0], *Wtl = sm.u.wt[1];  // over the phase-1 operands
     // X^T hi/lo of each block, over Q/K (block 0) and the dO rows (block 1) after phase 2
     uint16_t *Xt[NVB] = {sm.q, sm.dos[0]}, *Xtl[NVB] = {sm.k, sm.dos[1]};
-    const bool score_adj = a.dscores != nullptr;
+    constexpr bool score_adj = SCORE;
     WBPrepIn in;
     wbprep_load<0>(a, blockIdx.x, threadIdx.x, in);
     wbprep_load<1>(a, blockIdx.x, threadIdx.x, in);
@@ -1293,7 +1296,10 @@ hipError_t launch_wide_fwd(const ChunkArgs &a, hipStream_t stream, const hipEven
 hipError_t launch_wide_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_t *ev) {
     const int nch = a.B * a.H * a.nc;
     wmark(ev, 0, stream);
-    hipLaunchKernelGGL(wide_bprep_kernel, dim3(std::min(nch, device_cus())), dim3(NT), 0, stream, a, nch);
+    if (a.dscores)
+        hipLaunchKernelGGL(wide_bprep_kernel<true>, dim3(std::min(nch, device_cus())), dim3(NT), 0, stream, a, nch);
+    else
+        hipLaunchKernelGGL(wide_bprep_kernel<false>, dim3(std::min(nch, device_cus())), dim3(NT), 0, stream, a, nch);
     wmark(ev, 1, stream);
     wmark(ev, 2, stream);
     const hipError_t e = wide_scan(a, true, stream);
