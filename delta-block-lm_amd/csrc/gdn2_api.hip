@@ -227,10 +227,12 @@ static bool use_cw_path(const gdn2_shape *shape, const gdn2_view *q, const gdn2_
            rows_aligned(k) && rows_aligned(v);
 }
 
-// f32 q/k/v with d_k, d_v <= 64 run the f32 chunk kernels (gdn2_chunk_f32.hip;
-// any element strides), again whatever the chunk argument.
+// Otherwise q/k/v with d_k, d_v <= 64 run the f32 chunk kernels
+// (gdn2_chunk_f32.hip; any element strides; bf16 inputs are read as their exact
+// f32 values and the gradients written back as bf16), again whatever the chunk
+// argument.
 static bool use_fc_path(const gdn2_shape *shape, const gdn2_view *q) {
-    return fc_eligible_shape(shape) && q->dtype == GDN2_F32;
+    return fc_eligible_shape(shape) && (q->dtype == GDN2_F32 || q->dtype == GDN2_BF16);
 }
 
 // The checkpoint and workspace sizes do not depend on the dtype: each is the
@@ -254,9 +256,10 @@ static size_t training_workspace_bytes(const gdn2_shape *s) {
 }
 
 // The f32 chunk path's argument block over the token-sequential one.
-static FcArgs fc_args(const SeqArgs &s, void *checkpoint, void *workspace) {
+static FcArgs fc_args(const SeqArgs &s, const gdn2_view *q, void *checkpoint, void *workspace) {
     FcArgs f{};
     f.s = s;
+    f.in_bf16 = q->dtype == GDN2_BF16;
     f.nc = (s.T + FC_C - 1) / FC_C;
     fc_bind(f, checkpoint, workspace);
     return f;
@@ -337,7 +340,7 @@ int gdn2_training_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q,
     a.final_state = final_state;
     a.scores = scores;
     if (use_fc_path(shape, q)) {
-        const FcArgs f = fc_args(a, checkpoint, nullptr);
+        const FcArgs f = fc_args(a, q, checkpoint, nullptr);
         const hipEvent_t *ev = stage_events(0, (hipStream_t)stream);
         return launch_status(launch_fc_fwd(f, (hipStream_t)stream, ev), "gdn2_training_scan");
     }
@@ -403,7 +406,7 @@ int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gdn2_view *
     a.dwrite = dwrite;
     a.dinitial = d_initial;
     if (use_fc_path(shape, q)) {
-        const FcArgs f = fc_args(a, const_cast<void *>(checkpoint), workspace);
+        const FcArgs f = fc_args(a, q, const_cast<void *>(checkpoint), workspace);
         const hipEvent_t *ev = stage_events(3, (hipStream_t)stream);
         return launch_status(launch_fc_bwd(f, (hipStream_t)stream, ev), "gdn2_training_backward");
     }
@@ -453,7 +456,7 @@ int gdn2_scan(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k, c
     a.out = output;
     a.out_bf16 = output_dtype == GDN2_BF16;
     if (use_fc_path(shape, q)) {
-        const FcArgs f = fc_args(a, checkpoint, nullptr);
+        const FcArgs f = fc_args(a, q, checkpoint, nullptr);
         const hipEvent_t *ev = stage_events(0, (hipStream_t)stream);
         return launch_status(launch_fc_fwd(f, (hipStream_t)stream, ev), "gdn2_scan");
     }
@@ -515,7 +518,7 @@ int gdn2_backward(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *
     a.derase = derase;
     a.dwrite = dwrite;
     if (use_fc_path(shape, q)) {
-        const FcArgs f = fc_args(a, const_cast<void *>(checkpoint), workspace);
+        const FcArgs f = fc_args(a, q, const_cast<void *>(checkpoint), workspace);
         const hipEvent_t *ev = stage_events(3, (hipStream_t)stream);
         return launch_status(launch_fc_bwd(f, (hipStream_t)stream, ev), "gdn2_backward");
     }

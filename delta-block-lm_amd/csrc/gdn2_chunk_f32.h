@@ -27,6 +27,7 @@ inline bool fc_eligible_shape(const gdn2_shape *s) {
 struct FcArgs {
     SeqArgs s;
     int nc;
+    int in_bf16;  // q, k, v, dO and dq, dk, dv are bf16 (else f32)
     float *st, *tm, *dl, *fw, *fk, *fu, *gv;
     float *ds, *n;
 };

@@ -83,6 +83,15 @@ __device__ __forceinline__ float fc_in(const View &v, int b, int tg, int h, int 
     return (on && tg < T && ch < W) ? ld4<float>(v, b, tg, h, ch) : 0.f;
 }
 
+// q, k, v and dO elements as the caller holds them: f32, or bf16 when bf (the
+// products then run on the exact f32 values of the bf16 inputs).
+__device__ __forceinline__ float fc_ld(const View &v, bool bf, int b, int tg, int h, int ch) {
+    return bf ? ld4<bf16_t>(v, b, tg, h, ch) : ld4<float>(v, b, tg, h, ch);
+}
+__device__ __forceinline__ float fc_x(const View &v, bool bf, int b, int tg, int h, int ch, int T, int W, bool on) {
+    return (on && tg < T && ch < W) ? fc_ld(v, bf, b, tg, h, ch) : 0.f;
+}
+
 // b_t and lam_t of channel i (threads i < K): running products of the gates;
 // zero on the channels K .. 63, which the MFMA products read as padding.
 __device__ void fc_decay_rows(const float *al, const Masks &m, float *bt, float *lam, int K, int tid) {
@@ -207,12 +216,12 @@ __global__ void __launch_bounds__(NT) fc_prep_kernel(FcArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int i = 4 * g + e;
-        const float kv = fc_in(s.k, b, tg, h, i, s.T, K, on);
+        const float kv = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, on);
         const float al = (on && i < K) ? ld4<float>(s.alpha, b, tg, h, i) : 1.f;
         sm.k[t * LQ + i] = kv;
         sm.al[t * LQ + i] = al;
         sm.eh[t * LQ + i] = fc_in(s.erase, b, tg, h, i, s.T, K, on) * kv;
-        sm.wv[t * LQ + i] = fc_in(s.write, b, tg, h, i, s.T, V, on) * fc_in(s.v, b, tg, h, i, s.T, V, on);
+        sm.wv[t * LQ + i] = fc_in(s.write, b, tg, h, i, s.T, V, on) * fc_x(s.v, a.in_bf16, b, tg, h, i, s.T, V, on);
     }
     __syncthreads();
     fc_decay_rows(sm.al, sm.m, sm.bt, sm.lam, K, tid);
@@ -421,12 +430,12 @@ __global__ void __launch_bounds__(NT) fc_out_kernel(FcArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int i = 4 * g + e;
-        const float kv = fc_in(s.k, b, tg, h, i, s.T, K, on);
-        sm.q[t * LQ + i] = fc_in(s.q, b, tg, h, i, s.T, K, on);
+        const float kv = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, on);
+        sm.q[t * LQ + i] = fc_x(s.q, a.in_bf16, b, tg, h, i, s.T, K, on);
         sm.k[t * LQ + i] = kv;
         sm.al[t * LQ + i] = (on && i < K) ? ld4<float>(s.alpha, b, tg, h, i) : 1.f;
         sm.eh[t * LQ + i] = fc_in(s.erase, b, tg, h, i, s.T, K, on) * kv;
-        sm.wv[t * LQ + i] = fc_in(s.write, b, tg, h, i, s.T, V, on) * fc_in(s.v, b, tg, h, i, s.T, V, on);
+        sm.wv[t * LQ + i] = fc_in(s.write, b, tg, h, i, s.T, V, on) * fc_x(s.v, a.in_bf16, b, tg, h, i, s.T, V, on);
         ksq += kv * kv;
     }
     ksq += __shfl_xor(ksq, 1);
@@ -504,11 +513,11 @@ __global__ void __launch_bounds__(NT) fc_bprep_kernel(FcArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int i = 4 * g + e;
-        const float kv = fc_in(s.k, b, tg, h, i, s.T, K, on);
-        sm.q[t * LQ + i] = fc_in(s.q, b, tg, h, i, s.T, K, on);
+        const float kv = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, on);
+        sm.q[t * LQ + i] = fc_x(s.q, a.in_bf16, b, tg, h, i, s.T, K, on);
         sm.k[t * LQ + i] = kv;
         sm.al[t * LQ + i] = (on && i < K) ? ld4<float>(s.alpha, b, tg, h, i) : 1.f;
-        sm.dO[t * LQ + i] = (s.dout.data && on && tg < s.T && i < V) ? ld4<float>(s.dout, b, tg, h, i) : 0.f;
+        sm.dO[t * LQ + i] = (s.dout.data && on && tg < s.T && i < V) ? fc_ld(s.dout, a.in_bf16, b, tg, h, i) : 0.f;
         const float d = i < V ? a.dl[((int64_t)ci * C + t) * V + i] : 0.f;
         sm.dl[t * LQ + i] = d;
         ksq += kv * kv;
@@ -594,12 +603,12 @@ __global__ void __launch_bounds__(NT) fc_bgrad_kernel(FcArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int i = 4 * g + e;
-        const float kv = fc_in(s.k, b, tg, h, i, s.T, K, on);
-        sm.q[t * LQ + i] = fc_in(s.q, b, tg, h, i, s.T, K, on);
+        const float kv = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, on);
+        sm.q[t * LQ + i] = fc_x(s.q, a.in_bf16, b, tg, h, i, s.T, K, on);
         sm.k[t * LQ + i] = kv;
         sm.e[t * LQ + i] = fc_in(s.erase, b, tg, h, i, s.T, K, on);
         sm.al[t * LQ + i] = (on && i < K) ? ld4<float>(s.alpha, b, tg, h, i) : 1.f;
-        sm.dO[t * LQ + i] = (s.dout.data && on && tg < s.T && i < V) ? ld4<float>(s.dout, b, tg, h, i) : 0.f;
+        sm.dO[t * LQ + i] = (s.dout.data && on && tg < s.T && i < V) ? fc_ld(s.dout, a.in_bf16, b, tg, h, i) : 0.f;
         const float d = i < V ? a.dl[((int64_t)ci * C + t) * V + i] : 0.f;
         sm.dl[t * LQ + i] = d;
         ksq += kv * kv;
@@ -667,8 +676,8 @@ __global__ void __launch_bounds__(NT) fc_bgrad_kernel(FcArgs a) {
             if (j < V && tq < s.T) {
                 const bool von = sm.m.val[tt] != 0.f;
                 const int64_t o = (((int64_t)b * s.T + tq) * s.H + h) * V + j;
-                if (s.dwrite) s.dwrite[o] = von ? dr[r] * ld4<float>(s.v, b, tq, h, j) : 0.f;
-                if (s.dv) store_out(s.dv, 0, o, von ? dr[r] * ld4<float>(s.write, b, tq, h, j) : 0.f);
+                if (s.dwrite) s.dwrite[o] = von ? dr[r] * fc_ld(s.v, a.in_bf16, b, tq, h, j) : 0.f;
+                if (s.dv) store_out(s.dv, a.in_bf16, o, von ? dr[r] * ld4<float>(s.write, b, tq, h, j) : 0.f);
             }
         }
     }
@@ -761,8 +770,8 @@ __global__ void __launch_bounds__(NT) fc_bgrad_kernel(FcArgs a) {
             const float deh = bt * sm.u.gr.ga[u * LQ + i] + eA;
             const float dk = lt * sm.u.gr.gk[u * LQ + i] + kAP + ev * deh + sm.ck[u] * k;
             const int64_t o = (((int64_t)b * s.T + tq) * s.H + h) * K + i;
-            if (s.dq) store_out(s.dq, 0, o, von ? dq : 0.f);
-            if (s.dk) store_out(s.dk, 0, o, von ? dk : 0.f);
+            if (s.dq) store_out(s.dq, a.in_bf16, o, von ? dq : 0.f);
+            if (s.dk) store_out(s.dk, a.in_bf16, o, von ? dk : 0.f);
             if (s.derase) s.derase[o] = von ? k * deh : 0.f;
         }
     }

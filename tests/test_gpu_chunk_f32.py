@@ -15,6 +15,10 @@ q/k/v and d_k, d_v <= 64, in 16-token chunks, against the f64 oracle.
    chunk, tiny alpha; and ragged widths (d_k, d_v in 1..64) with padding and
    resets inside chunks and sequence ends off the chunk grid.
 4. Slow decay over 256 chunks (T = 4096), at both gates.
+5. bf16 q/k/v at widths the bf16 chunk kernels do not take (d_k != d_v, or
+   below 64): the same kernels read the exact f32 values of the bf16 inputs and
+   write bf16 gradients; gated at the bf16 tolerance against the oracle run on
+   the bf16-rounded inputs.
 """
 import numpy as np
 import pytest
@@ -22,7 +26,7 @@ import pytest
 torch = pytest.importorskip("torch")
 
 import fixtures as fx  # noqa: E402
-from gpu_util import TOL_F32, dev, gate  # noqa: E402
+from gpu_util import TOL_BF16, TOL_F32, dev, gate  # noqa: E402
 from oracle import oracle  # noqa: E402
 
 pytestmark = pytest.mark.gpu
@@ -40,17 +44,18 @@ def dk():
     return delta_kernels
 
 
-def run_and_check(dk, f, ref_gate=True, chunk=16):
+def run_and_check(dk, f, ref_gate=True, chunk=16, dtype=torch.float32, tol=TOL_F32):
     """Forward + backward through gdn_training_scan with the stage timers on,
     every output and gradient gated against the f64 oracle; returns the stages
-    that ran."""
-    xs = {n: dev(f[n]).requires_grad_(True) for n in GROUPS}
+    that ran.  dtype is that of q, k and v (and so of dO and dq, dk, dv)."""
+    xs = {n: dev(f[n], dtype if n in ("q", "k", "v") else torch.float32).requires_grad_(True)
+          for n in GROUPS}
     init = dev(f.initial).requires_grad_(True) if f.initial is not None else None
     dk.stage_timing(True)
     try:
         r = dk.gdn_training_scan(xs["q"], xs["k"], xs["v"], xs["alpha"], xs["erase"],
                                  xs["write"], dev(f.valid), dev(f.reset), init, chunk)
-        loss = (r.output * dev(f.upstream)).sum()
+        loss = (r.output.float() * dev(f.upstream)).sum()
         if f.final_adjoint is not None:
             loss = loss + (r.final_state * dev(f.final_adjoint)).sum()
         if f.score_adjoint is not None:
@@ -65,13 +70,13 @@ def run_and_check(dk, f, ref_gate=True, chunk=16):
     g = oracle.backward(f.q, f.k, f.v, f.alpha, f.erase, f.write, f.valid, f.reset, f.initial,
                         f.upstream, f.final_adjoint, f.score_adjoint)
     pad = (f.valid == 0)[:, :, None, None]
-    gate("output", r.output, out, TOL_F32, exact_zero=pad, ref_gate=ref_gate)
-    gate("final_state", r.final_state, fin, TOL_F32, ref_gate=ref_gate)
-    gate("scores", r.scores[..., 0], sc, TOL_F32, exact_zero=pad[..., 0], ref_gate=ref_gate)
+    gate("output", r.output, out, tol, exact_zero=pad, ref_gate=ref_gate)
+    gate("final_state", r.final_state, fin, tol, ref_gate=ref_gate)
+    gate("scores", r.scores[..., 0], sc, tol, exact_zero=pad[..., 0], ref_gate=ref_gate)
     for n in GROUPS:
-        gate(f"d{n}", xs[n].grad, g[n], TOL_F32, exact_zero=pad, ref_gate=ref_gate)
+        gate(f"d{n}", xs[n].grad, g[n], tol, exact_zero=pad, ref_gate=ref_gate)
     if init is not None:
-        gate("d_initial", init.grad, g["initial"], TOL_F32, ref_gate=ref_gate)
+        gate("d_initial", init.grad, g["initial"], tol, ref_gate=ref_gate)
     return ran, g
 
 
@@ -155,4 +160,25 @@ def test_slow_decay_long(dk, alpha):
     f = _random(7, 2, 4096, 2, 32, 64, alpha=alpha)
     print(f"f32 chunk: slow decay alpha {alpha} T4096", flush=True)
     ran, _ = run_and_check(dk, f)
+    assert STAGES <= ran, sorted(ran)
+
+
+def _bf16_round(f):
+    for n in ("q", "k", "v"):
+        f[n] = torch.tensor(f[n]).to(torch.bfloat16).float().numpy()
+    return f
+
+
+@pytest.mark.parametrize("K,V,T", [(32, 64, 512), (17, 64, 50), (64, 33, 77), (16, 16, 40)])
+def test_bf16_inputs(dk, K, V, T):
+    f = _bf16_round(_random(K * 7 + V, 2, T, 3, K, V))
+    print(f"f32 chunk: bf16 inputs K{K} V{V} T{T}", flush=True)
+    ran, _ = run_and_check(dk, f, ref_gate=False, dtype=torch.bfloat16, tol=TOL_BF16)
+    assert STAGES <= ran, sorted(ran)
+
+
+def test_bf16_gate_fixture(dk):
+    """The reference's gate fixture (K32, V64) with bf16 q/k/v."""
+    f = _bf16_round(fx.gate_fixture(35, 0))
+    ran, _ = run_and_check(dk, f, ref_gate=False, dtype=torch.bfloat16, tol=TOL_BF16)
     assert STAGES <= ran, sorted(ran)
