@@ -164,7 +164,9 @@ def test_slow_decay_long(dk, alpha):
 
 
 def _bf16_round(f):
-    for n in ("q", "k", "v"):
+    """q, k, v and the output adjoint as the bf16 values the kernels receive (dO
+    has q's dtype), so the oracle and the kernels see the same inputs."""
+    for n in ("q", "k", "v", "upstream"):
         f[n] = torch.tensor(f[n]).to(torch.bfloat16).float().numpy()
     return f
 
