@@ -961,6 +961,8 @@ __device__ __forceinline__ void load_tt_split(const float *ckt, uint16_t *th, ui
 }
 }  // namespace
 
+// SCORE: a score adjoint is given (its terms are compiled in only then).
+template <bool SCORE>
 __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
     __shared__ CwBGradSmem sm;
     static_assert(sizeof(CwBGradSmem) <= 80 * 1024, "two workgroups per CU");
@@ -1002,7 +1004,7 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
     for (int e = 0; e < 4; ++e) {
         const int tq = t0 + acc_row(e);
         eacc[e] = tq < a.T ? ld4<float>(a.erase, b, tq, h, 16 * w + acc_col()) : 0.f;
-        dacc[e] = a.dscores ? dck[acc_row(e) * 64 + 16 * w + acc_col()] : 0.f;
+        dacc[e] = SCORE ? dck[acc_row(e) * 64 + 16 * w + acc_col()] : 0.f;
     }
     if (a.dalpha) load4_f32(a.alpha, b, tg, h, c0, inb, 1.f, alv4);
     {
@@ -1038,7 +1040,7 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
         ksq = row16_sum(ksq);
         dsq = row16_sum(dsq);
         if ((tid & 15) == 0) {
-            const float dsc = (a.dscores && inb) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
+            const float dsc = (SCORE && inb) ? a.dscores[((int64_t)b * a.T + tg) * a.H + h] : 0.f;
             const float nk = sqrtf(ksq), nd = sqrtf(dsq);
             const bool ok = nk > 0.f && nd > 0.f;
             sm.cs[t] = ok ? dsc * nk / nd : 0.f;
@@ -1090,7 +1092,7 @@ __global__ void __launch_bounds__(NT4) cw_bgrad_kernel(ChunkArgs a) {
         f32x4 x = kds;
         x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.ptr, LDB, 0), db, x, 0, 0, 0);
         x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(sm.ptrl, LDB, 0), db, x, 0, 0, 0);
-        if (a.dscores) {
+        if (SCORE) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) x[e] += sm.cs[acc_row(e)] * dacc[e];
         }
@@ -1385,7 +1387,10 @@ hipError_t launch_cw_bwd(const ChunkArgs &a, hipStream_t stream, const hipEvent_
     if (e != hipSuccess) return e;
     cmark(ev, 3, stream);
     cmark(ev, 4, stream);
-    hipLaunchKernelGGL(cw_bgrad_kernel, dim3(nch), dim3(NT4), 0, stream, a);
+    if (a.dscores)
+        hipLaunchKernelGGL(cw_bgrad_kernel<true>, dim3(nch), dim3(NT4), 0, stream, a);
+    else
+        hipLaunchKernelGGL(cw_bgrad_kernel<false>, dim3(nch), dim3(NT4), 0, stream, a);
     cmark(ev, 5, stream);
     return hipGetLastError();
 }
