@@ -7,7 +7,8 @@ keep the chain alive over the whole sequence:
 
 * scalar gates alpha = e^g drawn from [0.90, 0.99] (the reference
   benchmark's draw, crates/experiment/src/kron_benchmark.rs:89) and from
-  [0.999, 1], at T = 8192 (128 chunks of 64) for d = 64 and d = 128;
+  [0.999, 1], at T = 8192 (128 chunks of 64) for d = 64 and d = 128, and at
+  T = 32768 (512 chunks) for d = 64;
 * channel-wise gates alpha in [0.90, 0.99] per channel, and the reference
   gate-fixture law alpha = 0.91 + 0.03 sin(...) (crates/mixers/src/checks.rs:138)
   with its erase/write law and masks, at K = V = 64 and T = 2048 (128 chunks of
@@ -84,6 +85,32 @@ def test_scalar_slow_decay_8192(dk, D, lo, hi):
     gate("dk", dkk, og["k"], TOL_BF16, exact_zero=pad[..., None])
     gate("dv", dv, og["v"], TOL_BF16, exact_zero=pad[..., None])
     gate("dbeta", db, odb, TOL_BF16, exact_zero=pad)
+    gate("dg", dg, odg, TOL_BF16, exact_zero=pad)
+    gate("d_initial", dinit, og["initial"], TOL_BF16)
+
+
+def test_scalar_slow_decay_32768_d64(dk):
+    """512 chunks of 64 with alpha in [0.999, 1]: row 1 carries one chain from
+    the initial state to the final state through every chunk, so the errors of
+    the dense-map scans (maps and their f32 additive terms) compound over four
+    times the 8192-token tests; the final state and d_initial are gated with
+    everything else."""
+    T, D = 32768, 64
+    p = slow_decay(problem(777, 2, T, 1, masks=True, K=D, V=D), 0.999, 1.0, D)
+    p["reset"][1] = 0
+    print(f"slow decay scalar: D={D} alpha in [0.999, 1] T={T}", flush=True)
+    (out, fin, sc), grads, ran = _scalar_fwd_bwd(dk, p)
+    assert chunk_stages(D) <= ran, f"chunk kernels did not all run: {sorted(ran)}"
+    a, e, w = oracle.scalar_gates(p["beta"], p["g"], D, D)
+    o_out, o_fin, o_sc = oracle.scan(p["q"], p["k"], p["v"], a, e, w, p["valid"], p["reset"],
+                                     p["initial"])
+    pad = (p["valid"] == 0)[:, :, None]
+    gate("output", out, o_out, TOL_BF16, exact_zero=pad[..., None])
+    gate("final_state", fin, o_fin, TOL_BF16)
+    og, odb, odg = scalar_oracle_grads(p)
+    dq, dkk, dv, db, dg, dinit = grads
+    gate("dq", dq, og["q"], TOL_BF16, exact_zero=pad[..., None])
+    gate("dk", dkk, og["k"], TOL_BF16, exact_zero=pad[..., None])
     gate("dg", dg, odg, TOL_BF16, exact_zero=pad)
     gate("d_initial", dinit, og["initial"], TOL_BF16)
 
