@@ -201,8 +201,11 @@ def test_inconsistent_limits_follow_reference_kernels(dk, dtype):
     assert np.abs(cpu_rule["k"][0, :20] - exact["k"][0, :20]).max() > 1e-2
 
 
-def test_bf16_d64_runs_chunk_kernels(dk):
-    x, start, end, up = _packed_problem(2, 100, 3, 64, 64, 9)
+@pytest.mark.parametrize("kv", [(64, 64), (32, 64)])
+def test_bf16_runs_chunk_kernels(dk, kv):
+    """bf16 at 64 x 64 runs the bf16 chunk kernels, at 32 x 64 the f32 chunk
+    kernels; both report the six chunk stages."""
+    x, start, end, up = _packed_problem(2, 100, 3, kv[0], kv[1], 9)
     xs = [dev(a, torch.bfloat16 if i < 3 else torch.float32).requires_grad_(True)
           for i, a in enumerate(x)]
     dk.stage_timing(True)
