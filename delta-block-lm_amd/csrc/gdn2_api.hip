@@ -218,8 +218,7 @@ static bool rows_aligned(const gdn2_view *v) {
 
 // The channel-wise op runs the 16-token chunk-WY MFMA kernels
 // (gdn2_chunk_cw.hip) for bf16 q/k/v with d_k = d_v = 64 and aligned rows,
-// whatever the chunk argument (the chunking changes no result); everything
-// else runs the token-sequential kernels.  Forward and backward apply the
+// whatever the chunk argument (the chunking changes no result).  Forward and backward apply the
 // same rule, so the checkpoint format always matches.
 static bool use_cw_path(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k,
                         const gdn2_view *v) {
@@ -227,10 +226,10 @@ static bool use_cw_path(const gdn2_shape *shape, const gdn2_view *q, const gdn2_
            rows_aligned(k) && rows_aligned(v);
 }
 
-// Otherwise q/k/v with d_k, d_v <= 64 run the f32 chunk kernels
-// (gdn2_chunk_f32.hip; any element strides; bf16 inputs are read as their exact
-// f32 values and the gradients written back as bf16), again whatever the chunk
-// argument.
+// Otherwise f32 or bf16 q/k/v of any width (d_k, d_v <= 128) run the f32 chunk
+// kernels (gdn2_chunk_f32.hip; any element strides; bf16 inputs are read as
+// their exact f32 values and the gradients written back as bf16), again
+// whatever the chunk argument.
 static bool use_fc_path(const gdn2_shape *shape, const gdn2_view *q) {
     return fc_eligible_shape(shape) && (q->dtype == GDN2_F32 || q->dtype == GDN2_BF16);
 }
@@ -319,6 +318,7 @@ int gdn2_training_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q,
     if (!output || !final_state || !scores)
         return fail(GDN2_ERR_ARGUMENT, "output, final_state and scores must be non-null");
     if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
+    if ((uintptr_t)checkpoint & 15) return fail(GDN2_ERR_ARGUMENT, "checkpoint must be 16-byte aligned");
     if (checkpoint_bytes < training_checkpoint_bytes(shape))
         return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
                     training_checkpoint_bytes(shape), checkpoint_bytes);
@@ -363,10 +363,12 @@ int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gdn2_view *
     GDN2_TRY(check_channel_inputs(shape, q, k, v, alpha, erase, write, valid, reset));
     if (d_output) GDN2_TRY(check_view(d_output, "d_output", q->dtype, true));
     if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
+    if ((uintptr_t)checkpoint & 15) return fail(GDN2_ERR_ARGUMENT, "checkpoint must be 16-byte aligned");
     if (checkpoint_bytes < training_checkpoint_bytes(shape))
         return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
                     training_checkpoint_bytes(shape), checkpoint_bytes);
     if (!workspace) return fail(GDN2_ERR_ARGUMENT, "workspace is null");
+    if ((uintptr_t)workspace & 15) return fail(GDN2_ERR_ARGUMENT, "workspace must be 16-byte aligned");
     if (workspace_bytes < training_workspace_bytes(shape))
         return fail(GDN2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
                     training_workspace_bytes(shape), workspace_bytes);
@@ -435,6 +437,7 @@ int gdn2_scan(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k, c
     GDN2_TRY(check_out_dtype(output_dtype));
     if (!output) return fail(GDN2_ERR_ARGUMENT, "output is null");
     if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
+    if ((uintptr_t)checkpoint & 15) return fail(GDN2_ERR_ARGUMENT, "checkpoint must be 16-byte aligned");
     if (checkpoint_bytes < training_checkpoint_bytes(shape))
         return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
                     training_checkpoint_bytes(shape), checkpoint_bytes);
@@ -475,10 +478,12 @@ int gdn2_backward(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *
     GDN2_TRY(check_doc_inputs(q, k, v, alpha, erase, write, doc_start, doc_end));
     if (d_output) GDN2_TRY(check_view(d_output, "d_output", q->dtype, true));
     if (!checkpoint) return fail(GDN2_ERR_ARGUMENT, "checkpoint is null");
+    if ((uintptr_t)checkpoint & 15) return fail(GDN2_ERR_ARGUMENT, "checkpoint must be 16-byte aligned");
     if (checkpoint_bytes < training_checkpoint_bytes(shape))
         return fail(GDN2_ERR_WORKSPACE, "checkpoint needs %zu bytes, got %zu",
                     training_checkpoint_bytes(shape), checkpoint_bytes);
     if (!workspace) return fail(GDN2_ERR_ARGUMENT, "workspace is null");
+    if ((uintptr_t)workspace & 15) return fail(GDN2_ERR_ARGUMENT, "workspace must be 16-byte aligned");
     if (workspace_bytes < training_workspace_bytes(shape))
         return fail(GDN2_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
                     training_workspace_bytes(shape), workspace_bytes);

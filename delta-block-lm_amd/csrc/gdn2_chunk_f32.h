@@ -1,4 +1,4 @@
-// Chunked channel-wise GDN-2 in f32 (d_k, d_v <= 64, 16-token chunks).
+// Chunked channel-wise GDN-2 in f32 (d_k, d_v <= 128, 16-token chunks).
 #pragma once
 
 #include "gdn2_seq.h"
@@ -6,7 +6,7 @@
 namespace gdn2 {
 
 constexpr int FC_C = 16;    // tokens per chunk
-constexpr int FC_MAX = 64;  // largest d_k and d_v
+constexpr int FC_MAX = 128;  // largest d_k and d_v
 
 inline bool fc_eligible_shape(const gdn2_shape *s) {
     return s->keys <= FC_MAX && s->values <= FC_MAX;
@@ -19,11 +19,15 @@ inline bool fc_eligible_shape(const gdn2_shape *s) {
 //   tm     T = (I + A)^-1, [16][16]                       (prep -> out, bgrad)
 //   dl     the edits delta, [16][V]                       (out -> bprep, bgrad)
 //   fw, fk the factored map: W' = T (b . e . k) and Ktil = lam . k, [16][KP] each
-//   fu     U = T (w . v), [16][V];  gv  b_15 (the map's diagonal), [KP]
-// KP = d_k rounded up to 16: the key axis of the map's factors is padded with
-// zeros to whole 16-row MFMA tiles for the scans.
-// Backward workspace: ds, the state adjoint at each chunk end, and n, the
-// adjoint map's additive term, [K][V] each.
+//   fu     U = T (w . v), lane-packed for the scan: [VT][4][16][4], element
+//          ((vt * 4 + g) * 16 + n) * 4 + r = U[4 g + r][16 vt + n]
+//   gv     b_15 (the map's diagonal), [KP]
+// KP = d_k and VP = d_v rounded up to 16 (VT = VP / 16): the key axis of the
+// map's factors is padded with zeros to whole 16-row MFMA tiles for the scans.
+// Backward workspace: ds, the state adjoint at each chunk end, [K][V]; and n,
+// the adjoint map's additive term, lane-packed: [VT][KP / 16][4][16][4], element
+// (((vt * KT + tau) * 4 + g) * 16 + n) * 4 + r = N[16 tau + 4 g + r][16 vt + n]
+// (zero outside K x V).  Every array starts on a 16-byte boundary.
 struct FcArgs {
     SeqArgs s;
     int nc;
@@ -34,39 +38,45 @@ struct FcArgs {
 
 inline int64_t fc_chunks(int64_t B, int64_t T, int64_t H) { return B * H * ((T + FC_C - 1) / FC_C); }
 __host__ __device__ inline int fc_kp(int K) { return (K + 15) & ~15; }
+inline size_t fc_pad4(size_t x) { return (x + 3) & ~(size_t)3; }
 
-inline size_t fc_chunk_floats(int K, int V) {
-    return (size_t)K * V + FC_C * FC_C + FC_C * V + 2 * FC_C * fc_kp(K) + FC_C * V + fc_kp(K);
+// The checkpoint's arrays in order, in floats, for n chunks.
+inline void fc_checkpoint_parts(int64_t n, int K, int V, size_t part[7]) {
+    const size_t KP = fc_kp(K), VP = fc_kp(V);
+    part[0] = fc_pad4(n * K * V);       // st
+    part[1] = fc_pad4(n * FC_C * FC_C); // tm
+    part[2] = fc_pad4(n * FC_C * V);    // dl
+    part[3] = n * FC_C * KP;            // fw
+    part[4] = n * FC_C * KP;            // fk
+    part[5] = n * FC_C * VP;            // fu
+    part[6] = n * KP;                   // gv
 }
 
 inline size_t fc_checkpoint_bytes(int64_t B, int64_t T, int64_t H, int K, int V) {
-    return (size_t)fc_chunks(B, T, H) * fc_chunk_floats(K, V) * sizeof(float);
+    size_t part[7], total = 0;
+    fc_checkpoint_parts(fc_chunks(B, T, H), K, V, part);
+    for (size_t x : part) total += x;
+    return total * sizeof(float);
 }
 
 inline size_t fc_workspace_bytes(int64_t B, int64_t T, int64_t H, int K, int V) {
-    return (size_t)fc_chunks(B, T, H) * 2 * K * V * sizeof(float);
+    const int64_t n = fc_chunks(B, T, H);
+    return (fc_pad4(n * K * V) + (size_t)n * fc_kp(K) * fc_kp(V)) * sizeof(float);
 }
 
 inline void fc_bind(FcArgs &a, void *ck, void *ws) {
     const int64_t n = fc_chunks(a.s.B, a.s.T, a.s.H);
-    const int K = a.s.K, V = a.s.V;
+    size_t part[7];
+    fc_checkpoint_parts(n, a.s.K, a.s.V, part);
     float *p = static_cast<float *>(ck);
-    a.st = p;
-    p += n * K * V;
-    a.tm = p;
-    p += n * FC_C * FC_C;
-    a.dl = p;
-    p += n * FC_C * V;
-    a.fw = p;
-    p += n * FC_C * fc_kp(K);
-    a.fk = p;
-    p += n * FC_C * fc_kp(K);
-    a.fu = p;
-    p += n * FC_C * V;
-    a.gv = p;
+    float **dst[7] = {&a.st, &a.tm, &a.dl, &a.fw, &a.fk, &a.fu, &a.gv};
+    for (int i = 0; i < 7; ++i) {
+        *dst[i] = p;
+        p += part[i];
+    }
     if (ws) {
         a.ds = static_cast<float *>(ws);
-        a.n = a.ds + n * K * V;
+        a.n = a.ds + fc_pad4(n * a.s.K * a.s.V);
     }
 }
 

@@ -1,7 +1,7 @@
 // Chunked channel-wise GDN-2 in f32 on gfx950: the reference's own op
 // configuration (f32 q/k/v, d_k = 32, d_v = 64, 16-token chunks;
 // crates/kernels/src/gdn2.rs:10-12, crates/kernels/src/gdn_training.rs:8-9), and
-// every d_k, d_v <= 64.
+// every d_k, d_v <= 128.
 //
 // Recurrence per valid token t (crates/mixers/src/reference.rs:68-111):
 //   bar = diag(alpha_t) S;  delta_t = w_t.v_t - bar^T (e_t.k_t);
@@ -21,9 +21,11 @@
 // (batch, head) (states forward, state adjoints in reverse), out (delta, O,
 // scores), bprep (the adjoint map's additive term N) and bgrad (every
 // gradient).  Work per chunk is small at these widths (a chunk's products are
-// 16 x 64 x 64 at most), so the kernels run in f32 on the VALU with LDS tiles:
-// one 256-thread workgroup per chunk, thread (token t = tid / 16, channels
-// 4 (tid % 16) .. + 3) for the [token][channel] tiles.
+// 16 x 128 x 128 at most), so the kernels run in f32 with LDS tiles: one
+// 256-thread workgroup per chunk.  Each kernel is built for two tile widths FK:
+// 64 (d_k, d_v <= 64) and 128 (either above 64).  Thread (token t = tid / 16,
+// g = tid % 16) holds FK / 16 channels of the [token][channel] tiles: 4 g .. 4 g
+// + 3 at FK = 64, g + 16 e at FK = 128 (adjacent lanes on adjacent banks).
 #include "gdn2_chunk_f32.h"
 #include "gdn2_mfma.h"
 
@@ -34,11 +36,29 @@ namespace gdn2 {
 namespace {
 
 constexpr int C = FC_C;
-constexpr int FK = FC_MAX;
-constexpr int NT = 256;
-constexpr int LQ = FK + 4;  // f32 row stride of [token][channel] tiles
-constexpr int LS = FK + 1;  // f32 row stride of [key][value] tiles
-constexpr int LT = C + 1;   // f32 row stride of 16 x 16 tiles
+constexpr int LT = C + 1;  // f32 row stride of 16 x 16 tiles
+constexpr int VB = 64;     // value columns per S0 / dS block in bgrad
+constexpr int LB = VB + 4; // f32 row stride of [key][value block] tiles
+
+// Geometry of the FK-wide kernels: 4 FK threads per workgroup (256 or 512),
+// LPT lanes per token row of the [token][channel] tiles, four channels each.
+template <int FK>
+struct Fc {
+    static constexpr int NT = 4 * FK;
+    static constexpr int NW = NT / 64;    // waves
+    static constexpr int LPT = NT / C;    // lanes per token row: 16 or 32
+    static constexpr int EPT = FK / LPT;  // channels per lane: 4
+    static constexpr int LQ = FK + 4;     // f32 row stride of [token][channel] tiles
+    static constexpr int LS = FK + 16;    // f32 row stride of [key][value] tiles: rows 16 banks apart
+    // channel e of lane column g (adjacent lanes on adjacent banks at FK = 128)
+    static __device__ __forceinline__ int ch(int g, int e) { return FK == 64 ? 4 * g + e : g + LPT * e; }
+    // sum over the LPT lanes of a token row
+    static __device__ __forceinline__ float row_sum(float x) {
+#pragma unroll
+        for (int m = 1; m < LPT; m <<= 1) x += __shfl_xor(x, m);
+        return x;
+    }
+};
 
 struct Masks {
     float val[C];
@@ -93,8 +113,10 @@ __device__ __forceinline__ float fc_x(const View &v, bool bf, int b, int tg, int
 }
 
 // b_t and lam_t of channel i (threads i < K): running products of the gates;
-// zero on the channels K .. 63, which the MFMA products read as padding.
+// zero on the channels K .. FK - 1, which the MFMA products read as padding.
+template <int FK>
 __device__ void fc_decay_rows(const float *al, const Masks &m, float *bt, float *lam, int K, int tid) {
+    constexpr int LQ = Fc<FK>::LQ;
     if (tid >= K && tid < FK)
         for (int t = 0; t < C; ++t) bt[t * LQ + tid] = lam[t * LQ + tid] = 0.f;
     if (tid < K) {
@@ -112,8 +134,10 @@ __device__ void fc_decay_rows(const float *al, const Masks &m, float *bt, float 
     }
 }
 
-// b_t alone (threads i < K; zero on the channels K .. 63).
+// b_t alone (threads i < K; zero on the channels K .. FK - 1).
+template <int FK>
 __device__ void fc_b_row(const float *al, const Masks &m, float *bt, int K, int tid) {
+    constexpr int LQ = Fc<FK>::LQ;
     if (tid >= K && tid < FK)
         for (int t = 0; t < C; ++t) bt[t * LQ + tid] = 0.f;
     if (tid < K) {
@@ -127,19 +151,20 @@ __device__ void fc_b_row(const float *al, const Masks &m, float *bt, int K, int 
 
 // out[t][s] = sum_i x[t][i] D_ts[i] y[s][i] for s < t (STRICT) or s <= t in the
 // same segment, zero elsewhere (the diagonal too when STRICT).  Thread
-// (t = tid / 16, g = tid % 16) takes channels 4 g .. 4 g + 3 of row t, forming
-// D_ts for s = t, t - 1, .. by a running product; the 16 partial rows of one t
-// (16 adjacent lanes) are summed by lane shuffles.  All 256 threads call it.
-template <bool STRICT>
+// (t = tid / LPT, g = tid % LPT) takes its four channels of row t, forming
+// D_ts for s = t, t - 1, .. by a running product; the LPT partial rows of one
+// t (adjacent lanes) are summed by lane shuffles.  All threads call it.
+template <int FK, bool STRICT>
 __device__ __forceinline__ void fc_tri(const float *x, const float *y, const float *al, const Masks &m,
                                        float *out, int K, int tid) {
-    const int t = tid >> 4, g = tid & 15;
+    constexpr int LQ = Fc<FK>::LQ;
+    const int t = tid / Fc<FK>::LPT, g = tid % Fc<FK>::LPT;
     float acc[C];
 #pragma unroll
     for (int s = 0; s < C; ++s) acc[s] = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int i = 4 * g + e;
+    for (int e = 0; e < Fc<FK>::EPT; ++e) {
+        const int i = Fc<FK>::ch(g, e);
         if (i < K) {
             const float xt = x[t * LQ + i];
             float d = 1.f;
@@ -154,49 +179,116 @@ __device__ __forceinline__ void fc_tri(const float *x, const float *y, const flo
     float r = 0.f;
 #pragma unroll
     for (int s = 0; s < C; ++s) {
-        float a = acc[s];
-        a += __shfl_xor(a, 1);
-        a += __shfl_xor(a, 2);
-        a += __shfl_xor(a, 4);
-        a += __shfl_xor(a, 8);
+        const float a = Fc<FK>::row_sum(acc[s]);
         if (s == g) r = a;
     }
-    const bool keep = (STRICT ? g < t : g <= t) && m.seg[g] == m.seg[t];
-    out[t * LT + g] = keep ? r : 0.f;
+    if (g < C) {
+        const bool keep = (STRICT ? g < t : g <= t) && m.seg[g] == m.seg[t];
+        out[t * LT + g] = keep ? r : 0.f;
+    }
 }
 
+// Stage the rows x COLS block at src0 (and src1, same shape; row stride sld;
+// zero where row >= rv or column >= cv) into dst0 (dst1) with row stride dld.
+// Each thread issues U loads per source before it stores any, so a batch's
+// loads are in flight together instead of one latency per element.
+template <int NT, int COLS, int U>
+__device__ __forceinline__ void fc_stage2(float *dst0, float *dst1, int dld, const float *src0,
+                                          const float *src1, int sld, int rows, int rv, int cv, int tid) {
+    const int n = rows * COLS;
+    for (int e0 = tid; e0 < n; e0 += U * NT) {
+        float x0[U], x1[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int e = e0 + u * NT, i = e / COLS, j = e % COLS;
+            const bool in = e < n && i < rv && j < cv;
+            x0[u] = in ? src0[(int64_t)i * sld + j] : 0.f;
+            x1[u] = (in && src1) ? src1[(int64_t)i * sld + j] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int e = e0 + u * NT, i = e / COLS, j = e % COLS;
+            if (e < n) {
+                dst0[i * dld + j] = x0[u];
+                if (dst1) dst1[i * dld + j] = x1[u];
+            }
+        }
+    }
+}
+
+// fc_stage2 for rows of 16-byte aligned float4s (sld, cv and the sources'
+// offsets multiples of 4): one 16-byte load per four elements.
+template <int NT, int COLS, int U>
+__device__ __forceinline__ void fc_stage2_v4(float *dst0, float *dst1, int dld, const float *src0,
+                                             const float *src1, int sld, int rows, int rv, int cv, int tid) {
+    constexpr int CQ = COLS / 4;
+    const int n = rows * CQ;
+    for (int e0 = tid; e0 < n; e0 += U * NT) {
+        float4 x0[U], x1[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int e = e0 + u * NT, i = e / CQ, j = 4 * (e % CQ);
+            const bool in = e < n && i < rv && j < cv;
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            x0[u] = in ? *reinterpret_cast<const float4 *>(src0 + (int64_t)i * sld + j) : z;
+            x1[u] = (in && src1) ? *reinterpret_cast<const float4 *>(src1 + (int64_t)i * sld + j) : z;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int e = e0 + u * NT, i = e / CQ, j = 4 * (e % CQ);
+            if (e < n) {
+                float *d = dst0 + i * dld + j;
+                d[0] = x0[u].x, d[1] = x0[u].y, d[2] = x0[u].z, d[3] = x0[u].w;
+                if (dst1) {
+                    float *d1 = dst1 + i * dld + j;
+                    d1[0] = x1[u].x, d1[1] = x1[u].y, d1[2] = x1[u].z, d1[3] = x1[u].w;
+                }
+            }
+        }
+    }
+}
+
+template <int FK>
 struct FcPrepSmem {
+    static constexpr int LQ = Fc<FK>::LQ;
     Masks m;
     float k[C * LQ], al[C * LQ], eh[C * LQ], wv[C * LQ], bt[C * LQ], lam[C * LQ];
     float A[C * LT], T[C * LT];
 };
 
+template <int FK>
 struct FcOutSmem {
+    static constexpr int LQ = Fc<FK>::LQ;
     Masks m;
     float q[C * LQ], k[C * LQ], al[C * LQ], eh[C * LQ], wv[C * LQ], bt[C * LQ];
-    float s0[FK * LS];  // S0, zero-padded to whole 16 x 16 tiles
+    float s0[FK * Fc<FK>::LS];  // S0, zero-padded to whole 16 x 16 tiles
     float T[C * LT], P[C * LT];
-    float kk[C], ddp[4][C];
+    float kk[C], ddp[FK / 16][C];
 };
 
+template <int FK>
 struct FcBPrepSmem {
+    static constexpr int LQ = Fc<FK>::LQ;
     Masks m;
     float q[C * LQ], k[C * LQ], al[C * LQ], bt[C * LQ], dO[C * LQ], dl[C * LQ], w[C * LQ];
     float P[C * LT];
     float cs[C];
 };
 
+template <int FK>
 struct FcBGradSmem {
+    static constexpr int LQ = Fc<FK>::LQ;
     Masks m;
     float q[C * LQ], k[C * LQ], e[C * LQ], al[C * LQ], dO[C * LQ], dl[C * LQ], dr[C * LQ];
     float bt[C * LQ], lam[C * LQ];
     union {
         struct {
-            float s0[FK * LS], ds[FK * LS];  // S0 and dS, zero-padded to whole 16 x 16 tiles
+            // one block of VB value columns of S0 and dS, zero outside K x V
+            float s0[FK * LB], ds[FK * LB];
         } st;
         struct {
             float ga[C * LQ], gq[C * LQ], gk[C * LQ];  // dAhat, dQhat, dKtil [token][key]
-            float part[4 * C * 64];  // dalpha partials: 4 rpw groups x C rows x 64 / rpw channels
+            float part[Fc<FK>::NT * C];  // dalpha partials: NT / cpl groups x C rows x cpl channels
         } gr;
     } u;
     float T[C * LT], P[C * LT], dA[C * LT], dP[C * LT];
@@ -206,16 +298,18 @@ struct FcBGradSmem {
 }  // namespace
 
 // ---- prep: gates, A, T and the factored map of every chunk ---------------------
-__global__ void __launch_bounds__(NT) fc_prep_kernel(FcArgs a) {
-    __shared__ FcPrepSmem sm;
+template <int FK>
+__global__ void __launch_bounds__(Fc<FK>::NT) fc_prep_kernel(FcArgs a) {
+    __shared__ FcPrepSmem<FK> sm;
+    constexpr int LQ = Fc<FK>::LQ, NW = Fc<FK>::NW;
     const SeqArgs &s = a.s;
     const int tid = threadIdx.x, ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / s.H, h = bh % s.H;
-    const int K = s.K, V = s.V, t = tid >> 4, g = tid & 15, tg = c * C + t;
+    const int K = s.K, V = s.V, t = tid / Fc<FK>::LPT, g = tid % Fc<FK>::LPT, tg = c * C + t;
     fc_masks(s, b, c, sm.m, tid);
     const bool on = sm.m.val[t] != 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int i = 4 * g + e;
+    for (int e = 0; e < Fc<FK>::EPT; ++e) {
+        const int i = Fc<FK>::ch(g, e);
         const float kv = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, on);
         const float al = (on && i < K) ? ld4<float>(s.alpha, b, tg, h, i) : 1.f;
         sm.k[t * LQ + i] = kv;
@@ -224,8 +318,8 @@ __global__ void __launch_bounds__(NT) fc_prep_kernel(FcArgs a) {
         sm.wv[t * LQ + i] = fc_in(s.write, b, tg, h, i, s.T, V, on) * fc_x(s.v, a.in_bf16, b, tg, h, i, s.T, V, on);
     }
     __syncthreads();
-    fc_decay_rows(sm.al, sm.m, sm.bt, sm.lam, K, tid);
-    fc_tri<true>(sm.eh, sm.k, sm.al, sm.m, sm.A, K, tid);  // A, strictly lower
+    fc_decay_rows<FK>(sm.al, sm.m, sm.bt, sm.lam, K, tid);
+    fc_tri<FK, true>(sm.eh, sm.k, sm.al, sm.m, sm.A, K, tid);  // A, strictly lower
     __syncthreads();
     if (tid < C) {
         // T = (I + A)^-1 by forward substitution, column j = tid: x_r = [r == j] -
@@ -243,22 +337,22 @@ __global__ void __launch_bounds__(NT) fc_prep_kernel(FcArgs a) {
         for (int r = 0; r < C; ++r) sm.T[r * LT + j] = tc[r];
     }
     __syncthreads();
-    // Ktil = lam . k (token t, channels 4g .. 4g + 3) and gv = b_15; zero on the
+    // Ktil = lam . k (token t, the thread's channels) and gv = b_15; zero on the
     // key padding up to KP.
     const int KP = fc_kp(K), KT = KP >> 4, VT = (V + 15) >> 4;
     const int64_t fo = (int64_t)ci * C;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int i = 4 * g + e;
+    for (int e = 0; e < Fc<FK>::EPT; ++e) {
+        const int i = Fc<FK>::ch(g, e);
         if (i < KP) a.fk[(fo + t) * KP + i] = i < K ? sm.lam[t * LQ + i] * sm.k[t * LQ + i] : 0.f;
     }
     if (tid < KP) a.gv[(int64_t)ci * KP + tid] = tid < K ? sm.bt[(C - 1) * LQ + tid] : 0.f;
-    a.tm[(int64_t)ci * C * C + tid] = sm.T[(tid >> 4) * LT + (tid & 15)];
+    if (tid < C * C) a.tm[(int64_t)ci * C * C + tid] = sm.T[(tid >> 4) * LT + (tid & 15)];
     // W' = T (b . ehat) and U = T wv on v_mfma_f32_16x16x4f32: tiles 0 .. KT - 1
     // of W' (key tiles), then VT tiles of U, taken by the waves in turn (lane
     // (lg, ln): tokens 4 lg + r, column 16 tile + ln).
     const int w = tid >> 6, l = tid & 63, lg = l >> 4, ln = l & 15;
-    for (int n = w; n < KT + VT; n += 4) {
+    for (int n = w; n < KT + VT; n += NW) {
         const bool isw = n < KT;
         const int col = 16 * (isw ? n : n - KT) + ln;
         f32x4 x = zero4();
@@ -268,11 +362,12 @@ __global__ void __launch_bounds__(NT) fc_prep_kernel(FcArgs a) {
             const float bv = isw ? sm.bt[ss * LQ + col] * sm.eh[ss * LQ + col] : sm.wv[ss * LQ + col];
             x = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.T[ln * LT + ss], bv, x, 0, 0, 0);
         }
+        if (isw) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int tt = 4 * lg + r;
-            if (isw) a.fw[(fo + tt) * KP + col] = x[r];
-            else if (col < V) a.fu[(fo + tt) * V + col] = x[r];
+            for (int r = 0; r < 4; ++r) a.fw[(fo + 4 * lg + r) * KP + col] = x[r];
+        } else {  // lane-packed for the scan (zero past V: wv is)
+            *reinterpret_cast<float4 *>(&a.fu[(((int64_t)ci * VT + n - KT) * 64 + l) * 4]) =
+                make_float4(x[0], x[1], x[2], x[3]);
         }
     }
 }
@@ -288,50 +383,43 @@ __global__ void __launch_bounds__(NT) fc_prep_kernel(FcArgs a) {
 // k-slice is {4 g + s}: the B operand of step s is then register s of the
 // lane's own accumulator tile (rows 4 g + s of S or X, rows 4 g + s of v), so
 // no value changes lanes; the A operand is the matching element of W' or Ktil,
-// read from global memory into registers one chunk ahead.
+// read from global memory into registers a few chunks ahead: W' or Ktil rows,
+// gv and the lane-packed U or N as 16-byte loads, the other factor's columns
+// as 4-byte loads coalesced over the 16 columns n.
 template <int KT>
 struct FcScanOps {
-    float w[KT][4], k[KT][4], g[KT][4], a[KT][4];  // A operands, gv rows, U or N
+    float4 w[KT], g[KT], a[KT];  // A operands (token n), gv rows, U (a[0]) or N
+    float k[KT][4];              // A operands (token 4 g + s)
 };
 
 template <int KT, bool REV>
-__device__ __forceinline__ void fc_scan_load(const FcArgs &a, int64_t ci, int cg, FcScanOps<KT> &o) {
-    // Every load is issued (indices past the widths are clamped and their values
-    // dropped by a select), so no load sits behind a branch and the compiler's
+__device__ __forceinline__ void fc_scan_load(const FcArgs &a, int64_t ci, int cg, int VT, FcScanOps<KT> &o) {
+    // Every load is issued (past the value tiles the lanes read tile 0, their
+    // values unused), so no load sits behind a branch and the compiler's
     // memory-counter waits stay exact across the prefetch ring.
-    const int K = a.s.K, V = a.s.V, KP = 16 * KT, l = lane_id(), g = l >> 4, n = l & 15, j = 16 * cg + n;
-    const bool jv = j < V;
-    const int jc = jv ? j : 0;
+    constexpr int KP = 16 * KT;
+    const int l = lane_id(), g = l >> 4, n = l & 15, cc = cg < VT ? cg : 0;
     const float *fw = a.fw + ci * C * KP, *fk = a.fk + ci * C * KP;
+    const float *rw = REV ? fk : fw, *ck = REV ? fw : fk;
 #pragma unroll
-    for (int tau = 0; tau < KT; ++tau)
+    for (int tau = 0; tau < KT; ++tau) {
+        // the operand (token n, keys 16 tau + 4 g ..) and (tokens 4 g + s, key 16 tau + n)
+        o.w[tau] = *reinterpret_cast<const float4 *>(&rw[n * KP + 16 * tau + 4 * g]);
+        o.g[tau] = *reinterpret_cast<const float4 *>(&a.gv[ci * KP + 16 * tau + 4 * g]);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            // the operand (token l % 16, key 16 tau + 4 g + s) and (token 4 g + s, key 16 tau + l % 16)
-            const float rowk = (REV ? fk : fw)[n * KP + 16 * tau + 4 * g + s];
-            const float colk = (REV ? fw : fk)[(4 * g + s) * KP + 16 * tau + n];
-            o.w[tau][s] = REV ? rowk : -rowk;
-            o.k[tau][s] = REV ? -colk : colk;
-            o.g[tau][s] = a.gv[ci * KP + 16 * tau + 4 * g + s];
-            if (REV) {
-                const int i = 16 * tau + 4 * g + s;
-                const bool in = i < K && jv;
-                const float x = a.n[(ci * K + (i < K ? i : 0)) * V + jc];
-                o.a[tau][s] = in ? x : 0.f;
-            } else if (tau == 0) {
-                const float x = a.fu[(ci * C + 4 * g + s) * V + jc];
-                o.a[tau][s] = jv ? x : 0.f;
-            } else {
-                o.a[tau][s] = 0.f;
-            }
-        }
+        for (int s = 0; s < 4; ++s) o.k[tau][s] = ck[(4 * g + s) * KP + 16 * tau + n];
+        if (REV)
+            o.a[tau] = *reinterpret_cast<const float4 *>(&a.n[(((ci * VT + cc) * KT + tau) * 64 + l) * 4]);
+        else if (tau == 0)
+            o.a[0] = *reinterpret_cast<const float4 *>(&a.fu[((ci * VT + cc) * 64 + l) * 4]);
+    }
 }
 
 template <int KT, bool REV>
 __global__ void __launch_bounds__(64) fc_scan_kernel(FcArgs a) {
     const SeqArgs &s = a.s;
-    const int K = s.K, V = s.V, ng = (V + 15) / 16;
-    const int wg = blockIdx.x, bh = wg / ng, cg = wg % ng, b = bh / s.H, h = bh % s.H;
+    const int K = s.K, V = s.V, VT = (V + 15) / 16;
+    const int wg = blockIdx.x, bh = wg / VT, cg = wg % VT, b = bh / s.H, h = bh % s.H;
     const int l = lane_id(), g = l >> 4, n = l & 15, j = 16 * cg + n;
     const bool jv = j < V;
     f32x4 X[KT];
@@ -356,7 +444,7 @@ __global__ void __launch_bounds__(64) fc_scan_kernel(FcArgs a) {
         return (int64_t)bh * a.nc + (REV ? a.nc - 1 - sc : sc);
     };
 #pragma unroll
-    for (int d = 0; d < D; ++d) fc_scan_load<KT, REV>(a, chunk_at(d), cg, ring[d]);
+    for (int d = 0; d < D; ++d) fc_scan_load<KT, REV>(a, chunk_at(d), cg, VT, ring[d]);
     float *keep = REV ? a.ds : a.st;
     for (int s0 = 0; s0 < a.nc; s0 += D) {
 #pragma unroll
@@ -374,24 +462,28 @@ __global__ void __launch_bounds__(64) fc_scan_kernel(FcArgs a) {
                     if (i < K && jv) keep[(ci * K + i) * V + j] = X[tau][r];
                 }
             // v[t][j], t = 4 g + r: U - W' S (forward) or Ktil X (reverse)
-            f32x4 v = REV ? zero4() : f32x4{cur.a[0][0], cur.a[0][1], cur.a[0][2], cur.a[0][3]};
+            f32x4 v = REV ? zero4() : f32x4{cur.a[0].x, cur.a[0].y, cur.a[0].z, cur.a[0].w};
 #pragma unroll
-            for (int tau = 0; tau < KT; ++tau)
+            for (int tau = 0; tau < KT; ++tau) {
+                const float wq[4] = {cur.w[tau].x, cur.w[tau].y, cur.w[tau].z, cur.w[tau].w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
-                    v = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.w[tau][q], X[tau][q], v, 0, 0, 0);
+                    v = __builtin_amdgcn_mfma_f32_16x16x4f32(REV ? wq[q] : -wq[q], X[tau][q], v, 0, 0, 0);
+            }
             // S <- diag(gv) S + Ktil^T v, or X <- diag(gv) X + N - W'^T v
 #pragma unroll
             for (int tau = 0; tau < KT; ++tau) {
+                const float gq[4] = {cur.g[tau].x, cur.g[tau].y, cur.g[tau].z, cur.g[tau].w};
+                const float an[4] = {cur.a[tau].x, cur.a[tau].y, cur.a[tau].z, cur.a[tau].w};
                 f32x4 x;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) x[r] = cur.g[tau][r] * X[tau][r] + (REV ? cur.a[tau][r] : 0.f);
+                for (int r = 0; r < 4; ++r) x[r] = gq[r] * X[tau][r] + (REV ? an[r] : 0.f);
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
-                    x = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.k[tau][q], v[q], x, 0, 0, 0);
+                    x = __builtin_amdgcn_mfma_f32_16x16x4f32(REV ? -cur.k[tau][q] : cur.k[tau][q], v[q], x, 0, 0, 0);
                 X[tau] = x;
             }
-            fc_scan_load<KT, REV>(a, chunk_at(step + D), cg, ring[d]);
+            fc_scan_load<KT, REV>(a, chunk_at(step + D), cg, VT, ring[d]);
         }
     }
     float *fin = REV ? s.dinitial : s.final_state;
@@ -412,24 +504,30 @@ static void launch_fc_scan(const FcArgs &a, hipStream_t stream) {
         case 1: hipLaunchKernelGGL((fc_scan_kernel<1, REV>), grid, block, 0, stream, a); break;
         case 2: hipLaunchKernelGGL((fc_scan_kernel<2, REV>), grid, block, 0, stream, a); break;
         case 3: hipLaunchKernelGGL((fc_scan_kernel<3, REV>), grid, block, 0, stream, a); break;
-        default: hipLaunchKernelGGL((fc_scan_kernel<4, REV>), grid, block, 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((fc_scan_kernel<4, REV>), grid, block, 0, stream, a); break;
+        case 5: hipLaunchKernelGGL((fc_scan_kernel<5, REV>), grid, block, 0, stream, a); break;
+        case 6: hipLaunchKernelGGL((fc_scan_kernel<6, REV>), grid, block, 0, stream, a); break;
+        case 7: hipLaunchKernelGGL((fc_scan_kernel<7, REV>), grid, block, 0, stream, a); break;
+        default: hipLaunchKernelGGL((fc_scan_kernel<8, REV>), grid, block, 0, stream, a); break;
     }
 }
 
 // ---- out: edits, outputs, scores ----------------------------------------------
-__global__ void __launch_bounds__(NT) fc_out_kernel(FcArgs a) {
-    __shared__ FcOutSmem sm;
+template <int FK>
+__global__ void __launch_bounds__(Fc<FK>::NT) fc_out_kernel(FcArgs a) {
+    __shared__ FcOutSmem<FK> sm;
+    constexpr int LQ = Fc<FK>::LQ, LS = Fc<FK>::LS, NT = Fc<FK>::NT, NW = Fc<FK>::NW;
     const SeqArgs &s = a.s;
     const int tid = threadIdx.x, ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / s.H, h = bh % s.H;
-    const int K = s.K, V = s.V, t = tid >> 4, g = tid & 15, tg = c * C + t;
+    const int K = s.K, V = s.V, t = tid / Fc<FK>::LPT, g = tid % Fc<FK>::LPT, tg = c * C + t;
     const int KP = fc_kp(K), VT = (V + 15) >> 4, VP = 16 * VT;
     const int w = tid >> 6, l = tid & 63, lg = l >> 4, ln = l & 15;
     fc_masks(s, b, c, sm.m, tid);
     const bool on = sm.m.val[t] != 0.f;
     float ksq = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int i = 4 * g + e;
+    for (int e = 0; e < Fc<FK>::EPT; ++e) {
+        const int i = Fc<FK>::ch(g, e);
         const float kv = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, on);
         sm.q[t * LQ + i] = fc_x(s.q, a.in_bf16, b, tg, h, i, s.T, K, on);
         sm.k[t * LQ + i] = kv;
@@ -438,29 +536,25 @@ __global__ void __launch_bounds__(NT) fc_out_kernel(FcArgs a) {
         sm.wv[t * LQ + i] = fc_in(s.write, b, tg, h, i, s.T, V, on) * fc_x(s.v, a.in_bf16, b, tg, h, i, s.T, V, on);
         ksq += kv * kv;
     }
-    ksq += __shfl_xor(ksq, 1);
-    ksq += __shfl_xor(ksq, 2);
-    ksq += __shfl_xor(ksq, 4);
-    ksq += __shfl_xor(ksq, 8);
+    ksq = Fc<FK>::row_sum(ksq);
     if (g == 0) sm.kk[t] = ksq;
-    {
-        const float *st = a.st + (int64_t)ci * K * V;
-        for (int e = tid; e < KP * VP; e += NT) {
-            const int i = e / VP, j = e - i * VP;
-            sm.s0[i * LS + j] = (i < K && j < V) ? st[i * V + j] : 0.f;
-        }
-    }
-    sm.T[(tid >> 4) * LT + (tid & 15)] = a.tm[(int64_t)ci * C * C + tid];
+    // S0 rows 0 .. KP - 1, all FK columns (zero outside K x V); 16-byte loads
+    // when the rows allow them
+    if ((V & 3) == 0 && (reinterpret_cast<uintptr_t>(a.st) & 15) == 0)
+        fc_stage2_v4<NT, FK, FK / 16>(sm.s0, nullptr, LS, a.st + (int64_t)ci * K * V, nullptr, V, KP, K, V, tid);
+    else
+        fc_stage2<NT, FK, 16>(sm.s0, nullptr, LS, a.st + (int64_t)ci * K * V, nullptr, V, KP, K, V, tid);
+    if (tid < C * C) sm.T[(tid >> 4) * LT + (tid & 15)] = a.tm[(int64_t)ci * C * C + tid];
     __syncthreads();
-    fc_b_row(sm.al, sm.m, sm.bt, K, tid);
-    fc_tri<false>(sm.q, sm.k, sm.al, sm.m, sm.P, K, tid);  // P, lower with the diagonal
+    fc_b_row<FK>(sm.al, sm.m, sm.bt, K, tid);
+    fc_tri<FK, false>(sm.q, sm.k, sm.al, sm.m, sm.P, K, tid);  // P, lower with the diagonal
     __syncthreads();
-    // Wave w: value tile w on v_mfma_f32_16x16x4f32 (lane (lg, ln): rows 4 lg + r,
-    // column 16 w + ln).  R = wv - Ahat S0, O = Qhat S0 over the key axis; then
-    // delta = T R and O += P delta with the accumulator rows as the B operand
-    // (step q reduces over the tokens 4 lg + q).
-    if (w < VT) {
-        const int j = 16 * w + ln;
+    // Wave w: value tiles w, w + NW, .. on v_mfma_f32_16x16x4f32 (lane (lg, ln):
+    // rows 4 lg + r, column 16 vt + ln).  R = wv - Ahat S0, O = Qhat S0 over the
+    // key axis; then delta = T R and O += P delta with the accumulator rows as the
+    // B operand (step q reduces over the tokens 4 lg + q).
+    for (int vt = w; vt < VT; vt += NW) {
+        const int j = 16 * vt + ln;
         f32x4 x = zero4(), o = zero4();
         for (int kk = 0; kk < KP; kk += 4) {
             const int i = kk + lg;
@@ -485,7 +579,7 @@ __global__ void __launch_bounds__(NT) fc_out_kernel(FcArgs a) {
             p += __shfl_xor(p, 4);
             p += __shfl_xor(p, 8);
             const int tt = 4 * lg + q, tq = c * C + tt;
-            if (ln == 0) sm.ddp[w][tt] = p;
+            if (ln == 0) sm.ddp[vt][tt] = p;
             if (j < V) {
                 a.dl[((int64_t)ci * C + tt) * V + j] = d[q];
                 if (tq < s.T) store_out(s.out, s.out_bf16, (((int64_t)b * s.T + tq) * s.H + h) * V + j, o[q]);
@@ -501,18 +595,20 @@ __global__ void __launch_bounds__(NT) fc_out_kernel(FcArgs a) {
 }
 
 // ---- bprep: N = Qhat^T dO - W'^T X, X = P^T dO + c delta ------------------------
-__global__ void __launch_bounds__(NT) fc_bprep_kernel(FcArgs a) {
-    __shared__ FcBPrepSmem sm;
+template <int FK>
+__global__ void __launch_bounds__(Fc<FK>::NT) fc_bprep_kernel(FcArgs a) {
+    __shared__ FcBPrepSmem<FK> sm;
+    constexpr int LQ = Fc<FK>::LQ, NW = Fc<FK>::NW;
     const SeqArgs &s = a.s;
     const int tid = threadIdx.x, ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / s.H, h = bh % s.H;
-    const int K = s.K, V = s.V, t = tid >> 4, g = tid & 15, tg = c * C + t;
+    const int K = s.K, V = s.V, t = tid / Fc<FK>::LPT, g = tid % Fc<FK>::LPT, tg = c * C + t;
     fc_masks(s, b, c, sm.m, tid);
     const bool on = sm.m.val[t] != 0.f;
     const bool score_adj = s.dscores != nullptr;
     float ksq = 0.f, dsq = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int i = 4 * g + e;
+    for (int e = 0; e < Fc<FK>::EPT; ++e) {
+        const int i = Fc<FK>::ch(g, e);
         const float kv = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, on);
         sm.q[t * LQ + i] = fc_x(s.q, a.in_bf16, b, tg, h, i, s.T, K, on);
         sm.k[t * LQ + i] = kv;
@@ -523,29 +619,29 @@ __global__ void __launch_bounds__(NT) fc_bprep_kernel(FcArgs a) {
         ksq += kv * kv;
         dsq += d * d;
     }
-    ksq += __shfl_xor(ksq, 1), ksq += __shfl_xor(ksq, 2), ksq += __shfl_xor(ksq, 4), ksq += __shfl_xor(ksq, 8);
-    dsq += __shfl_xor(dsq, 1), dsq += __shfl_xor(dsq, 2), dsq += __shfl_xor(dsq, 4), dsq += __shfl_xor(dsq, 8);
+    ksq = Fc<FK>::row_sum(ksq);
+    dsq = Fc<FK>::row_sum(dsq);
     if (g == 0) {
         const float nk = sqrtf(ksq), nd = sqrtf(dsq);
         const float dsc = (score_adj && tg < s.T) ? s.dscores[((int64_t)b * s.T + tg) * s.H + h] : 0.f;
         sm.cs[t] = (on && nk > 0.f && nd > 0.f) ? dsc * nk / nd : 0.f;
     }
     __syncthreads();
-    fc_b_row(sm.al, sm.m, sm.bt, K, tid);
-    fc_tri<false>(sm.q, sm.k, sm.al, sm.m, sm.P, K, tid);  // P, lower with the diagonal
+    fc_b_row<FK>(sm.al, sm.m, sm.bt, K, tid);
+    fc_tri<FK, false>(sm.q, sm.k, sm.al, sm.m, sm.P, K, tid);  // P, lower with the diagonal
     // W' rows of this chunk
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int i = 4 * g + e;
+    for (int e = 0; e < Fc<FK>::EPT; ++e) {
+        const int i = Fc<FK>::ch(g, e);
         sm.w[t * LQ + i] = i < K ? a.fw[((int64_t)ci * C + t) * fc_kp(K) + i] : 0.f;
     }
     __syncthreads();
-    // Wave w: value tile w on v_mfma_f32_16x16x4f32 (lane (lg, ln): rows 4 lg + r,
-    // column 16 w + ln).  X = P^T dO + c delta, then per key tile tau
-    // N = Qhat^T dO - W'^T X, X's accumulator rows as the B operand.
+    // Wave w: value tiles w, w + NW, .. on v_mfma_f32_16x16x4f32 (lane (lg, ln):
+    // rows 4 lg + r, column 16 vt + ln).  X = P^T dO + c delta, then per key tile
+    // tau N = Qhat^T dO - W'^T X, X's accumulator rows as the B operand.
     const int w = tid >> 6, l = tid & 63, lg = l >> 4, ln = l & 15, VT = (V + 15) >> 4, KT = fc_kp(K) >> 4;
-    if (w < VT) {
-        const int j = 16 * w + ln;
+    for (int vt = w; vt < VT; vt += NW) {
+        const int j = 16 * vt + ln;
         f32x4 x;
 #pragma unroll
         for (int q = 0; q < 4; ++q) x[q] = sm.cs[4 * lg + q] * sm.dl[(4 * lg + q) * LQ + j];
@@ -563,11 +659,9 @@ __global__ void __launch_bounds__(NT) fc_bprep_kernel(FcArgs a) {
                                                          0, 0, 0);
                 n = __builtin_amdgcn_mfma_f32_16x16x4f32(-sm.w[tt * LQ + i], x[q], n, 0, 0, 0);
             }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int ii = 16 * tau + 4 * lg + r;
-                if (ii < K && j < V) a.n[((int64_t)ci * K + ii) * V + j] = n[r];
-            }
+            // lane-packed for the scan; zero outside K x V, where the tiles are
+            *reinterpret_cast<float4 *>(&a.n[((((int64_t)ci * VT + vt) * KT + tau) * 64 + l) * 4]) =
+                make_float4(n[0], n[1], n[2], n[3]);
         }
     }
 }
@@ -589,20 +683,22 @@ __global__ void __launch_bounds__(NT) fc_bprep_kernel(FcArgs a) {
 // through b_t; end pairs k_s dKtil_s through lam_s; rowsum(S0 . dS) through
 // b_15): sum_{lo < u} L(lo, u) Y(u, lo) with L the gates over (lo, u) and Y by
 // Horner over hi, exact for zero and negative gates.
-__global__ void __launch_bounds__(NT) fc_bgrad_kernel(FcArgs a) {
-    __shared__ FcBGradSmem sm;
+template <int FK>
+__global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
+    __shared__ FcBGradSmem<FK> sm;
+    constexpr int LQ = Fc<FK>::LQ, NT = Fc<FK>::NT, NW = Fc<FK>::NW;
     const SeqArgs &s = a.s;
     const int tid = threadIdx.x, ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / s.H, h = bh % s.H;
-    const int K = s.K, V = s.V, t = tid >> 4, g = tid & 15, tg = c * C + t;
-    const int KT = (K + 15) >> 4, VT = (V + 15) >> 4, VP = 16 * VT;
+    const int K = s.K, V = s.V, t = tid / Fc<FK>::LPT, g = tid % Fc<FK>::LPT, tg = c * C + t;
+    const int KT = (K + 15) >> 4, VT = (V + 15) >> 4, VP = 16 * VT, KP = 16 * KT;
     const int w = tid >> 6, l = tid & 63, lg = l >> 4, ln = l & 15;
     fc_masks(s, b, c, sm.m, tid);
     const bool on = sm.m.val[t] != 0.f;
     const bool score_adj = s.dscores != nullptr;
     float ksq = 0.f, dsq = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int i = 4 * g + e;
+    for (int e = 0; e < Fc<FK>::EPT; ++e) {
+        const int i = Fc<FK>::ch(g, e);
         const float kv = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, on);
         sm.q[t * LQ + i] = fc_x(s.q, a.in_bf16, b, tg, h, i, s.T, K, on);
         sm.k[t * LQ + i] = kv;
@@ -614,8 +710,8 @@ __global__ void __launch_bounds__(NT) fc_bgrad_kernel(FcArgs a) {
         ksq += kv * kv;
         dsq += d * d;
     }
-    ksq += __shfl_xor(ksq, 1), ksq += __shfl_xor(ksq, 2), ksq += __shfl_xor(ksq, 4), ksq += __shfl_xor(ksq, 8);
-    dsq += __shfl_xor(dsq, 1), dsq += __shfl_xor(dsq, 2), dsq += __shfl_xor(dsq, 4), dsq += __shfl_xor(dsq, 8);
+    ksq = Fc<FK>::row_sum(ksq);
+    dsq = Fc<FK>::row_sum(dsq);
     if (g == 0) {
         const float nk = sqrtf(ksq), nd = sqrtf(dsq);
         const float dsc = (score_adj && tg < s.T) ? s.dscores[((int64_t)b * s.T + tg) * s.H + h] : 0.f;
@@ -623,89 +719,99 @@ __global__ void __launch_bounds__(NT) fc_bgrad_kernel(FcArgs a) {
         sm.cs[t] = ok ? dsc * nk / nd : 0.f;
         sm.ck[t] = ok ? dsc * nd / nk : 0.f;
     }
-    {
-        const float *st = a.st + (int64_t)ci * K * V, *ds = a.ds + (int64_t)ci * K * V;
-        const int KP = 16 * KT;
-        for (int e = tid; e < KP * VP; e += NT) {
-            const int i = e / VP, j = e - i * VP;
-            const bool in = i < K && j < V;
-            sm.u.st.s0[i * LS + j] = in ? st[i * V + j] : 0.f;
-            sm.u.st.ds[i * LS + j] = in ? ds[i * V + j] : 0.f;
-        }
-    }
-    sm.T[(tid >> 4) * LT + (tid & 15)] = a.tm[(int64_t)ci * C * C + tid];
+    if (tid < C * C) sm.T[(tid >> 4) * LT + (tid & 15)] = a.tm[(int64_t)ci * C * C + tid];
     __syncthreads();
-    fc_decay_rows(sm.al, sm.m, sm.bt, sm.lam, K, tid);
-    fc_tri<false>(sm.q, sm.k, sm.al, sm.m, sm.P, K, tid);
-    {  // rowsum(S0 . dS) of key channel i = tid / 4, in four column quarters
-        const int i = tid >> 2, j0 = 16 * (tid & 3);
-        float f = 0.f;
-        if (i < 16 * KT && j0 < VP)  // inside the zero-padded tiles
-#pragma unroll
-            for (int j = 0; j < 16; ++j) f += sm.u.st.s0[i * LS + j0 + j] * sm.u.st.ds[i * LS + j0 + j];
-        f += __shfl_xor(f, 1);
-        f += __shfl_xor(f, 2);
-        if ((tid & 3) == 0) sm.fs[i] = f;
-    }
-    __syncthreads();
-    // ddelta and dR of value tile w (lane (lg, ln): rows 4 lg + r, column 16 w + ln)
-    if (w < VT) {
-        const int j = 16 * w + ln;
-        f32x4 dd;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dd[r] = sm.cs[4 * lg + r] * sm.dl[(4 * lg + r) * LQ + j];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            dd = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.P[(4 * lg + q) * LT + ln], sm.dO[(4 * lg + q) * LQ + j], dd,
-                                                      0, 0, 0);
-        for (int tau = 0; tau < KT; ++tau)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int i = 16 * tau + 4 * lg + q;
-                dd = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.lam[ln * LQ + i] * sm.k[ln * LQ + i],
-                                                          sm.u.st.ds[i * LS + j], dd, 0, 0, 0);
-            }
-        f32x4 dr = zero4();
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            dr = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.T[(4 * lg + q) * LT + ln], dd[q], dr, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int tt = 4 * lg + r, tq = c * C + tt;
-            sm.dr[tt * LQ + j] = dr[r];
-            if (j < V && tq < s.T) {
-                const bool von = sm.m.val[tt] != 0.f;
-                const int64_t o = (((int64_t)b * s.T + tq) * s.H + h) * V + j;
-                if (s.dwrite) s.dwrite[o] = von ? dr[r] * fc_ld(s.v, a.in_bf16, b, tq, h, j) : 0.f;
-                if (s.dv) store_out(s.dv, a.in_bf16, o, von ? dr[r] * ld4<float>(s.write, b, tq, h, j) : 0.f);
-            }
-        }
-    }
-    __syncthreads();
-    // The 16 x 16 products over the value axis: tiles 0 .. 3 KT - 1 are dAhat,
-    // dQhat, dKtil of key tile tau = n / 3; tile 3 KT is dA, 3 KT + 1 is dP.
+    fc_decay_rows<FK>(sm.al, sm.m, sm.bt, sm.lam, K, tid);
+    fc_tri<FK, false>(sm.q, sm.k, sm.al, sm.m, sm.P, K, tid);
+    // The value axis in blocks of VB columns (one block at FK = 64, two at FK =
+    // 128), each with its columns of S0 and dS in LDS.  Per block: ddelta and dR
+    // of its value tiles, then the 16 x 16 products that reduce over the value
+    // axis take the block's part: tiles 0 .. 3 KT - 1 are dAhat, dQhat, dKtil of
+    // key tile tau = n / 3; tile 3 KT is dA, 3 KT + 1 is dP (wave w takes tiles
+    // w, w + NW, ..).
+    constexpr int MT = (3 * (FK / 16) + 2 + NW - 1) / NW;
     const int ntile = 3 * KT + 2;
-    f32x4 res[4];
+    f32x4 res[MT];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const int n = w + 4 * m;
-        res[m] = zero4();
-        if (n >= ntile) continue;
-        const int kind = n < 3 * KT ? n % 3 : 3 + (n - 3 * KT), tau = n < 3 * KT ? n / 3 : 0;
-        const float *xa = kind == 0 || kind == 3 ? sm.dr : (kind == 2 ? sm.dl : sm.dO);
-        const float *yb = kind == 2 ? sm.u.st.ds : sm.u.st.s0;
-        const int yo = kind >= 3 ? 0 : (16 * tau + ln) * LS, ys = kind >= 3 ? LQ : LS;
-        const float *yy = kind >= 3 ? sm.dl + ln * LQ : yb + yo;
-        (void)ys;
-        f32x4 acc = zero4();
-        for (int kk = 0; kk < VP; kk += 4)
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[ln * LQ + kk + lg], yy[kk + lg], acc, 0, 0, 0);
-        res[m] = acc;
+    for (int m = 0; m < MT; ++m) res[m] = zero4();
+    const float *st = a.st + (int64_t)ci * K * V, *dst = a.ds + (int64_t)ci * K * V;
+    const bool v4 = (V & 3) == 0 && ((reinterpret_cast<uintptr_t>(a.st) | reinterpret_cast<uintptr_t>(a.ds)) & 15) == 0;
+    for (int j0 = 0; j0 < VP; j0 += VB) {
+        if (j0 > 0) __syncthreads();  // the previous block's products have read S0 and dS
+        if (v4)
+            fc_stage2_v4<NT, VB, 4>(sm.u.st.s0, sm.u.st.ds, LB, st + j0, dst + j0, V, KP, K, V - j0, tid);
+        else
+            fc_stage2<NT, VB, 8>(sm.u.st.s0, sm.u.st.ds, LB, st + j0, dst + j0, V, KP, K, V - j0, tid);
+        __syncthreads();
+        {  // rowsum(S0 . dS) of key channel i over the block: TPC threads per channel
+            constexpr int TPC = NT / FK, CW = VB / TPC;
+            const int i = tid / TPC, jq = CW * (tid % TPC);
+            float f = 0.f;
+            if (i < KP)  // rows past KP are not loaded
+#pragma unroll
+                for (int j = 0; j < CW; ++j) f += sm.u.st.s0[i * LB + jq + j] * sm.u.st.ds[i * LB + jq + j];
+            f += __shfl_xor(f, 1);
+            f += __shfl_xor(f, 2);
+            static_assert(TPC == 4, "four threads per key channel");
+            if (tid % TPC == 0) sm.fs[i] = (j0 > 0 ? sm.fs[i] : 0.f) + f;
+        }
+        // ddelta and dR of value tile vt = j0 / 16 + w, waves 0 .. 3 (lane (lg, ln):
+        // rows 4 lg + r, column 16 vt + ln)
+        const int vt = j0 / 16 + w;
+        if (w < VB / 16 && vt < VT) {
+            const int j = 16 * vt + ln, jl = j - j0;
+            f32x4 dd;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dd[r] = sm.cs[4 * lg + r] * sm.dl[(4 * lg + r) * LQ + j];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                dd = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.P[(4 * lg + q) * LT + ln], sm.dO[(4 * lg + q) * LQ + j],
+                                                          dd, 0, 0, 0);
+            for (int tau = 0; tau < KT; ++tau)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int i = 16 * tau + 4 * lg + q;
+                    dd = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.lam[ln * LQ + i] * sm.k[ln * LQ + i],
+                                                              sm.u.st.ds[i * LB + jl], dd, 0, 0, 0);
+                }
+            f32x4 dr = zero4();
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                dr = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.T[(4 * lg + q) * LT + ln], dd[q], dr, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tt = 4 * lg + r, tq = c * C + tt;
+                sm.dr[tt * LQ + j] = dr[r];
+                if (j < V && tq < s.T) {
+                    const bool von = sm.m.val[tt] != 0.f;
+                    const int64_t o = (((int64_t)b * s.T + tq) * s.H + h) * V + j;
+                    if (s.dwrite) s.dwrite[o] = von ? dr[r] * fc_ld(s.v, a.in_bf16, b, tq, h, j) : 0.f;
+                    if (s.dv) store_out(s.dv, a.in_bf16, o, von ? dr[r] * ld4<float>(s.write, b, tq, h, j) : 0.f);
+                }
+            }
+        }
+        __syncthreads();  // the block's dR columns are in LDS
+        const int je = VP - j0 < VB ? VP - j0 : VB;  // the block's columns inside the value tiles
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const int n = w + NW * m;
+            if (n >= ntile) continue;
+            const int kind = n < 3 * KT ? n % 3 : 3 + (n - 3 * KT), tau = n < 3 * KT ? n / 3 : 0;
+            // A: [token][value] rows; B: S0 or dS rows of key 16 tau + ln (block
+            // columns), or delta rows (value columns) for dA and dP
+            const float *xa = (kind == 0 || kind == 3 ? sm.dr : (kind == 2 ? sm.dl : sm.dO)) + ln * LQ + j0;
+            const float *yy = kind >= 3 ? sm.dl + ln * LQ + j0
+                                        : (kind == 2 ? sm.u.st.ds : sm.u.st.s0) + (16 * tau + ln) * LB;
+            f32x4 acc = res[m];
+            for (int kk = 0; kk < je; kk += 4)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[kk + lg], yy[kk + lg], acc, 0, 0, 0);
+            res[m] = acc;
+        }
     }
     __syncthreads();  // S0 and dS are no longer read: their space takes dAhat, dQhat, dKtil
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const int n = w + 4 * m;
+    for (int m = 0; m < MT; ++m) {
+        const int n = w + NW * m;
         if (n >= ntile) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -722,14 +828,14 @@ __global__ void __launch_bounds__(NT) fc_bgrad_kernel(FcArgs a) {
         }
     }
     __syncthreads();
-    // Per key channel: lane i of a group of cpl lanes, rpw groups per wave; the
-    // lane keeps its channel's gates, k, q and ehat of the whole chunk in
-    // registers.  Group (w, sub) takes the rows u = 4 rpw p + rpw w + sub
-    // (p < 4 / rpw): the token rows of eA, qP, kAP and the outputs, then the
-    // start rows lo = u - 1 of the alpha gradient's pairs, whose partial sums
-    // over lo meet in LDS.
-    const int cpl = K <= 16 ? 16 : (K <= 32 ? 32 : 64), rpw = 64 / cpl;
-    const int i = l % cpl, sub = l / cpl, sg15 = sm.m.seg[C - 1], np = 4 / rpw;
+    // Per key channel: thread i of a group of cpl threads, ngr = NT / cpl groups
+    // (at most C; threads of further groups idle here);
+    // the thread keeps its channel's gates, k, q and ehat of the whole chunk in
+    // registers.  Group gi takes the rows u = ngr p + gi (p < C / ngr): the token
+    // rows of eA, qP, kAP and the outputs, then the start rows lo = u - 1 of the
+    // alpha gradient's pairs, whose partial sums over lo meet in LDS.
+    const int cpl = K <= 16 ? 16 : (K <= 32 ? 32 : (K <= 64 ? 64 : 128)), ngr = min(NT / cpl, C);
+    const int i = tid % cpl, gi = tid / cpl, sg15 = sm.m.seg[C - 1], np = gi < ngr ? C / ngr : 0;
     const bool iv = i < K;
     float ra[C], rk[C], rq[C], re[C];
     int sg[C];
@@ -742,7 +848,7 @@ __global__ void __launch_bounds__(NT) fc_bgrad_kernel(FcArgs a) {
         sg[x] = sm.m.seg[x];
     }
     for (int p = 0; p < np; ++p) {
-        const int u = 4 * rpw * p + rpw * w + sub, su = sm.m.seg[u];
+        const int u = ngr * p + gi, su = sm.m.seg[u];
         // eA, qP of row u (s <= u) and kAP of row u (t >= u); the running
         // decays stop at u's segment, where dA and dP end as well
         float eA = 0.f, qP = 0.f, kAP = 0.f, d = 1.f, d2 = 1.f;
@@ -781,7 +887,7 @@ __global__ void __launch_bounds__(NT) fc_bgrad_kernel(FcArgs a) {
 #pragma unroll
     for (int x = 0; x < C; ++x) dal[x] = 0.f;
     for (int p = 0; p < np; ++p) {
-        const int lo = 4 * rpw * p + rpw * w + sub - 1;  // -1 .. 14
+        const int lo = ngr * p + gi - 1;  // -1 .. 14
         const float kl = lo >= 0 ? sm.k[lo * LQ + i] : 0.f;
         const float endc = (lo >= 0 && sm.m.seg[lo] == sg15) ? kl * sm.u.gr.gk[lo * LQ + i] : 0.f;
         float Y[C], y = 0.f;
@@ -808,8 +914,8 @@ __global__ void __launch_bounds__(NT) fc_bgrad_kernel(FcArgs a) {
                 L *= ra[x];
             }
     }
-    // partials [group][u][channel] (4 rpw groups of C x cpl), then one sum per (u, channel)
-    float *part = sm.u.gr.part + (w * rpw + sub) * (C * cpl);
+    // partials [group][u][channel] (ngr groups of C x cpl), then one sum per (u, channel)
+    float *part = sm.u.gr.part + gi * (C * cpl);
 #pragma unroll
     for (int x = 0; x < C; ++x) part[x * cpl + i] = dal[x];
     __syncthreads();
@@ -817,7 +923,7 @@ __global__ void __launch_bounds__(NT) fc_bgrad_kernel(FcArgs a) {
         const int u = e / cpl, ch = e - u * cpl;
         if (ch >= K) continue;
         float x = 0.f;
-        for (int gq = 0; gq < 4 * rpw; ++gq) x += sm.u.gr.part[gq * (C * cpl) + e];
+        for (int gq = 0; gq < ngr; ++gq) x += sm.u.gr.part[gq * (C * cpl) + e];
         const int tq = c * C + u;
         if (tq < s.T && s.dalpha)
             s.dalpha[(((int64_t)b * s.T + tq) * s.H + h) * K + ch] =
@@ -829,31 +935,46 @@ static inline void fmark(const hipEvent_t *ev, int i, hipStream_t stream) {
     if (ev) (void)hipEventRecord(ev[i], stream);
 }
 
-hipError_t launch_fc_fwd(const FcArgs &a, hipStream_t stream, const hipEvent_t *ev) {
+// FK = 128 when either width is above 64.
+static bool fc_wide(const FcArgs &a) { return a.s.K > 64 || a.s.V > 64; }
+
+template <int FK>
+static void fc_fwd(const FcArgs &a, hipStream_t stream, const hipEvent_t *ev) {
     const int n = a.s.B * a.s.H * a.nc;
     fmark(ev, 0, stream);
-    hipLaunchKernelGGL(fc_prep_kernel, dim3(n), dim3(NT), 0, stream, a);
+    hipLaunchKernelGGL(fc_prep_kernel<FK>, dim3(n), dim3(Fc<FK>::NT), 0, stream, a);
     fmark(ev, 1, stream);
     fmark(ev, 2, stream);
     launch_fc_scan<false>(a, stream);
     fmark(ev, 3, stream);
     fmark(ev, 4, stream);
-    hipLaunchKernelGGL(fc_out_kernel, dim3(n), dim3(NT), 0, stream, a);
+    hipLaunchKernelGGL(fc_out_kernel<FK>, dim3(n), dim3(Fc<FK>::NT), 0, stream, a);
     fmark(ev, 5, stream);
-    return hipGetLastError();
 }
 
-hipError_t launch_fc_bwd(const FcArgs &a, hipStream_t stream, const hipEvent_t *ev) {
+template <int FK>
+static void fc_bwd(const FcArgs &a, hipStream_t stream, const hipEvent_t *ev) {
     const int n = a.s.B * a.s.H * a.nc;
     fmark(ev, 0, stream);
-    hipLaunchKernelGGL(fc_bprep_kernel, dim3(n), dim3(NT), 0, stream, a);
+    hipLaunchKernelGGL(fc_bprep_kernel<FK>, dim3(n), dim3(Fc<FK>::NT), 0, stream, a);
     fmark(ev, 1, stream);
     fmark(ev, 2, stream);
     launch_fc_scan<true>(a, stream);
     fmark(ev, 3, stream);
     fmark(ev, 4, stream);
-    hipLaunchKernelGGL(fc_bgrad_kernel, dim3(n), dim3(NT), 0, stream, a);
+    hipLaunchKernelGGL(fc_bgrad_kernel<FK>, dim3(n), dim3(Fc<FK>::NT), 0, stream, a);
     fmark(ev, 5, stream);
+}
+
+hipError_t launch_fc_fwd(const FcArgs &a, hipStream_t stream, const hipEvent_t *ev) {
+    if (fc_wide(a)) fc_fwd<128>(a, stream, ev);
+    else fc_fwd<64>(a, stream, ev);
+    return hipGetLastError();
+}
+
+hipError_t launch_fc_bwd(const FcArgs &a, hipStream_t stream, const hipEvent_t *ev) {
+    if (fc_wide(a)) fc_bwd<128>(a, stream, ev);
+    else fc_bwd<64>(a, stream, ev);
     return hipGetLastError();
 }
 

@@ -15,7 +15,7 @@ joins the scan output scaled by sigmoid(cache gate) per head:
   out += hola_read(rms(q_raw), rms(k_raw), v, scores, ...) * sigmoid(gate)
 The convolution fuses its SiLU (one pass over the projection), the gated RMSNorm
 is one pass, and the recurrence is the HIP scan (channel-wise gates: the
-token-sequential kernels).  Projections are plain GEMMs (torch, hipBLASLt).
+16-token chunk kernels).  Projections are plain GEMMs (torch, hipBLASLt).
 The reference's SBD block is not part of this module.
 """
 from __future__ import annotations

@@ -87,15 +87,17 @@ GDN2_API const char *gdn2_last_error(void);
  *
  * q, k, v: F32 or BF16 (same dtype); alpha, erase, write, valid, reset,
  * initial: F32.  initial.data may be NULL (zero state).  chunk: 1..64, the
- * checkpoint interval in tokens of the token-sequential kernels (the
- * reference allows 1..16, gdn_training.rs:370-373); results do not depend on
- * it.  bf16 q/k/v with keys = values = 64, unit channel stride and 16-byte
- * aligned token rows run the 16-token chunk-WY MFMA kernels whatever the
- * chunk argument; everything else runs the token-sequential kernels.  The
- * chunk kernels need alpha >= 0 on valid tokens: a negative alpha gives NaN
- * outputs, state and gradients for its sequence (the token-sequential kernels
- * accept any alpha).  alpha = 0 and tiny alphas get their exact gradient on
- * both.  On the chunk kernels d_output must have aligned rows too. */
+ * checkpoint interval of the reference (1..16, gdn_training.rs:370-373; up to
+ * 64 accepted here); results do not depend on it.  bf16 q/k/v with keys =
+ * values = 64, unit channel stride and 16-byte aligned token rows run the
+ * 16-token chunk-WY MFMA kernels; every other shape (keys, values <= 128, f32
+ * or bf16, any strides) runs the 16-token f32 chunk kernels, which read bf16
+ * inputs as their exact f32 values.  The bf16 MFMA kernels need alpha >= 0 on
+ * valid tokens: a negative alpha gives NaN outputs, state and gradients for
+ * its sequence (the f32 chunk kernels accept any alpha).  alpha = 0 and tiny
+ * alphas get their exact gradient on both.  On the MFMA kernels d_output must
+ * have aligned rows too.  checkpoint (and the backward's workspace) must be
+ * 16-byte aligned. */
 GDN2_API size_t gdn2_training_checkpoint_bytes(const gdn2_shape *shape, int chunk);
 
 GDN2_API int gdn2_training_scan(const gdn2_shape *shape, int chunk, const gdn2_view *q,
@@ -142,11 +144,12 @@ GDN2_API int gdn2_training_backward(const gdn2_shape *shape, int chunk, const gd
  * has no preceding end or an end no following reset.  Zero initial state; no
  * final state or score outputs.  q, k, v: F32 or BF16 (same dtype); alpha,
  * erase, write: F32.  bf16 q/k/v with keys = values = 64 and 16-byte aligned
- * rows run the 16-token chunk-WY MFMA kernels, everything else the
- * token-sequential kernels.  The chunk kernels need alpha >= 0 on live tokens
- * (a negative alpha gives NaN results for its sequence); the token-sequential
- * kernels accept any alpha.  The checkpoint (opaque) replaces the reference's
- * [B, H, T/16, 48, 64] checkpoint tensor. */
+ * rows run the 16-token chunk-WY MFMA kernels, every other shape (keys, values
+ * <= 128) the 16-token f32 chunk kernels.  The MFMA kernels need alpha >= 0 on
+ * live tokens (a negative alpha gives NaN results for its sequence); the f32
+ * chunk kernels accept any alpha.  The checkpoint (opaque, 16-byte aligned, as
+ * is the backward's workspace) replaces the reference's [B, H, T/16, 48, 64]
+ * checkpoint tensor. */
 GDN2_API size_t gdn2_scan_checkpoint_bytes(const gdn2_shape *shape);
 
 GDN2_API int gdn2_scan(const gdn2_shape *shape, const gdn2_view *q, const gdn2_view *k,

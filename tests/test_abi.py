@@ -54,7 +54,7 @@ def _view(dtype=0, data=0x1000):
     return v
 
 
-def _scan(L, shape, chunk=16, qdtype=0, gdtype=0, ck_bytes=None, out_dtype=0, nulls=()):
+def _scan(L, shape, chunk=16, qdtype=0, gdtype=0, ck_bytes=None, out_dtype=0, nulls=(), ck=0x5000):
     vs = [_view(qdtype)] * 3 + [_view(gdtype)] * 3 + [_view(0)] * 2
     vs = [(_view(v.dtype, 0) if i in nulls else v) for i, v in enumerate(vs)]
     init = _view(0, 0)
@@ -63,7 +63,7 @@ def _scan(L, shape, chunk=16, qdtype=0, gdtype=0, ck_bytes=None, out_dtype=0, nu
     return L.gdn2_training_scan(ctypes.byref(shape), chunk, *[ctypes.byref(v) for v in vs],
                                 ctypes.byref(init), ctypes.c_void_p(0x2000), out_dtype,
                                 ctypes.c_void_p(0x3000), ctypes.c_void_p(0x4000),
-                                ctypes.c_void_p(0x5000), size, None)
+                                ctypes.c_void_p(ck), size, None)
 
 
 @pytest.mark.parametrize("shape,msg", [((0, 8, 2, 32, 64), "nonempty"),
@@ -99,6 +99,12 @@ def test_rejects_small_checkpoint(L):
     assert need > 0
     assert _scan(L, s, ck_bytes=need - 1) == 4
     assert "checkpoint" in L.gdn2_last_error().decode()
+
+
+def test_rejects_misaligned_checkpoint(L):
+    """The chunk kernels read the checkpoint with 16-byte loads."""
+    assert _scan(L, _shape(), ck=0x5004) == 1
+    assert "16-byte aligned" in L.gdn2_last_error().decode()
 
 
 def test_workspace_sizes_scale(L):

@@ -166,8 +166,8 @@ def test_cw_alpha_zero_exact_gradient(dk):
 def test_cw_negative_alpha_fails_loudly(dk):
     """A negative alpha is outside the chunk kernels' log-domain decays: the
     sequence that holds it gets NaN outputs (never finite wrong values), the
-    other sequences are untouched, and the f32 token-sequential kernels give
-    the oracle's values for the same inputs."""
+    other sequences are untouched, and the f32 chunk kernels give the oracle's
+    values for the same inputs."""
     p = cw_problem(83, 2, 40, 1, masks=False)
     p["alpha"][1, 12, 0, 5] = -0.5
     x, init = _inputs(p, grad=False)
@@ -181,8 +181,8 @@ def test_cw_negative_alpha_fails_loudly(dk):
     xf = {n: dev(p[n]) for n in ("q", "k", "v")}
     rf = dk.gdn_training_scan(xf["q"], xf["k"], xf["v"], x["alpha"], x["erase"], x["write"],
                               dev(p["valid"]), dev(p["reset"]), init, 16)
-    gate("f32 (token-sequential) output with a negative alpha", rf.output, o_out, 1e-4)
-    gate("f32 (token-sequential) final state with a negative alpha", rf.final_state, o_fin, 1e-4)
+    gate("f32 (chunk kernels) output with a negative alpha", rf.output, o_out, 1e-4)
+    gate("f32 (chunk kernels) final state with a negative alpha", rf.final_state, o_fin, 1e-4)
 
 
 @pytest.mark.parametrize("t,mode", [(7, 0), (35, 0), (35, 1), (35, 2), (35, 3)])

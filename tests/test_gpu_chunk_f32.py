@@ -1,5 +1,5 @@
 """The f32 chunk kernels (csrc/gdn2_chunk_f32.hip): channel-wise GDN-2 with f32
-q/k/v and d_k, d_v <= 64, in 16-token chunks, against the f64 oracle.
+q/k/v and d_k, d_v <= 128, in 16-token chunks, against the f64 oracle.
 
 1. The reference's isolated-scan benchmark workload (kron_benchmark.rs:73-116:
    B8 T512 H4 K32 V64, alpha in [0.90, 0.99], erase/write in [0.1, 0.9], unit
@@ -12,11 +12,14 @@ q/k/v and d_k, d_v <= 64, in 16-token chunks, against the f64 oracle.
    p = 16, so the exact alpha gradient at alpha = 0 is gated too.
 3. Gates the chunk kernels handle with no special case, because they form every
    decay as a product of the gates: negative alpha, alpha = 0 on a whole
-   chunk, tiny alpha; and ragged widths (d_k, d_v in 1..64) with padding and
-   resets inside chunks and sequence ends off the chunk grid.
-4. Slow decay over 256 chunks (T = 4096), at both gates.
-5. bf16 q/k/v at widths the bf16 chunk kernels do not take (d_k != d_v, or
-   below 64): the same kernels read the exact f32 values of the bf16 inputs and
+   chunk, tiny alpha; and ragged widths (d_k, d_v in 1..128: the kernels built
+   for 64-wide tiles up to 64, for 128-wide tiles above, where bgrad walks the
+   value axis in two blocks) with padding and resets inside chunks and sequence
+   ends off the chunk grid.
+4. Slow decay over 256 chunks (T = 4096) at K32/V64, and over 128 chunks
+   (T = 2048) at K = V = 128, at both gates.
+5. bf16 q/k/v at widths the bf16 chunk kernels do not take (d_k != d_v, below
+   64 or above): the same kernels read the exact f32 values of the bf16 inputs and
    write bf16 gradients; gated at the bf16 tolerance against the oracle run on
    the bf16-rounded inputs.
 """
@@ -124,7 +127,8 @@ def _random(seed, B, T, H, K, V, alpha=(0.8, 1.0), masks=True):
 
 
 @pytest.mark.parametrize("K,V,T", [(1, 1, 19), (3, 4, 33), (17, 64, 50), (64, 33, 64),
-                                   (64, 64, 77), (32, 64, 130)])
+                                   (64, 64, 77), (32, 64, 130), (128, 128, 70), (96, 128, 50),
+                                   (128, 33, 40), (65, 64, 33), (1, 128, 20), (128, 80, 47)])
 def test_ragged_widths(dk, K, V, T):
     f = _random(K * 100 + V, 2, T, 3, K, V)
     print(f"f32 chunk: widths K{K} V{V} T{T}", flush=True)
@@ -163,6 +167,20 @@ def test_slow_decay_long(dk, alpha):
     assert STAGES <= ran, sorted(ran)
 
 
+@pytest.mark.parametrize("alpha", [(0.9, 0.99), (0.999, 1.0)])
+def test_slow_decay_wide(dk, alpha):
+    """128 chunks at K = V = 128 with slow decay: the 128-wide kernels and the
+    eight-tile scans.  Both draws pass the 1e-4 gate; the reference's gate
+    2e-5 + 3e-4|ref| is applied to alpha in [0.90, 0.99].  With alpha >= 0.999
+    the gradients grow to rms 30 (dk; max 159) and its absolute term, 7e-7 of
+    that rms, lies under the rounding of 128-term f32 sums carried over 2048
+    tokens, which the 1e-4 gate (relative to |ref| + rms) allows for."""
+    f = _random(8, 2, 2048, 1, 128, 128, alpha=alpha)
+    print(f"f32 chunk: slow decay alpha {alpha} T2048 K128 V128", flush=True)
+    ran, _ = run_and_check(dk, f, ref_gate=alpha[0] < 0.999)
+    assert STAGES <= ran, sorted(ran)
+
+
 def _bf16_round(f):
     """q, k, v and the output adjoint as the bf16 values the kernels receive (dO
     has q's dtype), so the oracle and the kernels see the same inputs."""
@@ -171,7 +189,8 @@ def _bf16_round(f):
     return f
 
 
-@pytest.mark.parametrize("K,V,T", [(32, 64, 512), (17, 64, 50), (64, 33, 77), (16, 16, 40)])
+@pytest.mark.parametrize("K,V,T", [(32, 64, 512), (17, 64, 50), (64, 33, 77), (16, 16, 40),
+                                   (128, 128, 100), (80, 128, 50)])
 def test_bf16_inputs(dk, K, V, T):
     f = _bf16_round(_random(K * 7 + V, 2, T, 3, K, V))
     print(f"f32 chunk: bf16 inputs K{K} V{V} T{T}", flush=True)

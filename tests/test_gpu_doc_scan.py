@@ -15,9 +15,8 @@
    GPU kernels compute it (crates/kernels/src/gdn2.rs:24-65, :288-490); the
    reference's f64 oracle lets the adjoint cross that reset instead.
 4. bf16 with K = V = 64 runs the 16-token chunk-WY MFMA kernels (stage
-   timers); f32 with K, V <= 64 (items 1 and 2 at K32/V64 and K = V = 64) the
-   f32 chunk kernels; bf16 at other widths and K = V = 128 the
-   token-sequential kernels.
+   timers); every other width and dtype the f32 chunk kernels (items 1 and 2,
+   and bf16 at 32 x 64 and 128 x 128 with the stage timers).
 """
 import numpy as np
 import pytest
@@ -201,10 +200,10 @@ def test_inconsistent_limits_follow_reference_kernels(dk, dtype):
     assert np.abs(cpu_rule["k"][0, :20] - exact["k"][0, :20]).max() > 1e-2
 
 
-@pytest.mark.parametrize("kv", [(64, 64), (32, 64)])
+@pytest.mark.parametrize("kv", [(64, 64), (32, 64), (128, 128)])
 def test_bf16_runs_chunk_kernels(dk, kv):
-    """bf16 at 64 x 64 runs the bf16 chunk kernels, at 32 x 64 the f32 chunk
-    kernels; both report the six chunk stages."""
+    """bf16 at 64 x 64 runs the bf16 chunk kernels, at 32 x 64 and 128 x 128
+    the f32 chunk kernels; each reports the six chunk stages."""
     x, start, end, up = _packed_problem(2, 100, 3, kv[0], kv[1], 9)
     xs = [dev(a, torch.bfloat16 if i < 3 else torch.float32).requires_grad_(True)
           for i, a in enumerate(x)]
