@@ -66,13 +66,14 @@ struct Masks {
     int seg[C];  // valid resets at or before the token
 };
 
-// Token masks (valid / reset, or the document limits) and segments.  Ends with
-// a barrier.
+// Token masks (valid / reset, or the document limits) and segments (an
+// inclusive prefix sum of the valid resets over the chunk's 16 tokens, by lane
+// shuffles in wave 0).  Ends with a barrier.
 __device__ void fc_masks(const SeqArgs &s, int b, int c, Masks &m, int tid) {
-    if (tid < C) {
+    if (tid < 64) {
         const int tg = c * C + tid;
         float vld = 0.f, rst = 0.f;
-        if (tg < s.T) {
+        if (tid < C && tg < s.T) {
             if (s.doc) {
                 const int st = reinterpret_cast<const int *>(s.doc_start.data)[b * s.doc_start.s0 + tg * s.doc_start.s1];
                 const int en = reinterpret_cast<const int *>(s.doc_end.data)[b * s.doc_end.s0 + tg * s.doc_end.s1];
@@ -83,15 +84,17 @@ __device__ void fc_masks(const SeqArgs &s, int b, int c, Masks &m, int tid) {
                 rst = ld4<float>(s.reset, b, tg, 0, 0);
             }
         }
-        m.val[tid] = vld != 0.f ? 1.f : 0.f;
-        m.rs[tid] = (vld != 0.f && rst != 0.f) ? 1 : 0;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        int sg = 0;
-        for (int t = 0; t < C; ++t) {
-            sg += m.rs[t];
-            m.seg[t] = sg;
+        const int r = (vld != 0.f && rst != 0.f) ? 1 : 0;
+        int sg = r;
+#pragma unroll
+        for (int d = 1; d < C; d <<= 1) {
+            const int y = __shfl_up(sg, d);
+            if (tid >= d) sg += y;
+        }
+        if (tid < C) {
+            m.val[tid] = vld != 0.f ? 1.f : 0.f;
+            m.rs[tid] = r;
+            m.seg[tid] = sg;
         }
     }
     __syncthreads();
@@ -305,17 +308,28 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_prep_kernel(FcArgs a) {
     const SeqArgs &s = a.s;
     const int tid = threadIdx.x, ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / s.H, h = bh % s.H;
     const int K = s.K, V = s.V, t = tid / Fc<FK>::LPT, g = tid % Fc<FK>::LPT, tg = c * C + t;
+    // The token rows are loaded before the masks arrive and masked after.
+    constexpr int EPT = Fc<FK>::EPT;
+    float rk[EPT], ral[EPT], re[EPT], rw[EPT], rv[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int i = Fc<FK>::ch(g, e);
+        rk[e] = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, true);
+        ral[e] = (i < K && tg < s.T) ? ld4<float>(s.alpha, b, tg, h, i) : 1.f;
+        re[e] = fc_in(s.erase, b, tg, h, i, s.T, K, true);
+        rw[e] = fc_in(s.write, b, tg, h, i, s.T, V, true);
+        rv[e] = fc_x(s.v, a.in_bf16, b, tg, h, i, s.T, V, true);
+    }
     fc_masks(s, b, c, sm.m, tid);
     const bool on = sm.m.val[t] != 0.f;
 #pragma unroll
-    for (int e = 0; e < Fc<FK>::EPT; ++e) {
+    for (int e = 0; e < EPT; ++e) {
         const int i = Fc<FK>::ch(g, e);
-        const float kv = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, on);
-        const float al = (on && i < K) ? ld4<float>(s.alpha, b, tg, h, i) : 1.f;
+        const float kv = on ? rk[e] : 0.f;
         sm.k[t * LQ + i] = kv;
-        sm.al[t * LQ + i] = al;
-        sm.eh[t * LQ + i] = fc_in(s.erase, b, tg, h, i, s.T, K, on) * kv;
-        sm.wv[t * LQ + i] = fc_in(s.write, b, tg, h, i, s.T, V, on) * fc_x(s.v, a.in_bf16, b, tg, h, i, s.T, V, on);
+        sm.al[t * LQ + i] = on ? ral[e] : 1.f;
+        sm.eh[t * LQ + i] = (on ? re[e] : 0.f) * kv;
+        sm.wv[t * LQ + i] = on ? rw[e] * rv[e] : 0.f;
     }
     __syncthreads();
     fc_decay_rows<FK>(sm.al, sm.m, sm.bt, sm.lam, K, tid);
@@ -522,22 +536,20 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_out_kernel(FcArgs a) {
     const int K = s.K, V = s.V, t = tid / Fc<FK>::LPT, g = tid % Fc<FK>::LPT, tg = c * C + t;
     const int KP = fc_kp(K), VT = (V + 15) >> 4, VP = 16 * VT;
     const int w = tid >> 6, l = tid & 63, lg = l >> 4, ln = l & 15;
-    fc_masks(s, b, c, sm.m, tid);
-    const bool on = sm.m.val[t] != 0.f;
-    float ksq = 0.f;
+    // The token rows, S0 and T are loaded before the masks arrive; the rows are
+    // masked after.
+    constexpr int EPT = Fc<FK>::EPT;
+    float rk[EPT], rq[EPT], ral[EPT], re[EPT], rw[EPT], rv[EPT];
 #pragma unroll
-    for (int e = 0; e < Fc<FK>::EPT; ++e) {
+    for (int e = 0; e < EPT; ++e) {
         const int i = Fc<FK>::ch(g, e);
-        const float kv = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, on);
-        sm.q[t * LQ + i] = fc_x(s.q, a.in_bf16, b, tg, h, i, s.T, K, on);
-        sm.k[t * LQ + i] = kv;
-        sm.al[t * LQ + i] = (on && i < K) ? ld4<float>(s.alpha, b, tg, h, i) : 1.f;
-        sm.eh[t * LQ + i] = fc_in(s.erase, b, tg, h, i, s.T, K, on) * kv;
-        sm.wv[t * LQ + i] = fc_in(s.write, b, tg, h, i, s.T, V, on) * fc_x(s.v, a.in_bf16, b, tg, h, i, s.T, V, on);
-        ksq += kv * kv;
+        rk[e] = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, true);
+        rq[e] = fc_x(s.q, a.in_bf16, b, tg, h, i, s.T, K, true);
+        ral[e] = (i < K && tg < s.T) ? ld4<float>(s.alpha, b, tg, h, i) : 1.f;
+        re[e] = fc_in(s.erase, b, tg, h, i, s.T, K, true);
+        rw[e] = fc_in(s.write, b, tg, h, i, s.T, V, true);
+        rv[e] = fc_x(s.v, a.in_bf16, b, tg, h, i, s.T, V, true);
     }
-    ksq = Fc<FK>::row_sum(ksq);
-    if (g == 0) sm.kk[t] = ksq;
     // S0 rows 0 .. KP - 1, all FK columns (zero outside K x V); 16-byte loads
     // when the rows allow them
     if ((V & 3) == 0 && (reinterpret_cast<uintptr_t>(a.st) & 15) == 0)
@@ -545,6 +557,22 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_out_kernel(FcArgs a) {
     else
         fc_stage2<NT, FK, 16>(sm.s0, nullptr, LS, a.st + (int64_t)ci * K * V, nullptr, V, KP, K, V, tid);
     if (tid < C * C) sm.T[(tid >> 4) * LT + (tid & 15)] = a.tm[(int64_t)ci * C * C + tid];
+    fc_masks(s, b, c, sm.m, tid);
+    const bool on = sm.m.val[t] != 0.f;
+    float ksq = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int i = Fc<FK>::ch(g, e);
+        const float kv = on ? rk[e] : 0.f;
+        sm.q[t * LQ + i] = on ? rq[e] : 0.f;
+        sm.k[t * LQ + i] = kv;
+        sm.al[t * LQ + i] = on ? ral[e] : 1.f;
+        sm.eh[t * LQ + i] = (on ? re[e] : 0.f) * kv;
+        sm.wv[t * LQ + i] = on ? rw[e] * rv[e] : 0.f;
+        ksq += kv * kv;
+    }
+    ksq = Fc<FK>::row_sum(ksq);
+    if (g == 0) sm.kk[t] = ksq;
     __syncthreads();
     fc_b_row<FK>(sm.al, sm.m, sm.bt, K, tid);
     fc_tri<FK, false>(sm.q, sm.k, sm.al, sm.m, sm.P, K, tid);  // P, lower with the diagonal
@@ -602,19 +630,31 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bprep_kernel(FcArgs a) {
     const SeqArgs &s = a.s;
     const int tid = threadIdx.x, ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / s.H, h = bh % s.H;
     const int K = s.K, V = s.V, t = tid / Fc<FK>::LPT, g = tid % Fc<FK>::LPT, tg = c * C + t;
+    // The token rows are loaded before the masks arrive and masked after.
+    constexpr int EPT = Fc<FK>::EPT;
+    float rk[EPT], rq[EPT], ral[EPT], rdo[EPT], rdl[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int i = Fc<FK>::ch(g, e);
+        rk[e] = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, true);
+        rq[e] = fc_x(s.q, a.in_bf16, b, tg, h, i, s.T, K, true);
+        ral[e] = (i < K && tg < s.T) ? ld4<float>(s.alpha, b, tg, h, i) : 1.f;
+        rdo[e] = (s.dout.data && tg < s.T && i < V) ? fc_ld(s.dout, a.in_bf16, b, tg, h, i) : 0.f;
+        rdl[e] = i < V ? a.dl[((int64_t)ci * C + t) * V + i] : 0.f;
+    }
     fc_masks(s, b, c, sm.m, tid);
     const bool on = sm.m.val[t] != 0.f;
     const bool score_adj = s.dscores != nullptr;
     float ksq = 0.f, dsq = 0.f;
 #pragma unroll
-    for (int e = 0; e < Fc<FK>::EPT; ++e) {
+    for (int e = 0; e < EPT; ++e) {
         const int i = Fc<FK>::ch(g, e);
-        const float kv = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, on);
-        sm.q[t * LQ + i] = fc_x(s.q, a.in_bf16, b, tg, h, i, s.T, K, on);
+        const float kv = on ? rk[e] : 0.f;
+        sm.q[t * LQ + i] = on ? rq[e] : 0.f;
         sm.k[t * LQ + i] = kv;
-        sm.al[t * LQ + i] = (on && i < K) ? ld4<float>(s.alpha, b, tg, h, i) : 1.f;
-        sm.dO[t * LQ + i] = (s.dout.data && on && tg < s.T && i < V) ? fc_ld(s.dout, a.in_bf16, b, tg, h, i) : 0.f;
-        const float d = i < V ? a.dl[((int64_t)ci * C + t) * V + i] : 0.f;
+        sm.al[t * LQ + i] = on ? ral[e] : 1.f;
+        sm.dO[t * LQ + i] = on ? rdo[e] : 0.f;
+        const float d = rdl[e];
         sm.dl[t * LQ + i] = d;
         ksq += kv * kv;
         dsq += d * d;
@@ -692,20 +732,35 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
     const int K = s.K, V = s.V, t = tid / Fc<FK>::LPT, g = tid % Fc<FK>::LPT, tg = c * C + t;
     const int KT = (K + 15) >> 4, VT = (V + 15) >> 4, VP = 16 * VT, KP = 16 * KT;
     const int w = tid >> 6, l = tid & 63, lg = l >> 4, ln = l & 15;
+    // The token rows and T are loaded before the masks arrive; the rows are
+    // masked after.
+    constexpr int EPT = Fc<FK>::EPT;
+    float xk[EPT], xq[EPT], xe[EPT], xal[EPT], xdo[EPT], xdl[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int i = Fc<FK>::ch(g, e);
+        xk[e] = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, true);
+        xq[e] = fc_x(s.q, a.in_bf16, b, tg, h, i, s.T, K, true);
+        xe[e] = fc_in(s.erase, b, tg, h, i, s.T, K, true);
+        xal[e] = (i < K && tg < s.T) ? ld4<float>(s.alpha, b, tg, h, i) : 1.f;
+        xdo[e] = (s.dout.data && tg < s.T && i < V) ? fc_ld(s.dout, a.in_bf16, b, tg, h, i) : 0.f;
+        xdl[e] = i < V ? a.dl[((int64_t)ci * C + t) * V + i] : 0.f;
+    }
+    if (tid < C * C) sm.T[(tid >> 4) * LT + (tid & 15)] = a.tm[(int64_t)ci * C * C + tid];
     fc_masks(s, b, c, sm.m, tid);
     const bool on = sm.m.val[t] != 0.f;
     const bool score_adj = s.dscores != nullptr;
     float ksq = 0.f, dsq = 0.f;
 #pragma unroll
-    for (int e = 0; e < Fc<FK>::EPT; ++e) {
+    for (int e = 0; e < EPT; ++e) {
         const int i = Fc<FK>::ch(g, e);
-        const float kv = fc_x(s.k, a.in_bf16, b, tg, h, i, s.T, K, on);
-        sm.q[t * LQ + i] = fc_x(s.q, a.in_bf16, b, tg, h, i, s.T, K, on);
+        const float kv = on ? xk[e] : 0.f;
+        sm.q[t * LQ + i] = on ? xq[e] : 0.f;
         sm.k[t * LQ + i] = kv;
-        sm.e[t * LQ + i] = fc_in(s.erase, b, tg, h, i, s.T, K, on);
-        sm.al[t * LQ + i] = (on && i < K) ? ld4<float>(s.alpha, b, tg, h, i) : 1.f;
-        sm.dO[t * LQ + i] = (s.dout.data && on && tg < s.T && i < V) ? fc_ld(s.dout, a.in_bf16, b, tg, h, i) : 0.f;
-        const float d = i < V ? a.dl[((int64_t)ci * C + t) * V + i] : 0.f;
+        sm.e[t * LQ + i] = on ? xe[e] : 0.f;
+        sm.al[t * LQ + i] = on ? xal[e] : 1.f;
+        sm.dO[t * LQ + i] = on ? xdo[e] : 0.f;
+        const float d = xdl[e];
         sm.dl[t * LQ + i] = d;
         ksq += kv * kv;
         dsq += d * d;
@@ -719,7 +774,6 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
         sm.cs[t] = ok ? dsc * nk / nd : 0.f;
         sm.ck[t] = ok ? dsc * nd / nk : 0.f;
     }
-    if (tid < C * C) sm.T[(tid >> 4) * LT + (tid & 15)] = a.tm[(int64_t)ci * C * C + tid];
     __syncthreads();
     fc_decay_rows<FK>(sm.al, sm.m, sm.bt, sm.lam, K, tid);
     fc_tri<FK, false>(sm.q, sm.k, sm.al, sm.m, sm.P, K, tid);
