@@ -18,7 +18,8 @@ from typing import NamedTuple, Optional
 
 import torch
 
-from ._lib import GDN2_BF16, GDN2_F32, GDN2_I32, Gdn2Shape, Gdn2View, check, lib
+from ._lib import (GDN2_BF16, GDN2_F32, GDN2_I32, Gdn2Shape, Gdn2View, check, lib, on_device,
+                   raw_stream)
 
 __all__ = ["GdnTrainingOutput", "gdn_training_scan", "gdn_training_forward",
            "gdn_training_backward", "gdn2_scan", "gdn2_scan_forward", "gdn2_backward",
@@ -33,30 +34,26 @@ class GdnTrainingOutput(NamedTuple):
     scores: torch.Tensor        # [batch, time, head, 1] f32: ||k|| * ||delta||
 
 
+_CODES = {torch.float32: GDN2_F32, torch.bfloat16: GDN2_BF16, torch.int32: GDN2_I32}
+_STRIDES = ctypes.c_int64 * 4
+
+
 def _code(t: torch.Tensor) -> int:
-    if t.dtype == torch.float32:
-        return GDN2_F32
-    if t.dtype == torch.bfloat16:
-        return GDN2_BF16
-    if t.dtype == torch.int32:
-        return GDN2_I32
-    raise TypeError(f"GDN-2 tensors must be float32 or bfloat16, got {t.dtype}")
+    c = _CODES.get(t.dtype)
+    if c is None:
+        raise TypeError(f"GDN-2 tensors must be float32 or bfloat16, got {t.dtype}")
+    return c
 
 
 def _view(t: Optional[torch.Tensor]) -> Gdn2View:
-    v = Gdn2View()
     if t is None:
-        v.data = None
-        v.dtype = GDN2_F32
-        return v
+        return Gdn2View(None, GDN2_F32)
     if not t.is_cuda:
         raise ValueError("GDN-2 tensors must live on the GPU; there is no CPU fallback")
-    v.data = t.data_ptr()
-    v.dtype = _code(t)
-    st = list(t.stride()) + [0] * (4 - t.dim())
-    for i in range(4):
-        v.stride[i] = st[i]
-    return v
+    st = t.stride()
+    if len(st) < 4:
+        st = st + (0,) * (4 - len(st))
+    return Gdn2View(t.data_ptr(), _code(t), 0, _STRIDES(*st))
 
 
 def _shape(q: torch.Tensor, v: torch.Tensor) -> Gdn2Shape:
@@ -69,7 +66,22 @@ def _ptr(t: Optional[torch.Tensor]):
 
 
 def _stream(t: torch.Tensor):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    return raw_stream(t.device)
+
+
+_SIZES: dict = {}
+
+
+def _size(query, shape: Gdn2Shape, *extra) -> int:
+    """A checkpoint or workspace size query, remembered per shape (the sizes
+    depend on nothing else)."""
+    key = (query, shape.batch, shape.time, shape.heads, shape.keys, shape.values) + extra
+    n = _SIZES.get(key)
+    if n is None:
+        n = getattr(lib(), query)(ctypes.byref(shape), *extra)
+        if n:
+            _SIZES[key] = n
+    return n
 
 
 def _rows_aligned(t: torch.Tensor) -> bool:
@@ -126,12 +138,12 @@ def _training_forward(q, k, v, alpha, erase, write, valid, reset, initial, chunk
     out = torch.empty((B, T, H, V), dtype=q.dtype, device=dev)
     final = torch.empty((B, H, K, V), dtype=torch.float32, device=dev)
     scores = torch.empty((B, T, H, 1), dtype=torch.float32, device=dev)
-    nck = L.gdn2_training_checkpoint_bytes(ctypes.byref(shape), chunk)
+    nck = _size("gdn2_training_checkpoint_bytes", shape, chunk)
     if nck == 0:
         check("gdn2_training_checkpoint_bytes", 1)
     ck = torch.empty((nck,), dtype=torch.uint8, device=dev)
     views = [_view(x) for x in (q, k, v, alpha, erase, write, valid, reset, initial)]
-    with torch.cuda.device(dev):
+    with on_device(dev):
         rc = L.gdn2_training_scan(ctypes.byref(shape), chunk, *[ctypes.byref(x) for x in views],
                                   _ptr(out), _code(out), _ptr(final), _ptr(scores), _ptr(ck), nck,
                                   _stream(q))
@@ -155,7 +167,7 @@ def gdn_training_backward(q, k, v, alpha, erase, write, valid, reset, checkpoint
     de = torch.empty((B, T, H, K), dtype=torch.float32, device=dev)
     dw = torch.empty((B, T, H, V), dtype=torch.float32, device=dev)
     dinit = torch.empty((B, H, K, V), dtype=torch.float32, device=dev)
-    nws = L.gdn2_training_workspace_bytes(ctypes.byref(shape), chunk)
+    nws = _size("gdn2_training_workspace_bytes", shape, chunk)
     ws = torch.empty((nws,), dtype=torch.uint8, device=dev)
     if d_output is not None:
         if d_output.dtype != q.dtype:
@@ -167,7 +179,7 @@ def gdn_training_backward(q, k, v, alpha, erase, write, valid, reset, checkpoint
     dsc = None if d_scores is None else d_scores.to(torch.float32).contiguous()
     views = [_view(x) for x in (q, k, v, alpha, erase, write, valid, reset)]
     dov = _view(d_output)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         rc = L.gdn2_training_backward(
             ctypes.byref(shape), chunk, *[ctypes.byref(x) for x in views], _ptr(checkpoint),
             checkpoint.numel(), ctypes.byref(dov) if d_output is not None else None, _ptr(dfin),
@@ -243,7 +255,7 @@ def gdn2_scan_forward(q, k, v, alpha, erase, write, doc_start, doc_end):
         check("gdn2_scan_checkpoint_bytes", 1)
     ck = torch.empty((nck,), dtype=torch.uint8, device=q.device)
     views = [_view(x) for x in (q, k, v, alpha, erase, write, doc_start, doc_end)]
-    with torch.cuda.device(q.device):
+    with on_device(q.device):
         rc = L.gdn2_scan(ctypes.byref(shape), *[ctypes.byref(x) for x in views], _ptr(out),
                          _code(out), _ptr(ck), nck, _stream(q))
     check("gdn2_scan", rc)
@@ -273,7 +285,7 @@ def gdn2_backward(q, k, v, alpha, erase, write, d_output, checkpoint, doc_start,
             d_output = d_output.contiguous()
     views = [_view(x) for x in (q, k, v, alpha, erase, write, doc_start, doc_end)]
     dov = _view(d_output)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         rc = L.gdn2_backward(ctypes.byref(shape), *[ctypes.byref(x) for x in views],
                              _ptr(checkpoint), checkpoint.numel(),
                              ctypes.byref(dov) if d_output is not None else None, _ptr(dq),
@@ -332,7 +344,7 @@ def gdn_scalar_forward(q, k, v, beta, g, valid, reset, initial=None, chunk: int 
         check("gdn_scalar_checkpoint_bytes", 1)
     ck = torch.empty((nck,), dtype=torch.uint8, device=dev)
     views = [_view(x) for x in (q, k, v, beta, g, valid, reset, initial)]
-    with torch.cuda.device(dev):
+    with on_device(dev):
         rc = L.gdn_scalar_scan(ctypes.byref(shape), chunk, *[ctypes.byref(x) for x in views],
                                _ptr(out), _code(out), _ptr(final), _ptr(scores), _ptr(ck), nck,
                                _stream(q))
@@ -367,7 +379,7 @@ def gdn_scalar_backward(q, k, v, beta, g, valid, reset, checkpoint, chunk: int =
     dsc = None if d_scores is None else d_scores.float().contiguous()
     views = [_view(x) for x in (q, k, v, beta, g, valid, reset)]
     dov = _view(d_output)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         rc = L.gdn_scalar_backward(
             ctypes.byref(shape), chunk, *[ctypes.byref(x) for x in views], _ptr(checkpoint),
             checkpoint.numel(), ctypes.byref(dov) if d_output is not None else None, _ptr(dfin),
@@ -439,7 +451,7 @@ def gdn_decode_step(state, q, k, v, alpha, erase, write, valid=None, reset=None)
     views = [_view(x) for x in (q, k, v, alpha, erase, write)]
     vv = _view(valid) if valid is not None else None
     rv = _view(reset) if reset is not None else None
-    with torch.cuda.device(q.device):
+    with on_device(q.device):
         rc = L.gdn2_decode_step(ctypes.byref(shape), *[ctypes.byref(x) for x in views],
                                 ctypes.byref(vv) if vv is not None else None,
                                 ctypes.byref(rv) if rv is not None else None, _ptr(state),

@@ -5,8 +5,11 @@ eager-PyTorch fallback behind these functions.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
+
+import torch
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG, "lib", "libgdn2_amd.so")
@@ -16,6 +19,23 @@ GDN2_BF16 = 1
 GDN2_I32 = 2
 
 STATUS = {0: "OK", 1: "ARGUMENT", 2: "SHAPE", 3: "DTYPE", 4: "WORKSPACE", 5: "LAUNCH"}
+
+
+def raw_stream(device: torch.device) -> ctypes.c_void_p:
+    """The handle of torch's current stream on device, for a library call."""
+    idx = device.index
+    if idx is None:
+        idx = torch._C._cuda_getDevice()
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(idx))
+
+
+def on_device(device: torch.device):
+    """The context for a library call on device: none when device is already
+    the current one (the common case: switching costs more than the call)."""
+    idx = device.index
+    if idx is None or idx == torch._C._cuda_getDevice():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
 
 
 class Gdn2Shape(ctypes.Structure):

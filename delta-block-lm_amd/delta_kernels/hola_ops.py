@@ -14,7 +14,7 @@ from typing import NamedTuple, Optional
 
 import torch
 
-from ._lib import Gdn2HolaShape, check, lib
+from ._lib import Gdn2HolaShape, check, lib, on_device
 
 __all__ = ["HolaReadOutput", "hola_schedule", "hola_read"]
 
@@ -58,7 +58,7 @@ def hola_schedule(scores, valid, documents, capacity: int, chunk: int,
     nc = -(-T // chunk)
     out = torch.empty((B, H, nc + 1, capacity), dtype=torch.float32, device=sc.device)
     shape = _shape(B, T, H, 1, 1, capacity, chunk)
-    with torch.cuda.device(sc.device):
+    with on_device(sc.device):
         rc = lib().gdn2_hola_schedule(ctypes.byref(shape), 1 if recency else 0,
                                       ctypes.byref(_view(sc)), ctypes.byref(_view(valid)),
                                       ctypes.byref(_view(documents)), _ptr(out), _stream(sc))
@@ -81,7 +81,7 @@ class _HolaRead(torch.autograd.Function):
             check("gdn2_hola_checkpoint_bytes", 1)
         ck = torch.empty((nck,), dtype=torch.uint8, device=q.device)
         views = [_view(x) for x in (q, k, v, scores, valid, documents, sink)]
-        with torch.cuda.device(q.device):
+        with on_device(q.device):
             rc = L.gdn2_hola_read(ctypes.byref(shape), 1 if recency else 0,
                                   *[ctypes.byref(x) for x in views], _ptr(out), _ptr(fin),
                                   _ptr(ck), nck, _stream(q))
@@ -107,7 +107,7 @@ class _HolaRead(torch.autograd.Function):
         d_out = d_out.float() if d_out is not None else None  # held until the launch
         dov = _view(d_out)
         views = [_view(x) for x in (q, k, v, valid, documents, sink)]
-        with torch.cuda.device(q.device):
+        with on_device(q.device):
             rc = L.gdn2_hola_backward(ctypes.byref(shape), *[ctypes.byref(x) for x in views],
                                       _ptr(ctx.checkpoint), ctx.checkpoint.numel(), _ptr(out),
                                       ctypes.byref(dov) if d_out is not None else None,

@@ -15,7 +15,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from ._lib import Gdn2LmMixerShape, check, lib
+from ._lib import Gdn2LmMixerShape, check, lib, on_device, raw_stream
 
 __all__ = ["norm_forward", "norm_backward", "mixer_in_forward", "mixer_in_backward",
            "mixer_out_forward", "mixer_out_backward", "swiglu_forward", "swiglu_backward"]
@@ -25,7 +25,7 @@ F32 = torch.float32
 
 
 def _stream(t: torch.Tensor):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    return raw_stream(t.device)
 
 
 def _p(t: Optional[torch.Tensor]):
@@ -64,7 +64,7 @@ def norm_forward(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torc
         u = torch.empty_like(x)
     y = torch.empty((rows, W), dtype=BF16, device=x.device)
     inv = torch.empty((rows,), dtype=F32, device=x.device)
-    with torch.cuda.device(x.device):
+    with on_device(x.device):
         rc = lib().gdn2_lm_norm_forward(rows, W, ctypes.c_float(eps), _p(x), _p(residual),
                                         _p(weight), _p(u) if residual is not None else None,
                                         _p(y), _p(inv), _stream(x))
@@ -89,7 +89,7 @@ def norm_backward(x: torch.Tensor, weight: torch.Tensor, inv: torch.Tensor, dy: 
     L = lib()
     nws = L.gdn2_lm_norm_workspace_bytes(rows, W)
     ws = _ws(nws, x.device)
-    with torch.cuda.device(x.device):
+    with on_device(x.device):
         rc = L.gdn2_lm_norm_backward(rows, W, _p(x), _p(weight), _p(inv), _p(dy), _p(dres),
                                      _p(dx), _p(dxb), _p(dw), _p(ws), ws.numel(), _stream(x))
     check("gdn2_lm_norm_backward", rc)
@@ -118,7 +118,7 @@ def mixer_in_forward(z, conv_w, valid, docs, decay_scale, decay_bias, B: int, T:
     qkv = torch.empty((B, T, 3 * H, 64), dtype=BF16, device=z.device)
     beta = torch.empty((B, T, H), dtype=F32, device=z.device)
     g = torch.empty((B, T, H), dtype=F32, device=z.device)
-    with torch.cuda.device(z.device):
+    with on_device(z.device):
         rc = lib().gdn2_lm_mixer_in_forward(ctypes.byref(shape), _p(z), _p(conv_w), _p(valid),
                                             _p(docs), _p(decay_scale), _p(decay_bias), _p(qkv),
                                             _p(beta), _p(g), _stream(z))
@@ -143,7 +143,7 @@ def mixer_in_backward(z, conv_w, valid, docs, decay_scale, decay_bias, dq, dk, d
     L = lib()
     nws = L.gdn2_lm_mixer_in_workspace_bytes(ctypes.byref(shape))
     ws = _ws(nws, z.device)
-    with torch.cuda.device(z.device):
+    with on_device(z.device):
         rc = L.gdn2_lm_mixer_in_backward(ctypes.byref(shape), _p(z), _p(conv_w), _p(valid),
                                          _p(docs), _p(decay_scale), _p(decay_bias), _p(dq), _p(dk),
                                          _p(dv), _p(dbeta), _p(dg), _p(dz), _p(dconv), _p(dds),
@@ -159,7 +159,7 @@ def mixer_out_forward(o, z, norm_w, eps: float, B: int, T: int, H: int):
     _need(norm_w, "norm_w", F32, (64,))
     y = torch.empty((B * T, H * 64), dtype=BF16, device=z.device)
     inv = torch.empty((B * T * H,), dtype=F32, device=z.device)
-    with torch.cuda.device(z.device):
+    with on_device(z.device):
         rc = lib().gdn2_lm_mixer_out_forward(ctypes.byref(shape), _p(o), _p(z), _p(norm_w),
                                              ctypes.c_float(eps), _p(y), _p(inv), _stream(z))
     check("gdn2_lm_mixer_out_forward", rc)
@@ -179,7 +179,7 @@ def mixer_out_backward(o, z, norm_w, inv, dy, dz, B: int, T: int, H: int):
     L = lib()
     nws = L.gdn2_lm_mixer_out_workspace_bytes(ctypes.byref(shape))
     ws = _ws(nws, z.device)
-    with torch.cuda.device(z.device):
+    with on_device(z.device):
         rc = L.gdn2_lm_mixer_out_backward(ctypes.byref(shape), _p(o), _p(z), _p(norm_w), _p(inv),
                                           _p(dy), _p(d_o), _p(dz), _p(dw), _p(ws), ws.numel(),
                                           _stream(z))
@@ -195,7 +195,7 @@ def swiglu_forward(h: torch.Tensor) -> torch.Tensor:
     _need(h, "h", BF16)
     rows, M2 = h.shape
     a = torch.empty((rows, M2 // 2), dtype=BF16, device=h.device)
-    with torch.cuda.device(h.device):
+    with on_device(h.device):
         rc = lib().gdn2_lm_swiglu_forward(rows, M2 // 2, _p(h), _p(a), _stream(h))
     check("gdn2_lm_swiglu_forward", rc)
     return a
@@ -206,7 +206,7 @@ def swiglu_backward(h: torch.Tensor, da: torch.Tensor) -> torch.Tensor:
     rows, M2 = h.shape
     _need(da, "da", BF16, (rows, M2 // 2))
     dh = torch.empty_like(h)
-    with torch.cuda.device(h.device):
+    with on_device(h.device):
         rc = lib().gdn2_lm_swiglu_backward(rows, M2 // 2, _p(h), _p(da), _p(dh), _stream(h))
     check("gdn2_lm_swiglu_backward", rc)
     return dh

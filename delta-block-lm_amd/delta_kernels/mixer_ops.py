@@ -17,7 +17,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import Gdn2ConvShape, Gdn2RowsShape, check, lib
+from ._lib import Gdn2ConvShape, Gdn2RowsShape, check, lib, on_device
 
 __all__ = ["causal_conv", "l2_norm", "rms_norm", "decay"]
 
@@ -50,7 +50,7 @@ class _CausalConv(torch.autograd.Function):
         shape = Gdn2ConvShape(B, T, C, w.shape[0])
         y = torch.empty((B, T, C), dtype=torch.float32, device=x.device)
         views = [_view(t) for t in (x, w, valid, docs)]
-        with torch.cuda.device(x.device):
+        with on_device(x.device):
             rc = lib().gdn2_conv_forward(ctypes.byref(shape), *[ctypes.byref(v) for v in views],
                                          act, _ptr(y), _stream(x))
         check("gdn2_conv_forward", rc)
@@ -73,7 +73,7 @@ class _CausalConv(torch.autograd.Function):
         nws = L.gdn2_conv_workspace_bytes(ctypes.byref(shape))
         ws = _workspace(nws, x.device)
         views = [_view(t) for t in (x, w, valid, docs, dy)]
-        with torch.cuda.device(x.device):
+        with on_device(x.device):
             rc = L.gdn2_conv_backward(ctypes.byref(shape), *[ctypes.byref(v) for v in views[:4]],
                                       ctx.act, ctypes.byref(views[4]), _ptr(dx), _ptr(dw),
                                       _ptr(ws), nws, _stream(x))
@@ -115,7 +115,7 @@ class _RowNorm(torch.autograd.Function):
         y = torch.empty((B, T, H, W), dtype=torch.float32, device=x4.device)
         inv = torch.empty((B * T * H,), dtype=torch.float32, device=x4.device)
         vx, vw, vg = _view(x4), _view(weight), _view(gate4)
-        with torch.cuda.device(x4.device):
+        with on_device(x4.device):
             rc = lib().gdn2_norm_forward(ctypes.byref(shape), mode, ctypes.c_float(eps),
                                          ctypes.byref(vx), ctypes.byref(vw), ctypes.byref(vg),
                                          _ptr(y), _ptr(inv), _stream(x4))
@@ -142,7 +142,7 @@ class _RowNorm(torch.autograd.Function):
         nws = L.gdn2_norm_workspace_bytes(ctypes.byref(shape))
         ws = _workspace(nws, x4.device)
         vx, vw, vg, vd = _view(x4), _view(weight), _view(gate4), _view(dy)
-        with torch.cuda.device(x4.device):
+        with on_device(x4.device):
             rc = L.gdn2_norm_backward(ctypes.byref(shape), mode, ctypes.byref(vx),
                                       ctypes.byref(vw), ctypes.byref(vg), _ptr(inv),
                                       ctypes.byref(vd), _ptr(dx), _ptr(dg), _ptr(dw), _ptr(ws),
@@ -189,7 +189,7 @@ class _Decay(torch.autograd.Function):
         shape = Gdn2RowsShape(B, T, H, W)
         y = torch.empty((B, T, H, W), dtype=torch.float32, device=x.device)
         vx, vb, vs = _view(x), _view(bias), _view(scale)
-        with torch.cuda.device(x.device):
+        with on_device(x.device):
             rc = lib().gdn2_decay_forward(ctypes.byref(shape), ctypes.byref(vx), ctypes.byref(vb),
                                           ctypes.byref(vs), _ptr(y), _stream(x))
         check("gdn2_decay_forward", rc)
@@ -211,7 +211,7 @@ class _Decay(torch.autograd.Function):
         nws = L.gdn2_decay_workspace_bytes(ctypes.byref(shape))
         ws = _workspace(nws, x.device)
         vx, vb, vs, vd = _view(x), _view(bias), _view(scale), _view(dy)
-        with torch.cuda.device(x.device):
+        with on_device(x.device):
             rc = L.gdn2_decay_backward(ctypes.byref(shape), ctypes.byref(vx), ctypes.byref(vb),
                                        ctypes.byref(vs), ctypes.byref(vd), _ptr(dx), _ptr(db),
                                        _ptr(ds), _ptr(ws), nws, _stream(x))

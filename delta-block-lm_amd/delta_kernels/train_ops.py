@@ -17,7 +17,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import Gdn2AdamwTensor, check, lib
+from ._lib import Gdn2AdamwTensor, check, lib, on_device
 
 __all__ = ["cross_entropy_rows", "linear_cross_entropy", "adamw_update", "FusedAdamW"]
 
@@ -47,7 +47,7 @@ class _CrossEntropyRows(torch.autograd.Function):
         rows, width = x.shape
         loss = torch.empty((rows,), dtype=torch.float32, device=x.device)
         stats = torch.empty((rows, 2), dtype=torch.float32, device=x.device)
-        with torch.cuda.device(x.device):
+        with on_device(x.device):
             rc = lib().gdn2_cross_entropy_forward(rows, width, ctypes.byref(_view(x)), _ptr(target),
                                                   target.stride(0), _ptr(loss), _ptr(stats),
                                                   _stream(x))
@@ -62,7 +62,7 @@ class _CrossEntropyRows(torch.autograd.Function):
         rows, width = x.shape
         up = d_loss.float()
         dx = torch.empty((rows, width), dtype=x.dtype, device=x.device)
-        with torch.cuda.device(x.device):
+        with on_device(x.device):
             rc = lib().gdn2_cross_entropy_backward(rows, width, ctypes.byref(_view(x)),
                                                    _ptr(target), target.stride(0), _ptr(stats),
                                                    _ptr(up), up.stride(0), _ptr(dx), _stream(x))
@@ -87,7 +87,7 @@ class _LinearCrossEntropy(torch.autograd.Function):
         width = w.shape[0]
         logits = torch.mm(h, w.t())
         loss = torch.empty((rows,), dtype=torch.float32, device=h.device)
-        with torch.cuda.device(h.device):
+        with on_device(h.device):
             rc = lib().gdn2_cross_entropy_fused(rows, width, ctypes.byref(_view(logits)),
                                                 _ptr(target), target.stride(0),
                                                 ctypes.c_float(1.0 / rows), _ptr(loss),
@@ -130,7 +130,7 @@ def _adamw_call(entries, initialized, time, lr, weight_decay, clip, workspace, r
     if workspace is None or workspace.numel() < nbytes:
         workspace = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=device)
         reuse = False
-    with torch.cuda.device(device):
+    with on_device(device):
         rc = lib().gdn2_adamw_update(n, arr, 1 if initialized else 0, time, float(lr),
                                      float(weight_decay), float(clip), 1 if reuse else 0,
                                      ctypes.c_void_p(workspace.data_ptr()), workspace.numel(),
