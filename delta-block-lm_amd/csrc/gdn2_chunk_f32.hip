@@ -387,27 +387,28 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_prep_kernel(FcArgs a) {
 }
 
 // ---- the scan over the chunks of one (batch, head) -----------------------------
-// One wave per (batch, head, 16 value columns j = 16 cg + l % 16), on
-// v_mfma_f32_16x16x4f32 (exact f32 products).  The state's key axis is cut
-// into KT tiles of 16 rows; tile tau lives in the accumulator layout: lane l
-// (g = l / 16, n = l % 16) holds S[16 tau + 4 g + r][16 cg + n] in register r.
+// One workgroup per (batch, head, 16 value columns j = 16 cg + l % 16), one wave
+// per 16-row key tile tau = w, on v_mfma_f32_16x16x4f32 (exact f32 products).
+// Wave tau holds its tile of the state in the accumulator layout: lane l
+// (g = l / 16, n = l % 16) holds S[16 tau + 4 g + r][j] in register r.
 // Per chunk, forward:  v = U - W' S,          S <- diag(gv) S + Ktil^T v
 //            reverse:  v = Ktil X,            X <- diag(gv) X + N - W'^T v
-// Each product's 16-long reduction runs as four k = 4 MFMA steps s whose
-// k-slice is {4 g + s}: the B operand of step s is then register s of the
-// lane's own accumulator tile (rows 4 g + s of S or X, rows 4 g + s of v), so
-// no value changes lanes; the A operand is the matching element of W' or Ktil,
-// read from global memory into registers a few chunks ahead: W' or Ktil rows,
-// gv and the lane-packed U or N as 16-byte loads, the other factor's columns
-// as 4-byte loads coalesced over the 16 columns n.
+// v sums over the key axis: each wave forms its tile's part (four k = 4 MFMA
+// steps whose k-slice {4 g + s} makes register s of the lane's own accumulator
+// the B operand), the parts meet in LDS (double-buffered by step parity, one
+// barrier per step) and every wave adds them in tile order, so all waves hold
+// the same v; each then updates its own tile, v's accumulator rows as the B
+// operand.  The A operands (W' or Ktil rows, gv, the lane-packed U or N) are
+// read from global memory into registers D chunks ahead.
 template <int KT>
 struct FcScanOps {
-    float4 w[KT], g[KT], a[KT];  // A operands (token n), gv rows, U (a[0]) or N
-    float k[KT][4];              // A operands (token 4 g + s)
+    float4 w, g, a;  // A operands (token n, keys 16 tau + 4 g ..), gv rows, U or N rows
+    float k[4];      // A operands (tokens 4 g + s, key 16 tau + n)
 };
 
 template <int KT, bool REV>
-__device__ __forceinline__ void fc_scan_load(const FcArgs &a, int64_t ci, int cg, int VT, FcScanOps<KT> &o) {
+__device__ __forceinline__ void fc_scan_load(const FcArgs &a, int64_t ci, int cg, int VT, int tau,
+                                             FcScanOps<KT> &o) {
     // Every load is issued (past the value tiles the lanes read tile 0, their
     // values unused), so no load sits behind a branch and the compiler's
     // memory-counter waits stay exact across the prefetch ring.
@@ -415,50 +416,44 @@ __device__ __forceinline__ void fc_scan_load(const FcArgs &a, int64_t ci, int cg
     const int l = lane_id(), g = l >> 4, n = l & 15, cc = cg < VT ? cg : 0;
     const float *fw = a.fw + ci * C * KP, *fk = a.fk + ci * C * KP;
     const float *rw = REV ? fk : fw, *ck = REV ? fw : fk;
+    o.w = *reinterpret_cast<const float4 *>(&rw[n * KP + 16 * tau + 4 * g]);
+    o.g = *reinterpret_cast<const float4 *>(&a.gv[ci * KP + 16 * tau + 4 * g]);
 #pragma unroll
-    for (int tau = 0; tau < KT; ++tau) {
-        // the operand (token n, keys 16 tau + 4 g ..) and (tokens 4 g + s, key 16 tau + n)
-        o.w[tau] = *reinterpret_cast<const float4 *>(&rw[n * KP + 16 * tau + 4 * g]);
-        o.g[tau] = *reinterpret_cast<const float4 *>(&a.gv[ci * KP + 16 * tau + 4 * g]);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) o.k[tau][s] = ck[(4 * g + s) * KP + 16 * tau + n];
-        if (REV)
-            o.a[tau] = *reinterpret_cast<const float4 *>(&a.n[(((ci * VT + cc) * KT + tau) * 64 + l) * 4]);
-        else if (tau == 0)
-            o.a[0] = *reinterpret_cast<const float4 *>(&a.fu[((ci * VT + cc) * 64 + l) * 4]);
-    }
+    for (int s = 0; s < 4; ++s) o.k[s] = ck[(4 * g + s) * KP + 16 * tau + n];
+    o.a = REV ? *reinterpret_cast<const float4 *>(&a.n[(((ci * VT + cc) * KT + tau) * 64 + l) * 4])
+              : *reinterpret_cast<const float4 *>(&a.fu[((ci * VT + cc) * 64 + l) * 4]);
 }
 
 template <int KT, bool REV>
-__global__ void __launch_bounds__(64) fc_scan_kernel(FcArgs a) {
+__global__ void __launch_bounds__(64 * KT) fc_scan_kernel(FcArgs a) {
+    __shared__ float4 vpart[2][KT][64];  // each wave's part of v, by step parity
     const SeqArgs &s = a.s;
     const int K = s.K, V = s.V, VT = (V + 15) / 16;
+    const int tau = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wg = blockIdx.x, bh = wg / VT, cg = wg % VT, b = bh / s.H, h = bh % s.H;
     const int l = lane_id(), g = l >> 4, n = l & 15, j = 16 * cg + n;
     const bool jv = j < V;
-    f32x4 X[KT];
+    f32x4 X;
 #pragma unroll
-    for (int tau = 0; tau < KT; ++tau)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int i = 16 * tau + 4 * g + r;
-            float x = 0.f;
-            if (i < K && jv) {
-                if (!REV) x = s.initial.data ? ld4<float>(s.initial, b, h, i, j) : 0.f;
-                else x = s.dfinal ? s.dfinal[((int64_t)bh * K + i) * V + j] : 0.f;
-            }
-            X[tau][r] = x;
+    for (int r = 0; r < 4; ++r) {
+        const int i = 16 * tau + 4 * g + r;
+        float x = 0.f;
+        if (i < K && jv) {
+            if (!REV) x = s.initial.data ? ld4<float>(s.initial, b, h, i, j) : 0.f;
+            else x = s.dfinal ? s.dfinal[((int64_t)bh * K + i) * V + j] : 0.f;
         }
+        X[r] = x;
+    }
     // A ring of D chunks' operands in registers: chunk step + D is loaded (the
     // last chunk again past the end) as soon as step's operands are used.
-    constexpr int D = KT <= 2 ? 3 : 2;
+    constexpr int D = 4;
     FcScanOps<KT> ring[D];
     auto chunk_at = [&](int step) {
         const int sc = step < a.nc ? step : a.nc - 1;
         return (int64_t)bh * a.nc + (REV ? a.nc - 1 - sc : sc);
     };
 #pragma unroll
-    for (int d = 0; d < D; ++d) fc_scan_load<KT, REV>(a, chunk_at(d), cg, VT, ring[d]);
+    for (int d = 0; d < D; ++d) fc_scan_load<KT, REV>(a, chunk_at(d), cg, VT, tau, ring[d]);
     float *keep = REV ? a.ds : a.st;
     for (int s0 = 0; s0 < a.nc; s0 += D) {
 #pragma unroll
@@ -469,52 +464,56 @@ __global__ void __launch_bounds__(64) fc_scan_kernel(FcArgs a) {
             const FcScanOps<KT> &cur = ring[d];
             // the state before (forward) / the adjoint after (reverse) this chunk
 #pragma unroll
-            for (int tau = 0; tau < KT; ++tau)
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * tau + 4 * g + r;
+                if (i < K && jv) keep[(ci * K + i) * V + j] = X[r];
+            }
+            // this tile's part of v[t][j], t = 4 g + r: -W' S (+ U in tile 0) or Ktil X
+            f32x4 vp = (!REV && tau == 0) ? f32x4{cur.a.x, cur.a.y, cur.a.z, cur.a.w} : zero4();
+            const float wq[4] = {cur.w.x, cur.w.y, cur.w.z, cur.w.w};
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int i = 16 * tau + 4 * g + r;
-                    if (i < K && jv) keep[(ci * K + i) * V + j] = X[tau][r];
+            for (int q = 0; q < 4; ++q)
+                vp = __builtin_amdgcn_mfma_f32_16x16x4f32(REV ? wq[q] : -wq[q], X[q], vp, 0, 0, 0);
+            f32x4 v = vp;
+            if (KT > 1) {
+                const int par = step & 1;
+                vpart[par][tau][l] = make_float4(vp[0], vp[1], vp[2], vp[3]);
+                __syncthreads();
+                float4 t0 = vpart[par][0][l];
+                v = f32x4{t0.x, t0.y, t0.z, t0.w};
+#pragma unroll
+                for (int u = 1; u < KT; ++u) {
+                    const float4 t = vpart[par][u][l];
+                    v += f32x4{t.x, t.y, t.z, t.w};
                 }
-            // v[t][j], t = 4 g + r: U - W' S (forward) or Ktil X (reverse)
-            f32x4 v = REV ? zero4() : f32x4{cur.a[0].x, cur.a[0].y, cur.a[0].z, cur.a[0].w};
-#pragma unroll
-            for (int tau = 0; tau < KT; ++tau) {
-                const float wq[4] = {cur.w[tau].x, cur.w[tau].y, cur.w[tau].z, cur.w[tau].w};
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    v = __builtin_amdgcn_mfma_f32_16x16x4f32(REV ? wq[q] : -wq[q], X[tau][q], v, 0, 0, 0);
             }
             // S <- diag(gv) S + Ktil^T v, or X <- diag(gv) X + N - W'^T v
+            const float gq[4] = {cur.g.x, cur.g.y, cur.g.z, cur.g.w};
+            const float an[4] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w};
+            f32x4 x;
 #pragma unroll
-            for (int tau = 0; tau < KT; ++tau) {
-                const float gq[4] = {cur.g[tau].x, cur.g[tau].y, cur.g[tau].z, cur.g[tau].w};
-                const float an[4] = {cur.a[tau].x, cur.a[tau].y, cur.a[tau].z, cur.a[tau].w};
-                f32x4 x;
+            for (int r = 0; r < 4; ++r) x[r] = gq[r] * X[r] + (REV ? an[r] : 0.f);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) x[r] = gq[r] * X[tau][r] + (REV ? an[r] : 0.f);
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    x = __builtin_amdgcn_mfma_f32_16x16x4f32(REV ? -cur.k[tau][q] : cur.k[tau][q], v[q], x, 0, 0, 0);
-                X[tau] = x;
-            }
-            fc_scan_load<KT, REV>(a, chunk_at(step + D), cg, VT, ring[d]);
+            for (int q = 0; q < 4; ++q)
+                x = __builtin_amdgcn_mfma_f32_16x16x4f32(REV ? -cur.k[q] : cur.k[q], v[q], x, 0, 0, 0);
+            X = x;
+            fc_scan_load<KT, REV>(a, chunk_at(step + D), cg, VT, tau, ring[d]);
         }
     }
     float *fin = REV ? s.dinitial : s.final_state;
     if (fin)
 #pragma unroll
-        for (int tau = 0; tau < KT; ++tau)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = 16 * tau + 4 * g + r;
-                if (i < K && jv) fin[((int64_t)bh * K + i) * V + j] = X[tau][r];
-            }
+        for (int r = 0; r < 4; ++r) {
+            const int i = 16 * tau + 4 * g + r;
+            if (i < K && jv) fin[((int64_t)bh * K + i) * V + j] = X[r];
+        }
 }
 
 template <bool REV>
 static void launch_fc_scan(const FcArgs &a, hipStream_t stream) {
-    const dim3 grid(a.s.B * a.s.H * ((a.s.V + 15) / 16)), block(64);
-    switch (fc_kp(a.s.K) / 16) {
+    const int KT = fc_kp(a.s.K) / 16;
+    const dim3 grid(a.s.B * a.s.H * ((a.s.V + 15) / 16)), block(64 * KT);
+    switch (KT) {
         case 1: hipLaunchKernelGGL((fc_scan_kernel<1, REV>), grid, block, 0, stream, a); break;
         case 2: hipLaunchKernelGGL((fc_scan_kernel<2, REV>), grid, block, 0, stream, a); break;
         case 3: hipLaunchKernelGGL((fc_scan_kernel<3, REV>), grid, block, 0, stream, a); break;
