@@ -30,6 +30,7 @@
 #include <utility>
 
 #include "gdn2_common.h"
+#include "gdn2_mfma.h"
 #include "gdn2_status.h"
 
 namespace gdn2 {
@@ -249,11 +250,15 @@ __device__ __forceinline__ void gather_rows(const View &x, int b, int h, int w, 
     }
 }
 
-template <int DK, int DV>
+// PAD = 1 (the read): lanes reading different rows of one column hit
+// different banks.  PAD = 4 (the query VJP's MFMA products): an operand read
+// of 16 rows x 4 columns hits 64 distinct banks, one of 4 rows x 16 columns
+// (its dq product) each bank at most four times.
+template <int DK, int DV, int PAD = 1>
 struct SlotTiles {
-    // +1: lanes reading different rows of one column hit different banks
-    float K[kMaxSlots][DK + 1];
-    float V[kMaxSlots][DV + 1];
+    static constexpr int LK = DK + PAD, LV = DV + PAD;
+    float K[kMaxSlots][LK];
+    float V[kMaxSlots][LV];
     float QT[DK][kMaxChunk] __attribute__((aligned(16)));  // [channel][query_slot(tt)]
     float pos[kMaxSlots], doc[kMaxSlots];
     float tpos[kMaxChunk], tval[kMaxChunk], tdoc[kMaxChunk];
@@ -261,8 +266,8 @@ struct SlotTiles {
 
 // Slots of chunk c (the cache before the chunk, then the chunk's tokens; empty
 // or invalid slots get position -1 and zero rows), and the chunk's queries.
-template <int DK, int DV>
-__device__ void stage_slots(const HolaArgs &a, int b, int h, int c, SlotTiles<DK, DV> &s) {
+template <int DK, int DV, int PAD>
+__device__ void stage_slots(const HolaArgs &a, int b, int h, int c, SlotTiles<DK, DV, PAD> &s) {
     const int lane = threadIdx.x, first = c * a.chunk, end = min(first + a.chunk, a.T);
     const int slots = a.cap + a.chunk;
     const float *sched = a.schedule + ((int64_t)(b * a.H + h) * (a.nc + 1) + c) * a.cap;
@@ -285,8 +290,8 @@ __device__ void stage_slots(const HolaArgs &a, int b, int h, int c, SlotTiles<DK
         s.tdoc[lane] = in ? ldf(a.docs, b, t) : 0.f;
     }
     __syncthreads();
-    gather_rows<DK, DK + 1, kMaxSlots, kReadThreads>(a.k, b, h, a.dk, s.pos, slots, &s.K[0][0]);
-    gather_rows<DV, DV + 1, kMaxSlots, kReadThreads>(a.v, b, h, a.dv, s.pos, slots, &s.V[0][0]);
+    gather_rows<DK, DK + PAD, kMaxSlots, kReadThreads>(a.k, b, h, a.dk, s.pos, slots, &s.K[0][0]);
+    gather_rows<DV, DV + PAD, kMaxSlots, kReadThreads>(a.v, b, h, a.dv, s.pos, slots, &s.V[0][0]);
     gather_rows<DK, DK, kMaxChunk, kReadThreads, true>(a.q, b, h, a.dk, s.tpos, kMaxChunk,
                                                       &s.QT[0][0]);
     __syncthreads();
@@ -299,8 +304,8 @@ struct WaveQueries {
     float doc[kWaveQueries];
 };
 
-template <int DK, int DV>
-__device__ __forceinline__ WaveQueries wave_queries(const SlotTiles<DK, DV> &s, int wave, int first,
+template <int DK, int DV, int PAD>
+__device__ __forceinline__ WaveQueries wave_queries(const SlotTiles<DK, DV, PAD> &s, int wave, int first,
                                                     int n) {
     WaveQueries w;
 #pragma unroll
@@ -337,6 +342,72 @@ __device__ __forceinline__ void wave_logits(const HolaArgs &a, const SlotTiles<D
         const bool vis = w.act[u] && p >= 0.f && p <= (float)w.t[u] && d == w.doc[u];
         lg[u] = vis ? acc[u] * a.scale : -FLT_MAX;
     }
+}
+
+// [query slot][slot] tiles of a chunk (logits, probabilities, their adjoints):
+// row stride 84 floats (20 mod 64), so an MFMA A-operand read (16 rows x 4
+// columns) and an accumulator store hit 64 distinct banks.
+constexpr int kLP = kMaxSlots + 4;
+
+// Query tt of the chunk behind query slot qs (the inverse of query_slot).
+__device__ __forceinline__ int slot_query(int qs) { return (qs >> 2) + 4 * (qs & 3); }
+
+// X Y^T over the reduction width D on v_mfma_f32_16x16x4f32: X^T [D][16] in
+// query-slot columns (the chunk's queries or their output adjoints), Y [slot]
+// rows of stride LY (K or V); out[qs][slot] for the 16-slot tiles that cover
+// the slots, wave w taking tiles w, w + 4, ...  Lane (lg, ln) reduces over
+// k = 4 ks + lg and holds rows 4 lg + r of column 16 n + ln.
+template <int D, int LY>
+__device__ __forceinline__ void chunk_xyt(const float (*XT)[kMaxChunk], const float *Y, int slots, int wave,
+                                          float (*out)[kLP]) {
+    const int l = lane_id(), lg = l >> 4, ln = l & 15;
+    for (int n = wave; 16 * n < slots; n += kReadWaves) {
+        f32x4 acc = zero4();
+#pragma unroll 4
+        for (int ks = 0; ks < D / 4; ++ks)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(XT[4 * ks + lg][ln], Y[(16 * n + ln) * LY + 4 * ks + lg],
+                                                       acc, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) out[4 * lg + r][16 * n + ln] = acc[r];
+    }
+}
+
+// P Y over the slots on v_mfma_f32_16x16x4f32: P [qs][slot] (zero past the
+// slots), Y [slot][channel] rows of stride LY (zero past the slots); wave w
+// takes the 16-channel tiles w, w + 4, .. of the W used channels and stores row
+// qs (query slot_query(qs) of the chunk) of each to dst[token][channel] when the
+// query is inside the sequence, zero when it is inactive.
+template <int D, int LY>
+__device__ __forceinline__ void chunk_py(const HolaArgs &a, const float (*P)[kLP], const float *Y, int slots,
+                                         int wave, int b, int h, int first, int n, const float *tval, int W,
+                                         float *dst) {
+    const int l = lane_id(), lg = l >> 4, ln = l & 15, nks = (slots + 3) >> 2;
+    for (int ct = wave; ct < D / 16; ct += kReadWaves) {
+        f32x4 acc = zero4();
+        for (int ks = 0; ks < nks; ++ks)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(P[ln][4 * ks + lg], Y[(4 * ks + lg) * LY + 16 * ct + ln],
+                                                       acc, 0, 0, 0);
+        const int ch = 16 * ct + ln;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tt = slot_query(4 * lg + r);
+            if (tt < n && ch < W)
+                dst[token(a, b, first + tt, h) * W + ch] = tval[tt] >= 0.5f ? acc[r] : 0.f;
+        }
+    }
+}
+
+// Scaled logit of the wave's query u against slot j from the chunk's raw
+// logits (-FLT_MAX where the slot is not visible: past the slots, empty, later
+// than the query, another document, or an inactive query).
+template <int DK, int DV, int PAD>
+__device__ __forceinline__ float visible_logit(const HolaArgs &a, const SlotTiles<DK, DV, PAD> &s,
+                                               const WaveQueries &w, const float (*L)[kLP], int wave, int u,
+                                               int j, int slots) {
+    if (j >= slots || !w.act[u]) return -FLT_MAX;
+    const float p = s.pos[j];
+    const bool vis = p >= 0.f && p <= (float)w.t[u] && s.doc[j] == w.doc[u];
+    return vis ? L[4 * wave + u][j] * a.scale : -FLT_MAX;
 }
 
 template <int DK, int DV>
@@ -404,8 +475,9 @@ __global__ void __launch_bounds__(kReadThreads) hola_forward_kernel(HolaArgs a) 
 
 template <int DK, int DV>
 __global__ void __launch_bounds__(kReadThreads) hola_query_backward_kernel(HolaArgs a) {
-    __shared__ SlotTiles<DK, DV> s;
-    __shared__ float4 DT[kReadWaves][kMaxSlots];  // logit gradients, [slot][query]
+    __shared__ SlotTiles<DK, DV, 4> s;
+    __shared__ float L[kMaxChunk][kLP];   // logits, then logit gradients: [query slot][slot]
+    __shared__ float Dt[kMaxChunk][kLP];  // dO . v_slot: [query slot][slot]
     __shared__ float GT[DV][kMaxChunk] __attribute__((aligned(16)));  // dO, [channel][query_slot]
     __shared__ float O[kMaxChunk][DV + 1];
     __shared__ float stat[kMaxChunk][2];
@@ -439,6 +511,9 @@ __global__ void __launch_bounds__(kReadThreads) hola_query_backward_kernel(HolaA
         }
     }
     __syncthreads();
+    // Raw logits and dO . v for every (query, slot) on MFMA.
+    chunk_xyt<DK, DK + 4>(s.QT, &s.K[0][0], slots, wave, L);
+    chunk_xyt<DV, DV + 4>(GT, &s.V[0][0], slots, wave, Dt);
     const float sink = ldf(a.sink, h);
     const WaveQueries w = wave_queries(s, wave, first, end - first);
     float delta[kWaveQueries], m[kWaveQueries], inv[kWaveQueries];
@@ -461,44 +536,25 @@ __global__ void __launch_bounds__(kReadThreads) hola_query_backward_kernel(HolaA
             a.aux[2 * tok + 1] = w.act[u] ? -delta[u] * expf(sink - m[u]) * inv[u] : 0.f;
         }
     }
-    for (int j = lane; j < slots; j += 64) {
-        float lg[kWaveQueries], dot[kWaveQueries] = {0.f, 0.f, 0.f, 0.f};
-        wave_logits(a, s, w, wave, j, lg);
-#pragma unroll 8
-        for (int i = 0; i < DV; ++i) {
-            const float vv = s.V[j][i];
-            const float4 g4 = *reinterpret_cast<const float4 *>(&GT[i][4 * wave]);
-            dot[0] += g4.x * vv;
-            dot[1] += g4.y * vv;
-            dot[2] += g4.z * vv;
-            dot[3] += g4.w * vv;
-        }
-        float d[kWaveQueries];
+    __syncthreads();
+    // Per slot (lanes): p and the logit gradient d = p (dO . v - delta) / sqrt(d_k),
+    // saved as pairs; the wave's rows of L take d (zero past the slots).
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int j = lane + 64 * r;
+        if (j >= kMaxSlots) continue;
 #pragma unroll
         for (int u = 0; u < kWaveQueries; ++u) {
-            const float p = lg[u] > -FLT_MAX ? expf(lg[u] - m[u]) * inv[u] : 0.f;
-            d[u] = lg[u] > -FLT_MAX ? p * (dot[u] - delta[u]) * a.scale : 0.f;
-            if (w.on[u])
-                reinterpret_cast<float2 *>(a.pairs)[token(a, b, w.t[u], h) * slots + j] =
-                    make_float2(p, d[u]);
+            const float lgv = visible_logit(a, s, w, L, wave, u, j, slots);
+            const float p = lgv > -FLT_MAX ? expf(lgv - m[u]) * inv[u] : 0.f;
+            const float d = lgv > -FLT_MAX ? p * (Dt[4 * wave + u][j] - delta[u]) * a.scale : 0.f;
+            if (w.on[u] && j < slots)
+                reinterpret_cast<float2 *>(a.pairs)[token(a, b, w.t[u], h) * slots + j] = make_float2(p, d);
+            L[4 * wave + u][j] = d;
         }
-        DT[wave][j] = make_float4(d[0], d[1], d[2], d[3]);
     }
-    __builtin_amdgcn_wave_barrier();
-    for (int i = lane; i < a.dk; i += 64) {
-        float g[kWaveQueries] = {0.f, 0.f, 0.f, 0.f};
-        for (int j = 0; j < slots; ++j) {
-            const float kv = s.K[j][i];
-            const float4 d4 = DT[wave][j];
-            g[0] += d4.x * kv;
-            g[1] += d4.y * kv;
-            g[2] += d4.z * kv;
-            g[3] += d4.w * kv;
-        }
-#pragma unroll
-        for (int u = 0; u < kWaveQueries; ++u)
-            if (w.on[u]) a.gq[token(a, b, w.t[u], h) * a.dk + i] = w.act[u] ? g[u] : 0.f;
-    }
+    __syncthreads();
+    chunk_py<DK, DK + 4>(a, L, &s.K[0][0], slots, wave, b, h, first, end - first, s.tval, a.dk, a.gq);
 }
 
 template <int DK, int DV>
