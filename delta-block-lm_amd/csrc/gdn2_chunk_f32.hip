@@ -117,10 +117,9 @@ __device__ __forceinline__ float fc_x(const View &v, bool bf, int b, int tg, int
 
 // b_t and lam_t of channel i (threads i < K): running products of the gates;
 // zero on the channels K .. FK - 1, which the MFMA products read as padding.
-template <int FK>
+template <int FK, int LQ = Fc<FK>::LQ, int FW = FK>
 __device__ void fc_decay_rows(const float *al, const Masks &m, float *bt, float *lam, int K, int tid) {
-    constexpr int LQ = Fc<FK>::LQ;
-    if (tid >= K && tid < FK)
+    if (tid >= K && tid < FW)
         for (int t = 0; t < C; ++t) bt[t * LQ + tid] = lam[t * LQ + tid] = 0.f;
     if (tid < K) {
         const int i = tid, sg15 = m.seg[C - 1];
@@ -138,10 +137,9 @@ __device__ void fc_decay_rows(const float *al, const Masks &m, float *bt, float 
 }
 
 // b_t alone (threads i < K; zero on the channels K .. FK - 1).
-template <int FK>
+template <int FK, int LQ = Fc<FK>::LQ, int FW = FK>
 __device__ void fc_b_row(const float *al, const Masks &m, float *bt, int K, int tid) {
-    constexpr int LQ = Fc<FK>::LQ;
-    if (tid >= K && tid < FK)
+    if (tid >= K && tid < FW)
         for (int t = 0; t < C; ++t) bt[t * LQ + tid] = 0.f;
     if (tid < K) {
         float p = 1.f;
@@ -157,10 +155,9 @@ __device__ void fc_b_row(const float *al, const Masks &m, float *bt, int K, int 
 // (t = tid / LPT, g = tid % LPT) takes its four channels of row t, forming
 // D_ts for s = t, t - 1, .. by a running product; the LPT partial rows of one
 // t (adjacent lanes) are summed by lane shuffles.  All threads call it.
-template <int FK, bool STRICT>
+template <int FK, bool STRICT, int LQ = Fc<FK>::LQ>
 __device__ __forceinline__ void fc_tri(const float *x, const float *y, const float *al, const Masks &m,
                                        float *out, int K, int tid) {
-    constexpr int LQ = Fc<FK>::LQ;
     const int t = tid / Fc<FK>::LPT, g = tid % Fc<FK>::LPT;
     float acc[C];
 #pragma unroll
@@ -259,12 +256,15 @@ struct FcPrepSmem {
     float A[C * LT], T[C * LT];
 };
 
-template <int FK>
+// FKK: the key tiles' width (FK, or 32 when d_k <= 32, so that the tiles of
+// the reference's K32/V64 shape fit four workgroups per CU).
+template <int FK, int FKK>
 struct FcOutSmem {
-    static constexpr int LQ = Fc<FK>::LQ;
+    static constexpr int LQ = Fc<FK>::LQ, LQK = FKK + 4;
     Masks m;
-    float q[C * LQ], k[C * LQ], al[C * LQ], eh[C * LQ], wv[C * LQ], bt[C * LQ];
-    float s0[FK * Fc<FK>::LS];  // S0, zero-padded to whole 16 x 16 tiles
+    float q[C * LQK], k[C * LQK], al[C * LQK], eh[C * LQK], bt[C * LQK];  // key side
+    float wv[C * LQ];
+    float s0[FKK * Fc<FK>::LS];  // S0, zero-padded to whole 16 x 16 tiles
     float T[C * LT], P[C * LT];
     float kk[C], ddp[FK / 16][C];
 };
@@ -526,10 +526,11 @@ static void launch_fc_scan(const FcArgs &a, hipStream_t stream) {
 }
 
 // ---- out: edits, outputs, scores ----------------------------------------------
-template <int FK>
+template <int FK, int FKK>
 __global__ void __launch_bounds__(Fc<FK>::NT) fc_out_kernel(FcArgs a) {
-    __shared__ FcOutSmem<FK> sm;
-    constexpr int LQ = Fc<FK>::LQ, LS = Fc<FK>::LS, NT = Fc<FK>::NT, NW = Fc<FK>::NW;
+    __shared__ FcOutSmem<FK, FKK> sm;
+    constexpr int LQ = Fc<FK>::LQ, LQK = FcOutSmem<FK, FKK>::LQK, LS = Fc<FK>::LS, NT = Fc<FK>::NT,
+                  NW = Fc<FK>::NW;
     const SeqArgs &s = a.s;
     const int tid = threadIdx.x, ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / s.H, h = bh % s.H;
     const int K = s.K, V = s.V, t = tid / Fc<FK>::LPT, g = tid % Fc<FK>::LPT, tg = c * C + t;
@@ -563,18 +564,20 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_out_kernel(FcArgs a) {
     for (int e = 0; e < EPT; ++e) {
         const int i = Fc<FK>::ch(g, e);
         const float kv = on ? rk[e] : 0.f;
-        sm.q[t * LQ + i] = on ? rq[e] : 0.f;
-        sm.k[t * LQ + i] = kv;
-        sm.al[t * LQ + i] = on ? ral[e] : 1.f;
-        sm.eh[t * LQ + i] = (on ? re[e] : 0.f) * kv;
+        if (i < FKK) {
+            sm.q[t * LQK + i] = on ? rq[e] : 0.f;
+            sm.k[t * LQK + i] = kv;
+            sm.al[t * LQK + i] = on ? ral[e] : 1.f;
+            sm.eh[t * LQK + i] = (on ? re[e] : 0.f) * kv;
+        }
         sm.wv[t * LQ + i] = on ? rw[e] * rv[e] : 0.f;
         ksq += kv * kv;
     }
     ksq = Fc<FK>::row_sum(ksq);
     if (g == 0) sm.kk[t] = ksq;
     __syncthreads();
-    fc_b_row<FK>(sm.al, sm.m, sm.bt, K, tid);
-    fc_tri<FK, false>(sm.q, sm.k, sm.al, sm.m, sm.P, K, tid);  // P, lower with the diagonal
+    fc_b_row<FK, LQK, FKK>(sm.al, sm.m, sm.bt, K, tid);
+    fc_tri<FK, false, LQK>(sm.q, sm.k, sm.al, sm.m, sm.P, K, tid);  // P, lower with the diagonal
     __syncthreads();
     // Wave w: value tiles w, w + NW, .. on v_mfma_f32_16x16x4f32 (lane (lg, ln):
     // rows 4 lg + r, column 16 vt + ln).  R = wv - Ahat S0, O = Qhat S0 over the
@@ -585,9 +588,9 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_out_kernel(FcArgs a) {
         f32x4 x = zero4(), o = zero4();
         for (int kk = 0; kk < KP; kk += 4) {
             const int i = kk + lg;
-            const float sv = sm.s0[i * LS + j], bti = sm.bt[ln * LQ + i];
-            x = __builtin_amdgcn_mfma_f32_16x16x4f32(bti * sm.eh[ln * LQ + i], sv, x, 0, 0, 0);
-            o = __builtin_amdgcn_mfma_f32_16x16x4f32(bti * sm.q[ln * LQ + i], sv, o, 0, 0, 0);
+            const float sv = sm.s0[i * LS + j], bti = sm.bt[ln * LQK + i];
+            x = __builtin_amdgcn_mfma_f32_16x16x4f32(bti * sm.eh[ln * LQK + i], sv, x, 0, 0, 0);
+            o = __builtin_amdgcn_mfma_f32_16x16x4f32(bti * sm.q[ln * LQK + i], sv, o, 0, 0, 0);
         }
         f32x4 r, d = zero4();
 #pragma unroll
@@ -1001,7 +1004,12 @@ static void fc_fwd(const FcArgs &a, hipStream_t stream, const hipEvent_t *ev) {
     launch_fc_scan<false>(a, stream);
     fmark(ev, 3, stream);
     fmark(ev, 4, stream);
-    hipLaunchKernelGGL(fc_out_kernel<FK>, dim3(n), dim3(Fc<FK>::NT), 0, stream, a);
+    bool narrow = false;
+    if constexpr (FK == 64) {
+        narrow = a.s.K <= 32;
+        if (narrow) hipLaunchKernelGGL((fc_out_kernel<64, 32>), dim3(n), dim3(Fc<64>::NT), 0, stream, a);
+    }
+    if (!narrow) hipLaunchKernelGGL((fc_out_kernel<FK, FK>), dim3(n), dim3(Fc<FK>::NT), 0, stream, a);
     fmark(ev, 5, stream);
 }
 
