@@ -15,7 +15,9 @@ inline bool fc_eligible_shape(const gdn2_shape *s) {
 // The token-sequential argument block (shapes, views, outputs, gradients)
 // plus the chunk path's checkpoint and workspace arrays, each indexed by
 // chunk ci = (b * H + h) * nc + c:
-//   st     S at the chunk start, [K][V]                 (forward scan -> out, bgrad)
+//   st     S at the chunk start, tile-packed: [VT][KT][4][16][4], element
+//          (((vt * KT + tau) * 4 + g) * 16 + n) * 4 + r = S[16 tau + 4 g + r][16 vt + n]
+//          (forward scan -> out, bgrad)
 //   tm     T = (I + A)^-1, [16][16]                       (prep -> out, bgrad)
 //   dl     the edits delta, [16][V]                       (out -> bprep, bgrad)
 //   fw, fk the factored map: W' = T (b . e . k) and Ktil = lam . k, [16][KP] each
@@ -24,10 +26,11 @@ inline bool fc_eligible_shape(const gdn2_shape *s) {
 //   gv     b_15 (the map's diagonal), [KP]
 // KP = d_k and VP = d_v rounded up to 16 (VT = VP / 16): the key axis of the
 // map's factors is padded with zeros to whole 16-row MFMA tiles for the scans.
-// Backward workspace: ds, the state adjoint at each chunk end, [K][V]; and n,
-// the adjoint map's additive term, lane-packed: [VT][KP / 16][4][16][4], element
-// (((vt * KT + tau) * 4 + g) * 16 + n) * 4 + r = N[16 tau + 4 g + r][16 vt + n]
-// (zero outside K x V).  Every array starts on a 16-byte boundary.
+// KT = KP / 16.  A scan wave stores its 16 x 16 tile of S as one 16-byte piece
+// per lane, its accumulator registers as they are.  Backward workspace: ds, the
+// state adjoint at each chunk end, and n, the adjoint map's additive term, both
+// tile-packed like st.  st, ds and n are zero outside K x V.  Every array starts
+// on a 16-byte boundary.
 struct FcArgs {
     SeqArgs s;
     int nc;
@@ -43,7 +46,7 @@ inline size_t fc_pad4(size_t x) { return (x + 3) & ~(size_t)3; }
 // The checkpoint's arrays in order, in floats, for n chunks.
 inline void fc_checkpoint_parts(int64_t n, int K, int V, size_t part[7]) {
     const size_t KP = fc_kp(K), VP = fc_kp(V);
-    part[0] = fc_pad4(n * K * V);       // st
+    part[0] = n * KP * VP;              // st
     part[1] = fc_pad4(n * FC_C * FC_C); // tm
     part[2] = fc_pad4(n * FC_C * V);    // dl
     part[3] = n * FC_C * KP;            // fw
@@ -61,7 +64,7 @@ inline size_t fc_checkpoint_bytes(int64_t B, int64_t T, int64_t H, int K, int V)
 
 inline size_t fc_workspace_bytes(int64_t B, int64_t T, int64_t H, int K, int V) {
     const int64_t n = fc_chunks(B, T, H);
-    return (fc_pad4(n * K * V) + (size_t)n * fc_kp(K) * fc_kp(V)) * sizeof(float);
+    return 2 * (size_t)n * fc_kp(K) * fc_kp(V) * sizeof(float);
 }
 
 inline void fc_bind(FcArgs &a, void *ck, void *ws) {
@@ -76,7 +79,7 @@ inline void fc_bind(FcArgs &a, void *ck, void *ws) {
     }
     if (ws) {
         a.ds = static_cast<float *>(ws);
-        a.n = a.ds + fc_pad4(n * a.s.K * a.s.V);
+        a.n = a.ds + n * fc_kp(a.s.K) * fc_kp(a.s.V);
     }
 }
 

@@ -188,60 +188,41 @@ __device__ __forceinline__ void fc_tri(const float *x, const float *y, const flo
     }
 }
 
-// Stage the rows x COLS block at src0 (and src1, same shape; row stride sld;
-// zero where row >= rv or column >= cv) into dst0 (dst1) with row stride dld.
-// Each thread issues U loads per source before it stores any, so a batch's
-// loads are in flight together instead of one latency per element.
-template <int NT, int COLS, int U>
-__device__ __forceinline__ void fc_stage2(float *dst0, float *dst1, int dld, const float *src0,
-                                          const float *src1, int sld, int rows, int rv, int cv, int tid) {
-    const int n = rows * COLS;
-    for (int e0 = tid; e0 < n; e0 += U * NT) {
-        float x0[U], x1[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int e = e0 + u * NT, i = e / COLS, j = e % COLS;
-            const bool in = e < n && i < rv && j < cv;
-            x0[u] = in ? src0[(int64_t)i * sld + j] : 0.f;
-            x1[u] = (in && src1) ? src1[(int64_t)i * sld + j] : 0.f;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int e = e0 + u * NT, i = e / COLS, j = e % COLS;
-            if (e < n) {
-                dst0[i * dld + j] = x0[u];
-                if (dst1) dst1[i * dld + j] = x1[u];
-            }
-        }
-    }
-}
-
-// fc_stage2 for rows of 16-byte aligned float4s (sld, cv and the sources'
-// offsets multiples of 4): one 16-byte load per four elements.
-template <int NT, int COLS, int U>
-__device__ __forceinline__ void fc_stage2_v4(float *dst0, float *dst1, int dld, const float *src0,
-                                             const float *src1, int sld, int rows, int rv, int cv, int tid) {
-    constexpr int CQ = COLS / 4;
-    const int n = rows * CQ;
+// Stage value tiles vt0 .. vt0 + NVT - 1 of the tile-packed arrays src0 (and
+// src1) (element (((vt * KT + tau) * 4 + g) * 16 + n) * 4 + r at row
+// 16 tau + 4 g + r, column 16 vt + n) into rows 0 .. 16 KT - 1 and columns
+// 0 .. 16 NVT - 1 of dst0 (dst1), row stride dld; zero where row >= rv, column
+// >= cv or vt >= VT.  One 16-byte load per lane and tile; each thread issues U
+// loads per source before it stores any.
+template <int NT, int NVT, int U>
+__device__ __forceinline__ void fc_stage_tiles(float *dst0, float *dst1, int dld, const float *src0,
+                                               const float *src1, int KT, int VT, int vt0, int rv, int cv,
+                                               int tid) {
+    const int n = NVT * KT * 64;
     for (int e0 = tid; e0 < n; e0 += U * NT) {
         float4 x0[U], x1[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int e = e0 + u * NT, i = e / CQ, j = 4 * (e % CQ);
-            const bool in = e < n && i < rv && j < cv;
+            const int e = e0 + u * NT, vt = vt0 + e / (KT * 64), o = e % (KT * 64);
+            const bool in = e < n && vt < VT;
+            const int64_t off = ((int64_t)vt * KT * 64 + o) * 4;
             const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-            x0[u] = in ? *reinterpret_cast<const float4 *>(src0 + (int64_t)i * sld + j) : z;
-            x1[u] = (in && src1) ? *reinterpret_cast<const float4 *>(src1 + (int64_t)i * sld + j) : z;
+            x0[u] = in ? *reinterpret_cast<const float4 *>(src0 + off) : z;
+            x1[u] = (in && src1) ? *reinterpret_cast<const float4 *>(src1 + off) : z;
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int e = e0 + u * NT, i = e / CQ, j = 4 * (e % CQ);
+            const int e = e0 + u * NT, vl = e / (KT * 64), o = e % (KT * 64);
+            const int l = o & 63, i = 16 * (o >> 6) + 4 * (l >> 4), jl = 16 * vl + (l & 15);
             if (e < n) {
-                float *d = dst0 + i * dld + j;
-                d[0] = x0[u].x, d[1] = x0[u].y, d[2] = x0[u].z, d[3] = x0[u].w;
-                if (dst1) {
-                    float *d1 = dst1 + i * dld + j;
-                    d1[0] = x1[u].x, d1[1] = x1[u].y, d1[2] = x1[u].z, d1[3] = x1[u].w;
+                const bool cj = 16 * vt0 + jl < cv;
+                const float a0[4] = {x0[u].x, x0[u].y, x0[u].z, x0[u].w};
+                const float a1[4] = {x1[u].x, x1[u].y, x1[u].z, x1[u].w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const bool ok = cj && i + r < rv;
+                    dst0[(i + r) * dld + jl] = ok ? a0[r] : 0.f;
+                    if (dst1) dst1[(i + r) * dld + jl] = ok ? a1[r] : 0.f;
                 }
             }
         }
@@ -463,10 +444,12 @@ __global__ void __launch_bounds__(64 * KT) fc_scan_kernel(FcArgs a) {
             const int64_t ci = chunk_at(step);
             const FcScanOps<KT> &cur = ring[d];
             // the state before (forward) / the adjoint after (reverse) this chunk
+            {
+                float kx[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = 16 * tau + 4 * g + r;
-                if (i < K && jv) keep[(ci * K + i) * V + j] = X[r];
+                for (int r = 0; r < 4; ++r) kx[r] = (16 * tau + 4 * g + r < K && jv) ? X[r] : 0.f;
+                *reinterpret_cast<float4 *>(&keep[(((ci * VT + cg) * KT + tau) * 64 + l) * 4]) =
+                    make_float4(kx[0], kx[1], kx[2], kx[3]);
             }
             // this tile's part of v[t][j], t = 4 g + r: -W' S (+ U in tile 0) or Ktil X
             f32x4 vp = (!REV && tau == 0) ? f32x4{cur.a.x, cur.a.y, cur.a.z, cur.a.w} : zero4();
@@ -550,12 +533,9 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_out_kernel(FcArgs a) {
         rw[e] = fc_in(s.write, b, tg, h, i, s.T, V, true);
         rv[e] = fc_x(s.v, a.in_bf16, b, tg, h, i, s.T, V, true);
     }
-    // S0 rows 0 .. KP - 1, all FK columns (zero outside K x V); 16-byte loads
-    // when the rows allow them
-    if ((V & 3) == 0 && (reinterpret_cast<uintptr_t>(a.st) & 15) == 0)
-        fc_stage2_v4<NT, FK, FK / 16>(sm.s0, nullptr, LS, a.st + (int64_t)ci * K * V, nullptr, V, KP, K, V, tid);
-    else
-        fc_stage2<NT, FK, 16>(sm.s0, nullptr, LS, a.st + (int64_t)ci * K * V, nullptr, V, KP, K, V, tid);
+    // S0 rows 0 .. KP - 1, all FK columns (zero outside K x V)
+    fc_stage_tiles<NT, FK / 16, FK / 32>(sm.s0, nullptr, LS, a.st + (int64_t)ci * KP * VP, nullptr, KP / 16, VT, 0,
+                                         K, V, tid);
     if (tid < C * C) sm.T[(tid >> 4) * LT + (tid & 15)] = a.tm[(int64_t)ci * C * C + tid];
     fc_masks(s, b, c, sm.m, tid);
     const bool on = sm.m.val[t] != 0.f;
@@ -790,14 +770,10 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
     f32x4 res[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) res[m] = zero4();
-    const float *st = a.st + (int64_t)ci * K * V, *dst = a.ds + (int64_t)ci * K * V;
-    const bool v4 = (V & 3) == 0 && ((reinterpret_cast<uintptr_t>(a.st) | reinterpret_cast<uintptr_t>(a.ds)) & 15) == 0;
+    const float *st = a.st + (int64_t)ci * KP * VP, *dst = a.ds + (int64_t)ci * KP * VP;
     for (int j0 = 0; j0 < VP; j0 += VB) {
         if (j0 > 0) __syncthreads();  // the previous block's products have read S0 and dS
-        if (v4)
-            fc_stage2_v4<NT, VB, 4>(sm.u.st.s0, sm.u.st.ds, LB, st + j0, dst + j0, V, KP, K, V - j0, tid);
-        else
-            fc_stage2<NT, VB, 8>(sm.u.st.s0, sm.u.st.ds, LB, st + j0, dst + j0, V, KP, K, V - j0, tid);
+        fc_stage_tiles<NT, VB / 16, 2>(sm.u.st.s0, sm.u.st.ds, LB, st, dst, KT, VT, j0 / 16, K, V, tid);
         __syncthreads();
         {  // rowsum(S0 . dS) of key channel i over the block: TPC threads per channel
             constexpr int TPC = NT / FK, CW = VB / TPC;
