@@ -117,21 +117,29 @@ __device__ __forceinline__ float fc_x(const View &v, bool bf, int b, int tg, int
 
 // b_t and lam_t of channel i (threads i < K): running products of the gates;
 // zero on the channels K .. FK - 1, which the MFMA products read as padding.
+// The channel's 16 gates are read first, so that the reads issue together
+// instead of one LDS round trip per step.
 template <int FK, int LQ = Fc<FK>::LQ, int FW = FK>
 __device__ void fc_decay_rows(const float *al, const Masks &m, float *bt, float *lam, int K, int tid) {
     if (tid >= K && tid < FW)
+#pragma unroll
         for (int t = 0; t < C; ++t) bt[t * LQ + tid] = lam[t * LQ + tid] = 0.f;
     if (tid < K) {
         const int i = tid, sg15 = m.seg[C - 1];
+        float a[C];
+#pragma unroll
+        for (int t = 0; t < C; ++t) a[t] = al[t * LQ + i];
         float p = 1.f;
+#pragma unroll
         for (int t = 0; t < C; ++t) {
-            p *= al[t * LQ + i];
+            p *= a[t];
             bt[t * LQ + i] = m.seg[t] == 0 ? p : 0.f;
         }
         float q = 1.f;
+#pragma unroll
         for (int s = C - 1; s >= 0; --s) {
             lam[s * LQ + i] = m.seg[s] == sg15 ? q : 0.f;
-            q *= al[s * LQ + i];
+            q *= a[s];
         }
     }
 }
@@ -140,11 +148,16 @@ __device__ void fc_decay_rows(const float *al, const Masks &m, float *bt, float 
 template <int FK, int LQ = Fc<FK>::LQ, int FW = FK>
 __device__ void fc_b_row(const float *al, const Masks &m, float *bt, int K, int tid) {
     if (tid >= K && tid < FW)
+#pragma unroll
         for (int t = 0; t < C; ++t) bt[t * LQ + tid] = 0.f;
     if (tid < K) {
+        float a[C];
+#pragma unroll
+        for (int t = 0; t < C; ++t) a[t] = al[t * LQ + tid];
         float p = 1.f;
+#pragma unroll
         for (int t = 0; t < C; ++t) {
-            p *= al[t * LQ + tid];
+            p *= a[t];
             bt[t * LQ + tid] = m.seg[t] == 0 ? p : 0.f;
         }
     }
@@ -259,24 +272,31 @@ struct FcBPrepSmem {
     float cs[C];
 };
 
-template <int FK>
+// FKK: the key tiles' width (FK, or 32 when d_k <= 32: the reference's K32/V64
+// shape then fits three workgroups per CU).
+template <int FK, int FKK>
 struct FcBGradSmem {
-    static constexpr int LQ = Fc<FK>::LQ;
+    static constexpr int LQ = Fc<FK>::LQ, LQK = FKK + 4;
     Masks m;
-    float q[C * LQ], k[C * LQ], e[C * LQ], al[C * LQ], dO[C * LQ], dl[C * LQ], dr[C * LQ];
-    float bt[C * LQ], lam[C * LQ];
+    float q[C * LQK], k[C * LQK], e[C * LQK], al[C * LQK], bt[C * LQK], lam[C * LQK];  // key side
+    union {
+        struct {
+            float dO[C * LQ], dl[C * LQ], dr[C * LQ];  // value side, read until the products end
+        } v;
+        struct {
+            float ga[C * LQK], gq[C * LQK], gk[C * LQK];  // then dAhat, dQhat, dKtil [token][key]
+        } g;
+    } w;
     union {
         struct {
             // one block of VB value columns of S0 and dS, zero outside K x V
-            float s0[FK * LB], ds[FK * LB];
+            float s0[FKK * LB], ds[FKK * LB];
         } st;
-        struct {
-            float ga[C * LQ], gq[C * LQ], gk[C * LQ];  // dAhat, dQhat, dKtil [token][key]
-            float part[Fc<FK>::NT * C];  // dalpha partials: NT / cpl groups x C rows x cpl channels
-        } gr;
+        float part[Fc<FK>::NT * C];  // then dalpha partials: NT / cpl groups x C rows x cpl channels
     } u;
     float T[C * LT], P[C * LT], dA[C * LT], dP[C * LT];
     float cs[C], ck[C], fs[FK];
+    static_assert(sizeof(u.st) >= sizeof(u.part), "the partials fit the S0 / dS block");
 };
 
 }  // namespace
@@ -705,10 +725,10 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bprep_kernel(FcArgs a) {
 // through b_t; end pairs k_s dKtil_s through lam_s; rowsum(S0 . dS) through
 // b_15): sum_{lo < u} L(lo, u) Y(u, lo) with L the gates over (lo, u) and Y by
 // Horner over hi, exact for zero and negative gates.
-template <int FK>
+template <int FK, int FKK>
 __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
-    __shared__ FcBGradSmem<FK> sm;
-    constexpr int LQ = Fc<FK>::LQ, NT = Fc<FK>::NT, NW = Fc<FK>::NW;
+    __shared__ FcBGradSmem<FK, FKK> sm;
+    constexpr int LQ = Fc<FK>::LQ, LQK = FcBGradSmem<FK, FKK>::LQK, NT = Fc<FK>::NT, NW = Fc<FK>::NW;
     const SeqArgs &s = a.s;
     const int tid = threadIdx.x, ci = blockIdx.x, bh = ci / a.nc, c = ci % a.nc, b = bh / s.H, h = bh % s.H;
     const int K = s.K, V = s.V, t = tid / Fc<FK>::LPT, g = tid % Fc<FK>::LPT, tg = c * C + t;
@@ -737,13 +757,15 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
     for (int e = 0; e < EPT; ++e) {
         const int i = Fc<FK>::ch(g, e);
         const float kv = on ? xk[e] : 0.f;
-        sm.q[t * LQ + i] = on ? xq[e] : 0.f;
-        sm.k[t * LQ + i] = kv;
-        sm.e[t * LQ + i] = on ? xe[e] : 0.f;
-        sm.al[t * LQ + i] = on ? xal[e] : 1.f;
-        sm.dO[t * LQ + i] = on ? xdo[e] : 0.f;
+        if (i < FKK) {
+            sm.q[t * LQK + i] = on ? xq[e] : 0.f;
+            sm.k[t * LQK + i] = kv;
+            sm.e[t * LQK + i] = on ? xe[e] : 0.f;
+            sm.al[t * LQK + i] = on ? xal[e] : 1.f;
+        }
+        sm.w.v.dO[t * LQ + i] = on ? xdo[e] : 0.f;
         const float d = xdl[e];
-        sm.dl[t * LQ + i] = d;
+        sm.w.v.dl[t * LQ + i] = d;
         ksq += kv * kv;
         dsq += d * d;
     }
@@ -757,8 +779,8 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
         sm.ck[t] = ok ? dsc * nd / nk : 0.f;
     }
     __syncthreads();
-    fc_decay_rows<FK>(sm.al, sm.m, sm.bt, sm.lam, K, tid);
-    fc_tri<FK, false>(sm.q, sm.k, sm.al, sm.m, sm.P, K, tid);
+    fc_decay_rows<FK, LQK, FKK>(sm.al, sm.m, sm.bt, sm.lam, K, tid);
+    fc_tri<FK, false, LQK>(sm.q, sm.k, sm.al, sm.m, sm.P, K, tid);
     // The value axis in blocks of VB columns (one block at FK = 64, two at FK =
     // 128), each with its columns of S0 and dS in LDS.  Per block: ddelta and dR
     // of its value tiles, then the 16 x 16 products that reduce over the value
@@ -794,16 +816,16 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
             const int j = 16 * vt + ln, jl = j - j0;
             f32x4 dd;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) dd[r] = sm.cs[4 * lg + r] * sm.dl[(4 * lg + r) * LQ + j];
+            for (int r = 0; r < 4; ++r) dd[r] = sm.cs[4 * lg + r] * sm.w.v.dl[(4 * lg + r) * LQ + j];
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                dd = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.P[(4 * lg + q) * LT + ln], sm.dO[(4 * lg + q) * LQ + j],
+                dd = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.P[(4 * lg + q) * LT + ln], sm.w.v.dO[(4 * lg + q) * LQ + j],
                                                           dd, 0, 0, 0);
             for (int tau = 0; tau < KT; ++tau)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int i = 16 * tau + 4 * lg + q;
-                    dd = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.lam[ln * LQ + i] * sm.k[ln * LQ + i],
+                    dd = __builtin_amdgcn_mfma_f32_16x16x4f32(sm.lam[ln * LQK + i] * sm.k[ln * LQK + i],
                                                               sm.u.st.ds[i * LB + jl], dd, 0, 0, 0);
                 }
             f32x4 dr = zero4();
@@ -813,7 +835,7 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int tt = 4 * lg + r, tq = c * C + tt;
-                sm.dr[tt * LQ + j] = dr[r];
+                sm.w.v.dr[tt * LQ + j] = dr[r];
                 if (j < V && tq < s.T) {
                     const bool von = sm.m.val[tt] != 0.f;
                     const int64_t o = (((int64_t)b * s.T + tq) * s.H + h) * V + j;
@@ -831,8 +853,8 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
             const int kind = n < 3 * KT ? n % 3 : 3 + (n - 3 * KT), tau = n < 3 * KT ? n / 3 : 0;
             // A: [token][value] rows; B: S0 or dS rows of key 16 tau + ln (block
             // columns), or delta rows (value columns) for dA and dP
-            const float *xa = (kind == 0 || kind == 3 ? sm.dr : (kind == 2 ? sm.dl : sm.dO)) + ln * LQ + j0;
-            const float *yy = kind >= 3 ? sm.dl + ln * LQ + j0
+            const float *xa = (kind == 0 || kind == 3 ? sm.w.v.dr : (kind == 2 ? sm.w.v.dl : sm.w.v.dO)) + ln * LQ + j0;
+            const float *yy = kind >= 3 ? sm.w.v.dl + ln * LQ + j0
                                         : (kind == 2 ? sm.u.st.ds : sm.u.st.s0) + (16 * tau + ln) * LB;
             f32x4 acc = res[m];
             for (int kk = 0; kk < je; kk += 4)
@@ -840,7 +862,7 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
             res[m] = acc;
         }
     }
-    __syncthreads();  // S0 and dS are no longer read: their space takes dAhat, dQhat, dKtil
+    __syncthreads();  // dO, delta and dR are no longer read: their space takes dAhat, dQhat, dKtil
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         const int n = w + NW * m;
@@ -850,8 +872,8 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
             const int tt = 4 * lg + r;
             if (n < 3 * KT) {
                 const int kind = n % 3, i = 16 * (n / 3) + ln;
-                float *dst = kind == 0 ? sm.u.gr.ga : (kind == 1 ? sm.u.gr.gq : sm.u.gr.gk);
-                dst[tt * LQ + i] = kind == 0 ? -res[m][r] : res[m][r];
+                float *dst = kind == 0 ? sm.w.g.ga : (kind == 1 ? sm.w.g.gq : sm.w.g.gk);
+                dst[tt * LQK + i] = kind == 0 ? -res[m][r] : res[m][r];
             } else {
                 const bool same = sm.m.seg[tt] == sm.m.seg[ln];
                 if (n == 3 * KT) sm.dA[tt * LT + ln] = (ln < tt && same) ? -res[m][r] : 0.f;
@@ -873,10 +895,10 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
     int sg[C];
 #pragma unroll
     for (int x = 0; x < C; ++x) {
-        ra[x] = sm.al[x * LQ + i];
-        rk[x] = sm.k[x * LQ + i];
-        rq[x] = sm.q[x * LQ + i];
-        re[x] = sm.e[x * LQ + i] * rk[x];
+        ra[x] = sm.al[x * LQK + i];
+        rk[x] = sm.k[x * LQK + i];
+        rq[x] = sm.q[x * LQK + i];
+        re[x] = sm.e[x * LQK + i] * rk[x];
         sg[x] = sm.m.seg[x];
     }
     for (int p = 0; p < np; ++p) {
@@ -902,11 +924,11 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
         const int tq = c * C + u;
         if (iv && tq < s.T) {
             const bool von = sm.m.val[u] != 0.f;
-            const float bt = sm.bt[u * LQ + i], lt = sm.lam[u * LQ + i];
-            const float k = sm.k[u * LQ + i], ev = sm.e[u * LQ + i];
-            const float dq = bt * sm.u.gr.gq[u * LQ + i] + qP;
-            const float deh = bt * sm.u.gr.ga[u * LQ + i] + eA;
-            const float dk = lt * sm.u.gr.gk[u * LQ + i] + kAP + ev * deh + sm.ck[u] * k;
+            const float bt = sm.bt[u * LQK + i], lt = sm.lam[u * LQK + i];
+            const float k = sm.k[u * LQK + i], ev = sm.e[u * LQK + i];
+            const float dq = bt * sm.w.g.gq[u * LQK + i] + qP;
+            const float deh = bt * sm.w.g.ga[u * LQK + i] + eA;
+            const float dk = lt * sm.w.g.gk[u * LQK + i] + kAP + ev * deh + sm.ck[u] * k;
             const int64_t o = (((int64_t)b * s.T + tq) * s.H + h) * K + i;
             if (s.dq) store_out(s.dq, a.in_bf16, o, von ? dq : 0.f);
             if (s.dk) store_out(s.dk, a.in_bf16, o, von ? dk : 0.f);
@@ -920,8 +942,8 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
     for (int x = 0; x < C; ++x) dal[x] = 0.f;
     for (int p = 0; p < np; ++p) {
         const int lo = ngr * p + gi - 1;  // -1 .. 14
-        const float kl = lo >= 0 ? sm.k[lo * LQ + i] : 0.f;
-        const float endc = (lo >= 0 && sm.m.seg[lo] == sg15) ? kl * sm.u.gr.gk[lo * LQ + i] : 0.f;
+        const float kl = lo >= 0 ? sm.k[lo * LQK + i] : 0.f;
+        const float endc = (lo >= 0 && sm.m.seg[lo] == sg15) ? kl * sm.w.g.gk[lo * LQK + i] : 0.f;
         float Y[C], y = 0.f;
 #pragma unroll
         for (int x = C - 1; x >= 0; --x) {
@@ -931,7 +953,7 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
                     cf = (sm.dA[x * LT + lo] * re[x] + sm.dP[x * LT + lo] * rq[x]) * kl;
                     if (x == C - 1) cf += endc;
                 } else {
-                    cf = sg[x] == 0 ? re[x] * sm.u.gr.ga[x * LQ + i] + rq[x] * sm.u.gr.gq[x * LQ + i] : 0.f;
+                    cf = sg[x] == 0 ? re[x] * sm.w.g.ga[x * LQK + i] + rq[x] * sm.w.g.gq[x * LQK + i] : 0.f;
                     if (x == C - 1 && sg15 == 0) cf += sm.fs[i];
                 }
             }
@@ -947,7 +969,7 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
             }
     }
     // partials [group][u][channel] (ngr groups of C x cpl), then one sum per (u, channel)
-    float *part = sm.u.gr.part + gi * (C * cpl);
+    float *part = sm.u.part + gi * (C * cpl);
 #pragma unroll
     for (int x = 0; x < C; ++x) part[x * cpl + i] = dal[x];
     __syncthreads();
@@ -955,7 +977,7 @@ __global__ void __launch_bounds__(Fc<FK>::NT) fc_bgrad_kernel(FcArgs a) {
         const int u = e / cpl, ch = e - u * cpl;
         if (ch >= K) continue;
         float x = 0.f;
-        for (int gq = 0; gq < ngr; ++gq) x += sm.u.gr.part[gq * (C * cpl) + e];
+        for (int gq = 0; gq < ngr; ++gq) x += sm.u.part[gq * (C * cpl) + e];
         const int tq = c * C + u;
         if (tq < s.T && s.dalpha)
             s.dalpha[(((int64_t)b * s.T + tq) * s.H + h) * K + ch] =
@@ -999,7 +1021,12 @@ static void fc_bwd(const FcArgs &a, hipStream_t stream, const hipEvent_t *ev) {
     launch_fc_scan<true>(a, stream);
     fmark(ev, 3, stream);
     fmark(ev, 4, stream);
-    hipLaunchKernelGGL(fc_bgrad_kernel<FK>, dim3(n), dim3(Fc<FK>::NT), 0, stream, a);
+    bool narrow = false;
+    if constexpr (FK == 64) {
+        narrow = a.s.K <= 32;
+        if (narrow) hipLaunchKernelGGL((fc_bgrad_kernel<64, 32>), dim3(n), dim3(Fc<64>::NT), 0, stream, a);
+    }
+    if (!narrow) hipLaunchKernelGGL((fc_bgrad_kernel<FK, FK>), dim3(n), dim3(Fc<FK>::NT), 0, stream, a);
     fmark(ev, 5, stream);
 }
 
