@@ -175,18 +175,28 @@ __device__ __forceinline__ void fc_tri(const float *x, const float *y, const flo
     float acc[C];
 #pragma unroll
     for (int s = 0; s < C; ++s) acc[s] = 0.f;
-#pragma unroll
+    // Per channel, its y and gate columns are read whole before the running
+    // product (the reads issue together instead of one LDS round trip per
+    // step; the terms past t are selected away, t differing between the lane
+    // groups of a wave).  One channel at a time keeps the registers down.
+#pragma unroll 1
     for (int e = 0; e < Fc<FK>::EPT; ++e) {
         const int i = Fc<FK>::ch(g, e);
-        if (i < K) {
-            const float xt = x[t * LQ + i];
-            float d = 1.f;
+        const bool iv = i < K;
+        const int ic = iv ? i : 0;  // channels past K read channel 0, unused
+        const float xt = x[t * LQ + ic];
+        float yv[C], av[C];
 #pragma unroll
-            for (int s = C - 1; s >= 0; --s)
-                if (s <= t) {
-                    acc[s] += xt * d * y[s * LQ + i];
-                    d *= al[s * LQ + i];
-                }
+        for (int s = 0; s < C; ++s) {
+            yv[s] = y[s * LQ + ic];
+            av[s] = al[s * LQ + ic];
+        }
+        float d = 1.f;
+#pragma unroll
+        for (int s = C - 1; s >= 0; --s) {
+            const bool in = iv && s <= t;
+            acc[s] += in ? xt * d * yv[s] : 0.f;
+            d = in ? d * av[s] : d;
         }
     }
     float r = 0.f;
